@@ -1,0 +1,144 @@
+/*
+ * telmo_hip.h - C ABI of the MI355X (gfx950) int8-weight matrix product.
+ *
+ * A drop-in for telmo's matrix-product operator surface. Plain pointers and sizes only; every
+ * entry point returns a status (TG_OK = 0, negative on error) and never aborts or throws across
+ * the boundary. Reference interfaces each entry point replaces (paths in the telmo repository):
+ *
+ *   Precision                    src/quant.rs:20-83
+ *   quant::encode / decode       src/quant.rs:200-303
+ *   PackedWeights::from_parts    src/kernels/mod.rs:214-237   -> tg_weights_upload
+ *   PackedWeights::bytes         src/kernels/mod.rs:301-303   -> tg_weights_bytes
+ *   Act, Epilogue                src/kernels/mod.rs:366-398   -> tg_epilogue
+ *   Kernels::matmul              src/kernels/mod.rs:657-688   -> tg_matmul, tg_matmul_device
+ *   Kernels::linear              src/kernels/mod.rs:691-701   -> tg_linear, tg_linear_device
+ *   Kernels::glu (row kernel)    src/kernels/mod.rs:463-464   -> tg_glu_device
+ *
+ * Error behaviour follows the reference's asserts (src/kernels/mod.rs:669-677): m == 0 or n == 0
+ * is a no-op that succeeds before any other check; then lda >= k, ldc >= n, the lengths of a and
+ * c, and the bias length (>= n) are checked and give TG_ERR_SHAPE; k == 0 stores the epilogue of
+ * a zero sum. The reference panics where this returns an error; a Rust shim maps the codes back.
+ */
+#ifndef TELMO_HIP_H
+#define TELMO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tg_ctx tg_ctx;
+typedef struct tg_weights tg_weights;
+
+/* Weight precisions, in the order of src/quant.rs:22-30. */
+enum { TG_F32 = 0, TG_F16 = 1, TG_BF16 = 2, TG_INT8 = 3, TG_Q8_0 = 4 };
+
+/* Epilogue activations, src/kernels/mod.rs:368-372. */
+enum { TG_ACT_NONE = 0, TG_ACT_RELU = 1, TG_ACT_SILU = 2 };
+
+/* Numerics of a context.
+ * TG_MODE_FAST: int8 and Q8_0 weights run the two-digit int8 MFMA GEMM (m > 8) or the dot4
+ *   GEMV (m <= 8). Activations are split per row into two int8 digits of a 15-bit fixed-point
+ *   value; sums are exact in i32; results are bit-identical for any m, tiling or split, and within
+ *   1e-4 row-normwise of the reference's fused f32 sums. Other precisions run the exact kernel.
+ * TG_MODE_EXACT: one lane per output sums fmaf(a, widen(w), acc) in input order, bit-identical
+ *   to the reference's AVX2 / AVX-512 / NEON kernels, epilogue included. Slow; for validation. */
+enum { TG_MODE_FAST = 0, TG_MODE_EXACT = 1 };
+
+/* Status codes. */
+enum {
+    TG_OK = 0,
+    TG_ERR_NULL = -1,        /* a required pointer is null */
+    TG_ERR_SHAPE = -2,       /* a precondition of Kernels::matmul fails */
+    TG_ERR_ALIGN = -3,       /* a buffer is not aligned as required */
+    TG_ERR_HIP = -4,         /* a HIP runtime call failed (see tg_last_error) */
+    TG_ERR_UNSUPPORTED = -5, /* precision, mode or size this library does not run */
+    TG_ERR_NOMEM = -6,       /* device allocation failed */
+    TG_ERR_ARG = -7          /* an argument is out of its range (precision, act, sizes of the weights) */
+};
+
+/* Epilogue: c = (accumulate ? c : 0) + scale * act(sum + bias). bias may be null; when set it
+ * holds bias_len >= n values (host memory for host entry points, device memory for _device ones). */
+typedef struct tg_epilogue {
+    const float *bias;
+    size_t bias_len;
+    uint32_t act;
+    float scale;
+    int32_t accumulate;
+} tg_epilogue;
+
+/* ---- contexts ---------------------------------------------------------------------------- */
+
+/* A context on HIP device `device`. `stream` is a hipStream_t to run on, or null for a stream of
+ * the context's own. Calls on one context are serialised; contexts are independent. */
+int tg_ctx_create(int device, void *stream, tg_ctx **out);
+void tg_ctx_destroy(tg_ctx *ctx);
+int tg_ctx_set_mode(tg_ctx *ctx, uint32_t mode);
+uint32_t tg_ctx_mode(const tg_ctx *ctx);
+/* The message of the last failed call on this context ("" if none). Valid until the next call. */
+const char *tg_last_error(const tg_ctx *ctx);
+/* Waits for all work queued on the context's stream. */
+int tg_synchronize(tg_ctx *ctx);
+
+/* ---- weights ------------------------------------------------------------------------------ */
+
+/* Uploads a matrix in telmo's panel layout (n outputs, k inputs; values_len bytes as
+ * tg_panel_bytes gives, scales as tg_scale_count gives). Host pointers. The device copy is the
+ * library's own and lives until tg_weights_free; int8 and Q8_0 values are re-laid out on the
+ * device for the MFMA and dot4 kernels. Mirrors PackedWeights::from_parts, whose refusals
+ * (wrong lengths, Q8_0 with k not a multiple of 32) give TG_ERR_ARG. */
+int tg_weights_upload(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *scales,
+                      size_t n_scales, uint32_t precision, size_t n, size_t k, tg_weights **out);
+/* The same with values and scales already in device memory (read during the call only). */
+int tg_weights_upload_device(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *scales,
+                             size_t n_scales, uint32_t precision, size_t n, size_t k, tg_weights **out);
+void tg_weights_free(tg_weights *w);
+/* Bytes of weight data in the panel layout, scales included (PackedWeights::bytes). */
+size_t tg_weights_bytes(const tg_weights *w);
+size_t tg_weights_n(const tg_weights *w);
+size_t tg_weights_k(const tg_weights *w);
+uint32_t tg_weights_precision(const tg_weights *w);
+
+/* ---- the matrix product ------------------------------------------------------------------- */
+
+/* c[m, n] = epilogue(a[m, k] * w^T) with a rows lda apart and c rows ldc apart. Host pointers;
+ * copies a (and c when accumulating) to the device, runs, copies c back, and returns when done.
+ * a_len and c_len are the lengths of the caller's slices, as the reference checks them. */
+int tg_matmul(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w, float *c,
+              size_t c_len, size_t ldc, const tg_epilogue *epi);
+/* tg_matmul with lda = k and ldc = n. */
+int tg_linear(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *c, size_t c_len,
+              const tg_epilogue *epi);
+
+/* The same on device pointers, queued on the context's stream and returning at once. Buffers
+ * must stay valid until the stream reaches the work (tg_synchronize). a and c must not overlap. */
+int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w,
+                     float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
+int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *c,
+                     size_t c_len, const tg_epilogue *epi);
+
+/* ---- row kernels -------------------------------------------------------------------------- */
+
+/* out[r, j] = x[r, j] * sigmoid(x[r, half + j]) for j < half (the GLU of a convolution module),
+ * with the exp of the reference's SIMD kernels. Device pointers, queued on the stream. */
+int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo);
+
+/* ---- the panel layout (host utilities, no device needed) ---------------------------------- */
+
+size_t tg_panel_bytes(uint32_t precision, size_t n, size_t k);
+size_t tg_scale_count(uint32_t precision, size_t n, size_t k);
+int tg_fits(uint32_t precision, size_t k);
+/* quant::encode of row-major f32 rows w[n][k] (Rows::F32). */
+int tg_encode(const float *w, size_t n, size_t k, uint32_t precision, uint8_t *values, size_t values_len,
+              float *scales, size_t n_scales);
+/* quant::decode into row-major out[n][k]. */
+int tg_decode(const uint8_t *values, size_t values_len, const float *scales, size_t n_scales, uint32_t precision,
+              size_t n, size_t k, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TELMO_HIP_H */

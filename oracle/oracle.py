@@ -1,0 +1,238 @@
+"""ctypes view of the oracle library (test infrastructure only).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this module,
+and only as the checker. The product (``telmo_amd``) never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+CPUBASE = os.path.join(HERE, "libcpubase.so")
+
+F32, F16, BF16, INT8, Q8_0 = range(5)
+NONE, RELU, SILU = range(3)
+EXP_NONFINITE = -(2**31)
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_sz = ctypes.c_size_t
+
+
+def build():
+    """Compile the oracle libraries in place (gcc/g++ only)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = ctypes.CDLL(LIB)
+        L.or_random.argtypes = [_f32p, _sz, ctypes.c_uint64]
+        L.or_value_bytes.argtypes = [ctypes.c_int]
+        L.or_value_bytes.restype = _sz
+        L.or_panel_bytes.argtypes = [ctypes.c_int, _sz, _sz]
+        L.or_panel_bytes.restype = _sz
+        L.or_scale_count.argtypes = [ctypes.c_int, _sz, _sz]
+        L.or_scale_count.restype = _sz
+        L.or_fits.argtypes = [ctypes.c_int, _sz]
+        L.or_f32_to_f16.argtypes = [ctypes.c_float]
+        L.or_f32_to_f16.restype = ctypes.c_uint16
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.or_f32_to_bf16.restype = ctypes.c_uint16
+        L.or_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_bf16_to_f32.restype = ctypes.c_float
+        L.or_quantize_q8_0_block.argtypes = [_f32p, _sz, _i8p]
+        L.or_quantize_q8_0_block.restype = ctypes.c_float
+        L.or_quantize_row_int8.argtypes = [_f32p, _sz, _i8p]
+        L.or_quantize_row_int8.restype = ctypes.c_float
+        L.or_encode_f32.argtypes = [_f32p, _sz, _sz, ctypes.c_int, _u8p, _f32p]
+        L.or_encode_q8.argtypes = [_f32p, _i8p, _sz, _sz, ctypes.c_int, _u8p, _f32p]
+        L.or_decode.argtypes = [_u8p, _f32p, _sz, _sz, ctypes.c_int, _f32p]
+        L.or_widen.argtypes = [ctypes.c_int, _sz, _u8p, _f32p, _f32p]
+        L.or_tile.argtypes = [ctypes.c_int, _sz, _f32p, _sz, _sz, _f32p, _sz, _f32p, ctypes.c_int]
+        L.or_exp_simd.argtypes = [ctypes.c_float]
+        L.or_exp_simd.restype = ctypes.c_float
+        L.or_silu_simd.argtypes = [ctypes.c_float]
+        L.or_silu_simd.restype = ctypes.c_float
+        L.or_store.argtypes = [ctypes.c_int, _f32p, _f32p, _sz, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
+                               ctypes.c_int]
+        mm = [_f32p, _sz, _sz, _sz, _u8p, ctypes.c_void_p, ctypes.c_int, _sz, _sz, _f32p, _sz, _sz,
+              ctypes.c_void_p, _sz, ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        L.or_matmul.argtypes = [ctypes.c_int] + mm
+        L.or_matmul_fast.argtypes = [_f32p, _sz, _sz, _sz, _u8p, _f32p, _sz, _sz, _f32p, _sz, _sz,
+                                     ctypes.c_void_p, _sz, ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        L.or_row_exponent.argtypes = [_f32p, _sz]
+        L.or_row_exponent.restype = ctypes.c_int32
+        L.or_quantize_rows.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _i8p, _i32p]
+        L.or_int_products.argtypes = [_i8p, _i8p, _sz, _sz, _i8p, _sz, _i32p, _i32p]
+        L.or_dequant.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float]
+        L.or_dequant.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _ptr(x):
+    return None if x is None else x.ctypes.data_as(ctypes.c_void_p)
+
+
+def random(length, seed):
+    """The reference's xorshift test generator: `length` values in [-1, 1)."""
+    out = np.empty(length, np.float32)
+    lib().or_random(out, length, seed)
+    return out
+
+
+def value_bytes(p):
+    return lib().or_value_bytes(p)
+
+
+def panel_bytes(p, n, k):
+    return lib().or_panel_bytes(p, n, k)
+
+
+def scale_count(p, n, k):
+    return lib().or_scale_count(p, n, k)
+
+
+def fits(p, k):
+    return bool(lib().or_fits(p, k))
+
+
+def f32_to_f16(x):
+    return lib().or_f32_to_f16(float(x))
+
+
+def f16_to_f32(h):
+    return np.float32(lib().or_f16_to_f32(int(h)))
+
+
+def f32_to_bf16(x):
+    return lib().or_f32_to_bf16(float(x))
+
+
+def bf16_to_f32(h):
+    return np.float32(lib().or_bf16_to_f32(int(h)))
+
+
+def quantize_q8_0_block(x):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.zeros(len(x), np.int8)
+    d = lib().or_quantize_q8_0_block(x, len(x), q)
+    return np.float32(d), q
+
+
+def quantize_row_int8(x):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.zeros(len(x), np.int8)
+    d = lib().or_quantize_row_int8(x, len(x), q)
+    return np.float32(d), q
+
+
+def encode(w, n, k, p):
+    """Row-major [n, k] f32 rows into the panel layout: (values u8, scales f32)."""
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    values = np.zeros(panel_bytes(p, n, k), np.uint8)
+    scales = np.zeros(max(scale_count(p, n, k), 1), np.float32)
+    rc = lib().or_encode_f32(w if w.size else np.zeros(1, np.float32), n, k, p, values if values.size else
+                             np.zeros(1, np.uint8), scales)
+    if rc != 0:
+        raise ValueError(f"encode failed ({rc})")
+    return values, scales[: scale_count(p, n, k)]
+
+
+def encode_q8(d, q, n, k, p):
+    """Q8_0 blocks (d: n*k/32 scales, q: n*k values) into the panel layout of precision p."""
+    d = np.ascontiguousarray(d, np.float32)
+    q = np.ascontiguousarray(q, np.int8)
+    values = np.zeros(max(panel_bytes(p, n, k), 1), np.uint8)
+    scales = np.zeros(max(scale_count(p, n, k), 1), np.float32)
+    rc = lib().or_encode_q8(d, q, n, k, p, values, scales)
+    if rc != 0:
+        raise ValueError(f"encode failed ({rc})")
+    return values[: panel_bytes(p, n, k)], scales[: scale_count(p, n, k)]
+
+
+def decode(values, scales, n, k, p):
+    out = np.zeros(max(n * k, 1), np.float32)
+    values = np.ascontiguousarray(values, np.uint8)
+    scales = np.ascontiguousarray(scales if scales is not None and len(scales) else np.zeros(1), np.float32)
+    lib().or_decode(values if values.size else np.zeros(1, np.uint8), scales, n, k, p, out)
+    return out[: n * k].reshape(n, k)
+
+
+def widen(p, k, src, scales):
+    out = np.zeros(max(k * 16, 1), np.float32)
+    scales = np.ascontiguousarray(scales if scales is not None and len(scales) else np.zeros(1), np.float32)
+    lib().or_widen(p, k, np.ascontiguousarray(src, np.uint8), scales, out)
+    return out[: k * 16].reshape(k, 16)
+
+
+def tile(fused, k, a, lda, rows, b, k_stride, out, load):
+    lib().or_tile(int(fused), k, a, lda, rows, b, k_stride, out, int(load))
+
+
+def exp_simd(x):
+    return np.float32(lib().or_exp_simd(float(x)))
+
+
+def silu_simd(x):
+    return np.float32(lib().or_silu_simd(float(x)))
+
+
+def store(fused, acc, c, cols, bias, act, scale, accumulate):
+    lib().or_store(int(fused), acc, c, cols, _ptr(bias), act, scale, int(accumulate))
+
+
+def matmul(fused, a, lda, m, values, scales, p, n, k, c, ldc, bias=None, act=NONE, scale=1.0,
+           accumulate=False):
+    """Kernels::matmul over packed weights, in place on `c`. Returns the status (0 or negative)."""
+    scales = None if scales is None or len(scales) == 0 else np.ascontiguousarray(scales, np.float32)
+    return lib().or_matmul(int(fused), a, a.size, lda, m, values, _ptr(scales), p, n, k, c, c.size, ldc,
+                           _ptr(bias), 0 if bias is None else bias.size, act, scale, int(accumulate))
+
+
+def matmul_fast(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, scale=1.0, accumulate=False):
+    """The integer oracle of the fast int8 path, in place on `c`."""
+    return lib().or_matmul_fast(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc, _ptr(bias),
+                                0 if bias is None else bias.size, act, scale, int(accumulate))
+
+
+def row_exponent(row):
+    row = np.ascontiguousarray(row, np.float32)
+    return lib().or_row_exponent(row if row.size else np.zeros(1, np.float32), row.size)
+
+
+def quantize_rows(a, lda, m, k):
+    hi = np.zeros(max(m * k, 1), np.int8)
+    lo = np.zeros(max(m * k, 1), np.int8)
+    ex = np.zeros(max(m, 1), np.int32)
+    lib().or_quantize_rows(a, lda, m, k, hi, lo, ex)
+    return hi[: m * k].reshape(m, k), lo[: m * k].reshape(m, k), ex[:m]
+
+
+def int_products(hi, lo, q):
+    """acc_hi, acc_lo [m, n] of digit planes [m, k] against int8 q [n, k]."""
+    m, k = hi.shape
+    n = q.shape[0]
+    acc_hi = np.zeros(max(m * n, 1), np.int32)
+    acc_lo = np.zeros(max(m * n, 1), np.int32)
+    lib().or_int_products(np.ascontiguousarray(hi), np.ascontiguousarray(lo), m, k, np.ascontiguousarray(q), n,
+                          acc_hi, acc_lo)
+    return acc_hi[: m * n].reshape(m, n), acc_lo[: m * n].reshape(m, n)
+
+
+def dequant(acc_hi, acc_lo, e, scale):
+    return np.float32(lib().or_dequant(int(acc_hi), int(acc_lo), int(e), float(scale)))

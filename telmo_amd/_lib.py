@@ -1,0 +1,55 @@
+"""Loads libtelmo_hip.so (built in place by telmo_amd.build) and declares its C ABI."""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtelmo_hip.so")
+
+_sz = ctypes.c_size_t
+_p = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+
+# name: (restype, argtypes), in the order of include/telmo_hip.h
+SIGNATURES = {
+    "tg_ctx_create": (ctypes.c_int, [ctypes.c_int, _p, ctypes.POINTER(_p)]),
+    "tg_ctx_destroy": (None, [_p]),
+    "tg_ctx_set_mode": (ctypes.c_int, [_p, _u32]),
+    "tg_ctx_mode": (_u32, [_p]),
+    "tg_last_error": (ctypes.c_char_p, [_p]),
+    "tg_synchronize": (ctypes.c_int, [_p]),
+    "tg_weights_upload": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _u32, _sz, _sz, ctypes.POINTER(_p)]),
+    "tg_weights_upload_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _u32, _sz, _sz, ctypes.POINTER(_p)]),
+    "tg_weights_free": (None, [_p]),
+    "tg_weights_bytes": (_sz, [_p]),
+    "tg_weights_n": (_sz, [_p]),
+    "tg_weights_k": (_sz, [_p]),
+    "tg_weights_precision": (_u32, [_p]),
+    "tg_matmul": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, _sz, _sz, _p]),
+    "tg_linear": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p]),
+    "tg_matmul_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, _sz, _sz, _p]),
+    "tg_linear_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p]),
+    "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
+    "tg_panel_bytes": (_sz, [_u32, _sz, _sz]),
+    "tg_scale_count": (_sz, [_u32, _sz, _sz]),
+    "tg_fits": (ctypes.c_int, [_u32, _sz]),
+    "tg_encode": (ctypes.c_int, [_p, _sz, _sz, _u32, _p, _sz, _p, _sz]),
+    "tg_decode": (ctypes.c_int, [_p, _sz, _p, _sz, _u32, _sz, _sz, _p]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library. Raises if it has not been built: there is no fallback."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m telmo_amd.build` "
+                               "(or __graft_entry__.build()); telmo_amd has no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib

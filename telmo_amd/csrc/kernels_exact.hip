@@ -1,0 +1,70 @@
+// The exact kernel: the reference's fused arithmetic on the GPU, for validation and for callers
+// that need bit-identity with telmo's SIMD CPU kernels.
+//
+// One lane per output sums acc = fmaf(a[r][i], widen(w)[o][i], acc) for i = 0..k-1 in order
+// (src/kernels/avx512.rs:70-105 and 156-213: input-order fused sums), with widen as
+// src/kernels/scalar.rs:54-107 (int8: one rounded product q * scale), then the shared epilogue,
+// which uses the reference's SIMD exp. Any precision; weights in the device layout.
+#include "tg_internal.hpp"
+
+namespace tg {
+
+namespace {
+
+__device__ __forceinline__ float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+    const uint32_t exp = (h >> 10) & 0x1f, man = h & 0x3ff;
+    if (exp == 0) {
+        if (man == 0) return __uint_as_float(sign);
+        const float v = (float)man * (1.0f / 16777216.0f);
+        return sign ? -v : v;
+    }
+    if (exp == 0x1f) return __uint_as_float(sign | 0x7f800000u | (man ? 0x400000u | (man << 13) : 0u));
+    return __uint_as_float(sign | ((exp + 112) << 23) | (man << 13));
+}
+
+__device__ __forceinline__ float widen_one(const uint8_t *__restrict__ wv, const float *__restrict__ scales,
+                                           uint32_t prec, size_t k, size_t kb, size_t p, int j, size_t i) {
+    switch (prec) {
+    case F32: return reinterpret_cast<const float *>(wv)[(p * k + i) * PANEL + j];
+    case F16: return half_to_float(reinterpret_cast<const uint16_t *>(wv)[(p * k + i) * PANEL + j]);
+    case BF16: return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(wv)[(p * k + i) * PANEL + j] << 16);
+    default: {
+        const size_t t = i / KBLK, g = (i % KBLK) / 16, ii = i % 16;
+        const int8_t q = (int8_t)wv[((p * kb + t) * 64 + g * 16 + j) * 16 + ii];
+        const float s = prec == INT8 ? scales[p * PANEL + j]
+                                     : scales[(p * div_ceil(k, Q8_BLOCK) + i / Q8_BLOCK) * PANEL + j];
+        return (float)q * s;
+    }
+    }
+}
+
+__global__ __launch_bounds__(256) void exact_kernel(const float *__restrict__ a, size_t lda, int m, int k,
+                                                    const uint8_t *__restrict__ wv, const float *__restrict__ scales,
+                                                    uint32_t prec, int N, int KB, float *__restrict__ c, size_t ldc,
+                                                    const float *__restrict__ bias, uint32_t act, float escale,
+                                                    int accumulate) {
+    const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (row >= m || col >= N) return;
+    const size_t p = col / PANEL;
+    const int j = col % PANEL;
+    const float *ar = a + (size_t)row * lda;
+    float acc = 0.0f;
+    for (int i = 0; i < k; i++) acc = __builtin_fmaf(ar[i], widen_one(wv, scales, prec, k, KB, p, j, i), acc);
+    float *cp = c + (size_t)row * ldc + col;
+    *cp = epilogue(acc, bias, (size_t)col, act, escale, accumulate != 0, cp);
+}
+
+}  // namespace
+
+hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                        const EpiArgs &epi, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    dim3 grid((unsigned)div_ceil(w.n, 64), (unsigned)div_ceil(m, 4));
+    hipLaunchKernelGGL(exact_kernel, grid, dim3(256), 0, s, a, lda, (int)m, (int)w.k, w.values, w.scales,
+                       w.precision, (int)w.n, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale, epi.accumulate);
+    return hipGetLastError();
+}
+
+}  // namespace tg

@@ -1,0 +1,117 @@
+// Row kernels of the int8 path: the one-time re-layout of int8 / Q8_0 weight panels into the
+// MFMA layout, the per-row two-digit quantisation of f32 activations, and the GLU row kernel.
+// All of them are HBM-bound byte work: coalesced loads, no MFMA.
+#include "tg_internal.hpp"
+
+namespace tg {
+
+// One workgroup of 64 lanes per (panel, k-block): the 64 input rows of 16 outputs (1 KB,
+// contiguous in telmo's layout) go through LDS, and each lane writes the 16 inputs of one
+// output that its MFMA operand needs, 16 contiguous bytes.
+__global__ __launch_bounds__(64) void repack_i8_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                       size_t k, size_t kb) {
+    __shared__ uint8_t tile[KBLK][PANEL + 4];
+    const size_t blk = blockIdx.x;  // p * kb + t
+    const size_t p = blk / kb, t = blk % kb;
+    const int l = threadIdx.x;
+    const size_t kk = t * KBLK + l;
+    uint32_t v[4] = {0, 0, 0, 0};
+    if (kk < k) {
+        const uint32_t *s = reinterpret_cast<const uint32_t *>(src + (p * k + kk) * PANEL);
+        for (int i = 0; i < 4; i++) v[i] = s[i];
+    }
+    for (int i = 0; i < 4; i++)
+        for (int b = 0; b < 4; b++) tile[l][4 * i + b] = (uint8_t)(v[i] >> (8 * b));
+    __syncthreads();
+    const int g = l >> 4, j = l & 15;
+    uint32_t o[4];
+    for (int i = 0; i < 4; i++) {
+        o[i] = 0;
+        for (int b = 0; b < 4; b++) o[i] |= (uint32_t)tile[16 * g + 4 * i + b][j] << (8 * b);
+    }
+    uint4 out = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<uint4 *>(dst + (blk * 64 + l) * 16) = out;
+}
+
+hipError_t launch_repack_i8(const uint8_t *src, uint8_t *dst, size_t panels, size_t k, size_t kb, hipStream_t s) {
+    if (panels == 0 || kb == 0) return hipSuccess;
+    hipLaunchKernelGGL(repack_i8_kernel, dim3((unsigned)(panels * kb)), dim3(64), 0, s, src, dst, k, kb);
+    return hipGetLastError();
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_or(int v) {
+    for (int off = 32; off > 0; off >>= 1) v |= __shfl_xor(v, off, 64);
+    return v;
+}
+
+// One wavefront per row: the largest magnitude (and any NaN or infinity) over the row's k
+// inputs, the row exponent, then the digits of each input. Lane l writes the digits of inputs
+// 64 t + l, so each wave store is 64 contiguous bytes of the QA row.
+__device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ ar, size_t k, size_t kb,
+                                                     uint8_t *__restrict__ q, int lane) {
+    float amax = 0.0f;
+    int bad = 0;
+    for (size_t i = lane; i < k; i += 64) {
+        float x = ar[i];
+        bad |= !__builtin_isfinite(x);
+        amax = fmaxf(amax, fabsf(x));
+    }
+    amax = wave_max(amax);
+    bad = wave_or(bad);
+    const int32_t e = bad ? EXP_NONFINITE : row_exponent_of(amax);
+    for (size_t t = 0; t < kb; t++) {
+        const size_t i = t * KBLK + lane;
+        int8_t hi = 0, lo = 0;
+        if (i < k) digits_of(ar[i], e, hi, lo);
+        q[t * 128 + lane] = (uint8_t)hi;
+        q[t * 128 + 64 + lane] = (uint8_t)lo;
+    }
+    return e;
+}
+
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restrict__ a, size_t lda, size_t m,
+                                                            size_t k, size_t kb, uint8_t *__restrict__ qa,
+                                                            int32_t *__restrict__ exps) {
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa + row * kb * 128, lane);
+    if (lane == 0) exps[row] = e;
+}
+
+hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
+                                hipStream_t s) {
+    if (m == 0) return hipSuccess;
+    size_t kb = div_ceil(k, KBLK);
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)div_ceil(m, 4)), dim3(256), 0, s, a, lda, m, k, kb, qa,
+                       exps);
+    return hipGetLastError();
+}
+
+// out = a * sigmoid(b) as the reference's SIMD glu computes it: a / (1 + exp(0 - b))
+// (src/kernels/avx512.rs:370-385).
+__global__ __launch_bounds__(256) void glu_kernel(const float *__restrict__ x, size_t ldx, size_t m, size_t half,
+                                                  float *__restrict__ out, size_t ldo) {
+    const size_t total = m * half;
+    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+        const size_t r = idx / half, j = idx % half;
+        const float av = x[r * ldx + j], bv = x[r * ldx + half + j];
+        out[r * ldo + j] = av / (1.0f + exp_simd(0.0f - bv));
+    }
+}
+
+hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s) {
+    size_t total = m * half;
+    if (total == 0) return hipSuccess;
+    size_t blocks = div_ceil(total, 256);
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(glu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, ldx, m, half, out, ldo);
+    return hipGetLastError();
+}
+
+}  // namespace tg

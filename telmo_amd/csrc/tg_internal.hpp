@@ -1,0 +1,155 @@
+// Shared definitions of the MI355X int8-weight matrix product: device layouts, the dequantisation
+// and epilogue arithmetic every kernel shares, and the launchers each kernel file provides.
+//
+// Everything here is compiled with -ffp-contract=off: a product followed by a sum is two
+// roundings unless written as __builtin_fmaf, so results match the reference bit for bit where
+// the arithmetic is the same.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstddef>
+
+namespace tg {
+
+// Outputs per weight panel (src/kernels/mod.rs:29) and inputs per Q8_0 block (src/quant.rs:17).
+constexpr int PANEL = 16;
+constexpr int Q8_BLOCK = 32;
+// Inputs per MFMA k-block of the device layout.
+constexpr int KBLK = 64;
+// Largest |v| of a 15-bit activation split into two signed int8 digits v = 256 hi + lo.
+constexpr float DIGIT_MAX = 32639.0f;
+// Exponent marking a row that holds a NaN or an infinity: its sums are NaN.
+constexpr int32_t EXP_NONFINITE = INT32_MIN;
+// Longest k the integer path takes: |sum of hi * q| < 2^14 * k stays below 2^31.
+constexpr size_t MAX_K_INT = 65536;
+
+enum Precision : uint32_t { F32 = 0, F16 = 1, BF16 = 2, INT8 = 3, Q8_0 = 4 };
+enum Act : uint32_t { ACT_NONE = 0, ACT_RELU = 1, ACT_SILU = 2 };
+
+__host__ __device__ inline size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+
+// Device copy of a weight matrix.
+//   f32 / f16 / bf16: telmo's panel layout unchanged: value (o, i) at ((o/16 * k + i) * 16 + o%16).
+//   int8 / Q8_0: the "MFMA layout": per panel p and k-block t of 64 inputs, 1024 bytes in lane
+//     order, lane l = 16 g + j holding the 16 inputs 64 t + 16 g + [0, 16) of output 16 p + j.
+//     Inputs past k are zero. One 16-byte load per lane is then the operand of an i8 MFMA
+//     (16x16x64) for both the GEMM and the dot4 GEMV.
+//   scales: unchanged ([panels * 16] for int8, [panels * blocks * 16] for Q8_0).
+struct DeviceWeights {
+    size_t n, k;
+    uint32_t precision;
+    size_t panels;   // ceil(n / 16)
+    size_t kb;       // ceil(k / 64): k-blocks of the MFMA layout
+    uint8_t *values; // device
+    float *scales;   // device, or null
+    size_t values_bytes, n_scales;
+};
+
+// Quantised activations ("QA"): per row, kb blocks of 128 bytes: the hi digits of inputs
+// 64 t + [0, 64) then their lo digits. Digits of inputs past k are zero.
+inline size_t qa_row_bytes(size_t k) { return div_ceil(k, KBLK) * 128; }
+
+// ---------------------------------------------------------------------------- device arithmetic
+
+// e^x in the steps of the reference's SIMD exp (src/kernels/avx512.rs:279-304): clamp, n =
+// rint(x log2 e), a two-part reduction, a degree-6 fused polynomial, times 2^n from the exponent
+// bits. x86 max/min return their second operand when either is NaN; fmaxf/fminf of (x, c) return
+// c for a NaN x as well.
+__device__ __forceinline__ float exp_simd(float x) {
+    x = fminf(fmaxf(x, -87.33654f), 88.37626f);
+    float n = __builtin_rintf(x * 1.44269504088896340736f);
+    float r = __builtin_fmaf(-n, 0.6933594f, x);
+    r = __builtin_fmaf(-n, -2.1219444e-4f, r);
+    float p = 1.9875691e-4f;
+    p = __builtin_fmaf(p, r, 1.3982e-3f);
+    p = __builtin_fmaf(p, r, 8.333452e-3f);
+    p = __builtin_fmaf(p, r, 4.1665796e-2f);
+    p = __builtin_fmaf(p, r, 0.16666665f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r * r, r);
+    p = p + 1.0f;
+    float pow2n = __uint_as_float((uint32_t)((int32_t)n + 127) << 23);
+    return p * pow2n;
+}
+
+// The epilogue of one output (src/kernels/avx512.rs:313-343): bias, activation, scale, then
+// accumulate onto the old value. ReLU is x86 MAXPS(v, 0): v if v > 0, else 0.
+__device__ __forceinline__ float epilogue(float v, const float *bias, size_t col, uint32_t act, float scale,
+                                          bool accumulate, const float *cptr) {
+    if (bias) v = v + bias[col];
+    if (act == ACT_RELU) {
+        v = v > 0.0f ? v : 0.0f;
+    } else if (act == ACT_SILU) {
+        v = v / (1.0f + exp_simd(0.0f - v));
+    }
+    v = v * scale;
+    if (accumulate) v = *cptr + v;
+    return v;
+}
+
+// The f32 sum of the integer path: S = 256 acc_hi + acc_lo exactly, one rounding to f32, times
+// the output's scale, then the exact power-of-two unscaling of the row. "+ 0" makes an exact
+// zero +0 whatever the scale's sign, as the reference's sums start at +0.
+__device__ __forceinline__ float dequant(int32_t acc_hi, int32_t acc_lo, int32_t e, float scale) {
+    if (e == EXP_NONFINITE) return __builtin_nanf("");
+    long long s = (long long)acc_hi * 256 + acc_lo;
+    float u = (float)s * scale + 0.0f;
+    return __builtin_ldexpf(u, -e);
+}
+
+// The row exponent e: the largest with max|a| * 2^e <= DIGIT_MAX, from the bits of amax
+// (positive, finite) so that subnormals are handled exactly.
+__device__ __forceinline__ int32_t row_exponent_of(float amax) {
+    if (amax == 0.0f) return 0;
+    uint32_t b = __float_as_uint(amax);
+    int32_t be = (int32_t)(b >> 23);
+    int32_t E = be == 0 ? (31 - __builtin_clz(b & 0x7fffff)) - 148 : be - 126;
+    int32_t e = 15 - E;
+    if (__builtin_ldexpf(amax, e) > DIGIT_MAX) e -= 1;
+    return e;
+}
+
+// The two digits of one activation under exponent e: v = rint(a 2^e) = 256 hi + lo.
+__device__ __forceinline__ void digits_of(float a, int32_t e, int8_t &hi, int8_t &lo) {
+    int32_t v = e == EXP_NONFINITE ? 0 : (int32_t)__builtin_rintf(__builtin_ldexpf(a, e));
+    int32_t l = ((v + 128) & 255) - 128;
+    hi = (int8_t)((v - l) >> 8);
+    lo = (int8_t)l;
+}
+
+// ---------------------------------------------------------------------------- launchers
+
+struct EpiArgs {
+    const float *bias;  // device or null
+    uint32_t act;
+    float scale;
+    int accumulate;
+};
+
+// Re-lays int8 / Q8_0 panel values (device, telmo's layout) into the MFMA layout.
+hipError_t launch_repack_i8(const uint8_t *src, uint8_t *dst, size_t panels, size_t k, size_t kb, hipStream_t s);
+
+// Per-row digits and exponents of a[m][lda] (k inputs) into qa / exps.
+hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
+                                hipStream_t s);
+
+// out[r][j] = x[r][j] * sigmoid(x[r][half + j]).
+hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s);
+
+// The two-digit int8 MFMA GEMM over quantised rows.
+hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
+                          size_t ldc, const EpiArgs &epi, hipStream_t s);
+
+// The dot4 GEMV for m <= 8 (quantises the rows itself).
+constexpr size_t GEMV_MAX_ROWS = 8;
+bool gemv_fits(size_t m, size_t k);
+hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                          const EpiArgs &epi, hipStream_t s);
+
+// The exact kernel: the reference's fused sums in input order, any precision.
+hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                        const EpiArgs &epi, hipStream_t s);
+
+}  // namespace tg

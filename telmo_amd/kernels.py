@@ -1,0 +1,269 @@
+"""Python mirror of telmo's matrix-product operator surface over the HIP library's C ABI.
+
+Names, argument meanings and refusals follow the reference:
+
+* ``Precision`` - src/quant.rs:20-83 (``name``, ``from_name``, ``value_bytes``, ``panel_bytes``,
+  ``scale_count``, ``fits``)
+* ``Act``, ``Epilogue`` - src/kernels/mod.rs:366-398 (``Epilogue.PLAIN``, ``Epilogue.bias``)
+* ``PackedWeights`` - src/kernels/mod.rs:173-304 (``from_rows``, ``encode``, ``from_parts``,
+  ``n``/``k``/``precision``, ``bytes``, ``to_rows``)
+* ``Kernels.linear`` / ``Kernels.matmul`` - src/kernels/mod.rs:657-701
+
+Where the reference panics on a violated precondition, these raise ``TelmoError`` with the
+library's status code. Host arrays are numpy float32; the ``*_device`` methods take torch tensors
+already on the GPU and queue the work on the context's stream. The library must be built
+(``telmo_amd.build``): nothing here falls back to the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+
+
+class TelmoError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{message} (status {code})")
+        self.code = code
+
+
+class Precision(enum.IntEnum):
+    F32 = 0
+    F16 = 1
+    BF16 = 2
+    INT8 = 3
+    Q8_0 = 4
+
+    def name_(self) -> str:
+        return ["f32", "f16", "bf16", "int8", "q8_0"][self]
+
+    @staticmethod
+    def from_name(name: str) -> Optional["Precision"]:
+        for p in Precision:
+            if p.name_() == name:
+                return p
+        return None
+
+    def value_bytes(self) -> int:
+        return {0: 4, 1: 2, 2: 2, 3: 1, 4: 1}[int(self)]
+
+    def panel_bytes(self, n: int, k: int) -> int:
+        return _lib.lib().tg_panel_bytes(int(self), n, k)
+
+    def scale_count(self, n: int, k: int) -> int:
+        return _lib.lib().tg_scale_count(int(self), n, k)
+
+    def fits(self, k: int) -> bool:
+        return bool(_lib.lib().tg_fits(int(self), k))
+
+
+class Act(enum.IntEnum):
+    NONE = 0
+    RELU = 1
+    SILU = 2
+
+
+@dataclass
+class Epilogue:
+    """c = (accumulate ? c : 0) + scale * act(sum + bias)."""
+
+    bias: Optional[object] = None
+    act: Act = Act.NONE
+    scale: float = 1.0
+    accumulate: bool = False
+
+    @staticmethod
+    def with_bias(bias) -> "Epilogue":
+        return Epilogue(bias=bias)
+
+
+Epilogue.PLAIN = Epilogue()
+
+
+def _f32(x) -> np.ndarray:
+    arr = np.asarray(x)
+    if arr.dtype != np.float32 or not arr.flags.c_contiguous:
+        raise TypeError("host buffers must be C-contiguous float32 arrays")
+    return arr
+
+
+def _check(code: int, ctx) -> None:
+    if code != 0:
+        msg = _lib.lib().tg_last_error(ctx).decode() if ctx else "error"
+        raise TelmoError(code, msg or "telmo_hip call failed")
+
+
+class PackedWeights:
+    """A weight matrix of n outputs and k inputs, uploaded once to the context's device."""
+
+    def __init__(self, kernels: "Kernels", handle, n: int, k: int, precision: Precision):
+        self._kernels = kernels
+        self._handle = handle
+        self._n, self._k, self._precision = n, k, Precision(precision)
+
+    @staticmethod
+    def from_parts(kernels: "Kernels", n: int, k: int, precision: Precision, values, scales=None):
+        """Weights already in the panel layout, as a pack stores them (host numpy arrays)."""
+        values = np.ascontiguousarray(values, np.uint8)
+        sc = None if scales is None else _f32(np.ascontiguousarray(scales, np.float32))
+        out = ctypes.c_void_p()
+        L = _lib.lib()
+        rc = L.tg_weights_upload(kernels._ctx, values.ctypes.data_as(ctypes.c_void_p), values.size,
+                                 None if sc is None else sc.ctypes.data_as(ctypes.c_void_p),
+                                 0 if sc is None else sc.size, int(precision), n, k, ctypes.byref(out))
+        _check(rc, kernels._ctx)
+        return PackedWeights(kernels, out, n, k, precision)
+
+    @staticmethod
+    def encode(kernels: "Kernels", rows, n: int, k: int, precision: Precision):
+        """Packs row-major [n, k] f32 rows in `precision`, quantising or rounding as needed."""
+        values, scales = encode(rows, n, k, precision)
+        return PackedWeights.from_parts(kernels, n, k, precision, values, scales if scales.size else None)
+
+    @staticmethod
+    def from_rows(kernels: "Kernels", rows, n: int, k: int):
+        return PackedWeights.encode(kernels, rows, n, k, Precision.F32)
+
+    def n(self) -> int:
+        return self._n
+
+    def k(self) -> int:
+        return self._k
+
+    def precision(self) -> Precision:
+        return self._precision
+
+    def bytes(self) -> int:
+        return _lib.lib().tg_weights_bytes(self._handle)
+
+    def close(self) -> None:
+        if self._handle:
+            _lib.lib().tg_weights_free(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def encode(rows, n: int, k: int, precision: Precision):
+    """quant::encode of row-major f32 rows: (values u8, scales f32) in the panel layout."""
+    rows = _f32(np.ascontiguousarray(rows, np.float32).reshape(-1))
+    p = Precision(precision)
+    values = np.zeros(p.panel_bytes(n, k), np.uint8)
+    scales = np.zeros(p.scale_count(n, k), np.float32)
+    rc = _lib.lib().tg_encode(rows.ctypes.data_as(ctypes.c_void_p), n, k, int(p),
+                              values.ctypes.data_as(ctypes.c_void_p), values.size,
+                              scales.ctypes.data_as(ctypes.c_void_p), scales.size)
+    _check(rc, None)
+    return values, scales
+
+
+def decode(values, scales, n: int, k: int, precision: Precision) -> np.ndarray:
+    """quant::decode: the row-major [n, k] values a stored matrix stands for."""
+    values = np.ascontiguousarray(values, np.uint8)
+    scales = np.ascontiguousarray(scales if scales is not None else np.zeros(0), np.float32)
+    out = np.zeros(n * k, np.float32)
+    rc = _lib.lib().tg_decode(values.ctypes.data_as(ctypes.c_void_p), values.size,
+                              scales.ctypes.data_as(ctypes.c_void_p), scales.size, int(precision), n, k,
+                              out.ctypes.data_as(ctypes.c_void_p))
+    _check(rc, None)
+    return out.reshape(n, k)
+
+
+class _Epi(ctypes.Structure):
+    _fields_ = [("bias", ctypes.c_void_p), ("bias_len", ctypes.c_size_t), ("act", ctypes.c_uint32),
+                ("scale", ctypes.c_float), ("accumulate", ctypes.c_int32)]
+
+
+class Kernels:
+    """The GPU matrix-product entry points of one device and stream (one C-ABI context)."""
+
+    FAST = 0
+    EXACT = 1
+
+    def __init__(self, device: int = 0, stream: Optional[int] = None, mode: int = FAST):
+        L = _lib.lib()
+        ctx = ctypes.c_void_p()
+        rc = L.tg_ctx_create(device, ctypes.c_void_p(stream) if stream else None, ctypes.byref(ctx))
+        if rc != 0:
+            raise TelmoError(rc, f"no gfx950 context on device {device}")
+        self._ctx = ctx
+        self.set_mode(mode)
+
+    def set_mode(self, mode: int) -> None:
+        _check(_lib.lib().tg_ctx_set_mode(self._ctx, mode), self._ctx)
+
+    def mode(self) -> int:
+        return _lib.lib().tg_ctx_mode(self._ctx)
+
+    def close(self) -> None:
+        if self._ctx:
+            _lib.lib().tg_ctx_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- host buffers ---------------------------------------------------------------------
+    def _epi_host(self, epi: Optional[Epilogue], keep):
+        if epi is None:
+            return None
+        e = _Epi()
+        if epi.bias is not None:
+            b = _f32(epi.bias)
+            keep.append(b)
+            e.bias, e.bias_len = b.ctypes.data, b.size
+        e.act, e.scale, e.accumulate = int(epi.act), float(epi.scale), int(bool(epi.accumulate))
+        return ctypes.byref(e)
+
+    def matmul(self, a, lda: int, m: int, w: PackedWeights, c, ldc: int, epi: Epilogue = Epilogue.PLAIN):
+        """c[m, n] = epilogue(a[m, k] * w^T) with a rows lda apart and c rows ldc apart, in place."""
+        a, c = _f32(a), _f32(c)
+        keep = []
+        rc = _lib.lib().tg_matmul(self._ctx, a.ctypes.data_as(ctypes.c_void_p), a.size, lda, m, w._handle,
+                                  c.ctypes.data_as(ctypes.c_void_p), c.size, ldc, self._epi_host(epi, keep))
+        _check(rc, self._ctx)
+
+    def linear(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
+        """c = epilogue(a * w^T) for contiguous a [m, k] and c [m, n], in place."""
+        self.matmul(a, w.k(), m, w, c, w.n(), epi)
+
+    # -- device buffers (torch tensors) -----------------------------------------------------
+    def _epi_dev(self, epi: Optional[Epilogue]):
+        if epi is None:
+            return None
+        e = _Epi()
+        if epi.bias is not None:
+            e.bias, e.bias_len = epi.bias.data_ptr(), epi.bias.numel()
+        e.act, e.scale, e.accumulate = int(epi.act), float(epi.scale), int(bool(epi.accumulate))
+        return ctypes.byref(e)
+
+    def matmul_device(self, a, lda: int, m: int, w: PackedWeights, c, ldc: int, epi: Epilogue = Epilogue.PLAIN,
+                      a_len: Optional[int] = None, c_len: Optional[int] = None):
+        """Queues the product on GPU tensors (float32). a_len / c_len default to the tensors' sizes."""
+        rc = _lib.lib().tg_matmul_device(self._ctx, ctypes.c_void_p(a.data_ptr()), a.numel() if a_len is None
+                                         else a_len, lda, m, w._handle, ctypes.c_void_p(c.data_ptr()),
+                                         c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
+        _check(rc, self._ctx)
+
+    def linear_device(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
+        self.matmul_device(a, w.k(), m, w, c, w.n(), epi)
+
+    def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int):
+        rc = _lib.lib().tg_glu_device(self._ctx, ctypes.c_void_p(x.data_ptr()), ldx, m, half,
+                                      ctypes.c_void_p(out.data_ptr()), ldo)
+        _check(rc, self._ctx)
+
+    def synchronize(self) -> None:
+        _check(_lib.lib().tg_synchronize(self._ctx), self._ctx)

@@ -1,0 +1,106 @@
+"""The C ABI without a GPU: the library loads, exports every entry point include/telmo_hip.h
+declares, its host layout utilities match the oracle bit for bit, and its refusals follow the
+reference's preconditions."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "telmo_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_the_library_exports_every_declared_entry_point():
+    from telmo_amd import _lib
+
+    names = declared_functions()
+    assert len(names) >= 20
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in names:
+        assert hasattr(raw, name), name
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+
+
+def test_sizes_match_the_reference_layout(orc):
+    from telmo_amd import Precision
+
+    for p in Precision:
+        for n, k in [(1, 1), (16, 32), (37, 64), (8198, 640), (4096, 1024)]:
+            assert p.panel_bytes(n, k) == orc.panel_bytes(int(p), n, k)
+            assert p.scale_count(n, k) == orc.scale_count(int(p), n, k)
+        assert p.fits(64) and p.fits(33) == (p != Precision.Q8_0)
+    assert Precision.from_name("q8_0") == Precision.Q8_0 and Precision.from_name("int4") is None
+
+
+def test_host_encode_and_decode_match_the_oracle(orc):
+    from telmo_amd import Precision, decode, encode
+
+    for n, k in [(37, 64), (5, 7), (20, 96), (1, 1)]:
+        i = np.arange(n * k)
+        w = (orc.random(n * k, 5) * (1 + i // max(k, 1)).astype(np.float32)).astype(np.float32)
+        w[::17] = 0.0
+        for p in Precision:
+            if not p.fits(k):
+                continue
+            v1, s1 = encode(w, n, k, p)
+            v2, s2 = orc.encode(w, n, k, int(p))
+            assert np.array_equal(v1, v2), (p, n, k)
+            assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32)), (p, n, k)
+            d1 = decode(v1, s1, n, k, p)
+            d2 = orc.decode(v2, s2, n, k, int(p))
+            assert np.array_equal(d1.view(np.uint32), d2.view(np.uint32)), (p, n, k)
+
+
+def test_special_values_encode_like_the_oracle(orc):
+    from telmo_amd import Precision, encode
+
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65520.0, 65519.0, 2.0**-24, 2.0**-25,
+                         1.5 * 2.0**-25, 3.4e38, 1e-40, -7.5, 1.0 + 2.0**-11] + [0.0] * 2, np.float32)
+    for p in (Precision.F16, Precision.BF16):
+        v1, _ = encode(specials, 1, specials.size, p)
+        v2, _ = orc.encode(specials, 1, specials.size, int(p))
+        assert np.array_equal(v1, v2), p
+
+
+def test_encode_refuses_what_the_reference_refuses():
+    from telmo_amd import Precision, TelmoError, encode
+
+    with pytest.raises(TelmoError):
+        encode(np.zeros(3 * 65, np.float32), 3, 65, Precision.Q8_0)
+
+
+def test_entry_points_refuse_null_contexts_without_a_gpu():
+    from telmo_amd import _lib
+
+    L = _lib.lib()
+    assert L.tg_ctx_set_mode(None, 0) == -1
+    assert L.tg_synchronize(None) == -1
+    assert L.tg_linear(None, None, 0, 0, None, None, 0, None) == -1
+    assert L.tg_matmul_device(None, None, 0, 0, 0, None, None, 0, 0, None) == -1
+    assert L.tg_last_error(None) == b"null context"
+    out = ctypes.c_void_p()
+    assert L.tg_ctx_create(0, None, None) == -1
+    assert L.tg_weights_bytes(None) == 0
+    L.tg_weights_free(None)
+    L.tg_ctx_destroy(None)
+    del out
+
+
+def test_no_gpu_means_a_clean_error_not_a_fallback():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from telmo_amd import Kernels, TelmoError
+
+    with pytest.raises(TelmoError):
+        Kernels()

@@ -1,0 +1,263 @@
+"""Parity of the HIP path with the oracle, through the C ABI, on an MI355X.
+
+* Exact mode: bit-identical to the reference's fused arithmetic (src/kernels/avx512.rs tile and
+  store, mod.rs gemm_panels) for every precision, shape and epilogue.
+* Fast mode, int8 weights: bit-identical to the integer oracle (two int8 digits, exact i32 sums,
+  one dequantisation), and within 1e-4 row-normwise of the reference's fused f32 sums (gate 1e-3).
+* The GEMV (m <= 8) and GEMM paths give the same bits for the same row.
+"""
+import numpy as np
+import pytest
+
+from helpers import int8_weights, normal, pack_int8, rel_norm_err
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16, INT8, Q8_0 = range(5)
+NONE, RELU, SILU = range(3)
+EPIS = [(NONE, False, False), (RELU, False, True), (SILU, True, True), (NONE, True, False)]
+
+
+def say(*args):
+    print("[case]", *args, flush=True)
+
+
+@pytest.fixture(scope="module")
+def tk():
+    import telmo_amd
+
+    k = telmo_amd.Kernels()
+    yield k
+    k.close()
+
+
+def epi_of(telmo_amd, bias, act, accumulate, scale=0.5):
+    return telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act(act), scale=scale, accumulate=accumulate)
+
+
+def run_gpu(tk, a, lda, m, values, scales, p, n, k, c0, ldc, bias, act, acc, scale=0.5):
+    import telmo_amd
+
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision(p), values,
+                                           scales if scales is not None and len(scales) else None)
+    c = c0.copy()
+    tk.matmul(a, lda, m, w, c, ldc, epi_of(telmo_amd, bias, act, acc, scale))
+    w.close()
+    return c
+
+
+EXACT_SHAPES = [(1, 1, 1), (1, 7, 5), (5, 13, 17), (6, 64, 16), (7, 33, 31), (13, 100, 50), (64, 128, 96),
+                (3, 544, 40), (9, 64, 8198)]
+
+
+@pytest.mark.parametrize("p", [F32, F16, BF16, INT8, Q8_0])
+def test_exact_mode_is_bit_identical_to_the_fused_reference(tk, orc, p):
+    tk.set_mode(tk.EXACT)
+    try:
+        for m, k, n in EXACT_SHAPES:
+            if p == Q8_0 and k % 32:
+                continue
+            say("exact", p, m, k, n)
+            a = orc.random(m * k, 1)
+            w = orc.random(n * k, 2)
+            bias, c0 = orc.random(n, 3), orc.random(m * n, 4)
+            values, scales = orc.encode(w, n, k, p)
+            for act, acc, with_bias in EPIS:
+                b = bias if with_bias else None
+                want = c0.copy()
+                assert orc.matmul(True, a, k, m, values, scales, p, n, k, want, n, b, act, 0.5, acc) == 0
+                got = run_gpu(tk, a, k, m, values, scales, p, n, k, c0, n, b, act, acc)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (p, m, k, n, act)
+    finally:
+        tk.set_mode(tk.FAST)
+
+
+FAST_SHAPES = [(1, 1, 1), (3, 7, 5), (8, 64, 16), (9, 64, 16), (13, 100, 50), (64, 128, 96), (130, 1000, 255),
+               (200, 640, 8198), (257, 2048, 130), (1, 4096, 1024), (8, 1280, 2560)]
+
+
+@pytest.mark.parametrize("m,k,n", FAST_SHAPES)
+def test_fast_int8_is_bit_identical_to_its_integer_oracle(tk, orc, m, k, n):
+    rng = np.random.default_rng(m * 7919 + k * 31 + n)
+    a = normal(rng, m * k)
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    bias, c0 = normal(rng, n), normal(rng, m * n)
+    for act, acc, with_bias in EPIS:
+        say("fast", m, k, n, act, acc, with_bias)
+        b = bias if with_bias else None
+        want = c0.copy()
+        assert orc.matmul_fast(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc) == 0
+        got = run_gpu(tk, a, k, m, values, scales, INT8, n, k, c0, n, b, act, acc)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+        ref = c0.copy()
+        orc.matmul(True, a, k, m, values, scales, INT8, n, k, ref, n, b, act, 0.5, acc)
+        err = rel_norm_err(got.reshape(m, n), ref.reshape(m, n))
+        print(f"[err] m={m} k={k} n={n} act={act}: {err:.2e}")
+        assert err <= 1e-3
+
+
+def test_gemv_rows_equal_gemm_rows(tk):
+    import telmo_amd
+
+    rng = np.random.default_rng(11)
+    m, k, n = 64, 640, 8198
+    a = normal(rng, (m, k))
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    bias = normal(rng, n)
+    epi = telmo_amd.Epilogue(bias=bias)
+    say("gemv-vs-gemm", m, k, n)
+    full = np.zeros(m * n, np.float32)
+    tk.linear(a.reshape(-1), m, w, full, epi)
+    full = full.reshape(m, n)
+    for rows in range(1, 9):
+        for r0 in (0, 17, m - rows):
+            part = np.zeros(rows * n, np.float32)
+            tk.linear(np.ascontiguousarray(a[r0:r0 + rows]).reshape(-1), rows, w, part, epi)
+            assert np.array_equal(part.reshape(rows, n).view(np.uint32), full[r0:r0 + rows].view(np.uint32)), \
+                (rows, r0)
+    w.close()
+
+
+@pytest.mark.parametrize("m", [3, 40])
+def test_strides_leave_the_gaps_alone(tk, orc, m):
+    rng = np.random.default_rng(12)
+    k, n, lda, ldc = 100, 37, 130, 50
+    a = normal(rng, m * lda)
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    c0 = np.full(m * ldc, 7.25, np.float32)
+    for mode in (0, 1):
+        tk.set_mode(mode)
+        say("strides", m, mode)
+        want = c0.copy()
+        if mode == 0:
+            orc.matmul_fast(a, lda, m, values, scales, n, k, want, ldc, None, RELU, 2.0, True)
+        else:
+            orc.matmul(True, a, lda, m, values, scales, INT8, n, k, want, ldc, None, RELU, 2.0, True)
+        got = run_gpu(tk, a, lda, m, values, scales, INT8, n, k, c0, ldc, None, RELU, True, 2.0)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        assert np.all(got.reshape(m, ldc)[:, n:] == 7.25)
+    tk.set_mode(0)
+
+
+def test_empty_and_zero_k(tk):
+    import telmo_amd
+
+    say("empty")
+    w = telmo_amd.PackedWeights.from_parts(tk, 5, 0, telmo_amd.Precision.INT8, np.zeros(0, np.uint8),
+                                           np.zeros(16, np.float32))
+    bias = np.arange(5, dtype=np.float32) - 2
+    c = np.full(15, 9.0, np.float32)
+    tk.linear(np.zeros(1, np.float32), 3, w, c, telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act.RELU, scale=2.0))
+    assert np.array_equal(c.reshape(3, 5), np.tile(np.maximum(bias, 0) * 2, (3, 1)))
+    c = np.full(15, 9.0, np.float32)
+    tk.linear(np.zeros(1, np.float32), 0, w, c)  # m = 0: nothing happens
+    assert np.all(c == 9.0)
+    w.close()
+
+
+def test_refusals_follow_the_reference(tk):
+    import telmo_amd
+
+    rng = np.random.default_rng(13)
+    q, s = int8_weights(rng, 20, 64)
+    values, scales = pack_int8(q, s)
+    w = telmo_amd.PackedWeights.from_parts(tk, 20, 64, telmo_amd.Precision.INT8, values, scales)
+    a = np.zeros(3 * 64, np.float32)
+    c = np.zeros(3 * 20, np.float32)
+    say("refusals")
+    for args, code in [((a, 63, 3, w, c, 20), -2), ((a, 64, 3, w, c, 19), -2), ((a, 64, 4, w, c, 20), -2),
+                       ((a, 64, 3, w, c[:59], 20), -2)]:
+        with pytest.raises(telmo_amd.TelmoError) as e:
+            tk.matmul(*args)
+        assert e.value.code == code
+    with pytest.raises(telmo_amd.TelmoError) as e:
+        tk.linear(a, 3, w, c, telmo_amd.Epilogue(bias=np.zeros(19, np.float32)))
+    assert e.value.code == -2
+    with pytest.raises(telmo_amd.TelmoError) as e:
+        telmo_amd.PackedWeights.from_parts(tk, 20, 64, telmo_amd.Precision.INT8, values[:-1], scales)
+    assert e.value.code == -7
+    w.close()
+
+
+@pytest.mark.parametrize("m", [2, 30])
+def test_rows_with_nan_or_inf_give_nan_rows(tk, m):
+    import telmo_amd
+
+    rng = np.random.default_rng(14)
+    k, n = 128, 48
+    a = normal(rng, (m, k))
+    a[0, 5] = np.nan
+    a[1, 7] = np.inf
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    c = np.zeros(m * n, np.float32)
+    say("nonfinite", m)
+    tk.linear(a.reshape(-1), m, w, c)
+    c = c.reshape(m, n)
+    assert np.all(np.isnan(c[:2])) and np.all(np.isfinite(c[2:]))
+    w.close()
+
+
+def test_device_entry_points_match_host_ones(tk):
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(15)
+    for m, k, n in [(4, 640, 2560), (300, 1024, 1000)]:
+        a = normal(rng, (m, k))
+        q, s = int8_weights(rng, n, k)
+        values, scales = pack_int8(q, s)
+        bias = normal(rng, n)
+        w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+        host = normal(rng, m * n)
+        dev = torch.from_numpy(host.copy()).cuda()
+        epi = telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act.SILU, accumulate=True, scale=0.5)
+        say("device", m, k, n)
+        tk.linear(a.reshape(-1), m, w, host, epi)
+        tk.linear_device(torch.from_numpy(a).cuda(), m, w, dev,
+                         telmo_amd.Epilogue(bias=torch.from_numpy(bias).cuda(), act=telmo_amd.Act.SILU,
+                                            accumulate=True, scale=0.5))
+        tk.synchronize()
+        assert np.array_equal(dev.cpu().numpy().view(np.uint32), host.view(np.uint32))
+        w.close()
+
+
+def test_glu_matches_the_reference_steps(tk, orc):
+    import torch
+
+    rng = np.random.default_rng(16)
+    m, half = 7, 300
+    x = normal(rng, (m, 2 * half)) * np.float32(6.0)
+    out = torch.zeros((m, half), dtype=torch.float32, device="cuda")
+    say("glu")
+    tk.glu_device(torch.from_numpy(x).cuda(), 2 * half, m, half, out, half)
+    tk.synchronize()
+    got = out.cpu().numpy()
+    want = np.array([[x[r, j] / (np.float32(1.0) + orc.exp_simd(np.float32(0.0) - x[r, half + j]))
+                      for j in range(half)] for r in range(m)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_config_1_at_full_size(tk, orc):
+    # 750 x 1024 activations ~N(0,1), 4096 x 1024 int8 weights, scales U(0.001, 0.01), seed 0.
+    rng = np.random.default_rng(0)
+    m, k, n = 750, 1024, 4096
+    a = normal(rng, (m, k)).reshape(-1)
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    say("config1", m, k, n)
+    got = run_gpu(tk, a, k, m, values, scales, INT8, n, k, np.zeros(m * n, np.float32), n, None, NONE, False, 1.0)
+    want = np.zeros(m * n, np.float32)
+    orc.matmul_fast(a, k, m, values, scales, n, k, want, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ref = np.zeros(m * n, np.float32)
+    orc.matmul(True, a, k, m, values, scales, INT8, n, k, ref, n)
+    err = rel_norm_err(got.reshape(m, n), ref.reshape(m, n))
+    print(f"[config1] row-normwise error vs the fused reference: {err:.3e}")
+    assert err <= 1e-3
