@@ -1,0 +1,304 @@
+"""Benchmark of the MI355X int8-weight matrix product on telmo's encoder shapes.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one pass of the hot path over one Conformer layer's projection set at T = 750 frames
+(60 s of audio at 80 ms per frame), d = 1024, ff = 4096, all weights int8 with per-output
+scales, activations f32 ~N(0, 1):
+
+    FF1 up 1024->4096 (SiLU), FF1 down 4096->1024 (x0.5, accumulate), QKV 1024->3072,
+    attention out 1024->1024 (input: the V third of QKV, accumulate), conv pw1 1024->2048,
+    GLU -> 1024, pw2 1024->1024 (accumulate), FF2 up and down as FF1.
+
+Each step first restores the layer input (a 3 MB device copy), so every step does the same work
+on the same data. The step runs as one captured HIP graph; the eager (stream) figure is reported
+beside it. value = 2 * sum(M N K) over the 8 GEMMs / step time, in TOPS.
+
+The JSON line also carries:
+  roofline      the GEMM kernel alone: each of the layer's 8 shapes on pre-quantised rows, timed
+                with HIP events on the library's stream; achieved = algorithmic ops / kernel time,
+                against the dense int8 MFMA peak. traffic comes from the rocprofv3 PMC summary in
+                profiles/ when one is there.
+  cpu_baseline  the C++ port of telmo's AVX-512 8x16 tile + thread pool (oracle/cpu_baseline.cpp,
+                bit-identical to the fused oracle) on the host's cores, on the same bytes.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+T_FRAMES = 750
+D, FF, CONV = 1024, 4096, 2048
+PEAK_INT8 = 5.0e15  # dense int8 MFMA ops/s (MI355X)
+PEAK_HBM = 8.0e12   # bytes/s
+METRIC = "int8 GEMM TOPS & %MFMA peak; decode GEMV GB/s & %HBM; encoder audio-s/s"
+
+# (name, k, n, act, scale, accumulate, input)
+LAYER = [
+    ("ff1_up", D, FF, "silu", 1.0, False, "x"),
+    ("ff1_down", FF, D, "none", 0.5, True, "h"),
+    ("qkv", D, 3 * D, "none", 1.0, False, "x"),
+    ("att_out", D, D, "none", 1.0, True, "v"),
+    ("pw1", D, CONV, "none", 1.0, False, "x"),
+    ("pw2", D, D, "none", 1.0, True, "u"),
+    ("ff2_up", D, FF, "silu", 1.0, False, "x"),
+    ("ff2_down", FF, D, "none", 0.5, True, "h"),
+]
+
+
+def ops_of(m):
+    return sum(2 * m * k * n for _, k, n, *_ in LAYER)
+
+
+def bytes_of(m):
+    """Algorithmic HBM bytes of the 8 GEMMs: A f32, int8 weights, f32 scales, C f32 (+ C read when
+    accumulating), each tensor once (panels padded to 16 outputs)."""
+    total = 0
+    for _, k, n, _, _, acc, _ in LAYER:
+        npad = -(-n // 16) * 16
+        total += 4 * m * k + npad * k + 4 * npad + 4 * m * n * (2 if acc else 1)
+    return total
+
+
+def make_weights(rng):
+    out = []
+    for name, k, n, *_ in LAYER:
+        q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+        s = (0.001 + 0.009 * rng.random(n)).astype(np.float32)
+        panels = -(-n // 16)
+        pad = np.zeros((panels * 16, k), np.int8)
+        pad[:n] = q
+        values = pad.reshape(panels, 16, k).transpose(0, 2, 1).reshape(-1).view(np.uint8).copy()
+        scales = np.zeros(panels * 16, np.float32)
+        scales[:n] = s
+        out.append((name, k, n, values, scales))
+    return out
+
+
+def gpu_leg(args, weights, x0_host):
+    import torch
+
+    import telmo_amd
+    from telmo_amd import Act, Epilogue
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    W = {name: telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, v, s)
+         for name, k, n, v, s in weights}
+    T = T_FRAMES
+    dev = "cuda"
+    x0 = torch.from_numpy(x0_host).to(dev)
+    x = x0.clone()
+    h = torch.empty((T, FF), dtype=torch.float32, device=dev)
+    qkv = torch.empty((T, 3 * D), dtype=torch.float32, device=dev)
+    g = torch.empty((T, CONV), dtype=torch.float32, device=dev)
+    u = torch.empty((T, D), dtype=torch.float32, device=dev)
+    v = qkv[:, 2 * D:]
+    silu = Epilogue(act=Act.SILU)
+    half_acc = Epilogue(scale=0.5, accumulate=True)
+    acc = Epilogue(accumulate=True)
+
+    def step():
+        x.copy_(x0)
+        kern.linear_device(x, T, W["ff1_up"], h, silu)
+        kern.linear_device(h, T, W["ff1_down"], x, half_acc)
+        kern.linear_device(x, T, W["qkv"], qkv)
+        kern.matmul_device(v, 3 * D, T, W["att_out"], x, D, acc, a_len=qkv.numel() - 2 * D)
+        kern.linear_device(x, T, W["pw1"], g)
+        kern.glu_device(g, CONV, T, D, u, D)
+        kern.linear_device(u, T, W["pw2"], x, acc)
+        kern.linear_device(x, T, W["ff2_up"], h, silu)
+        kern.linear_device(h, T, W["ff2_down"], x, half_acc)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    if not torch.isfinite(x).all():
+        raise RuntimeError("the layer output is not finite")
+
+    def timed(fn, reps):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps  # ms
+
+    eager_ms = timed(step, args.steps)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    graph_ms = timed(graph.replay, args.steps)
+    # The graph's output equals the eager step's.
+    graph.replay()
+    torch.cuda.synchronize()
+    out_graph = x.clone()
+    step()
+    torch.cuda.synchronize()
+    if not torch.equal(out_graph, x):
+        raise RuntimeError("graph replay differs from the eager step")
+
+    # Roofline leg: the GEMM kernel alone, per shape, on pre-quantised rows.
+    per_shape = []
+    inputs = {"x": x, "h": h, "v": v, "u": u}
+    for name, k, n, act, scale, accumulate, src in LAYER:
+        a = inputs[src]
+        lda = 3 * D if src == "v" else k
+        qa = torch.empty(kern.quant_bytes(T, k), dtype=torch.uint8, device=dev)
+        ex = torch.empty(T, dtype=torch.int32, device=dev)
+        kern.quantize_rows_device(a, lda, T, k, qa, ex)
+        c = torch.zeros((T, n), dtype=torch.float32, device=dev)
+        epi = Epilogue(act=Act.SILU if act == "silu" else Act.NONE, scale=scale, accumulate=accumulate)
+        launch = lambda: kern.matmul_quantized_device(qa, ex, T, W[name], c, n, epi)  # noqa: E731
+        for _ in range(5):
+            launch()
+        ms = timed(launch, args.kernel_reps)
+        per_shape.append({"gemm": name, "m": T, "k": k, "n": n, "us": round(ms * 1e3, 3),
+                          "tops": round(2 * T * k * n / (ms * 1e-3) / 1e12, 1)})
+    for w in W.values():
+        w.close()
+    kern.close()
+    return eager_ms, graph_ms, per_shape
+
+
+def cpu_leg(weights, x0_host, budget_s):
+    """telmo's SIMD + pool path (C++ port) on every host core, same bytes, 8 GEMMs per layer."""
+    from oracle import oracle as orc
+
+    L = ctypes.CDLL(orc.CPUBASE)
+    L.cb_isa.restype = ctypes.c_int
+    L.cb_pool_new.restype = ctypes.c_void_p
+    L.cb_pool_new.argtypes = [ctypes.c_size_t]
+    L.cb_pool_free.argtypes = [ctypes.c_void_p]
+    L.cb_matmul.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                             ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t,
+                             ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p,
+                             ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_int])
+    isa = L.cb_isa()
+    if isa == 0:
+        return None
+    cores = len(os.sched_getaffinity(0))
+    pool = L.cb_pool_new(cores)
+    T = T_FRAMES
+    x = x0_host.copy()
+    h = np.zeros((T, FF), np.float32)
+    qkv = np.zeros((T, 3 * D), np.float32)
+    u = np.random.default_rng(1).standard_normal((T, D)).astype(np.float32)
+    bufs = {"x": x, "h": h, "u": u}
+    p = lambda arr: arr.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    W = {name: (k, n, v, s) for name, k, n, v, s in weights}
+
+    def gemm(name, act, scale, accumulate, src, out, ldc):
+        k, n, v, s = W[name]
+        if src == "v":  # the V third of QKV: rows 3D apart, starting at column 2D
+            a_ptr, lda = ctypes.c_void_p(qkv.ctypes.data + 4 * 2 * D), 3 * D
+        else:
+            a_ptr, lda = p(bufs[src]), k
+        rc = L.cb_matmul(pool, isa, a_ptr, (T - 1) * lda + k, lda, T, p(v), p(s), 3, n, k, p(out), out.size, ldc,
+                         None, 0, 2 if act == "silu" else 0, scale, int(accumulate))
+        assert rc == 0, rc
+
+    outs = {"ff1_up": h, "ff1_down": x, "qkv": qkv, "att_out": x, "pw1": np.zeros((T, CONV), np.float32),
+            "pw2": x, "ff2_up": h, "ff2_down": x}
+
+    def layer():
+        for name, k, n, act, scale, accumulate, src in LAYER:
+            gemm(name, act, scale, accumulate, src, outs[name], n)
+
+    # Bit-identity with the fused oracle before timing (FF1 up on the layer input).
+    k, n, v, s = W["ff1_up"]
+    got, want = np.zeros((T, n), np.float32), np.zeros((T, n), np.float32)
+    assert L.cb_matmul(pool, isa, p(x0_host), x0_host.size, k, T, p(v), p(s), 3, n, k, p(got), got.size, n, None, 0,
+                       2, 1.0, 0) == 0
+    orc.matmul(True, x0_host.reshape(-1), k, T, v, s, 3, n, k, want.reshape(-1), n, None, 2, 1.0, False)
+    if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+        raise RuntimeError("the CPU baseline differs from the fused oracle")
+
+    t0 = time.perf_counter()
+    x[:] = x0_host
+    layer()
+    one = time.perf_counter() - t0
+    reps = max(1, int(budget_s / 5 / one))
+    best = float("inf")
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            x[:] = x0_host
+            layer()
+        best = min(best, (time.perf_counter() - t0) / reps)
+    L.cb_pool_free(pool)
+    return {"value": round(ops_of(T) / best / 1e12, 4), "unit": "TOPS", "cores": cores,
+            "kind": "port", "isa": "avx512" if isa == 2 else "avx2",
+            "sample": f"the same 8-GEMM layer at T={T}, best of 5 rounds of {reps} layers "
+                      f"({reps * 5 * best:.1f} s in all), {cores} threads",
+            "ms_per_step": round(best * 1e3, 3)}
+
+
+def load_traffic():
+    path = os.path.join(ROOT, "profiles", "gemm_i8_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--kernel-reps", type=int, default=500)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        sys.exit("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)")
+
+    rng = np.random.default_rng(0)
+    weights = make_weights(rng)
+    x0 = rng.standard_normal((T_FRAMES, D)).astype(np.float32)
+
+    eager_ms, graph_ms, per_shape = gpu_leg(args, weights, x0)
+    ops = ops_of(T_FRAMES)
+    gemm_us = sum(s["us"] for s in per_shape)
+    achieved = ops / (gemm_us * 1e-6)
+    traffic = load_traffic()
+    roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_INT8 / 1e12,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8, 4), "traffic": traffic,
+                "kernel": "gemm_i8_kernel", "avg_launch_us": round(gemm_us / len(per_shape), 3),
+                "ops_per_launch_avg": ops / len(per_shape),
+                "mfma_int8_ops_per_launch_avg": 2 * ops / len(per_shape),
+                "mfma_busy_frac": round(2 * achieved / PEAK_INT8, 4),
+                "note": "two int8 digits per activation: the MFMA executes 2x the algorithmic ops",
+                "per_shape": per_shape}
+    cpu = None if args.no_cpu else cpu_leg(weights, x0, args.cpu_seconds)
+    value = ops / (graph_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(graph_ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "conformer layer projection set: 8 int8 GEMMs + GLU at T=750 frames "
+                               "(60 s audio), d=1024, ff=4096, conv 2048 (config 2)",
+                   "frames": T_FRAMES, "ops_per_step": ops, "hbm_bytes_per_step": bytes_of(T_FRAMES),
+                   "ms_per_step_eager": round(eager_ms, 5), "timing": "hip graph replay of the step",
+                   "audio_s_per_s_one_layer": round(60.0 / (graph_ms * 1e-3), 1)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -28,6 +28,9 @@ SIGNATURES = {
     "tg_linear": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p]),
     "tg_matmul_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, _sz, _sz, _p]),
     "tg_linear_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p]),
+    "tg_quant_bytes": (_sz, [_sz, _sz]),
+    "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
+    "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
     "tg_panel_bytes": (_sz, [_u32, _sz, _sz]),
     "tg_scale_count": (_sz, [_u32, _sz, _sz]),

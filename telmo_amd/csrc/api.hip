@@ -314,6 +314,42 @@ int tg_linear(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weig
     return tg_matmul(ctx, a, a_len, w->d.k, m, w, c, c_len, w->d.n, epi);
 }
 
+size_t tg_quant_bytes(size_t m, size_t k) { return m * tg::qa_row_bytes(k); }
+
+int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, size_t k, void *qa,
+                            size_t qa_len, int32_t *exps) {
+    if (!ctx) return TG_ERR_NULL;
+    if (m == 0) return TG_OK;
+    if ((!a && k) || !qa || !exps) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (lda < k || a_len < (m - 1) * lda + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (qa_len < tg_quant_bytes(m, k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (k > tg::MAX_K_INT) return fail(ctx, TG_ERR_UNSUPPORTED, "k beyond the integer path's limit");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_quantize_rows(a, lda, m, k, static_cast<uint8_t *>(qa), exps, ctx->stream));
+    return TG_OK;
+}
+
+int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
+                               const tg_weights *w, float *c, size_t c_len, size_t ldc, const tg_epilogue *epi) {
+    if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
+    if (m == 0 || w->d.n == 0) return TG_OK;
+    const size_t n = w->d.n;
+    if (w->d.precision != TG_INT8 || w->d.k > tg::MAX_K_INT)
+        return fail(ctx, TG_ERR_UNSUPPORTED, "the staged path takes int8 weights with k <= 65536");
+    if (!qa || !exps || !c) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (ldc < n || c_len < (m - 1) * ldc + n) return fail(ctx, TG_ERR_SHAPE, "c is too short");
+    if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
+    if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, c, ldc,
+                                   epi_args(epi, nullptr, false), ctx->stream));
+    return TG_OK;
+}
+
 int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;
     if (m == 0 || half == 0) return TG_OK;

@@ -260,6 +260,25 @@ class Kernels:
     def linear_device(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
         self.matmul_device(a, w.k(), m, w, c, w.n(), epi)
 
+    def quant_bytes(self, m: int, k: int) -> int:
+        return _lib.lib().tg_quant_bytes(m, k)
+
+    def quantize_rows_device(self, a, lda: int, m: int, k: int, qa, exps):
+        """Splits rows of a GPU tensor into the two-digit form (qa: uint8 tensor, exps: int32)."""
+        rc = _lib.lib().tg_quantize_rows_device(self._ctx, ctypes.c_void_p(a.data_ptr()), a.numel(), lda, m, k,
+                                                ctypes.c_void_p(qa.data_ptr()), qa.numel(),
+                                                ctypes.c_void_p(exps.data_ptr()))
+        _check(rc, self._ctx)
+
+    def matmul_quantized_device(self, qa, exps, m: int, w: PackedWeights, c, ldc: int,
+                                epi: Epilogue = Epilogue.PLAIN):
+        """The MFMA GEMM alone over rows quantised by quantize_rows_device."""
+        rc = _lib.lib().tg_matmul_quantized_device(self._ctx, ctypes.c_void_p(qa.data_ptr()), qa.numel(),
+                                                   ctypes.c_void_p(exps.data_ptr()), m, w._handle,
+                                                   ctypes.c_void_p(c.data_ptr()), c.numel(), ldc,
+                                                   self._epi_dev(epi))
+        _check(rc, self._ctx)
+
     def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int):
         rc = _lib.lib().tg_glu_device(self._ctx, ctypes.c_void_p(x.data_ptr()), ldx, m, half,
                                       ctypes.c_void_p(out.data_ptr()), ldo)
