@@ -158,7 +158,7 @@ def gpu_leg(args, weights, x0_host):
         lda = 3 * D if src == "v" else k
         qa = torch.empty(kern.quant_bytes(T, k), dtype=torch.uint8, device=dev)
         ex = torch.empty(T, dtype=torch.int32, device=dev)
-        kern.quantize_rows_device(a, lda, T, k, qa, ex)
+        kern.quantize_rows_device(a, lda, T, k, qa, ex, a_len=(T - 1) * lda + k)
         c = torch.zeros((T, n), dtype=torch.float32, device=dev)
         epi = Epilogue(act=Act.SILU if act == "silu" else Act.NONE, scale=scale, accumulate=accumulate)
         launch = lambda: kern.matmul_quantized_device(qa, ex, T, W[name], c, n, epi)  # noqa: E731

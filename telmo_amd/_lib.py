@@ -42,10 +42,22 @@ SIGNATURES = {
 _lib = None
 
 
+def _share_the_process_hip_runtime():
+    """PyTorch-ROCm ships its own libamdhip64 / libhsa-runtime64 (same sonames, loaded by path).
+    Two HIP runtimes in one process cannot both open the GPU, so when torch is installed it is
+    loaded first: this library's dependencies then resolve to the runtime already in the
+    process. Without torch the system ROCm runtime is used."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     """The loaded library. Raises if it has not been built: there is no fallback."""
     global _lib
     if _lib is None:
+        _share_the_process_hip_runtime()
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m telmo_amd.build` "
                                "(or __graft_entry__.build()); telmo_amd has no CPU fallback")

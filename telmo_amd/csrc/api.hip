@@ -111,7 +111,7 @@ int run_device(tg_ctx *ctx, const float *a, size_t lda, size_t m, const tg_weigh
         TG_HIP(ctx, tg::launch_gemv_i8(a, lda, m, d, c, ldc, epi, ctx->stream));
         return TG_OK;
     }
-    int rc = grow(ctx, ctx->qa, ctx->qa_cap, m * tg::qa_row_bytes(d.k));
+    int rc = grow(ctx, ctx->qa, ctx->qa_cap, tg::qa_bytes(m, d.k));
     if (rc) return rc;
     rc = grow(ctx, ctx->exps, ctx->exps_cap, m * sizeof(int32_t));
     if (rc) return rc;
@@ -143,6 +143,9 @@ int upload(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *s
     d.n_scales = n_scales;
     const bool mfma_layout = precision == TG_INT8 || precision == TG_Q8_0;
     d.values_bytes = mfma_layout ? d.panels * d.kb * 1024 : values_len;
+    // The MFMA layout is k-block-major: the panels of one k-block are contiguous.
+    d.panel_stride = mfma_layout ? 1024 : k * tg::PANEL * (precision == TG_F32 ? 4 : 2);
+    d.blk_stride = mfma_layout ? d.panels * 1024 : 0;
     const hipMemcpyKind kind = from_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     auto cleanup = [&](int code, const std::string &msg) {
         if (d.values) (void)hipFree(d.values);
@@ -161,7 +164,7 @@ int upload(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *s
             uint8_t *raw = nullptr;
             if (hipMalloc(&raw, values_len) != hipSuccess) return cleanup(TG_ERR_NOMEM, "device allocation failed");
             e = hipMemcpyAsync(raw, values, values_len, kind, ctx->stream);
-            if (e == hipSuccess) e = tg::launch_repack_i8(raw, d.values, d.panels, k, d.kb, ctx->stream);
+            if (e == hipSuccess) e = tg::launch_repack_i8(raw, d, ctx->stream);
             if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
             (void)hipFree(raw);
         } else {
@@ -314,7 +317,7 @@ int tg_linear(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weig
     return tg_matmul(ctx, a, a_len, w->d.k, m, w, c, c_len, w->d.n, epi);
 }
 
-size_t tg_quant_bytes(size_t m, size_t k) { return m * tg::qa_row_bytes(k); }
+size_t tg_quant_bytes(size_t m, size_t k) { return tg::qa_bytes(m, k); }
 
 int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, size_t k, void *qa,
                             size_t qa_len, int32_t *exps) {

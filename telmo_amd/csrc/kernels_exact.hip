@@ -24,14 +24,14 @@ __device__ __forceinline__ float half_to_float(uint16_t h) {
 }
 
 __device__ __forceinline__ float widen_one(const uint8_t *__restrict__ wv, const float *__restrict__ scales,
-                                           uint32_t prec, size_t k, size_t kb, size_t p, int j, size_t i) {
+                                           uint32_t prec, size_t k, size_t ps, size_t bs, size_t p, int j, size_t i) {
     switch (prec) {
     case F32: return reinterpret_cast<const float *>(wv)[(p * k + i) * PANEL + j];
     case F16: return half_to_float(reinterpret_cast<const uint16_t *>(wv)[(p * k + i) * PANEL + j]);
     case BF16: return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(wv)[(p * k + i) * PANEL + j] << 16);
     default: {
         const size_t t = i / KBLK, g = (i % KBLK) / 16, ii = i % 16;
-        const int8_t q = (int8_t)wv[((p * kb + t) * 64 + g * 16 + j) * 16 + ii];
+        const int8_t q = (int8_t)wv[p * ps + t * bs + (g * 16 + j) * 16 + ii];
         const float s = prec == INT8 ? scales[p * PANEL + j]
                                      : scales[(p * div_ceil(k, Q8_BLOCK) + i / Q8_BLOCK) * PANEL + j];
         return (float)q * s;
@@ -41,9 +41,9 @@ __device__ __forceinline__ float widen_one(const uint8_t *__restrict__ wv, const
 
 __global__ __launch_bounds__(256) void exact_kernel(const float *__restrict__ a, size_t lda, int m, int k,
                                                     const uint8_t *__restrict__ wv, const float *__restrict__ scales,
-                                                    uint32_t prec, int N, int KB, float *__restrict__ c, size_t ldc,
-                                                    const float *__restrict__ bias, uint32_t act, float escale,
-                                                    int accumulate) {
+                                                    uint32_t prec, int N, size_t ps, size_t bs, float *__restrict__ c,
+                                                    size_t ldc, const float *__restrict__ bias, uint32_t act,
+                                                    float escale, int accumulate) {
     const int col = blockIdx.x * 64 + (threadIdx.x & 63);
     const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (row >= m || col >= N) return;
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void exact_kernel(const float *__restrict__ a,
     const int j = col % PANEL;
     const float *ar = a + (size_t)row * lda;
     float acc = 0.0f;
-    for (int i = 0; i < k; i++) acc = __builtin_fmaf(ar[i], widen_one(wv, scales, prec, k, KB, p, j, i), acc);
+    for (int i = 0; i < k; i++) acc = __builtin_fmaf(ar[i], widen_one(wv, scales, prec, k, ps, bs, p, j, i), acc);
     float *cp = c + (size_t)row * ldc + col;
     *cp = epilogue(acc, bias, (size_t)col, act, escale, accumulate != 0, cp);
 }
@@ -63,7 +63,8 @@ hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeight
     if (m == 0 || w.n == 0) return hipSuccess;
     dim3 grid((unsigned)div_ceil(w.n, 64), (unsigned)div_ceil(m, 4));
     hipLaunchKernelGGL(exact_kernel, grid, dim3(256), 0, s, a, lda, (int)m, (int)w.k, w.values, w.scales,
-                       w.precision, (int)w.n, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale, epi.accumulate);
+                       w.precision, (int)w.n, w.panel_stride, w.blk_stride, c, ldc, epi.bias, epi.act, epi.scale,
+                       epi.accumulate);
     return hipGetLastError();
 }
 

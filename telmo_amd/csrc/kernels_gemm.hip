@@ -1,15 +1,20 @@
 // The encoder-shaped int8-weight GEMM on gfx950 matrix cores.
 //
 // c[m, n] = epilogue(dequant(sum_k hi[m, k] q[n, k], sum_k lo[m, k] q[n, k])), where hi/lo are
-// the two int8 digits of each activation (the QA rows) and q the int8 weights in the MFMA
-// layout. Both sums run on v_mfma_i32_16x16x64_i8 and are exact, so the result does not depend
-// on tiling, k-order or splits; the f32 arithmetic happens once per output in the epilogue.
+// the two int8 digits of each activation and q the int8 weights. Both sums run on
+// v_mfma_i32_16x16x64_i8 and are exact, so the result does not depend on tiling, k-order or
+// splits; the f32 arithmetic happens once per output in the epilogue.
 //
-// Tiling: a workgroup of 4 wavefronts owns a BM x BN = 128 x 128 output tile; each wavefront a
-// 64 x 64 quarter as 4 x 4 MFMA blocks of 16 x 16, with one i32 accumulator set per digit
-// (128 accumulator VGPRs). Per k-block of 64 inputs the tile's A (128 rows x 128 digit bytes)
-// and B (8 panels x 1 KB) are staged through LDS, double-buffered, with 16-byte coalesced global
-// loads issued one k-block ahead.
+// Operands come straight from global memory into registers, with no LDS in the main loop and no
+// barriers: both the quantised rows (fragment-major QA) and the weights (MFMA layout) store each
+// 16 x 64 MFMA operand as 1 KB in lane order, so one 16-byte load per lane is one operand, fully
+// coalesced. A workgroup is 2 x 2 independent wavefronts; the two wavefronts that share an operand
+// sit on one CU, so the second load of it hits L1. Each wavefront keeps S k-blocks of operands in
+// flight (a register ring) so loads overlap the MFMAs. Measured on MI355X this beats an LDS-staged
+// pipeline: LDS writes run at about 64 B/clk/CU, and the two-digit A tile doubles them.
+//
+// Tiles: wavefront RB x CB MFMA blocks of 16 x 16 (workgroup 32 RB x 32 CB outputs). The launcher
+// takes 4 x 4 (128 x 128 per workgroup) when that fills the chip twice over, else 2 x 2 (64 x 64).
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -18,119 +23,150 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 128;
-constexpr int BP = BN / PANEL;          // panels per tile
-constexpr int A_STRIDE = 128 + 16;      // LDS bytes per A row (padded against bank conflicts)
-constexpr int A_TILE = BM * A_STRIDE;   // 18432
-constexpr int B_TILE = BP * 1024;       // 8192
-constexpr int STAGE = A_TILE + B_TILE;  // 26624
 constexpr int THREADS = 256;
 
-__global__ __launch_bounds__(THREADS) void gemm_i8_kernel(const uint8_t *__restrict__ qa,
-                                                          const int32_t *__restrict__ exps, int M,
-                                                          const uint8_t *__restrict__ wv,
-                                                          const float *__restrict__ scales, int N, int P, int KB,
-                                                          float *__restrict__ c, size_t ldc,
-                                                          const float *__restrict__ bias, uint32_t act, float escale,
-                                                          int accumulate) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+template <int RB, int CB, int S, int OCC>
+__global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
+                                                               const int32_t *__restrict__ exps, int M,
+                                                               const uint8_t *__restrict__ wv,
+                                                               const float *__restrict__ scales, int N, int P, int KB,
+                                                               float *__restrict__ c, size_t ldc,
+                                                               const float *__restrict__ bias, uint32_t act,
+                                                               float escale, int accumulate, size_t b_panel,
+                                                               size_t b_blk) {
+    constexpr int WM = RB * 16, WN = CB * 16;
+    constexpr int C_STRIDE = WN + 4;  // f32 per row of a wavefront's staged tile
+    __shared__ float staged[4][WM * C_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = blockIdx.y * BM, p0 = blockIdx.x * BP;
-    const size_t qa_stride = (size_t)KB * 128;
+    const int m0 = blockIdx.y * 2 * WM + wm * WM, n0 = blockIdx.x * 2 * WN + wn * WN;
+    const int R0 = m0 / 16, P0 = n0 / 16, RLAST = (M + 15) / 16 - 1;
+    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
 
-    // Global -> LDS assignment. A: 128 rows x 8 chunks of 16 bytes, 4 chunks per thread.
-    // B: 8 panels x 64 chunks, 2 per thread. Rows and panels past the edge read the last valid
-    // one; their results are never stored.
-    const uint8_t *a_src[4];
-    int a_dst[4];
-    for (int i = 0; i < 4; i++) {
-        const int row = (tid >> 3) + 32 * i;
-        const int grow = min(m0 + row, M - 1);
-        a_src[i] = qa + (size_t)grow * qa_stride + (tid & 7) * 16;
-        a_dst[i] = row * A_STRIDE + (tid & 7) * 16;
-    }
-    const uint8_t *b_src[2];
-    int b_dst[2];
-    for (int i = 0; i < 2; i++) {
-        const int pl = (tid >> 6) + 4 * i;
-        const int gp = min(p0 + pl, P - 1);
-        b_src[i] = wv + (size_t)gp * KB * 1024 + (tid & 63) * 16;
-        b_dst[i] = A_TILE + pl * 1024 + (tid & 63) * 16;
-    }
+    // The epilogue's row exponents and column scales, fetched first so their latency hides under
+    // the main loop. Rows and columns past the edge read the last valid one and are never stored.
+    int32_t e_row[RB][4];
+    float s_col[CB];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
 
-    v4i acc_hi[4][4], acc_lo[4][4];
-    for (int i = 0; i < 4; i++)
-        for (int j = 0; j < 4; j++) {
-            acc_hi[i][j] = v4i{0, 0, 0, 0};
-            acc_lo[i][j] = v4i{0, 0, 0, 0};
-        }
+    // Operand blocks of this wavefront: row block R of the QA at (R * KB + t) * 2048 (+1024 for
+    // the lo digits), panel p of the weights at p * b_panel + t * b_blk.
+    const uint8_t *ap[RB];
+    const uint8_t *bp[CB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) ap[r] = qf + (size_t)min(R0 + r, RLAST) * KB * 2048 + lane * 16;
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) bp[cb] = wv + (size_t)min(P0 + cb, P - 1) * b_panel + lane * 16;
 
-    uint4 ra[4], rb[2];
-    auto load_global = [&](int t) {
-        for (int i = 0; i < 4; i++) ra[i] = *reinterpret_cast<const uint4 *>(a_src[i] + (size_t)t * 128);
-        for (int i = 0; i < 2; i++) rb[i] = *reinterpret_cast<const uint4 *>(b_src[i] + (size_t)t * 1024);
-    };
-    auto store_lds = [&](int stage) {
-        uint8_t *st = smem + stage * STAGE;
-        for (int i = 0; i < 4; i++) *reinterpret_cast<uint4 *>(st + a_dst[i]) = ra[i];
-        for (int i = 0; i < 2; i++) *reinterpret_cast<uint4 *>(st + b_dst[i]) = rb[i];
-    };
+    v4i acc_hi[RB][CB], acc_lo[RB][CB];
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+        for (int j = 0; j < CB; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
+
+    v4i fa[S][RB][2], fb[S][CB];
+#define TG_LOAD(st, tt)                                                                                \
+    do {                                                                                               \
+        const size_t t_ = (size_t)(tt);                                                                \
+        _Pragma("unroll") for (int r = 0; r < RB; r++) {                                               \
+            fa[st][r][0] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048);                          \
+            fa[st][r][1] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048 + 1024);                   \
+        }                                                                                              \
+        _Pragma("unroll") for (int cb = 0; cb < CB; cb++) fb[st][cb] =                                 \
+            *reinterpret_cast<const v4i *>(bp[cb] + t_ * b_blk);                                       \
+    } while (0)
+#define TG_MMA(st)                                                                                     \
+    do {                                                                                               \
+        _Pragma("unroll") for (int r = 0; r < RB; r++)                                                 \
+            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
+                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[st][r][0], fb[st][cb], acc_hi[r][cb], 0, 0, 0); \
+                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[st][r][1], fb[st][cb], acc_lo[r][cb], 0, 0, 0); \
+            }                                                                                          \
+    } while (0)
 
     if (KB > 0) {
-        load_global(0);
-        store_lds(0);
-    }
-    __syncthreads();
-
-    const int frag_row = lane & 15, frag_k = (lane >> 4) * 16;
-    for (int t = 0; t < KB; t++) {
-        const uint8_t *st = smem + (t & 1) * STAGE;
-        if (t + 1 < KB) load_global(t + 1);
-        v4i bw[4];
-        for (int cb = 0; cb < 4; cb++)
-            bw[cb] = *reinterpret_cast<const v4i *>(st + A_TILE + (wn * 4 + cb) * 1024 + lane * 16);
-        for (int rb_ = 0; rb_ < 4; rb_++) {
-            const uint8_t *ap = st + (wm * 64 + rb_ * 16 + frag_row) * A_STRIDE + frag_k;
-            const v4i ahi = *reinterpret_cast<const v4i *>(ap);
-            const v4i alo = *reinterpret_cast<const v4i *>(ap + 64);
-            for (int cb = 0; cb < 4; cb++) {
-                acc_hi[rb_][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, bw[cb], acc_hi[rb_][cb], 0, 0, 0);
-                acc_lo[rb_][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, bw[cb], acc_lo[rb_][cb], 0, 0, 0);
+        // Ring of S register stages: block t sits in stage t % S. Loads past the end reload the
+        // last block (in bounds, never used).
+#pragma unroll
+        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, KB - 1));
+        int t = 0;
+        for (; t + S <= KB; t += S) {
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                TG_LOAD((s + S - 1) % S, min(t + s + S - 1, KB - 1));
+                TG_MMA(s);
             }
         }
-        if (t + 1 < KB) store_lds((t + 1) & 1);
-        __syncthreads();
+        // At most S - 1 blocks remain, already loaded into stages 0, 1, ...
+        if (t < KB) TG_MMA(0);
+        if constexpr (S > 2) {
+            if (t + 1 < KB) TG_MMA(1);
+        }
     }
+#undef TG_LOAD
+#undef TG_MMA
 
-    // Accumulator element v of lane l holds output row 4 (l / 16) + v, column l % 16 of its block.
-    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
-    for (int rb_ = 0; rb_ < 4; rb_++) {
-        for (int cb = 0; cb < 4; cb++) {
-            const int col = (p0 + wn * 4 + cb) * PANEL + out_col;
-            if (col >= N) continue;
-            const float sc = scales[col];
-            for (int v = 0; v < 4; v++) {
-                const int row = m0 + wm * 64 + rb_ * 16 + out_row + v;
-                if (row >= M) continue;
-                float *cp = c + (size_t)row * ldc + col;
-                const float s = dequant(acc_hi[rb_][cb][v], acc_lo[rb_][cb][v], exps[row], sc);
-                *cp = epilogue(s, bias, (size_t)col, act, escale, accumulate != 0, cp);
-            }
+    // Epilogue: the wavefront stages its f32 sums in LDS (element v of lane l holds row
+    // 4 (l / 16) + v, column l % 16 of its 16 x 16 block), then stores them row after row,
+    // 64 consecutive outputs per instruction, eight at a time so the loads of c overlap.
+    float *tile = staged[wave];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                    dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
+    __syncthreads();
+    constexpr int TOTAL = WM * WN;
+    for (int i0 = lane; i0 < TOTAL; i0 += 8 * 64) {
+        float old[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
+            old[u] = (accumulate && i < TOTAL && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
+            if (i < TOTAL && row < M && col < N)
+                c[(size_t)row * ldc + col] = epilogue(tile[(i / WN) * C_STRIDE + i % WN], bias, (size_t)col, act,
+                                                      escale, accumulate != 0, &old[u]);
         }
     }
 }
 
+template <int RB, int CB, int S, int OCC>
+hipError_t launch_tile(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                       const EpiArgs &epi, hipStream_t s) {
+    const size_t bm = 2 * RB * 16, bn = 2 * CB * 16;
+    dim3 grid((unsigned)div_ceil(w.panels * PANEL, bn), (unsigned)div_ceil(m, bm));
+    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, OCC>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
+                       w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
+                       epi.accumulate, w.panel_stride, w.blk_stride);
+    return hipGetLastError();
+}
+
 }  // namespace
 
-hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
+// 128 x 128 workgroup tiles when there are at least 1024 of them (two per CU, twice over), else
+// 64 x 64 tiles, which keep more CUs busy on short products.
+int gemm_tile_choice(size_t m, size_t panels) {
+    const size_t big = div_ceil(m, 128) * div_ceil(panels * PANEL, 128);
+    return big >= 1024 ? 0 : 1;
+}
+
+hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    dim3 grid((unsigned)div_ceil(w.panels, BP), (unsigned)div_ceil(m, BM));
-    hipLaunchKernelGGL(gemm_i8_kernel, grid, dim3(THREADS), 0, s, qa, exps, (int)m, w.values, w.scales, (int)w.n,
-                       (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale, epi.accumulate);
-    return hipGetLastError();
+    if (gemm_tile_choice(m, w.panels) == 0) return launch_tile<4, 4, 2, 2>(qf, exps, m, w, c, ldc, epi, s);
+    return launch_tile<2, 2, 3, 2>(qf, exps, m, w, c, ldc, epi, s);
 }
 
 }  // namespace tg

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(THREADS) void gemv_i8_kernel(const float *__restric
                                                           const float *__restrict__ scales, int N, int P, int KB,
                                                           float *__restrict__ c, size_t ldc,
                                                           const float *__restrict__ bias, uint32_t act, float escale,
-                                                          int accumulate) {
+                                                          int accumulate, size_t panel_stride, size_t blk_stride) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];  // MR rows x KB x 128 bytes
     __shared__ int32_t sexp[MR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -73,11 +73,11 @@ __global__ __launch_bounds__(THREADS) void gemv_i8_kernel(const float *__restric
         const uint8_t *wp[4];
         for (int q = 0; q < 4; q++) {
             const int p = min(grp * 4 + q, P - 1);
-            wp[q] = wv + (size_t)p * KB * 1024 + lane * 16;
+            wp[q] = wv + (size_t)p * panel_stride + lane * 16;
         }
         for (int t = 0; t < KB; t++) {
             uint4 w[4];
-            for (int q = 0; q < 4; q++) w[q] = *reinterpret_cast<const uint4 *>(wp[q] + (size_t)t * 1024);
+            for (int q = 0; q < 4; q++) w[q] = *reinterpret_cast<const uint4 *>(wp[q] + (size_t)t * blk_stride);
             for (int r = 0; r < MR; r++) {
                 const uint8_t *ap = sqa + r * row_bytes + t * 128 + g * 16;
                 const uint4 ahi = *reinterpret_cast<const uint4 *>(ap);
@@ -138,7 +138,7 @@ hipError_t launch_rows(const float *a, size_t lda, const DeviceWeights &w, float
     const size_t lds = (size_t)MR * w.kb * 128;
     hipLaunchKernelGGL(gemv_i8_kernel<MR>, dim3((unsigned)blocks), dim3(THREADS), lds, s, a, lda, (int)w.k,
                        w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
-                       epi.accumulate);
+                       epi.accumulate, w.panel_stride, w.blk_stride);
     return hipGetLastError();
 }
 

@@ -9,7 +9,7 @@ namespace tg {
 // contiguous in telmo's layout) go through LDS, and each lane writes the 16 inputs of one
 // output that its MFMA operand needs, 16 contiguous bytes.
 __global__ __launch_bounds__(64) void repack_i8_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
-                                                       size_t k, size_t kb) {
+                                                       size_t k, size_t kb, size_t panel_stride, size_t blk_stride) {
     __shared__ uint8_t tile[KBLK][PANEL + 4];
     const size_t blk = blockIdx.x;  // p * kb + t
     const size_t p = blk / kb, t = blk % kb;
@@ -30,12 +30,13 @@ __global__ __launch_bounds__(64) void repack_i8_kernel(const uint8_t *__restrict
         for (int b = 0; b < 4; b++) o[i] |= (uint32_t)tile[16 * g + 4 * i + b][j] << (8 * b);
     }
     uint4 out = make_uint4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<uint4 *>(dst + (blk * 64 + l) * 16) = out;
+    *reinterpret_cast<uint4 *>(dst + p * panel_stride + t * blk_stride + l * 16) = out;
 }
 
-hipError_t launch_repack_i8(const uint8_t *src, uint8_t *dst, size_t panels, size_t k, size_t kb, hipStream_t s) {
-    if (panels == 0 || kb == 0) return hipSuccess;
-    hipLaunchKernelGGL(repack_i8_kernel, dim3((unsigned)(panels * kb)), dim3(64), 0, s, src, dst, k, kb);
+hipError_t launch_repack_i8(const uint8_t *src, const DeviceWeights &w, hipStream_t s) {
+    if (w.panels == 0 || w.kb == 0) return hipSuccess;
+    hipLaunchKernelGGL(repack_i8_kernel, dim3((unsigned)(w.panels * w.kb)), dim3(64), 0, s, src, w.values, w.k, w.kb,
+                       w.panel_stride, w.blk_stride);
     return hipGetLastError();
 }
 
@@ -50,10 +51,9 @@ __device__ __forceinline__ int wave_or(int v) {
 }
 
 // One wavefront per row: the largest magnitude (and any NaN or infinity) over the row's k
-// inputs, the row exponent, then the digits of each input. Lane l writes the digits of inputs
-// 64 t + l, so each wave store is 64 contiguous bytes of the QA row.
+// inputs, the row exponent, then the digits of each input into the fragment-major QA.
 __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ ar, size_t k, size_t kb,
-                                                     uint8_t *__restrict__ q, int lane) {
+                                                     uint8_t *__restrict__ qa, size_t row, int lane) {
     float amax = 0.0f;
     int bad = 0;
     for (size_t i = lane; i < k; i += 64) {
@@ -68,8 +68,9 @@ __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ a
         const size_t i = t * KBLK + lane;
         int8_t hi = 0, lo = 0;
         if (i < k) digits_of(ar[i], e, hi, lo);
-        q[t * 128 + lane] = (uint8_t)hi;
-        q[t * 128 + 64 + lane] = (uint8_t)lo;
+        const size_t at = qa_offset(row, t, 0, kb) + (lane >> 4) * 256 + (lane & 15);
+        qa[at] = (uint8_t)hi;
+        qa[at + 1024] = (uint8_t)lo;
     }
     return e;
 }
@@ -80,16 +81,100 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restr
     const int lane = threadIdx.x & 63;
     const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= m) return;
-    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa + row * kb * 128, lane);
+    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa, row, lane);
     if (lane == 0) exps[row] = e;
+}
+
+// The digits of four consecutive inputs packed as (hi dword, lo dword).
+__device__ __forceinline__ void digits4(const float4 &v, int32_t e, uint32_t &hi, uint32_t &lo) {
+    int8_t h0, l0, h1, l1, h2, l2, h3, l3;
+    digits_of(v.x, e, h0, l0);
+    digits_of(v.y, e, h1, l1);
+    digits_of(v.z, e, h2, l2);
+    digits_of(v.w, e, h3, l3);
+    hi = (uint32_t)(uint8_t)h0 | (uint32_t)(uint8_t)h1 << 8 | (uint32_t)(uint8_t)h2 << 16 | (uint32_t)(uint8_t)h3 << 24;
+    lo = (uint32_t)(uint8_t)l0 | (uint32_t)(uint8_t)l1 << 8 | (uint32_t)(uint8_t)l2 << 16 | (uint32_t)(uint8_t)l3 << 24;
+}
+
+// One workgroup per row, the row held in registers: thread t owns the 4-input chunks t + 256 j
+// (j < J), loaded as one float4 when the rows are 16-byte aligned. A block reduction gives the
+// row's exponent; each thread then writes the 4 hi and 4 lo digits of each chunk as two dwords
+// of the fragment-major QA. Chunks from k up to the 64-input padding are written as zeros.
+template <int J>
+__global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__restrict__ a, size_t lda, int k,
+                                                                 int kb, uint8_t *__restrict__ qa,
+                                                                 int32_t *__restrict__ exps, int vec) {
+    __shared__ float s_max[4];
+    __shared__ int s_bad[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t row = blockIdx.x;
+    const float *ar = a + row * lda;
+    float4 v[J];
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int k0 = 4 * (tid + 256 * j);
+        if (vec && k0 + 3 < k) {
+            v[j] = *reinterpret_cast<const float4 *>(ar + k0);
+        } else {
+            v[j].x = k0 < k ? ar[k0] : 0.0f;
+            v[j].y = k0 + 1 < k ? ar[k0 + 1] : 0.0f;
+            v[j].z = k0 + 2 < k ? ar[k0 + 2] : 0.0f;
+            v[j].w = k0 + 3 < k ? ar[k0 + 3] : 0.0f;
+        }
+        bad |= !__builtin_isfinite(v[j].x) | !__builtin_isfinite(v[j].y) | !__builtin_isfinite(v[j].z) |
+               !__builtin_isfinite(v[j].w);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+    amax = wave_max(amax);
+    bad = wave_or(bad);
+    if (lane == 0) {
+        s_max[wave] = amax;
+        s_bad[wave] = bad;
+    }
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    bad = s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3];
+    const int32_t e = bad ? EXP_NONFINITE : row_exponent_of(amax);
+    if (tid == 0) exps[row] = e;
+    const int chunks = kb * 16;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int c = tid + 256 * j;
+        if (c < chunks) {
+            uint32_t hi, lo;
+            digits4(v[j], e, hi, lo);
+            // chunk c: k-block c / 16, 16-input group (c % 16) / 4, byte (c % 4) * 4 of its 16
+            const size_t at = qa_offset(row, c >> 4, 0, kb) + ((c & 15) >> 2) * 256 + (c & 3) * 4;
+            *reinterpret_cast<uint32_t *>(qa + at) = hi;
+            *reinterpret_cast<uint32_t *>(qa + at + 1024) = lo;
+        }
+    }
+}
+
+template <int J>
+void launch_regs(const float *a, size_t lda, size_t m, size_t k, size_t kb, uint8_t *qa, int32_t *exps, int vec,
+                 hipStream_t s) {
+    hipLaunchKernelGGL(quantize_rows_regs_kernel<J>, dim3((unsigned)m), dim3(256), 0, s, a, lda, (int)k, (int)kb, qa,
+                       exps, vec);
 }
 
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
                                 hipStream_t s) {
     if (m == 0) return hipSuccess;
-    size_t kb = div_ceil(k, KBLK);
-    hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)div_ceil(m, 4)), dim3(256), 0, s, a, lda, m, k, kb, qa,
-                       exps);
+    const size_t kb = div_ceil(k, KBLK);
+    // 16-byte loads need every row 16-byte aligned.
+    const int vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (lda % 4 == 0);
+    const size_t j = div_ceil(kb * 16, 256);  // 4-input chunks per thread
+    if (j <= 1) launch_regs<1>(a, lda, m, k, kb, qa, exps, vec, s);
+    else if (j <= 2) launch_regs<2>(a, lda, m, k, kb, qa, exps, vec, s);
+    else if (j <= 4) launch_regs<4>(a, lda, m, k, kb, qa, exps, vec, s);
+    else if (j <= 8) launch_regs<8>(a, lda, m, k, kb, qa, exps, vec, s);
+    else if (j <= 16) launch_regs<16>(a, lda, m, k, kb, qa, exps, vec, s);
+    else
+        hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)div_ceil(m, 4)), dim3(256), 0, s, a, lda, m, k, kb,
+                           qa, exps);
     return hipGetLastError();
 }
 

@@ -33,9 +33,9 @@ __host__ __device__ inline size_t div_ceil(size_t a, size_t b) { return (a + b -
 // Device copy of a weight matrix.
 //   f32 / f16 / bf16: telmo's panel layout unchanged: value (o, i) at ((o/16 * k + i) * 16 + o%16).
 //   int8 / Q8_0: the "MFMA layout": per panel p and k-block t of 64 inputs, 1024 bytes in lane
-//     order, lane l = 16 g + j holding the 16 inputs 64 t + 16 g + [0, 16) of output 16 p + j.
-//     Inputs past k are zero. One 16-byte load per lane is then the operand of an i8 MFMA
-//     (16x16x64) for both the GEMM and the dot4 GEMV.
+//     order, lane l = 16 g + j holding the 16 inputs 64 t + 16 g + [0, 16) of output 16 p + j,
+//     at p * panel_stride + t * blk_stride. Inputs past k are zero. One 16-byte load per lane is
+//     then the operand of an i8 MFMA (16x16x64) for both the GEMM and the dot4 GEMV.
 //   scales: unchanged ([panels * 16] for int8, [panels * blocks * 16] for Q8_0).
 struct DeviceWeights {
     size_t n, k;
@@ -45,11 +45,17 @@ struct DeviceWeights {
     uint8_t *values; // device
     float *scales;   // device, or null
     size_t values_bytes, n_scales;
+    size_t panel_stride, blk_stride;  // bytes between panels and between k-blocks (MFMA layout)
 };
 
-// Quantised activations ("QA"): per row, kb blocks of 128 bytes: the hi digits of inputs
-// 64 t + [0, 64) then their lo digits. Digits of inputs past k are zero.
-inline size_t qa_row_bytes(size_t k) { return div_ceil(k, KBLK) * 128; }
+// Quantised activations ("QA"), fragment-major: for each block of 16 rows R, k-block t and digit d
+// (hi = 0, lo = 1), 1 KB at ((R * kb + t) * 2 + d) * 1024 in MFMA lane order: lane g * 16 + r holds
+// the 16 digits of inputs 64 t + 16 g + [0, 16) of row 16 R + r. Digits of inputs past k are zero;
+// rows past m in the last block are never read into a stored result.
+inline size_t qa_bytes(size_t m, size_t k) { return div_ceil(m, 16) * div_ceil(k, KBLK) * 2048; }
+__host__ __device__ inline size_t qa_offset(size_t row, size_t t, int d, size_t kb) {
+    return (((row / 16) * kb + t) * 2 + d) * 1024 + (row % 16) * 16;
+}
 
 // ---------------------------------------------------------------------------- device arithmetic
 
@@ -94,8 +100,9 @@ __device__ __forceinline__ float epilogue(float v, const float *bias, size_t col
 // zero +0 whatever the scale's sign, as the reference's sums start at +0.
 __device__ __forceinline__ float dequant(int32_t acc_hi, int32_t acc_lo, int32_t e, float scale) {
     if (e == EXP_NONFINITE) return __builtin_nanf("");
-    long long s = (long long)acc_hi * 256 + acc_lo;
-    float u = (float)s * scale + 0.0f;
+    // 256 hi + lo is exact in f64 (|S| < 2^39), so the conversion to f32 is the one rounding of S.
+    const double s = __builtin_fma((double)acc_hi, 256.0, (double)acc_lo);
+    const float u = (float)s * scale + 0.0f;
     return __builtin_ldexpf(u, -e);
 }
 
@@ -128,10 +135,10 @@ struct EpiArgs {
     int accumulate;
 };
 
-// Re-lays int8 / Q8_0 panel values (device, telmo's layout) into the MFMA layout.
-hipError_t launch_repack_i8(const uint8_t *src, uint8_t *dst, size_t panels, size_t k, size_t kb, hipStream_t s);
+// Re-lays int8 / Q8_0 panel values (device, telmo's layout) into w's MFMA layout.
+hipError_t launch_repack_i8(const uint8_t *src, const DeviceWeights &w, hipStream_t s);
 
-// Per-row digits and exponents of a[m][lda] (k inputs) into qa / exps.
+// Per-row digits and exponents of a[m][lda] (k inputs) into qa (fragment-major) / exps.
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
                                 hipStream_t s);
 

@@ -263,9 +263,10 @@ class Kernels:
     def quant_bytes(self, m: int, k: int) -> int:
         return _lib.lib().tg_quant_bytes(m, k)
 
-    def quantize_rows_device(self, a, lda: int, m: int, k: int, qa, exps):
+    def quantize_rows_device(self, a, lda: int, m: int, k: int, qa, exps, a_len: Optional[int] = None):
         """Splits rows of a GPU tensor into the two-digit form (qa: uint8 tensor, exps: int32)."""
-        rc = _lib.lib().tg_quantize_rows_device(self._ctx, ctypes.c_void_p(a.data_ptr()), a.numel(), lda, m, k,
+        rc = _lib.lib().tg_quantize_rows_device(self._ctx, ctypes.c_void_p(a.data_ptr()),
+                                                a.numel() if a_len is None else a_len, lda, m, k,
                                                 ctypes.c_void_p(qa.data_ptr()), qa.numel(),
                                                 ctypes.c_void_p(exps.data_ptr()))
         _check(rc, self._ctx)
