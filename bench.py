@@ -173,6 +173,126 @@ def gpu_leg(args, weights, x0_host):
     return eager_ms, graph_ms, per_shape
 
 
+def _pack(rng, n, k):
+    q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+    s = (0.001 + 0.009 * rng.random(n)).astype(np.float32)
+    panels = -(-n // 16)
+    pad = np.zeros((panels * 16, k), np.int8)
+    pad[:n] = q
+    values = pad.reshape(panels, 16, k).transpose(0, 2, 1).reshape(-1).view(np.uint8).copy()
+    scales = np.zeros(panels * 16, np.float32)
+    scales[:n] = s
+    return values, scales
+
+
+def gemv_leg(args):
+    """Config 5: the decode-step GEMVs (m = 1, 4, 8 streams), no MFMA.
+
+    (i) each shape with its weights evicted: calls rotate over copies totalling more than 512 MB
+        (twice the 256 MB Infinity Cache), so every call streams its weights from HBM;
+    (ii) the same kernel on one large matrix (64 - 256 MB) for its asymptotic HBM rate;
+    (iii) the token loop: 2000 dependent steps of gates 640 -> 2560 then joint 640 -> 8198 (+ bias),
+        each step's input taken from the previous step's gate output, weights reused (cache-resident).
+    GB/s counts the weight bytes of the panel layout plus scales once per call.
+    """
+    import torch
+
+    import telmo_amd
+    from telmo_amd import Epilogue
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    rng = np.random.default_rng(5)
+    out = {"rotating": [], "sweep": [], "token_loop": []}
+
+    def timed(fn, reps):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3  # s
+
+    shapes = [("joint", 640, 8198, True), ("gates", 640, 2560, False), ("lstm_layer", 1280, 2560, False)]
+    for name, k, n, with_bias in shapes:
+        values, scales = _pack(rng, n, k)
+        one = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+        wbytes = one.bytes()
+        copies = [one] + [telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+                          for _ in range(int(600e6 // wbytes))]
+        bias = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda() if with_bias else None
+        for m in (1, 4, 8):
+            a = torch.randn(m, k, device="cuda")
+            c = torch.empty(m, n, device="cuda")
+            epi = Epilogue(bias=bias)
+            call = lambda i: kern.linear_device(a, m, copies[i % len(copies)], c, epi)  # noqa: E731
+            for i in range(len(copies)):
+                call(i)
+            t = timed(call, 4 * len(copies))
+            out["rotating"].append({"gemv": name, "m": m, "k": k, "n": n, "weight_mb": round(wbytes / 1e6, 3),
+                                    "us": round(t * 1e6, 2), "gb_s": round(wbytes / t / 1e9, 1),
+                                    "hbm_frac": round(wbytes / t / PEAK_HBM, 3)})
+        for w in copies:
+            w.close()
+    for mb in (64, 256):
+        k = 640
+        n = int(mb * 1e6 // k) // 16 * 16
+        values, scales = _pack(rng, n, k)
+        w = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+        del values
+        for m in (1, 4, 8):
+            a = torch.randn(m, k, device="cuda")
+            c = torch.empty(m, n, device="cuda")
+            call = lambda i: kern.linear_device(a, m, w, c)  # noqa: E731
+            call(0)
+            t = timed(call, 20)
+            out["sweep"].append({"m": m, "k": k, "n": n, "weight_mb": round(w.bytes() / 1e6, 1), "us": round(t * 1e6, 1),
+                                 "gb_s": round(w.bytes() / t / 1e9, 1), "hbm_frac": round(w.bytes() / t / PEAK_HBM, 3)})
+        w.close()
+    # Token loop.
+    vg, sg = _pack(rng, 2560, 640)
+    vj, sj = _pack(rng, 8198, 640)
+    wg = telmo_amd.PackedWeights.from_parts(kern, 2560, 640, telmo_amd.Precision.INT8, vg, sg)
+    wj = telmo_amd.PackedWeights.from_parts(kern, 8198, 640, telmo_amd.Precision.INT8, vj, sj)
+    bg = torch.from_numpy(rng.standard_normal(2560).astype(np.float32)).cuda()
+    bj = torch.from_numpy(rng.standard_normal(8198).astype(np.float32)).cuda()
+    steps = 2000
+    for m in (1, 4, 8):
+        gates = torch.randn(m, 2560, device="cuda")
+        logits = torch.empty(m, 8198, device="cuda")
+        g_epi = Epilogue(bias=bg, scale=1.0 / 16)
+        j_epi = Epilogue(bias=bj)
+        h = gates[:, 640:1280]
+        z = gates[:, :640]
+        alen = (m - 1) * 2560 + 640
+
+        def step():
+            kern.matmul_device(h, 2560, m, wg, gates, 2560, g_epi, a_len=alen)
+            kern.matmul_device(z, 2560, m, wj, logits, 8198, j_epi, a_len=alen)
+
+        for _ in range(10):
+            step()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(100):
+                step()
+        graph.replay()
+        t = timed(lambda i: graph.replay(), steps // 100) / 100  # s per step
+        if not torch.isfinite(logits).all():
+            raise RuntimeError("the token loop diverged")
+        step_bytes = wg.bytes() + wj.bytes()
+        out["token_loop"].append({"m": m, "steps": steps, "us_per_step": round(t * 1e6, 2),
+                                  "tokens_per_s": round(m / t, 1), "effective_gb_s": round(step_bytes / t / 1e9, 1),
+                                  "note": "weights reused every step (cache-resident), effective rate"})
+    wg.close()
+    wj.close()
+    kern.close()
+    return out
+
+
 def cpu_leg(weights, x0_host, budget_s):
     """telmo's SIMD + pool path (C++ port) on every host core, same bytes, 8 GEMMs per layer."""
     from oracle import oracle as orc
@@ -262,6 +382,7 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=500)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)")
@@ -283,6 +404,7 @@ def main():
                 "mfma_busy_frac": round(2 * achieved / PEAK_INT8, 4),
                 "note": "two int8 digits per activation: the MFMA executes 2x the algorithmic ops",
                 "per_shape": per_shape}
+    gemv = None if args.no_gemv else gemv_leg(args)
     cpu = None if args.no_cpu else cpu_leg(weights, x0, args.cpu_seconds)
     value = ops / (graph_ms * 1e-3) / 1e12
     line = {
@@ -296,6 +418,7 @@ def main():
                    "audio_s_per_s_one_layer": round(60.0 / (graph_ms * 1e-3), 1)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "gemv": gemv,
     }
     print(json.dumps(line))
 

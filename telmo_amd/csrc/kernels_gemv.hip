@@ -1,13 +1,19 @@
-// The decode-step GEMV (m = 1..8 rows) over int8 weights: bandwidth-bound, no MFMA.
+// The decode-step GEMVs (m = 1..16 rows) over int8 weights: HBM-bound streams of the weights.
 //
-// Each workgroup first splits its m activation rows into two int8 digits in LDS (the same
-// digits and exponents as the GEMM path, so a row gives bit-identical outputs on either path).
-// Each wavefront then streams groups of 4 weight panels (64 outputs) in the MFMA layout: per
-// k-block of 64 inputs, lane l = 16 g + j loads 16 contiguous bytes per panel (the inputs
-// 64 t + 16 g + [0, 16) of output j), a fully coalesced 1 KB per panel per wave, and sums them
-// against the digits with v_dot4_i32_i8 (4 products per lane-op, exact in i32). After the k loop a
-// two-step reduce-scatter over g (lane xor 32, then xor 16) leaves lane (g, j) the full sums of
-// output j of panel g, and the 64 lanes store 64 contiguous outputs per row.
+// Both kernels split their rows into two int8 digits in LDS themselves (the same digits and
+// exponents as the GEMM path, so a row gives bit-identical outputs on every path) and read the
+// weights in the MFMA layout: per k-block of 64 inputs of a 16-output panel, lane l = 16 g + j
+// loads 16 contiguous bytes (inputs 64 t + 16 g + [0, 16) of output j), 1 KB per wave, coalesced.
+//
+// gemv_mfma_kernel (m <= 16, k <= 1984): the digits sit in LDS as 16 x 64 MFMA A operands in lane
+// order, so each 1 KB weight block costs one 16-byte LDS read per digit and two
+// v_mfma_i32_16x16x64_i8, whatever m is. The rows are read once into registers ahead of the
+// weights; workgroups stay resident and walk the panels, so the rows are digitised once per
+// workgroup, and the next panel's weights, scales, bias and old outputs are requested before the
+// current panel's epilogue.
+//
+// gemv_i8_kernel (m <= 8, longer rows): one panel per wavefront, v_dot4_i32_i8 against each
+// row's digits; the four input groups meet by lane exchanges (xor 16, xor 32).
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -15,7 +21,7 @@ namespace tg {
 namespace {
 
 constexpr int THREADS = 256;
-constexpr size_t GEMV_LDS_BUDGET = 64 * 1024;
+constexpr size_t GEMV_LDS_BUDGET = 64 * 1024 - 256;  // the rest of 64 KB holds the exponents
 
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
@@ -27,7 +33,12 @@ __device__ __forceinline__ int wave_or(int v) {
     return v;
 }
 
-template <int MR>
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// One weight panel (16 outputs) per wavefront. The panel's first KBC k-blocks are requested
+// before anything else, so their HBM latency overlaps the workgroup's quantisation of the rows
+// into LDS; longer rows continue in chunks of KBC k-blocks.
+template <int MR, int KBC>
 __global__ __launch_bounds__(THREADS) void gemv_i8_kernel(const float *__restrict__ a, size_t lda, int k,
                                                           const uint8_t *__restrict__ wv,
                                                           const float *__restrict__ scales, int N, int P, int KB,
@@ -38,6 +49,14 @@ __global__ __launch_bounds__(THREADS) void gemv_i8_kernel(const float *__restric
     __shared__ int32_t sexp[MR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t row_bytes = (size_t)KB * 128;
+    const int p = blockIdx.x * (THREADS / 64) + wave;
+    const uint8_t *wp = wv + (size_t)min(p, P - 1) * panel_stride + lane * 16;
+
+    v4i wr[KBC];
+    if (KB > 0) {
+#pragma unroll
+        for (int t = 0; t < KBC; t++) wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(t, KB - 1) * blk_stride);
+    }
 
     // Digits of the rows, one wavefront per row.
     for (int r = wave; r < MR; r += THREADS / 64) {
@@ -65,66 +84,56 @@ __global__ __launch_bounds__(THREADS) void gemv_i8_kernel(const float *__restric
     __syncthreads();
 
     const int g = lane >> 4, j = lane & 15;
-    const int groups = (P + 3) / 4;
-    for (int grp = blockIdx.x * (THREADS / 64) + wave; grp < groups; grp += gridDim.x * (THREADS / 64)) {
-        int acc[4][MR][2];
-        for (int q = 0; q < 4; q++)
-            for (int r = 0; r < MR; r++) acc[q][r][0] = acc[q][r][1] = 0;
-        const uint8_t *wp[4];
-        for (int q = 0; q < 4; q++) {
-            const int p = min(grp * 4 + q, P - 1);
-            wp[q] = wv + (size_t)p * panel_stride + lane * 16;
+    int acc[MR][2];
+#pragma unroll
+    for (int r = 0; r < MR; r++) acc[r][0] = acc[r][1] = 0;
+    for (int c0 = 0; c0 < KB; c0 += KBC) {
+        if (c0 > 0) {
+#pragma unroll
+            for (int t = 0; t < KBC; t++)
+                wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(c0 + t, KB - 1) * blk_stride);
         }
-        for (int t = 0; t < KB; t++) {
-            uint4 w[4];
-            for (int q = 0; q < 4; q++) w[q] = *reinterpret_cast<const uint4 *>(wp[q] + (size_t)t * blk_stride);
-            for (int r = 0; r < MR; r++) {
-                const uint8_t *ap = sqa + r * row_bytes + t * 128 + g * 16;
-                const uint4 ahi = *reinterpret_cast<const uint4 *>(ap);
-                const uint4 alo = *reinterpret_cast<const uint4 *>(ap + 64);
-                for (int q = 0; q < 4; q++) {
-                    int h = acc[q][r][0], l = acc[q][r][1];
-                    h = __builtin_amdgcn_sdot4((int)ahi.x, (int)w[q].x, h, false);
-                    h = __builtin_amdgcn_sdot4((int)ahi.y, (int)w[q].y, h, false);
-                    h = __builtin_amdgcn_sdot4((int)ahi.z, (int)w[q].z, h, false);
-                    h = __builtin_amdgcn_sdot4((int)ahi.w, (int)w[q].w, h, false);
-                    l = __builtin_amdgcn_sdot4((int)alo.x, (int)w[q].x, l, false);
-                    l = __builtin_amdgcn_sdot4((int)alo.y, (int)w[q].y, l, false);
-                    l = __builtin_amdgcn_sdot4((int)alo.z, (int)w[q].z, l, false);
-                    l = __builtin_amdgcn_sdot4((int)alo.w, (int)w[q].w, l, false);
-                    acc[q][r][0] = h;
-                    acc[q][r][1] = l;
+#pragma unroll
+        for (int t = 0; t < KBC; t++) {
+            if (c0 + t < KB) {
+#pragma unroll
+                for (int r = 0; r < MR; r++) {
+                    const uint8_t *ap = sqa + r * row_bytes + (c0 + t) * 128 + g * 16;
+                    const v4i ahi = *reinterpret_cast<const v4i *>(ap);
+                    const v4i alo = *reinterpret_cast<const v4i *>(ap + 64);
+                    int h = acc[r][0], l = acc[r][1];
+                    h = __builtin_amdgcn_sdot4(ahi.x, wr[t].x, h, false);
+                    h = __builtin_amdgcn_sdot4(ahi.y, wr[t].y, h, false);
+                    h = __builtin_amdgcn_sdot4(ahi.z, wr[t].z, h, false);
+                    h = __builtin_amdgcn_sdot4(ahi.w, wr[t].w, h, false);
+                    l = __builtin_amdgcn_sdot4(alo.x, wr[t].x, l, false);
+                    l = __builtin_amdgcn_sdot4(alo.y, wr[t].y, l, false);
+                    l = __builtin_amdgcn_sdot4(alo.z, wr[t].z, l, false);
+                    l = __builtin_amdgcn_sdot4(alo.w, wr[t].w, l, false);
+                    acc[r][0] = h;
+                    acc[r][1] = l;
                 }
             }
         }
-        // Reduce-scatter over g. Step 1 (xor 32): lanes with g < 2 keep panels 0, 1 and take the
-        // partner's partial sums of them; lanes with g >= 2 keep panels 2, 3.
-        const bool upper = (g & 2) != 0, odd = (g & 1) != 0;
-        int half[2][MR][2];
-        for (int i = 0; i < 2; i++)
-            for (int r = 0; r < MR; r++)
-                for (int d = 0; d < 2; d++) {
-                    const int keep = upper ? acc[i + 2][r][d] : acc[i][r][d];
-                    const int send = upper ? acc[i][r][d] : acc[i + 2][r][d];
-                    half[i][r][d] = keep + __shfl_xor(send, 32, 64);
-                }
-        // Step 2 (xor 16): even g keeps the first of its two panels, odd g the second.
-        int fin[MR][2];
-        for (int r = 0; r < MR; r++)
-            for (int d = 0; d < 2; d++) {
-                const int keep = odd ? half[1][r][d] : half[0][r][d];
-                const int send = odd ? half[0][r][d] : half[1][r][d];
-                fin[r][d] = keep + __shfl_xor(send, 16, 64);
-            }
-        const int p = grp * 4 + g;
-        const int col = p * PANEL + j;
-        if (p < P && col < N) {
-            const float sc = scales[col];
-            for (int r = 0; r < MR; r++) {
-                float *cp = c + (size_t)r * ldc + col;
-                const float s = dequant(fin[r][0], fin[r][1], sexp[r], sc);
-                *cp = epilogue(s, bias, (size_t)col, act, escale, accumulate != 0, cp);
-            }
+    }
+    // Sum over the four 16-input groups (lanes j, j + 16, j + 32, j + 48).
+#pragma unroll
+    for (int r = 0; r < MR; r++)
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            int v = acc[r][d];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[r][d] = v;
+        }
+    const int col = p * PANEL + j;
+    if (g == 0 && p < P && col < N) {
+        const float sc = scales[col];
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            float *cp = c + (size_t)r * ldc + col;
+            const float s = dequant(acc[r][0], acc[r][1], sexp[r], sc);
+            *cp = epilogue(s, bias, (size_t)col, act, escale, accumulate != 0, cp);
         }
     }
 }
@@ -132,25 +141,245 @@ __global__ __launch_bounds__(THREADS) void gemv_i8_kernel(const float *__restric
 template <int MR>
 hipError_t launch_rows(const float *a, size_t lda, const DeviceWeights &w, float *c, size_t ldc, const EpiArgs &epi,
                        hipStream_t s) {
-    const size_t groups = div_ceil(w.panels, 4);
-    size_t blocks = div_ceil(groups, THREADS / 64);
-    if (blocks > 2048) blocks = 2048;
+    const size_t blocks = div_ceil(w.panels, THREADS / 64);
     const size_t lds = (size_t)MR * w.kb * 128;
-    hipLaunchKernelGGL(gemv_i8_kernel<MR>, dim3((unsigned)blocks), dim3(THREADS), lds, s, a, lda, (int)w.k,
-                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
-                       epi.accumulate, w.panel_stride, w.blk_stride);
+#define TG_GEMV(KBC)                                                                                     \
+    hipLaunchKernelGGL((gemv_i8_kernel<MR, KBC>), dim3((unsigned)blocks), dim3(THREADS), lds, s, a, lda,  \
+                       (int)w.k, w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias,  \
+                       epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride)
+    if (w.kb <= 10) TG_GEMV(10);
+    else TG_GEMV(20);
+#undef TG_GEMV
+    return hipGetLastError();
+}
+
+
+// The maximum over the 64 lanes (all active), returned to every lane. DPP moves within rows of
+// 16 lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror) leave each row's
+// maximum in all its lanes; the four rows meet through v_readlane. No LDS traffic.
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// What one wavefront needs of panel p: its KBC first weight blocks, and for its lane's column the
+// scale, the bias and the old outputs of its four rows (when accumulating).
+template <int KBC>
+__device__ __forceinline__ void fetch_panel(v4i (&wr)[KBC], float &sc, float &bv, float (&old)[4], int p, int lane,
+                                            const uint8_t *wv, size_t panel_stride, size_t blk_stride, int KB,
+                                            const float *scales, const float *bias, const float *c, size_t ldc,
+                                            int N, int m, int accumulate) {
+    const uint8_t *wp = wv + (size_t)p * panel_stride + lane * 16;
+#pragma unroll
+    for (int t = 0; t < KBC; t++) wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(t, KB - 1) * blk_stride);
+    const int col = p * PANEL + (lane & 15), orow = (lane >> 4) * 4;
+    sc = scales[col];
+    bv = bias ? bias[min(col, N - 1)] : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+        old[v] = (accumulate && orow + v < m && col < N) ? c[(size_t)(orow + v) * ldc + col] : 0.0f;
+}
+
+// The row exponent from the row's n <= 8 per-wavefront maxima (bits of |x|, all ones for a
+// non-finite input).
+__device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, int n) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+        if (s < n) mx = max(mx, slots[s]);
+    return mx == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(mx));
+}
+
+// Rows are split into 4-input chunks, ceil(KB / 4) wavefronts of them per row (the tail of the
+// last wavefront idle), and thread tid holds chunks tid + NT j (j < J) in registers: the rows are
+// read once, before the weights, so the weight loads stay in flight while the rows are digitised.
+template <int WAVES, int KBC, int J>
+__global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__restrict__ a, size_t lda, int m, int k,
+                                                               int vec, const uint8_t *__restrict__ wv,
+                                                               const float *__restrict__ scales, int N, int P, int KB,
+                                                               float *__restrict__ c, size_t ldc,
+                                                               const float *__restrict__ bias, uint32_t act,
+                                                               float escale, int accumulate, size_t panel_stride,
+                                                               size_t blk_stride) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];  // KB x (hi, lo) x 1 KB operands
+    __shared__ uint32_t slot[WAVES * J];                           // max |x| bits per wavefront of chunks
+    constexpr int NT = WAVES * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int spr = (KB + 3) / 4, cpr = spr * 64;  // wavefronts and chunk slots per row
+    const int step = gridDim.x * WAVES;
+    int p = blockIdx.x * WAVES + wave;
+
+    float4 x[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int ci = tid + NT * j, r = ci / cpr, i0 = (ci - r * cpr) * 4;
+        x[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < m && i0 < k) {
+            const float *ar = a + (size_t)r * lda + i0;
+            if (vec && i0 + 4 <= k) {
+                x[j] = *reinterpret_cast<const float4 *>(ar);
+            } else {
+                x[j].x = ar[0];
+                x[j].y = i0 + 1 < k ? ar[1] : 0.0f;
+                x[j].z = i0 + 2 < k ? ar[2] : 0.0f;
+                x[j].w = i0 + 3 < k ? ar[3] : 0.0f;
+            }
+        }
+    }
+    v4i wr[KBC];
+    float sc = 0.0f, bv = 0.0f, old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (p < P)
+        fetch_panel<KBC>(wr, sc, bv, old, p, lane, wv, panel_stride, blk_stride, KB, scales, bias, c, ldc, N, m,
+                         accumulate);
+
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const float4 v = x[j];
+        const bool bad = !__builtin_isfinite(v.x) | !__builtin_isfinite(v.y) | !__builtin_isfinite(v.z) |
+                         !__builtin_isfinite(v.w);
+        const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        const uint32_t b = wave_max_u(bad ? 0xffffffffu : __float_as_uint(mx));
+        if (lane == 0) slot[wave + WAVES * j] = b;
+    }
+    __syncthreads();
+    // Lane r < m of every wavefront holds row r's exponent; the rest read it from there.
+    const int32_t e_lane = lane < m ? exponent_from_slots(slot + lane * spr, spr) : 0;
+    // Digits: chunk cc of row r holds inputs 4 cc .. 4 cc + 3, i.e. k-block cc / 16 and bytes
+    // 4 (cc % 16) .. of that block's 64; they go where lane 16 (cc % 16 / 4) + r reads its A operand.
+    // A wavefront's chunks of one j lie in one row (cpr is a multiple of 64).
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int ci = __builtin_amdgcn_readfirstlane(wave * 64 + NT * j) + lane;
+        const int r = __builtin_amdgcn_readfirstlane((wave * 64 + NT * j) / cpr), cc = ci - r * cpr;
+        if (r < m && cc < KB * 16) {
+            const int32_t e = __builtin_amdgcn_readlane(e_lane, r);
+            uint32_t h, l;
+            digits4(x[j].x, x[j].y, x[j].z, x[j].w, e, h, l);
+            uint8_t *d = sqa + (cc >> 4) * 2048 + ((cc & 15) >> 2) * 256 + r * 16 + (cc & 3) * 4;
+            *reinterpret_cast<uint32_t *>(d) = h;
+            *reinterpret_cast<uint32_t *>(d + 1024) = l;
+        }
+    }
+    // C operand of the MFMA: element v of lane l is row 4 (l / 16) + v, column l % 16. Rows m..15
+    // of the A operands are never written; their outputs are never stored.
+    const int orow = (lane >> 4) * 4, ocol = lane & 15;
+    int32_t erow[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) erow[v] = __shfl(e_lane, min(orow + v, 15), 64);
+    __syncthreads();
+
+    const uint8_t *ap = sqa + lane * 16;
+    for (; p < P; p += step) {
+        v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+        const uint8_t *wp = wv + (size_t)p * panel_stride + lane * 16;
+        for (int c0 = 0; c0 < KB; c0 += KBC) {
+            if (c0 > 0) {
+#pragma unroll
+                for (int t = 0; t < KBC; t++)
+                    wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(c0 + t, KB - 1) * blk_stride);
+            }
+#pragma unroll
+            for (int t = 0; t < KBC; t++) {
+                if (c0 + t < KB) {
+                    const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
+                    const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
+                    acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
+                    acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
+                }
+            }
+        }
+        const float sc0 = sc, bv0 = bv;
+        float old0[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) old0[v] = old[v];
+        if (p + step < P)
+            fetch_panel<KBC>(wr, sc, bv, old, p + step, lane, wv, panel_stride, blk_stride, KB, scales, bias, c, ldc,
+                             N, m, accumulate);
+        const int col = p * PANEL + ocol;
+        if (col < N) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                if (orow + v < m) {
+                    const float s = dequant(acc_hi[v], acc_lo[v], erow[v], sc0);
+                    c[(size_t)(orow + v) * ldc + col] =
+                        epilogue_vals(s, bias != nullptr, bv0, act, escale, accumulate != 0, old0[v]);
+                }
+            }
+        }
+    }
+}
+
+constexpr int MFMA_MAX_KB = 31;       // digits within 62 KB of LDS
+constexpr size_t MFMA_MAX_WAVE_ROWS = 64;  // m * ceil(KB / 4): chunk wavefronts, at most 16 per thread of 256
+constexpr size_t MFMA_MAX_GRID = 1024;     // four resident workgroups per CU; more panels are walked
+
+bool mfma_fits(size_t m, size_t kb) {
+    return m >= 1 && m <= GEMV_MAX_ROWS && kb >= 1 && kb <= (size_t)MFMA_MAX_KB &&
+           m * div_ceil(kb, (size_t)4) <= MFMA_MAX_WAVE_ROWS;
+}
+
+template <int WAVES, int KBC, int J>
+void launch_mfma_t(const float *a, size_t lda, size_t m, int vec, const DeviceWeights &w, float *c, size_t ldc,
+                   const EpiArgs &epi, size_t blocks, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, KBC, J>), dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a,
+                       lda, (int)m, (int)w.k, vec, w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc,
+                       epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
+}
+
+template <int WAVES, int KBC>
+void launch_mfma_j(size_t j, const float *a, size_t lda, size_t m, int vec, const DeviceWeights &w, float *c,
+                   size_t ldc, const EpiArgs &epi, size_t blocks, hipStream_t s) {
+    if (j <= 1) launch_mfma_t<WAVES, KBC, 1>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    else launch_mfma_t<WAVES, KBC, 16>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+}
+
+hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                       const EpiArgs &epi, hipStream_t s) {
+    const int vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (lda % 4 == 0);
+    const size_t chunks = m * div_ceil(w.kb, (size_t)4) * 64;
+    // Two-wave workgroups for short products, so they spread over more CUs.
+    int waves = w.panels < 1024 ? 2 : 4;
+    size_t j = div_ceil(chunks, (size_t)waves * 64);
+    if (j > 16) {
+        waves = 4;
+        j = div_ceil(chunks, (size_t)256);
+    }
+    if (j > 16) return hipErrorInvalidValue;  // excluded by mfma_fits
+    const size_t per_wave = div_ceil(w.panels, (size_t)waves * MFMA_MAX_GRID);
+    const size_t blocks = div_ceil(w.panels, (size_t)waves * per_wave);
+    if (waves == 2) {
+        if (w.kb <= 10) launch_mfma_j<2, 10>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
+        else launch_mfma_j<2, 16>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    } else {
+        if (w.kb <= 10) launch_mfma_j<4, 10>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
+        else launch_mfma_j<4, 16>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
 bool gemv_fits(size_t m, size_t k) {
-    return m >= 1 && m <= GEMV_MAX_ROWS && m * div_ceil(k, KBLK) * 128 <= GEMV_LDS_BUDGET;
+    const size_t kb = div_ceil(k, KBLK);
+    if (m == 0 || k == 0) return false;
+    return mfma_fits(m, kb) || (m <= 8 && m * kb * 128 <= GEMV_LDS_BUDGET);
 }
 
 hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                           const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
+    if (mfma_fits(m, w.kb)) return launch_mfma(a, lda, m, w, c, ldc, epi, s);
     switch (m) {
     case 1: return launch_rows<1>(a, lda, w, c, ldc, epi, s);
     case 2: return launch_rows<2>(a, lda, w, c, ldc, epi, s);

@@ -85,17 +85,6 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restr
     if (lane == 0) exps[row] = e;
 }
 
-// The digits of four consecutive inputs packed as (hi dword, lo dword).
-__device__ __forceinline__ void digits4(const float4 &v, int32_t e, uint32_t &hi, uint32_t &lo) {
-    int8_t h0, l0, h1, l1, h2, l2, h3, l3;
-    digits_of(v.x, e, h0, l0);
-    digits_of(v.y, e, h1, l1);
-    digits_of(v.z, e, h2, l2);
-    digits_of(v.w, e, h3, l3);
-    hi = (uint32_t)(uint8_t)h0 | (uint32_t)(uint8_t)h1 << 8 | (uint32_t)(uint8_t)h2 << 16 | (uint32_t)(uint8_t)h3 << 24;
-    lo = (uint32_t)(uint8_t)l0 | (uint32_t)(uint8_t)l1 << 8 | (uint32_t)(uint8_t)l2 << 16 | (uint32_t)(uint8_t)l3 << 24;
-}
-
 // One workgroup per row, the row held in registers: thread t owns the 4-input chunks t + 256 j
 // (j < J), loaded as one float4 when the rows are 16-byte aligned. A block reduction gives the
 // row's exponent; each thread then writes the 4 hi and 4 lo digits of each chunk as two dwords
@@ -144,7 +133,7 @@ __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__
         const int c = tid + 256 * j;
         if (c < chunks) {
             uint32_t hi, lo;
-            digits4(v[j], e, hi, lo);
+            digits4(v[j].x, v[j].y, v[j].z, v[j].w, e, hi, lo);
             // chunk c: k-block c / 16, 16-input group (c % 16) / 4, byte (c % 4) * 4 of its 16
             const size_t at = qa_offset(row, c >> 4, 0, kb) + ((c & 15) >> 2) * 256 + (c & 3) * 4;
             *reinterpret_cast<uint32_t *>(qa + at) = hi;

@@ -81,18 +81,25 @@ __device__ __forceinline__ float exp_simd(float x) {
 }
 
 // The epilogue of one output (src/kernels/avx512.rs:313-343): bias, activation, scale, then
-// accumulate onto the old value. ReLU is x86 MAXPS(v, 0): v if v > 0, else 0.
-__device__ __forceinline__ float epilogue(float v, const float *bias, size_t col, uint32_t act, float scale,
-                                          bool accumulate, const float *cptr) {
-    if (bias) v = v + bias[col];
+// accumulate onto the old value. ReLU is x86 MAXPS(v, 0): v if v > 0, else 0. The bias value b and
+// the old output are used only when has_bias / accumulate are set.
+__device__ __forceinline__ float epilogue_vals(float v, bool has_bias, float b, uint32_t act, float scale,
+                                               bool accumulate, float old) {
+    if (has_bias) v = v + b;
     if (act == ACT_RELU) {
         v = v > 0.0f ? v : 0.0f;
     } else if (act == ACT_SILU) {
         v = v / (1.0f + exp_simd(0.0f - v));
     }
     v = v * scale;
-    if (accumulate) v = *cptr + v;
+    if (accumulate) v = old + v;
     return v;
+}
+
+__device__ __forceinline__ float epilogue(float v, const float *bias, size_t col, uint32_t act, float scale,
+                                          bool accumulate, const float *cptr) {
+    return epilogue_vals(v, bias != nullptr, bias ? bias[col] : 0.0f, act, scale, accumulate,
+                         accumulate ? *cptr : 0.0f);
 }
 
 // The f32 sum of the integer path: S = 256 acc_hi + acc_lo exactly, one rounding to f32, times
@@ -126,6 +133,26 @@ __device__ __forceinline__ void digits_of(float a, int32_t e, int8_t &hi, int8_t
     lo = (int8_t)l;
 }
 
+// The digits of four consecutive inputs packed as (hi dword, lo dword): the same digits as
+// digits_of, since lo = v mod 256 (as a signed byte) is the low byte of v, and
+// hi = (v - lo) / 256 = (v + 128) >> 8 is byte 1 of v + 128 (|v| <= 32639).
+__device__ __forceinline__ void digits4(float x0, float x1, float x2, float x3, int32_t e, uint32_t &hi,
+                                        uint32_t &lo) {
+    const bool ok = e != EXP_NONFINITE;
+    const uint32_t v0 = ok ? (uint32_t)(int32_t)__builtin_rintf(__builtin_ldexpf(x0, e)) : 0u;
+    const uint32_t v1 = ok ? (uint32_t)(int32_t)__builtin_rintf(__builtin_ldexpf(x1, e)) : 0u;
+    const uint32_t v2 = ok ? (uint32_t)(int32_t)__builtin_rintf(__builtin_ldexpf(x2, e)) : 0u;
+    const uint32_t v3 = ok ? (uint32_t)(int32_t)__builtin_rintf(__builtin_ldexpf(x3, e)) : 0u;
+    // v_perm_b32(s0, s1, sel): byte i of the result is byte sel_i of s0:s1 (0-3 from s1, 4-7 from
+    // s0), 0x0c gives zero.
+    const uint32_t lo01 = __builtin_amdgcn_perm(v1, v0, 0x0c0c0400u);
+    const uint32_t lo23 = __builtin_amdgcn_perm(v3, v2, 0x0c0c0400u);
+    lo = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(v1 + 128u, v0 + 128u, 0x0c0c0501u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(v3 + 128u, v2 + 128u, 0x0c0c0501u);
+    hi = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+}
+
 // ---------------------------------------------------------------------------- launchers
 
 struct EpiArgs {
@@ -149,8 +176,10 @@ hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *
 hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s);
 
-// The dot4 GEMV for m <= 8 (quantises the rows itself).
-constexpr size_t GEMV_MAX_ROWS = 8;
+// The decode GEMVs (quantise the rows themselves): the MFMA GEMV for m <= 16 rows of k <= 1984
+// inputs (m * ceil(k / 256) <= 64), else the dot4 GEMV for m <= 8 rows whose digits fit 64 KB of
+// LDS.
+constexpr size_t GEMV_MAX_ROWS = 16;
 bool gemv_fits(size_t m, size_t k);
 hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                           const EpiArgs &epi, hipStream_t s);

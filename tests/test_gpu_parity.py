@@ -73,7 +73,8 @@ def test_exact_mode_is_bit_identical_to_the_fused_reference(tk, orc, p):
 
 
 FAST_SHAPES = [(1, 1, 1), (3, 7, 5), (8, 64, 16), (9, 64, 16), (13, 100, 50), (64, 128, 96), (130, 1000, 255),
-               (200, 640, 8198), (257, 2048, 130), (1, 4096, 1024), (8, 1280, 2560)]
+               (200, 640, 8198), (257, 2048, 130), (1, 4096, 1024), (8, 1280, 2560), (16, 2048, 100),
+               (4, 2112, 300), (16, 2049, 77), (2, 64, 140000), (11, 700, 20000)]
 
 
 @pytest.mark.parametrize("m,k,n", FAST_SHAPES)
@@ -112,7 +113,7 @@ def test_gemv_rows_equal_gemm_rows(tk):
     full = np.zeros(m * n, np.float32)
     tk.linear(a.reshape(-1), m, w, full, epi)
     full = full.reshape(m, n)
-    for rows in range(1, 9):
+    for rows in range(1, 17):
         for r0 in (0, 17, m - rows):
             part = np.zeros(rows * n, np.float32)
             tk.linear(np.ascontiguousarray(a[r0:r0 + rows]).reshape(-1), rows, w, part, epi)
