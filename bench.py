@@ -385,7 +385,7 @@ def main():
     ap.add_argument("--no-gemv", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        sys.exit("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)")
+        sys.exit("bench.py measures one GPU and has no multi-GPU path: run it with --gpus 1")
 
     rng = np.random.default_rng(0)
     weights = make_weights(rng)

@@ -1,8 +1,8 @@
 /*
  * Oracle for telmo's int8-weight matrix product: a plain-C restatement of the reference's
  * CPU algorithm. TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
- * bench's cpu_baseline leg load this library, and only as the checker. The product path
- * (telmo_amd/) never links, loads or calls it.
+ * bench's cpu_baseline leg load this library, and only to check results against. The product
+ * path (telmo_amd/) never links, loads or calls it.
  *
  * Built with -ffp-contract=off so that every `a * b + c` below is two roundings, and
  * every fused step is an explicit fmaf().
@@ -29,7 +29,7 @@
  * widen == decode for every int8 value and every scale exponent (mod.rs:1130-1183), and
  * exp/sigmoid accuracy against math.exp (mod.rs:1261-1277).
  *
- * The second half of the file is the integer oracle of this build's fast path (two int8
+ * The second half of the file is the integer oracle of telmo_amd's fast path (two int8
  * digits per activation, exact i32 sums, one shared dequantisation). It has no counterpart
  * in the reference; tests pin it with numpy int64 products and invariants of the digit split.
  */

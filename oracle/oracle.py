@@ -1,7 +1,7 @@
 """ctypes view of the oracle library (test infrastructure only).
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this module,
-and only as the checker. The product (``telmo_amd``) never imports it.
+and only to check results against. The product (``telmo_amd``) never imports it.
 """
 import ctypes
 import os

@@ -107,7 +107,7 @@ int run_device(tg_ctx *ctx, const float *a, size_t lda, size_t m, const tg_weigh
         TG_HIP(ctx, tg::launch_exact(a, lda, m, d, c, ldc, epi, ctx->stream));
         return TG_OK;
     }
-    if (tg::gemv_fits(m, d.k)) {
+    if (tg::gemv_fits(m, d.k, a, lda)) {
         TG_HIP(ctx, tg::launch_gemv_i8(a, lda, m, d, c, ldc, epi, ctx->stream));
         return TG_OK;
     }

@@ -5,14 +5,14 @@
 // weights in the MFMA layout: per k-block of 64 inputs of a 16-output panel, lane l = 16 g + j
 // loads 16 contiguous bytes (inputs 64 t + 16 g + [0, 16) of output j), 1 KB per wave, coalesced.
 //
-// gemv_mfma_kernel (m <= 16, k <= 1984): the digits sit in LDS as 16 x 64 MFMA A operands in lane
+// gemv_mfma_kernel (m <= 16, k <= 1984, 16-byte aligned rows, k % 4 == 0): the digits sit in LDS as 16 x 64 MFMA A operands in lane
 // order, so each 1 KB weight block costs one 16-byte LDS read per digit and two
 // v_mfma_i32_16x16x64_i8, whatever m is. The rows are read once into registers ahead of the
 // weights; workgroups stay resident and walk the panels, so the rows are digitised once per
 // workgroup, and the next panel's weights, scales, bias and old outputs are requested before the
 // current panel's epilogue.
 //
-// gemv_i8_kernel (m <= 8, longer rows): one panel per wavefront, v_dot4_i32_i8 against each
+// gemv_i8_kernel (m <= 8, other rows): one panel per wavefront, v_dot4_i32_i8 against each
 // row's digits; the four input groups meet by lane exchanges (xor 16, xor 32).
 #include "tg_internal.hpp"
 
@@ -34,6 +34,11 @@ __device__ __forceinline__ int wave_or(int v) {
 }
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Four zero inputs: what the MFMA GEMV loads for chunks past the end of a row. Never written; not
+// const, so that it lives in global memory like the rows and the loads stay global loads.
+__device__ __attribute__((aligned(16))) float ZERO_CHUNK[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
 // One weight panel (16 outputs) per wavefront. The panel's first KBC k-blocks are requested
 // before anything else, so their HBM latency overlaps the workgroup's quantisation of the rows
@@ -179,12 +184,16 @@ __device__ __forceinline__ void fetch_panel(v4i (&wr)[KBC], float &sc, float &bv
     const uint8_t *wp = wv + (size_t)p * panel_stride + lane * 16;
 #pragma unroll
     for (int t = 0; t < KBC; t++) wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(t, KB - 1) * blk_stride);
+    // Branch-free: loads that are not needed read a valid address and are discarded, so the
+    // compiler's load counting stays exact and nothing here waits on earlier loads.
     const int col = p * PANEL + (lane & 15), orow = (lane >> 4) * 4;
     sc = scales[col];
-    bv = bias ? bias[min(col, N - 1)] : 0.0f;
+    bv = *(bias ? bias + min(col, N - 1) : scales + col);
 #pragma unroll
-    for (int v = 0; v < 4; v++)
-        old[v] = (accumulate && orow + v < m && col < N) ? c[(size_t)(orow + v) * ldc + col] : 0.0f;
+    for (int v = 0; v < 4; v++) {
+        const bool need = accumulate && orow + v < m && col < N;
+        old[v] = *(need ? c + (size_t)(orow + v) * ldc + col : c);
+    }
 }
 
 // The row exponent from the row's n <= 8 per-wavefront maxima (bits of |x|, all ones for a
@@ -198,11 +207,12 @@ __device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, in
 }
 
 // Rows are split into 4-input chunks, ceil(KB / 4) wavefronts of them per row (the tail of the
-// last wavefront idle), and thread tid holds chunks tid + NT j (j < J) in registers: the rows are
-// read once, before the weights, so the weight loads stay in flight while the rows are digitised.
+// last wavefront idle); wavefront w holds chunk wavefronts w + WAVES j (j < J) in registers. The
+// rows are read once, before the weights, so the weight loads stay in flight while the rows are
+// digitised.
 template <int WAVES, int KBC, int J>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__restrict__ a, size_t lda, int m, int k,
-                                                               int vec, const uint8_t *__restrict__ wv,
+                                                               const uint8_t *__restrict__ wv,
                                                                const float *__restrict__ scales, int N, int P, int KB,
                                                                float *__restrict__ c, size_t ldc,
                                                                const float *__restrict__ bias, uint32_t act,
@@ -210,61 +220,63 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
                                                                size_t blk_stride) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];  // KB x (hi, lo) x 1 KB operands
     __shared__ uint32_t slot[WAVES * J];                           // max |x| bits per wavefront of chunks
-    constexpr int NT = WAVES * 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int spr = (KB + 3) / 4, cpr = spr * 64;  // wavefronts and chunk slots per row
+    // Chunk wavefront q = wave + WAVES j covers chunks 64 (q - r spr) + [0, 64) of row
+    // r = q / spr, where spr = ceil(KB / 4) wavefronts cover a row (its tail idle). All of it is
+    // uniform over the wavefront; q / spr is (q inv) >> 16, exact for q < 1024 and spr <= 8.
+    const int spr = (KB + 3) / 4, inv = (65536 + spr - 1) / spr;
+    const int wq = __builtin_amdgcn_readfirstlane(wave);
     const int step = gridDim.x * WAVES;
     int p = blockIdx.x * WAVES + wave;
 
-    float4 x[J];
+    // One 16-byte load per chunk (rows 16-byte aligned, k % 4 == 0); chunks past the rows read
+    // the zero chunk. Every load is unconditional and used as loaded, so the loads stay ahead of
+    // the weight loads and waiting for them never waits for the weights.
+    v4f x[J];
 #pragma unroll
     for (int j = 0; j < J; j++) {
-        const int ci = tid + NT * j, r = ci / cpr, i0 = (ci - r * cpr) * 4;
-        x[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < m && i0 < k) {
-            const float *ar = a + (size_t)r * lda + i0;
-            if (vec && i0 + 4 <= k) {
-                x[j] = *reinterpret_cast<const float4 *>(ar);
-            } else {
-                x[j].x = ar[0];
-                x[j].y = i0 + 1 < k ? ar[1] : 0.0f;
-                x[j].z = i0 + 2 < k ? ar[2] : 0.0f;
-                x[j].w = i0 + 3 < k ? ar[3] : 0.0f;
-            }
-        }
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        const int i0 = ((q - r * spr) * 64 + lane) * 4;
+        const float *src = (r < m && i0 < k) ? a + (size_t)r * lda + i0 : ZERO_CHUNK;
+        x[j] = *reinterpret_cast<const v4f *>(src);
     }
+    // Panel fetches are unconditional (a wavefront past the last panel re-reads panel P - 1 and
+    // never uses it): under a branch the compiler's load counting would wait for them early.
     v4i wr[KBC];
-    float sc = 0.0f, bv = 0.0f, old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (p < P)
-        fetch_panel<KBC>(wr, sc, bv, old, p, lane, wv, panel_stride, blk_stride, KB, scales, bias, c, ldc, N, m,
-                         accumulate);
+    float sc, bv, old[4];
+    fetch_panel<KBC>(wr, sc, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias, c, ldc, N,
+                     m, accumulate);
 
 #pragma unroll
     for (int j = 0; j < J; j++) {
-        const float4 v = x[j];
-        const bool bad = !__builtin_isfinite(v.x) | !__builtin_isfinite(v.y) | !__builtin_isfinite(v.z) |
-                         !__builtin_isfinite(v.w);
-        const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        const uint32_t b = wave_max_u(bad ? 0xffffffffu : __float_as_uint(mx));
-        if (lane == 0) slot[wave + WAVES * j] = b;
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        if (r < m) {
+            const v4f v = x[j];
+            const bool bad = !__builtin_isfinite(v.x) | !__builtin_isfinite(v.y) | !__builtin_isfinite(v.z) |
+                             !__builtin_isfinite(v.w);
+            const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            const uint32_t b = wave_max_u(bad ? 0xffffffffu : __float_as_uint(mx));
+            if (lane == 0) slot[q] = b;
+        }
     }
     __syncthreads();
     // Lane r < m of every wavefront holds row r's exponent; the rest read it from there.
     const int32_t e_lane = lane < m ? exponent_from_slots(slot + lane * spr, spr) : 0;
     // Digits: chunk cc of row r holds inputs 4 cc .. 4 cc + 3, i.e. k-block cc / 16 and bytes
     // 4 (cc % 16) .. of that block's 64; they go where lane 16 (cc % 16 / 4) + r reads its A operand.
-    // A wavefront's chunks of one j lie in one row (cpr is a multiple of 64).
 #pragma unroll
     for (int j = 0; j < J; j++) {
-        const int ci = __builtin_amdgcn_readfirstlane(wave * 64 + NT * j) + lane;
-        const int r = __builtin_amdgcn_readfirstlane((wave * 64 + NT * j) / cpr), cc = ci - r * cpr;
-        if (r < m && cc < KB * 16) {
-            const int32_t e = __builtin_amdgcn_readlane(e_lane, r);
-            uint32_t h, l;
-            digits4(x[j].x, x[j].y, x[j].z, x[j].w, e, h, l);
-            uint8_t *d = sqa + (cc >> 4) * 2048 + ((cc & 15) >> 2) * 256 + r * 16 + (cc & 3) * 4;
-            *reinterpret_cast<uint32_t *>(d) = h;
-            *reinterpret_cast<uint32_t *>(d + 1024) = l;
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        if (r < m) {
+            const int cc = (q - r * spr) * 64 + lane;
+            if (cc < KB * 16) {
+                const int32_t e = __builtin_amdgcn_readlane(e_lane, r);
+                uint32_t h, l;
+                digits4(x[j].x, x[j].y, x[j].z, x[j].w, e, h, l);
+                uint8_t *d = sqa + (cc >> 4) * 2048 + ((cc & 15) >> 2) * 256 + r * 16 + (cc & 3) * 4;
+                *reinterpret_cast<uint32_t *>(d) = h;
+                *reinterpret_cast<uint32_t *>(d + 1024) = l;
+            }
         }
     }
     // C operand of the MFMA: element v of lane l is row 4 (l / 16) + v, column l % 16. Rows m..15
@@ -299,9 +311,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
         float old0[4];
 #pragma unroll
         for (int v = 0; v < 4; v++) old0[v] = old[v];
-        if (p + step < P)
-            fetch_panel<KBC>(wr, sc, bv, old, p + step, lane, wv, panel_stride, blk_stride, KB, scales, bias, c, ldc,
-                             N, m, accumulate);
+        fetch_panel<KBC>(wr, sc, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias,
+                         c, ldc, N, m, accumulate);
         const int col = p * PANEL + ocol;
         if (col < N) {
 #pragma unroll
@@ -320,33 +331,37 @@ constexpr int MFMA_MAX_KB = 31;       // digits within 62 KB of LDS
 constexpr size_t MFMA_MAX_WAVE_ROWS = 64;  // m * ceil(KB / 4): chunk wavefronts, at most 16 per thread of 256
 constexpr size_t MFMA_MAX_GRID = 1024;     // four resident workgroups per CU; more panels are walked
 
-bool mfma_fits(size_t m, size_t kb) {
+// The MFMA GEMV reads rows with 16-byte loads: rows 16-byte aligned, k a multiple of 4.
+bool mfma_fits(size_t m, size_t k, const float *a, size_t lda) {
+    const size_t kb = div_ceil(k, KBLK);
     return m >= 1 && m <= GEMV_MAX_ROWS && kb >= 1 && kb <= (size_t)MFMA_MAX_KB &&
-           m * div_ceil(kb, (size_t)4) <= MFMA_MAX_WAVE_ROWS;
+           m * div_ceil(kb, (size_t)4) <= MFMA_MAX_WAVE_ROWS && reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
+           lda % 4 == 0 && k % 4 == 0;
 }
 
 template <int WAVES, int KBC, int J>
-void launch_mfma_t(const float *a, size_t lda, size_t m, int vec, const DeviceWeights &w, float *c, size_t ldc,
+void launch_mfma_t(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                    const EpiArgs &epi, size_t blocks, hipStream_t s) {
     hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, KBC, J>), dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a,
-                       lda, (int)m, (int)w.k, vec, w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc,
+                       lda, (int)m, (int)w.k, w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc,
                        epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
 }
 
 template <int WAVES, int KBC>
-void launch_mfma_j(size_t j, const float *a, size_t lda, size_t m, int vec, const DeviceWeights &w, float *c,
+void launch_mfma_j(size_t j, const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c,
                    size_t ldc, const EpiArgs &epi, size_t blocks, hipStream_t s) {
-    if (j <= 1) launch_mfma_t<WAVES, KBC, 1>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
-    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
-    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
-    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
-    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
-    else launch_mfma_t<WAVES, KBC, 16>(a, lda, m, vec, w, c, ldc, epi, blocks, s);
+    if (j <= 1) launch_mfma_t<WAVES, KBC, 1>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else if (j <= 3) launch_mfma_t<WAVES, KBC, 3>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else if (j <= 6) launch_mfma_t<WAVES, KBC, 6>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12>(a, lda, m, w, c, ldc, epi, blocks, s);
+    else launch_mfma_t<WAVES, KBC, 16>(a, lda, m, w, c, ldc, epi, blocks, s);
 }
 
 hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                        const EpiArgs &epi, hipStream_t s) {
-    const int vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (lda % 4 == 0);
     const size_t chunks = m * div_ceil(w.kb, (size_t)4) * 64;
     // Two-wave workgroups for short products, so they spread over more CUs.
     int waves = w.panels < 1024 ? 2 : 4;
@@ -359,27 +374,27 @@ hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights
     const size_t per_wave = div_ceil(w.panels, (size_t)waves * MFMA_MAX_GRID);
     const size_t blocks = div_ceil(w.panels, (size_t)waves * per_wave);
     if (waves == 2) {
-        if (w.kb <= 10) launch_mfma_j<2, 10>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
-        else launch_mfma_j<2, 16>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
+        if (w.kb <= 10) launch_mfma_j<2, 10>(j, a, lda, m, w, c, ldc, epi, blocks, s);
+        else launch_mfma_j<2, 16>(j, a, lda, m, w, c, ldc, epi, blocks, s);
     } else {
-        if (w.kb <= 10) launch_mfma_j<4, 10>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
-        else launch_mfma_j<4, 16>(j, a, lda, m, vec, w, c, ldc, epi, blocks, s);
+        if (w.kb <= 10) launch_mfma_j<4, 10>(j, a, lda, m, w, c, ldc, epi, blocks, s);
+        else launch_mfma_j<4, 16>(j, a, lda, m, w, c, ldc, epi, blocks, s);
     }
     return hipGetLastError();
 }
 
 }  // namespace
 
-bool gemv_fits(size_t m, size_t k) {
+bool gemv_fits(size_t m, size_t k, const float *a, size_t lda) {
     const size_t kb = div_ceil(k, KBLK);
     if (m == 0 || k == 0) return false;
-    return mfma_fits(m, kb) || (m <= 8 && m * kb * 128 <= GEMV_LDS_BUDGET);
+    return mfma_fits(m, k, a, lda) || (m <= 8 && m * kb * 128 <= GEMV_LDS_BUDGET);
 }
 
 hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                           const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    if (mfma_fits(m, w.kb)) return launch_mfma(a, lda, m, w, c, ldc, epi, s);
+    if (mfma_fits(m, w.k, a, lda)) return launch_mfma(a, lda, m, w, c, ldc, epi, s);
     switch (m) {
     case 1: return launch_rows<1>(a, lda, w, c, ldc, epi, s);
     case 2: return launch_rows<2>(a, lda, w, c, ldc, epi, s);

@@ -177,10 +177,10 @@ hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, cons
                           size_t ldc, const EpiArgs &epi, hipStream_t s);
 
 // The decode GEMVs (quantise the rows themselves): the MFMA GEMV for m <= 16 rows of k <= 1984
-// inputs (m * ceil(k / 256) <= 64), else the dot4 GEMV for m <= 8 rows whose digits fit 64 KB of
-// LDS.
+// inputs (m * ceil(k / 256) <= 64; 16-byte aligned rows, k % 4 == 0), else the dot4 GEMV for
+// m <= 8 rows whose digits fit 64 KB of LDS.
 constexpr size_t GEMV_MAX_ROWS = 16;
-bool gemv_fits(size_t m, size_t k);
+bool gemv_fits(size_t m, size_t k, const float *a, size_t lda);
 hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                           const EpiArgs &epi, hipStream_t s);
 
