@@ -39,11 +39,11 @@ enum { TG_F32 = 0, TG_F16 = 1, TG_BF16 = 2, TG_INT8 = 3, TG_Q8_0 = 4 };
 enum { TG_ACT_NONE = 0, TG_ACT_RELU = 1, TG_ACT_SILU = 2 };
 
 /* Numerics of a context.
- * TG_MODE_FAST: int8 weights run the two-digit int8 MFMA GEMM (m > 8) or the dot4 GEMV
- *   (m <= 8). Activations are split per row into two int8 digits of a 15-bit fixed-point value;
- *   sums are exact in i32; results are bit-identical for any m, tiling or split, and within about
- *   1e-4 row-normwise of the reference's fused f32 sums (gate 1e-3). Other precisions run the
- *   exact kernel.
+ * TG_MODE_FAST: int8 weights run the two-digit int8 path: the MFMA GEMM, or for m <= 16 decode
+ *   rows the MFMA GEMV (the dot4 GEMV for m <= 8 rows it cannot take). Activations are split per
+ *   row into two int8 digits of a 15-bit fixed-point value; sums are exact in i32; results are
+ *   bit-identical for any m, kernel, tiling or split, and within about 1e-4 row-normwise of the
+ *   reference's fused f32 sums (gate 1e-3). Other precisions run the exact kernel.
  * TG_MODE_EXACT: one lane per output sums fmaf(a, widen(w), acc) in input order, bit-identical
  *   to the reference's AVX2 / AVX-512 / NEON kernels, epilogue included. Slow; for validation. */
 enum { TG_MODE_FAST = 0, TG_MODE_EXACT = 1 };

@@ -8,6 +8,7 @@
 // Dispatch (fast mode, int8 weights): m <= 8 with the row digits fitting the GEMV's LDS -> the
 // dot4 GEMV (one launch); otherwise the row quantiser then the MFMA GEMM (two launches). Other
 // precisions, the exact mode, and k beyond the integer path's limit run the exact kernel.
+#include <cstring>
 #include <mutex>
 #include <string>
 
@@ -29,6 +30,9 @@ struct tg_ctx {
     // Device staging of the host-pointer entry points, grown on demand.
     float *da = nullptr, *dc = nullptr, *dbias = nullptr;
     size_t da_cap = 0, dc_cap = 0, dbias_cap = 0;
+    // Pinned host staging of the same: rows are gathered here so each direction is one DMA.
+    float *hst = nullptr;
+    size_t hst_cap = 0;
 };
 
 struct tg_weights {
@@ -71,6 +75,32 @@ int grow(tg_ctx *ctx, T *&buf, size_t &cap, size_t bytes) {
     buf = static_cast<T *>(p);
     cap = want;
     return TG_OK;
+}
+
+// Pinned host staging (hipHostMalloc), grown on demand; the stream is idle between host calls.
+int grow_host(tg_ctx *ctx, size_t bytes) {
+    if (bytes <= ctx->hst_cap) return TG_OK;
+    if (ctx->hst) {
+        TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        TG_HIP(ctx, hipHostFree(ctx->hst));
+        ctx->hst = nullptr;
+        ctx->hst_cap = 0;
+    }
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess)
+        return fail(ctx, TG_ERR_NOMEM, "pinned host allocation failed");
+    ctx->hst = static_cast<float *>(p);
+    ctx->hst_cap = bytes;
+    return TG_OK;
+}
+
+// Copies m rows of cols floats between a strided and a packed buffer (host memory).
+void copy_rows(float *dst, size_t ldd, const float *src, size_t lds, size_t m, size_t cols) {
+    if (ldd == cols && lds == cols) {
+        std::memcpy(dst, src, m * cols * sizeof(float));
+        return;
+    }
+    for (size_t r = 0; r < m; r++) std::memcpy(dst + r * ldd, src + r * lds, cols * sizeof(float));
 }
 
 // The checks of Kernels::matmul (src/kernels/mod.rs:669-677), in its order.
@@ -213,6 +243,7 @@ void tg_ctx_destroy(tg_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (void *p : {(void *)ctx->qa, (void *)ctx->exps, (void *)ctx->da, (void *)ctx->dc, (void *)ctx->dbias})
         if (p) (void)hipFree(p);
+    if (ctx->hst) (void)hipHostFree(ctx->hst);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -293,20 +324,32 @@ int tg_matmul(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, c
     if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
     TG_HIP(ctx, hipSetDevice(ctx->device));
     const size_t k = w->d.k, n = w->d.n;
-    // Compact device copies: a as [m][k], c as [m][n]; the strided host rows move with 2-D copies,
-    // so the columns between rows of c are never written.
+    // Compact device copies: a as [m][k], c as [m][n]. The rows are gathered into pinned staging
+    // ([m][k] then [m][n] floats) and move in one DMA each way; only the n columns of each row of
+    // c are written back, so the columns between rows are never touched.
+    const bool has_bias = epi && epi->bias, acc = epi && epi->accumulate;
     if ((rc = grow(ctx, ctx->da, ctx->da_cap, m * (k ? k : 1) * sizeof(float)))) return rc;
     if ((rc = grow(ctx, ctx->dc, ctx->dc_cap, m * n * sizeof(float)))) return rc;
-    const bool has_bias = epi && epi->bias;
     if (has_bias && (rc = grow(ctx, ctx->dbias, ctx->dbias_cap, n * sizeof(float)))) return rc;
-    if (k) TG_HIP(ctx, hipMemcpy2DAsync(ctx->da, k * 4, a, lda * 4, k * 4, m, hipMemcpyHostToDevice, ctx->stream));
-    if (epi && epi->accumulate)
-        TG_HIP(ctx, hipMemcpy2DAsync(ctx->dc, n * 4, c, ldc * 4, n * 4, m, hipMemcpyHostToDevice, ctx->stream));
-    if (has_bias) TG_HIP(ctx, hipMemcpyAsync(ctx->dbias, epi->bias, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = grow_host(ctx, (m * k + m * n + (has_bias ? n : 0)) * sizeof(float)))) return rc;
+    float *ha = ctx->hst, *hc = ha + m * k, *hb = hc + m * n;
+    if (k) {
+        copy_rows(ha, k, a, lda, m, k);
+        TG_HIP(ctx, hipMemcpyAsync(ctx->da, ha, m * k * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
+    if (acc) {
+        copy_rows(hc, n, c, ldc, m, n);
+        TG_HIP(ctx, hipMemcpyAsync(ctx->dc, hc, m * n * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
+    if (has_bias) {
+        std::memcpy(hb, epi->bias, n * 4);
+        TG_HIP(ctx, hipMemcpyAsync(ctx->dbias, hb, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    }
     rc = run_device(ctx, ctx->da, k, m, w, ctx->dc, n, epi_args(epi, ctx->dbias, has_bias));
     if (rc) return rc;
-    TG_HIP(ctx, hipMemcpy2DAsync(c, ldc * 4, ctx->dc, n * 4, n * 4, m, hipMemcpyDeviceToHost, ctx->stream));
+    TG_HIP(ctx, hipMemcpyAsync(hc, ctx->dc, m * n * 4, hipMemcpyDeviceToHost, ctx->stream));
     TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    copy_rows(c, ldc, hc, n, m, n);
     ctx->err.clear();
     return TG_OK;
 }

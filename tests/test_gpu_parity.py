@@ -4,7 +4,8 @@
   store, mod.rs gemm_panels) for every precision, shape and epilogue.
 * Fast mode, int8 weights: bit-identical to the integer oracle (two int8 digits, exact i32 sums,
   one dequantisation), and within 1e-4 row-normwise of the reference's fused f32 sums (gate 1e-3).
-* The GEMV (m <= 8) and GEMM paths give the same bits for the same row.
+* The GEMVs (m <= 16) and the GEMM give the same bits for the same row.
+* The committed golden fixtures (tests/golden) hold in both modes.
 """
 import numpy as np
 import pytest
@@ -262,3 +263,27 @@ def test_config_1_at_full_size(tk, orc):
     err = rel_norm_err(got.reshape(m, n), ref.reshape(m, n))
     print(f"[config1] row-normwise error vs the fused reference: {err:.3e}")
     assert err <= 1e-3
+
+
+def test_golden_fixtures(tk):
+    """The committed fixtures (tests/golden): exact mode gives the fused reference's bits for every
+    precision; fast mode gives the integer oracle's bits for int8."""
+    from golden_cases import ACT, PREC, cases, load
+
+    for meta in cases():
+        g = load(meta)
+        m, k, n, lda, ldc = meta["m"], meta["k"], meta["n"], meta["lda"], meta["ldc"]
+        bias = g["bias"] if meta["bias"] else None
+        p, act = PREC[meta["precision"]], ACT[meta["act"]]
+        say("golden", meta["name"])
+        tk.set_mode(tk.EXACT)
+        try:
+            got = run_gpu(tk, g["a"], lda, m, g["values"], g["scales"], p, n, k, g["c0"], ldc, bias, act,
+                          meta["accumulate"], meta["scale"])
+        finally:
+            tk.set_mode(tk.FAST)
+        assert np.array_equal(got.view(np.uint32), g["c_fused"].view(np.uint32)), meta["name"]
+        if meta["precision"] == "int8":
+            got = run_gpu(tk, g["a"], lda, m, g["values"], g["scales"], p, n, k, g["c0"], ldc, bias, act,
+                          meta["accumulate"], meta["scale"])
+            assert np.array_equal(got.view(np.uint32), g["c_fast"].view(np.uint32)), meta["name"]
