@@ -67,6 +67,37 @@ def bytes_of(m):
     return total
 
 
+def run_layer(kern, W, bufs, T):
+    """The layer's products in order: FFN (SiLU, half-step residual), QKV, attention output (the V
+    third of QKV standing in for attention), the conv module's pointwise pair around the GLU, and
+    the second FFN. bufs holds x [T, D], h [T, FF], qkv [T, 3D], g [T, CONV], u [T, D]."""
+    from telmo_amd import Act, Epilogue
+
+    x, h, qkv, g, u = (bufs[key] for key in ("x", "h", "qkv", "g", "u"))
+    silu = Epilogue(act=Act.SILU)
+    half_acc = Epilogue(scale=0.5, accumulate=True)
+    acc = Epilogue(accumulate=True)
+    kern.linear_device(x, T, W["ff1_up"], h, silu)
+    kern.linear_device(h, T, W["ff1_down"], x, half_acc)
+    kern.linear_device(x, T, W["qkv"], qkv)
+    kern.matmul_device(qkv[:, 2 * D:], 3 * D, T, W["att_out"], x, D, acc, a_len=qkv.numel() - 2 * D)
+    kern.linear_device(x, T, W["pw1"], g)
+    kern.glu_device(g, CONV, T, D, u, D)
+    kern.linear_device(u, T, W["pw2"], x, acc)
+    kern.linear_device(x, T, W["ff2_up"], h, silu)
+    kern.linear_device(h, T, W["ff2_down"], x, half_acc)
+
+
+def layer_buffers(T, dev="cuda"):
+    import torch
+
+    return {"x": torch.empty((T, D), dtype=torch.float32, device=dev),
+            "h": torch.empty((T, FF), dtype=torch.float32, device=dev),
+            "qkv": torch.empty((T, 3 * D), dtype=torch.float32, device=dev),
+            "g": torch.empty((T, CONV), dtype=torch.float32, device=dev),
+            "u": torch.empty((T, D), dtype=torch.float32, device=dev)}
+
+
 def make_weights(rng):
     out = []
     for name, k, n, *_ in LAYER:
@@ -96,27 +127,13 @@ def gpu_leg(args, weights, x0_host):
     T = T_FRAMES
     dev = "cuda"
     x0 = torch.from_numpy(x0_host).to(dev)
-    x = x0.clone()
-    h = torch.empty((T, FF), dtype=torch.float32, device=dev)
-    qkv = torch.empty((T, 3 * D), dtype=torch.float32, device=dev)
-    g = torch.empty((T, CONV), dtype=torch.float32, device=dev)
-    u = torch.empty((T, D), dtype=torch.float32, device=dev)
+    bufs = layer_buffers(T, dev)
+    x, h, qkv, u = bufs["x"], bufs["h"], bufs["qkv"], bufs["u"]
     v = qkv[:, 2 * D:]
-    silu = Epilogue(act=Act.SILU)
-    half_acc = Epilogue(scale=0.5, accumulate=True)
-    acc = Epilogue(accumulate=True)
 
     def step():
         x.copy_(x0)
-        kern.linear_device(x, T, W["ff1_up"], h, silu)
-        kern.linear_device(h, T, W["ff1_down"], x, half_acc)
-        kern.linear_device(x, T, W["qkv"], qkv)
-        kern.matmul_device(v, 3 * D, T, W["att_out"], x, D, acc, a_len=qkv.numel() - 2 * D)
-        kern.linear_device(x, T, W["pw1"], g)
-        kern.glu_device(g, CONV, T, D, u, D)
-        kern.linear_device(u, T, W["pw2"], x, acc)
-        kern.linear_device(x, T, W["ff2_up"], h, silu)
-        kern.linear_device(h, T, W["ff2_down"], x, half_acc)
+        run_layer(kern, W, bufs, T)
 
     for _ in range(args.warmup):
         step()
@@ -171,6 +188,74 @@ def gpu_leg(args, weights, x0_host):
         w.close()
     kern.close()
     return eager_ms, graph_ms, per_shape
+
+
+ENC_LAYERS = 24
+# (workload, rows, audio seconds): 32 utterances of 30 s at 80 ms per frame; one 600 s utterance.
+ENC_CASES = [("batch of 32 x 30 s utterances", 32 * 375, 960.0), ("one 600 s utterance", 7500, 600.0)]
+
+
+def encoder_leg(args):
+    """The encoder stack: 24 Conformer layers of the layer step's shapes, each with its own random
+    int8 weights and scales (580 MB in all, generated on the GPU), LayerNorm (gamma 1, beta 0)
+    after every layer to keep the activations N(0, 1). Audio-seconds per second = the audio the
+    rows stand for / the time of one pass over all 24 layers."""
+    import torch
+
+    import telmo_amd
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    layers, wbytes = [], 0
+    for _ in range(ENC_LAYERS):
+        W = {}
+        for name, k, n, *_ in LAYER:
+            q = torch.randint(-127, 128, (n * k,), generator=gen, device="cuda", dtype=torch.int16)
+            q = q.to(torch.int8).view(torch.uint8)
+            sc = 0.001 + 0.009 * torch.rand(n, generator=gen, device="cuda")
+            W[name] = telmo_amd.PackedWeights.from_device(kern, n, k, telmo_amd.Precision.INT8, q, sc)
+            wbytes += W[name].bytes()
+            del q, sc
+        layers.append(W)
+    gamma = torch.ones(D, device="cuda")
+    beta = torch.zeros(D, device="cuda")
+    out = []
+    for label, M, audio_s in ENC_CASES:
+        x0 = torch.randn((M, D), generator=gen, device="cuda")
+        bufs = layer_buffers(M)
+        x = bufs["x"]
+
+        def run():
+            x.copy_(x0)
+            for W in layers:
+                run_layer(kern, W, bufs, M)
+                kern.layer_norm_device(x, D, M, D, gamma, beta, 1e-5, x, D)
+
+        run()
+        torch.cuda.synchronize()
+        if not torch.isfinite(x).all():
+            raise RuntimeError("the encoder output is not finite")
+        reps = 3
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        ops = ENC_LAYERS * ops_of(M)
+        out.append({"workload": f"{ENC_LAYERS}-layer encoder, {label}", "m": M, "audio_s": audio_s,
+                    "ms_per_pass": round(ms, 3), "audio_s_per_s": round(audio_s / (ms * 1e-3), 1),
+                    "tops": round(ops / (ms * 1e-3) / 1e12, 1), "weights_mb": round(wbytes / 1e6, 1)})
+        del bufs, x0
+    for W in layers:
+        for w in W.values():
+            w.close()
+    kern.close()
+    return out
 
 
 def _pack(rng, n, k):
@@ -388,7 +473,10 @@ def cpu_leg(weights, x0_host, budget_s):
             "kind": "port", "isa": "avx512" if isa == 2 else "avx2",
             "sample": f"the same 8-GEMM layer at T={T}, best of 5 rounds of {reps} layers "
                       f"({reps * 5 * best:.1f} s in all), {cores} threads",
-            "ms_per_step": round(best * 1e3, 3)}
+            "ms_per_step": round(best * 1e3, 3),
+            "encoder_audio_s_per_s": round(T * 0.08 / (ENC_LAYERS * best), 1),
+            "encoder_note": f"{ENC_LAYERS} layers of this step per {T} frames (80 ms each): the CPU path's "
+                            "encoder audio-seconds per second, GEMMs only, scaled from the sample"}
 
 
 def load_traffic():
@@ -408,6 +496,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU and has no multi-GPU path: run it with --gpus 1")
@@ -431,6 +520,7 @@ def main():
                 "per_shape": per_shape}
     gemv = None if args.no_gemv else gemv_leg(args)
     host = host_leg(weights, x0)
+    encoder = None if args.no_encoder else encoder_leg(args)
     cpu = None if args.no_cpu else cpu_leg(weights, x0, args.cpu_seconds)
     value = ops / (graph_ms * 1e-3) / 1e12
     line = {
@@ -446,6 +536,7 @@ def main():
         "cpu_baseline": cpu,
         "gemv": gemv,
         "pcie_inclusive": host,
+        "encoder": encoder,
     }
     print(json.dumps(line))
 

@@ -13,6 +13,7 @@
  *   Kernels::matmul              src/kernels/mod.rs:657-688   -> tg_matmul, tg_matmul_device
  *   Kernels::linear              src/kernels/mod.rs:691-701   -> tg_linear, tg_linear_device
  *   Kernels::glu (row kernel)    src/kernels/mod.rs:463-464   -> tg_glu_device
+ *   Kernels::layer_norm          src/kernels/mod.rs:458       -> tg_layer_norm_device
  *
  * Error behaviour follows the reference's asserts (src/kernels/mod.rs:669-677): m == 0 or n == 0
  * is a no-op that succeeds before any other check; then lda >= k, ldc >= n, the lengths of a and
@@ -138,6 +139,12 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
 /* out[r, j] = x[r, j] * sigmoid(x[r, half + j]) for j < half (the GLU of a convolution module),
  * with the exp of the reference's SIMD kernels. Device pointers, queued on the stream. */
 int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo);
+
+/* out[r, :] = LayerNorm(x[r, :]) * gamma + beta over n values per row, with the summation order of
+ * the reference's AVX-512 layer_norm (src/kernels/avx512.rs:346-380). gamma and beta hold n device
+ * floats; out may equal x. Device pointers, queued on the stream. */
+int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                         const float *beta, float eps, float *out, size_t ldo);
 
 /* ---- the panel layout (host utilities, no device needed) ---------------------------------- */
 

@@ -18,6 +18,8 @@
  *   or_tile               src/kernels/scalar.rs:26-49 (unfused) and avx512.rs:70-105,
  *                         avx2.rs:62-107 (fused, sums in input order)
  *   or_exp_simd           src/kernels/avx512.rs:279-304 == avx2.rs:305-331 (same steps)
+ *   or_glu                src/kernels/avx512.rs:410-430
+ *   or_layer_norm         src/kernels/avx512.rs:346-380 (AVX-512 summation order)
  *   or_store              src/kernels/scalar.rs:110-124 (unfused, libm exp) and
  *                         avx512.rs:313-343 (fused ISAs)
  *   or_matmul             src/kernels/mod.rs:530-688   (gemm_panels with KC = 256, the
@@ -298,6 +300,42 @@ float or_exp_simd(float x) {
 }
 
 float or_silu_simd(float v) { return v / (1.0f + or_exp_simd(0.0f - v)); }
+
+/* glu: out = a / (1 + exp(0 - b)) with the SIMD exp (src/kernels/avx512.rs:410-430). */
+void or_glu(const float *a, const float *b, float *out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = a[i] / (1.0f + or_exp_simd(0.0f - b[i]));
+}
+
+/* Sum of sixteen partials as the reduction of a 512-bit register: halves added lane by lane
+ * (j + 8, then j + 4, j + 2, j + 1). */
+static float reduce16(const float *p) {
+    float h8[8], h4[4], h2[2];
+    for (int j = 0; j < 8; j++) h8[j] = p[j] + p[j + 8];
+    for (int j = 0; j < 4; j++) h4[j] = h8[j] + h8[j + 4];
+    for (int j = 0; j < 2; j++) h2[j] = h4[j] + h4[j + 2];
+    return h2[0] + h2[1];
+}
+
+/* layer_norm of one row, AVX-512 (src/kernels/avx512.rs:346-380): sixteen partial sums over the
+ * row in steps of 16 (masked tail lanes add zero), reduced; mean = sum / n; partial fma(d, d, q)
+ * with d = x - mean (zero in masked lanes); rstd = 1 / sqrt(q / n + eps); out = fma((x - mean) *
+ * rstd, gamma, beta). */
+void or_layer_norm(const float *x, size_t n, float *out, const float *gamma, const float *beta, float eps) {
+    float s[16] = {0}, q[16] = {0};
+    for (size_t i = 0; i < n; i += 16)
+        for (size_t j = 0; j < 16; j++) s[j] = s[j] + (i + j < n ? x[i + j] : 0.0f);
+    const float mean = reduce16(s) / (float)n;
+    for (size_t i = 0; i < n; i += 16)
+        for (size_t j = 0; j < 16; j++) {
+            const float d = i + j < n ? x[i + j] - mean : 0.0f;
+            q[j] = fmaf(d, d, q[j]);
+        }
+    const float rstd = 1.0f / sqrtf(reduce16(q) / (float)n + eps);
+    for (size_t i = 0; i < n; i++) {
+        const float d = (x[i] - mean) * rstd;
+        out[i] = fmaf(d, gamma[i], beta[i]);
+    }
+}
 
 float or_activate_scalar(float v, int act) {
     switch (act) {

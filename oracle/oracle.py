@@ -67,6 +67,8 @@ def lib():
         L.or_exp_simd.restype = ctypes.c_float
         L.or_silu_simd.argtypes = [ctypes.c_float]
         L.or_silu_simd.restype = ctypes.c_float
+        L.or_glu.argtypes = [_f32p, _f32p, _f32p, _sz]
+        L.or_layer_norm.argtypes = [_f32p, _sz, _f32p, _f32p, _f32p, ctypes.c_float]
         L.or_store.argtypes = [ctypes.c_int, _f32p, _f32p, _sz, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
                                ctypes.c_int]
         mm = [_f32p, _sz, _sz, _sz, _u8p, ctypes.c_void_p, ctypes.c_int, _sz, _sz, _f32p, _sz, _sz,
@@ -190,6 +192,22 @@ def exp_simd(x):
 
 def silu_simd(x):
     return np.float32(lib().or_silu_simd(float(x)))
+
+
+def glu(a, b):
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    out = np.zeros_like(a)
+    lib().or_glu(a, b, out, a.size)
+    return out
+
+
+def layer_norm(x, gamma, beta, eps):
+    """One row, the reference's AVX-512 order."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    lib().or_layer_norm(x, x.size, out, np.ascontiguousarray(gamma, np.float32),
+                        np.ascontiguousarray(beta, np.float32), float(eps))
+    return out
 
 
 def store(fused, acc, c, cols, bias, act, scale, accumulate):

@@ -32,6 +32,7 @@ SIGNATURES = {
     "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
+    "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, ctypes.c_float, _p, _sz]),
     "tg_panel_bytes": (_sz, [_u32, _sz, _sz]),
     "tg_scale_count": (_sz, [_u32, _sz, _sz]),
     "tg_fits": (ctypes.c_int, [_u32, _sz]),

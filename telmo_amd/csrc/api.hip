@@ -396,6 +396,19 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
     return TG_OK;
 }
 
+int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                         const float *beta, float eps, float *out, size_t ldo) {
+    if (!ctx) return TG_ERR_NULL;
+    if (m == 0 || n == 0) return TG_OK;
+    if (!x || !gamma || !beta || !out) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (ldx < n || ldo < n) return fail(ctx, TG_ERR_SHAPE, "ldx and ldo must be >= n");
+    if (n > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "rows longer than 2^31 values");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_layer_norm(x, ldx, m, n, gamma, beta, eps, out, ldo, ctx->stream));
+    return TG_OK;
+}
+
 int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;
     if (m == 0 || half == 0) return TG_OK;

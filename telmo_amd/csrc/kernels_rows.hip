@@ -1,6 +1,6 @@
 // Row kernels of the int8 path: the one-time re-layout of int8 / Q8_0 weight panels into the
-// MFMA layout, the per-row two-digit quantisation of f32 activations, and the GLU row kernel.
-// All of them are HBM-bound byte work: coalesced loads, no MFMA.
+// MFMA layout, the per-row two-digit quantisation of f32 activations, and the GLU and LayerNorm
+// row kernels of the Conformer glue. All of them are HBM-bound: coalesced loads, no MFMA.
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -185,6 +185,56 @@ hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *
     size_t blocks = div_ceil(total, 256);
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(glu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, ldx, m, half, out, ldo);
+    return hipGetLastError();
+}
+
+// LayerNorm of rows of n values as the reference's AVX-512 kernel computes it
+// (src/kernels/avx512.rs:346-380): sixteen partial sums, partial j adding inputs j, j + 16, ... in
+// order, folded by halves (j + 8, j + 4, j + 2, j + 1) into the row sum; mean = sum / n; the same
+// for fma(d, d, q) with d = x - mean; rstd = 1 / sqrt(q / n + eps); out = fma((x - mean) rstd,
+// gamma, beta). Sixteen lanes per row hold the sixteen partials, so a wavefront takes four rows.
+// out may be x (each input is read before its own output is written).
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, size_t ldx, size_t m, int n,
+                                                         const float *__restrict__ gamma,
+                                                         const float *__restrict__ beta, float eps, float *out,
+                                                         size_t ldo) {
+    const int j = threadIdx.x & 15;
+    const size_t row = (size_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool valid = row < m;
+    const float *xr = x + (valid ? row : 0) * ldx;
+    float s = 0.0f;
+    if (valid)
+        for (int i = j; i < n; i += 16) s = s + xr[i];
+    s = s + __shfl_xor(s, 8, 16);
+    s = s + __shfl_xor(s, 4, 16);
+    s = s + __shfl_xor(s, 2, 16);
+    s = s + __shfl_xor(s, 1, 16);
+    const float mean = s / (float)n;
+    float q = 0.0f;
+    if (valid)
+        for (int i = j; i < n; i += 16) {
+            const float d = xr[i] - mean;
+            q = __builtin_fmaf(d, d, q);
+        }
+    q = q + __shfl_xor(q, 8, 16);
+    q = q + __shfl_xor(q, 4, 16);
+    q = q + __shfl_xor(q, 2, 16);
+    q = q + __shfl_xor(q, 1, 16);
+    const float rstd = 1.0f / __builtin_sqrtf(q / (float)n + eps);
+    if (valid) {
+        float *orow = out + row * ldo;
+        for (int i = j; i < n; i += 16) {
+            const float d = (xr[i] - mean) * rstd;
+            orow[i] = __builtin_fmaf(d, gamma[i], beta[i]);
+        }
+    }
+}
+
+hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+                             float eps, float *out, size_t ldo, hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)div_ceil(m, (size_t)16)), dim3(256), 0, s, x, ldx, m, (int)n,
+                       gamma, beta, eps, out, ldo);
     return hipGetLastError();
 }
 

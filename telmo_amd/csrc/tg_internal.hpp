@@ -172,6 +172,10 @@ hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, 
 // out[r][j] = x[r][j] * sigmoid(x[r][half + j]).
 hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s);
 
+// LayerNorm of m rows of n values (the reference's AVX-512 summation order).
+hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+                             float eps, float *out, size_t ldo, hipStream_t s);
+
 // The two-digit int8 MFMA GEMM over quantised rows.
 hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s);

@@ -120,6 +120,17 @@ class PackedWeights:
         return PackedWeights(kernels, out, n, k, precision)
 
     @staticmethod
+    def from_device(kernels: "Kernels", n: int, k: int, precision: Precision, values, scales=None):
+        """from_parts on GPU tensors (uint8 values, float32 scales) already in the panel layout."""
+        out = ctypes.c_void_p()
+        rc = _lib.lib().tg_weights_upload_device(kernels._ctx, ctypes.c_void_p(values.data_ptr()), values.numel(),
+                                                 None if scales is None else ctypes.c_void_p(scales.data_ptr()),
+                                                 0 if scales is None else scales.numel(), int(precision), n, k,
+                                                 ctypes.byref(out))
+        _check(rc, kernels._ctx)
+        return PackedWeights(kernels, out, n, k, precision)
+
+    @staticmethod
     def encode(kernels: "Kernels", rows, n: int, k: int, precision: Precision):
         """Packs row-major [n, k] f32 rows in `precision`, quantising or rounding as needed."""
         values, scales = encode(rows, n, k, precision)
@@ -283,6 +294,13 @@ class Kernels:
     def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int):
         rc = _lib.lib().tg_glu_device(self._ctx, ctypes.c_void_p(x.data_ptr()), ldx, m, half,
                                       ctypes.c_void_p(out.data_ptr()), ldo)
+        _check(rc, self._ctx)
+
+    def layer_norm_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, out, ldo: int):
+        """LayerNorm of m rows of GPU tensor x (n values each) into out (may be x)."""
+        rc = _lib.lib().tg_layer_norm_device(self._ctx, ctypes.c_void_p(x.data_ptr()), ldx, m, n,
+                                             ctypes.c_void_p(gamma.data_ptr()), ctypes.c_void_p(beta.data_ptr()),
+                                             float(eps), ctypes.c_void_p(out.data_ptr()), ldo)
         _check(rc, self._ctx)
 
     def synchronize(self) -> None:

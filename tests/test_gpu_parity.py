@@ -287,3 +287,27 @@ def test_golden_fixtures(tk):
             got = run_gpu(tk, g["a"], lda, m, g["values"], g["scales"], p, n, k, g["c0"], ldc, bias, act,
                           meta["accumulate"], meta["scale"])
             assert np.array_equal(got.view(np.uint32), g["c_fast"].view(np.uint32)), meta["name"]
+
+
+def test_layer_norm_matches_the_reference_order(tk, orc):
+    """LayerNorm rows on the GPU are bit-identical to the oracle's AVX-512 restatement, in place too."""
+    import torch
+
+    rng = np.random.default_rng(17)
+    for m, n, ldx in ((37, 1024, 1024), (5, 1000, 1003), (19, 17, 17), (3, 1, 4)):
+        x = (2.0 + 3.0 * rng.standard_normal((m, ldx))).astype(np.float32)
+        gamma = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        say("layer_norm", m, n, ldx)
+        want = np.array([orc.layer_norm(x[r, :n], gamma, beta, 1e-5) for r in range(m)], np.float32)
+        xd = torch.from_numpy(x).cuda()
+        gd, bd = torch.from_numpy(gamma).cuda(), torch.from_numpy(beta).cuda()
+        out = torch.full((m, n + 2), 9.5, dtype=torch.float32, device="cuda")
+        tk.layer_norm_device(xd, ldx, m, n, gd, bd, 1e-5, out, n + 2)
+        tk.layer_norm_device(xd, ldx, m, n, gd, bd, 1e-5, xd, ldx)  # in place
+        tk.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:, :n].view(np.uint32), want.view(np.uint32)), (m, n)
+        assert np.all(got[:, n:] == 9.5)
+        got_in_place = xd.cpu().numpy()
+        assert np.array_equal(got_in_place[:, :n].view(np.uint32), want.view(np.uint32)), (m, n)
