@@ -14,7 +14,8 @@
 // pipeline: LDS writes run at about 64 B/clk/CU, and the two-digit A tile doubles them.
 //
 // Tiles: wavefront RB x CB MFMA blocks of 16 x 16 (workgroup 32 RB x 32 CB outputs). The launcher
-// takes 4 x 4 (128 x 128 per workgroup) when that fills the chip twice over, else 2 x 2 (64 x 64).
+// takes 4 x 4 (128 x 128 per workgroup, tiles in XCD-contiguous runs) when that fills the chip twice
+// over, else 2 x 2 (64 x 64, tiles walked four tile-rows at a time).
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -25,7 +26,33 @@ namespace {
 
 constexpr int THREADS = 256;
 
-template <int RB, int CB, int S, int OCC>
+// Order in which workgroups take tiles. Workgroup L of a launch goes to XCD L % 8 (each XCD has
+// its own L2). XCD: hand each XCD a contiguous run of tiles (rows of the tile grid), so the A row
+// blocks its tiles share stay in its L2. G > 0: walk the tiles G tile-rows at a time, column by
+// column, so a weight panel is reused by G row blocks while it is hot.
+template <int XCD, int G>
+__device__ __forceinline__ void tile_of(int &bx, int &by) {
+    bx = blockIdx.x;
+    by = blockIdx.y;
+    if constexpr (XCD || G) {
+        const int gx = gridDim.x, gy = gridDim.y, total = gx * gy;
+        int L = by * gx + bx;
+        if constexpr (XCD) {
+            const int full = total - total % 8;
+            if (L < full) L = (L % 8) * (full / 8) + L / 8;
+        }
+        if constexpr (G > 0) {
+            const int group = L / (G * gx), first = group * G, rows = min(G, gy - first), local = L - group * G * gx;
+            by = first + local % rows;
+            bx = local / rows;
+        } else {
+            by = L / gx;
+            bx = L % gx;
+        }
+    }
+}
+
+template <int RB, int CB, int S, int OCC, int XCD, int G>
 __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
                                                                const int32_t *__restrict__ exps, int M,
                                                                const uint8_t *__restrict__ wv,
@@ -39,7 +66,9 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
     __shared__ float staged[4][WM * C_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = blockIdx.y * 2 * WM + wm * WM, n0 = blockIdx.x * 2 * WN + wn * WN;
+    int bx, by;
+    tile_of<XCD, G>(bx, by);
+    const int m0 = by * 2 * WM + wm * WM, n0 = bx * 2 * WN + wn * WN;
     const int R0 = m0 / 16, P0 = n0 / 16, RLAST = (M + 15) / 16 - 1;
     const int out_col = lane & 15, out_row = (lane >> 4) * 4;
 
@@ -142,12 +171,12 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
     }
 }
 
-template <int RB, int CB, int S, int OCC>
+template <int RB, int CB, int S, int OCC, int XCD, int G>
 hipError_t launch_tile(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                        const EpiArgs &epi, hipStream_t s) {
     const size_t bm = 2 * RB * 16, bn = 2 * CB * 16;
     dim3 grid((unsigned)div_ceil(w.panels * PANEL, bn), (unsigned)div_ceil(m, bm));
-    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, OCC>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
+    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, OCC, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
                        w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
                        epi.accumulate, w.panel_stride, w.blk_stride);
     return hipGetLastError();
@@ -165,8 +194,8 @@ int gemm_tile_choice(size_t m, size_t panels) {
 hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    if (gemm_tile_choice(m, w.panels) == 0) return launch_tile<4, 4, 2, 2>(qf, exps, m, w, c, ldc, epi, s);
-    return launch_tile<2, 2, 3, 2>(qf, exps, m, w, c, ldc, epi, s);
+    if (gemm_tile_choice(m, w.panels) == 0) return launch_tile<4, 4, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+    return launch_tile<2, 2, 3, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 
 }  // namespace tg
