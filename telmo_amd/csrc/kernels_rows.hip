@@ -89,14 +89,22 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restr
 // (j < J), loaded as one float4 when the rows are 16-byte aligned. A block reduction gives the
 // row's exponent; each thread then writes the 4 hi and 4 lo digits of each chunk as two dwords
 // of the fragment-major QA. Chunks from k up to the 64-input padding are written as zeros.
+//
+// Rows go to workgroups so that the 16 rows of a QA row block run on one XCD: workgroup L runs on
+// XCD L % 8 and takes row 16 (x bpx + i / 16) + i % 16 with x = L % 8, i = L / 8, bpx = row blocks
+// per XCD. The row block's lines are then filled in one L2 instead of written back in pieces by
+// several. Workgroups past the last row exit at once.
 template <int J>
 __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__restrict__ a, size_t lda, int k,
                                                                  int kb, uint8_t *__restrict__ qa,
-                                                                 int32_t *__restrict__ exps, int vec) {
+                                                                 int32_t *__restrict__ exps, int vec, size_t m,
+                                                                 size_t bpx) {
     __shared__ float s_max[4];
     __shared__ int s_bad[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const size_t row = blockIdx.x;
+    const size_t x = blockIdx.x % 8, i = blockIdx.x / 8;
+    const size_t row = (x * bpx + i / 16) * 16 + i % 16;
+    if (row >= m) return;
     const float *ar = a + row * lda;
     float4 v[J];
     float amax = 0.0f;
@@ -145,8 +153,9 @@ __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__
 template <int J>
 void launch_regs(const float *a, size_t lda, size_t m, size_t k, size_t kb, uint8_t *qa, int32_t *exps, int vec,
                  hipStream_t s) {
-    hipLaunchKernelGGL(quantize_rows_regs_kernel<J>, dim3((unsigned)m), dim3(256), 0, s, a, lda, (int)k, (int)kb, qa,
-                       exps, vec);
+    const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
+    hipLaunchKernelGGL(quantize_rows_regs_kernel<J>, dim3((unsigned)(8 * bpx * 16)), dim3(256), 0, s, a, lda, (int)k,
+                       (int)kb, qa, exps, vec, m, bpx);
 }
 
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
