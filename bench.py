@@ -258,6 +258,70 @@ def encoder_leg(args):
     return out
 
 
+def q8_leg(args):
+    """The same Conformer layer step (T=750) and the decode GEMVs (m = 1, weights rotated past the
+    Infinity Cache) with Q8_0 weights: one f16-exact scale per 32 inputs of each output."""
+    import torch
+
+    import telmo_amd
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(13)
+
+    def q8_weights(n, k):
+        q = torch.randint(-127, 128, (-(-n // 16) * 16 * k,), generator=gen, device="cuda", dtype=torch.int16)
+        q = q.to(torch.int8).view(torch.uint8)
+        d = (0.001 + 0.009 * torch.rand(-(-n // 16) * 16 * (k // 32), generator=gen, device="cuda")).half().float()
+        return telmo_amd.PackedWeights.from_device(kern, n, k, telmo_amd.Precision.Q8_0, q, d)
+
+    def timed(fn, reps):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    W = {name: q8_weights(n, k) for name, k, n, *_ in LAYER}
+    T = T_FRAMES
+    x0 = torch.randn((T, D), generator=gen, device="cuda")
+    bufs = layer_buffers(T)
+
+    def step(_):
+        bufs["x"].copy_(x0)
+        run_layer(kern, W, bufs, T)
+
+    for i in range(10):
+        step(i)
+    t = timed(step, 50)
+    out = {"layer_step": {"workload": "conformer layer projection set at T=750 (8 GEMMs + GLU), Q8_0 weights",
+                          "ms_per_step": round(t * 1e3, 4), "tops": round(ops_of(T) / t / 1e12, 1)},
+           "rotating": []}
+    for w in W.values():
+        w.close()
+    for name, k, n in (("joint", 640, 8198), ("gates", 640, 2560)):
+        one = q8_weights(n, k)
+        copies = [one] + [q8_weights(n, k) for _ in range(int(600e6 // one.bytes()))]
+        a = torch.randn(1, k, device="cuda")
+        c = torch.empty(1, n, device="cuda")
+        call = lambda i: kern.linear_device(a, 1, copies[i % len(copies)], c)  # noqa: E731
+        for i in range(len(copies)):
+            call(i)
+        t = timed(call, 4 * len(copies))
+        out["rotating"].append({"gemv": name, "m": 1, "k": k, "n": n, "weight_mb": round(one.bytes() / 1e6, 3),
+                                "us": round(t * 1e6, 2), "gb_s": round(one.bytes() / t / 1e9, 1),
+                                "hbm_frac": round(one.bytes() / t / PEAK_HBM, 3)})
+        for w in copies:
+            w.close()
+    kern.close()
+    return out
+
+
 def _pack(rng, n, k):
     q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
     s = (0.001 + 0.009 * rng.random(n)).astype(np.float32)
@@ -497,6 +561,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-encoder", action="store_true")
+    ap.add_argument("--no-q8", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU and has no multi-GPU path: run it with --gpus 1")
@@ -521,6 +586,7 @@ def main():
     gemv = None if args.no_gemv else gemv_leg(args)
     host = host_leg(weights, x0)
     encoder = None if args.no_encoder else encoder_leg(args)
+    q8 = None if args.no_q8 else q8_leg(args)
     cpu = None if args.no_cpu else cpu_leg(weights, x0, args.cpu_seconds)
     value = ops / (graph_ms * 1e-3) / 1e12
     line = {
@@ -537,6 +603,7 @@ def main():
         "gemv": gemv,
         "pcie_inclusive": host,
         "encoder": encoder,
+        "q8_0": q8,
     }
     print(json.dumps(line))
 

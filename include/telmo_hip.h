@@ -40,11 +40,13 @@ enum { TG_F32 = 0, TG_F16 = 1, TG_BF16 = 2, TG_INT8 = 3, TG_Q8_0 = 4 };
 enum { TG_ACT_NONE = 0, TG_ACT_RELU = 1, TG_ACT_SILU = 2 };
 
 /* Numerics of a context.
- * TG_MODE_FAST: int8 weights run the two-digit int8 path: the MFMA GEMM, or for m <= 16 decode
- *   rows the MFMA GEMV (the dot4 GEMV for m <= 8 rows it cannot take). Activations are split per
- *   row into two int8 digits of a 15-bit fixed-point value; sums are exact in i32; results are
- *   bit-identical for any m, kernel, tiling or split, and within about 1e-4 row-normwise of the
- *   reference's fused f32 sums (gate 1e-3). Other precisions run the exact kernel.
+ * TG_MODE_FAST: int8 and Q8_0 weights run the two-digit int8 path: the MFMA GEMM, or for m <= 16
+ *   decode rows the MFMA GEMV (for int8, the dot4 GEMV for m <= 8 rows it cannot take).
+ *   Activations are split per row into two int8 digits of a 15-bit fixed-point value; sums are
+ *   exact in i32 (per 32-input block for Q8_0, whose block sums are scaled and added in f32 in
+ *   block order); results are bit-identical for any m, kernel, tiling or split, and within about
+ *   1e-4 row-normwise of the reference's fused f32 sums (gate 1e-3). Other precisions run the
+ *   exact kernel.
  * TG_MODE_EXACT: one lane per output sums fmaf(a, widen(w), acc) in input order, bit-identical
  *   to the reference's AVX2 / AVX-512 / NEON kernels, epilogue included. Slow; for validation. */
 enum { TG_MODE_FAST = 0, TG_MODE_EXACT = 1 };
@@ -129,8 +131,8 @@ int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const 
 size_t tg_quant_bytes(size_t m, size_t k);
 int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, size_t k, void *qa,
                             size_t qa_len, int32_t *exps);
-/* c = epilogue(product of the quantised rows and int8 weights w) on the MFMA GEMM, any m >= 1.
- * TG_ERR_UNSUPPORTED for weights other than int8 or k beyond the integer path's limit (65536). */
+/* c = epilogue(product of the quantised rows and int8 or Q8_0 weights w) on the MFMA GEMM, any
+ * m >= 1. TG_ERR_UNSUPPORTED for other weights or k beyond the integer path's limit (65536). */
 int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                const tg_weights *w, float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
 

@@ -522,3 +522,53 @@ int or_matmul_fast(const float *a, size_t a_len, size_t lda, size_t m, const uin
     free(qt);
     return OR_OK;
 }
+
+/* The fast path for Q8_0 weights (no counterpart in the reference, whose sums are all f32): per
+ * 32-input block b of output o, T_b = 256 sum(hi q) + sum(lo q) exactly (|T_b| < 2^31), then
+ * F = fmaf(d[o][b], (float)T_b, F) over the blocks in order from +0, and the row's 2^-e. NaN
+ * for rows holding a NaN or infinity. The epilogue is the fused one. */
+int or_matmul_fast_q8(const float *a, size_t a_len, size_t lda, size_t m, const uint8_t *values, const float *scales,
+                      size_t n, size_t k, float *c, size_t c_len, size_t ldc, const float *bias, size_t bias_len,
+                      int act, float scale, int accumulate) {
+    if (m == 0 || n == 0) return OR_OK;
+    if (lda < k || ldc < n) return OR_ERR_SHAPE;
+    if (a_len < (m - 1) * lda + k) return OR_ERR_SHAPE;
+    if (c_len < (m - 1) * ldc + n) return OR_ERR_SHAPE;
+    if (bias && bias_len < n) return OR_ERR_SHAPE;
+    if (k > 65536 || k % Q8_BLOCK) return OR_ERR_ARG;
+    size_t kk = k ? k : 1, panels = div_ceil(n, PANEL), blocks = k / Q8_BLOCK;
+    int8_t *hi = (int8_t *)malloc(m * kk), *lo = (int8_t *)malloc(m * kk);
+    int32_t *ex = (int32_t *)malloc(m * sizeof(int32_t));
+    int8_t *qt = (int8_t *)malloc(panels * PANEL * kk);
+    or_quantize_rows(a, lda, m, k, hi, lo, ex);
+    for (size_t o = 0; o < panels * PANEL; o++)
+        for (size_t i = 0; i < k; i++) qt[o * kk + i] = (int8_t)values[((o / PANEL) * k + i) * PANEL + o % PANEL];
+#pragma omp parallel for schedule(dynamic, 1)
+    for (size_t r = 0; r < m; r++) {
+        float sums[PANEL];
+        for (size_t o0 = 0; o0 < n; o0 += PANEL) {
+            size_t cols = n - o0 < PANEL ? n - o0 : PANEL;
+            for (size_t j = 0; j < cols; j++) {
+                const size_t o = o0 + j, p = o / PANEL;
+                const int8_t *q = qt + o * kk, *h = hi + r * kk, *l = lo + r * kk;
+                float f = 0.0f;
+                for (size_t b = 0; b < blocks; b++) {
+                    int32_t sh = 0, sl = 0;
+                    for (size_t i = b * Q8_BLOCK; i < (b + 1) * Q8_BLOCK; i++) {
+                        sh += (int32_t)h[i] * q[i];
+                        sl += (int32_t)l[i] * q[i];
+                    }
+                    const int32_t t = sh * 256 + sl;
+                    f = fmaf(scales[(p * blocks + b) * PANEL + o % PANEL], (float)t, f);
+                }
+                sums[j] = ex[r] == OR_EXP_NONFINITE ? NAN : ldexpf(f, -ex[r]);
+            }
+            or_store(1, sums, c + r * ldc + o0, cols, bias ? bias + o0 : NULL, act, scale, accumulate);
+        }
+    }
+    free(hi);
+    free(lo);
+    free(ex);
+    free(qt);
+    return OR_OK;
+}

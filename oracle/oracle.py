@@ -76,6 +76,7 @@ def lib():
         L.or_matmul.argtypes = [ctypes.c_int] + mm
         L.or_matmul_fast.argtypes = [_f32p, _sz, _sz, _sz, _u8p, _f32p, _sz, _sz, _f32p, _sz, _sz,
                                      ctypes.c_void_p, _sz, ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        L.or_matmul_fast_q8.argtypes = L.or_matmul_fast.argtypes
         L.or_row_exponent.argtypes = [_f32p, _sz]
         L.or_row_exponent.restype = ctypes.c_int32
         L.or_quantize_rows.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _i8p, _i32p]
@@ -226,6 +227,12 @@ def matmul_fast(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, sc
     """The integer oracle of the fast int8 path, in place on `c`."""
     return lib().or_matmul_fast(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc, _ptr(bias),
                                 0 if bias is None else bias.size, act, scale, int(accumulate))
+
+
+def matmul_fast_q8(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, scale=1.0, accumulate=False):
+    """The integer oracle of the fast Q8_0 path (block sums scaled in block order), in place on `c`."""
+    return lib().or_matmul_fast_q8(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc, _ptr(bias),
+                                   0 if bias is None else bias.size, act, scale, int(accumulate))
 
 
 def row_exponent(row):

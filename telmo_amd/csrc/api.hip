@@ -132,12 +132,13 @@ tg::EpiArgs epi_args(const tg_epilogue *epi, const float *bias_override, bool us
 int run_device(tg_ctx *ctx, const float *a, size_t lda, size_t m, const tg_weights *w, float *c, size_t ldc,
                const tg::EpiArgs &epi) {
     const tg::DeviceWeights &d = w->d;
-    const bool int_path = ctx->mode == TG_MODE_FAST && d.precision == TG_INT8 && d.k <= tg::MAX_K_INT;
+    const bool int_path = ctx->mode == TG_MODE_FAST && (d.precision == TG_INT8 || d.precision == TG_Q8_0) &&
+                          d.k <= tg::MAX_K_INT;
     if (!int_path) {
         TG_HIP(ctx, tg::launch_exact(a, lda, m, d, c, ldc, epi, ctx->stream));
         return TG_OK;
     }
-    if (tg::gemv_fits(m, d.k, a, lda)) {
+    if (tg::gemv_fits(m, d.k, a, lda, d.precision)) {
         TG_HIP(ctx, tg::launch_gemv_i8(a, lda, m, d, c, ldc, epi, ctx->stream));
         return TG_OK;
     }
@@ -381,8 +382,8 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
     if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
     if (m == 0 || w->d.n == 0) return TG_OK;
     const size_t n = w->d.n;
-    if (w->d.precision != TG_INT8 || w->d.k > tg::MAX_K_INT)
-        return fail(ctx, TG_ERR_UNSUPPORTED, "the staged path takes int8 weights with k <= 65536");
+    if ((w->d.precision != TG_INT8 && w->d.precision != TG_Q8_0) || w->d.k > tg::MAX_K_INT)
+        return fail(ctx, TG_ERR_UNSUPPORTED, "the staged path takes int8 or Q8_0 weights with k <= 65536");
     if (!qa || !exps || !c) return fail(ctx, TG_ERR_NULL, "null buffer");
     if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
     if (ldc < n || c_len < (m - 1) * ldc + n) return fail(ctx, TG_ERR_SHAPE, "c is too short");

@@ -182,6 +182,151 @@ hipError_t launch_tile(const uint8_t *qf, const int32_t *exps, size_t m, const D
     return hipGetLastError();
 }
 
+
+// Q8_0 weights: one scale per 32 inputs of each output. Each 32-input half of a k-block runs on
+// v_mfma_i32_16x16x32_i8 from zero, giving the block's exact sums H (hi digits) and L (lo digits);
+// T = 256 H + L (|T| < 2^31) is folded into an f32 accumulator as fmaf(d, (float)T, F), blocks in
+// order. The 8-byte operands come from the same 1 KB k-block layouts as the int8 path: for half h,
+// lane 16 g + x reads bytes 8 (g % 2) .. of layout lane 16 (2 h + g / 2) + x, i.e. inputs
+// 32 h + 8 g .. + 8 of its row (A) or output (B), the same k for both operands.
+template <int RB, int CB, int S, int OCC, int XCD, int G>
+__global__ __launch_bounds__(THREADS, OCC) void gemm_q8_kernel(const uint8_t *__restrict__ qf,
+                                                               const int32_t *__restrict__ exps, int M,
+                                                               const uint8_t *__restrict__ wv,
+                                                               const float *__restrict__ scales, int N, int P, int KB,
+                                                               int NB, float *__restrict__ c, size_t ldc,
+                                                               const float *__restrict__ bias, uint32_t act,
+                                                               float escale, int accumulate, size_t b_panel,
+                                                               size_t b_blk) {
+    constexpr int WM = RB * 16, WN = CB * 16;
+    constexpr int C_STRIDE = WN + 4;
+    __shared__ float staged[4][WM * C_STRIDE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    int bx, by;
+    tile_of<XCD, G>(bx, by);
+    const int m0 = by * 2 * WM + wm * WM, n0 = bx * 2 * WN + wn * WN;
+    const int R0 = m0 / 16, P0 = n0 / 16, RLAST = (M + 15) / 16 - 1;
+    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
+    const int g = lane >> 4;
+
+    int32_t e_row[RB][4];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
+
+    // Byte offsets, within a 1 KB layout block, of this lane's 8 bytes for halves 0 and 1.
+    const int off0 = (16 * (g >> 1) + out_col) * 16 + 8 * (g & 1), off1 = off0 + 32 * 16;
+    const uint8_t *ap[RB];
+    const uint8_t *bp[CB];
+    const float *sp[CB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) ap[r] = qf + (size_t)min(R0 + r, RLAST) * KB * 2048;
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) {
+        const int p = min(P0 + cb, P - 1);
+        bp[cb] = wv + (size_t)p * b_panel;
+        sp[cb] = scales + (size_t)p * NB * PANEL + out_col;
+    }
+
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    v4f acc[RB][CB];
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+        for (int j = 0; j < CB; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    long fa[S][RB][2][2], fb[S][CB][2];
+    float fs[S][CB][2];
+#define TG_LOAD(st, tt)                                                                                 \
+    do {                                                                                                \
+        const size_t t_ = (size_t)(tt);                                                                 \
+        _Pragma("unroll") for (int r = 0; r < RB; r++) _Pragma("unroll") for (int d = 0; d < 2; d++) {  \
+            fa[st][r][d][0] = *reinterpret_cast<const long *>(ap[r] + t_ * 2048 + d * 1024 + off0);     \
+            fa[st][r][d][1] = *reinterpret_cast<const long *>(ap[r] + t_ * 2048 + d * 1024 + off1);     \
+        }                                                                                               \
+        _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                             \
+            fb[st][cb][0] = *reinterpret_cast<const long *>(bp[cb] + t_ * b_blk + off0);                \
+            fb[st][cb][1] = *reinterpret_cast<const long *>(bp[cb] + t_ * b_blk + off1);                \
+            const int b0_ = 2 * (int)t_, b1_ = b0_ + 1;                                                 \
+            fs[st][cb][0] = sp[cb][(size_t)b0_ * PANEL];                                                \
+            fs[st][cb][1] = b1_ < NB ? sp[cb][(size_t)b1_ * PANEL] : 0.0f;                              \
+        }                                                                                               \
+    } while (0)
+#define TG_MMA(st)                                                                                      \
+    do {                                                                                                \
+        _Pragma("unroll") for (int h = 0; h < 2; h++) _Pragma("unroll") for (int r = 0; r < RB; r++)    \
+            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                         \
+            const v4i hh = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[st][r][0][h], fb[st][cb][h],        \
+                                                                 v4i{0, 0, 0, 0}, 0, 0, 0);             \
+            const v4i ll = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[st][r][1][h], fb[st][cb][h],        \
+                                                                 v4i{0, 0, 0, 0}, 0, 0, 0);             \
+            _Pragma("unroll") for (int v = 0; v < 4; v++) acc[r][cb][v] =                               \
+                __builtin_fmaf(fs[st][cb][h], (float)(hh[v] * 256 + ll[v]), acc[r][cb][v]);             \
+        }                                                                                               \
+    } while (0)
+
+    if (KB > 0) {
+#pragma unroll
+        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, KB - 1));
+        int t = 0;
+        for (; t + S <= KB; t += S) {
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                TG_LOAD((s + S - 1) % S, min(t + s + S - 1, KB - 1));
+                TG_MMA(s);
+            }
+        }
+        if (t < KB) TG_MMA(0);
+        if constexpr (S > 2) {
+            if (t + 1 < KB) TG_MMA(1);
+        }
+    }
+#undef TG_LOAD
+#undef TG_MMA
+
+    float *tile = staged[wave];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int32_t e = e_row[r][v];
+                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                    e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(acc[r][cb][v], -e);
+            }
+    __syncthreads();
+    constexpr int TOTAL = WM * WN;
+    for (int i0 = lane; i0 < TOTAL; i0 += 8 * 64) {
+        float old[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
+            old[u] = (accumulate && i < TOTAL && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
+            if (i < TOTAL && row < M && col < N)
+                c[(size_t)row * ldc + col] = epilogue(tile[(i / WN) * C_STRIDE + i % WN], bias, (size_t)col, act,
+                                                      escale, accumulate != 0, &old[u]);
+        }
+    }
+}
+
+template <int RB, int CB, int S, int OCC, int XCD, int G>
+hipError_t launch_q8(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                     const EpiArgs &epi, hipStream_t s) {
+    const size_t bm = 2 * RB * 16, bn = 2 * CB * 16;
+    dim3 grid((unsigned)div_ceil(w.panels * PANEL, bn), (unsigned)div_ceil(m, bm));
+    hipLaunchKernelGGL((gemm_q8_kernel<RB, CB, S, OCC, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
+                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc, epi.bias,
+                       epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 // 128 x 128 workgroup tiles when there are at least 1024 of them (two per CU, twice over), else
@@ -194,6 +339,12 @@ int gemm_tile_choice(size_t m, size_t panels) {
 hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
+    if (w.precision == Q8_0) {
+        // 64 x 64 tiles only: the 8-byte operands, block scales and per-block MFMA results do not
+        // leave room in registers for larger wavefront tiles.
+        if (gemm_tile_choice(m, w.panels) == 0) return launch_q8<2, 2, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_q8<2, 2, 2, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    }
     if (gemm_tile_choice(m, w.panels) == 0) return launch_tile<4, 4, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     return launch_tile<2, 2, 3, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }

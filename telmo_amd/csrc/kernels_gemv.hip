@@ -196,6 +196,42 @@ __device__ __forceinline__ void fetch_panel(v4i (&wr)[KBC], float &sc, float &bv
     }
 }
 
+// Q8_0 weights: for k-blocks c0 .. c0 + KBC - 1 of panel p, the two 8-byte operand halves of this
+// lane (inputs 32 h + 8 g .. + 8 of output j, read from layout lane 16 (2 h + g / 2) + j at byte
+// 8 (g % 2)) and the scales of the two 32-input blocks (zero past the last block).
+template <int KBC>
+__device__ __forceinline__ void load_q8(long (&wq)[KBC][2], float (&sq)[KBC][2], const uint8_t *wp, const float *sp,
+                                        int c0, int KB, int NB, size_t blk_stride, int off0) {
+#pragma unroll
+    for (int t = 0; t < KBC; t++) {
+        const int tt = min(c0 + t, KB - 1), b0 = 2 * tt, b1 = b0 + 1;
+        wq[t][0] = *reinterpret_cast<const long *>(wp + (size_t)tt * blk_stride + off0);
+        wq[t][1] = *reinterpret_cast<const long *>(wp + (size_t)tt * blk_stride + off0 + 512);
+        sq[t][0] = sp[(size_t)b0 * PANEL];
+        const float s1 = sp[(size_t)min(b1, NB - 1) * PANEL];
+        sq[t][1] = b1 < NB ? s1 : 0.0f;
+    }
+}
+
+// What one wavefront needs of Q8_0 panel p: its first KBC k-blocks' operand halves and block
+// scales, and for its lane's column the bias and the old outputs (branch-free, as fetch_panel).
+template <int KBC>
+__device__ __forceinline__ void fetch_panel_q8(long (&wq)[KBC][2], float (&sq)[KBC][2], float &bv, float (&old)[4],
+                                               int p, int lane, const uint8_t *wv, size_t panel_stride,
+                                               size_t blk_stride, int KB, int NB, int off0, const float *scales,
+                                               const float *bias, const float *c, size_t ldc, int N, int m,
+                                               int accumulate) {
+    const int col = p * PANEL + (lane & 15), orow = (lane >> 4) * 4;
+    load_q8<KBC>(wq, sq, wv + (size_t)p * panel_stride, scales + (size_t)p * NB * PANEL + (lane & 15), 0, KB, NB,
+                 blk_stride, off0);
+    bv = *(bias ? bias + min(col, N - 1) : scales);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const bool need = accumulate && orow + v < m && col < N;
+        old[v] = *(need ? c + (size_t)(orow + v) * ldc + col : c);
+    }
+}
+
 // The row exponent from the row's n <= 8 per-wavefront maxima (bits of |x|, all ones for a
 // non-finite input).
 __device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, int n) {
@@ -210,11 +246,11 @@ __device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, in
 // last wavefront idle); wavefront w holds chunk wavefronts w + WAVES j (j < J) in registers. The
 // rows are read once, before the weights, so the weight loads stay in flight while the rows are
 // digitised.
-template <int WAVES, int KBC, int J>
+template <int WAVES, int KBC, int J, int Q8>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__restrict__ a, size_t lda, int m, int k,
                                                                const uint8_t *__restrict__ wv,
                                                                const float *__restrict__ scales, int N, int P, int KB,
-                                                               float *__restrict__ c, size_t ldc,
+                                                               int NB, float *__restrict__ c, size_t ldc,
                                                                const float *__restrict__ bias, uint32_t act,
                                                                float escale, int accumulate, size_t panel_stride,
                                                                size_t blk_stride) {
@@ -242,10 +278,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
     }
     // Panel fetches are unconditional (a wavefront past the last panel re-reads panel P - 1 and
     // never uses it): under a branch the compiler's load counting would wait for them early.
-    v4i wr[KBC];
-    float sc, bv, old[4];
-    fetch_panel<KBC>(wr, sc, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias, c, ldc, N,
-                     m, accumulate);
+    // int8: whole 16-byte operands and one scale per column. Q8_0: 8-byte halves and block scales.
+    const int off0 = (16 * ((lane >> 4) >> 1) + (lane & 15)) * 16 + 8 * ((lane >> 4) & 1);
+    v4i wr[Q8 ? 1 : KBC];
+    long wh[Q8 ? KBC : 1][2];
+    float sq[Q8 ? KBC : 1][2];
+    float sc = 0.0f, bv, old[4];
+    if constexpr (Q8)
+        fetch_panel_q8<KBC>(wh, sq, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, NB, off0, scales,
+                            bias, c, ldc, N, m, accumulate);
+    else
+        fetch_panel<KBC>(wr, sc, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias, c,
+                         ldc, N, m, accumulate);
 
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -290,20 +334,43 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
     const uint8_t *ap = sqa + lane * 16;
     for (; p < P; p += step) {
         v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
-        const uint8_t *wp = wv + (size_t)p * panel_stride + lane * 16;
+        v4f accq = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint8_t *wp = wv + (size_t)p * panel_stride;
         for (int c0 = 0; c0 < KB; c0 += KBC) {
-            if (c0 > 0) {
+            if constexpr (Q8) {
+                if (c0 > 0)
+                    load_q8<KBC>(wh, sq, wp, scales + (size_t)p * NB * PANEL + (lane & 15), c0, KB, NB, blk_stride,
+                                 off0);
 #pragma unroll
-                for (int t = 0; t < KBC; t++)
-                    wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(c0 + t, KB - 1) * blk_stride);
-            }
+                for (int t = 0; t < KBC; t++) {
+                    if (c0 + t < KB) {
 #pragma unroll
-            for (int t = 0; t < KBC; t++) {
-                if (c0 + t < KB) {
-                    const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
-                    const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
-                    acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
-                    acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
+                        for (int h = 0; h < 2; h++) {
+                            const uint8_t *aq = sqa + (c0 + t) * 2048 + off0 + h * 512;
+                            const long ahi = *reinterpret_cast<const long *>(aq);
+                            const long alo = *reinterpret_cast<const long *>(aq + 1024);
+                            const v4i hh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi, wh[t][h], v4i{0, 0, 0, 0}, 0, 0, 0);
+                            const v4i ll = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo, wh[t][h], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                accq[v] = __builtin_fmaf(sq[t][h], (float)(hh[v] * 256 + ll[v]), accq[v]);
+                        }
+                    }
+                }
+            } else {
+                if (c0 > 0) {
+#pragma unroll
+                    for (int t = 0; t < KBC; t++)
+                        wr[t] = *reinterpret_cast<const v4i *>(wp + lane * 16 + (size_t)min(c0 + t, KB - 1) * blk_stride);
+                }
+#pragma unroll
+                for (int t = 0; t < KBC; t++) {
+                    if (c0 + t < KB) {
+                        const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
+                        const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
+                        acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
+                        acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
+                    }
                 }
             }
         }
@@ -311,14 +378,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
         float old0[4];
 #pragma unroll
         for (int v = 0; v < 4; v++) old0[v] = old[v];
-        fetch_panel<KBC>(wr, sc, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias,
-                         c, ldc, N, m, accumulate);
+        if constexpr (Q8)
+            fetch_panel_q8<KBC>(wh, sq, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, NB, off0,
+                                scales, bias, c, ldc, N, m, accumulate);
+        else
+            fetch_panel<KBC>(wr, sc, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, scales,
+                             bias, c, ldc, N, m, accumulate);
         const int col = p * PANEL + ocol;
         if (col < N) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 if (orow + v < m) {
-                    const float s = dequant(acc_hi[v], acc_lo[v], erow[v], sc0);
+                    float s;
+                    if constexpr (Q8)
+                        s = erow[v] == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(accq[v], -erow[v]);
+                    else
+                        s = dequant(acc_hi[v], acc_lo[v], erow[v], sc0);
                     c[(size_t)(orow + v) * ldc + col] =
                         epilogue_vals(s, bias != nullptr, bv0, act, escale, accumulate != 0, old0[v]);
                 }
@@ -342,8 +417,10 @@ bool mfma_fits(size_t m, size_t k, const float *a, size_t lda) {
 template <int WAVES, int KBC, int J>
 void launch_mfma_t(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                    const EpiArgs &epi, size_t blocks, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_mfma_kernel<WAVES, KBC, J>), dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a,
-                       lda, (int)m, (int)w.k, w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc,
+    const bool q8 = w.precision == Q8_0;
+    hipLaunchKernelGGL(q8 ? (gemv_mfma_kernel<WAVES, KBC, J, 1>) : (gemv_mfma_kernel<WAVES, KBC, J, 0>),
+                       dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a, lda, (int)m, (int)w.k, w.values,
+                       w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc,
                        epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
 }
 
@@ -385,16 +462,18 @@ hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights
 
 }  // namespace
 
-bool gemv_fits(size_t m, size_t k, const float *a, size_t lda) {
+bool gemv_fits(size_t m, size_t k, const float *a, size_t lda, uint32_t precision) {
     const size_t kb = div_ceil(k, KBLK);
     if (m == 0 || k == 0) return false;
-    return mfma_fits(m, k, a, lda) || (m <= 8 && m * kb * 128 <= GEMV_LDS_BUDGET);
+    if (mfma_fits(m, k, a, lda)) return true;
+    return precision == INT8 && m <= 8 && m * kb * 128 <= GEMV_LDS_BUDGET;  // the dot4 GEMV is int8 only
 }
 
 hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                           const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
     if (mfma_fits(m, w.k, a, lda)) return launch_mfma(a, lda, m, w, c, ldc, epi, s);
+    if (w.precision != INT8) return hipErrorInvalidValue;  // excluded by gemv_fits
     switch (m) {
     case 1: return launch_rows<1>(a, lda, w, c, ldc, epi, s);
     case 2: return launch_rows<2>(a, lda, w, c, ldc, epi, s);

@@ -176,15 +176,15 @@ hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s);
 
-// The two-digit int8 MFMA GEMM over quantised rows.
+// The two-digit int8 MFMA GEMM over quantised rows (int8 and Q8_0 weights).
 hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s);
 
-// The decode GEMVs (quantise the rows themselves): the MFMA GEMV for m <= 16 rows of k <= 1984
-// inputs (m * ceil(k / 256) <= 64; 16-byte aligned rows, k % 4 == 0), else the dot4 GEMV for
-// m <= 8 rows whose digits fit 64 KB of LDS.
+// The decode GEMVs (quantise the rows themselves; int8 and Q8_0 weights): the MFMA GEMV for
+// m <= 16 rows of k <= 1984 inputs (m * ceil(k / 256) <= 64; 16-byte aligned rows, k % 4 == 0),
+// else, for int8 only, the dot4 GEMV for m <= 8 rows whose digits fit 64 KB of LDS.
 constexpr size_t GEMV_MAX_ROWS = 16;
-bool gemv_fits(size_t m, size_t k, const float *a, size_t lda);
+bool gemv_fits(size_t m, size_t k, const float *a, size_t lda, uint32_t precision);
 hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                           const EpiArgs &epi, hipStream_t s);
 

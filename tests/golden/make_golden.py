@@ -3,8 +3,8 @@
 Inputs come from telmo's test generator (xorshift64, src/kernels/mod.rs:795-805) through the
 oracle: uniform u in [-1, 1), normals by Box-Muller, int8 weights floor(u01 * 255) - 127 and
 scales 0.001 + 0.009 u01. Expected outputs are the oracle's fused sums (the reference's AVX2 /
-AVX-512 / NEON semantics, src/kernels/mod.rs:530-688) and, for int8 weights, the integer oracle
-of the two-digit fast path. Each case is one .npz (no pickled objects) plus an entry in
+AVX-512 / NEON semantics, src/kernels/mod.rs:530-688) and, for int8 and Q8_0 weights, the
+integer oracle of the two-digit fast path. Each case is one .npz (no pickled objects) plus an entry in
 cases.json.
 
     python tests/golden/make_golden.py
@@ -74,6 +74,8 @@ CASES = [
     ("f16_13x64x40", 13, 64, 40, "f16", "relu", 1.0, True, False, 0, 0),
     ("bf16_13x64x40", 13, 64, 40, "bf16", "none", 0.5, False, True, 0, 0),
     ("q8_0_13x64x40", 13, 64, 40, "q8_0", "silu", 1.0, False, True, 0, 0),
+    ("q8_0_4x96x33", 4, 96, 33, "q8_0", "relu", 0.5, True, True, 0, 0),
+    ("q8_0_40x256x70", 40, 256, 70, "q8_0", "none", 1.0, False, True, 2, 3),
 ]
 
 
@@ -93,10 +95,10 @@ def make(case, seed):
                     bias if with_bias else None, ACT[act], scale, acc)
     assert rc == 0, (name, rc)
     out = {"a": a, "values": values, "scales": scales, "bias": bias, "c0": c0, "c_fused": fused}
-    if prec == "int8":
+    if prec in ("int8", "q8_0"):
         fast = c0.copy()
-        orc.matmul_fast(a, lda, m, values, scales, n, k, fast, ldc, bias if with_bias else None, ACT[act], scale,
-                        acc)
+        fn = orc.matmul_fast if prec == "int8" else orc.matmul_fast_q8
+        fn(a, lda, m, values, scales, n, k, fast, ldc, bias if with_bias else None, ACT[act], scale, acc)
         out["c_fast"] = fast
     meta = {"name": name, "m": m, "k": k, "n": n, "lda": lda, "ldc": ldc, "precision": prec, "act": act,
             "scale": scale, "accumulate": acc, "bias": with_bias, "seed": seed}

@@ -31,3 +31,22 @@ def rel_norm_err(got, want):
     want = np.asarray(want, np.float64)
     den = np.maximum(np.abs(want).max(axis=1, keepdims=True), 1e-30)
     return float((np.abs(got - want) / den).max())
+
+
+def q8_0_weights(rng, n, k, full_range=False):
+    """Q8_0 weights: int8 q [n, k] and f16-exact block scales d [n, k / 32] (GGUF's Q8_0)."""
+    lo = -128 if full_range else -127
+    q = rng.integers(lo, 128, size=(n, k)).astype(np.int8)
+    d = (0.001 + 0.009 * rng.random((n, k // 32))).astype(np.float16).astype(np.float32)
+    return q, d
+
+
+def pack_q8_0(q, d):
+    """Panel layout of Q8_0 rows: values as int8, scales [(p * blocks + b) * 16 + j] (src/quant.rs:8-13)."""
+    n, k = q.shape
+    values, _ = pack_int8(q, np.ones(n, np.float32))
+    panels, blocks = -(-n // 16), k // 32
+    scales = np.zeros((panels, blocks, 16), np.float32)
+    for o in range(n):
+        scales[o // 16, :, o % 16] = d[o]
+    return values, scales.reshape(-1)

@@ -20,10 +20,11 @@ def test_the_oracle_reproduces_the_fixture(orc, meta):
     assert orc.matmul(True, g["a"], lda, m, g["values"], g["scales"], PREC[meta["precision"]], n, k, c, ldc, bias,
                       ACT[meta["act"]], meta["scale"], meta["accumulate"]) == 0
     assert np.array_equal(c.view(np.uint32), g["c_fused"].view(np.uint32))
-    if meta["precision"] == "int8":
+    if meta["precision"] in ("int8", "q8_0"):
         c = g["c0"].copy()
-        orc.matmul_fast(g["a"], lda, m, g["values"], g["scales"], n, k, c, ldc, bias, ACT[meta["act"]],
-                        meta["scale"], meta["accumulate"])
+        fast = orc.matmul_fast if meta["precision"] == "int8" else orc.matmul_fast_q8
+        fast(g["a"], lda, m, g["values"], g["scales"], n, k, c, ldc, bias, ACT[meta["act"]],
+             meta["scale"], meta["accumulate"])
         assert np.array_equal(c.view(np.uint32), g["c_fast"].view(np.uint32))
         # the fast path stays within the gate of the fused sums on every fixture
         got, want = g["c_fast"].reshape(m, ldc)[:, :n], g["c_fused"].reshape(m, ldc)[:, :n]

@@ -267,7 +267,7 @@ def test_config_1_at_full_size(tk, orc):
 
 def test_golden_fixtures(tk):
     """The committed fixtures (tests/golden): exact mode gives the fused reference's bits for every
-    precision; fast mode gives the integer oracle's bits for int8."""
+    precision; fast mode gives the integer oracle's bits for int8 and Q8_0."""
     from golden_cases import ACT, PREC, cases, load
 
     for meta in cases():
@@ -283,7 +283,7 @@ def test_golden_fixtures(tk):
         finally:
             tk.set_mode(tk.FAST)
         assert np.array_equal(got.view(np.uint32), g["c_fused"].view(np.uint32)), meta["name"]
-        if meta["precision"] == "int8":
+        if meta["precision"] in ("int8", "q8_0"):
             got = run_gpu(tk, g["a"], lda, m, g["values"], g["scales"], p, n, k, g["c0"], ldc, bias, act,
                           meta["accumulate"], meta["scale"])
             assert np.array_equal(got.view(np.uint32), g["c_fast"].view(np.uint32)), meta["name"]
@@ -311,3 +311,48 @@ def test_layer_norm_matches_the_reference_order(tk, orc):
         assert np.all(got[:, n:] == 9.5)
         got_in_place = xd.cpu().numpy()
         assert np.array_equal(got_in_place[:, :n].view(np.uint32), want.view(np.uint32)), (m, n)
+
+
+Q8_SHAPES = [(1, 32, 3), (1, 640, 200), (4, 96, 33), (8, 1280, 2560), (16, 1920, 100), (5, 2048, 70), (17, 96, 50),
+             (64, 128, 96), (130, 992, 255), (257, 2048, 130), (750, 1024, 512)]
+
+
+@pytest.mark.parametrize("m,k,n", Q8_SHAPES)
+def test_fast_q8_0_is_bit_identical_to_its_integer_oracle(tk, orc, m, k, n):
+    """Q8_0 weights in fast mode: per-block exact sums scaled in block order, on the GEMV (m <= 16)
+    and the GEMM; bit-identical to the oracle, within the gate of the fused reference."""
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    a = normal(rng, m * k)
+    q, d = q8_0_weights(rng, n, k, full_range=True)
+    values, scales = pack_q8_0(q, d)
+    bias, c0 = normal(rng, n), normal(rng, m * n)
+    for act, acc, with_bias in EPIS:
+        b = bias if with_bias else None
+        say("fast-q8", m, k, n, act, acc)
+        want = c0.copy()
+        assert orc.matmul_fast_q8(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc) == 0
+        got = run_gpu(tk, a, k, m, values, scales, Q8_0, n, k, c0, n, b, act, acc)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+    ref = np.zeros(m * n, np.float32)
+    assert orc.matmul(True, a, k, m, values, scales, Q8_0, n, k, ref, n) == 0
+    got = run_gpu(tk, a, k, m, values, scales, Q8_0, n, k, np.zeros(m * n, np.float32), n, None, NONE, False, 1.0)
+    err = rel_norm_err(got.reshape(m, n), ref.reshape(m, n))
+    print(f"[err] q8 m={m} k={k} n={n}: {err:.2e}")
+    assert err <= 1e-3
+
+
+def test_fast_q8_0_unaligned_rows_take_the_gemm(tk, orc):
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(31)
+    m, k, n, lda = 3, 160, 40, 161
+    a = normal(rng, m * lda)
+    q, d = q8_0_weights(rng, n, k)
+    values, scales = pack_q8_0(q, d)
+    say("fast-q8-unaligned")
+    want = np.zeros(m * n, np.float32)
+    assert orc.matmul_fast_q8(a, lda, m, values, scales, n, k, want, n) == 0
+    got = run_gpu(tk, a, lda, m, values, scales, Q8_0, n, k, np.zeros(m * n, np.float32), n, None, NONE, False, 1.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

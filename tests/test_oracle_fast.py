@@ -125,3 +125,76 @@ def test_a_wrong_digit_weight_is_caught(orc):
     ah, al = 1000, 37
     assert orc.dequant(ah, al, 0, 1.0) == np.float32(ah * 256 + al)
     assert orc.dequant(ah, al, 0, 1.0) != np.float32(ah * 128 + al)
+
+
+def q8_fast_by_parts(orc, a, m, k, q, d, n):
+    """The fast Q8_0 sums from independent parts: numpy int64 block products of the oracle's digits,
+    then the f32 fma chain over blocks evaluated in exact rational arithmetic."""
+    from exact import fma32
+
+    hi, lo, ex = orc.quantize_rows(a, k, m, k)
+    out = np.zeros((m, n), np.float32)
+    blocks = k // 32
+    for r in range(m):
+        for o in range(n):
+            f = np.float32(0.0)
+            for b in range(blocks):
+                sl = slice(32 * b, 32 * b + 32)
+                t = int(hi[r, sl].astype(np.int64) @ q[o, sl].astype(np.int64)) * 256 + \
+                    int(lo[r, sl].astype(np.int64) @ q[o, sl].astype(np.int64))
+                f = fma32(d[o, b], np.float32(t), f)
+            out[r, o] = np.float32(math.ldexp(float(f), -int(ex[r])))
+    return out
+
+
+def test_q8_0_fast_path_is_its_block_sums(orc):
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(21)
+    for m, k, n in ((1, 32, 3), (3, 96, 17), (4, 160, 9)):
+        a = normal(rng, m * k)
+        q, d = q8_0_weights(rng, n, k, full_range=True)
+        values, scales = pack_q8_0(q, d)
+        got = np.zeros(m * n, np.float32)
+        assert orc.matmul_fast_q8(a, k, m, values, scales, n, k, got, n) == 0
+        want = q8_fast_by_parts(orc, a.reshape(m, k), m, k, q, d, n)
+        assert np.array_equal(got.reshape(m, n).view(np.uint32), want.view(np.uint32)), (m, k, n)
+
+
+def test_q8_0_fast_path_is_within_1e_4_of_the_reference(orc):
+    from helpers import pack_q8_0, q8_0_weights
+
+    Q8_0 = 4
+    rng = np.random.default_rng(22)
+    for m, k, n in ((7, 1024, 64), (2, 2048, 33), (16, 96, 40)):
+        a = normal(rng, m * k)
+        q, d = q8_0_weights(rng, n, k)
+        values, scales = pack_q8_0(q, d)
+        fast = np.zeros(m * n, np.float32)
+        ref = np.zeros(m * n, np.float32)
+        assert orc.matmul_fast_q8(a, k, m, values, scales, n, k, fast, n) == 0
+        assert orc.matmul(True, a, k, m, values, scales, Q8_0, n, k, ref, n) == 0
+        assert rel_norm_err(fast.reshape(m, n), ref.reshape(m, n)) <= 1e-4
+
+
+def test_a_misplaced_block_scale_is_caught(orc):
+    """Planted in the check, not the product: swapping two blocks' scales of one output changes
+    the result, so the block-scale indexing is exercised."""
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(23)
+    m, k, n = 2, 128, 5
+    a = normal(rng, m * k)
+    q, d = q8_0_weights(rng, n, k)
+    d[:, 1] = d[:, 0] * np.float32(4.0)
+    values, scales = pack_q8_0(q, d)
+    good = np.zeros(m * n, np.float32)
+    orc.matmul_fast_q8(a, k, m, values, scales, n, k, good, n)
+    d2 = d.copy()
+    d2[:, [0, 1]] = d2[:, [1, 0]]
+    values2, scales2 = pack_q8_0(q, d2)
+    bad = np.zeros(m * n, np.float32)
+    orc.matmul_fast_q8(a, k, m, values2, scales2, n, k, bad, n)
+    assert not np.array_equal(good, bad)
+    assert np.array_equal(good.reshape(m, n).view(np.uint32),
+                          q8_fast_by_parts(orc, a.reshape(m, k), m, k, q, d, n).view(np.uint32))
