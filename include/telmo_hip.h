@@ -14,6 +14,10 @@
  *   Kernels::linear              src/kernels/mod.rs:691-701   -> tg_linear, tg_linear_device
  *   Kernels::glu (row kernel)    src/kernels/mod.rs:463-464   -> tg_glu_device
  *   Kernels::layer_norm          src/kernels/mod.rs:458       -> tg_layer_norm_device
+ *   Pack::open / from_bytes      src/pack.rs:79-96            -> tg_pack_open, tg_pack_from_bytes
+ *   Pack::parse (the checks)     src/pack.rs:98-259           -> tg_pack_open, tg_pack_last_error
+ *   Pack::model / meta / entries src/pack.rs:248-265          -> tg_pack_model, tg_pack_meta, tg_pack_entry_at
+ *   Pack::matrix                 src/pack.rs:279-305          -> tg_pack_find + tg_pack_upload_matrix
  *
  * Error behaviour follows the reference's asserts (src/kernels/mod.rs:669-677): m == 0 or n == 0
  * is a no-op that succeeds before any other check; then lda >= k, ldc >= n, the lengths of a and
@@ -147,6 +151,51 @@ int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half
  * floats; out may equal x. Device pointers, queued on the stream. */
 int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                          const float *beta, float eps, float *out, size_t ldo);
+
+/* ---- packs: the reference's weight files (src/pack.rs) -------------------------------------
+ * A pack is "TELMOPAK", a u32 version (1) and 4 zero bytes; entries' data at multiples of 64
+ * bytes; a JSON index; the index's offset and length (u64) and "TELMOIDX". Opening maps the file
+ * read-only and checks the index as Pack::parse does, with its messages; entries are views into
+ * the mapping until tg_pack_close. No device is needed except for tg_pack_upload_matrix. */
+typedef struct tg_pack tg_pack;
+
+enum { TG_ENTRY_MATRIX = 0, TG_ENTRY_F32 = 1, TG_ENTRY_BYTES = 2 };
+
+typedef struct tg_pack_entry {
+    const char *name;
+    uint32_t type;        /* TG_ENTRY_* */
+    uint32_t precision;   /* matrices: TG_F32 .. TG_Q8_0 */
+    size_t n, k;          /* matrices: outputs, inputs */
+    size_t rank;          /* f32 tensors: dimensions (at most 8) */
+    size_t shape[8];
+    const void *data;     /* panel values, tensor data or bytes */
+    size_t bytes;
+    const float *scales;  /* matrices with scales (int8, Q8_0), else null */
+    size_t n_scales;
+} tg_pack_entry;
+
+/* TG_ERR_ARG for a file that is not a usable pack (message from tg_pack_last_error). */
+int tg_pack_open(const char *path, tg_pack **out);
+/* A pack held in memory (copied). */
+int tg_pack_from_bytes(const void *data, size_t len, tg_pack **out);
+void tg_pack_close(tg_pack *pack);
+/* The message of this thread's last failed tg_pack_* call ("" if none). */
+const char *tg_pack_last_error(void);
+/* Whether the entries are a mapping of the file (else a copy in memory). */
+int tg_pack_is_mapped(const tg_pack *pack);
+const char *tg_pack_model(const tg_pack *pack);
+/* A metadata value, or null if the key is absent. */
+const char *tg_pack_meta(const tg_pack *pack, const char *key);
+size_t tg_pack_meta_count(const tg_pack *pack);
+int tg_pack_meta_at(const tg_pack *pack, size_t i, const char **key, const char **value);
+size_t tg_pack_entry_count(const tg_pack *pack);
+int tg_pack_entry_at(const tg_pack *pack, size_t i, tg_pack_entry *out);
+/* The named entry; TG_ERR_ARG "Entry <name> is missing." when there is none. */
+int tg_pack_find(const tg_pack *pack, const char *name, tg_pack_entry *out);
+/* Pack::matrix then tg_weights_upload: the named matrix, which must be n x k, uploaded once
+ * (TG_ERR_ARG if it is missing or not a matrix, TG_ERR_SHAPE if its shape differs). */
+int tg_pack_upload_matrix(tg_ctx *ctx, const tg_pack *pack, const char *name, size_t n, size_t k,
+                          tg_weights **out);
 
 /* ---- the panel layout (host utilities, no device needed) ---------------------------------- */
 

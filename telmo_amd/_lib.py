@@ -33,6 +33,19 @@ SIGNATURES = {
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
     "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, ctypes.c_float, _p, _sz]),
+    "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
+    "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),
+    "tg_pack_close": (None, [_p]),
+    "tg_pack_last_error": (ctypes.c_char_p, []),
+    "tg_pack_is_mapped": (ctypes.c_int, [_p]),
+    "tg_pack_model": (ctypes.c_char_p, [_p]),
+    "tg_pack_meta": (ctypes.c_char_p, [_p, ctypes.c_char_p]),
+    "tg_pack_meta_count": (_sz, [_p]),
+    "tg_pack_meta_at": (ctypes.c_int, [_p, _sz, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p)]),
+    "tg_pack_entry_count": (_sz, [_p]),
+    "tg_pack_entry_at": (ctypes.c_int, [_p, _sz, _p]),
+    "tg_pack_find": (ctypes.c_int, [_p, ctypes.c_char_p, _p]),
+    "tg_pack_upload_matrix": (ctypes.c_int, [_p, _p, ctypes.c_char_p, _sz, _sz, ctypes.POINTER(_p)]),
     "tg_panel_bytes": (_sz, [_u32, _sz, _sz]),
     "tg_scale_count": (_sz, [_u32, _sz, _sz]),
     "tg_fits": (ctypes.c_int, [_u32, _sz]),

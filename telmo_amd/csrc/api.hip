@@ -397,6 +397,24 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
     return TG_OK;
 }
 
+int tg_pack_upload_matrix(tg_ctx *ctx, const tg_pack *pack, const char *name, size_t n, size_t k,
+                          tg_weights **out) {
+    if (!ctx || !pack || !name || !out) return fail(ctx, TG_ERR_NULL, "null argument");
+    *out = nullptr;
+    tg_pack_entry e;
+    if (tg_pack_find(pack, name, &e) != TG_OK) return fail(ctx, TG_ERR_ARG, tg_pack_last_error());
+    const std::string head = std::string("The pack file isn't usable. Entry ") + name;
+    if (e.type != TG_ENTRY_MATRIX) return fail(ctx, TG_ERR_ARG, head + " isn't a matrix.");
+    if (e.n != n || e.k != k)
+        return fail(ctx, TG_ERR_SHAPE, head + " is " + std::to_string(e.n) + " x " + std::to_string(e.k) +
+                                           ", and the model needs " + std::to_string(n) + " x " + std::to_string(k) +
+                                           ".");
+    const int rc = tg_weights_upload(ctx, static_cast<const uint8_t *>(e.data), e.bytes, e.scales, e.n_scales,
+                                     e.precision, n, k, out);
+    if (rc == TG_ERR_ARG || rc == TG_ERR_ALIGN) return fail(ctx, rc, head + " doesn't fit its shape.");
+    return rc;
+}
+
 int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                          const float *beta, float eps, float *out, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;

@@ -356,3 +356,39 @@ def test_fast_q8_0_unaligned_rows_take_the_gemm(tk, orc):
     assert orc.matmul_fast_q8(a, lda, m, values, scales, n, k, want, n) == 0
     got = run_gpu(tk, a, lda, m, values, scales, Q8_0, n, k, np.zeros(m * n, np.float32), n, None, NONE, False, 1.0)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_pack_matrices_upload_like_their_parts(tk, tmp_path):
+    """Pack::matrix then upload (tg_pack_upload_matrix) gives the same products, bit for bit, as the
+    same panel bytes handed to tg_weights_upload; shape mismatches are refused as the reference does."""
+    import telmo_amd
+    from packs import sample_pack
+
+    data = sample_pack(lambda w, n, k, p: telmo_amd.encode(w, n, k, telmo_amd.Precision(p)))
+    path = tmp_path / "sample.pack"
+    path.write_bytes(data)
+    pack = telmo_amd.Pack.open(str(path))
+    rng = np.random.default_rng(41)
+    a = normal(rng, 9 * 64)
+    for name in ("w8", "wq", "wh"):
+        say("pack", name)
+        values, scales = pack.matrix_parts(name)
+        prec = [e for e in pack.entries() if e.name == name][0].precision
+        w_pack = pack.matrix(tk, name, 40, 64)
+        w_parts = telmo_amd.PackedWeights.from_parts(tk, 40, 64, prec, values, scales)
+        for mode in (tk.FAST, tk.EXACT):
+            tk.set_mode(mode)
+            c1 = np.zeros(9 * 40, np.float32)
+            c2 = np.zeros(9 * 40, np.float32)
+            tk.linear(a, 9, w_pack, c1)
+            tk.linear(a, 9, w_parts, c2)
+            assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32)), (name, mode)
+        tk.set_mode(tk.FAST)
+        w_pack.close()
+        w_parts.close()
+    with pytest.raises(telmo_amd.TelmoError, match="Entry w8 is 40 x 64, and the model needs 64 x 40."):
+        pack.matrix(tk, "w8", 64, 40)
+    with pytest.raises(telmo_amd.TelmoError, match="Entry bias isn't a matrix."):
+        pack.matrix(tk, "bias", 2, 3)
+    with pytest.raises(telmo_amd.TelmoError, match="Entry nope is missing."):
+        pack.matrix(tk, "nope", 2, 3)
