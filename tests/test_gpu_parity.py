@@ -392,3 +392,21 @@ def test_pack_matrices_upload_like_their_parts(tk, tmp_path):
         pack.matrix(tk, "bias", 2, 3)
     with pytest.raises(telmo_amd.TelmoError, match="Entry nope is missing."):
         pack.matrix(tk, "nope", 2, 3)
+
+
+@pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384)])
+def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
+    """Products that fill the chip with 128 x 128 tiles (>= 1024 of them) run the LDS-staged GEMM;
+    partial edge tiles in both directions, every epilogue, bit-identical to the integer oracle."""
+    rng = np.random.default_rng(m + k + n)
+    a = normal(rng, m * k)
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    bias, c0 = normal(rng, n), normal(rng, m * n)
+    for act, acc, with_bias in EPIS[:3]:
+        b = bias if with_bias else None
+        say("large", m, k, n, act, acc)
+        want = c0.copy()
+        orc.matmul_fast(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc)
+        got = run_gpu(tk, a, k, m, values, scales, INT8, n, k, c0, n, b, act, acc)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
