@@ -36,6 +36,7 @@ sys.path.insert(0, ROOT)
 
 T_FRAMES = 750
 D, FF, CONV = 1024, 4096, 2048
+DW_KERNEL = 9  # the conv module's depthwise kernel (parakeet's conv_kernel_size)
 PEAK_INT8 = 5.0e15  # dense int8 MFMA ops/s (MI355X)
 PEAK_HBM = 8.0e12   # bytes/s
 METRIC = "int8 GEMM TOPS & %MFMA peak; decode GEMV GB/s & %HBM; encoder audio-s/s"
@@ -67,10 +68,12 @@ def bytes_of(m):
     return total
 
 
-def run_layer(kern, W, bufs, T):
+def run_layer(kern, W, bufs, T, dw=None):
     """The layer's products in order: FFN (SiLU, half-step residual), QKV, attention output (the V
-    third of QKV standing in for attention), the conv module's pointwise pair around the GLU, and
-    the second FFN. bufs holds x [T, D], h [T, FF], qkv [T, 3D], g [T, CONV], u [T, D]."""
+    third of QKV standing in for attention), the conv module's pointwise pair around the GLU (and,
+    given dw = (weights [DW_KERNEL, D], bias [D]), the depthwise convolution + SiLU between GLU and
+    pw2; dw[2] utterances of T / dw[2] frames each), and the second FFN. bufs holds x [T, D], h [T, FF], qkv [T, 3D], g [T, CONV], u and d
+    [T, D]."""
     from telmo_amd import Act, Epilogue
 
     x, h, qkv, g, u = (bufs[key] for key in ("x", "h", "qkv", "g", "u"))
@@ -83,6 +86,10 @@ def run_layer(kern, W, bufs, T):
     kern.matmul_device(qkv[:, 2 * D:], 3 * D, T, W["att_out"], x, D, acc, a_len=qkv.numel() - 2 * D)
     kern.linear_device(x, T, W["pw1"], g)
     kern.glu_device(g, CONV, T, D, u, D)
+    if dw is not None:
+        seqs = dw[2]  # equal-length utterances stacked along the rows, each convolved on its own
+        kern.dwconv1d_device(u, D, T // seqs, D, dw[0], DW_KERNEL, dw[1], bufs["d"], D, act=Act.SILU, batch=seqs)
+        u = bufs["d"]
     kern.linear_device(u, T, W["pw2"], x, acc)
     kern.linear_device(x, T, W["ff2_up"], h, silu)
     kern.linear_device(h, T, W["ff2_down"], x, half_acc)
@@ -95,7 +102,8 @@ def layer_buffers(T, dev="cuda"):
             "h": torch.empty((T, FF), dtype=torch.float32, device=dev),
             "qkv": torch.empty((T, 3 * D), dtype=torch.float32, device=dev),
             "g": torch.empty((T, CONV), dtype=torch.float32, device=dev),
-            "u": torch.empty((T, D), dtype=torch.float32, device=dev)}
+            "u": torch.empty((T, D), dtype=torch.float32, device=dev),
+            "d": torch.empty((T, D), dtype=torch.float32, device=dev)}
 
 
 def make_weights(rng):
@@ -191,15 +199,19 @@ def gpu_leg(args, weights, x0_host):
 
 
 ENC_LAYERS = 24
-# (workload, rows, audio seconds): 32 utterances of 30 s at 80 ms per frame; one 600 s utterance.
-ENC_CASES = [("batch of 32 x 30 s utterances", 32 * 375, 960.0), ("one 600 s utterance", 7500, 600.0)]
+# (workload, rows, audio seconds, utterances): 32 utterances of 30 s at 80 ms per frame; one 600 s
+# utterance.
+ENC_CASES = [("batch of 32 x 30 s utterances", 32 * 375, 960.0, 32), ("one 600 s utterance", 7500, 600.0, 1)]
 
 
 def encoder_leg(args):
     """The encoder stack: 24 Conformer layers of the layer step's shapes, each with its own random
-    int8 weights and scales (580 MB in all, generated on the GPU), LayerNorm (gamma 1, beta 0)
-    after every layer to keep the activations N(0, 1). Audio-seconds per second = the audio the
-    rows stand for / the time of one pass over all 24 layers."""
+    int8 weights and scales (580 MB in all, generated on the GPU), the conv module's depthwise
+    convolution (kernel 9, per utterance) + SiLU between GLU and pw2, and LayerNorm (gamma 1,
+    beta 0) after every layer to keep the activations N(0, 1). Audio-seconds per second = the audio
+    the rows stand for / the time of one pass over all 24 layers. The depthwise convolution is
+    also timed alone (HIP events, 20 launches) against HBM: its algorithmic bytes are the input and
+    output rows plus its weights."""
     import torch
 
     import telmo_amd
@@ -219,19 +231,21 @@ def encoder_leg(args):
             W[name] = telmo_amd.PackedWeights.from_device(kern, n, k, telmo_amd.Precision.INT8, q, sc)
             wbytes += W[name].bytes()
             del q, sc
-        layers.append(W)
+        dw = (0.3 * torch.randn((DW_KERNEL, D), generator=gen, device="cuda"),
+              0.1 * torch.randn(D, generator=gen, device="cuda"))
+        layers.append((W, dw))
     gamma = torch.ones(D, device="cuda")
     beta = torch.zeros(D, device="cuda")
     out = []
-    for label, M, audio_s in ENC_CASES:
+    for label, M, audio_s, seqs in ENC_CASES:
         x0 = torch.randn((M, D), generator=gen, device="cuda")
         bufs = layer_buffers(M)
         x = bufs["x"]
 
         def run():
             x.copy_(x0)
-            for W in layers:
-                run_layer(kern, W, bufs, M)
+            for W, dw in layers:
+                run_layer(kern, W, bufs, M, dw + (seqs,))
                 kern.layer_norm_device(x, D, M, D, gamma, beta, 1e-5, x, D)
 
         run()
@@ -246,12 +260,23 @@ def encoder_leg(args):
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / reps
+        dw_w, dw_b = layers[0][1]
+        e0.record(stream)
+        for _ in range(20):
+            kern.dwconv1d_device(bufs["u"], D, M // seqs, D, dw_w, DW_KERNEL, dw_b, bufs["d"], D,
+                                 act=telmo_amd.Act.SILU, batch=seqs)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        dw_s = e0.elapsed_time(e1) / 20 * 1e-3
+        dw_bytes = 4 * (2 * M * D + DW_KERNEL * D + D)
         ops = ENC_LAYERS * ops_of(M)
         out.append({"workload": f"{ENC_LAYERS}-layer encoder, {label}", "m": M, "audio_s": audio_s,
                     "ms_per_pass": round(ms, 3), "audio_s_per_s": round(audio_s / (ms * 1e-3), 1),
-                    "tops": round(ops / (ms * 1e-3) / 1e12, 1), "weights_mb": round(wbytes / 1e6, 1)})
+                    "tops": round(ops / (ms * 1e-3) / 1e12, 1), "weights_mb": round(wbytes / 1e6, 1),
+                    "dwconv_us": round(dw_s * 1e6, 2),
+                    "dwconv_hbm_frac": round(dw_bytes / dw_s / PEAK_HBM, 3)})
         del bufs, x0
-    for W in layers:
+    for W, _ in layers:
         for w in W.values():
             w.close()
     kern.close()

@@ -14,6 +14,7 @@
  *   Kernels::linear              src/kernels/mod.rs:691-701   -> tg_linear, tg_linear_device
  *   Kernels::glu (row kernel)    src/kernels/mod.rs:463-464   -> tg_glu_device
  *   Kernels::layer_norm          src/kernels/mod.rs:458       -> tg_layer_norm_device
+ *   Kernels::dwconv1d_frame + silu  src/kernels/mod.rs:464-475  -> tg_dwconv1d_device
  *   Pack::open / from_bytes      src/pack.rs:79-96            -> tg_pack_open, tg_pack_from_bytes
  *   Pack::parse (the checks)     src/pack.rs:98-259           -> tg_pack_open, tg_pack_last_error
  *   Pack::model / meta / entries src/pack.rs:248-265          -> tg_pack_model, tg_pack_meta, tg_pack_entry_at
@@ -151,6 +152,21 @@ int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half
  * floats; out may equal x. Device pointers, queued on the stream. */
 int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                          const float *beta, float eps, float *out, size_t ldo);
+
+/* Depthwise 1-D convolution of frames x channels rows, "same" zero padding: output row r is frame
+ * t = t0 + r * stride, out[r, c] = bias[c] + sum over taps j in order of w[j * channels + c] *
+ * x[t + j - kernel/2, c], each term a rounded product and a rounded sum, taps outside [0, frames)
+ * skipped: the reference's dwconv1d_frame (src/kernels/scalar.rs:164-187) called once per output
+ * frame, as the conv modules do (src/parakeet.rs:1107-1122 with t = r; src/granite.rs:900-915
+ * with t = stride * (out_start + r) - lo). act TG_ACT_SILU then applies the caller's
+ * (k.silu)(row) (v / (1 + exp(0 - v)), src/kernels/avx512.rs:308-311, 432-443); TG_ACT_NONE leaves
+ * the sums. w holds kernel x channels floats, bias channels floats. batch equal-length sequences
+ * may be laid one after another (sequence b: input rows b * frames .., output rows b * rows ..),
+ * each convolved on its own; batch = 1 is the reference's call. out must not overlap x. Device
+ * pointers, queued on the stream. */
+int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
+                       const float *w, size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows,
+                       uint32_t act, float *out, size_t ldo);
 
 /* ---- packs: the reference's weight files (src/pack.rs) -------------------------------------
  * A pack is "TELMOPAK", a u32 version (1) and 4 zero bytes; entries' data at multiples of 64

@@ -20,6 +20,9 @@
  *   or_exp_simd           src/kernels/avx512.rs:279-304 == avx2.rs:305-331 (same steps)
  *   or_glu                src/kernels/avx512.rs:410-430
  *   or_layer_norm         src/kernels/avx512.rs:346-380 (AVX-512 summation order)
+ *   or_dwconv1d_frame     src/kernels/scalar.rs:164-187 (== avx512.rs:445-459, the same loop)
+ *   or_dwconv1d           src/parakeet.rs:1107-1122, src/granite.rs:900-915 (one frame per
+ *                         output row, then silu, avx512.rs:308-311 and 432-443)
  *   or_store              src/kernels/scalar.rs:110-124 (unfused, libm exp) and
  *                         avx512.rs:313-343 (fused ISAs)
  *   or_matmul             src/kernels/mod.rs:530-688   (gemm_panels with KC = 256, the
@@ -29,7 +32,9 @@
  * half bit pattern, numpy's float16 conversion on random values, exact-rational FMA sums for
  * the fused tile, an f64 triple loop within 1e-5*sqrt(k)*(1+|w|) (src/kernels/mod.rs:962-1005),
  * widen == decode for every int8 value and every scale exponent (mod.rs:1130-1183), and
- * exp/sigmoid accuracy against math.exp (mod.rs:1261-1277).
+ * exp/sigmoid accuracy against math.exp (mod.rs:1261-1277), the depthwise convolution against
+ * an f64 direct sum (mod.rs:1279-1300), exact integer correlations (numpy) and numpy's per-op
+ * float32 rounding.
  *
  * The second half of the file is the integer oracle of telmo_amd's fast path (two int8
  * digits per activation, exact i32 sums, one shared dequantisation). It has no counterpart
@@ -335,6 +340,37 @@ void or_layer_norm(const float *x, size_t n, float *out, const float *gamma, con
         const float d = (x[i] - mean) * rstd;
         out[i] = fmaf(d, gamma[i], beta[i]);
     }
+}
+
+/* One output frame of the depthwise convolution (src/kernels/scalar.rs:164-187): out = bias, then
+ * for each tap j in order whose source frame t + j - kernel/2 lies in [0, frames), out[c] =
+ * out[c] + w[j * channels + c] * input[src * channels + c], a rounded product then a rounded sum. */
+void or_dwconv1d_frame(const float *input, size_t channels, size_t frames, size_t t, const float *w, size_t kernel,
+                       const float *bias, float *out) {
+    memcpy(out, bias, channels * sizeof(float));
+    const size_t half = kernel / 2;
+    for (size_t j = 0; j < kernel; j++) {
+        if (t + j < half || t + j - half >= frames) continue;
+        const float *row = input + (t + j - half) * channels;
+        const float *wj = w + j * channels;
+        for (size_t c = 0; c < channels; c++) out[c] = out[c] + wj[c] * row[c];
+    }
+}
+
+/* The conv modules' loop: output row r (stride ldo) is or_dwconv1d_frame at t = t0 + r * stride
+ * over the frames of input (stride ldx), then, when silu is set, v / (1 + exp(0 - v)) with the
+ * SIMD exp (src/kernels/avx512.rs:308-311). */
+void or_dwconv1d(const float *input, size_t ldx, size_t frames, size_t channels, const float *w, size_t kernel,
+                 const float *bias, size_t t0, size_t stride, size_t rows, int silu, float *out, size_t ldo) {
+    float *dense = malloc((frames ? frames : 1) * channels * sizeof(float));
+    for (size_t f = 0; f < frames; f++) memcpy(dense + f * channels, input + f * ldx, channels * sizeof(float));
+    for (size_t r = 0; r < rows; r++) {
+        float *o = out + r * ldo;
+        or_dwconv1d_frame(dense, channels, frames, t0 + r * stride, w, kernel, bias, o);
+        if (silu)
+            for (size_t c = 0; c < channels; c++) o[c] = or_silu_simd(o[c]);
+    }
+    free(dense);
 }
 
 float or_activate_scalar(float v, int act) {

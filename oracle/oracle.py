@@ -69,6 +69,9 @@ def lib():
         L.or_silu_simd.restype = ctypes.c_float
         L.or_glu.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.or_layer_norm.argtypes = [_f32p, _sz, _f32p, _f32p, _f32p, ctypes.c_float]
+        L.or_dwconv1d_frame.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _sz, _f32p, _f32p]
+        L.or_dwconv1d.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _sz, _f32p, _sz, _sz, _sz, ctypes.c_int,
+                                  _f32p, _sz]
         L.or_store.argtypes = [ctypes.c_int, _f32p, _f32p, _sz, ctypes.c_void_p, ctypes.c_int, ctypes.c_float,
                                ctypes.c_int]
         mm = [_f32p, _sz, _sz, _sz, _u8p, ctypes.c_void_p, ctypes.c_int, _sz, _sz, _f32p, _sz, _sz,
@@ -208,6 +211,33 @@ def layer_norm(x, gamma, beta, eps):
     out = np.zeros_like(x)
     lib().or_layer_norm(x, x.size, out, np.ascontiguousarray(gamma, np.float32),
                         np.ascontiguousarray(beta, np.float32), float(eps))
+    return out
+
+
+def dwconv1d_frame(x, t, w, bias):
+    """One output frame of the depthwise convolution over x [frames, channels], w [kernel, channels]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    frames, channels = x.shape
+    out = np.empty(channels, np.float32)
+    lib().or_dwconv1d_frame(x.reshape(-1) if x.size else np.zeros(1, np.float32), channels, frames, t,
+                            w.reshape(-1) if w.size else np.zeros(1, np.float32), w.shape[0],
+                            np.ascontiguousarray(bias, np.float32), out)
+    return out
+
+
+def dwconv1d(x, w, bias, rows=None, t0=0, stride=1, silu=False):
+    """Output rows r = 0 .. rows - 1 of dwconv1d_frame at t0 + r * stride, then SiLU when silu."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    frames, channels = x.shape
+    rows = frames if rows is None else rows
+    out = np.empty((rows, channels), np.float32)
+    if rows:
+        lib().or_dwconv1d(x.reshape(-1) if x.size else np.zeros(1, np.float32), channels, frames, channels,
+                          w.reshape(-1) if w.size else np.zeros(1, np.float32), w.shape[0],
+                          np.ascontiguousarray(bias, np.float32), t0, stride, rows, int(silu), out.reshape(-1),
+                          channels)
     return out
 
 

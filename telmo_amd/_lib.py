@@ -33,6 +33,7 @@ SIGNATURES = {
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
     "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, ctypes.c_float, _p, _sz]),
+    "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, _sz, _sz, _u32, _p, _sz]),
     "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),
     "tg_pack_close": (None, [_p]),

@@ -439,4 +439,33 @@ int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half
     return TG_OK;
 }
 
+int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
+                       const float *w, size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows,
+                       uint32_t act, float *out, size_t ldo) {
+    if (!ctx) return TG_ERR_NULL;
+    if (act != TG_ACT_NONE && act != TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "act must be TG_ACT_NONE or TG_ACT_SILU");
+    if (rows == 0 || channels == 0 || batch == 0) return TG_OK;
+    if (!bias || !out || (frames > 0 && !x) || (kernel > 0 && !w)) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (ldo < channels || (frames > 0 && ldx < channels)) return fail(ctx, TG_ERR_SHAPE, "ldx and ldo must be >= channels");
+    const size_t lim = (size_t)1 << 40;  // frame indices and sizes stay far inside int64
+    // the dispatch's x extent (rows / 8 blocks of 256 work-items) must stay below 2^32 work-items
+    if (frames >= lim || kernel >= ((size_t)1 << 30) || t0 >= lim || stride >= lim || rows >= ((size_t)1 << 26))
+        return fail(ctx, TG_ERR_UNSUPPORTED, "frames, t0 and stride must be < 2^40, rows < 2^26, kernel < 2^30");
+    if (stride > 0 && rows - 1 > (lim - t0) / stride)
+        return fail(ctx, TG_ERR_UNSUPPORTED, "the last row's frame t0 + (rows - 1) stride must be < 2^40");
+    if (tg::div_ceil(channels, (size_t)256) >= 65536 || batch >= 65536 ||
+        tg::div_ceil(rows, (size_t)8) * tg::div_ceil(channels, (size_t)256) * batch >= ((size_t)1 << 24))
+        return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^24 channels, 65535 sequences or 2^35 outputs per call");
+    if (frames > 0) {
+        const size_t xn = ((batch * frames - 1) * ldx + channels) * 4, on = ((batch * rows - 1) * ldo + channels) * 4;
+        const uintptr_t xb = reinterpret_cast<uintptr_t>(x), ob = reinterpret_cast<uintptr_t>(out);
+        if (ob < xb + xn && xb < ob + on) return fail(ctx, TG_ERR_ARG, "out must not overlap x");
+    }
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_dwconv1d(x, ldx, frames, batch, channels, w, kernel, bias, t0, stride, rows,
+                                    act == TG_ACT_SILU, out, ldo, ctx->stream));
+    return TG_OK;
+}
+
 }  // extern "C"

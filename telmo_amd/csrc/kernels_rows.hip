@@ -177,7 +177,7 @@ hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, 
 }
 
 // out = a * sigmoid(b) as the reference's SIMD glu computes it: a / (1 + exp(0 - b))
-// (src/kernels/avx512.rs:370-385).
+// (src/kernels/avx512.rs:410-430).
 __global__ __launch_bounds__(256) void glu_kernel(const float *__restrict__ x, size_t ldx, size_t m, size_t half,
                                                   float *__restrict__ out, size_t ldo) {
     const size_t total = m * half;
@@ -244,6 +244,164 @@ hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, con
     if (m == 0 || n == 0) return hipSuccess;
     hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)div_ceil(m, (size_t)16)), dim3(256), 0, s, x, ldx, m, (int)n,
                        gamma, beta, eps, out, ldo);
+    return hipGetLastError();
+}
+
+// Depthwise 1-D convolution with "same" zero padding, one output row per frame
+// t = t0 + r * stride, as the reference's dwconv1d_frame computes it (src/kernels/scalar.rs:164-187):
+// out[c] = bias[c], then for each tap j in order, out[c] = out[c] + w[j][c] * x[t + j - kernel/2][c]
+// (a rounded product, then a rounded sum), taps outside [0, frames) skipped. With silu the row then
+// goes through v / (1 + exp(0 - v)) as the caller's (k.silu)(row) does. Grid z walks a batch of
+// equal-length sequences laid one after another (frames input rows, rows output rows each).
+//
+// Main kernel: a block owns 256 channels (one per lane) and R = 16 (8 for 32 taps at stride 2)
+// consecutive output rows; kernel <= KMAX
+// and the stride is STRIDE. Each lane loads the SPAN = (R - 1) * STRIDE + KMAX frames its rows reach
+// and the KMAX tap weights into registers in one batch of independent loads (frames outside the
+// input are clamped to an edge row, their taps skipped below; taps past kernel are never summed),
+// then sums its R rows, taps in order, without touching memory. Blocks wholly inside the input
+// (all but the first and last of a sequence) skip the edge tests. HBM reads each input row about
+// SPAN / (R * STRIDE) times per 256-channel slice and writes each output once.
+template <int R, int STRIDE, int KMAX>
+__global__ __launch_bounds__(256) void dwconv1d_reg_kernel(const float *__restrict__ x, size_t ldx, int64_t frames,
+                                                           size_t channels, const float *__restrict__ w, int kernel,
+                                                           const float *__restrict__ bias, int64_t t0, size_t rows,
+                                                           int silu, float *__restrict__ out, size_t ldo,
+                                                           unsigned tiles, unsigned slices, unsigned total) {
+    constexpr int SPAN = (R - 1) * STRIDE + KMAX;
+    // Workgroup L runs on XCD L % 8. Each XCD takes a contiguous run of (sequence, row tile, channel
+    // slice) work items, slices fastest, so the frames a tile shares with its neighbours are read
+    // into one L2 at about the same time.
+    const unsigned per = (total + 7) / 8, idx = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (idx >= total) return;
+    const unsigned slice = idx % slices, tile = (idx / slices) % tiles, seq = idx / slices / tiles;
+    const size_t c = (size_t)slice * 256 + threadIdx.x;
+    const size_t cc = c < channels ? c : channels - 1;  // idle lanes load a valid column and store nothing
+    x += (size_t)seq * (size_t)frames * ldx;
+    out += (size_t)seq * rows * ldo;
+    const size_t r0 = (size_t)tile * R;
+    const int64_t first = t0 + (int64_t)r0 * STRIDE - kernel / 2;  // the frame of window slot 0
+    float v[SPAN], wr[KMAX];
+#pragma unroll
+    for (int s = 0; s < SPAN; s++) {
+        const int64_t f = first + s;
+        const int64_t fc = f < 0 ? 0 : (f >= frames ? frames - 1 : f);
+        v[s] = x[(size_t)fc * ldx + cc];
+    }
+#pragma unroll
+    for (int j = 0; j < KMAX; j++) wr[j] = w[(size_t)(j < kernel ? j : kernel - 1) * channels + cc];
+    const float b = bias[cc];
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) acc[i] = b;
+    if (first >= 0 && first + (R - 1) * STRIDE + kernel <= frames) {
+#pragma unroll
+        for (int j = 0; j < KMAX; j++) {
+            if (j < kernel) {
+#pragma unroll
+                for (int i = 0; i < R; i++) acc[i] = acc[i] + wr[j] * v[i * STRIDE + j];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KMAX; j++) {
+            if (j < kernel) {
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    const float nv = acc[i] + wr[j] * v[i * STRIDE + j];
+                    acc[i] = (uint64_t)(first + i * STRIDE + j) < (uint64_t)frames ? nv : acc[i];
+                }
+            }
+        }
+    }
+    if (c >= channels) return;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        if (r0 + i >= rows) break;
+        float o = acc[i];
+        if (silu) o = o / (1.0f + exp_simd(0.0f - o));
+        out[(r0 + i) * ldo + c] = o;
+    }
+}
+
+// Fallback for kernels beyond 32 taps, strides beyond 2 and empty inputs or kernels: the same sums
+// straight from global memory, DW_ROWS output rows per lane.
+constexpr int DW_ROWS = 8;
+
+__global__ __launch_bounds__(256) void dwconv1d_kernel(const float *__restrict__ x, size_t ldx, int64_t frames,
+                                                       size_t channels, const float *__restrict__ w, int kernel,
+                                                       const float *__restrict__ bias, int64_t t0, int64_t stride,
+                                                       size_t rows, int silu, float *__restrict__ out, size_t ldo) {
+    const size_t c = (size_t)blockIdx.y * 256 + threadIdx.x;
+    if (c >= channels) return;
+    x += (size_t)blockIdx.z * (size_t)frames * ldx;  // sequence z of the batch
+    out += (size_t)blockIdx.z * rows * ldo;
+    const size_t r0 = (size_t)blockIdx.x * DW_ROWS;
+    const int64_t half = kernel / 2;
+    const float b = bias[c];
+    float acc[DW_ROWS];
+#pragma unroll
+    for (int i = 0; i < DW_ROWS; i++) acc[i] = b;
+    for (int j = 0; j < kernel; j++) {
+        const float wj = w[(size_t)j * channels + c];
+#pragma unroll
+        for (int i = 0; i < DW_ROWS; i++) {
+            const int64_t src = t0 + (int64_t)(r0 + i) * stride + j - half;
+            if (r0 + i < rows && src >= 0 && src < frames) acc[i] = acc[i] + wj * x[(size_t)src * ldx + c];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DW_ROWS; i++) {
+        if (r0 + i >= rows) break;
+        float v = acc[i];
+        if (silu) v = v / (1.0f + exp_simd(0.0f - v));
+        out[(r0 + i) * ldo + c] = v;
+    }
+}
+
+template <int R, int STRIDE, int KMAX>
+void launch_dwconv_reg(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels, const float *w,
+                       size_t kernel, const float *bias, size_t t0, size_t rows, int silu, float *out, size_t ldo,
+                       hipStream_t s) {
+    // the host keeps tiles * slices * batch below 2^24 work items
+    const unsigned tiles = (unsigned)div_ceil(rows, (size_t)R), slices = (unsigned)div_ceil(channels, (size_t)256);
+    const unsigned total = tiles * slices * (unsigned)batch;
+    hipLaunchKernelGGL((dwconv1d_reg_kernel<R, STRIDE, KMAX>), dim3(div_ceil(total, 8u) * 8), dim3(256), 0, s, x, ldx,
+                       (int64_t)frames, channels, w, (int)kernel, bias, (int64_t)t0, rows, silu, out, ldo, tiles, slices,
+                       total);
+}
+
+hipError_t launch_dwconv1d(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels, const float *w,
+                           size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows, int silu,
+                           float *out, size_t ldo, hipStream_t s) {
+    if (rows == 0 || channels == 0 || batch == 0) return hipSuccess;
+    // the register window needs a frame to clamp to and at least one tap
+    if (frames > 0 && kernel > 0 && (stride == 1 || stride == 2) && kernel <= 32) {
+        if (stride == 1) {
+            if (kernel <= 9)
+                launch_dwconv_reg<16, 1, 9>(x, ldx, frames, batch, channels, w, kernel, bias, t0, rows, silu, out, ldo, s);
+            else if (kernel <= 16)
+                launch_dwconv_reg<16, 1, 16>(x, ldx, frames, batch, channels, w, kernel, bias, t0, rows, silu, out, ldo,
+                                             s);
+            else
+                launch_dwconv_reg<16, 1, 32>(x, ldx, frames, batch, channels, w, kernel, bias, t0, rows, silu, out, ldo,
+                                             s);
+        } else {
+            if (kernel <= 9)
+                launch_dwconv_reg<16, 2, 9>(x, ldx, frames, batch, channels, w, kernel, bias, t0, rows, silu, out, ldo, s);
+            else if (kernel <= 16)
+                launch_dwconv_reg<16, 2, 16>(x, ldx, frames, batch, channels, w, kernel, bias, t0, rows, silu, out, ldo,
+                                             s);
+            else
+                launch_dwconv_reg<8, 2, 32>(x, ldx, frames, batch, channels, w, kernel, bias, t0, rows, silu, out, ldo, s);
+        }
+        return hipGetLastError();
+    }
+    // row tiles along x, 256-channel slices along y, sequences along z (the host keeps y, z < 65536)
+    const dim3 grid((unsigned)div_ceil(rows, (size_t)DW_ROWS), (unsigned)div_ceil(channels, (size_t)256),
+                    (unsigned)batch);
+    hipLaunchKernelGGL(dwconv1d_kernel, grid, dim3(256), 0, s, x, ldx, (int64_t)frames, channels, w, (int)kernel, bias,
+                       (int64_t)t0, (int64_t)stride, rows, silu, out, ldo);
     return hipGetLastError();
 }
 

@@ -173,6 +173,9 @@ hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, 
 hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s);
 
 // LayerNorm of m rows of n values (the reference's AVX-512 summation order).
+hipError_t launch_dwconv1d(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels, const float *w,
+                           size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows, int silu,
+                           float *out, size_t ldo, hipStream_t s);
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s);
 

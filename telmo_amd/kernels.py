@@ -303,5 +303,19 @@ class Kernels:
                                              float(eps), ctypes.c_void_p(out.data_ptr()), ldo)
         _check(rc, self._ctx)
 
+    def dwconv1d_device(self, x, ldx: int, frames: int, channels: int, w, kernel: int, bias, out, ldo: int,
+                        rows: int = None, t0: int = 0, stride: int = 1, act: "Act" = None, batch: int = 1):
+        """Depthwise convolution of GPU tensor x (frames x channels) into out: row r is
+        dwconv1d_frame at frame t0 + r * stride (rows defaults to frames), then SiLU when act is
+        Act.SILU, as the conv module applies it. batch equal-length sequences of frames rows
+        (rows output rows each) laid one after another are convolved each on its own."""
+        rows = frames if rows is None else rows
+        a = int(Act.NONE if act is None else act)
+        xp = ctypes.c_void_p(x.data_ptr()) if x is not None else None
+        rc = _lib.lib().tg_dwconv1d_device(self._ctx, xp, ldx, frames, batch, channels,
+                                           ctypes.c_void_p(w.data_ptr()), kernel, ctypes.c_void_p(bias.data_ptr()),
+                                           t0, stride, rows, a, ctypes.c_void_p(out.data_ptr()), ldo)
+        _check(rc, self._ctx)
+
     def synchronize(self) -> None:
         _check(_lib.lib().tg_synchronize(self._ctx), self._ctx)

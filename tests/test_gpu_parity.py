@@ -313,6 +313,94 @@ def test_layer_norm_matches_the_reference_order(tk, orc):
         assert np.array_equal(got_in_place[:, :n].view(np.uint32), want.view(np.uint32)), (m, n)
 
 
+DWCONV_CASES = [  # frames, channels, kernel, ldx, ldo, t0, stride, rows, silu
+    (750, 1024, 9, 1024, 1024, 0, 1, 750, True),
+    (3, 37, 9, 40, 41, 0, 1, 3, False),
+    (20, 300, 4, 300, 303, 0, 1, 20, True),
+    (50, 257, 7, 257, 260, 3, 2, 24, True),
+    (100, 512, 15, 515, 512, 1, 2, 50, False),
+    (9, 5, 1, 5, 5, 0, 1, 11, True),
+    (4, 6, 0, 6, 6, 0, 1, 4, False),
+    (12000, 1024, 9, 1024, 1024, 0, 1, 12000, True),
+    (60, 300, 25, 300, 300, 0, 1, 60, True),  # up to 32 taps, stride 1
+    (45, 100, 16, 100, 100, 0, 1, 45, False),  # up to 16 taps, stride 1
+    (33, 70, 12, 70, 70, 1, 2, 16, True),  # up to 16 taps, stride 2
+    (80, 129, 31, 129, 129, 2, 2, 39, False),  # up to 32 taps, stride 2
+    (70, 200, 20, 200, 200, 3, 4, 17, True),  # stride 4: the direct kernel
+    (90, 64, 5, 64, 64, 1, 3, 30, True),  # stride 3: the direct kernel
+    (50, 64, 33, 64, 64, 0, 1, 50, True),  # 33 taps: the direct kernel
+    (0, 40, 9, 40, 40, 0, 1, 3, True),  # no input frames: SiLU(bias)
+]
+
+
+@pytest.mark.parametrize("case", DWCONV_CASES)
+def test_depthwise_conv_matches_the_reference_steps(tk, orc, case):
+    """The depthwise convolution (+ SiLU) is bit-identical to the oracle's dwconv1d_frame loop, and
+    leaves the gaps of out and the rows past it alone."""
+    import torch
+
+    from telmo_amd import Act
+
+    frames, channels, kernel, ldx, ldo, t0, stride, rows, silu = case
+    rng = np.random.default_rng(frames + channels + kernel)
+    x = (2.0 * rng.standard_normal((frames, ldx))).astype(np.float32)
+    w = (0.3 * rng.standard_normal((kernel, channels))).astype(np.float32)
+    bias = rng.standard_normal(channels).astype(np.float32)
+    say("dwconv1d", case)
+    want = orc.dwconv1d(x[:, :channels], w, bias, rows=rows, t0=t0, stride=stride, silu=silu)
+    xd = torch.from_numpy(x).cuda() if frames else None
+    wd = torch.from_numpy(w).cuda() if kernel else torch.zeros(1, device="cuda")
+    bd = torch.from_numpy(bias).cuda()
+    out = torch.full((rows + 1, ldo), 9.5, dtype=torch.float32, device="cuda")
+    tk.dwconv1d_device(xd, ldx, frames, channels, wd, kernel, bd, out, ldo, rows=rows, t0=t0, stride=stride,
+                       act=Act.SILU if silu else Act.NONE)
+    tk.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:rows, :channels].view(np.uint32), want.view(np.uint32)), case
+    assert np.all(got[:rows, channels:] == 9.5) and np.all(got[rows:] == 9.5)
+
+
+@pytest.mark.parametrize("batch,frames,rows,t0,stride", [(4, 40, 40, 0, 1), (32, 375, 375, 0, 1), (3, 17, 9, 1, 2)])
+def test_depthwise_conv_batches_sequences_apart(tk, orc, batch, frames, rows, t0, stride):
+    """A batch of sequences laid one after another is convolved each on its own: no tap reaches into
+    a neighbouring sequence."""
+    import torch
+
+    from telmo_amd import Act
+
+    channels, kernel = 300, 9
+    rng = np.random.default_rng(batch * frames)
+    x = rng.standard_normal((batch * frames, channels)).astype(np.float32)
+    w = (0.3 * rng.standard_normal((kernel, channels))).astype(np.float32)
+    bias = rng.standard_normal(channels).astype(np.float32)
+    say("dwconv1d batch", batch, frames, rows, t0, stride)
+    want = np.concatenate([orc.dwconv1d(x[b * frames:(b + 1) * frames], w, bias, rows=rows, t0=t0, stride=stride,
+                                        silu=True) for b in range(batch)])
+    out = torch.full((batch * rows, channels), 9.5, dtype=torch.float32, device="cuda")
+    tk.dwconv1d_device(torch.from_numpy(x).cuda(), channels, frames, channels, torch.from_numpy(w).cuda(), kernel,
+                       torch.from_numpy(bias).cuda(), out, channels, rows=rows, t0=t0, stride=stride, act=Act.SILU,
+                       batch=batch)
+    tk.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_depthwise_conv_refusals(tk):
+    import torch
+
+    import telmo_amd
+    from telmo_amd import Act
+
+    x = torch.zeros((8, 16), device="cuda")
+    w = torch.zeros((3, 16), device="cuda")
+    b = torch.zeros(16, device="cuda")
+    with pytest.raises(telmo_amd.TelmoError):
+        tk.dwconv1d_device(x, 16, 8, 16, w, 3, b, torch.zeros((8, 16), device="cuda"), 16, act=Act.RELU)
+    with pytest.raises(telmo_amd.TelmoError):
+        tk.dwconv1d_device(x, 16, 8, 16, w, 3, b, x[4:], 16, rows=4)  # out overlaps x
+    with pytest.raises(telmo_amd.TelmoError):
+        tk.dwconv1d_device(x, 8, 8, 16, w, 3, b, torch.zeros((8, 16), device="cuda"), 16)  # ldx < channels
+
+
 Q8_SHAPES = [(1, 32, 3), (1, 640, 200), (4, 96, 33), (8, 1280, 2560), (16, 1920, 100), (5, 2048, 70), (17, 96, 50),
              (64, 128, 96), (130, 992, 255), (257, 2048, 130), (750, 1024, 512)]
 
