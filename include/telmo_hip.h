@@ -15,6 +15,8 @@
  *   Kernels::glu (row kernel)    src/kernels/mod.rs:463-464   -> tg_glu_device
  *   Kernels::layer_norm          src/kernels/mod.rs:458       -> tg_layer_norm_device
  *   Kernels::dwconv1d_frame + silu  src/kernels/mod.rs:464-475  -> tg_dwconv1d_device
+ *   Parakeet::predict_rows       src/parakeet.rs:1524-1577    -> tg_tdt_predict_device
+ *   Parakeet::decode_inner       src/parakeet.rs:1412-1513    -> tg_tdt_decode_device
  *   Pack::open / from_bytes      src/pack.rs:79-96            -> tg_pack_open, tg_pack_from_bytes
  *   Pack::parse (the checks)     src/pack.rs:98-259           -> tg_pack_open, tg_pack_last_error
  *   Pack::model / meta / entries src/pack.rs:248-265          -> tg_pack_model, tg_pack_meta, tg_pack_entry_at
@@ -167,6 +169,51 @@ int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size
 int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
                        const float *w, size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows,
                        uint32_t act, float *out, size_t ldo);
+
+/* ---- the TDT decoder (src/parakeet.rs:1412-1577) --------------------------------------------
+ * Parakeet's prediction network (embedding, LSTM layers, projection) and joint, decoded greedily
+ * with every step on the device. The matrices are tg_weights of int8 or Q8_0 values; the handles,
+ * biases and embedding stay the caller's and must outlive the network. */
+typedef struct tg_tdt tg_tdt;
+typedef struct {
+    size_t hidden;                 /* pred_hidden h: a multiple of 4, at most 992 */
+    size_t vocab;                  /* tokens, the blank last (blank_token_id = vocab - 1) */
+    const int32_t *durations;      /* host, n_durations values >= 0 (the TDT durations) */
+    size_t n_durations;            /* 1 to 64 */
+    size_t max_symbols;            /* max_symbols_per_step */
+    size_t layers;                 /* LSTM layers, 1 to 4 */
+    const tg_weights *joint;       /* (vocab + n_durations) x h */
+    const float *joint_bias;       /* device, vocab + n_durations */
+    const float *embedding;        /* device, vocab x h, 16-byte aligned */
+    const tg_weights *lstm[4];     /* 4h x 2h: gates i, f, g, o of [x; h_l] */
+    const float *lstm_bias[4];     /* device, 4h */
+    const tg_weights *proj;        /* h x h */
+    const float *proj_bias;        /* device, h */
+} tg_tdt_desc;
+/* One emitted token (parakeet.rs Token): its id, its frame (relative to enc_proj's first row) and
+ * its duration. */
+typedef struct {
+    uint32_t id, frame, duration;
+} tg_token;
+int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out);
+void tg_tdt_destroy(tg_tdt *tdt);
+/* Rows tg_tdt_predict_device takes at once (16 for Parakeet's h = 640). */
+size_t tg_tdt_max_rows(const tg_tdt *tdt);
+/* predict_rows (src/parakeet.rs:1524-1577): for each row r, the token's embedding runs through the
+ * LSTM layers with row r's state (states: rows x layers x [h, c] of h floats each, updated in place),
+ * and preds[r] = proj(h_last) + bias. Gate math as the reference's: sigmoid = 1 / (1 + exp(-x)),
+ * tanh, c = f c + i g, h = o tanh(c). Device pointers, 16-byte aligned; queued on the stream. */
+int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_t rows, float *states, float *preds);
+/* decode_inner (src/parakeet.rs:1412-1513) from frame *frame with *on_frame tokens already on it:
+ * per frame t, logits = joint(relu(enc_proj[t] + pred)) + bias; the token and duration are the
+ * argmaxes of the vocabulary and duration logits; a blank moves max(duration, 1) frames, a token
+ * is emitted, runs through the prediction network (state: layers x [h, c], and pred, updated in
+ * place) and moves by its duration, or after max_symbols tokens of duration 0 by one frame. Runs
+ * until t >= frames and returns the emitted tokens (at most cap into tokens; *count is the number
+ * emitted, TG_ERR_SHAPE when it exceeds cap) with *frame and *on_frame where the loop stopped.
+ * enc_proj: frames rows of h floats at stride lde, on the device. Blocks until the decode ends. */
+int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t lde, size_t frames, float *state,
+                         float *pred, size_t *frame, size_t *on_frame, tg_token *tokens, size_t cap, size_t *count);
 
 /* ---- packs: the reference's weight files (src/pack.rs) -------------------------------------
  * A pack is "TELMOPAK", a u32 version (1) and 4 zero bytes; entries' data at multiples of 64

@@ -23,6 +23,9 @@
  *   or_dwconv1d_frame     src/kernels/scalar.rs:164-187 (== avx512.rs:445-459, the same loop)
  *   or_dwconv1d           src/parakeet.rs:1107-1122, src/granite.rs:900-915 (one frame per
  *                         output row, then silu, avx512.rs:308-311 and 432-443)
+ *   or_tdt_predict        src/parakeet.rs:1524-1577 (predict_rows), its products by the fast path's
+ *                         integer oracle, sigmoid as parakeet.rs:1678-1680, libm expf / tanhf
+ *   or_tdt_decode         src/parakeet.rs:1412-1513 (decode_inner), argmax as parakeet.rs:1682-1691
  *   or_store              src/kernels/scalar.rs:110-124 (unfused, libm exp) and
  *                         avx512.rs:313-343 (fused ISAs)
  *   or_matmul             src/kernels/mod.rs:530-688   (gemm_panels with KC = 256, the
@@ -607,4 +610,106 @@ int or_matmul_fast_q8(const float *a, size_t a_len, size_t lda, size_t m, const 
     free(ex);
     free(qt);
     return OR_OK;
+}
+
+/* ---- the TDT decoder ----------------------------------------------------------------------- */
+
+/* c = a w^T + bias for m rows by the fast path's integer oracle (int8 or Q8_0 weights). */
+static void tdt_linear(int p, const float *a, size_t m, size_t k, const uint8_t *values, const float *scales,
+                       size_t n, const float *bias, float *c) {
+    if (p == P_Q8_0)
+        or_matmul_fast_q8(a, m * k, k, m, values, scales, n, k, c, m * n, n, bias, n, ACT_NONE, 1.0f, 0);
+    else
+        or_matmul_fast(a, m * k, k, m, values, scales, n, k, c, m * n, n, bias, n, ACT_NONE, 1.0f, 0);
+}
+
+static float tdt_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* The first largest of n values (a NaN is never larger). */
+static size_t tdt_argmax(const float *v, size_t n) {
+    size_t best = 0;
+    for (size_t i = 0; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+/* predict_rows: states are rows x layers x [h, c] (h floats each), preds rows x h. lstm_v / lstm_s /
+ * lstm_b hold `layers` matrices 4h x 2h in the panel layout, their scales and biases. */
+void or_tdt_predict(int p, size_t h, size_t layers, const float *emb, const uint8_t *const *lstm_v,
+                    const float *const *lstm_s, const float *const *lstm_b, const uint8_t *proj_v,
+                    const float *proj_s, const float *proj_b, const int32_t *tokens, size_t rows, float *states,
+                    float *preds) {
+    const size_t width = layers * 2 * h;
+    float *input = calloc(rows * 2 * h, sizeof(float)), *gates = calloc(rows * 4 * h, sizeof(float));
+    float *last = calloc(rows * h, sizeof(float));
+    for (size_t r = 0; r < rows; r++) memcpy(input + r * 2 * h, emb + (size_t)tokens[r] * h, h * sizeof(float));
+    for (size_t l = 0; l < layers; l++) {
+        for (size_t r = 0; r < rows; r++)
+            memcpy(input + r * 2 * h + h, states + r * width + l * 2 * h, h * sizeof(float));
+        tdt_linear(p, input, rows, 2 * h, lstm_v[l], lstm_s[l], 4 * h, lstm_b[l], gates);
+        for (size_t r = 0; r < rows; r++) {
+            float *hs = states + r * width + l * 2 * h, *cs = hs + h;
+            const float *g = gates + r * 4 * h;
+            for (size_t j = 0; j < h; j++) {
+                const float i = tdt_sigmoid(g[j]), f = tdt_sigmoid(g[h + j]), gg = tanhf(g[2 * h + j]),
+                            o = tdt_sigmoid(g[3 * h + j]);
+                cs[j] = f * cs[j] + i * gg;
+                hs[j] = o * tanhf(cs[j]);
+            }
+            memcpy(input + r * 2 * h, hs, h * sizeof(float));
+        }
+    }
+    for (size_t r = 0; r < rows; r++) memcpy(last + r * h, input + r * 2 * h, h * sizeof(float));
+    tdt_linear(p, last, rows, h, proj_v, proj_s, h, proj_b, preds);
+    free(input);
+    free(gates);
+    free(last);
+}
+
+/* decode_inner from frame *t with *on_frame tokens on it: tokens get (id, frame, duration) triples,
+ * at most cap of them; returns the number emitted. enc holds frames rows of h floats (stride lde);
+ * the joint is (vocab + ndur) x h; the blank is vocab - 1. */
+size_t or_tdt_decode(int p, size_t h, size_t layers, size_t vocab, const int32_t *durations, size_t ndur,
+                     size_t max_symbols, const uint8_t *joint_v, const float *joint_s, const float *joint_b,
+                     const float *emb, const uint8_t *const *lstm_v, const float *const *lstm_s,
+                     const float *const *lstm_b, const uint8_t *proj_v, const float *proj_s, const float *proj_b,
+                     const float *enc, size_t lde, size_t frames, float *state, float *pred, size_t *t_io,
+                     size_t *on_frame_io, int32_t *tokens, size_t cap) {
+    const size_t outputs = vocab + ndur, blank = vocab - 1;
+    float *z = calloc(h, sizeof(float)), *logits = calloc(outputs, sizeof(float));
+    size_t t = *t_io, on_frame = *on_frame_io, count = 0;
+    while (t < frames) {
+        for (size_t i = 0; i < h; i++) z[i] = fmaxf(enc[t * lde + i] + pred[i], 0.0f);
+        tdt_linear(p, z, 1, h, joint_v, joint_s, outputs, joint_b, logits);
+        const size_t token = tdt_argmax(logits, vocab);
+        const size_t duration = (size_t)durations[tdt_argmax(logits + vocab, ndur)];
+        if (token == blank) {
+            t += duration > 1 ? duration : 1;
+            on_frame = 0;
+            continue;
+        }
+        if (count < cap) {
+            tokens[3 * count] = (int32_t)token;
+            tokens[3 * count + 1] = (int32_t)t;
+            tokens[3 * count + 2] = (int32_t)duration;
+        }
+        count++;
+        const int32_t tok = (int32_t)token;
+        or_tdt_predict(p, h, layers, emb, lstm_v, lstm_s, lstm_b, proj_v, proj_s, proj_b, &tok, 1, state, pred);
+        if (duration > 0) {
+            t += duration;
+            on_frame = 0;
+        } else {
+            on_frame += 1;
+            if (on_frame >= max_symbols) {
+                t += 1;
+                on_frame = 0;
+            }
+        }
+    }
+    *t_io = t;
+    *on_frame_io = on_frame;
+    free(z);
+    free(logits);
+    return count;
 }

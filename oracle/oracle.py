@@ -69,6 +69,12 @@ def lib():
         L.or_silu_simd.restype = ctypes.c_float
         L.or_glu.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.or_layer_norm.argtypes = [_f32p, _sz, _f32p, _f32p, _f32p, ctypes.c_float]
+        _vp = ctypes.c_void_p
+        L.or_tdt_predict.argtypes = [ctypes.c_int, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]
+        L.or_tdt_decode.argtypes = [ctypes.c_int, _sz, _sz, _sz, _vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                    _vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp, ctypes.POINTER(_sz),
+                                    ctypes.POINTER(_sz), _vp, _sz]
+        L.or_tdt_decode.restype = _sz
         L.or_dwconv1d_frame.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _sz, _f32p, _f32p]
         L.or_dwconv1d.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _sz, _f32p, _sz, _sz, _sz, ctypes.c_int,
                                   _f32p, _sz]
@@ -239,6 +245,47 @@ def dwconv1d(x, w, bias, rows=None, t0=0, stride=1, silu=False):
                           np.ascontiguousarray(bias, np.float32), t0, stride, rows, int(silu), out.reshape(-1),
                           channels)
     return out
+
+
+def _addr(x):
+    return x.ctypes.data_as(ctypes.c_void_p)
+
+
+def _tdt_common(net):
+    """Pointer arrays of a TDT network (a dict of contiguous numpy arrays; see tests/helpers.py)."""
+    L = len(net["lstm"])
+    keep = [net["emb"], net["proj"][0], net["proj"][1], net["proj_b"]]
+    lv = (ctypes.c_void_p * L)(*[w[0].ctypes.data for w in net["lstm"]])
+    ls = (ctypes.c_void_p * L)(*[w[1].ctypes.data for w in net["lstm"]])
+    lb = (ctypes.c_void_p * L)(*[b.ctypes.data for b in net["lstm_b"]])
+    return keep, lv, ls, lb
+
+
+def tdt_predict(net, tokens, states, preds):
+    """predict_rows in place: states [rows, layers * 2h] and preds [rows, h] (float32, C order)."""
+    keep, lv, ls, lb = _tdt_common(net)
+    toks = np.ascontiguousarray(tokens, np.int32)
+    lib().or_tdt_predict(net["p"], net["h"], len(net["lstm"]), _addr(net["emb"]), lv, ls, lb, _addr(net["proj"][0]),
+                         _addr(net["proj"][1]), _addr(net["proj_b"]), _addr(toks), toks.size, _addr(states),
+                         _addr(preds))
+
+
+def tdt_decode(net, enc, state, pred, frame=0, on_frame=0):
+    """decode_inner over the rows of enc [frames, h]: returns ([(id, frame, duration)], frame,
+    on_frame); state [layers * 2h] and pred [h] are updated in place."""
+    keep, lv, ls, lb = _tdt_common(net)
+    enc = np.ascontiguousarray(enc, np.float32)
+    frames = enc.shape[0]
+    durs = np.ascontiguousarray(net["durations"], np.int32)
+    cap = max(frames - frame, 0) * max(net["max_symbols"], 1) + 1
+    toks = np.zeros(3 * cap, np.int32)
+    f, o = ctypes.c_size_t(frame), ctypes.c_size_t(on_frame)
+    n = lib().or_tdt_decode(net["p"], net["h"], len(net["lstm"]), net["vocab"], _addr(durs), durs.size,
+                            net["max_symbols"], _addr(net["joint"][0]), _addr(net["joint"][1]),
+                            _addr(net["joint_b"]), _addr(net["emb"]), lv, ls, lb, _addr(net["proj"][0]),
+                            _addr(net["proj"][1]), _addr(net["proj_b"]), _addr(enc), enc.shape[1], frames,
+                            _addr(state), _addr(pred), ctypes.byref(f), ctypes.byref(o), _addr(toks), cap)
+    return [tuple(int(v) for v in toks[3 * i:3 * i + 3]) for i in range(n)], f.value, o.value
 
 
 def store(fused, acc, c, cols, bias, act, scale, accumulate):

@@ -3,7 +3,8 @@
 The compute is the HIP library ``lib/libtelmo_hip.so`` behind the C ABI of
 ``include/telmo_hip.h``; this package mirrors the reference's Python-visible names over it.
 """
-from .kernels import Act, Epilogue, Kernels, PackedWeights, Precision, TelmoError, decode, encode
+from .kernels import Act, Epilogue, Kernels, PackedWeights, Precision, TdtDecoder, TelmoError, Token, decode, encode
 from .pack import Pack
 
-__all__ = ["Act", "Epilogue", "Kernels", "Pack", "PackedWeights", "Precision", "TelmoError", "decode", "encode"]
+__all__ = ["Act", "Epilogue", "Kernels", "Pack", "PackedWeights", "Precision", "TdtDecoder", "TelmoError", "Token",
+           "decode", "encode"]

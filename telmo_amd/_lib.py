@@ -9,6 +9,22 @@ _sz = ctypes.c_size_t
 _p = ctypes.c_void_p
 _u32 = ctypes.c_uint32
 
+
+
+class TdtDesc(ctypes.Structure):
+    """tg_tdt_desc."""
+    _fields_ = [("hidden", _sz), ("vocab", _sz), ("durations", ctypes.POINTER(ctypes.c_int32)),
+                ("n_durations", _sz), ("max_symbols", _sz), ("layers", _sz), ("joint", _p), ("joint_bias", _p),
+                ("embedding", _p), ("lstm", _p * 4), ("lstm_bias", _p * 4), ("proj", _p), ("proj_bias", _p)]
+
+
+class Token(ctypes.Structure):
+    """tg_token."""
+    _fields_ = [("id", ctypes.c_uint32), ("frame", ctypes.c_uint32), ("duration", ctypes.c_uint32)]
+
+
+_szp = ctypes.POINTER(_sz)
+
 # name: (restype, argtypes), in the order of include/telmo_hip.h
 SIGNATURES = {
     "tg_ctx_create": (ctypes.c_int, [ctypes.c_int, _p, ctypes.POINTER(_p)]),
@@ -34,6 +50,11 @@ SIGNATURES = {
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
     "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, ctypes.c_float, _p, _sz]),
     "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, _sz, _sz, _u32, _p, _sz]),
+    "tg_tdt_create": (ctypes.c_int, [_p, _p, ctypes.POINTER(_p)]),
+    "tg_tdt_destroy": (None, [_p]),
+    "tg_tdt_max_rows": (_sz, [_p]),
+    "tg_tdt_predict_device": (ctypes.c_int, [_p, _p, _p, _sz, _p, _p]),
+    "tg_tdt_decode_device": (ctypes.c_int, [_p, _p, _p, _sz, _sz, _p, _p, _szp, _szp, _p, _sz, _szp]),
     "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),
     "tg_pack_close": (None, [_p]),

@@ -10,7 +10,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libtelmo_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["api.hip", "kernels_rows.hip", "kernels_gemm.hip", "kernels_gemv.hip", "kernels_exact.hip", "layout.cpp", "pack.cpp"]
+SOURCES = ["api.hip", "kernels_rows.hip", "kernels_gemm.hip", "kernels_gemv.hip", "kernels_tdt.hip", "kernels_exact.hip",
+           "layout.cpp", "pack.cpp"]
 
 # -ffp-contract=off: no implicit fused multiply-adds, so the f32 epilogue and the exact kernel
 # round as the reference does. Packed f32 instructions are turned off for the device code.

@@ -11,6 +11,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/telmo_hip.h"
 #include "tg_internal.hpp"
@@ -38,6 +39,20 @@ struct tg_ctx {
 struct tg_weights {
     tg::DeviceWeights d;
     int device;
+};
+
+// A TDT prediction network and joint on the device (the weights stay the caller's), with the
+// buffers of its decode steps.
+struct tg_tdt {
+    tg::TdtNet net;
+    int device = 0;
+    tg::TdtCtl *ctl = nullptr;          // device control block
+    tg::TdtCtl *ctl_host = nullptr;     // pinned copy
+    int32_t *durations = nullptr;       // device
+    float *logits = nullptr, *gates = nullptr;
+    void *partials = nullptr;
+    int32_t *tokens = nullptr;          // device, 3 int32 per token
+    size_t tokens_cap = 0;              // tokens the buffer holds
 };
 
 namespace {
@@ -465,6 +480,204 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, s
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, tg::launch_dwconv1d(x, ldx, frames, batch, channels, w, kernel, bias, t0, stride, rows,
                                     act == TG_ACT_SILU, out, ldo, ctx->stream));
+    return TG_OK;
+}
+
+/* ---- the TDT decode -------------------------------------------------------------------------- */
+
+namespace {
+
+void tdt_release(tg_tdt *t) {
+    if (!t) return;
+    if (t->ctl) (void)hipFree(t->ctl);
+    if (t->ctl_host) (void)hipHostFree(t->ctl_host);
+    if (t->durations) (void)hipFree(t->durations);
+    if (t->logits) (void)hipFree(t->logits);
+    if (t->gates) (void)hipFree(t->gates);
+    if (t->partials) (void)hipFree(t->partials);
+    if (t->tokens) (void)hipFree(t->tokens);
+    delete t;
+}
+
+bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// A matrix of the network: present, on the context's device, int8 or Q8_0, of the given shape.
+int tdt_matrix(tg_ctx *ctx, const tg_weights *w, size_t n, size_t k, const char *what) {
+    if (!w) return fail(ctx, TG_ERR_NULL, std::string(what) + " is null");
+    if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, std::string(what) + " lives on another device");
+    if (w->d.precision != tg::INT8 && w->d.precision != tg::Q8_0)
+        return fail(ctx, TG_ERR_UNSUPPORTED, std::string(what) + ": the TDT step takes int8 or Q8_0 weights");
+    if (w->d.n != n || w->d.k != k)
+        return fail(ctx, TG_ERR_SHAPE, std::string(what) + " is " + std::to_string(w->d.n) + " x " +
+                                           std::to_string(w->d.k) + ", and the network needs " + std::to_string(n) +
+                                           " x " + std::to_string(k));
+    return TG_OK;
+}
+
+}  // namespace
+
+int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out) {
+    if (!ctx || !desc || !out) return fail(ctx, TG_ERR_NULL, "null argument");
+    *out = nullptr;
+    const size_t h = desc->hidden, layers = desc->layers, ndur = desc->n_durations, vocab = desc->vocab;
+    if (layers < 1 || layers > (size_t)tg::TDT_MAX_LAYERS) return fail(ctx, TG_ERR_ARG, "layers must be 1 to 4");
+    if (h == 0 || h % 4) return fail(ctx, TG_ERR_ARG, "hidden must be a positive multiple of 4");
+    if (2 * h > 1984) return fail(ctx, TG_ERR_UNSUPPORTED, "hidden beyond 992 (the LSTM rows exceed the GEMV's LDS)");
+    if (vocab == 0 || vocab > (size_t)INT32_MAX / 2) return fail(ctx, TG_ERR_ARG, "vocab must be positive");
+    if (ndur == 0 || ndur > 64 || !desc->durations) return fail(ctx, TG_ERR_ARG, "durations must hold 1 to 64 values");
+    for (size_t i = 0; i < ndur; i++)
+        if (desc->durations[i] < 0) return fail(ctx, TG_ERR_ARG, "durations must be >= 0");
+    if (desc->max_symbols > (size_t)INT32_MAX) return fail(ctx, TG_ERR_ARG, "max_symbols out of range");
+    int rc = tdt_matrix(ctx, desc->joint, vocab + ndur, h, "joint");
+    if (rc) return rc;
+    for (size_t l = 0; l < layers; l++) {
+        rc = tdt_matrix(ctx, desc->lstm[l], 4 * h, 2 * h, "lstm");
+        if (rc) return rc;
+        if (!desc->lstm_bias[l]) return fail(ctx, TG_ERR_NULL, "an LSTM bias is null");
+    }
+    rc = tdt_matrix(ctx, desc->proj, h, h, "proj");
+    if (rc) return rc;
+    if (!desc->joint_bias || !desc->embedding || !desc->proj_bias) return fail(ctx, TG_ERR_NULL, "null bias or embedding");
+    if (!aligned16(desc->embedding)) return fail(ctx, TG_ERR_ALIGN, "the embedding must be 16-byte aligned");
+
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    tg_tdt *t = new tg_tdt();
+    t->device = ctx->device;
+    tg::TdtNet &net = t->net;
+    net.h = h;
+    net.vocab = vocab;
+    net.ndur = ndur;
+    net.layers = layers;
+    net.blank = vocab - 1;
+    net.max_symbols = desc->max_symbols;
+    net.joint = &desc->joint->d;
+    net.proj = &desc->proj->d;
+    net.joint_b = desc->joint_bias;
+    net.proj_b = desc->proj_bias;
+    net.emb = desc->embedding;
+    for (size_t l = 0; l < layers; l++) {
+        net.lstm[l] = &desc->lstm[l]->d;
+        net.lstm_b[l] = desc->lstm_bias[l];
+    }
+    const size_t outputs = vocab + ndur;
+    bool ok = hipMalloc(&t->ctl, sizeof(tg::TdtCtl)) == hipSuccess &&
+              hipHostMalloc(&t->ctl_host, sizeof(tg::TdtCtl), hipHostMallocDefault) == hipSuccess &&
+              hipMalloc(&t->durations, ndur * sizeof(int32_t)) == hipSuccess &&
+              hipMalloc(&t->logits, (size_t)tg::TDT_ROWS * outputs * sizeof(float)) == hipSuccess &&
+              hipMalloc(&t->gates, (size_t)tg::TDT_ROWS * 4 * h * sizeof(float)) == hipSuccess &&
+              hipMalloc(&t->partials, tg::tdt_partials_bytes()) == hipSuccess;
+    if (!ok) {
+        tdt_release(t);
+        return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+    }
+    net.durations = t->durations;
+    std::memset(t->ctl_host, 0, sizeof(tg::TdtCtl));
+    hipError_t e = hipMemcpyAsync(t->ctl, t->ctl_host, sizeof(tg::TdtCtl), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(t->durations, desc->durations, ndur * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        tdt_release(t);
+        return hip_fail(ctx, e, "tg_tdt_create");
+    }
+    *out = t;
+    return TG_OK;
+}
+
+void tg_tdt_destroy(tg_tdt *tdt) {
+    if (!tdt) return;
+    (void)hipSetDevice(tdt->device);
+    (void)hipDeviceSynchronize();
+    tdt_release(tdt);
+}
+
+size_t tg_tdt_max_rows(const tg_tdt *tdt) { return tdt ? tg::tdt_max_rows(*tdt->net.lstm[0]) : 0; }
+
+int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_t rows, float *states, float *preds) {
+    if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
+    if (rows == 0) return TG_OK;
+    if (!tokens || !states || !preds) return fail(ctx, TG_ERR_NULL, "null tokens, states or preds");
+    if (tdt->device != ctx->device) return fail(ctx, TG_ERR_ARG, "the network lives on another device");
+    if (rows > tg::tdt_max_rows(*tdt->net.lstm[0]))
+        return fail(ctx, TG_ERR_UNSUPPORTED, "more rows than tg_tdt_max_rows");
+    if (!aligned16(states) || !aligned16(preds)) return fail(ctx, TG_ERR_ALIGN, "states and preds must be 16-byte aligned");
+    tg::TdtTokens toks{};
+    for (size_t r = 0; r < rows; r++) {
+        if (tokens[r] < 0 || (size_t)tokens[r] >= tdt->net.vocab) return fail(ctx, TG_ERR_ARG, "a token is out of range");
+        toks.tok[r] = tokens[r];
+    }
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_tdt_predict(tdt->ctl, 0, toks, rows, tdt->net, states, preds, tdt->gates, 0, ctx->stream));
+    return TG_OK;
+}
+
+int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t lde, size_t frames, float *state,
+                         float *pred, size_t *frame, size_t *on_frame, tg_token *tokens, size_t cap, size_t *count) {
+    if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
+    if (!state || !pred || !frame || !on_frame || !count || (cap && !tokens))
+        return fail(ctx, TG_ERR_NULL, "null argument");
+    *count = 0;
+    if (tdt->device != ctx->device) return fail(ctx, TG_ERR_ARG, "the network lives on another device");
+    const tg::TdtNet &net = tdt->net;
+    if (frames >= ((size_t)1 << 24)) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^24 frames");
+    if (*frame >= frames) return TG_OK;  // the reference's loop does not start
+    if (!enc_proj) return fail(ctx, TG_ERR_NULL, "enc_proj is null");
+    if (lde < net.h || lde % 4) return fail(ctx, TG_ERR_SHAPE, "lde must be >= hidden and a multiple of 4");
+    if (!aligned16(enc_proj) || !aligned16(state) || !aligned16(pred))
+        return fail(ctx, TG_ERR_ALIGN, "enc_proj, state and pred must be 16-byte aligned");
+    if (*on_frame > (size_t)INT32_MAX) return fail(ctx, TG_ERR_ARG, "on_frame out of range");
+    // At most max(max_symbols, 1) tokens per frame: a token either moves on by its duration or
+    // counts towards max_symbols on its frame.
+    const size_t per_frame = net.max_symbols > 1 ? net.max_symbols : 1;
+    const size_t most = (frames - *frame) * per_frame;
+    if (most >= ((size_t)1 << 30)) return fail(ctx, TG_ERR_UNSUPPORTED, "too many possible tokens");
+
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    if (most > tdt->tokens_cap) {
+        TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (tdt->tokens) TG_HIP(ctx, hipFree(tdt->tokens));
+        tdt->tokens = nullptr;
+        tdt->tokens_cap = 0;
+        if (hipMalloc(&tdt->tokens, most * 3 * sizeof(int32_t)) != hipSuccess)
+            return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+        tdt->tokens_cap = most;
+    }
+    tg::TdtCtl *hc = tdt->ctl_host;
+    TG_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the pinned copy is free to rewrite
+    std::memset(hc, 0, sizeof(*hc));
+    hc->t = (int32_t)*frame;
+    hc->on_frame = (int32_t)*on_frame;
+    TG_HIP(ctx, hipMemcpyAsync(tdt->ctl, hc, sizeof(*hc), hipMemcpyHostToDevice, ctx->stream));
+    // Steps are queued in batches; a step after the end returns at once. Every step emits a token
+    // or moves at least one frame, so (frames - frame) (per_frame + 1) steps always suffice.
+    const size_t limit = (frames - *frame) * (per_frame + 1) + 1;
+    size_t steps = 0, batch = 4;
+    while (true) {
+        for (size_t i = 0; i < batch; i++)
+            TG_HIP(ctx, tg::launch_tdt_step(tdt->ctl, net, enc_proj, lde, (int)frames, state, pred, tdt->logits,
+                                           tdt->gates, tdt->partials, tdt->tokens, (int)most, ctx->stream));
+        steps += batch;
+        TG_HIP(ctx, hipMemcpyAsync(hc, tdt->ctl, sizeof(*hc), hipMemcpyDeviceToHost, ctx->stream));
+        TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (hc->done) break;
+        if (steps > limit) return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
+        batch = batch < 64 ? batch * 2 : 64;
+    }
+    const size_t n = (size_t)hc->ntok;
+    *frame = (size_t)hc->t;
+    *on_frame = (size_t)hc->on_frame;
+    *count = n;
+    const size_t copy = n < cap ? n : cap;
+    if (copy) {
+        std::vector<int32_t> buf(copy * 3);
+        TG_HIP(ctx, hipMemcpy(buf.data(), tdt->tokens, copy * 3 * sizeof(int32_t), hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < copy; i++)
+            tokens[i] = tg_token{(uint32_t)buf[3 * i], (uint32_t)buf[3 * i + 1], (uint32_t)buf[3 * i + 2]};
+    }
+    if (n > cap) return fail(ctx, TG_ERR_SHAPE, "tokens holds " + std::to_string(cap) + " entries and the decode emitted " + std::to_string(n));
     return TG_OK;
 }
 

@@ -1,0 +1,276 @@
+// The MFMA GEMV of the decode steps (m <= 16 rows, k <= 1984) as a device-function template over
+// where its input rows come from and where its outputs go, so the plain GEMV and the fused TDT step
+// share one body. The rows are read once into registers ahead of the weights, split into two int8
+// digits in LDS as 16 x 64 MFMA A operands, and every 1 KB weight block costs one 16-byte LDS read
+// per digit and two v_mfma_i32_16x16x64_i8 (Q8_0: four 16x16x32 MFMAs and a per-block f32 fold).
+// Workgroups stay resident and walk the panels, requesting the next panel's weights, scales, bias
+// and old outputs before the current panel's epilogue.
+#pragma once
+#include "tg_internal.hpp"
+
+namespace tg {
+namespace gemv {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Four zero inputs: what the GEMV loads for chunks past the end of a row. Never written; not const,
+// so that it lives in global memory like the rows and the loads stay global loads.
+static __device__ __attribute__((aligned(16))) float ZERO_CHUNK[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+// Input rows read from memory: row r at a + r lda (16-byte aligned rows, k % 4 == 0).
+struct RowsIn {
+    const float *a;
+    size_t lda;
+    __device__ __forceinline__ v4f load(int r, int i0, int m, int k) const {
+        const float *src = (r < m && i0 < k) ? a + (size_t)r * lda + i0 : ZERO_CHUNK;
+        return *reinterpret_cast<const v4f *>(src);
+    }
+};
+
+// Outputs stored to c (row stride ldc).
+struct StoreC {
+    float *c;
+    size_t ldc;
+    __device__ __forceinline__ void store(int r, int col, float v) { c[(size_t)r * ldc + col] = v; }
+};
+
+// The maximum over the 64 lanes (all active), returned to every lane. DPP moves within rows of
+// 16 lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror) leave each row's
+// maximum in all its lanes; the four rows meet through v_readlane. No LDS traffic.
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// What one wavefront needs of panel p: its KBC first weight blocks, and for its lane's column the
+// scale, the bias and the old outputs of its four rows (when accumulating).
+template <int KBC>
+__device__ __forceinline__ void fetch_panel(v4i (&wr)[KBC], float &sc, float &bv, float (&old)[4], int p, int lane,
+                                            const uint8_t *wv, size_t panel_stride, size_t blk_stride, int KB,
+                                            const float *scales, const float *bias, const float *c, size_t ldc,
+                                            int N, int m, int accumulate) {
+    const uint8_t *wp = wv + (size_t)p * panel_stride + lane * 16;
+#pragma unroll
+    for (int t = 0; t < KBC; t++) wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(t, KB - 1) * blk_stride);
+    // Branch-free: loads that are not needed read a valid address and are discarded, so the
+    // compiler's load counting stays exact and nothing here waits on earlier loads.
+    const int col = p * PANEL + (lane & 15), orow = (lane >> 4) * 4;
+    sc = scales[col];
+    bv = *(bias ? bias + min(col, N - 1) : scales + col);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const bool need = accumulate && orow + v < m && col < N;
+        old[v] = *(need ? c + (size_t)(orow + v) * ldc + col : c);
+    }
+}
+
+// Q8_0 weights: for k-blocks c0 .. c0 + KBC - 1 of panel p, the two 8-byte operand halves of this
+// lane (inputs 32 h + 8 g .. + 8 of output j, read from layout lane 16 (2 h + g / 2) + j at byte
+// 8 (g % 2)) and the scales of the two 32-input blocks (zero past the last block).
+template <int KBC>
+__device__ __forceinline__ void load_q8(long (&wq)[KBC][2], float (&sq)[KBC][2], const uint8_t *wp, const float *sp,
+                                        int c0, int KB, int NB, size_t blk_stride, int off0) {
+#pragma unroll
+    for (int t = 0; t < KBC; t++) {
+        const int tt = min(c0 + t, KB - 1), b0 = 2 * tt, b1 = b0 + 1;
+        wq[t][0] = *reinterpret_cast<const long *>(wp + (size_t)tt * blk_stride + off0);
+        wq[t][1] = *reinterpret_cast<const long *>(wp + (size_t)tt * blk_stride + off0 + 512);
+        sq[t][0] = sp[(size_t)b0 * PANEL];
+        const float s1 = sp[(size_t)min(b1, NB - 1) * PANEL];
+        sq[t][1] = b1 < NB ? s1 : 0.0f;
+    }
+}
+
+// What one wavefront needs of Q8_0 panel p: its first KBC k-blocks' operand halves and block
+// scales, and for its lane's column the bias and the old outputs (branch-free, as fetch_panel).
+template <int KBC>
+__device__ __forceinline__ void fetch_panel_q8(long (&wq)[KBC][2], float (&sq)[KBC][2], float &bv, float (&old)[4],
+                                               int p, int lane, const uint8_t *wv, size_t panel_stride,
+                                               size_t blk_stride, int KB, int NB, int off0, const float *scales,
+                                               const float *bias, const float *c, size_t ldc, int N, int m,
+                                               int accumulate) {
+    const int col = p * PANEL + (lane & 15), orow = (lane >> 4) * 4;
+    load_q8<KBC>(wq, sq, wv + (size_t)p * panel_stride, scales + (size_t)p * NB * PANEL + (lane & 15), 0, KB, NB,
+                 blk_stride, off0);
+    bv = *(bias ? bias + min(col, N - 1) : scales);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const bool need = accumulate && orow + v < m && col < N;
+        old[v] = *(need ? c + (size_t)(orow + v) * ldc + col : c);
+    }
+}
+
+// The row exponent from the row's n <= 8 per-wavefront maxima (bits of |x|, all ones for a
+// non-finite input).
+__device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, int n) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+        if (s < n) mx = max(mx, slots[s]);
+    return mx == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(mx));
+}
+
+// Rows are split into 4-input chunks, ceil(KB / 4) wavefronts of them per row (the tail of the
+// last wavefront idle); wavefront w holds chunk wavefronts w + WAVES j (j < J) in registers. The
+// rows are read once, before the weights, so the weight loads stay in flight while the rows are
+// digitised.
+template <int WAVES, int KBC, int J, int Q8, class In, class Out>
+__device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
+                                          const float *__restrict__ scales, int N, int P, int KB, int NB,
+                                          const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
+                                          uint32_t act, float escale, int accumulate, size_t panel_stride,
+                                          size_t blk_stride, uint8_t *sqa, uint32_t *slot) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Chunk wavefront q = wave + WAVES j covers chunks 64 (q - r spr) + [0, 64) of row
+    // r = q / spr, where spr = ceil(KB / 4) wavefronts cover a row (its tail idle). All of it is
+    // uniform over the wavefront; q / spr is (q inv) >> 16, exact for q < 1024 and spr <= 8.
+    const int spr = (KB + 3) / 4, inv = (65536 + spr - 1) / spr;
+    const int wq = __builtin_amdgcn_readfirstlane(wave);
+    const int step = gridDim.x * WAVES;
+    int p = blockIdx.x * WAVES + wave;
+
+    // One 16-byte load per chunk (rows 16-byte aligned, k % 4 == 0); chunks past the rows read
+    // the zero chunk. Every load is unconditional and used as loaded, so the loads stay ahead of
+    // the weight loads and waiting for them never waits for the weights.
+    v4f x[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        x[j] = in.load(r, ((q - r * spr) * 64 + lane) * 4, m, k);
+    }
+    // Panel fetches are unconditional (a wavefront past the last panel re-reads panel P - 1 and
+    // never uses it): under a branch the compiler's load counting would wait for them early.
+    // int8: whole 16-byte operands and one scale per column. Q8_0: 8-byte halves and block scales.
+    const int off0 = (16 * ((lane >> 4) >> 1) + (lane & 15)) * 16 + 8 * ((lane >> 4) & 1);
+    v4i wr[Q8 ? 1 : KBC];
+    long wh[Q8 ? KBC : 1][2];
+    float sq[Q8 ? KBC : 1][2];
+    float sc = 0.0f, bv, old[4];
+    if constexpr (Q8)
+        fetch_panel_q8<KBC>(wh, sq, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, NB, off0, scales,
+                            bias, c, ldc, N, m, accumulate);
+    else
+        fetch_panel<KBC>(wr, sc, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias, c,
+                         ldc, N, m, accumulate);
+
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        if (r < m) {
+            const v4f v = x[j];
+            const bool bad = !__builtin_isfinite(v.x) | !__builtin_isfinite(v.y) | !__builtin_isfinite(v.z) |
+                             !__builtin_isfinite(v.w);
+            const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+            const uint32_t b = wave_max_u(bad ? 0xffffffffu : __float_as_uint(mx));
+            if (lane == 0) slot[q] = b;
+        }
+    }
+    __syncthreads();
+    // Lane r < m of every wavefront holds row r's exponent; the rest read it from there.
+    const int32_t e_lane = lane < m ? exponent_from_slots(slot + lane * spr, spr) : 0;
+    // Digits: chunk cc of row r holds inputs 4 cc .. 4 cc + 3, i.e. k-block cc / 16 and bytes
+    // 4 (cc % 16) .. of that block's 64; they go where lane 16 (cc % 16 / 4) + r reads its A operand.
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        if (r < m) {
+            const int cc = (q - r * spr) * 64 + lane;
+            if (cc < KB * 16) {
+                const int32_t e = __builtin_amdgcn_readlane(e_lane, r);
+                uint32_t h, l;
+                digits4(x[j].x, x[j].y, x[j].z, x[j].w, e, h, l);
+                uint8_t *d = sqa + (cc >> 4) * 2048 + ((cc & 15) >> 2) * 256 + r * 16 + (cc & 3) * 4;
+                *reinterpret_cast<uint32_t *>(d) = h;
+                *reinterpret_cast<uint32_t *>(d + 1024) = l;
+            }
+        }
+    }
+    // C operand of the MFMA: element v of lane l is row 4 (l / 16) + v, column l % 16. Rows m..15
+    // of the A operands are never written; their outputs are never stored.
+    const int orow = (lane >> 4) * 4, ocol = lane & 15;
+    int32_t erow[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) erow[v] = __shfl(e_lane, min(orow + v, 15), 64);
+    __syncthreads();
+
+    const uint8_t *ap = sqa + lane * 16;
+    for (; p < P; p += step) {
+        v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+        v4f accq = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint8_t *wp = wv + (size_t)p * panel_stride;
+        for (int c0 = 0; c0 < KB; c0 += KBC) {
+            if constexpr (Q8) {
+                if (c0 > 0)
+                    load_q8<KBC>(wh, sq, wp, scales + (size_t)p * NB * PANEL + (lane & 15), c0, KB, NB, blk_stride,
+                                 off0);
+#pragma unroll
+                for (int t = 0; t < KBC; t++) {
+                    if (c0 + t < KB) {
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const uint8_t *aq = sqa + (c0 + t) * 2048 + off0 + h * 512;
+                            const long ahi = *reinterpret_cast<const long *>(aq);
+                            const long alo = *reinterpret_cast<const long *>(aq + 1024);
+                            const v4i hh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ahi, wh[t][h], v4i{0, 0, 0, 0}, 0, 0, 0);
+                            const v4i ll = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo, wh[t][h], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                accq[v] = __builtin_fmaf(sq[t][h], (float)(hh[v] * 256 + ll[v]), accq[v]);
+                        }
+                    }
+                }
+            } else {
+                if (c0 > 0) {
+#pragma unroll
+                    for (int t = 0; t < KBC; t++)
+                        wr[t] = *reinterpret_cast<const v4i *>(wp + lane * 16 + (size_t)min(c0 + t, KB - 1) * blk_stride);
+                }
+#pragma unroll
+                for (int t = 0; t < KBC; t++) {
+                    if (c0 + t < KB) {
+                        const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
+                        const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
+                        acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
+                        acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        const float sc0 = sc, bv0 = bv;
+        float old0[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) old0[v] = old[v];
+        if constexpr (Q8)
+            fetch_panel_q8<KBC>(wh, sq, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, NB, off0,
+                                scales, bias, c, ldc, N, m, accumulate);
+        else
+            fetch_panel<KBC>(wr, sc, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, scales,
+                             bias, c, ldc, N, m, accumulate);
+        const int col = p * PANEL + ocol;
+        if (col < N) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                if (orow + v < m) {
+                    float s;
+                    if constexpr (Q8)
+                        s = erow[v] == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(accq[v], -erow[v]);
+                    else
+                        s = dequant(acc_hi[v], acc_lo[v], erow[v], sc0);
+                    out.store(orow + v, col,
+                              epilogue_vals(s, bias != nullptr, bv0, act, escale, accumulate != 0, old0[v]));
+                }
+            }
+        }
+    }
+}
+
+}  // namespace gemv
+}  // namespace tg

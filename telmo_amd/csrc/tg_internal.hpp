@@ -195,4 +195,32 @@ hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeig
 hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                         const EpiArgs &epi, hipStream_t s);
 
+// The greedy TDT decode (kernels_tdt.hip). The control block lives in device memory; the host
+// writes it before a decode and reads it between batches of steps.
+constexpr int TDT_ROWS = 16;       // frames the joint scores per step; rows of a standalone prediction
+constexpr int TDT_MAX_LAYERS = 4;  // LSTM layers of the prediction network
+struct TdtCtl {
+    int32_t t, on_frame, ntok;  // the frame, tokens on it so far, tokens emitted
+    int32_t active;             // a token waits for the prediction network
+    int32_t done;               // the frames are used up and no prediction waits
+    int32_t tok[TDT_ROWS];      // the tokens the prediction network runs on (the decode uses tok[0])
+    uint32_t arrive[TDT_MAX_LAYERS + 2];  // workgroups arrived: joint, each layer, projection
+};
+struct TdtTokens {
+    int32_t tok[TDT_ROWS];
+};
+struct TdtNet {
+    size_t h, vocab, ndur, layers, blank, max_symbols;
+    const DeviceWeights *joint, *lstm[TDT_MAX_LAYERS], *proj;
+    const float *joint_b, *lstm_b[TDT_MAX_LAYERS], *proj_b, *emb;  // device
+    const int32_t *durations;                                       // device, ndur
+};
+size_t tdt_max_rows(const DeviceWeights &lstm);
+size_t tdt_partials_bytes();
+hipError_t launch_tdt_predict(TdtCtl *ctl, int gated, const TdtTokens &toks, size_t m, const TdtNet &net,
+                              float *states, float *preds, float *gates, int frames, hipStream_t s);
+hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, size_t lde, int frames, float *states,
+                           float *pred, float *logits, float *gates, void *partials, int32_t *tokens, int cap,
+                           hipStream_t s);
+
 }  // namespace tg

@@ -19,7 +19,7 @@ from __future__ import annotations
 import ctypes
 import enum
 from dataclasses import dataclass
-from typing import Optional
+from typing import NamedTuple, Optional
 
 import numpy as np
 
@@ -319,3 +319,80 @@ class Kernels:
 
     def synchronize(self) -> None:
         _check(_lib.lib().tg_synchronize(self._ctx), self._ctx)
+
+
+class Token(NamedTuple):
+    """An emitted token (src/parakeet.rs Token): id, frame (relative to enc_proj's first row) and
+    duration."""
+    id: int
+    frame: int
+    duration: int
+
+
+class TdtDecoder:
+    """Parakeet's prediction network and joint on the GPU (src/parakeet.rs:1412-1577): int8 or Q8_0
+    PackedWeights for the joint ((vocab + durations) x h), the LSTM layers (4h x 2h, gates i, f, g,
+    o of [x; h_l]) and the projection (h x h); biases and the embedding (vocab x h) as float32 GPU
+    tensors. The blank is the last token. The weights and tensors are held, not copied."""
+
+    def __init__(self, kernels: "Kernels", hidden: int, vocab: int, durations, max_symbols: int,
+                 joint: PackedWeights, joint_bias, embedding, lstm, lstm_bias, proj: PackedWeights, proj_bias):
+        self._kernels = kernels
+        self._keep = (joint, joint_bias, embedding, list(lstm), list(lstm_bias), proj, proj_bias)
+        self.hidden, self.vocab, self.max_symbols = hidden, vocab, max_symbols
+        self.layers = len(lstm)
+        self.durations = [int(d) for d in durations]
+        self._durs = (ctypes.c_int32 * len(self.durations))(*self.durations)
+        desc = _lib.TdtDesc()
+        desc.hidden, desc.vocab, desc.max_symbols, desc.layers = hidden, vocab, max_symbols, len(lstm)
+        desc.durations = ctypes.cast(self._durs, ctypes.POINTER(ctypes.c_int32))
+        desc.n_durations = len(self.durations)
+        desc.joint, desc.joint_bias = joint._handle, joint_bias.data_ptr()
+        desc.embedding = embedding.data_ptr()
+        if len(lstm) > 4 or len(lstm) != len(lstm_bias):
+            raise ValueError("1 to 4 LSTM layers, each with its bias")
+        for i, (w, b) in enumerate(zip(lstm, lstm_bias)):
+            desc.lstm[i] = w._handle
+            desc.lstm_bias[i] = b.data_ptr()
+        desc.proj, desc.proj_bias = proj._handle, proj_bias.data_ptr()
+        handle = ctypes.c_void_p()
+        _check(_lib.lib().tg_tdt_create(kernels._ctx, ctypes.addressof(desc), ctypes.byref(handle)), kernels._ctx)
+        self._handle = handle
+
+    def max_rows(self) -> int:
+        return int(_lib.lib().tg_tdt_max_rows(self._handle))
+
+    def predict_rows(self, tokens, states, preds) -> None:
+        """predict_rows: each token runs through the LSTM layers with its row of states (GPU tensor,
+        rows x layers x [h, c]), updated in place; preds (rows x h) gets the projection."""
+        toks = (ctypes.c_int32 * max(len(tokens), 1))(*[int(t) for t in tokens])
+        _check(_lib.lib().tg_tdt_predict_device(self._kernels._ctx, self._handle, ctypes.addressof(toks), len(tokens),
+                                                ctypes.c_void_p(states.data_ptr()),
+                                                ctypes.c_void_p(preds.data_ptr())), self._kernels._ctx)
+
+    def decode(self, enc_proj, state, pred, frame: int = 0, on_frame: int = 0, cap: Optional[int] = None):
+        """The greedy decode over the rows of enc_proj (GPU tensor, frames x >= h) from frame with
+        on_frame tokens on it; state (layers x [h, c]) and pred (h) are updated in place. Returns
+        (tokens, frame, on_frame)."""
+        frames = enc_proj.shape[0]
+        if cap is None:
+            cap = max(frames - frame, 0) * max(self.max_symbols, 1)
+        out = (_lib.Token * max(cap, 1))()
+        f, o, n = ctypes.c_size_t(frame), ctypes.c_size_t(on_frame), ctypes.c_size_t(0)
+        rc = _lib.lib().tg_tdt_decode_device(self._kernels._ctx, self._handle, ctypes.c_void_p(enc_proj.data_ptr()),
+                                             enc_proj.stride(0), frames, ctypes.c_void_p(state.data_ptr()),
+                                             ctypes.c_void_p(pred.data_ptr()), ctypes.byref(f), ctypes.byref(o),
+                                             ctypes.addressof(out), cap, ctypes.byref(n))
+        _check(rc, self._kernels._ctx)
+        return [Token(t.id, t.frame, t.duration) for t in out[:n.value]], f.value, o.value
+
+    def close(self) -> None:
+        if self._handle:
+            _lib.lib().tg_tdt_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

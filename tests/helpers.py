@@ -50,3 +50,35 @@ def pack_q8_0(q, d):
     for o in range(n):
         scales[o // 16, :, o % 16] = d[o]
     return values, scales.reshape(-1)
+
+
+INT8_P, Q8_0_P = 3, 4
+
+
+def tdt_network(rng, h, vocab, durations, layers=2, precision=INT8_P, max_symbols=10, blank_bias=0.0,
+                lstm_scale=0.0004):
+    """A random TDT prediction network and joint (src/parakeet.rs:1412-1577) in the panel layout:
+    int8 (or Q8_0) joint (vocab + durations) x h, LSTM layers 4h x 2h, projection h x h, f32 biases
+    and embedding. LSTM scales stay small so its gates are not saturated and its recurrence does not
+    amplify small differences from step to step (with scales 5x larger, 1e-6 of noise in the state
+    grows to 1e-2 over 25 tokens); blank_bias is added to the blank's (the last token's) joint bias."""
+    def mat(n, k, lo, hi):
+        if precision == Q8_0_P:  # block scales in the int8 scales' range, f16-exact
+            q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+            d = (lo + (hi - lo) * rng.random((n, k // 32))).astype(np.float16).astype(np.float32)
+            return pack_q8_0(q, d)
+        q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+        sc = (lo + (hi - lo) * rng.random(n)).astype(np.float32)
+        return pack_int8(q, sc)
+
+    outputs = vocab + len(durations)
+    joint_b = (0.5 * rng.standard_normal(outputs)).astype(np.float32)
+    joint_b[vocab - 1] += blank_bias
+    return {
+        "p": precision, "h": h, "vocab": vocab, "durations": list(durations), "max_symbols": max_symbols,
+        "joint": mat(outputs, h, 0.001, 0.01), "joint_b": joint_b,
+        "emb": (0.5 * rng.standard_normal((vocab, h))).astype(np.float32),
+        "lstm": [mat(4 * h, 2 * h, lstm_scale, 2 * lstm_scale) for _ in range(layers)],
+        "lstm_b": [(0.1 * rng.standard_normal(4 * h)).astype(np.float32) for _ in range(layers)],
+        "proj": mat(h, h, 0.001, 0.003), "proj_b": (0.1 * rng.standard_normal(h)).astype(np.float32),
+    }

@@ -1,0 +1,173 @@
+"""Parity of the device TDT decoder (tg_tdt_predict_device, tg_tdt_decode_device) with the oracle's
+predict_rows and decode_inner, through the C ABI, on an MI355X.
+
+The GEMVs are the fast path's, bit-identical to the integer oracle for the same inputs. The gate
+math uses the GPU's expf / tanhf where the oracle (like the reference) uses the host libm, so a
+gate output can differ by an ulp. That can move a rounding of the next product's two-digit input by
+one unit (1/32639 of the row's largest |value|), a step of about |q| s / 32639 in each output it
+feeds (1e-6 to 1e-5 here). States and predictions are therefore held to the fast path's own bound,
+1e-4 (absolute for states, row-normwise for predictions; the north-star bound is 1e-3), and the
+emitted tokens, frames and durations must be identical.
+"""
+import numpy as np
+import pytest
+
+from helpers import INT8_P, Q8_0_P, rel_norm_err, tdt_network
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def say(*args):
+    print("[case]", *args, flush=True)
+
+
+@pytest.fixture(scope="module")
+def tk():
+    import telmo_amd
+
+    k = telmo_amd.Kernels()
+    yield k
+    k.close()
+
+
+def upload(tk, net, durations=None):
+    import torch
+
+    import telmo_amd
+
+    P = telmo_amd.Precision(net["p"])
+    h, vocab, nd = net["h"], net["vocab"], len(net["durations"])
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    joint = telmo_amd.PackedWeights.from_parts(tk, vocab + nd, h, P, *net["joint"])
+    lstm = [telmo_amd.PackedWeights.from_parts(tk, 4 * h, 2 * h, P, *w) for w in net["lstm"]]
+    proj = telmo_amd.PackedWeights.from_parts(tk, h, h, P, *net["proj"])
+    durations = net["durations"] if durations is None else durations
+    return telmo_amd.TdtDecoder(tk, h, vocab, durations, net["max_symbols"], joint, dev(net["joint_b"]),
+                                dev(net["emb"]), lstm, [dev(b) for b in net["lstm_b"]], proj, dev(net["proj_b"]))
+
+
+@pytest.mark.parametrize("p,rows", [(INT8_P, 1), (INT8_P, 4), (INT8_P, 16), (Q8_0_P, 1), (Q8_0_P, 16)])
+def test_predict_rows_matches_the_oracle(tk, orc, p, rows):
+    import torch
+
+    rng = np.random.default_rng(100 + rows + p)
+    net = tdt_network(rng, 640, 1025, [0, 1, 2, 3, 4], layers=2, precision=p)
+    dec = upload(tk, net)
+    assert dec.max_rows() == 16
+    tokens = rng.integers(0, 1025, size=rows)
+    states = (0.5 * rng.standard_normal((rows, 2 * 2 * 640))).astype(np.float32)
+    preds = np.zeros((rows, 640), np.float32)
+    say("predict", p, rows)
+    sd, pd = torch.from_numpy(states.copy()).cuda(), torch.zeros((rows, 640), device="cuda")
+    dec.predict_rows(list(tokens), sd, pd)
+    tk.synchronize()
+    orc.tdt_predict(net, tokens, states, preds)
+    assert np.max(np.abs(sd.cpu().numpy() - states)) <= TOL
+    assert rel_norm_err(pd.cpu().numpy(), preds) <= TOL
+    dec.close()
+
+
+DECODE_CASES = [  # h, vocab, durations, layers, precision, frames, blank_bias, max_symbols
+    (64, 100, [0, 1, 2, 3, 4], 2, INT8_P, 60, 3.0, 10),
+    (64, 100, [0, 1, 2, 3, 4], 2, INT8_P, 200, 6.0, 3),
+    (128, 300, [0, 2, 4], 1, INT8_P, 77, 4.0, 2),
+    (64, 100, [1, 2], 3, Q8_0_P, 50, 2.0, 5),
+    (640, 8193, [0, 1, 2, 3, 4], 2, INT8_P, 120, 6.0, 10),
+    (640, 8193, [0, 1, 2, 3, 4], 2, Q8_0_P, 60, 6.0, 10),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES)
+def test_decode_matches_the_oracle(tk, orc, case):
+    import torch
+
+    h, vocab, durs, layers, p, frames, blank_bias, ms = case
+    rng = np.random.default_rng(frames + h + layers)
+    net = tdt_network(rng, h, vocab, durs, layers=layers, precision=p, max_symbols=ms, blank_bias=blank_bias)
+    dec = upload(tk, net)
+    enc = rng.standard_normal((frames, h)).astype(np.float32)
+    state = (0.3 * rng.standard_normal(layers * 2 * h)).astype(np.float32)
+    pred = (0.3 * rng.standard_normal(h)).astype(np.float32)
+    sd, pdv = torch.from_numpy(state.copy()).cuda(), torch.from_numpy(pred.copy()).cuda()
+    say("decode", case)
+    toks, frame, on = dec.decode(torch.from_numpy(enc).cuda(), sd, pdv)
+    want, wframe, won = orc.tdt_decode(net, enc, state, pred)
+    assert [tuple(t) for t in toks] == want
+    assert (frame, on) == (wframe, won)
+    assert np.max(np.abs(sd.cpu().numpy() - state)) <= TOL
+    assert rel_norm_err(pdv.cpu().numpy()[None], pred[None]) <= TOL
+    dec.close()
+
+
+def test_decode_known_answers(tk, orc):
+    """Zero joints, so the logits are the bias: blank runs, duration-0 tokens up to max_symbols, a
+    start part-way through a frame, ties and a NaN first logit, as the oracle's pinned cases."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    base = tdt_network(rng, 32, 20, [0, 1, 2, 3, 4], layers=2, max_symbols=3)
+    enc = torch.from_numpy(rng.standard_normal((23, 32)).astype(np.float32)).cuda()
+
+    def run(bias, frames, frame=0, on_frame=0):
+        net = dict(base)
+        net["joint"] = (np.zeros_like(base["joint"][0]), base["joint"][1])
+        net["joint_b"] = np.asarray(bias, np.float32)
+        dec = upload(tk, net)
+        state = torch.zeros(2 * 2 * 32, device="cuda")
+        pred = torch.zeros(32, device="cuda")
+        out = dec.decode(enc[:frames], state, pred, frame, on_frame)
+        dec.close()
+        return out
+
+    def bias(token, d):
+        b = np.zeros(25, np.float32)
+        b[token] = 5.0
+        b[20 + d] = 5.0
+        return b
+
+    say("decode known answers")
+    assert run(bias(19, 3), 23) == ([], 24, 0)
+    assert run(bias(19, 0), 23) == ([], 23, 0)
+    assert [tuple(t) for t in run(bias(7, 0), 6)[0]] == [(7, t, 0) for t in range(6) for _ in range(3)]
+    assert [tuple(t) for t in run(bias(11, 2), 9)[0]] == [(11, t, 2) for t in range(0, 9, 2)]
+    toks, frame, on = run(bias(4, 0), 3, frame=1, on_frame=2)
+    assert [tuple(t) for t in toks] == [(4, 1, 0), (4, 2, 0), (4, 2, 0), (4, 2, 0)] and (frame, on) == (3, 0)
+    b = bias(9, 2)
+    b[6] = b[9]
+    b[24] = b[22]
+    assert [tuple(t) for t in run(b, 4)[0]] == [(6, 0, 2), (6, 2, 2)]
+    b = bias(9, 1)
+    b[0] = np.nan
+    assert [tuple(t) for t in run(b, 2)[0]] == [(0, 0, 1), (0, 1, 1)]
+    assert run(bias(7, 0), 5, frame=5, on_frame=1) == ([], 5, 1)
+
+
+def test_decode_refusals(tk):
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(8)
+    net = tdt_network(rng, 32, 20, [0, 1, 2], layers=1, max_symbols=2)
+    with pytest.raises(telmo_amd.TelmoError):  # the joint has 23 outputs, 20 tokens + 2 durations need 22
+        upload(tk, net, durations=[0, 1])
+    with pytest.raises(telmo_amd.TelmoError):  # a negative duration
+        upload(tk, net, durations=[0, -1, 2])
+    dec = upload(tk, net)
+    with pytest.raises(telmo_amd.TelmoError):
+        dec.predict_rows([20], torch.zeros((1, 64), device="cuda"), torch.zeros((1, 32), device="cuda"))
+    with pytest.raises(telmo_amd.TelmoError):
+        dec.predict_rows([0] * 17, torch.zeros((17, 64), device="cuda"), torch.zeros((17, 32), device="cuda"))
+    b = np.zeros(23, np.float32)
+    b[5] = b[20] = 5.0  # token 5, duration 0: two tokens per frame
+    net2 = dict(net)
+    net2["joint"] = (np.zeros_like(net["joint"][0]), net["joint"][1])
+    net2["joint_b"] = b
+    dec2 = upload(tk, net2)
+    enc = torch.zeros((4, 32), device="cuda")
+    with pytest.raises(telmo_amd.TelmoError):  # 8 tokens, room for 3
+        dec2.decode(enc, torch.zeros(64, device="cuda"), torch.zeros(32, device="cuda"), cap=3)
+    dec.close()
+    dec2.close()
