@@ -568,6 +568,101 @@ def cpu_leg(weights, x0_host, budget_s):
                             "encoder audio-seconds per second, GEMMs only, scaled from the sample"}
 
 
+
+# The TDT decoder of Parakeet: h = 640, vocab 8193 (blank last) + 5 durations, 2 LSTM layers.
+TDT_H, TDT_VOCAB, TDT_DURS, TDT_MAX_SYMBOLS = 640, 8193, [0, 1, 2, 3, 4], 10
+TDT_BLANK_BIAS = 28.0  # on random weights: blank runs between tokens
+
+
+def _panels(q, s):
+    n, k = q.shape
+    panels = -(-n // 16)
+    pad = np.zeros((panels * 16, k), np.int8)
+    pad[:n] = q
+    values = pad.reshape(panels, 16, k).transpose(0, 2, 1).reshape(-1).view(np.uint8).copy()
+    scales = np.zeros(panels * 16, np.float32)
+    scales[:n] = s
+    return values, scales
+
+
+def tdt_network(seed=21):
+    """Random int8 network of Parakeet's decoder shapes in the panel layout (numpy)."""
+    rng = np.random.default_rng(seed)
+    h, vocab = TDT_H, TDT_VOCAB
+
+    def mat(n, k, lo, hi):
+        q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+        return _panels(q, (lo + (hi - lo) * rng.random(n)).astype(np.float32))
+
+    outputs = vocab + len(TDT_DURS)
+    joint_b = (0.5 * rng.standard_normal(outputs)).astype(np.float32)
+    joint_b[vocab - 1] += TDT_BLANK_BIAS
+    return {"p": 3, "h": h, "vocab": vocab, "durations": TDT_DURS, "max_symbols": TDT_MAX_SYMBOLS,
+            "joint": mat(outputs, h, 0.001, 0.01), "joint_b": joint_b,
+            "emb": (0.5 * rng.standard_normal((vocab, h))).astype(np.float32),
+            "lstm": [mat(4 * h, 2 * h, 0.0004, 0.0008) for _ in range(2)],
+            "lstm_b": [(0.1 * rng.standard_normal(4 * h)).astype(np.float32) for _ in range(2)],
+            "proj": mat(h, h, 0.001, 0.003), "proj_b": (0.1 * rng.standard_normal(h)).astype(np.float32)}
+
+
+def tdt_leg(args, net, enc_host):
+    """The greedy TDT decode of 60 s of audio (750 encoder frames) on the device, from the start
+    state (the blank through the prediction network), through tg_tdt_decode_device: one call, every
+    step on the GPU, the host waking once per batch of steps. Reported per decode (median of 5)."""
+    import torch
+
+    import telmo_amd
+
+    kern = telmo_amd.Kernels(0)
+    h, vocab = net["h"], net["vocab"]
+    P = telmo_amd.Precision.INT8
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    joint = telmo_amd.PackedWeights.from_parts(kern, vocab + len(TDT_DURS), h, P, *net["joint"])
+    lstm = [telmo_amd.PackedWeights.from_parts(kern, 4 * h, 2 * h, P, *w) for w in net["lstm"]]
+    proj = telmo_amd.PackedWeights.from_parts(kern, h, h, P, *net["proj"])
+    dec = telmo_amd.TdtDecoder(kern, h, vocab, TDT_DURS, TDT_MAX_SYMBOLS, joint, dev(net["joint_b"]),
+                               dev(net["emb"]), lstm, [dev(b) for b in net["lstm_b"]], proj, dev(net["proj_b"]))
+    enc = dev(enc_host)
+    state0 = torch.zeros(2 * 2 * h, device="cuda")
+    pred0 = torch.zeros(h, device="cuda")
+    dec.predict_rows([vocab - 1], state0.view(1, -1), pred0.view(1, -1))
+    kern.synchronize()
+    times, toks = [], None
+    for _ in range(6):
+        state, pred = state0.clone(), pred0.clone()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks, frame, _ = dec.decode(enc, state, pred)
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times[1:])) * 1e3
+    frames = enc_host.shape[0]
+    weight_bytes = joint.bytes() + sum(w.bytes() for w in lstm) + proj.bytes()
+    out = {"workload": f"greedy TDT decode, {frames} frames (60 s audio), h={h}, vocab {vocab} + "
+                       f"{len(TDT_DURS)} durations, 2 LSTM layers, int8",
+           "frames": frames, "tokens": len(toks), "tokens_per_frame": round(len(toks) / frames, 3),
+           "ms_per_decode": round(ms, 3), "us_per_token": round(ms * 1e3 / max(len(toks), 1), 2),
+           "audio_s_per_s": round(60.0 / (ms * 1e-3), 1), "decoder_weight_mb": round(weight_bytes / 1e6, 2),
+           "timing": "wall clock around tg_tdt_decode_device (blocks until the decode ends), median of 5"}
+    dec.close()
+    kern.close()
+    return out, toks
+
+
+def cpu_tdt(net, enc_host, frames):
+    """The oracle's decode_inner (plain C, one core) on the first frames of the same decode."""
+    from oracle import oracle as orc
+
+    state = np.zeros(2 * 2 * TDT_H, np.float32)
+    pred = np.zeros(TDT_H, np.float32)
+    orc.tdt_predict(net, [TDT_VOCAB - 1], state.reshape(1, -1), pred.reshape(1, -1))
+    t0 = time.perf_counter()
+    toks, _, _ = orc.tdt_decode(net, enc_host[:frames], state, pred)
+    dt = time.perf_counter() - t0
+    return {"ms_per_token": round(dt * 1e3 / max(len(toks), 1), 3), "cores": 1, "kind": "port",
+            "sample": f"the oracle's decode (scalar C, integer products) over the first {frames} frames: "
+                      f"{len(toks)} tokens in {dt:.2f} s"}, toks
+
+
 def load_traffic():
     path = os.path.join(ROOT, "profiles", "gemm_i8_traffic.json")
     if not os.path.exists(path):
@@ -587,6 +682,7 @@ def main():
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-encoder", action="store_true")
     ap.add_argument("--no-q8", action="store_true")
+    ap.add_argument("--no-tdt", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU and has no multi-GPU path: run it with --gpus 1")
@@ -612,7 +708,16 @@ def main():
     host = host_leg(weights, x0)
     encoder = None if args.no_encoder else encoder_leg(args)
     q8 = None if args.no_q8 else q8_leg(args)
+    tdt = None
+    if not args.no_tdt:
+        net = tdt_network()
+        enc = np.random.default_rng(22).standard_normal((T_FRAMES, TDT_H)).astype(np.float32)
+        tdt, gpu_toks = tdt_leg(args, net, enc)
     cpu = None if args.no_cpu else cpu_leg(weights, x0, args.cpu_seconds)
+    if cpu is not None and tdt is not None:
+        cpu["tdt_decode"], cpu_toks = cpu_tdt(net, enc, 150)
+        # the sample's tokens are the first tokens of the GPU decode
+        tdt["cpu_sample_tokens_match"] = [tuple(t) for t in gpu_toks[:len(cpu_toks)]] == cpu_toks
     value = ops / (graph_ms * 1e-3) / 1e12
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
@@ -629,6 +734,7 @@ def main():
         "pcie_inclusive": host,
         "encoder": encoder,
         "q8_0": q8,
+        "tdt": tdt,
     }
     print(json.dumps(line))
 

@@ -172,8 +172,10 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, s
 
 /* ---- the TDT decoder (src/parakeet.rs:1412-1577) --------------------------------------------
  * Parakeet's prediction network (embedding, LSTM layers, projection) and joint, decoded greedily
- * with every step on the device. The matrices are tg_weights of int8 or Q8_0 values; the handles,
- * biases and embedding stay the caller's and must outlive the network. */
+ * with every step on the device. The matrices are tg_weights of int8 or Q8_0 values. The network
+ * keeps its own copies of the LSTM matrices and biases (rows interleaved so a unit's four gates meet
+ * in one output quad); the joint, projection, their biases and the embedding stay the caller's and
+ * must outlive the network. */
 typedef struct tg_tdt tg_tdt;
 typedef struct {
     size_t hidden;                 /* pred_hidden h: a multiple of 4, at most 992 */

@@ -41,19 +41,29 @@ struct tg_weights {
     int device;
 };
 
-// A TDT prediction network and joint on the device (the weights stay the caller's), with the
-// buffers of its decode steps.
+// A TDT prediction network and joint on the device (the joint, projection, biases and embedding
+// stay the caller's), with the interleaved LSTM copies and the buffers of its decode steps.
 struct tg_tdt {
     tg::TdtNet net;
     int device = 0;
-    tg::TdtCtl *ctl = nullptr;          // device control block
-    tg::TdtCtl *ctl_host = nullptr;     // pinned copy
-    int32_t *durations = nullptr;       // device
-    float *logits = nullptr, *gates = nullptr;
+    tg::DeviceWeights lstm[tg::TDT_MAX_LAYERS];  // interleaved copies (owned values and scales)
+    float *lstm_b[tg::TDT_MAX_LAYERS] = {};       // interleaved biases (owned)
+    tg::TdtCtl *ctl = nullptr;                    // device control block
+    tg::TdtCtl *ctl_host = nullptr;               // pinned copy
+    int32_t *durations = nullptr;                 // device
+    float *extras = nullptr;                      // the joint's first and duration logits per row
+    float *scratch = nullptr;                     // TDT_ROWS states: the other buffer of a prediction
     void *partials = nullptr;
-    int32_t *tokens = nullptr;          // device, 3 int32 per token
-    size_t tokens_cap = 0;              // tokens the buffer holds
+    int32_t *tokens = nullptr;                    // device, 3 int32 per token
+    size_t tokens_cap = 0;                        // tokens the buffer holds
+    // TDT_GRAPH_STEPS steps captured as one graph for the arguments in key (enc_proj, lde, frames,
+    // state, pred, token buffer, its capacity), replayed until the decode ends.
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uintptr_t key[7] = {};
 };
+
+constexpr int TDT_GRAPH_STEPS = 16;
 
 namespace {
 
@@ -487,13 +497,26 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, s
 
 namespace {
 
+void tdt_drop_graph(tg_tdt *t) {
+    if (t->exec) (void)hipGraphExecDestroy(t->exec);
+    if (t->graph) (void)hipGraphDestroy(t->graph);
+    t->exec = nullptr;
+    t->graph = nullptr;
+}
+
 void tdt_release(tg_tdt *t) {
     if (!t) return;
+    tdt_drop_graph(t);
+    for (int l = 0; l < tg::TDT_MAX_LAYERS; l++) {
+        if (t->lstm[l].values) (void)hipFree(t->lstm[l].values);
+        if (t->lstm[l].scales) (void)hipFree(t->lstm[l].scales);
+        if (t->lstm_b[l]) (void)hipFree(t->lstm_b[l]);
+    }
     if (t->ctl) (void)hipFree(t->ctl);
     if (t->ctl_host) (void)hipHostFree(t->ctl_host);
     if (t->durations) (void)hipFree(t->durations);
-    if (t->logits) (void)hipFree(t->logits);
-    if (t->gates) (void)hipFree(t->gates);
+    if (t->extras) (void)hipFree(t->extras);
+    if (t->scratch) (void)hipFree(t->scratch);
     if (t->partials) (void)hipFree(t->partials);
     if (t->tokens) (void)hipFree(t->tokens);
     delete t;
@@ -556,20 +579,35 @@ int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out) {
     net.joint_b = desc->joint_bias;
     net.proj_b = desc->proj_bias;
     net.emb = desc->embedding;
-    for (size_t l = 0; l < layers; l++) {
-        net.lstm[l] = &desc->lstm[l]->d;
-        net.lstm_b[l] = desc->lstm_bias[l];
-    }
-    const size_t outputs = vocab + ndur;
     bool ok = hipMalloc(&t->ctl, sizeof(tg::TdtCtl)) == hipSuccess &&
               hipHostMalloc(&t->ctl_host, sizeof(tg::TdtCtl), hipHostMallocDefault) == hipSuccess &&
               hipMalloc(&t->durations, ndur * sizeof(int32_t)) == hipSuccess &&
-              hipMalloc(&t->logits, (size_t)tg::TDT_ROWS * outputs * sizeof(float)) == hipSuccess &&
-              hipMalloc(&t->gates, (size_t)tg::TDT_ROWS * 4 * h * sizeof(float)) == hipSuccess &&
+              hipMalloc(&t->extras, tg::tdt_extras_bytes()) == hipSuccess &&
+              hipMalloc(&t->scratch, (size_t)tg::TDT_ROWS * layers * 2 * h * sizeof(float)) == hipSuccess &&
               hipMalloc(&t->partials, tg::tdt_partials_bytes()) == hipSuccess;
+    for (size_t l = 0; ok && l < layers; l++) {
+        const tg::DeviceWeights &src = desc->lstm[l]->d;
+        tg::DeviceWeights &dst = t->lstm[l];
+        dst = src;
+        dst.values = nullptr;
+        dst.scales = nullptr;
+        ok = hipMalloc(&dst.values, src.values_bytes) == hipSuccess &&
+             hipMalloc(&dst.scales, src.n_scales * sizeof(float)) == hipSuccess &&
+             hipMalloc(&t->lstm_b[l], 4 * h * sizeof(float)) == hipSuccess;
+    }
     if (!ok) {
         tdt_release(t);
         return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+    }
+    for (size_t l = 0; l < layers; l++) {
+        net.lstm[l] = &t->lstm[l];
+        net.lstm_b[l] = t->lstm_b[l];
+        const hipError_t e = tg::launch_tdt_interleave(desc->lstm[l]->d, desc->lstm_bias[l], t->lstm[l],
+                                                       t->lstm_b[l], h, ctx->stream);
+        if (e != hipSuccess) {
+            tdt_release(t);
+            return hip_fail(ctx, e, "tg_tdt_create");
+        }
     }
     net.durations = t->durations;
     std::memset(t->ctl_host, 0, sizeof(tg::TdtCtl));
@@ -609,7 +647,11 @@ int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_
     }
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
-    TG_HIP(ctx, tg::launch_tdt_predict(tdt->ctl, 0, toks, rows, tdt->net, states, preds, tdt->gates, 0, ctx->stream));
+    // The new states go to the scratch rows (other workgroups still read the old ones), then back.
+    TG_HIP(ctx, tg::launch_tdt_predict(tdt->ctl, toks, rows, tdt->net, states, tdt->scratch, preds, ctx->stream));
+    const size_t width = tdt->net.layers * 2 * tdt->net.h;
+    TG_HIP(ctx, hipMemcpyAsync(states, tdt->scratch, rows * width * sizeof(float), hipMemcpyDeviceToDevice,
+                               ctx->stream));
     return TG_OK;
 }
 
@@ -650,22 +692,44 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
     std::memset(hc, 0, sizeof(*hc));
     hc->t = (int32_t)*frame;
     hc->on_frame = (int32_t)*on_frame;
+    hc->rows = tg::TDT_ROWS;
     TG_HIP(ctx, hipMemcpyAsync(tdt->ctl, hc, sizeof(*hc), hipMemcpyHostToDevice, ctx->stream));
-    // Steps are queued in batches; a step after the end returns at once. Every step emits a token
+    // Steps run as a captured graph of TDT_GRAPH_STEPS steps, replayed in growing batches between
+    // looks at the control block; a step after the end returns at once. Every step emits a token
     // or moves at least one frame, so (frames - frame) (per_frame + 1) steps always suffice.
+    const uintptr_t key[7] = {reinterpret_cast<uintptr_t>(enc_proj), lde, frames, reinterpret_cast<uintptr_t>(state),
+                              reinterpret_cast<uintptr_t>(pred), reinterpret_cast<uintptr_t>(tdt->tokens), most};
+    if (!tdt->exec || std::memcmp(key, tdt->key, sizeof(key)) != 0) {
+        tdt_drop_graph(tdt);
+        TG_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        hipError_t e = hipSuccess;
+        for (int i = 0; i < TDT_GRAPH_STEPS && e == hipSuccess; i++)
+            e = tg::launch_tdt_step(tdt->ctl, net, enc_proj, lde, (int)frames, state, tdt->scratch, pred,
+                                    tdt->partials, tdt->extras, tdt->tokens, (int)most, ctx->stream);
+        hipGraph_t g = nullptr;
+        const hipError_t e2 = hipStreamEndCapture(ctx->stream, &g);
+        if (e != hipSuccess || e2 != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return hip_fail(ctx, e != hipSuccess ? e : e2, "capturing the decode step");
+        }
+        tdt->graph = g;
+        TG_HIP(ctx, hipGraphInstantiate(&tdt->exec, g, nullptr, nullptr, 0));
+        std::memcpy(tdt->key, key, sizeof(key));
+    }
     const size_t limit = (frames - *frame) * (per_frame + 1) + 1;
-    size_t steps = 0, batch = 4;
+    size_t steps = 0, graphs = 1;
     while (true) {
-        for (size_t i = 0; i < batch; i++)
-            TG_HIP(ctx, tg::launch_tdt_step(tdt->ctl, net, enc_proj, lde, (int)frames, state, pred, tdt->logits,
-                                           tdt->gates, tdt->partials, tdt->tokens, (int)most, ctx->stream));
-        steps += batch;
+        for (size_t i = 0; i < graphs; i++) TG_HIP(ctx, hipGraphLaunch(tdt->exec, ctx->stream));
+        steps += graphs * TDT_GRAPH_STEPS;
         TG_HIP(ctx, hipMemcpyAsync(hc, tdt->ctl, sizeof(*hc), hipMemcpyDeviceToHost, ctx->stream));
         TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (hc->done) break;
         if (steps > limit) return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
-        batch = batch < 64 ? batch * 2 : 64;
+        graphs = graphs < 8 ? graphs * 2 : 8;
     }
+    if (hc->cur)  // the last prediction left the state in the scratch buffer
+        TG_HIP(ctx, hipMemcpyAsync(state, tdt->scratch, net.layers * 2 * net.h * sizeof(float),
+                                   hipMemcpyDeviceToDevice, ctx->stream));
     const size_t n = (size_t)hc->ntok;
     *frame = (size_t)hc->t;
     *on_frame = (size_t)hc->on_frame;

@@ -2,19 +2,26 @@
 // joint, both argmaxes, the blank / duration bookkeeping, the prediction network's LSTM layers and
 // its projection run as one chain of kernels per step, with no host round trip per token.
 //
-// Each kernel is the MFMA GEMV of gemv_core.hpp with its own input rows and outputs, followed by a
-// finisher: the last workgroup to arrive (an atomic count, nothing waits) does the step's serial
-// part (argmax, cell update, bookkeeping). A kernel whose step has nothing to do returns at once.
+// Each kernel is the MFMA GEMV of gemv_core.hpp with its own input rows and outputs. No kernel
+// waits for, or counts, the workgroups of its own grid: what a step decides is computed from one
+// kernel's outputs by the next kernel, after the boundary between them has made them visible.
 //
-// * tdt_joint_kernel scores TDT_ROWS consecutive frames t, t + 1, ... against the same prediction
-//   in one GEMV (z = relu(enc_proj[f] + pred), the joint's bias): a row's logits do not depend on
-//   the other rows, so this equals TDT_ROWS separate joints while the prediction is unchanged. The
-//   finisher then walks the frames as the reference's loop does (blank: skip max(duration, 1)
-//   frames; a token: record it, hand it to the prediction network, move by its duration) until a
-//   token is emitted, the window is used up or the frames end.
-// * tdt_lstm_kernel runs layer l: gates = W_l [x; h_l] + b_l (x the token's embedding for l = 0,
-//   the new h_{l-1} otherwise); its finisher applies the cell update to every row.
-// * tdt_proj_kernel writes pred = W_p h_last + b_p and closes the step.
+// * tdt_joint_kernel scores a window of up to TDT_ROWS consecutive frames t, t + 1, ... against
+//   the same prediction in one GEMV (z = relu(enc_proj[f] + pred), the joint's bias): a row's logits
+//   do not depend on the other rows, so this equals that many separate joints while the prediction
+//   is unchanged. Each workgroup leaves, per row, the best vocabulary entry of its panels; the
+//   first and the duration logits are kept as well. Workgroup 0 snapshots the control block.
+// * tdt_lstm_kernel, layer 0 of the decode, first decides the step in every workgroup alike from
+//   the joint's partials and the snapshot: the rows' tokens and durations, then the frames walked as
+//   the reference's loop does (blank: skip max(duration, 1) frames; a token: record it, hand it to
+//   the prediction network, move by its duration) until a token is emitted, the window is used up
+//   or the frames end. Workgroup 0 publishes the outcome. The window shrinks after a token (tokens
+//   come close together) and grows back over blanks.
+// * tdt_lstm_kernel runs layer l on weights whose rows are interleaved at set-up (output 4 u + q is
+//   gate q of unit u), so the four gates of a unit land in four adjacent lanes of one MFMA output
+//   and the cell update happens in the epilogue. The state is read from one buffer and written to
+//   the other (the decode flips between them), so no workgroup reads a state another has replaced.
+// * tdt_proj_kernel writes pred = W_p h_last + b_p.
 #include "gemv_core.hpp"
 
 namespace tg {
@@ -25,6 +32,8 @@ using gemv::v4f;
 
 constexpr int TDT_WAVES = 4;
 constexpr int TDT_THREADS = TDT_WAVES * 64;
+constexpr int TDT_MAX_GRID = 1024;  // workgroups of a persistent GEMV grid
+constexpr int TDT_EXTRA = 1 + TDT_MAX_DURATIONS;  // per joint row: the first logit, the duration logits
 
 struct Best {
     float v;
@@ -44,24 +53,6 @@ __device__ __forceinline__ int load_i(const int32_t *p) {
 }
 __device__ __forceinline__ void store_i(int32_t *p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// True in every thread of the last workgroup of the grid to get here. Each wavefront's stores are
-// released before the count, and the last workgroup acquires everything the others released. The
-// count is reset for the next launch.
-__device__ __forceinline__ bool last_to_arrive(uint32_t *count, int *flag) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = prev == gridDim.x - 1;
-        if (last) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = last;
-    }
-    __syncthreads();
-    const bool last = *flag != 0;
-    if (last) __threadfence();
-    return last;
 }
 
 // Joint input row r: relu(enc_proj[min(t + r, frames - 1)] + pred), as (e + p).max(0.0).
@@ -84,36 +75,70 @@ struct JointIn {
     }
 };
 
-// Joint outputs: the logits, and per lane the best vocabulary entry of its four rows so far.
+// Joint outputs: per lane the best vocabulary entry of its four rows so far; the first logit and the
+// duration logits of each row go to extras (row r at r * TDT_EXTRA: first, then the durations).
 struct JointOut {
-    float *logits;
-    int outputs, vocab;
+    float *extras;
+    int vocab;
     float bv[4];
     int bi[4];
     __device__ __forceinline__ void store(int r, int col, float v) {
-        logits[(size_t)r * outputs + col] = v;
-        if (col < vocab && before(v, col, bv[r & 3], bi[r & 3])) {
-            bv[r & 3] = v;
-            bi[r & 3] = col;
+        if (col < vocab) {
+            if (before(v, col, bv[r & 3], bi[r & 3])) {
+                bv[r & 3] = v;
+                bi[r & 3] = col;
+            }
+            if (col == 0) extras[r * TDT_EXTRA] = v;
+        } else {
+            extras[r * TDT_EXTRA + 1 + (col - vocab)] = v;
         }
     }
 };
 
-// LSTM layer l input row r: [x; h_l] with x = embedding[tok[r]] (l = 0) or the new h_{l-1}. The
-// tokens sit in LDS (a register array indexed by row would live in scratch memory).
+// LSTM layer l input row r: [x; h_l] with x = embedding[tok[r]] (l = 0) or the new h_{l-1} (from
+// the output state). The tokens sit in LDS (a register array indexed by row would live in scratch
+// memory).
 struct LstmIn {
     const float *emb;
-    const float *states;
+    const float *s_in, *s_out;
     size_t width;
     int h, l;
     const int *tok;
     __device__ __forceinline__ v4f load(int r, int i0, int m, int k) const {
         const bool ok = r < m && i0 < k;
         const int rr = ok ? r : 0;
-        const float *row = states + (size_t)rr * width;
-        const float *src = i0 < h ? (l == 0 ? emb + (size_t)tok[rr] * h + i0 : row + (size_t)(l - 1) * 2 * h + i0)
-                                  : row + (size_t)l * 2 * h + (i0 - h);
+        const size_t row = (size_t)rr * width;
+        const float *src = i0 < h ? (l == 0 ? emb + (size_t)tok[rr] * h + i0 : s_out + row + (size_t)(l - 1) * 2 * h + i0)
+                                  : s_in + row + (size_t)l * 2 * h + (i0 - h);
         return *reinterpret_cast<const v4f *>(ok ? src : gemv::ZERO_CHUNK);
+    }
+};
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(0.0f - x)); }
+
+// The value of quad lane Q (0..3) in every lane of the quad (DPP quad_perm [Q, Q, Q, Q]).
+template <int Q>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Q * 0x55, 0xF, 0xF, false));
+}
+
+// LSTM outputs on interleaved rows: output col = 4 u + q is gate q (i, f, g, o) of unit u. The four
+// lanes of a quad hold one unit's gates for the same row; lane q = 0 applies the cell update
+// (src/parakeet.rs:1549-1562): c = f c + i g, h = o tanh(c), each product rounded before the sum.
+struct LstmOut {
+    const float *s_in;
+    float *s_out;
+    size_t width;
+    int h, l;
+    __device__ __forceinline__ void store(int r, int col, float v) {
+        const float gi = quad_lane<0>(v), gf = quad_lane<1>(v), gg = quad_lane<2>(v), go = quad_lane<3>(v);
+        if ((col & 3) == 0) {
+            const size_t at = (size_t)r * width + (size_t)l * 2 * h + (col >> 2);
+            const float i = sigmoid(gi), f = sigmoid(gf), g = tanhf(gg), o = sigmoid(go);
+            const float c = f * s_in[at + h] + i * g;
+            s_out[at + h] = c;
+            s_out[at] = o * tanhf(c);
+        }
     }
 };
 
@@ -124,31 +149,48 @@ struct Weights {
     size_t panel_stride, blk_stride;
 };
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(0.0f - x)); }
-
 template <int KBC, int J, int Q8>
 __global__ __launch_bounds__(TDT_THREADS) void tdt_joint_kernel(TdtCtl *ctl, const float *__restrict__ enc, size_t lde,
                                                                 const float *__restrict__ pred, int frames, Weights w,
-                                                                const float *__restrict__ bias, float *logits,
-                                                                int vocab, int blank, const int32_t *durations,
-                                                                int ndur, int max_symbols, Best *partials,
-                                                                int32_t *tokens, int cap) {
+                                                                const float *__restrict__ bias, int vocab,
+                                                                Best *partials, float *extras) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];
     __shared__ uint32_t slot[TDT_WAVES * J];
     __shared__ Best red[TDT_WAVES][TDT_ROWS];
-    __shared__ int tok_s[TDT_ROWS], dur_s[TDT_ROWS], flag;
-    if (load_i(&ctl->done) || load_i(&ctl->active)) return;
-    const int t = load_i(&ctl->t);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    JointOut out{logits, w.n, vocab, {}, {}};
+    const bool lead = blockIdx.x == 0 && tid == 0;
+    if (load_i(&ctl->done)) {
+        if (lead) store_i(&ctl->snap.valid, 0);
+        return;
+    }
+    const int t = load_i(&ctl->t), rows = load_i(&ctl->rows);
+    if (t >= frames) {
+        // Only the last prediction's state flip is left: the decode ends here.
+        if (lead) {
+            if (load_i(&ctl->active)) store_i(&ctl->cur, load_i(&ctl->cur) ^ 1);
+            store_i(&ctl->active, 0);
+            store_i(&ctl->done, 1);
+            store_i(&ctl->snap.valid, 0);
+        }
+        return;
+    }
+    if (lead) {
+        store_i(&ctl->snap.t, t);
+        store_i(&ctl->snap.rows, rows);
+        store_i(&ctl->snap.on_frame, load_i(&ctl->on_frame));
+        store_i(&ctl->snap.ntok, load_i(&ctl->ntok));
+        store_i(&ctl->snap.active, load_i(&ctl->active));
+        store_i(&ctl->snap.cur, load_i(&ctl->cur));
+        store_i(&ctl->snap.valid, 1);
+    }
+    JointOut out{extras, vocab, {}, {}};
 #pragma unroll
     for (int v = 0; v < 4; v++) {
         out.bv[v] = __builtin_nanf("");
         out.bi[v] = INT32_MAX;
     }
-    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(JointIn{enc, lde, pred, t, frames}, out, TDT_ROWS, w.k, w.values, w.scales,
-                                           w.n, w.P, w.KB, w.NB, logits, (size_t)w.n, bias, ACT_NONE, 1.0f, 0,
+    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(JointIn{enc, lde, pred, t, frames}, out, rows, w.k, w.values, w.scales,
+                                           w.n, w.P, w.KB, w.NB, extras, 0, bias, ACT_NONE, 1.0f, 0,
                                            w.panel_stride, w.blk_stride, sqa, slot);
     // Lanes 16 g .. 16 g + 15 hold 16 columns of rows 4 g .. 4 g + 3: fold them, then the wavefronts.
 #pragma unroll
@@ -174,19 +216,48 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_joint_kernel(TdtCtl *ctl, con
             if (before(red[q][tid].v, red[q][tid].i, b.v, b.i)) b = red[q][tid];
         partials[(size_t)blockIdx.x * TDT_ROWS + tid] = b;
     }
-    if (!last_to_arrive(&ctl->arrive[0], &flag)) return;
+}
 
-    // Finisher. Row r's best over all workgroups: thread (r, s) takes workgroups s, s + 16, ...
+// What the decider of a step reads besides the control block.
+struct Decide {
+    const Best *partials;
+    const float *extras;
+    int joint_grid, vocab, blank, ndur, max_symbols, frames, cap;
+    const int32_t *durations;
+    int32_t *tokens;
+};
+
+// The step's decision, computed alike in every workgroup of the kernel after the joint (so it needs
+// no communication between them). Returns the token handed to the prediction network, or -1; the
+// state buffer to read is left in *cur. Workgroup 0 publishes the new control values.
+__device__ __forceinline__ int decide_step(TdtCtl *ctl, const Decide &d, int *cur) {
+    __shared__ int tok_s[TDT_ROWS], dur_s[TDT_ROWS], durs[TDT_MAX_DURATIONS], result;
+    __shared__ float dlog[TDT_ROWS][TDT_MAX_DURATIONS];
+    const int tid = threadIdx.x;
+    const int t = load_i(&ctl->snap.t), rows = load_i(&ctl->snap.rows);
+    *cur = load_i(&ctl->snap.cur) ^ load_i(&ctl->snap.active);  // the last prediction wrote the other buffer
+    if (tid < d.ndur) durs[tid] = d.durations[tid];
     {
-        const int r = tid >> 4, s = tid & 15;
+        // Thread (r, s) takes row r's partials of workgroups s, s + 16, ... (sixteen loads per round,
+        // one round up to 256 joint workgroups), with the row's first and duration logits.
+        const int r = tid >> 4, s = tid & 15, nb = d.joint_grid;
+        const float *ex = d.extras + (size_t)min(r, rows - 1) * TDT_EXTRA;
+        const float first = ex[0];
+        float dl[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) dl[q] = ex[1 + min(s + 16 * q, d.ndur - 1)];
         float bv = __builtin_nanf("");
         int bi = INT32_MAX;
-        for (int b = s; b < (int)gridDim.x; b += 16) {
-            const Best x = partials[(size_t)b * TDT_ROWS + r];
-            if (before(x.v, x.i, bv, bi)) {
-                bv = x.v;
-                bi = x.i;
-            }
+        for (int b0 = s; b0 < nb; b0 += 16 * 16) {
+            Best x[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) x[u] = d.partials[(size_t)min(b0 + 16 * u, nb - 1) * TDT_ROWS + r];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (b0 + 16 * u < nb && before(x[u].v, x[u].i, bv, bi)) {
+                    bv = x[u].v;
+                    bi = x[u].i;
+                }
         }
 #pragma unroll
         for (int off = 1; off < 16; off <<= 1) {
@@ -197,110 +268,138 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_joint_kernel(TdtCtl *ctl, con
                 bi = oi;
             }
         }
-        if (s == 0) {
-            const float *row = logits + (size_t)r * w.n;
-            // a NaN first entry is never beaten in the reference's scan
-            tok_s[r] = __builtin_isnan(row[0]) || bi == INT32_MAX ? 0 : bi;
-            int d = 0;
-            for (int i = 1; i < ndur; i++)
-                if (row[vocab + i] > row[vocab + d]) d = i;
-            dur_s[r] = durations[d];
-        }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (s + 16 * q < d.ndur) dlog[r][s + 16 * q] = dl[q];
+        if (s == 0) tok_s[r] = __builtin_isnan(first) || bi == INT32_MAX ? 0 : bi;  // a NaN first is never beaten
+    }
+    __syncthreads();
+    if (tid < TDT_ROWS) {
+        int k = 0;
+        for (int i = 1; i < d.ndur; i++)
+            if (dlog[tid][i] > dlog[tid][k]) k = i;
+        dur_s[tid] = durs[k];
     }
     __syncthreads();
     if (tid == 0) {
-        int tc = t, on = load_i(&ctl->on_frame), ntok = load_i(&ctl->ntok), active = 0, done = 0;
+        int tc = t, on = load_i(&ctl->snap.on_frame), ntok = load_i(&ctl->snap.ntok), token = -1, done = 0;
+        // The next window: after a token, twice the frames this one walked (at least 4); after a
+        // window of blanks, the most.
+        int next = TDT_ROWS;
         while (true) {
             const int r = tc - t;
-            if (r >= TDT_ROWS) break;  // the next window scores the frames from tc
-            const int token = tok_s[r], dur = dur_s[r];
-            if (token == blank) {
+            if (r >= rows) break;  // the next window scores the frames from tc
+            const int tok = tok_s[r], dur = dur_s[r];
+            if (tok == d.blank) {
                 tc += max(dur, 1);
                 on = 0;
-                if (tc >= frames) {
+                if (tc >= d.frames) {
                     done = 1;
                     break;
                 }
                 continue;
             }
-            if (ntok < cap) {
-                tokens[3 * ntok] = token;
-                tokens[3 * ntok + 1] = tc;
-                tokens[3 * ntok + 2] = dur;
+            if (blockIdx.x == 0 && ntok < d.cap) {
+                d.tokens[3 * ntok] = tok;
+                d.tokens[3 * ntok + 1] = tc;
+                d.tokens[3 * ntok + 2] = dur;
             }
             ntok++;
-            store_i(&ctl->tok[0], token);
-            active = 1;
+            token = tok;
+            next = min(TDT_ROWS, max(4, 2 * (r + 1)));
             if (dur > 0) {
                 tc += dur;
                 on = 0;
-            } else if (++on >= max_symbols) {
+            } else if (++on >= d.max_symbols) {
                 tc += 1;
                 on = 0;
             }
             break;
         }
-        store_i(&ctl->t, tc);
-        store_i(&ctl->on_frame, on);
-        store_i(&ctl->ntok, ntok);
-        store_i(&ctl->active, active);
-        store_i(&ctl->done, done);
+        if (blockIdx.x == 0) {
+            store_i(&ctl->t, tc);
+            store_i(&ctl->on_frame, on);
+            store_i(&ctl->ntok, ntok);
+            store_i(&ctl->rows, next);
+            store_i(&ctl->cur, *cur);
+            store_i(&ctl->active, token >= 0);
+            store_i(&ctl->done, done);
+        }
+        result = token;
     }
-}
-
-// The cell update of row r, unit j (src/parakeet.rs:1549-1562): i, f, o = sigmoid, g = tanh of the
-// gates, c = f c + i g, h = o tanh(c), each product rounded before the sum.
-__device__ __forceinline__ void cell_update(const float *gates, float *state, int h, int j) {
-    const float i = sigmoid(gates[j]), f = sigmoid(gates[h + j]), g = tanhf(gates[2 * h + j]),
-                o = sigmoid(gates[3 * h + j]);
-    const float c = f * state[h + j] + i * g;
-    state[h + j] = c;
-    state[j] = o * tanhf(c);
-}
-
-template <int KBC, int J, int Q8>
-__global__ __launch_bounds__(TDT_THREADS) void tdt_lstm_kernel(TdtCtl *ctl, int gated, TdtTokens toks, int m, int l,
-                                                               const float *__restrict__ emb, float *states,
-                                                               size_t width, Weights w,
-                                                               const float *__restrict__ bias, float *gates) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];
-    __shared__ uint32_t slot[TDT_WAVES * J];
-    __shared__ int tok_s[TDT_ROWS], flag;
-    if (gated && !load_i(&ctl->active)) return;
-    const int h = w.k / 2;
-    if (threadIdx.x < TDT_ROWS) tok_s[threadIdx.x] = gated ? load_i(&ctl->tok[threadIdx.x]) : toks.tok[threadIdx.x];
     __syncthreads();
-    LstmIn in{emb, states, width, h, l, tok_s};
-    gemv::StoreC out{gates, (size_t)w.n};
-    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(in, out, m, w.k, w.values, w.scales, w.n, w.P, w.KB, w.NB, gates,
-                                           (size_t)w.n, bias, ACT_NONE, 1.0f, 0, w.panel_stride, w.blk_stride, sqa,
-                                           slot);
-    if (!last_to_arrive(&ctl->arrive[1 + l], &flag)) return;
-    for (int x = threadIdx.x; x < m * h; x += TDT_THREADS) {
-        const int r = x / h, j = x - r * h;
-        cell_update(gates + (size_t)r * w.n, states + (size_t)r * width + (size_t)l * 2 * h, h, j);
+    return result;
+}
+
+// State buffers of a prediction: a (rows x width) is read and b written when cur is 0, the other
+// way round when it is 1. mode 0: a standalone prediction (cur 0, tokens by value); 1: a later layer
+// of the decode (runs when a token was handed on); 2: layer 0 of the decode, which decides the step.
+template <int KBC, int J, int Q8>
+__global__ __launch_bounds__(TDT_THREADS) void tdt_lstm_kernel(TdtCtl *ctl, int mode, TdtTokens toks, Decide dec,
+                                                               int m, int l, const float *__restrict__ emb,
+                                                               float *sa, float *sb, size_t width, Weights w,
+                                                               const float *__restrict__ bias) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];
+    __shared__ uint32_t slot[TDT_WAVES * J];
+    __shared__ int tok_s[TDT_ROWS];
+    int cur = 0;
+    if (mode == 2) {
+        if (!load_i(&ctl->snap.valid)) return;
+        const int token = decide_step(ctl, dec, &cur);
+        if (token < 0) return;
+        if (threadIdx.x == 0) tok_s[0] = token;
+    } else {
+        if (mode == 1) {
+            if (!load_i(&ctl->active)) return;
+            cur = load_i(&ctl->cur);
+        }
+        if (threadIdx.x < TDT_ROWS) tok_s[threadIdx.x] = toks.tok[threadIdx.x];
     }
+    __syncthreads();
+    float *s_in = cur ? sb : sa, *s_out = cur ? sa : sb;
+    const int h = w.k / 2;
+    LstmOut out{s_in, s_out, width, h, l};
+    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(LstmIn{emb, s_in, s_out, width, h, l, tok_s}, out, m, w.k, w.values,
+                                           w.scales, w.n, w.P, w.KB, w.NB, s_out, width, bias, ACT_NONE, 1.0f, 0,
+                                           w.panel_stride, w.blk_stride, sqa, slot);
 }
 
 template <int KBC, int J, int Q8>
-__global__ __launch_bounds__(TDT_THREADS) void tdt_proj_kernel(TdtCtl *ctl, int gated, int m, const float *states,
-                                                               size_t width, int layers, Weights w,
-                                                               const float *__restrict__ bias, float *preds,
-                                                               int frames) {
+__global__ __launch_bounds__(TDT_THREADS) void tdt_proj_kernel(TdtCtl *ctl, int gated, int m, const float *sa,
+                                                               const float *sb, size_t width, int layers, Weights w,
+                                                               const float *__restrict__ bias, float *preds) {
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];
     __shared__ uint32_t slot[TDT_WAVES * J];
-    __shared__ int flag;
     if (gated && !load_i(&ctl->active)) return;
+    const float *s_out = (gated && load_i(&ctl->cur)) ? sa : sb;
     const int h = w.k;
     gemv::StoreC out{preds, (size_t)h};
-    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(gemv::RowsIn{states + (size_t)(layers - 1) * 2 * h, width}, out, m, w.k,
+    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(gemv::RowsIn{s_out + (size_t)(layers - 1) * 2 * h, width}, out, m, w.k,
                                            w.values, w.scales, w.n, w.P, w.KB, w.NB, preds, (size_t)h, bias, ACT_NONE,
                                            1.0f, 0, w.panel_stride, w.blk_stride, sqa, slot);
-    if (!gated) return;
-    if (!last_to_arrive(&ctl->arrive[TDT_MAX_LAYERS + 1], &flag)) return;
-    if (threadIdx.x == 0) {
-        store_i(&ctl->active, 0);
-        if (load_i(&ctl->t) >= frames) store_i(&ctl->done, 1);
+}
+
+// Interleaves the rows of an LSTM matrix (4h outputs, gate-major: gate q of unit u at q h + u) so
+// that output 4 u + q is gate q of unit u: a gather of the 16-byte lane operands within each
+// k-block, and of the scales alike. One wavefront per (panel, k-block).
+__global__ __launch_bounds__(64) void tdt_interleave_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                            const float *__restrict__ ssrc, float *__restrict__ sdst,
+                                                            const float *__restrict__ bsrc, float *__restrict__ bdst,
+                                                            int h, int KB, int NB, int q8, size_t panel_stride,
+                                                            size_t blk_stride) {
+    const int p = blockIdx.x / KB, t = blockIdx.x % KB, lane = threadIdx.x, g = lane >> 4, j = lane & 15;
+    const int o = 16 * p + j, old = (o & 3) * h + (o >> 2), po = old >> 4, jo = old & 15;
+    const uint4 v = *reinterpret_cast<const uint4 *>(src + (size_t)po * panel_stride + (size_t)t * blk_stride +
+                                                     (size_t)(16 * g + jo) * 16);
+    *reinterpret_cast<uint4 *>(dst + (size_t)p * panel_stride + (size_t)t * blk_stride + (size_t)lane * 16) = v;
+    if (g == 0) {
+        if (q8) {
+            for (int b = t; b < NB; b += KB)
+                sdst[((size_t)p * NB + b) * PANEL + j] = ssrc[((size_t)po * NB + b) * PANEL + jo];
+        } else if (t == 0) {
+            sdst[o] = ssrc[old];
+        }
+        if (t == 0) bdst[o] = bsrc[old];
     }
 }
 
@@ -311,7 +410,7 @@ Weights weights_of(const DeviceWeights &d) {
 
 // Persistent grid as the plain MFMA GEMV sizes it: at most 1024 workgroups walking the panels.
 unsigned grid_of(const DeviceWeights &d) {
-    const size_t per_wave = div_ceil(d.panels, (size_t)TDT_WAVES * 1024);
+    const size_t per_wave = div_ceil(d.panels, (size_t)TDT_WAVES * TDT_MAX_GRID);
     return (unsigned)div_ceil(d.panels, (size_t)TDT_WAVES * per_wave);
 }
 
@@ -321,30 +420,27 @@ int j_of(size_t m, const DeviceWeights &d) {
     return j <= 2 ? 2 : j <= 4 ? 4 : j <= 8 ? 8 : j <= 12 ? 12 : j <= 16 ? 16 : 20;
 }
 
-#define TG_TDT_DISPATCH(KERNEL, J_, D, ...)                                                                        \
-    do {                                                                                                           \
-        const bool q8_ = (D).precision == Q8_0;                                                                    \
-        const size_t lds_ = (D).kb * 2048;                                                                         \
-        const dim3 g_(grid_of(D)), b_(TDT_THREADS);                                                                \
-        if ((D).kb <= 10) {                                                                                        \
-            switch (J_) {                                                                                          \
-            case 2: hipLaunchKernelGGL(q8_ ? (KERNEL<10, 2, 1>) : (KERNEL<10, 2, 0>), g_, b_, lds_, s, __VA_ARGS__); break;     \
-            case 4: hipLaunchKernelGGL(q8_ ? (KERNEL<10, 4, 1>) : (KERNEL<10, 4, 0>), g_, b_, lds_, s, __VA_ARGS__); break;     \
-            case 8: hipLaunchKernelGGL(q8_ ? (KERNEL<10, 8, 1>) : (KERNEL<10, 8, 0>), g_, b_, lds_, s, __VA_ARGS__); break;     \
-            case 12: hipLaunchKernelGGL(q8_ ? (KERNEL<10, 12, 1>) : (KERNEL<10, 12, 0>), g_, b_, lds_, s, __VA_ARGS__); break;  \
-            case 16: hipLaunchKernelGGL(q8_ ? (KERNEL<10, 16, 1>) : (KERNEL<10, 16, 0>), g_, b_, lds_, s, __VA_ARGS__); break;  \
-            default: hipLaunchKernelGGL(q8_ ? (KERNEL<10, 20, 1>) : (KERNEL<10, 20, 0>), g_, b_, lds_, s, __VA_ARGS__); break; \
-            }                                                                                                      \
-        } else {                                                                                                   \
-            switch (J_) {                                                                                          \
-            case 2: hipLaunchKernelGGL(q8_ ? (KERNEL<16, 2, 1>) : (KERNEL<16, 2, 0>), g_, b_, lds_, s, __VA_ARGS__); break;     \
-            case 4: hipLaunchKernelGGL(q8_ ? (KERNEL<16, 4, 1>) : (KERNEL<16, 4, 0>), g_, b_, lds_, s, __VA_ARGS__); break;     \
-            case 8: hipLaunchKernelGGL(q8_ ? (KERNEL<16, 8, 1>) : (KERNEL<16, 8, 0>), g_, b_, lds_, s, __VA_ARGS__); break;     \
-            case 12: hipLaunchKernelGGL(q8_ ? (KERNEL<16, 12, 1>) : (KERNEL<16, 12, 0>), g_, b_, lds_, s, __VA_ARGS__); break;  \
-            case 16: hipLaunchKernelGGL(q8_ ? (KERNEL<16, 16, 1>) : (KERNEL<16, 16, 0>), g_, b_, lds_, s, __VA_ARGS__); break;  \
-            default: hipLaunchKernelGGL(q8_ ? (KERNEL<16, 20, 1>) : (KERNEL<16, 20, 0>), g_, b_, lds_, s, __VA_ARGS__); break; \
-            }                                                                                                      \
-        }                                                                                                          \
+// The k-blocks fetched ahead: all of them up to 20 (one memory round trip for Parakeet's LSTM rows
+// of 1280 inputs), 16 per round beyond.
+#define TG_TDT_KBC(KERNEL, KBC, ...)                                                                          \
+    do {                                                                                                      \
+        if (jj_ == 2) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 2, 1>) : (KERNEL<KBC, 2, 0>), g_, b_, lds_, s, __VA_ARGS__);          \
+        else if (jj_ == 4) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 4, 1>) : (KERNEL<KBC, 4, 0>), g_, b_, lds_, s, __VA_ARGS__);     \
+        else if (jj_ == 8) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 8, 1>) : (KERNEL<KBC, 8, 0>), g_, b_, lds_, s, __VA_ARGS__);     \
+        else if (jj_ == 12) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 12, 1>) : (KERNEL<KBC, 12, 0>), g_, b_, lds_, s, __VA_ARGS__);  \
+        else if (jj_ == 16) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 16, 1>) : (KERNEL<KBC, 16, 0>), g_, b_, lds_, s, __VA_ARGS__);  \
+        else hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 20, 1>) : (KERNEL<KBC, 20, 0>), g_, b_, lds_, s, __VA_ARGS__);                 \
+    } while (0)
+
+#define TG_TDT_DISPATCH(KERNEL, JJ, D, ...)                              \
+    do {                                                                 \
+        const bool q8_ = (D).precision == Q8_0;                          \
+        const size_t lds_ = (D).kb * 2048;                               \
+        const dim3 g_(grid_of(D)), b_(TDT_THREADS);                      \
+        const int jj_ = (JJ);                                            \
+        if ((D).kb <= 10) TG_TDT_KBC(KERNEL, 10, __VA_ARGS__);           \
+        else if ((D).kb <= 20) TG_TDT_KBC(KERNEL, 20, __VA_ARGS__);      \
+        else TG_TDT_KBC(KERNEL, 16, __VA_ARGS__);                        \
     } while (0)
 
 }  // namespace
@@ -355,30 +451,51 @@ size_t tdt_max_rows(const DeviceWeights &lstm) {
     return rows < (size_t)TDT_ROWS ? rows : (size_t)TDT_ROWS;
 }
 
-size_t tdt_partials_bytes() { return (size_t)1024 * TDT_ROWS * sizeof(Best); }
+size_t tdt_partials_bytes() { return (size_t)TDT_MAX_GRID * TDT_ROWS * sizeof(Best); }
 
-hipError_t launch_tdt_predict(TdtCtl *ctl, int gated, const TdtTokens &toks, size_t m, const TdtNet &net,
-                              float *states, float *preds, float *gates, int frames, hipStream_t s) {
-    const size_t width = net.layers * 2 * net.h;
-    for (size_t l = 0; l < net.layers; l++) {
-        const DeviceWeights &d = *net.lstm[l];
-        TG_TDT_DISPATCH(tdt_lstm_kernel, j_of(m, d), d, ctl, gated, toks, (int)m, (int)l, net.emb, states, width,
-                        weights_of(d), net.lstm_b[l], gates);
-    }
-    const DeviceWeights &p = *net.proj;
-    TG_TDT_DISPATCH(tdt_proj_kernel, j_of(m, p), p, ctl, gated, (int)m, states, width, (int)net.layers, weights_of(p),
-                    net.proj_b, preds, frames);
+hipError_t launch_tdt_interleave(const DeviceWeights &src, const float *bias, const DeviceWeights &dst,
+                                 float *bias_dst, size_t h, hipStream_t s) {
+    hipLaunchKernelGGL(tdt_interleave_kernel, dim3((unsigned)(src.panels * src.kb)), dim3(64), 0, s, src.values,
+                       dst.values, src.scales, dst.scales, bias, bias_dst, (int)h, (int)src.kb,
+                       (int)(src.k / Q8_BLOCK), src.precision == Q8_0 ? 1 : 0, src.panel_stride, src.blk_stride);
     return hipGetLastError();
 }
 
-hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, size_t lde, int frames, float *states,
-                           float *pred, float *logits, float *gates, void *partials, int32_t *tokens, int cap,
+hipError_t launch_tdt_predict(TdtCtl *ctl, const TdtTokens &toks, size_t m, const TdtNet &net, float *sa, float *sb,
+                              float *preds, hipStream_t s) {
+    const size_t width = net.layers * 2 * net.h;
+    const Decide none{};
+    for (size_t l = 0; l < net.layers; l++) {
+        const DeviceWeights &d = *net.lstm[l];
+        TG_TDT_DISPATCH(tdt_lstm_kernel, j_of(m, d), d, ctl, 0, toks, none, (int)m, (int)l, net.emb, sa, sb, width,
+                        weights_of(d), net.lstm_b[l]);
+    }
+    const DeviceWeights &p = *net.proj;
+    TG_TDT_DISPATCH(tdt_proj_kernel, j_of(m, p), p, ctl, 0, (int)m, sa, sb, width, (int)net.layers, weights_of(p),
+                    net.proj_b, preds);
+    return hipGetLastError();
+}
+
+hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, size_t lde, int frames, float *sa,
+                           float *sb, float *pred, void *partials, float *extras, int32_t *tokens, int cap,
                            hipStream_t s) {
     const DeviceWeights &d = *net.joint;
     TG_TDT_DISPATCH(tdt_joint_kernel, j_of(TDT_ROWS, d), d, ctl, enc, lde, pred, frames, weights_of(d), net.joint_b,
-                    logits, (int)net.vocab, (int)net.blank, net.durations, (int)net.ndur, (int)net.max_symbols,
-                    static_cast<Best *>(partials), tokens, cap);
-    return launch_tdt_predict(ctl, 1, TdtTokens{}, 1, net, states, pred, gates, frames, s);
+                    (int)net.vocab, static_cast<Best *>(partials), extras);
+    const Decide dec{static_cast<const Best *>(partials), extras, (int)grid_of(d), (int)net.vocab, (int)net.blank,
+                     (int)net.ndur, (int)net.max_symbols, frames, cap, net.durations, tokens};
+    const size_t width = net.layers * 2 * net.h;
+    for (size_t l = 0; l < net.layers; l++) {
+        const DeviceWeights &w = *net.lstm[l];
+        TG_TDT_DISPATCH(tdt_lstm_kernel, j_of(1, w), w, ctl, l == 0 ? 2 : 1, TdtTokens{}, dec, 1, (int)l, net.emb, sa,
+                        sb, width, weights_of(w), net.lstm_b[l]);
+    }
+    const DeviceWeights &p = *net.proj;
+    TG_TDT_DISPATCH(tdt_proj_kernel, j_of(1, p), p, ctl, 1, 1, sa, sb, width, (int)net.layers, weights_of(p),
+                    net.proj_b, pred);
+    return hipGetLastError();
 }
+
+size_t tdt_extras_bytes() { return (size_t)TDT_ROWS * TDT_EXTRA * sizeof(float); }
 
 }  // namespace tg

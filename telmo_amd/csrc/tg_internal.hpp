@@ -197,18 +197,25 @@ hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeight
 
 // The greedy TDT decode (kernels_tdt.hip). The control block lives in device memory; the host
 // writes it before a decode and reads it between batches of steps.
-constexpr int TDT_ROWS = 16;       // frames the joint scores per step; rows of a standalone prediction
-constexpr int TDT_MAX_LAYERS = 4;  // LSTM layers of the prediction network
+constexpr int TDT_ROWS = 16;            // most frames the joint scores per step; rows of a prediction
+constexpr int TDT_MAX_LAYERS = 4;       // LSTM layers of the prediction network
+constexpr int TDT_MAX_DURATIONS = 64;
+// The control values the joint of a step saw, for the kernel that decides the step.
+struct TdtSnap {
+    int32_t valid, t, rows, on_frame, ntok, active, cur;
+};
 struct TdtCtl {
     int32_t t, on_frame, ntok;  // the frame, tokens on it so far, tokens emitted
-    int32_t active;             // a token waits for the prediction network
+    int32_t active;             // a token went to the prediction network this step
     int32_t done;               // the frames are used up and no prediction waits
-    int32_t tok[TDT_ROWS];      // the tokens the prediction network runs on (the decode uses tok[0])
-    uint32_t arrive[TDT_MAX_LAYERS + 2];  // workgroups arrived: joint, each layer, projection
+    int32_t cur;                // the state buffer holding the current LSTM state (0: the caller's)
+    int32_t rows;               // frames the next joint scores (1 .. TDT_ROWS)
+    TdtSnap snap;
 };
 struct TdtTokens {
     int32_t tok[TDT_ROWS];
 };
+// lstm[] and lstm_b[] are the interleaved copies (output 4 u + q is gate q of unit u).
 struct TdtNet {
     size_t h, vocab, ndur, layers, blank, max_symbols;
     const DeviceWeights *joint, *lstm[TDT_MAX_LAYERS], *proj;
@@ -217,10 +224,13 @@ struct TdtNet {
 };
 size_t tdt_max_rows(const DeviceWeights &lstm);
 size_t tdt_partials_bytes();
-hipError_t launch_tdt_predict(TdtCtl *ctl, int gated, const TdtTokens &toks, size_t m, const TdtNet &net,
-                              float *states, float *preds, float *gates, int frames, hipStream_t s);
-hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, size_t lde, int frames, float *states,
-                           float *pred, float *logits, float *gates, void *partials, int32_t *tokens, int cap,
+size_t tdt_extras_bytes();
+hipError_t launch_tdt_interleave(const DeviceWeights &src, const float *bias, const DeviceWeights &dst,
+                                 float *bias_dst, size_t h, hipStream_t s);
+hipError_t launch_tdt_predict(TdtCtl *ctl, const TdtTokens &toks, size_t m, const TdtNet &net, float *sa, float *sb,
+                              float *preds, hipStream_t s);
+hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, size_t lde, int frames, float *sa,
+                           float *sb, float *pred, void *partials, float *extras, int32_t *tokens, int cap,
                            hipStream_t s);
 
 }  // namespace tg
