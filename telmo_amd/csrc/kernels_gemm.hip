@@ -331,24 +331,23 @@ hipError_t launch_q8(const uint8_t *qf, const int32_t *exps, size_t m, const Dev
 
 // ---------------------------------------------------------------------------- LDS-staged GEMM
 //
-// For products large enough to fill the chip with 128 x 128 tiles: the workgroup's operands go
-// from global memory straight into LDS with global_load_lds_dwordx4 (no VGPRs, no ds_write), one
-// k-block stage of 24 KB (A: 8 row blocks x hi, lo; B: 8 panels, each 1 KB in lane order) per
-// buffer, in a ring of DMA_NS buffers. Each wavefront moves 6 of the 24 KB of a stage, waits for
-// its own copies with s_waitcnt vmcnt, and a barrier makes the stage visible to all four; the
-// buffer a stage came from is refilled only after every wavefront has read it. The four 64 x 64
-// wavefronts then read their MFMA operands with linear 16-byte LDS reads. Loading each operand
-// once per workgroup instead of once per wavefront halves the L1 traffic of the direct kernel.
-constexpr int DMA_NS = 3;
-constexpr int DMA_STAGE = 24576;
-constexpr int DMA_PER_WAVE = 6;  // 1 KB copies per wavefront per stage
+// The workgroup's operands go from global memory straight into LDS with global_load_lds_dwordx4
+// (no VGPRs, no ds_write): per k-block one stage of 2 TM + TN chunks of 1 KB in lane order (A: TM
+// row blocks x hi, lo; B: TN panels), in a ring of NS buffers. Each wavefront moves a quarter of
+// the chunks, waits for its own copies with s_waitcnt vmcnt, and a barrier makes the stage visible
+// to all four; a buffer is refilled only after every wavefront has read it. The four wavefronts
+// (2 x 2, each TM / 2 row blocks by TN / 2 panels) then read their MFMA operands with linear
+// 16-byte LDS reads. Loading each operand once per workgroup instead of once per wavefront halves
+// the L1 traffic of the direct kernel. Instances: 128 x 128 tiles in XCD order for products that
+// fill the chip twice over; 64 x 64 tiles grouped four tile-rows at a time for mid-size products
+// of at least 2048 outputs.
 
+// 64 lanes x 16 bytes from g (per lane) to LDS at lds (the wavefront's base; lane l's bytes land at
+// lds + 16 l). M0 holds the LDS address; it is set before every copy and nothing else here uses it.
 __device__ __forceinline__ uint32_t lds_address(const void *p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
 }
 
-// 64 lanes x 16 bytes from g (per lane) to LDS at lds (the wavefront's base; lane l's bytes land at
-// lds + 16 l). M0 holds the LDS address; it is set before every copy and nothing else here uses it.
 __device__ __forceinline__ void copy_to_lds(const uint8_t *g, uint8_t *lds) {
     const uint32_t a = __builtin_amdgcn_readfirstlane(lds_address(lds));
 #pragma clang diagnostic push
@@ -363,7 +362,24 @@ __device__ __forceinline__ void wait_copies() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__global__ __launch_bounds__(THREADS, 2) void gemm_dma_kernel(const uint8_t *__restrict__ qf,
+// Waits until at most `ahead` stages of CPW copies each are still on the way (ahead < NS - 1).
+template <int CPW, int NS>
+__device__ __forceinline__ void wait_stages(int ahead) {
+    static_assert(NS >= 2 && NS <= 4, "ring of 2 to 4 stages");
+    if constexpr (NS == 4) {
+        if (ahead >= 2) wait_copies<2 * CPW>();
+        else if (ahead == 1) wait_copies<CPW>();
+        else wait_copies<0>();
+    } else if constexpr (NS == 3) {
+        if (ahead >= 1) wait_copies<CPW>();
+        else wait_copies<0>();
+    } else {
+        wait_copies<0>();
+    }
+}
+
+template <int TM, int TN, int NS, int XCD, int G>
+__global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__restrict__ qf,
                                                               const int32_t *__restrict__ exps, int M,
                                                               const uint8_t *__restrict__ wv,
                                                               const float *__restrict__ scales, int N, int P, int KB,
@@ -371,80 +387,83 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_dma_kernel(const uint8_t *__r
                                                               const float *__restrict__ bias, uint32_t act,
                                                               float escale, int accumulate, size_t b_panel,
                                                               size_t b_blk) {
-    constexpr int C_STRIDE = 68;
-    static_assert(4 * 64 * C_STRIDE * 4 <= DMA_NS * DMA_STAGE, "the epilogue reuses the ring");
-    __shared__ __attribute__((aligned(16))) uint8_t smem[DMA_NS * DMA_STAGE];
+    constexpr int RB = TM / 2, CB = TN / 2;  // 16 x 16 blocks per wavefront
+    constexpr int CH = 2 * TM + TN;          // 1 KB chunks per stage
+    static_assert(CH % 4 == 0, "the chunks split evenly over four wavefronts");
+    constexpr int CPW = CH / 4, STAGE = CH * 1024;
+    constexpr int WM = RB * 16, WN = CB * 16, C_STRIDE = WN + 4;
+    static_assert(4 * WM * C_STRIDE * 4 <= NS * STAGE, "the epilogue reuses the ring");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     int bx, by;
-    tile_of<1, 0>(bx, by);
-    const int R0 = by * 8, P0 = bx * 8, RLAST = (M + 15) / 16 - 1;
-    const int m0 = by * 128 + wm * 64, n0 = bx * 128 + wn * 64;
+    tile_of<XCD, G>(bx, by);
+    const int R0 = by * TM, P0 = bx * TN, RLAST = (M + 15) / 16 - 1;
+    const int m0 = by * TM * 16 + wm * WM, n0 = bx * TN * 16 + wn * WN;
     const int out_col = lane & 15, out_row = (lane >> 4) * 4;
 
-    int32_t e_row[4][4];
-    float s_col[4];
+    int32_t e_row[RB][4];
+    float s_col[CB];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int r = 0; r < RB; r++)
 #pragma unroll
         for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
 #pragma unroll
-    for (int cb = 0; cb < 4; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
+    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
 
-    // This wavefront's copies: A chunks wave + 4 i (row block R0 + chunk / 2, digit chunk % 2) and
-    // B chunks wave + 4 i (panel P0 + chunk); rows and panels past the edge repeat the last one.
-    const uint8_t *ga[4];
-    const uint8_t *gb[2];
+    // This wavefront's copies: chunk ch = wave + 4 i is row block R0 + ch / 2, digit ch % 2 when
+    // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one.
+    const uint8_t *g[CPW];
+    size_t gs[CPW];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < CPW; i++) {
         const int ch = wave + 4 * i;
-        ga[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024 + lane * 16;
+        if (ch < 2 * TM) {
+            g[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024 + lane * 16;
+            gs[i] = 2048;
+        } else {
+            g[i] = wv + (size_t)min(P0 + ch - 2 * TM, P - 1) * b_panel + lane * 16;
+            gs[i] = b_blk;
+        }
     }
-#pragma unroll
-    for (int i = 0; i < 2; i++) gb[i] = wv + (size_t)min(P0 + wave + 4 * i, P - 1) * b_panel + lane * 16;
-#define TG_ISSUE(buf, tt)                                                                                 \
-    do {                                                                                                  \
-        uint8_t *st_ = smem + (buf) * DMA_STAGE;                                                          \
-        const size_t t_ = (size_t)(tt);                                                                   \
-        _Pragma("unroll") for (int i = 0; i < 4; i++) copy_to_lds(ga[i] + t_ * 2048, st_ + (wave + 4 * i) * 1024); \
-        _Pragma("unroll") for (int i = 0; i < 2; i++)                                                    \
-            copy_to_lds(gb[i] + t_ * b_blk, st_ + 16384 + (wave + 4 * i) * 1024);                         \
+#define TG_ISSUE(buf, tt)                                                                              \
+    do {                                                                                               \
+        uint8_t *st_ = smem + (buf) * STAGE;                                                           \
+        const size_t t_ = (size_t)(tt);                                                                \
+        _Pragma("unroll") for (int i = 0; i < CPW; i++) copy_to_lds(g[i] + t_ * gs[i], st_ + (wave + 4 * i) * 1024); \
     } while (0)
 
-    v4i acc_hi[4][4], acc_lo[4][4];
+    v4i acc_hi[RB][CB], acc_lo[RB][CB];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < RB; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < CB; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int s = 0; s < DMA_NS - 1; s++)
+    for (int s = 0; s < NS - 1; s++)
         if (s < KB) TG_ISSUE(s, s);
-    for (int t0 = 0; t0 < KB; t0 += DMA_NS) {
+    for (int t0 = 0; t0 < KB; t0 += NS) {
 #pragma unroll
-        for (int s = 0; s < DMA_NS; s++) {
+        for (int s = 0; s < NS; s++) {
             const int t = t0 + s;
             if (t < KB) {
-                // k-block t sits in buffer s; k-blocks t + 1 .. t + DMA_NS - 2 may still be on the way.
-                if (min(DMA_NS - 2, KB - 1 - t) >= 1)
-                    wait_copies<DMA_PER_WAVE>();
-                else
-                    wait_copies<0>();
+                // k-block t sits in buffer s; up to NS - 2 later k-blocks may still be on the way.
+                wait_stages<CPW, NS>(min(NS - 2, KB - 1 - t));
                 __syncthreads();
-                if (t + DMA_NS - 1 < KB) TG_ISSUE((s + DMA_NS - 1) % DMA_NS, t + DMA_NS - 1);
-                const uint8_t *st = smem + s * DMA_STAGE;
-                v4i fa[4][2], fb[4];
+                if (t + NS - 1 < KB) TG_ISSUE((s + NS - 1) % NS, t + NS - 1);
+                const uint8_t *st = smem + s * STAGE;
+                v4i fa[RB][2], fb[CB];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * 4 + r) * 2) * 1024 + lane * 16);
-                    fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * 4 + r) * 2 + 1) * 1024 + lane * 16);
+                for (int r = 0; r < RB; r++) {
+                    fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2) * 1024 + lane * 16);
+                    fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2 + 1) * 1024 + lane * 16);
                 }
 #pragma unroll
-                for (int cb = 0; cb < 4; cb++)
-                    fb[cb] = *reinterpret_cast<const v4i *>(st + 16384 + (wn * 4 + cb) * 1024 + lane * 16);
+                for (int cb = 0; cb < CB; cb++)
+                    fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
 #pragma unroll
-                for (int r = 0; r < 4; r++)
+                for (int r = 0; r < RB; r++)
 #pragma unroll
-                    for (int cb = 0; cb < 4; cb++) {
+                    for (int cb = 0; cb < CB; cb++) {
                         acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[r][0], fb[cb], acc_hi[r][cb], 0, 0, 0);
                         acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[r][1], fb[cb], acc_lo[r][cb], 0, 0, 0);
                     }
@@ -454,39 +473,41 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_dma_kernel(const uint8_t *__r
 #undef TG_ISSUE
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
 
-    float *tile = reinterpret_cast<float *>(smem) + wave * 64 * C_STRIDE;
+    float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int r = 0; r < RB; r++)
 #pragma unroll
-        for (int cb = 0; cb < 4; cb++)
+        for (int cb = 0; cb < CB; cb++)
 #pragma unroll
             for (int v = 0; v < 4; v++)
                 tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
                     dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
     __syncthreads();
-    for (int i0 = lane; i0 < 4096; i0 += 8 * 64) {
+    constexpr int TOTAL = WM * WN;
+    for (int i0 = lane; i0 < TOTAL; i0 += 8 * 64) {
         float old[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / 64, col = n0 + i % 64;
-            old[u] = (accumulate && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
+            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
+            old[u] = (accumulate && i < TOTAL && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / 64, col = n0 + i % 64;
-            if (row < M && col < N)
-                c[(size_t)row * ldc + col] = epilogue(tile[(i / 64) * C_STRIDE + i % 64], bias, (size_t)col, act,
+            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
+            if (i < TOTAL && row < M && col < N)
+                c[(size_t)row * ldc + col] = epilogue(tile[(i / WN) * C_STRIDE + i % WN], bias, (size_t)col, act,
                                                       escale, accumulate != 0, &old[u]);
         }
     }
 }
 
-hipError_t launch_dma(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+template <int TM, int TN, int NS, int XCD, int G>
+hipError_t launch_lds(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                       const EpiArgs &epi, hipStream_t s) {
-    dim3 grid((unsigned)div_ceil(w.panels * PANEL, (size_t)128), (unsigned)div_ceil(m, (size_t)128));
-    hipLaunchKernelGGL(gemm_dma_kernel, grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values, w.scales, (int)w.n,
-                       (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride,
-                       w.blk_stride);
+    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)TN), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
+    hipLaunchKernelGGL((gemm_lds_kernel<TM, TN, NS, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
+                       w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
+                       epi.accumulate, w.panel_stride, w.blk_stride);
     return hipGetLastError();
 }
 
@@ -508,7 +529,10 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         if (gemm_tile_choice(m, w.panels) == 0) return launch_q8<2, 2, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
         return launch_q8<2, 2, 2, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
     }
-    if (gemm_tile_choice(m, w.panels) == 0) return launch_dma(qf, exps, m, w, c, ldc, epi, s);
+    if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+    // Mid-size products: LDS staging pays from 2048 outputs (the direct kernel's duplicate operand
+    // loads dominate there); narrower ones keep the direct kernel.
+    if (w.panels >= 128) return launch_lds<4, 4, 3, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
     return launch_tile<2, 2, 3, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 
