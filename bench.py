@@ -15,7 +15,7 @@ on the same data. The step runs as one captured HIP graph; the eager (stream) fi
 beside it. value = 2 * sum(M N K) over the 8 GEMMs / step time, in TOPS.
 
 The JSON line also carries:
-  roofline      the GEMM kernel alone: each of the layer's 8 shapes on pre-quantised rows, timed
+  roofline      the GEMM kernels alone: each of the layer's 8 shapes on pre-quantised rows, timed
                 with HIP events on the library's stream; achieved = algorithmic ops / kernel time,
                 against the dense int8 MFMA peak. traffic comes from the rocprofv3 PMC summary in
                 profiles/ when one is there.
@@ -664,7 +664,7 @@ def cpu_tdt(net, enc_host, frames):
 
 
 def load_traffic():
-    path = os.path.join(ROOT, "profiles", "gemm_i8_traffic.json")
+    path = os.path.join(ROOT, "profiles", "gemm_layer_T750_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -698,7 +698,7 @@ def main():
     traffic = load_traffic()
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_INT8 / 1e12,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8, 4), "traffic": traffic,
-                "kernel": "gemm_i8_kernel", "avg_launch_us": round(gemm_us / len(per_shape), 3),
+                "kernel": "gemm_lds_kernel<4,4,3> (n >= 2048) and gemm_i8_kernel<2,2,3> (n = 1024)", "avg_launch_us": round(gemm_us / len(per_shape), 3),
                 "ops_per_launch_avg": ops / len(per_shape),
                 "mfma_int8_ops_per_launch_avg": 2 * ops / len(per_shape),
                 "mfma_busy_frac": round(2 * achieved / PEAK_INT8, 4),
