@@ -15,6 +15,7 @@
  *   Kernels::glu (row kernel)    src/kernels/mod.rs:463-464   -> tg_glu_device
  *   Kernels::layer_norm          src/kernels/mod.rs:458       -> tg_layer_norm_device
  *   Kernels::dwconv1d_frame + silu  src/kernels/mod.rs:464-475  -> tg_dwconv1d_device
+ *   BView::row_major + matmul    src/kernels/mod.rs:320-339, 657-688 -> tg_matmul_rowmajor_device
  *   Parakeet::predict_rows       src/parakeet.rs:1524-1577    -> tg_tdt_predict_device
  *   Parakeet::decode_inner       src/parakeet.rs:1412-1513    -> tg_tdt_decode_device
  *   Pack::open / from_bytes      src/pack.rs:79-96            -> tg_pack_open, tg_pack_from_bytes
@@ -129,6 +130,16 @@ int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size
                      float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
 int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *c,
                      size_t c_len, const tg_epilogue *epi);
+
+/* c = epi(a . b) with b a row-major [k, ldb] f32 matrix whose first n columns are used: the
+ * reference's BView::row_major right-hand side (src/kernels/mod.rs:320-339, the attention path's
+ * f32 activations) through Kernels::matmul (657-688) / matmul_serial (732-765). The sums are the
+ * reference's fused ones, fmaf over the inputs in order, whatever the context's mode. As
+ * BView::check (341-351) requires, b holds whole 16-column panels: b_len >= (ceil(n / 16) - 1) 16
+ * + (k - 1) ldb + 16 floats (TG_ERR_SHAPE otherwise); then matmul's checks. Device pointers. */
+int tg_matmul_rowmajor_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const float *b,
+                              size_t b_len, size_t k, size_t n, size_t ldb, float *c, size_t c_len, size_t ldc,
+                              const tg_epilogue *epi);
 
 /* ---- the staged int8 path ------------------------------------------------------------------
  * The fast int8 product in its two stages, for callers that reuse one quantised input across

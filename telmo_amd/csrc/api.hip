@@ -334,6 +334,34 @@ int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size
     return rc;
 }
 
+int tg_matmul_rowmajor_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const float *b,
+                              size_t b_len, size_t k, size_t n, size_t ldb, float *c, size_t c_len, size_t ldc,
+                              const tg_epilogue *epi) {
+    if (!ctx) return TG_ERR_NULL;
+    // BView::row_major's check (src/kernels/mod.rs:341-351): the view reads whole 16-column panels.
+    if (n > 0 && k > 0) {
+        const size_t last = (tg::div_ceil(n, (size_t)tg::PANEL) - 1) * tg::PANEL + (k - 1) * ldb + tg::PANEL;
+        if (b_len < last) return fail(ctx, TG_ERR_SHAPE, "the matrix view reads past its buffer");
+        if (!b) return fail(ctx, TG_ERR_NULL, "b is null");
+    }
+    if (m == 0 || n == 0) return TG_OK;
+    // Kernels::matmul's checks (src/kernels/mod.rs:669-677), in its order.
+    if (lda < k || ldc < n) return fail(ctx, TG_ERR_SHAPE, "lda must be >= k and ldc >= n");
+    if (a_len < (m - 1) * lda + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (c_len < (m - 1) * ldc + n) return fail(ctx, TG_ERR_SHAPE, "c is too short");
+    if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
+    if (!a && k > 0) return fail(ctx, TG_ERR_NULL, "a is null");
+    if (!c) return fail(ctx, TG_ERR_NULL, "c is null");
+    if (k > (size_t)INT32_MAX || n > (size_t)INT32_MAX || m > (size_t)INT32_MAX)
+        return fail(ctx, TG_ERR_UNSUPPORTED, "sizes beyond 2^31");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_rowmajor(a, lda, m, k, b, ldb, n, c, ldc, epi_args(epi, nullptr, false), ctx->stream));
+    ctx->err.clear();
+    return TG_OK;
+}
+
 int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *c,
                      size_t c_len, const tg_epilogue *epi) {
     if (!w) return fail(ctx, TG_ERR_NULL, "null weights");

@@ -56,7 +56,32 @@ __global__ __launch_bounds__(256) void exact_kernel(const float *__restrict__ a,
     *cp = epilogue(acc, bias, (size_t)col, act, escale, accumulate != 0, cp);
 }
 
+// BView::row_major as the right-hand side (src/kernels/mod.rs:320-339): column col of input i is
+// b[i ldb + col], read straight from the row-major f32 matrix, summed as the exact kernel sums.
+__global__ __launch_bounds__(256) void rowmajor_kernel(const float *__restrict__ a, size_t lda, int m, int k,
+                                                       const float *__restrict__ b, size_t ldb, int N,
+                                                       float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
+                                                       uint32_t act, float escale, int accumulate) {
+    const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (row >= m || col >= N) return;
+    const float *ar = a + (size_t)row * lda;
+    float acc = 0.0f;
+    for (int i = 0; i < k; i++) acc = __builtin_fmaf(ar[i], b[(size_t)i * ldb + col], acc);
+    float *cp = c + (size_t)row * ldc + col;
+    *cp = epilogue(acc, bias, (size_t)col, act, escale, accumulate != 0, cp);
+}
+
 }  // namespace
+
+hipError_t launch_rowmajor(const float *a, size_t lda, size_t m, size_t k, const float *b, size_t ldb, size_t n,
+                           float *c, size_t ldc, const EpiArgs &epi, hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    dim3 grid((unsigned)div_ceil(n, 64), (unsigned)div_ceil(m, 4));
+    hipLaunchKernelGGL(rowmajor_kernel, grid, dim3(256), 0, s, a, lda, (int)m, (int)k, b, ldb, (int)n, c, ldc, epi.bias,
+                       epi.act, epi.scale, epi.accumulate);
+    return hipGetLastError();
+}
 
 hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                         const EpiArgs &epi, hipStream_t s) {

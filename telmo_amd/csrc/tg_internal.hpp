@@ -194,6 +194,9 @@ hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeig
 // The exact kernel: the reference's fused sums in input order, any precision.
 hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                         const EpiArgs &epi, hipStream_t s);
+// A row-major f32 right-hand side [k, ldb], the exact kernel's sums (kernels_exact.hip).
+hipError_t launch_rowmajor(const float *a, size_t lda, size_t m, size_t k, const float *b, size_t ldb, size_t n,
+                           float *c, size_t ldc, const EpiArgs &epi, hipStream_t s);
 
 // The greedy TDT decode (kernels_tdt.hip). The control block lives in device memory; the host
 // writes it before a decode and reads it between batches of steps.

@@ -271,6 +271,17 @@ class Kernels:
     def linear_device(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
         self.matmul_device(a, w.k(), m, w, c, w.n(), epi)
 
+    def matmul_rowmajor_device(self, a, lda: int, m: int, b, k: int, n: int, ldb: int, c, ldc: int,
+                               epi: Epilogue = Epilogue.PLAIN, a_len: Optional[int] = None,
+                               b_len: Optional[int] = None, c_len: Optional[int] = None):
+        """matmul with BView::row_major(b, k, n, ldb) as the right-hand side: f32 GPU tensors, the
+        reference's fused sums. b must hold whole 16-column panels, as the reference's view checks."""
+        rc = _lib.lib().tg_matmul_rowmajor_device(
+            self._ctx, ctypes.c_void_p(a.data_ptr()), a.numel() if a_len is None else a_len, lda, m,
+            ctypes.c_void_p(b.data_ptr()), b.numel() if b_len is None else b_len, k, n, ldb,
+            ctypes.c_void_p(c.data_ptr()), c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
+        _check(rc, self._ctx)
+
     def quant_bytes(self, m: int, k: int) -> int:
         return _lib.lib().tg_quant_bytes(m, k)
 

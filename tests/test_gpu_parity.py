@@ -498,3 +498,34 @@ def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
         orc.matmul_fast(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc)
         got = run_gpu(tk, a, k, m, values, scales, INT8, n, k, c0, n, b, act, acc)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+
+
+@pytest.mark.parametrize("m,k,n,ldb", [(7, 128, 255, 255), (40, 128, 255, 256), (1, 33, 16, 20), (130, 300, 40, 64)])
+def test_rowmajor_right_hand_side_is_the_fused_reference(tk, orc, m, k, n, ldb):
+    """BView::row_major (f32 activations as the right-hand side) gives the fused reference's bits: the
+    same values packed into panels through the oracle's fused matmul. Granite's packed rel product
+    is (m <= 128) x 128 -> 255."""
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(m + k + n)
+    a = normal(rng, (m, k))
+    npad = -(-n // 16) * 16
+    b = normal(rng, (k - 1) * ldb + npad)  # exactly what the reference's view needs
+    bias = normal(rng, n)
+    dense = np.stack([b[i * ldb:i * ldb + n] for i in range(k)])  # [k, n]
+    values, _ = orc.encode(np.ascontiguousarray(dense.T), n, k, F32)  # the same values as 16-column panels
+    for act, acc in ((NONE, False), (SILU, True)):
+        c0 = normal(rng, (m, n))
+        want = c0.copy()
+        orc.matmul(True, a.reshape(-1), k, m, values, None, F32, n, k, want.reshape(-1), n, bias, act, 0.5, acc)
+        say("rowmajor", m, k, n, ldb, act)
+        cd = torch.from_numpy(c0.copy()).cuda()
+        tk.matmul_rowmajor_device(torch.from_numpy(a).cuda(), k, m, torch.from_numpy(b).cuda(), k, n, ldb, cd, n,
+                                  telmo_amd.Epilogue(bias=torch.from_numpy(bias).cuda(), act=telmo_amd.Act(act), scale=0.5,
+                                                     accumulate=acc))
+        tk.synchronize()
+        assert np.array_equal(cd.cpu().numpy().view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+    with pytest.raises(telmo_amd.TelmoError):  # one float short of the last panel
+        tk.matmul_rowmajor_device(torch.from_numpy(a).cuda(), k, m, torch.from_numpy(b[:-1]).cuda(), k, n, ldb, cd, n)
