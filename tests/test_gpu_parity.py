@@ -529,3 +529,38 @@ def test_rowmajor_right_hand_side_is_the_fused_reference(tk, orc, m, k, n, ldb):
         assert np.array_equal(cd.cpu().numpy().view(np.uint32), want.view(np.uint32)), (m, k, n, act)
     with pytest.raises(telmo_amd.TelmoError):  # one float short of the last panel
         tk.matmul_rowmajor_device(torch.from_numpy(a).cuda(), k, m, torch.from_numpy(b[:-1]).cuda(), k, n, ldb, cd, n)
+
+
+@pytest.mark.parametrize("m,k,n", [(750, 1024, 4096), (16, 640, 8198)])
+def test_unit_scales_agree_with_the_library_f32_gemm(tk, orc, m, k, n):
+    """With all scales 1 and no activation the product is an ordinary f32 GEMM against integer-valued
+    weights: both modes are checked against hipBLASLt's f32 GEMM (TF32 / XF32 off) on the same GPU, a
+    run-only cross-check with a library routine. Exact mode: two f32 sums of k products in different
+    orders, so within twice the recursive-summation bound, 2 k 2^-24 sum |a_i w_i|, per output; fast
+    mode: within the 1e-4 row-normwise bound."""
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(m + n)
+    q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+    values, scales = pack_int8(q, np.ones(n, np.float32))
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    a = normal(rng, (m, k))
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ad = torch.from_numpy(a).cuda()
+    lib = (ad @ torch.from_numpy(q.astype(np.float32)).cuda().t()).cpu().numpy()
+    say("library cross-check", m, k, n)
+    for mode, bound in ((telmo_amd.Kernels.EXACT, None), (telmo_amd.Kernels.FAST, 1e-4)):
+        tk.set_mode(mode)
+        c = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        tk.linear_device(ad, m, w, c)
+        tk.synchronize()
+        got = c.cpu().numpy()
+        if bound is None:
+            mag = np.abs(a).astype(np.float64) @ np.abs(q.astype(np.float64)).T
+            assert np.all(np.abs(got.astype(np.float64) - lib) <= 2 * k * 2.0**-24 * mag)
+        else:
+            assert rel_norm_err(got, lib) <= bound
+    tk.set_mode(telmo_amd.Kernels.FAST)
+    w.close()
