@@ -564,3 +564,36 @@ def test_unit_scales_agree_with_the_library_f32_gemm(tk, orc, m, k, n):
             assert rel_norm_err(got, lib) <= bound
     tk.set_mode(telmo_amd.Kernels.FAST)
     w.close()
+
+
+
+def test_row_fixtures(tk):
+    """The committed LayerNorm, GLU and depthwise-convolution fixtures, bit for bit."""
+    import torch
+
+    from golden_cases import load, rows
+
+    from telmo_amd import Act
+
+    for meta in rows():
+        g = load(meta)
+        say("row fixture", meta["name"])
+        if meta["kind"] == "layer_norm":
+            m, n = meta["m"], meta["n"]
+            out = torch.zeros((m, n), device="cuda")
+            tk.layer_norm_device(torch.from_numpy(g["x"]).cuda(), n, m, n, torch.from_numpy(g["gamma"]).cuda(),
+                                 torch.from_numpy(g["beta"]).cuda(), meta["eps"], out, n)
+        elif meta["kind"] == "glu":
+            m, h = meta["m"], meta["half"]
+            out = torch.zeros((m, h), device="cuda")
+            tk.glu_device(torch.from_numpy(g["x"]).cuda(), 2 * h, m, h, out, h)
+        elif meta["kind"] == "dwconv":
+            c = meta["channels"]
+            out = torch.zeros((meta["rows"], c), device="cuda")
+            tk.dwconv1d_device(torch.from_numpy(g["x"]).cuda(), c, meta["frames"], c, torch.from_numpy(g["w"]).cuda(),
+                               meta["kernel"], torch.from_numpy(g["bias"]).cuda(), out, c, rows=meta["rows"],
+                               t0=meta["t0"], stride=meta["stride"], act=Act.SILU if meta["silu"] else Act.NONE)
+        else:
+            continue
+        tk.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), g["out"].view(np.uint32)), meta["name"]

@@ -171,3 +171,30 @@ def test_decode_refusals(tk):
         dec2.decode(enc, torch.zeros(64, device="cuda"), torch.zeros(32, device="cuda"), cap=3)
     dec.close()
     dec2.close()
+
+
+
+def test_decode_fixture(tk):
+    """The committed TDT fixture (a small int8 network from telmo's generator): predict_rows and the
+    decode from the start state; tokens exact, states within TOL."""
+    import torch
+
+    from golden_cases import load, rows, tdt_net
+
+    meta = [r for r in rows() if r["kind"] == "tdt"][0]
+    g = load(meta)
+    net = tdt_net(meta, g)
+    dec = upload(tk, net)
+    say("tdt fixture", meta["name"])
+    sd = torch.from_numpy(g["states0"].copy()).cuda()
+    pd = torch.zeros(g["preds"].shape, device="cuda")
+    dec.predict_rows(list(g["tokens_in"]), sd, pd)
+    tk.synchronize()
+    assert np.max(np.abs(sd.cpu().numpy() - g["states"])) <= TOL
+    assert rel_norm_err(pd.cpu().numpy(), g["preds"]) <= TOL
+    state, pred = torch.from_numpy(g["state0"].copy()).cuda(), torch.from_numpy(g["pred0"].copy()).cuda()
+    toks, frame, on = dec.decode(torch.from_numpy(g["enc"]).cuda(), state, pred)
+    assert np.array_equal(np.asarray([tuple(t) for t in toks], np.int32).reshape(-1, 3), g["tokens"])
+    assert [frame, on] == list(g["end"])
+    assert np.max(np.abs(state.cpu().numpy() - g["state"])) <= TOL
+    dec.close()
