@@ -649,18 +649,37 @@ def tdt_leg(args, net, enc_host):
 
 
 def cpu_tdt(net, enc_host, frames):
-    """The oracle's decode_inner (plain C, one core) on the first frames of the same decode."""
+    """telmo's decode_inner on the CPU: the C++ port (every product by the SIMD port on a pool of
+    all host cores, libm gate math) over the whole decode, best of 3; and, as the parity check, the
+    oracle's decode (scalar C, the fast path's integer products) over the first `frames` frames."""
     from oracle import oracle as orc
 
-    state = np.zeros(2 * 2 * TDT_H, np.float32)
-    pred = np.zeros(TDT_H, np.float32)
-    orc.tdt_predict(net, [TDT_VOCAB - 1], state.reshape(1, -1), pred.reshape(1, -1))
+    L = orc.cpubase()
+    if L.cb_isa() == 0:
+        return None, None, None
+    cores = len(os.sched_getaffinity(0))
+    pool = L.cb_pool_new(cores)
+    start = np.zeros(2 * 2 * TDT_H, np.float32), np.zeros(TDT_H, np.float32)
+    orc.tdt_predict(net, [TDT_VOCAB - 1], start[0].reshape(1, -1), start[1].reshape(1, -1))
+    best, toks = float("inf"), None
+    for _ in range(3):
+        state, pred = start[0].copy(), start[1].copy()
+        t0 = time.perf_counter()
+        toks, _, _ = orc.cpu_tdt_decode(net, enc_host, state, pred, pool)
+        best = min(best, time.perf_counter() - t0)
+    L.cb_pool_free(pool)
+    state, pred = start[0].copy(), start[1].copy()
     t0 = time.perf_counter()
-    toks, _, _ = orc.tdt_decode(net, enc_host[:frames], state, pred)
+    oracle_toks, _, _ = orc.tdt_decode(net, enc_host[:frames], state, pred)
     dt = time.perf_counter() - t0
-    return {"ms_per_token": round(dt * 1e3 / max(len(toks), 1), 3), "cores": 1, "kind": "port",
-            "sample": f"the oracle's decode (scalar C, integer products) over the first {frames} frames: "
-                      f"{len(toks)} tokens in {dt:.2f} s"}, toks
+    out = {"value": round(best * 1e3, 3), "unit": "ms per decode", "cores": cores, "kind": "port",
+           "ms_per_token": round(best * 1e3 / max(len(toks), 1), 4), "tokens": len(toks),
+           "sample": f"the whole decode ({enc_host.shape[0]} frames) by the C++ port of decode_inner and "
+                     f"predict_rows, products on the SIMD pool port, best of 3",
+           "oracle_scalar": {"ms_per_token": round(dt * 1e3 / max(len(oracle_toks), 1), 3), "cores": 1,
+                             "sample": f"the oracle's decode over the first {frames} frames: "
+                                       f"{len(oracle_toks)} tokens in {dt:.2f} s"}}
+    return out, toks, oracle_toks
 
 
 def load_traffic():
@@ -715,9 +734,13 @@ def main():
         tdt, gpu_toks = tdt_leg(args, net, enc)
     cpu = None if args.no_cpu else cpu_leg(weights, x0, args.cpu_seconds)
     if cpu is not None and tdt is not None:
-        cpu["tdt_decode"], cpu_toks = cpu_tdt(net, enc, 150)
-        # the sample's tokens are the first tokens of the GPU decode
-        tdt["cpu_sample_tokens_match"] = [tuple(t) for t in gpu_toks[:len(cpu_toks)]] == cpu_toks
+        cpu["tdt_decode"], port_toks, oracle_toks = cpu_tdt(net, enc, 150)
+        if port_toks is not None:
+            gpu = [tuple(t) for t in gpu_toks]
+            # the port's tokens (fused f32 sums, as telmo's decode) are the GPU decode's, and the
+            # oracle's over the first frames are its first tokens
+            tdt["cpu_port_tokens_match"] = gpu == port_toks
+            tdt["oracle_sample_tokens_match"] = gpu[:len(oracle_toks)] == oracle_toks
     value = ops / (graph_ms * 1e-3) / 1e12
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,

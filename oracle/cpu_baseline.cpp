@@ -11,10 +11,15 @@
 //                         ceil(panels / (4 * threads)) task split)
 //   Pool                  src/threads.rs:49-191 (the caller works too, idle workers spin 50 us
 //                         and then sleep, a task's failure is raised again after all tasks end)
+//   tdt_decode            src/parakeet.rs:1412-1513 (decode_inner) and 1524-1577 (predict_rows):
+//                         every product is Kernels::linear on the pool, gate math by the host
+//                         libm (sigmoid = 1/(1+exp(-x)), parakeet.rs:1678-1680), argmax the first
+//                         largest value (parakeet.rs:1682-1691)
 #include <immintrin.h>
 
 #include <atomic>
 #include <chrono>
+#include <cmath>
 #include <condition_variable>
 #include <cstdint>
 #include <cstring>
@@ -486,6 +491,67 @@ void gemm_panels(const Kernels &kn, const float *a, size_t lda, size_t m, const 
     }
 }
 
+// Kernels::matmul: the pool splits the panels, a few tasks per thread. False if a task threw.
+bool pool_matmul(Pool *pl, const Kernels &kn, const float *a, size_t lda, size_t m, const uint8_t *values,
+                 const float *scales, int p, size_t n, size_t k, float *c, size_t ldc, const float *bias, int act,
+                 float scale, bool accumulate) {
+    size_t panels = div_ceil(n, PANEL);
+    size_t per_task = div_ceil(panels, pl->threads() * 4);
+    if (per_task < 1) per_task = 1;
+    size_t tasks = div_ceil(panels, per_task);
+    return pl->run(tasks, [&](size_t t) {
+        size_t p0 = t * per_task, p1 = (t + 1) * per_task < panels ? (t + 1) * per_task : panels;
+        gemm_panels(kn, a, lda, m, values, scales, p, n, k, p0, p1, c, ldc, bias, act, scale, accumulate);
+    });
+}
+
+// ------------------------------------------------------------------ the TDT decoder
+
+float sigmoid(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+
+size_t argmax(const float *v, size_t n) {
+    size_t best = 0;
+    for (size_t i = 0; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+struct Tdt {
+    Pool *pool;
+    Kernels kn;
+    int p;
+    size_t h, layers;
+    const float *emb;
+    const uint8_t *const *lstm_v;
+    const float *const *lstm_s, *const *lstm_b;
+    const uint8_t *proj_v;
+    const float *proj_s, *proj_b;
+    std::vector<float> input, gates;
+
+    bool linear(const float *a, const uint8_t *v, const float *s, size_t n, size_t k, const float *bias, float *c) {
+        return pool_matmul(pool, kn, a, k, 1, v, s, p, n, k, c, n, bias, ACT_NONE, 1.0f, false);
+    }
+
+    // predict_rows for one token: state is layers x [h, c], pred h floats.
+    bool predict(size_t token, float *state, float *pred) {
+        std::memcpy(input.data(), emb + token * h, h * sizeof(float));
+        for (size_t l = 0; l < layers; l++) {
+            float *hs = state + l * 2 * h, *cs = hs + h;
+            std::memcpy(input.data() + h, hs, h * sizeof(float));
+            if (!linear(input.data(), lstm_v[l], lstm_s[l], 4 * h, 2 * h, lstm_b[l], gates.data())) return false;
+            const float *g = gates.data();
+            for (size_t j = 0; j < h; j++) {
+                float i = sigmoid(g[j]), f = sigmoid(g[h + j]), gg = std::tanh(g[2 * h + j]),
+                      o = sigmoid(g[3 * h + j]);
+                cs[j] = f * cs[j] + i * gg;
+                hs[j] = o * std::tanh(cs[j]);
+            }
+            std::memcpy(input.data(), hs, h * sizeof(float));
+        }
+        return linear(input.data(), proj_v, proj_s, h, h, proj_b, pred);
+    }
+};
+
 }  // namespace
 
 extern "C" {
@@ -518,16 +584,58 @@ int cb_matmul(void *pool, int isa, const float *a, size_t a_len, size_t lda, siz
     if (p == P_Q8_0 && k % Q8_BLOCK) return -7;
     Kernels kn;
     if (!make_kernels(isa == 0 ? detect_isa() : isa, kn) || (isa != 0 && detect_isa() < isa)) return -5;
-    Pool *pl = static_cast<Pool *>(pool);
-    size_t panels = div_ceil(n, PANEL);
-    size_t per_task = div_ceil(panels, pl->threads() * 4);
-    if (per_task < 1) per_task = 1;
-    size_t tasks = div_ceil(panels, per_task);
-    bool ok = pl->run(tasks, [&](size_t t) {
-        size_t p0 = t * per_task, p1 = (t + 1) * per_task < panels ? (t + 1) * per_task : panels;
-        gemm_panels(kn, a, lda, m, values, scales, p, n, k, p0, p1, c, ldc, bias, act, scale, accumulate != 0);
-    });
+    bool ok = pool_matmul(static_cast<Pool *>(pool), kn, a, lda, m, values, scales, p, n, k, c, ldc, bias, act,
+                          scale, accumulate != 0);
     return ok ? 0 : -4;
+}
+
+// decode_inner from frame *t_io with *on_frame_io tokens on it, every product on the pool with the
+// ISA `isa` (0 picks the fastest). Weights are int8 (p = 3) or Q8_0 (p = 4) in the panel layout:
+// the joint (vocab + ndur) x h, `layers` LSTM matrices 4h x 2h, the projection h x h. enc holds
+// frames rows of h floats (stride lde); state is layers x [h, c] and pred h floats, both updated.
+// Tokens get (id, frame, duration) triples, at most cap of them. Returns the number emitted, -5 if
+// the ISA is not available, -4 if a task failed.
+long cb_tdt_decode(void *pool, int isa, int p, size_t h, size_t layers, size_t vocab, const int32_t *durations,
+                   size_t ndur, size_t max_symbols, const uint8_t *joint_v, const float *joint_s,
+                   const float *joint_b, const float *emb, const uint8_t *const *lstm_v,
+                   const float *const *lstm_s, const float *const *lstm_b, const uint8_t *proj_v,
+                   const float *proj_s, const float *proj_b, const float *enc, size_t lde, size_t frames,
+                   float *state, float *pred, size_t *t_io, size_t *on_frame_io, int32_t *tokens, size_t cap) {
+    Tdt d{static_cast<Pool *>(pool), {}, p, h, layers, emb, lstm_v, lstm_s, lstm_b, proj_v, proj_s, proj_b,
+          std::vector<float>(2 * h), std::vector<float>(4 * h)};
+    if (!make_kernels(isa == 0 ? detect_isa() : isa, d.kn) || (isa != 0 && detect_isa() < isa)) return -5;
+    const size_t outputs = vocab + ndur, blank = vocab - 1;
+    std::vector<float> z(h), logits(outputs);
+    size_t t = *t_io, on_frame = *on_frame_io;
+    long count = 0;
+    while (t < frames) {
+        for (size_t i = 0; i < h; i++) z[i] = std::fmax(enc[t * lde + i] + pred[i], 0.0f);
+        if (!d.linear(z.data(), joint_v, joint_s, outputs, h, joint_b, logits.data())) return -4;
+        const size_t token = argmax(logits.data(), vocab);
+        const size_t duration = (size_t)durations[argmax(logits.data() + vocab, ndur)];
+        if (token == blank) {
+            t += duration > 1 ? duration : 1;
+            on_frame = 0;
+            continue;
+        }
+        if ((size_t)count < cap) {
+            tokens[3 * count] = (int32_t)token;
+            tokens[3 * count + 1] = (int32_t)t;
+            tokens[3 * count + 2] = (int32_t)duration;
+        }
+        count++;
+        if (!d.predict(token, state, pred)) return -4;
+        if (duration > 0) {
+            t += duration;
+            on_frame = 0;
+        } else if (++on_frame >= max_symbols) {
+            t += 1;
+            on_frame = 0;
+        }
+    }
+    *t_io = t;
+    *on_frame_io = on_frame;
+    return count;
 }
 
 }  // extern "C"

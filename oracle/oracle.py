@@ -288,6 +288,46 @@ def tdt_decode(net, enc, state, pred, frame=0, on_frame=0):
     return [tuple(int(v) for v in toks[3 * i:3 * i + 3]) for i in range(n)], f.value, o.value
 
 
+_CB = None
+
+
+def cpubase():
+    """The CPU baseline library (the C++ port of telmo's SIMD + pool path)."""
+    global _CB
+    if _CB is None:
+        L = ctypes.CDLL(CPUBASE)
+        L.cb_isa.restype = ctypes.c_int
+        L.cb_pool_new.restype = ctypes.c_void_p
+        L.cb_pool_new.argtypes = [ctypes.c_size_t]
+        L.cb_pool_free.argtypes = [ctypes.c_void_p]
+        sz, vp = ctypes.c_size_t, ctypes.c_void_p
+        L.cb_tdt_decode.restype = ctypes.c_long
+        L.cb_tdt_decode.argtypes = [vp, ctypes.c_int, ctypes.c_int, sz, sz, sz, vp, sz, sz, vp, vp, vp, vp, vp, vp,
+                                    vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, vp, vp, sz]
+        _CB = L
+    return _CB
+
+
+def cpu_tdt_decode(net, enc, state, pred, pool, frame=0, on_frame=0, isa=0):
+    """decode_inner on the CPU baseline's pool `pool` (from cpubase().cb_pool_new): the same
+    arguments and results as tdt_decode, every product by the SIMD port."""
+    keep, lv, ls, lb = _tdt_common(net)
+    enc = np.ascontiguousarray(enc, np.float32)
+    frames = enc.shape[0]
+    durs = np.ascontiguousarray(net["durations"], np.int32)
+    cap = max(frames - frame, 0) * max(net["max_symbols"], 1) + 1
+    toks = np.zeros(3 * cap, np.int32)
+    f, o = ctypes.c_size_t(frame), ctypes.c_size_t(on_frame)
+    n = cpubase().cb_tdt_decode(pool, isa, net["p"], net["h"], len(net["lstm"]), net["vocab"], _addr(durs), durs.size,
+                                net["max_symbols"], _addr(net["joint"][0]), _addr(net["joint"][1]),
+                                _addr(net["joint_b"]), _addr(net["emb"]), lv, ls, lb, _addr(net["proj"][0]),
+                                _addr(net["proj"][1]), _addr(net["proj_b"]), _addr(enc), enc.shape[1], frames,
+                                _addr(state), _addr(pred), ctypes.byref(f), ctypes.byref(o), _addr(toks), cap)
+    if n < 0:
+        raise RuntimeError(f"cb_tdt_decode failed ({n})")
+    return [tuple(int(v) for v in toks[3 * i:3 * i + 3]) for i in range(n)], f.value, o.value
+
+
 def store(fused, acc, c, cols, bias, act, scale, accumulate):
     lib().or_store(int(fused), acc, c, cols, _ptr(bias), act, scale, int(accumulate))
 

@@ -6,6 +6,8 @@ import ctypes
 import numpy as np
 import pytest
 
+from helpers import tdt_network
+
 F32, F16, BF16, INT8, Q8_0 = range(5)
 NONE, RELU, SILU = range(3)
 
@@ -103,4 +105,59 @@ def test_the_port_refuses_what_the_reference_asserts(orc, cb):
     c = np.zeros(12, np.float32)
     assert cb_matmul(cb, pool, 0, a, 3, 3, values, None, F32, 4, 4, c, 4, None, NONE, 1.0, False) == -2
     assert cb_matmul(cb, pool, 0, a, 4, 0, values, None, F32, 4, 4, c, 4, None, NONE, 1.0, False) == 0
+    cb.cb_pool_free(pool)
+
+
+def _tdt_cases():
+    """Zero-joint networks (logits exactly the joint bias) whose token lists the oracle's tests pin
+    by hand, and one start part-way through a frame."""
+    from test_oracle_tdt import joint_bias, zero_joint
+
+    base = tdt_network(np.random.default_rng(7), 32, 20, [0, 1, 2, 3, 4], layers=2, max_symbols=3)
+    nan = joint_bias(20, 5, 9, 1)
+    nan[0] = np.nan
+    tie = joint_bias(20, 5, 9, 2)
+    tie[6], tie[24] = tie[9], tie[22]
+    return [(zero_joint(base, joint_bias(20, 5, 19, 3)), 23, 0, 0),
+            (zero_joint(base, joint_bias(20, 5, 7, 0)), 6, 0, 0),
+            (zero_joint(base, joint_bias(20, 5, 11, 2)), 9, 0, 0),
+            (zero_joint(base, joint_bias(20, 5, 4, 0)), 3, 1, 2),
+            (zero_joint(base, tie), 4, 0, 0),
+            (zero_joint(base, nan), 2, 0, 0),
+            (base, 5, 5, 1)]
+
+
+def _decode_both(orc, net, frames, frame, on_frame, pool):
+    enc = np.random.default_rng(frames).standard_normal((frames, net["h"])).astype(np.float32)
+    width = len(net["lstm"]) * 2 * net["h"]
+    s1, p1 = np.zeros(width, np.float32), np.zeros(net["h"], np.float32)
+    s2, p2 = s1.copy(), p1.copy()
+    want = orc.tdt_decode(net, enc, s1, p1, frame, on_frame)
+    got = orc.cpu_tdt_decode(net, enc, s2, p2, pool, frame, on_frame)
+    return want, got, (s1, p1), (s2, p2)
+
+
+def test_the_tdt_decode_port_keeps_decode_inners_control_flow(orc, cb):
+    if not isas(cb):
+        pytest.skip("no AVX2/AVX-512 on this host")
+    pool = cb.cb_pool_new(3)
+    for net, frames, frame, on_frame in _tdt_cases():
+        want, got, _, _ = _decode_both(orc, net, frames, frame, on_frame, pool)
+        assert got == want
+    cb.cb_pool_free(pool)
+
+
+@pytest.mark.parametrize("precision", ["int8", "q8_0"])
+def test_the_tdt_decode_port_agrees_with_the_oracle_on_random_networks(orc, cb, precision):
+    """Fused f32 sums (the port) against the fast path's integer sums (the oracle): the same tokens,
+    states and predictions within the fast path's error."""
+    if not isas(cb):
+        pytest.skip("no AVX2/AVX-512 on this host")
+    pool = cb.cb_pool_new(4)
+    rng = np.random.default_rng(11)
+    net = tdt_network(rng, 64, 100, [0, 1, 2, 3, 4], precision=INT8 if precision == "int8" else Q8_0,
+                      blank_bias=3.0)
+    want, got, (s1, p1), (s2, p2) = _decode_both(orc, net, 60, 0, 0, pool)
+    assert len(want[0]) > 5 and got == want
+    assert np.max(np.abs(s1 - s2)) < 1e-3 and np.max(np.abs(p1 - p2)) < 1e-3
     cb.cb_pool_free(pool)
