@@ -22,15 +22,87 @@
 namespace tg {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace {
 
 constexpr int THREADS = 256;
 
-// Order in which workgroups take tiles. Workgroup L of a launch goes to XCD L % 8 (each XCD has
-// its own L2). XCD: hand each XCD a contiguous run of tiles (rows of the tile grid), so the A row
-// blocks its tiles share stay in its L2. G > 0: walk the tiles G tile-rows at a time, column by
-// column, so a weight panel is reused by G row blocks while it is hot.
+// The store of a wavefront's WM x WN tile of sums through the epilogue into c[m0.., n0..]. Lane l
+// owns the runs of four outputs at column 4 (l % (WN / 4)) of rows l / (WN / 4), + 64 / (WN / 4),
+// ...: per run one 16-byte load of the old outputs (when accumulating), one 16-byte LDS read of the
+// staged sums (rows C_STRIDE floats apart) and one 16-byte store. begin() issues the loads of the
+// bias and old outputs, before the sums are staged, so their latency overlaps the staging (for
+// tiles of up to eight runs per lane; larger ones load in finish(), where the accumulators no
+// longer hold registers); finish() stores, and nothing waits for a store, so the wavefront ends
+// once its stores are issued. Runs past the right edge of c, or in a c or ldc not 16-byte aligned,
+// go one output at a time; rows past M are skipped.
+template <int WM, int WN, int C_STRIDE>
+struct TileStore {
+    static constexpr int RPR = WN / 4, STEP = 64 / RPR, PER = WM / STEP;
+    static constexpr bool EARLY = PER <= 8;
+    static_assert(WN % 4 == 0 && 64 % RPR == 0 && WM % STEP == 0, "whole runs per lane");
+    static_assert(C_STRIDE % 4 == 0, "16-byte aligned staged rows");
+    int cr, r0, col;
+    bool vec;
+    v4f b, old[PER];
+
+    __device__ __forceinline__ void begin(int lane, const float *__restrict__ c, size_t ldc, int m0, int n0, int M,
+                                          int N, const float *__restrict__ bias, int accumulate) {
+        cr = lane % RPR;
+        r0 = lane / RPR;
+        col = n0 + 4 * cr;
+        vec = ((reinterpret_cast<uintptr_t>(c) | ldc * sizeof(float)) % 16 == 0) && col + 4 <= N;
+        b = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (bias) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) b[j] = col + j < N ? bias[col + j] : 0.0f;
+        }
+        if constexpr (EARLY) load_old(c, ldc, m0, M, N, accumulate);
+    }
+
+    __device__ __forceinline__ void load_old(const float *__restrict__ c, size_t ldc, int m0, int M, int N,
+                                             int accumulate) {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            old[u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const int row = m0 + r0 + u * STEP;
+            if (accumulate && row < M) {
+                const float *src = c + (size_t)row * ldc + col;
+                if (vec) {
+                    old[u] = *reinterpret_cast<const v4f *>(src);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (col + j < N) old[u][j] = src[j];
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void finish(const float *tile, float *__restrict__ c, size_t ldc, int m0, int M, int N,
+                                           bool has_bias, uint32_t act, float escale, int accumulate) {
+        if constexpr (!EARLY) load_old(c, ldc, m0, M, N, accumulate);
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int row = m0 + r0 + u * STEP;
+            if (row >= M) continue;
+            v4f v = *reinterpret_cast<const v4f *>(tile + (r0 + u * STEP) * C_STRIDE + 4 * cr);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v[j] = epilogue_vals(v[j], has_bias, b[j], act, escale, accumulate != 0, old[u][j]);
+            float *dst = c + (size_t)row * ldc + col;
+            if (vec) {
+                *reinterpret_cast<v4f *>(dst) = v;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (col + j < N) dst[j] = v[j];
+            }
+        }
+    }
+};
+
 template <int XCD, int G>
 __device__ __forceinline__ void tile_of(int &bx, int &by) {
     bx = blockIdx.x;
@@ -53,19 +125,21 @@ __device__ __forceinline__ void tile_of(int &bx, int &by) {
     }
 }
 
-template <int RB, int CB, int S, int OCC, int XCD, int G>
-__global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
-                                                               const int32_t *__restrict__ exps, int M,
-                                                               const uint8_t *__restrict__ wv,
-                                                               const float *__restrict__ scales, int N, int P, int KB,
-                                                               float *__restrict__ c, size_t ldc,
-                                                               const float *__restrict__ bias, uint32_t act,
-                                                               float escale, int accumulate, size_t b_panel,
-                                                               size_t b_blk) {
+template <int RB, int CB, int S, int KG, int OCC, int XCD, int G>
+__global__ __launch_bounds__(THREADS * KG, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
+                                                                    const int32_t *__restrict__ exps, int M,
+                                                                    const uint8_t *__restrict__ wv,
+                                                                    const float *__restrict__ scales, int N, int P,
+                                                                    int KB, float *__restrict__ c, size_t ldc,
+                                                                    const float *__restrict__ bias, uint32_t act,
+                                                                    float escale, int accumulate, size_t b_panel,
+                                                                    size_t b_blk) {
     constexpr int WM = RB * 16, WN = CB * 16;
     constexpr int C_STRIDE = WN + 4;  // f32 per row of a wavefront's staged tile
-    __shared__ float staged[4][WM * C_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int NACC = RB * CB * 2;  // accumulators (v4i) per lane
+    constexpr int STAGED = 4 * WM * C_STRIDE * 4, PARTIALS = (KG - 1) * 4 * NACC * 64 * 16;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGED > PARTIALS ? STAGED : PARTIALS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = tid >> 8;
     const int wm = wave & 1, wn = wave >> 1;
     int bx, by;
     tile_of<XCD, G>(bx, by);
@@ -84,14 +158,16 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
 #pragma unroll
     for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
 
-    // Operand blocks of this wavefront: row block R of the QA at (R * KB + t) * 2048 (+1024 for
-    // the lo digits), panel p of the weights at p * b_panel + t * b_blk.
+    // Wavefront group grp takes the k-blocks grp, grp + KG, grp + 2 KG, ...: NB of them. Operand
+    // blocks: row block R of the QA at (R * KB + t) * 2048 (+1024 for the lo digits), panel p of
+    // the weights at p * b_panel + t * b_blk.
+    const int NB = KB > grp ? (KB - grp + KG - 1) / KG : 0;
     const uint8_t *ap[RB];
     const uint8_t *bp[CB];
 #pragma unroll
-    for (int r = 0; r < RB; r++) ap[r] = qf + (size_t)min(R0 + r, RLAST) * KB * 2048 + lane * 16;
+    for (int r = 0; r < RB; r++) ap[r] = qf + ((size_t)min(R0 + r, RLAST) * KB + grp) * 2048 + lane * 16;
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) bp[cb] = wv + (size_t)min(P0 + cb, P - 1) * b_panel + lane * 16;
+    for (int cb = 0; cb < CB; cb++) bp[cb] = wv + (size_t)min(P0 + cb, P - 1) * b_panel + grp * b_blk + lane * 16;
 
     v4i acc_hi[RB][CB], acc_lo[RB][CB];
 #pragma unroll
@@ -100,9 +176,9 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
         for (int j = 0; j < CB; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
 
     v4i fa[S][RB][2], fb[S][CB];
-#define TG_LOAD(st, tt)                                                                                \
+#define TG_LOAD(st, ii)                                                                                \
     do {                                                                                               \
-        const size_t t_ = (size_t)(tt);                                                                \
+        const size_t t_ = (size_t)(ii) * KG;                                                           \
         _Pragma("unroll") for (int r = 0; r < RB; r++) {                                               \
             fa[st][r][0] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048);                          \
             fa[st][r][1] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048 + 1024);                   \
@@ -119,65 +195,233 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
             }                                                                                          \
     } while (0)
 
-    if (KB > 0) {
-        // Ring of S register stages: block t sits in stage t % S. Loads past the end reload the
-        // last block (in bounds, never used).
+    if (NB > 0) {
+        // Ring of S register stages: the group's i-th block sits in stage i % S. Loads past the
+        // end reload the group's last block (in bounds, never used).
 #pragma unroll
-        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, KB - 1));
-        int t = 0;
-        for (; t + S <= KB; t += S) {
+        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, NB - 1));
+        int i = 0;
+        for (; i + S <= NB; i += S) {
 #pragma unroll
             for (int s = 0; s < S; s++) {
-                TG_LOAD((s + S - 1) % S, min(t + s + S - 1, KB - 1));
+                TG_LOAD((s + S - 1) % S, min(i + s + S - 1, NB - 1));
                 TG_MMA(s);
             }
         }
-        // At most S - 1 blocks remain, already loaded into stages 0, 1, ...
-        if (t < KB) TG_MMA(0);
-        if constexpr (S > 2) {
-            if (t + 1 < KB) TG_MMA(1);
-        }
+        // At most S - 1 blocks remain: block i + j is already in stage j.
+#pragma unroll
+        for (int j = 0; j < S - 1; j++)
+            if (i + j < NB) TG_MMA(j);
     }
 #undef TG_LOAD
 #undef TG_MMA
 
-    // Epilogue: the wavefront stages its f32 sums in LDS (element v of lane l holds row
-    // 4 (l / 16) + v, column l % 16 of its 16 x 16 block), then stores them row after row,
-    // 64 consecutive outputs per instruction, eight at a time so the loads of c overlap.
-    float *tile = staged[wave];
+    TileStore<WM, WN, C_STRIDE> out;
+    if (grp == 0) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    if constexpr (KG > 1) {
+        // The other groups hand their integer sums to group 0 through LDS; integer sums are exact,
+        // so the k-split does not change any result.
+        v4i *part = reinterpret_cast<v4i *>(smem);
+        if (grp > 0) {
 #pragma unroll
-    for (int r = 0; r < RB; r++)
+            for (int r = 0; r < RB; r++)
 #pragma unroll
-        for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-            for (int v = 0; v < 4; v++)
-                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
-                    dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
-    __syncthreads();
-    constexpr int TOTAL = WM * WN;
-    for (int i0 = lane; i0 < TOTAL; i0 += 8 * 64) {
-        float old[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
-            old[u] = (accumulate && i < TOTAL && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
+                for (int cb = 0; cb < CB; cb++) {
+                    const int a = ((grp - 1) * 4 + wave) * NACC + (r * CB + cb) * 2;
+                    part[a * 64 + lane] = acc_hi[r][cb];
+                    part[(a + 1) * 64 + lane] = acc_lo[r][cb];
+                }
         }
+        __syncthreads();
+        if (grp == 0) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
-            if (i < TOTAL && row < M && col < N)
-                c[(size_t)row * ldc + col] = epilogue(tile[(i / WN) * C_STRIDE + i % WN], bias, (size_t)col, act,
-                                                      escale, accumulate != 0, &old[u]);
+            for (int g = 1; g < KG; g++)
+#pragma unroll
+                for (int r = 0; r < RB; r++)
+#pragma unroll
+                    for (int cb = 0; cb < CB; cb++) {
+                        const int a = ((g - 1) * 4 + wave) * NACC + (r * CB + cb) * 2;
+                        acc_hi[r][cb] += part[a * 64 + lane];
+                        acc_lo[r][cb] += part[(a + 1) * 64 + lane];
+                    }
         }
+        __syncthreads();  // the partials are read before the LDS holds the staged outputs
     }
+
+    // Epilogue (group 0): the wavefront stages its f32 sums in LDS (element v of lane l holds row
+    // 4 (l / 16) + v, column l % 16 of its 16 x 16 block), then stores them in 16-byte runs. Every
+    // wavefront passes the same barriers.
+    float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
+    if (grp == 0) {
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                        dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
+    }
+    __syncthreads();
+    if (grp == 0) out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
 }
 
-template <int RB, int CB, int S, int OCC, int XCD, int G>
+template <int RB, int CB, int S, int KG, int OCC, int XCD, int G>
 hipError_t launch_tile(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                        const EpiArgs &epi, hipStream_t s) {
     const size_t bm = 2 * RB * 16, bn = 2 * CB * 16;
     dim3 grid((unsigned)div_ceil(w.panels * PANEL, bn), (unsigned)div_ceil(m, bm));
-    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, OCC, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
+    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, KG, OCC, XCD, G>), grid, dim3(THREADS * KG), 0, s, qf, exps, (int)m,
+                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
+                       epi.accumulate, w.panel_stride, w.blk_stride);
+    return hipGetLastError();
+}
+
+
+// The k-split kernel for products with few output tiles. Each of the four wavefronts of a
+// workgroup computes the whole 64 x 64 tile (4 row blocks x 4 panels) over every fourth k-block
+// (wavefront w takes k-blocks w, w + 4, ...), so every operand byte crosses the CU's L1 once, where
+// the 2 x 2 kernel loads each twice. The four integer partial sums are then combined through LDS:
+// wavefront q keeps row block q, receives the other three wavefronts' sums for it and stores its
+// 16 x 64 strip. The sums are exact integers, so the split changes no result.
+template <int S, int XCD, int G>
+__global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *__restrict__ qf,
+                                                                const int32_t *__restrict__ exps, int M,
+                                                                const uint8_t *__restrict__ wv,
+                                                                const float *__restrict__ scales, int N, int P, int KB,
+                                                                float *__restrict__ c, size_t ldc,
+                                                                const float *__restrict__ bias, uint32_t act,
+                                                                float escale, int accumulate, size_t b_panel,
+                                                                size_t b_blk) {
+    constexpr int RB = 4, CB = 4, WN = CB * 16, C_STRIDE = WN + 4;
+    constexpr int SLOT = CB * 2 * 64;          // v4i per partial strip (one row block, hi and lo)
+    constexpr int PARTS = RB * 3 * SLOT * 16;  // bytes: three strips for each row block
+    constexpr int STAGE = 16 * C_STRIDE * 4;   // bytes of one wavefront's staged strip
+    __shared__ __attribute__((aligned(16))) uint8_t smem[PARTS + 4 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
+    int bx, by;
+    tile_of<XCD, G>(bx, by);
+    const int R0 = by * RB, P0 = bx * CB, RLAST = (M + 15) / 16 - 1;
+    const int m0 = R0 * 16, n0 = P0 * 16;
+    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
+
+    int32_t e_row[4];
+    float s_col[CB];
+#pragma unroll
+    for (int v = 0; v < 4; v++) e_row[v] = exps[min(m0 + q * 16 + out_row + v, M - 1)];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
+
+    const int NB = KB > q ? (KB - q + 3) / 4 : 0;
+    const uint8_t *ap[RB];
+    const uint8_t *bp[CB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) ap[r] = qf + ((size_t)min(R0 + r, RLAST) * KB + q) * 2048 + lane * 16;
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) bp[cb] = wv + (size_t)min(P0 + cb, P - 1) * b_panel + q * b_blk + lane * 16;
+
+    v4i acc_hi[RB][CB], acc_lo[RB][CB];
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+        for (int j = 0; j < CB; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
+
+    v4i fa[S][RB][2], fb[S][CB];
+#define TG_LOAD(st, ii)                                                                                \
+    do {                                                                                               \
+        const size_t t_ = (size_t)(ii) * 4;                                                            \
+        _Pragma("unroll") for (int r = 0; r < RB; r++) {                                               \
+            fa[st][r][0] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048);                          \
+            fa[st][r][1] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048 + 1024);                   \
+        }                                                                                              \
+        _Pragma("unroll") for (int cb = 0; cb < CB; cb++) fb[st][cb] =                                 \
+            *reinterpret_cast<const v4i *>(bp[cb] + t_ * b_blk);                                       \
+    } while (0)
+#define TG_MMA(st)                                                                                     \
+    do {                                                                                               \
+        _Pragma("unroll") for (int r = 0; r < RB; r++)                                                 \
+            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
+                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[st][r][0], fb[st][cb], acc_hi[r][cb], 0, 0, 0); \
+                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[st][r][1], fb[st][cb], acc_lo[r][cb], 0, 0, 0); \
+            }                                                                                          \
+    } while (0)
+
+    if (NB > 0) {
+        // Ring of S register stages: the wavefront's i-th block sits in stage i % S; loads past
+        // the end reload its last block (in bounds, never used).
+#pragma unroll
+        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, NB - 1));
+        int i = 0;
+        for (; i + S <= NB; i += S) {
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                TG_LOAD((s + S - 1) % S, min(i + s + S - 1, NB - 1));
+                TG_MMA(s);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < S - 1; j++)
+            if (i + j < NB) TG_MMA(j);
+    }
+#undef TG_LOAD
+#undef TG_MMA
+
+    TileStore<16, WN, C_STRIDE> out;
+    out.begin(lane, c, ldc, m0 + q * 16, n0, M, N, bias, accumulate);
+
+    // Row block r's strip from wavefront w != r goes to slot (r, w - (w > r)).
+    v4i *part = reinterpret_cast<v4i *>(smem);
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+        if (r == q) continue;
+        v4i *slot = part + (r * 3 + (q > r ? q - 1 : q)) * SLOT;
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {
+            slot[(cb * 2) * 64 + lane] = acc_hi[r][cb];
+            slot[(cb * 2 + 1) * 64 + lane] = acc_lo[r][cb];
+        }
+    }
+    v4i mine_hi[CB], mine_lo[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) {
+        mine_hi[cb] = acc_hi[0][cb];
+        mine_lo[cb] = acc_lo[0][cb];
+#pragma unroll
+        for (int r = 1; r < RB; r++)
+            if (r == q) {
+                mine_hi[cb] = acc_hi[r][cb];
+                mine_lo[cb] = acc_lo[r][cb];
+            }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 3; w++) {
+        const v4i *slot = part + (q * 3 + w) * SLOT;
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {
+            mine_hi[cb] += slot[(cb * 2) * 64 + lane];
+            mine_lo[cb] += slot[(cb * 2 + 1) * 64 + lane];
+        }
+    }
+
+    // Epilogue: the strip (element v of lane l: row 4 (l / 16) + v, column l % 16 of each 16 x 16
+    // block) is staged in the wavefront's own LDS area and stored in 16-byte runs.
+    float *tile = reinterpret_cast<float *>(smem + PARTS + q * STAGE);
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            tile[(out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                dequant(mine_hi[cb][v], mine_lo[cb][v], e_row[v], s_col[cb]);
+    __syncthreads();
+    out.finish(tile, c, ldc, m0 + q * 16, M, N, bias != nullptr, act, escale, accumulate);
+}
+
+template <int S, int XCD, int G>
+hipError_t launch_kq(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                     const EpiArgs &epi, hipStream_t s) {
+    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)4), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)4));
+    hipLaunchKernelGGL((gemm_i8_kq_kernel<S, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
                        w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
                        epi.accumulate, w.panel_stride, w.blk_stride);
     return hipGetLastError();
@@ -201,7 +445,7 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_q8_kernel(const uint8_t *__
                                                                size_t b_blk) {
     constexpr int WM = RB * 16, WN = CB * 16;
     constexpr int C_STRIDE = WN + 4;
-    __shared__ float staged[4][WM * C_STRIDE];
+    __shared__ __attribute__((aligned(16))) float staged[4][WM * C_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     int bx, by;
@@ -279,14 +523,15 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_q8_kernel(const uint8_t *__
                 TG_MMA(s);
             }
         }
-        if (t < KB) TG_MMA(0);
-        if constexpr (S > 2) {
-            if (t + 1 < KB) TG_MMA(1);
-        }
+#pragma unroll
+        for (int j = 0; j < S - 1; j++)
+            if (t + j < KB) TG_MMA(j);
     }
 #undef TG_LOAD
 #undef TG_MMA
 
+    TileStore<WM, WN, C_STRIDE> out;
+    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     float *tile = staged[wave];
 #pragma unroll
     for (int r = 0; r < RB; r++)
@@ -299,22 +544,7 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_q8_kernel(const uint8_t *__
                     e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(acc[r][cb][v], -e);
             }
     __syncthreads();
-    constexpr int TOTAL = WM * WN;
-    for (int i0 = lane; i0 < TOTAL; i0 += 8 * 64) {
-        float old[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
-            old[u] = (accumulate && i < TOTAL && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
-            if (i < TOTAL && row < M && col < N)
-                c[(size_t)row * ldc + col] = epilogue(tile[(i / WN) * C_STRIDE + i % WN], bias, (size_t)col, act,
-                                                      escale, accumulate != 0, &old[u]);
-        }
-    }
+    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
 }
 
 template <int RB, int CB, int S, int OCC, int XCD, int G>
@@ -362,19 +592,16 @@ __device__ __forceinline__ void wait_copies() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Waits until at most `ahead` stages of CPW copies each are still on the way (ahead < NS - 1).
-template <int CPW, int NS>
+// Waits until at most `ahead` stages of CPW copies each are still on the way (ahead <= A, with A
+// = NS - 2 at the top of the recursion). `ahead` is uniform, so the branches are scalar.
+template <int CPW, int A>
 __device__ __forceinline__ void wait_stages(int ahead) {
-    static_assert(NS >= 2 && NS <= 4, "ring of 2 to 4 stages");
-    if constexpr (NS == 4) {
-        if (ahead >= 2) wait_copies<2 * CPW>();
-        else if (ahead == 1) wait_copies<CPW>();
-        else wait_copies<0>();
-    } else if constexpr (NS == 3) {
-        if (ahead >= 1) wait_copies<CPW>();
-        else wait_copies<0>();
-    } else {
+    static_assert(A >= 0 && A * CPW < 64, "vmcnt holds 6 bits");
+    if constexpr (A == 0) {
         wait_copies<0>();
+    } else {
+        if (ahead >= A) wait_copies<A * CPW>();
+        else wait_stages<CPW, A - 1>(ahead);
     }
 }
 
@@ -447,7 +674,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
             const int t = t0 + s;
             if (t < KB) {
                 // k-block t sits in buffer s; up to NS - 2 later k-blocks may still be on the way.
-                wait_stages<CPW, NS>(min(NS - 2, KB - 1 - t));
+                wait_stages<CPW, NS - 2>(min(NS - 2, KB - 1 - t));
                 __syncthreads();
                 if (t + NS - 1 < KB) TG_ISSUE((s + NS - 1) % NS, t + NS - 1);
                 const uint8_t *st = smem + s * STAGE;
@@ -471,6 +698,8 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         }
     }
 #undef TG_ISSUE
+    TileStore<WM, WN, C_STRIDE> out;
+    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
 
     float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
@@ -483,22 +712,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                 tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
                     dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
     __syncthreads();
-    constexpr int TOTAL = WM * WN;
-    for (int i0 = lane; i0 < TOTAL; i0 += 8 * 64) {
-        float old[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
-            old[u] = (accumulate && i < TOTAL && row < M && col < N) ? c[(size_t)row * ldc + col] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * 64, row = m0 + i / WN, col = n0 + i % WN;
-            if (i < TOTAL && row < M && col < N)
-                c[(size_t)row * ldc + col] = epilogue(tile[(i / WN) * C_STRIDE + i % WN], bias, (size_t)col, act,
-                                                      escale, accumulate != 0, &old[u]);
-        }
-    }
+    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
 }
 
 template <int TM, int TN, int NS, int XCD, int G>
@@ -531,9 +745,12 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     }
     if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     // Mid-size products: LDS staging pays from 2048 outputs (the direct kernel's duplicate operand
-    // loads dominate there); narrower ones keep the direct kernel.
+    // loads dominate there); narrower ones keep the direct kernel, or the k-split kernel when the
+    // inputs are long (at least 32 k-blocks) and the tiles too few to fill the CUs twice.
     if (w.panels >= 128) return launch_lds<4, 4, 3, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
-    return launch_tile<2, 2, 3, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512)
+        return launch_kq<5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    return launch_tile<2, 2, 6, 1, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 
 }  // namespace tg
