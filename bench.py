@@ -717,7 +717,8 @@ def main():
     traffic = load_traffic()
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_INT8 / 1e12,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8, 4), "traffic": traffic,
-                "kernel": "gemm_lds_kernel<4,4,3> (n >= 2048) and gemm_i8_kernel<2,2,3> (n = 1024)", "avg_launch_us": round(gemm_us / len(per_shape), 3),
+                "kernel": "gemm_lds_kernel<4,4,3> (n >= 2048), gemm_i8_kq_kernel<5> (k = 4096, n = 1024) and "
+                          "gemm_i8_kernel<2,2,6> (k = 1024, n = 1024)", "avg_launch_us": round(gemm_us / len(per_shape), 3),
                 "ops_per_launch_avg": ops / len(per_shape),
                 "mfma_int8_ops_per_launch_avg": 2 * ops / len(per_shape),
                 "mfma_busy_frac": round(2 * achieved / PEAK_INT8, 4),
