@@ -127,21 +127,19 @@ __device__ __forceinline__ void tile_of(int &bx, int &by) {
     }
 }
 
-template <int RB, int CB, int S, int KG, int OCC, int XCD, int G>
-__global__ __launch_bounds__(THREADS * KG, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
-                                                                    const int32_t *__restrict__ exps, int M,
-                                                                    const uint8_t *__restrict__ wv,
-                                                                    const float *__restrict__ scales, int N, int P,
-                                                                    int KB, float *__restrict__ c, size_t ldc,
-                                                                    const float *__restrict__ bias, uint32_t act,
-                                                                    float escale, int accumulate, size_t b_panel,
-                                                                    size_t b_blk) {
+template <int RB, int CB, int S, int OCC, int XCD, int G>
+__global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
+                                                               const int32_t *__restrict__ exps, int M,
+                                                               const uint8_t *__restrict__ wv,
+                                                               const float *__restrict__ scales, int N, int P, int KB,
+                                                               float *__restrict__ c, size_t ldc,
+                                                               const float *__restrict__ bias, uint32_t act,
+                                                               float escale, int accumulate, size_t b_panel,
+                                                               size_t b_blk) {
     constexpr int WM = RB * 16, WN = CB * 16;
     constexpr int C_STRIDE = WN + 4;  // f32 per row of a wavefront's staged tile
-    constexpr int NACC = RB * CB * 2;  // accumulators (v4i) per lane
-    constexpr int STAGED = 4 * WM * C_STRIDE * 4, PARTIALS = (KG - 1) * 4 * NACC * 64 * 16;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGED > PARTIALS ? STAGED : PARTIALS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = tid >> 8;
+    __shared__ __attribute__((aligned(16))) float staged[4][WM * C_STRIDE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     int bx, by;
     tile_of<XCD, G>(bx, by);
@@ -160,16 +158,14 @@ __global__ __launch_bounds__(THREADS * KG, OCC) void gemm_i8_kernel(const uint8_
 #pragma unroll
     for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
 
-    // Wavefront group grp takes the k-blocks grp, grp + KG, grp + 2 KG, ...: NB of them. Operand
-    // blocks: row block R of the QA at (R * KB + t) * 2048 (+1024 for the lo digits), panel p of
-    // the weights at p * b_panel + t * b_blk.
-    const int NB = KB > grp ? (KB - grp + KG - 1) / KG : 0;
+    // Operand blocks of this wavefront: row block R of the QA at (R * KB + t) * 2048 (+1024 for
+    // the lo digits), panel p of the weights at p * b_panel + t * b_blk.
     const uint8_t *ap[RB];
     const uint8_t *bp[CB];
 #pragma unroll
-    for (int r = 0; r < RB; r++) ap[r] = qf + ((size_t)min(R0 + r, RLAST) * KB + grp) * 2048 + lane * 16;
+    for (int r = 0; r < RB; r++) ap[r] = qf + (size_t)min(R0 + r, RLAST) * KB * 2048 + lane * 16;
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) bp[cb] = wv + (size_t)min(P0 + cb, P - 1) * b_panel + grp * b_blk + lane * 16;
+    for (int cb = 0; cb < CB; cb++) bp[cb] = wv + (size_t)min(P0 + cb, P - 1) * b_panel + lane * 16;
 
     v4i acc_hi[RB][CB], acc_lo[RB][CB];
 #pragma unroll
@@ -178,9 +174,9 @@ __global__ __launch_bounds__(THREADS * KG, OCC) void gemm_i8_kernel(const uint8_
         for (int j = 0; j < CB; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
 
     v4i fa[S][RB][2], fb[S][CB];
-#define TG_LOAD(st, ii)                                                                                \
+#define TG_LOAD(st, tt)                                                                                \
     do {                                                                                               \
-        const size_t t_ = (size_t)(ii) * KG;                                                           \
+        const size_t t_ = (size_t)(tt);                                                                \
         _Pragma("unroll") for (int r = 0; r < RB; r++) {                                               \
             fa[st][r][0] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048);                          \
             fa[st][r][1] = *reinterpret_cast<const v4i *>(ap[r] + t_ * 2048 + 1024);                   \
@@ -197,84 +193,51 @@ __global__ __launch_bounds__(THREADS * KG, OCC) void gemm_i8_kernel(const uint8_
             }                                                                                          \
     } while (0)
 
-    if (NB > 0) {
-        // Ring of S register stages: the group's i-th block sits in stage i % S. Loads past the
-        // end reload the group's last block (in bounds, never used).
+    if (KB > 0) {
+        // Ring of S register stages: block t sits in stage t % S. Loads past the end reload the
+        // last block (in bounds, never used).
 #pragma unroll
-        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, NB - 1));
-        int i = 0;
-        for (; i + S <= NB; i += S) {
+        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, KB - 1));
+        int t = 0;
+        for (; t + S <= KB; t += S) {
 #pragma unroll
             for (int s = 0; s < S; s++) {
-                TG_LOAD((s + S - 1) % S, min(i + s + S - 1, NB - 1));
+                TG_LOAD((s + S - 1) % S, min(t + s + S - 1, KB - 1));
                 TG_MMA(s);
             }
         }
-        // At most S - 1 blocks remain: block i + j is already in stage j.
+        // At most S - 1 blocks remain: block t + j is already in stage j.
 #pragma unroll
         for (int j = 0; j < S - 1; j++)
-            if (i + j < NB) TG_MMA(j);
+            if (t + j < KB) TG_MMA(j);
     }
 #undef TG_LOAD
 #undef TG_MMA
 
+    // Epilogue: the wavefront stages its f32 sums in LDS (element v of lane l holds row
+    // 4 (l / 16) + v, column l % 16 of its 16 x 16 block), then stores them in 16-byte runs.
     TileStore<WM, WN, C_STRIDE> out;
-    if (grp == 0) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
-    if constexpr (KG > 1) {
-        // The other groups hand their integer sums to group 0 through LDS; integer sums are exact,
-        // so the k-split does not change any result.
-        v4i *part = reinterpret_cast<v4i *>(smem);
-        if (grp > 0) {
+    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    float *tile = staged[wave];
 #pragma unroll
-            for (int r = 0; r < RB; r++)
+    for (int r = 0; r < RB; r++)
 #pragma unroll
-                for (int cb = 0; cb < CB; cb++) {
-                    const int a = ((grp - 1) * 4 + wave) * NACC + (r * CB + cb) * 2;
-                    part[a * 64 + lane] = acc_hi[r][cb];
-                    part[(a + 1) * 64 + lane] = acc_lo[r][cb];
-                }
-        }
-        __syncthreads();
-        if (grp == 0) {
+        for (int cb = 0; cb < CB; cb++)
 #pragma unroll
-            for (int g = 1; g < KG; g++)
-#pragma unroll
-                for (int r = 0; r < RB; r++)
-#pragma unroll
-                    for (int cb = 0; cb < CB; cb++) {
-                        const int a = ((g - 1) * 4 + wave) * NACC + (r * CB + cb) * 2;
-                        acc_hi[r][cb] += part[a * 64 + lane];
-                        acc_lo[r][cb] += part[(a + 1) * 64 + lane];
-                    }
-        }
-        __syncthreads();  // the partials are read before the LDS holds the staged outputs
-    }
-
-    // Epilogue (group 0): the wavefront stages its f32 sums in LDS (element v of lane l holds row
-    // 4 (l / 16) + v, column l % 16 of its 16 x 16 block), then stores them in 16-byte runs. Every
-    // wavefront passes the same barriers.
-    float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
-    if (grp == 0) {
-#pragma unroll
-        for (int r = 0; r < RB; r++)
-#pragma unroll
-            for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
-                        dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
-    }
+            for (int v = 0; v < 4; v++)
+                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                    dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
     __syncthreads();
-    if (grp == 0) out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
 }
 
-template <int RB, int CB, int S, int KG, int OCC, int XCD, int G>
+template <int RB, int CB, int S, int OCC, int XCD, int G>
 hipError_t launch_tile(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                        const EpiArgs &epi, hipStream_t s) {
     const size_t bm = 2 * RB * 16, bn = 2 * CB * 16;
     dim3 grid((unsigned)div_ceil(w.panels * PANEL, bn), (unsigned)div_ceil(m, bm));
-    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, KG, OCC, XCD, G>), grid, dim3(THREADS * KG), 0, s, qf, exps, (int)m,
-                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
+    hipLaunchKernelGGL((gemm_i8_kernel<RB, CB, S, OCC, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
+                       w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
                        epi.accumulate, w.panel_stride, w.blk_stride);
     return hipGetLastError();
 }
@@ -752,7 +715,7 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     if (w.panels >= 128) return launch_lds<4, 4, 3, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
     if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512)
         return launch_kq<5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
-    return launch_tile<2, 2, 6, 1, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 
 }  // namespace tg
