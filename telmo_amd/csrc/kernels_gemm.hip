@@ -624,6 +624,26 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         const size_t t_ = (size_t)(tt);                                                                \
         _Pragma("unroll") for (int i = 0; i < CPW; i++) copy_to_lds(g[i] + t_ * gs[i], st_ + (wave + 4 * i) * 1024); \
     } while (0)
+    // This wavefront's operands of one k-block from the stage at st: row blocks wm * RB + r (hi and
+    // lo digits) and panels wn * CB + cb.
+    auto read_frags = [&](const uint8_t *st, v4i (&fa)[RB][2], v4i (&fb)[CB]) {
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2) * 1024 + lane * 16);
+            fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2 + 1) * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+            fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
+    };
+#define TG_MMA(fa, fb)                                                                                 \
+    do {                                                                                               \
+        _Pragma("unroll") for (int r = 0; r < RB; r++)                                                 \
+            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
+                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][0], (fb)[cb], acc_hi[r][cb], 0, 0, 0); \
+                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][1], (fb)[cb], acc_lo[r][cb], 0, 0, 0); \
+            }                                                                                          \
+    } while (0)
 
     v4i acc_hi[RB][CB], acc_lo[RB][CB];
 #pragma unroll
@@ -642,27 +662,14 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                 wait_stages<CPW, NS - 2>(min(NS - 2, KB - 1 - t));
                 __syncthreads();
                 if (t + NS - 1 < KB) TG_ISSUE((s + NS - 1) % NS, t + NS - 1);
-                const uint8_t *st = smem + s * STAGE;
                 v4i fa[RB][2], fb[CB];
-#pragma unroll
-                for (int r = 0; r < RB; r++) {
-                    fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2) * 1024 + lane * 16);
-                    fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2 + 1) * 1024 + lane * 16);
-                }
-#pragma unroll
-                for (int cb = 0; cb < CB; cb++)
-                    fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
-#pragma unroll
-                for (int r = 0; r < RB; r++)
-#pragma unroll
-                    for (int cb = 0; cb < CB; cb++) {
-                        acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[r][0], fb[cb], acc_hi[r][cb], 0, 0, 0);
-                        acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[r][1], fb[cb], acc_lo[r][cb], 0, 0, 0);
-                    }
+                read_frags(smem + s * STAGE, fa, fb);
+                TG_MMA(fa, fb);
             }
         }
     }
 #undef TG_ISSUE
+#undef TG_MMA
     TileStore<WM, WN, C_STRIDE> out;
     out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
