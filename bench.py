@@ -742,16 +742,20 @@ def main():
             # oracle's over the first frames are its first tokens
             tdt["cpu_port_tokens_match"] = gpu == port_toks
             tdt["oracle_sample_tokens_match"] = gpu[:len(oracle_toks)] == oracle_toks
-    value = ops / (graph_ms * 1e-3) / 1e12
+    # The step runs either as a captured HIP graph or launched eagerly on one stream; both run the
+    # same kernels on the same resident inputs, and the faster of the two is the step time.
+    step_ms = min(graph_ms, eager_ms)
+    value = ops / (step_ms * 1e-3) / 1e12
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(graph_ms, 5), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "conformer layer projection set: 8 int8 GEMMs + GLU at T=750 frames "
                                "(60 s audio), d=1024, ff=4096, conv 2048",
                    "frames": T_FRAMES, "ops_per_step": ops, "hbm_bytes_per_step": bytes_of(T_FRAMES),
-                   "ms_per_step_eager": round(eager_ms, 5), "timing": "hip graph replay of the step",
-                   "audio_s_per_s_one_layer": round(60.0 / (graph_ms * 1e-3), 1)},
+                   "ms_per_step_eager": round(eager_ms, 5), "ms_per_step_graph": round(graph_ms, 5),
+                   "timing": "HIP events around the timed steps; the faster of eager launches and HIP graph replay",
+                   "audio_s_per_s_one_layer": round(60.0 / (step_ms * 1e-3), 1)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gemv": gemv,
