@@ -5,18 +5,18 @@
 // v_mfma_i32_16x16x64_i8 and are exact, so the result does not depend on tiling, k-order or
 // splits; the f32 arithmetic happens once per output in the epilogue.
 //
-// Operands come straight from global memory into registers, with no LDS in the main loop and no
-// barriers: both the quantised rows (fragment-major QA) and the weights (MFMA layout) store each
-// 16 x 64 MFMA operand as 1 KB in lane order, so one 16-byte load per lane is one operand, fully
-// coalesced. A workgroup is 2 x 2 independent wavefronts; the two wavefronts that share an operand
-// sit on one CU, so the second load of it hits L1. Each wavefront keeps S k-blocks of operands in
-// flight (a register ring) so loads overlap the MFMAs. Measured on MI355X this beats an LDS-staged
-// pipeline: LDS writes run at about 64 B/clk/CU, and the two-digit A tile doubles them.
-//
-// Tiles: wavefront RB x CB MFMA blocks of 16 x 16 (workgroup 32 RB x 32 CB outputs). The launcher
-// takes 2 x 2 (64 x 64, tiles walked four tile-rows at a time) for short products and, when
-// 128 x 128 tiles fill the chip twice over, the LDS-staged kernel below (tiles in XCD-contiguous
-// runs).
+// Both the quantised rows (fragment-major QA) and the weights (MFMA layout) store each 16 x 64
+// MFMA operand as 1 KB in lane order, so one 16-byte load per lane is one operand, fully coalesced.
+// Three kernels share that layout and the epilogue (TileStore):
+//   gemm_lds_kernel    operands copied from global memory straight into an LDS ring
+//                      (global_load_lds_dwordx4), one copy per workgroup: 128 x 128 tiles when
+//                      they fill the chip twice over, 64 x 64 tiles for products of >= 2048 outputs;
+//   gemm_i8_kernel     2 x 2 independent wavefronts loading their operands straight into a
+//                      register ring (no LDS, no barriers in the loop): narrower products;
+//   gemm_i8_kq_kernel  the narrower products with long inputs: each wavefront takes the whole
+//                      64 x 64 tile over a quarter of the k-blocks, and the integer partial sums
+//                      meet in LDS.
+// launch_gemm_i8 at the end picks one by shape.
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -33,12 +33,12 @@ constexpr int THREADS = 256;
 // ...: per run one 16-byte load of the old outputs (when accumulating), one 16-byte LDS read of the
 // staged sums (rows C_STRIDE floats apart) and one 16-byte store, marked nontemporal: the outputs
 // are read by the next kernel, not this one, and streaming them out as they are stored leaves less
-// to write back when the kernel ends (1-1.5 us less per launch on the 4096-output products). begin() issues the loads of the
-// bias and old outputs, before the sums are staged, so their latency overlaps the staging (for
-// tiles of up to eight runs per lane; larger ones load in finish(), where the accumulators no
-// longer hold registers); finish() stores, and nothing waits for a store, so the wavefront ends
-// once its stores are issued. Runs past the right edge of c, or in a c or ldc not 16-byte aligned,
-// go one output at a time; rows past M are skipped.
+// to write back when the kernel ends (1-1.5 us less per launch on the 4096-output products).
+// begin() issues the loads of the bias and old outputs before the sums are staged, so their
+// latency overlaps the staging (for tiles of up to eight runs per lane; larger ones load in
+// finish(), where the accumulators no longer hold registers). finish() stores, and nothing waits
+// for a store, so the wavefront ends once its stores are issued. Runs past the right edge of c, or
+// in a c or ldc not 16-byte aligned, go one output at a time; rows past M are skipped.
 template <int WM, int WN, int C_STRIDE>
 struct TileStore {
     static constexpr int RPR = WN / 4, STEP = 64 / RPR, PER = WM / STEP;
@@ -105,6 +105,10 @@ struct TileStore {
     }
 };
 
+// Order in which workgroups take tiles. Workgroup L of a launch goes to XCD L % 8 (each XCD has
+// its own L2). XCD: hand each XCD a contiguous run of tiles (rows of the tile grid), so the A row
+// blocks its tiles share stay in its L2. G > 0: walk the tiles G tile-rows at a time, column by
+// column, so a weight panel is reused by G row blocks while it is hot.
 template <int XCD, int G>
 __device__ __forceinline__ void tile_of(int &bx, int &by) {
     bx = blockIdx.x;
