@@ -239,9 +239,99 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, size_t 
     }
 }
 
+// The same arithmetic with the rows staged in LDS: R rows of n values (n <= LN_LDS_MAX, rows
+// LN_PAD floats apart so the four rows of a wavefront's partial sums fall in different banks) are
+// read once with 16-byte loads when every row is 16-byte aligned, the sixteen partials of each row
+// are summed from LDS in the order above, and the outputs go out in 16-byte runs when out's rows
+// are aligned. Every input of the block is read before any output is written, so out may be x.
+constexpr int LN_PAD = 16, LN_LDS_MAX = 16384 - LN_PAD;  // one padded row fits 64 KB
+
+__global__ __launch_bounds__(256) void layer_norm_lds_kernel(const float *x, size_t ldx, size_t m, int n, int R,
+                                                             const float *__restrict__ gamma,
+                                                             const float *__restrict__ beta, float eps, float *out,
+                                                             size_t ldo) {
+    extern __shared__ __attribute__((aligned(16))) float rows_s[];
+    __shared__ float stat[16][2];
+    const int tid = threadIdx.x, stride = n + LN_PAD;
+    const size_t row0 = (size_t)blockIdx.x * R;
+    const int nr = (int)min((size_t)R, m - row0);
+    const bool vin = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float)) % 16 == 0) && n % 4 == 0;
+    if (vin) {
+        const int q = n / 4;
+        for (int c = tid; c < nr * q; c += 256) {
+            const int r = c / q, i = 4 * (c - r * q);
+            *reinterpret_cast<float4 *>(rows_s + r * stride + i) =
+                *reinterpret_cast<const float4 *>(x + (row0 + r) * ldx + i);
+        }
+    } else {
+        for (int c = tid; c < nr * n; c += 256) {
+            const int r = c / n, i = c - r * n;
+            rows_s[r * stride + i] = x[(row0 + r) * ldx + i];
+        }
+    }
+    __syncthreads();
+    const int j = tid & 15, r = tid >> 4;
+    if (r < nr) {
+        const float *xr = rows_s + r * stride;
+        float s = 0.0f;
+        for (int i = j; i < n; i += 16) s = s + xr[i];
+        s = s + __shfl_xor(s, 8, 16);
+        s = s + __shfl_xor(s, 4, 16);
+        s = s + __shfl_xor(s, 2, 16);
+        s = s + __shfl_xor(s, 1, 16);
+        const float mean = s / (float)n;
+        float q = 0.0f;
+        for (int i = j; i < n; i += 16) {
+            const float d = xr[i] - mean;
+            q = __builtin_fmaf(d, d, q);
+        }
+        q = q + __shfl_xor(q, 8, 16);
+        q = q + __shfl_xor(q, 4, 16);
+        q = q + __shfl_xor(q, 2, 16);
+        q = q + __shfl_xor(q, 1, 16);
+        if (j == 0) {
+            stat[r][0] = mean;
+            stat[r][1] = 1.0f / __builtin_sqrtf(q / (float)n + eps);
+        }
+    }
+    __syncthreads();
+    const bool vout = ((reinterpret_cast<uintptr_t>(out) | ldo * sizeof(float)) % 16 == 0) && n % 4 == 0 &&
+                      (reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 == 0;
+    if (vout) {
+        const int q = n / 4;
+        for (int c = tid; c < nr * q; c += 256) {
+            const int rr = c / q, i = 4 * (c - rr * q);
+            const float mean = stat[rr][0], rstd = stat[rr][1];
+            const float4 v = *reinterpret_cast<const float4 *>(rows_s + rr * stride + i);
+            const float4 g = *reinterpret_cast<const float4 *>(gamma + i);
+            const float4 b = *reinterpret_cast<const float4 *>(beta + i);
+            float4 o;
+            o.x = __builtin_fmaf((v.x - mean) * rstd, g.x, b.x);
+            o.y = __builtin_fmaf((v.y - mean) * rstd, g.y, b.y);
+            o.z = __builtin_fmaf((v.z - mean) * rstd, g.z, b.z);
+            o.w = __builtin_fmaf((v.w - mean) * rstd, g.w, b.w);
+            *reinterpret_cast<float4 *>(out + (row0 + rr) * ldo + i) = o;
+        }
+    } else {
+        for (int c = tid; c < nr * n; c += 256) {
+            const int rr = c / n, i = c - rr * n;
+            const float d = (rows_s[rr * stride + i] - stat[rr][0]) * stat[rr][1];
+            out[(row0 + rr) * ldo + i] = __builtin_fmaf(d, gamma[i], beta[i]);
+        }
+    }
+}
+
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
+    if (n <= (size_t)LN_LDS_MAX) {
+        // Up to sixteen rows and 64 KB of LDS per block.
+        const int R = (int)min((size_t)16, (size_t)16384 / (n + LN_PAD));
+        const size_t lds = (size_t)R * (n + LN_PAD) * sizeof(float);
+        hipLaunchKernelGGL(layer_norm_lds_kernel, dim3((unsigned)div_ceil(m, (size_t)R)), dim3(256), lds, s, x, ldx, m,
+                           (int)n, R, gamma, beta, eps, out, ldo);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)div_ceil(m, (size_t)16)), dim3(256), 0, s, x, ldx, m, (int)n,
                        gamma, beta, eps, out, ldo);
     return hipGetLastError();
