@@ -70,13 +70,13 @@ def bytes_of(m):
 
 def run_layer(kern, W, bufs, T, dw=None):
     """The layer's products in order: FFN (SiLU, half-step residual), QKV, attention output (the V
-    third of QKV standing in for attention), the conv module's pointwise pair around the GLU (and,
-    given dw = (weights [DW_KERNEL, D], bias [D]), the depthwise convolution + SiLU between GLU and
-    pw2; dw[2] utterances of T / dw[2] frames each), and the second FFN. bufs holds x [T, D], h [T, FF], qkv [T, 3D], g [T, CONV], u and d
-    [T, D]."""
+    third of QKV standing in for attention), the conv module's pointwise pair around the GLU (pw1
+    and the GLU as one fused GEMM; given dw = (weights [DW_KERNEL, D], bias [D], utterances), the
+    depthwise convolution + SiLU between GLU and pw2, each of the utterances' T / dw[2] frames on
+    its own), and the second FFN. bufs holds x [T, D], h [T, FF], qkv [T, 3D], u and d [T, D]."""
     from telmo_amd import Act, Epilogue
 
-    x, h, qkv, g, u = (bufs[key] for key in ("x", "h", "qkv", "g", "u"))
+    x, h, qkv, u = (bufs[key] for key in ("x", "h", "qkv", "u"))
     silu = Epilogue(act=Act.SILU)
     half_acc = Epilogue(scale=0.5, accumulate=True)
     acc = Epilogue(accumulate=True)
@@ -84,8 +84,7 @@ def run_layer(kern, W, bufs, T, dw=None):
     kern.linear_device(h, T, W["ff1_down"], x, half_acc)
     kern.linear_device(x, T, W["qkv"], qkv)
     kern.matmul_device(qkv[:, 2 * D:], 3 * D, T, W["att_out"], x, D, acc, a_len=qkv.numel() - 2 * D)
-    kern.linear_device(x, T, W["pw1"], g)
-    kern.glu_device(g, CONV, T, D, u, D)
+    kern.linear_glu_device(x, T, W["pw1"], u)  # pw1 with the GLU in its epilogue
     if dw is not None:
         seqs = dw[2]  # equal-length utterances stacked along the rows, each convolved on its own
         kern.dwconv1d_device(u, D, T // seqs, D, dw[0], DW_KERNEL, dw[1], bufs["d"], D, act=Act.SILU, batch=seqs)
@@ -101,7 +100,6 @@ def layer_buffers(T, dev="cuda"):
     return {"x": torch.empty((T, D), dtype=torch.float32, device=dev),
             "h": torch.empty((T, FF), dtype=torch.float32, device=dev),
             "qkv": torch.empty((T, 3 * D), dtype=torch.float32, device=dev),
-            "g": torch.empty((T, CONV), dtype=torch.float32, device=dev),
             "u": torch.empty((T, D), dtype=torch.float32, device=dev),
             "d": torch.empty((T, D), dtype=torch.float32, device=dev)}
 

@@ -154,6 +154,20 @@ int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t ld
 int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                const tg_weights *w, float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
 
+/* out = glu(epi(a . w)): the convolution module's pointwise_conv1 followed by its GLU
+ * (src/parakeet.rs:1087-1104, src/granite.rs:881-899: Kernels::linear into [m, n], then
+ * out[r, j] = g[r, j] * sigmoid(g[r, n / 2 + j]) for j < n / 2 through Kernels::glu), giving
+ * exactly what tg_linear_device followed by tg_glu_device writes. For int8 weights in fast mode
+ * with n a multiple of 64, past the GEMV sizes, the GLU runs in the GEMM's epilogue and the
+ * [m, n] product never reaches memory; otherwise the two steps run through a context-owned
+ * buffer. out is [m, ldo] (ldo >= n / 2, out_len >= (m - 1) ldo + n / 2); epi may carry a bias
+ * of n values, an activation and a scale, applied before the GLU, but not accumulate
+ * (TG_ERR_ARG). n odd: TG_ERR_SHAPE. a holds m rows of k; a and out must not overlap. Device
+ * pointers, queued on the stream. No single counterpart in the reference, which runs the two
+ * kernels one after the other. */
+int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *out,
+                         size_t out_len, size_t ldo, const tg_epilogue *epi);
+
 /* ---- row kernels -------------------------------------------------------------------------- */
 
 /* out[r, j] = x[r, j] * sigmoid(x[r, half + j]) for j < half (the GLU of a convolution module),

@@ -49,6 +49,7 @@ SIGNATURES = {
     "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
+    "tg_linear_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _sz, _p]),
     "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, ctypes.c_float, _p, _sz]),
     "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, _sz, _sz, _u32, _p, _sz]),
     "tg_tdt_create": (ctypes.c_int, [_p, _p, ctypes.POINTER(_p)]),

@@ -34,6 +34,9 @@ struct tg_ctx {
     // Pinned host staging of the same: rows are gathered here so each direction is one DMA.
     float *hst = nullptr;
     size_t hst_cap = 0;
+    // The product before the GLU, when tg_linear_glu_device cannot fuse them.
+    float *dg = nullptr;
+    size_t dg_cap = 0;
 };
 
 struct tg_weights {
@@ -267,7 +270,8 @@ void tg_ctx_destroy(tg_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (void *p : {(void *)ctx->qa, (void *)ctx->exps, (void *)ctx->da, (void *)ctx->dc, (void *)ctx->dbias})
+    for (void *p : {(void *)ctx->qa, (void *)ctx->exps, (void *)ctx->da, (void *)ctx->dc, (void *)ctx->dbias,
+                    (void *)ctx->dg})
         if (p) (void)hipFree(p);
     if (ctx->hst) (void)hipHostFree(ctx->hst);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -489,6 +493,44 @@ int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, tg::launch_glu(x, ldx, m, half, out, ldo, ctx->stream));
+    return TG_OK;
+}
+
+int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *out,
+                         size_t out_len, size_t ldo, const tg_epilogue *epi) {
+    if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
+    const size_t k = w->d.k, n = w->d.n, half = n / 2;
+    if (n % 2) return fail(ctx, TG_ERR_SHAPE, "the product's outputs must be an even count");
+    if (epi && epi->accumulate) return fail(ctx, TG_ERR_ARG, "the GLU's input is not accumulated");
+    if (m == 0 || n == 0) return TG_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    // tg_linear_device's checks on a and the epilogue, then the GLU output's.
+    if (a_len < (m - 1) * k + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
+    if (!a && k > 0) return fail(ctx, TG_ERR_NULL, "a is null");
+    if (ldo < half) return fail(ctx, TG_ERR_SHAPE, "ldo must be >= n / 2");
+    if (out_len < (m - 1) * ldo + half) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (!out) return fail(ctx, TG_ERR_NULL, "out is null");
+    if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    const tg::EpiArgs e = epi_args(epi, nullptr, false);
+    const tg::DeviceWeights &d = w->d;
+    int rc;
+    if (ctx->mode == TG_MODE_FAST && d.precision == TG_INT8 && d.k <= tg::MAX_K_INT && tg::gemm_glu_fits(n) &&
+        !tg::gemv_fits(m, k, a, k, d.precision)) {
+        // One GEMM whose epilogue applies the GLU: the product never leaves the chip.
+        if ((rc = grow(ctx, ctx->qa, ctx->qa_cap, tg::qa_bytes(m, k)))) return rc;
+        if ((rc = grow(ctx, ctx->exps, ctx->exps_cap, m * sizeof(int32_t)))) return rc;
+        TG_HIP(ctx, tg::launch_quantize_rows(a, k, m, k, ctx->qa, ctx->exps, ctx->stream));
+        TG_HIP(ctx, tg::launch_gemm_i8_glu(ctx->qa, ctx->exps, m, d, out, ldo, e, ctx->stream));
+    } else {
+        // The product into the context's buffer, then the GLU.
+        if ((rc = grow(ctx, ctx->dg, ctx->dg_cap, m * n * sizeof(float)))) return rc;
+        if ((rc = run_device(ctx, a, k, m, w, ctx->dg, n, e))) return rc;
+        TG_HIP(ctx, tg::launch_glu(ctx->dg, n, m, half, out, ldo, ctx->stream));
+    }
+    ctx->err.clear();
     return TG_OK;
 }
 

@@ -105,6 +105,52 @@ struct TileStore {
     }
 };
 
+// The GLU of a pair of staged tiles, the a and b halves of the same rows and columns (rows
+// C_STRIDE floats apart): out[r, col] = va / (1 + exp(0 - vb)) with va and vb the sums through
+// the epilogue (bias, activation, scale; no accumulation), the values tg_linear_device writes and
+// tg_glu_device then combines. The b half's bias sits Nh columns on. Runs of four outputs per lane
+// as TileStore, 16-byte nontemporal stores when out's rows are 16-byte aligned.
+template <int WM, int WN, int C_STRIDE>
+__device__ __forceinline__ void glu_store(const float *ta, const float *tb, int lane, float *__restrict__ out,
+                                          size_t ldo, int m0, int n0, int M, int Nh, const float *__restrict__ bias,
+                                          uint32_t act, float escale) {
+    constexpr int RPR = WN / 4, STEP = 64 / RPR, PER = WM / STEP;
+    static_assert(WN % 4 == 0 && 64 % RPR == 0 && WM % STEP == 0, "whole runs per lane");
+    const int cr = lane % RPR, r0 = lane / RPR, col = n0 + 4 * cr;
+    const bool vec = ((reinterpret_cast<uintptr_t>(out) | ldo * sizeof(float)) % 16 == 0) && col + 4 <= Nh;
+    v4f ba = {0.0f, 0.0f, 0.0f, 0.0f}, bb = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (col + j < Nh) {
+                ba[j] = bias[col + j];
+                bb[j] = bias[Nh + col + j];
+            }
+    }
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int row = m0 + r0 + u * STEP;
+        if (row >= M) continue;
+        const v4f a = *reinterpret_cast<const v4f *>(ta + (r0 + u * STEP) * C_STRIDE + 4 * cr);
+        const v4f b = *reinterpret_cast<const v4f *>(tb + (r0 + u * STEP) * C_STRIDE + 4 * cr);
+        v4f o;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float va = epilogue_vals(a[j], bias != nullptr, ba[j], act, escale, false, 0.0f);
+            const float vb = epilogue_vals(b[j], bias != nullptr, bb[j], act, escale, false, 0.0f);
+            o[j] = va / (1.0f + exp_simd(0.0f - vb));
+        }
+        float *dst = out + (size_t)row * ldo + col;
+        if (vec) {
+            __builtin_nontemporal_store(o, reinterpret_cast<v4f *>(dst));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (col + j < Nh) dst[j] = o[j];
+        }
+    }
+}
+
 // Order in which workgroups take tiles. Workgroup L of a launch goes to XCD L % 8 (each XCD has
 // its own L2). XCD: hand each XCD a contiguous run of tiles (rows of the tile grid), so the A row
 // blocks its tiles share stay in its L2. G > 0: walk the tiles G tile-rows at a time, column by
@@ -574,7 +620,7 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     }
 }
 
-template <int TM, int TN, int NS, int XCD, int G>
+template <int TM, int TN, int NS, int XCD, int G, int GLU>
 __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__restrict__ qf,
                                                               const int32_t *__restrict__ exps, int M,
                                                               const uint8_t *__restrict__ wv,
@@ -582,7 +628,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                                                               float *__restrict__ c, size_t ldc,
                                                               const float *__restrict__ bias, uint32_t act,
                                                               float escale, int accumulate, size_t b_panel,
-                                                              size_t b_blk) {
+                                                              size_t b_blk, int hp) {
     constexpr int RB = TM / 2, CB = TN / 2;  // 16 x 16 blocks per wavefront
     constexpr int CH = 2 * TM + TN;          // 1 KB chunks per stage
     static_assert(CH % 4 == 0, "the chunks split evenly over four wavefronts");
@@ -597,6 +643,13 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
     const int R0 = by * TM, P0 = bx * TN, RLAST = (M + 15) / 16 - 1;
     const int m0 = by * TM * 16 + wm * WM, n0 = bx * TN * 16 + wn * WN;
     const int out_col = lane & 15, out_row = (lane >> 4) * 4;
+    // Weight panel of B chunk cc (0 <= cc < TN). GLU: the first TN / 2 chunks are panels of the
+    // first half of the outputs and the rest their partners hp panels on, so the wavefronts with
+    // wn = 0 hold the a half of a GLU and those with wn = 1 the b half of the same columns.
+    auto panel_of = [&](int cc) {
+        if constexpr (GLU) return cc < TN / 2 ? bx * (TN / 2) + cc : hp + bx * (TN / 2) + cc - TN / 2;
+        return P0 + cc;
+    };
 
     int32_t e_row[RB][4];
     float s_col[CB];
@@ -605,7 +658,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
 #pragma unroll
         for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
+    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(panel_of(wn * CB + cb) * 16 + out_col, P * 16 - 1)];
 
     // This wavefront's copies: chunk ch = wave + 4 i is row block R0 + ch / 2, digit ch % 2 when
     // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one.
@@ -618,7 +671,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
             g[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024 + lane * 16;
             gs[i] = 2048;
         } else {
-            g[i] = wv + (size_t)min(P0 + ch - 2 * TM, P - 1) * b_panel + lane * 16;
+            g[i] = wv + (size_t)min(panel_of(ch - 2 * TM), P - 1) * b_panel + lane * 16;
             gs[i] = b_blk;
         }
     }
@@ -675,7 +728,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
 #undef TG_ISSUE
 #undef TG_MMA
     TileStore<WM, WN, C_STRIDE> out;
-    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
 
     float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
@@ -688,16 +741,27 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                 tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
                     dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
     __syncthreads();
-    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+    if constexpr (GLU) {
+        // Wavefronts (wm, 0) and (wm, 1) hold the a and b halves of the same rows and columns; each
+        // stores the GLU of half of those rows. c is the GLU output, hp * 16 columns wide.
+        const float *ta = reinterpret_cast<const float *>(smem) + wm * WM * C_STRIDE + wn * (WM / 2) * C_STRIDE;
+        glu_store<WM / 2, WN, C_STRIDE>(ta, ta + 2 * WM * C_STRIDE, lane, c, ldc, m0 + wn * (WM / 2), bx * WN, M,
+                                        hp * 16, bias, act, escale);
+    } else {
+        out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+    }
 }
 
-template <int TM, int TN, int NS, int XCD, int G>
+template <int TM, int TN, int NS, int XCD, int G, int GLU = 0>
 hipError_t launch_lds(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                       const EpiArgs &epi, hipStream_t s) {
-    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)TN), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
-    hipLaunchKernelGGL((gemm_lds_kernel<TM, TN, NS, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
-                       w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
-                       epi.accumulate, w.panel_stride, w.blk_stride);
+    // GLU: a workgroup column covers TN / 2 panels of each half (the launcher checks that they
+    // divide the half's panels).
+    const size_t hp = w.panels / 2, cols = GLU ? hp / (TN / 2) : div_ceil(w.panels, (size_t)TN);
+    const dim3 grid((unsigned)cols, (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
+    hipLaunchKernelGGL((gemm_lds_kernel<TM, TN, NS, XCD, G, GLU>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
+                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
+                       epi.accumulate, w.panel_stride, w.blk_stride, (int)hp);
     return hipGetLastError();
 }
 
@@ -731,6 +795,21 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512)
         return launch_kq<5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
     return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+}
+
+// The GLU-fused product: 128 x 128 tiles (four panels of each half) when they fill the chip twice
+// over and the half has a multiple of 64 outputs, else 64 x 64 tiles (two panels of each half),
+// which need a multiple of 32.
+bool gemm_glu_fits(size_t n) { return n % 64 == 0; }
+
+hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *out,
+                              size_t ldo, const EpiArgs &epi, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    if (w.precision != INT8 || !gemm_glu_fits(w.n)) return hipErrorInvalidValue;
+    const size_t half = w.n / 2;
+    if (half % 64 == 0 && gemm_tile_choice(m, w.panels) == 0)
+        return launch_lds<8, 8, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
+    return launch_lds<4, 4, 3, 0, 4, 1>(qf, exps, m, w, out, ldo, epi, s);
 }
 
 }  // namespace tg

@@ -271,6 +271,19 @@ class Kernels:
     def linear_device(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
         self.matmul_device(a, w.k(), m, w, c, w.n(), epi)
 
+    def linear_glu_device(self, a, m: int, w: PackedWeights, out, ldo: Optional[int] = None,
+                          epi: Epilogue = Epilogue.PLAIN, a_len: Optional[int] = None,
+                          out_len: Optional[int] = None):
+        """out = glu(epi(a . w)) on GPU tensors: linear_device into [m, n] then glu_device, fused into
+        one GEMM for int8 weights in fast mode (n a multiple of 64). out is [m, ldo], ldo >= n / 2
+        (default n / 2); epi must not accumulate."""
+        ldo = w.n() // 2 if ldo is None else ldo
+        rc = _lib.lib().tg_linear_glu_device(self._ctx, ctypes.c_void_p(a.data_ptr()),
+                                             a.numel() if a_len is None else a_len, m, w._handle,
+                                             ctypes.c_void_p(out.data_ptr()),
+                                             out.numel() if out_len is None else out_len, ldo, self._epi_dev(epi))
+        _check(rc, self._ctx)
+
     def matmul_rowmajor_device(self, a, lda: int, m: int, b, k: int, n: int, ldb: int, c, ldc: int,
                                epi: Epilogue = Epilogue.PLAIN, a_len: Optional[int] = None,
                                b_len: Optional[int] = None, c_len: Optional[int] = None):

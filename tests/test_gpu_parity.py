@@ -600,3 +600,77 @@ def test_row_fixtures(tk):
             continue
         tk.synchronize()
         assert np.array_equal(out.cpu().numpy().view(np.uint32), g["out"].view(np.uint32)), meta["name"]
+
+
+# (m, k, n, ldo): the M=750 layer's pw1 (64 x 64 GLU tiles), 128 x 128 GLU tiles, ragged rows and
+# inputs, strided and unaligned outputs, and products the fused kernel does not take (n % 64 != 0,
+# GEMV rows), which go through the context's buffer.
+GLU_SHAPES = [(750, 1024, 2048, 1024), (1100, 200, 16384, 8192), (37, 200, 256, 130), (130, 64, 128, 64),
+              (300, 100, 96, 48), (5, 64, 128, 64)]
+
+
+@pytest.mark.parametrize("m,k,n,ldo", GLU_SHAPES)
+def test_linear_glu_is_linear_then_glu(tk, orc, m, k, n, ldo):
+    """tg_linear_glu_device writes exactly what tg_linear_device followed by tg_glu_device writes
+    (src/parakeet.rs:1087-1104), for every epilogue it accepts; and the GLU of the oracle's product
+    for one of them."""
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(m + k + n)
+    a = normal(rng, (m, k))
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    ad = torch.from_numpy(a).cuda()
+    bias = torch.from_numpy(normal(rng, n)).cuda()
+    half = n // 2
+    for act, with_bias, scale in ((NONE, False, 1.0), (NONE, True, 1.0), (SILU, True, 0.5)):
+        say("linear_glu", m, k, n, ldo, act, with_bias)
+        epi = telmo_amd.Epilogue(bias=bias if with_bias else None, act=telmo_amd.Act(act), scale=scale)
+        g = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        want = torch.full((m, ldo), 7.5, dtype=torch.float32, device="cuda")
+        got = torch.full((m, ldo), 7.5, dtype=torch.float32, device="cuda")
+        tk.linear_device(ad, m, w, g, epi)
+        tk.glu_device(g, n, m, half, want, ldo)
+        tk.linear_glu_device(ad, m, w, got, ldo, epi)
+        tk.synchronize()
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32)), (m, k, n)
+    if m * k * n > 10 ** 9:  # the oracle is plain C; the big case is covered by the comparison above
+        w.close()
+        return
+    # the oracle: the integer product, then the reference's glu
+    c = np.zeros(m * n, np.float32)
+    assert orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, c, n, None, NONE, 1.0, False) == 0
+    c = c.reshape(m, n)
+    want = np.stack([orc.glu(c[r, :half], c[r, half:]) for r in range(m)])
+    got = torch.empty((m, ldo), dtype=torch.float32, device="cuda")
+    tk.linear_glu_device(ad, m, w, got, ldo)
+    tk.synchronize()
+    assert np.array_equal(got.cpu().numpy()[:, :half].view(np.uint32), want.view(np.uint32))
+    w.close()
+
+
+def test_linear_glu_refuses_what_it_cannot_do(tk):
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(5)
+    q, s = int8_weights(rng, 130, 64)
+    w = telmo_amd.PackedWeights.from_parts(tk, 130, 64, telmo_amd.Precision.INT8, *pack_int8(q, s))
+    a = torch.zeros((40, 64), dtype=torch.float32, device="cuda")
+    out = torch.zeros((40, 65), dtype=torch.float32, device="cuda")
+    with pytest.raises(telmo_amd.TelmoError, match="not accumulated"):
+        tk.linear_glu_device(a, 40, w, out, epi=telmo_amd.Epilogue(accumulate=True))
+    with pytest.raises(telmo_amd.TelmoError, match="out is too short"):
+        tk.linear_glu_device(a, 40, w, out, 65, out_len=39 * 65 + 64)
+    with pytest.raises(telmo_amd.TelmoError, match="ldo must be"):
+        tk.linear_glu_device(a, 40, w, out, 64)
+    w.close()
+    q, s = int8_weights(rng, 129, 64)
+    w = telmo_amd.PackedWeights.from_parts(tk, 129, 64, telmo_amd.Precision.INT8, *pack_int8(q, s))
+    with pytest.raises(telmo_amd.TelmoError, match="even"):
+        tk.linear_glu_device(a, 40, w, out, 65)
+    w.close()
