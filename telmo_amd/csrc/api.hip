@@ -1,13 +1,15 @@
-// The C ABI (include/telmo_hip.h): contexts, device weights, argument checks with the
-// reference's semantics, and dispatch to the kernels.
+// The C ABI (include/telmo_hip.h, which cites the reference line each entry point replaces):
+// contexts, device weights, argument checks with the reference's semantics, and dispatch to the
+// kernels. Among them:
 //
 //   tg_matmul / tg_matmul_device   Kernels::matmul        src/kernels/mod.rs:657-688
 //   tg_linear / tg_linear_device   Kernels::linear        src/kernels/mod.rs:691-701
 //   tg_weights_upload              PackedWeights::from_parts  src/kernels/mod.rs:214-237
 //
-// Dispatch (fast mode, int8 weights): m <= 8 with the row digits fitting the GEMV's LDS -> the
-// dot4 GEMV (one launch); otherwise the row quantiser then the MFMA GEMM (two launches). Other
-// precisions, the exact mode, and k beyond the integer path's limit run the exact kernel.
+// Dispatch (fast mode, int8 and Q8_0 weights, k <= 65536): up to 16 rows that fit a GEMV
+// (gemv_fits) take the MFMA GEMV, or for int8 the dot4 GEMV, in one launch; otherwise the row
+// quantiser then the MFMA GEMM, whose kernel launch_gemm_i8 picks by shape. The exact mode, other
+// precisions and longer inputs run the exact kernel.
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -22,6 +24,9 @@ struct tg_ctx {
     bool own_stream = false;
     uint32_t mode = TG_MODE_FAST;
     std::mutex mu;
+    // The last error message. Argument checks can fail before a call takes mu, so the message has
+    // a mutex of its own; a caller reading it while another thread calls on the context races.
+    std::mutex err_mu;
     std::string err;
     // Workspace of the quantised rows and their exponents, grown on demand.
     uint8_t *qa = nullptr;
@@ -71,8 +76,16 @@ constexpr int TDT_GRAPH_STEPS = 16;
 namespace {
 
 int fail(tg_ctx *ctx, int code, const std::string &msg) {
-    if (ctx) ctx->err = msg;
+    if (ctx) {
+        std::lock_guard<std::mutex> g(ctx->err_mu);
+        ctx->err = msg;
+    }
     return code;
+}
+
+void clear_error(tg_ctx *ctx) {
+    std::lock_guard<std::mutex> g(ctx->err_mu);
+    ctx->err.clear();
 }
 
 int hip_fail(tg_ctx *ctx, hipError_t e, const char *what) {
@@ -232,7 +245,7 @@ int upload(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *s
     }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return cleanup(TG_ERR_HIP, std::string("weight upload: ") + hipGetErrorString(e));
-    ctx->err.clear();
+    clear_error(ctx);
     *out = w;
     return TG_OK;
 }
@@ -334,7 +347,7 @@ int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size
     if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
     TG_HIP(ctx, hipSetDevice(ctx->device));
     rc = run_device(ctx, a, lda, m, w, c, ldc, epi_args(epi, nullptr, false));
-    if (rc == TG_OK) ctx->err.clear();
+    if (rc == TG_OK) clear_error(ctx);
     return rc;
 }
 
@@ -362,7 +375,7 @@ int tg_matmul_rowmajor_device(tg_ctx *ctx, const float *a, size_t a_len, size_t 
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, tg::launch_rowmajor(a, lda, m, k, b, ldb, n, c, ldc, epi_args(epi, nullptr, false), ctx->stream));
-    ctx->err.clear();
+    clear_error(ctx);
     return TG_OK;
 }
 
@@ -408,7 +421,7 @@ int tg_matmul(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, c
     TG_HIP(ctx, hipMemcpyAsync(hc, ctx->dc, m * n * 4, hipMemcpyDeviceToHost, ctx->stream));
     TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
     copy_rows(c, ldc, hc, n, m, n);
-    ctx->err.clear();
+    clear_error(ctx);
     return TG_OK;
 }
 
@@ -530,7 +543,7 @@ int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, co
         if ((rc = run_device(ctx, a, k, m, w, ctx->dg, n, e))) return rc;
         TG_HIP(ctx, tg::launch_glu(ctx->dg, n, m, half, out, ldo, ctx->stream));
     }
-    ctx->err.clear();
+    clear_error(ctx);
     return TG_OK;
 }
 
