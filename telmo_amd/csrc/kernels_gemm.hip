@@ -651,15 +651,6 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         return P0 + cc;
     };
 
-    int32_t e_row[RB][4];
-    float s_col[CB];
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(panel_of(wn * CB + cb) * 16 + out_col, P * 16 - 1)];
-
     // This wavefront's copies: chunk ch = wave + 4 i is row block R0 + ch / 2, digit ch % 2 when
     // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one.
     const uint8_t *g[CPW];
@@ -721,12 +712,25 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                 if (t + NS - 1 < KB) TG_ISSUE((s + NS - 1) % NS, t + NS - 1);
                 v4i fa[RB][2], fb[CB];
                 read_frags(smem + s * STAGE, fa, fb);
+                // All twelve reads are issued before the first MFMA, so that the LDS latency is
+                // waited out once per k-block, not once per row block.
+                __builtin_amdgcn_sched_barrier(0);
                 TG_MMA(fa, fb);
             }
         }
     }
 #undef TG_ISSUE
 #undef TG_MMA
+    // Row exponents and column scales are loaded after the k-loop, which leaves their registers
+    // to the operand fragments.
+    int32_t e_row[RB][4];
+    float s_col[CB];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(panel_of(wn * CB + cb) * 16 + out_col, P * 16 - 1)];
     TileStore<WM, WN, C_STRIDE> out;
     if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
