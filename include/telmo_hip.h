@@ -200,7 +200,9 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, s
  * with every step on the device. The matrices are tg_weights of int8 or Q8_0 values. The network
  * keeps its own copies of the LSTM matrices and biases (rows interleaved so a unit's four gates meet
  * in one output quad); the joint, projection, their biases and the embedding stay the caller's and
- * must outlive the network. */
+ * must outlive the network. Every call on a network uses the network's scratch rows and decode
+ * control block, so calls on one network must not overlap on the device: issue them through one
+ * context, or synchronise between contexts. */
 typedef struct tg_tdt tg_tdt;
 typedef struct {
     size_t hidden;                 /* pred_hidden h: a multiple of 4, at most 992 */
