@@ -484,11 +484,12 @@ def test_pack_matrices_upload_like_their_parts(tk, tmp_path):
         pack.matrix(tk, "nope", 2, 3)
 
 
-@pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384), (4100, 200, 1000)])
+@pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384), (4100, 200, 1000), (4100, 1000, 1000)])
 def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
     """Products that fill the chip with 128 x 128 tiles (>= 1024 of them), and narrow products
     (< 2048 outputs) with >= 256 of them, run the 128 x 128 LDS-staged GEMM; partial edge tiles in
-    both directions, every epilogue, bit-identical to the integer oracle."""
+    both directions, every epilogue, bit-identical to the integer oracle. k = 1000 (16 k-blocks)
+    goes round the three-stage ring five times and ends on a partial round."""
     rng = np.random.default_rng(m + k + n)
     a = normal(rng, m * k)
     q, s = int8_weights(rng, n, k)
