@@ -92,6 +92,14 @@ def _f32(x) -> np.ndarray:
     return arr
 
 
+def _dev(t, dtype: str, name: str) -> ctypes.c_void_p:
+    """The device address of GPU tensor t, after checking that t is a GPU tensor of the element type
+    the library reads there: the lengths passed beside it count elements of that type."""
+    if str(t.dtype) != "torch." + dtype or not t.is_cuda:
+        raise TypeError(f"{name} must be a {dtype} GPU tensor, not {t.dtype} on {t.device}")
+    return ctypes.c_void_p(t.data_ptr())
+
+
 def _check(code: int, ctx) -> None:
     if code != 0:
         msg = _lib.lib().tg_last_error(ctx).decode() if ctx else "error"
@@ -123,8 +131,8 @@ class PackedWeights:
     def from_device(kernels: "Kernels", n: int, k: int, precision: Precision, values, scales=None):
         """from_parts on GPU tensors (uint8 values, float32 scales) already in the panel layout."""
         out = ctypes.c_void_p()
-        rc = _lib.lib().tg_weights_upload_device(kernels._ctx, ctypes.c_void_p(values.data_ptr()), values.numel(),
-                                                 None if scales is None else ctypes.c_void_p(scales.data_ptr()),
+        rc = _lib.lib().tg_weights_upload_device(kernels._ctx, _dev(values, "uint8", "values"), values.numel(),
+                                                 None if scales is None else _dev(scales, "float32", "scales"),
                                                  0 if scales is None else scales.numel(), int(precision), n, k,
                                                  ctypes.byref(out))
         _check(rc, kernels._ctx)
@@ -256,15 +264,15 @@ class Kernels:
             return None
         e = _Epi()
         if epi.bias is not None:
-            e.bias, e.bias_len = epi.bias.data_ptr(), epi.bias.numel()
+            e.bias, e.bias_len = _dev(epi.bias, "float32", "bias").value, epi.bias.numel()
         e.act, e.scale, e.accumulate = int(epi.act), float(epi.scale), int(bool(epi.accumulate))
         return ctypes.byref(e)
 
     def matmul_device(self, a, lda: int, m: int, w: PackedWeights, c, ldc: int, epi: Epilogue = Epilogue.PLAIN,
                       a_len: Optional[int] = None, c_len: Optional[int] = None):
         """Queues the product on GPU tensors (float32). a_len / c_len default to the tensors' sizes."""
-        rc = _lib.lib().tg_matmul_device(self._ctx, ctypes.c_void_p(a.data_ptr()), a.numel() if a_len is None
-                                         else a_len, lda, m, w._handle, ctypes.c_void_p(c.data_ptr()),
+        rc = _lib.lib().tg_matmul_device(self._ctx, _dev(a, "float32", "a"), a.numel() if a_len is None
+                                         else a_len, lda, m, w._handle, _dev(c, "float32", "c"),
                                          c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
         _check(rc, self._ctx)
 
@@ -278,9 +286,9 @@ class Kernels:
         one GEMM for int8 weights in fast mode (n a multiple of 64). out is [m, ldo], ldo >= n / 2
         (default n / 2); epi must not accumulate."""
         ldo = w.n() // 2 if ldo is None else ldo
-        rc = _lib.lib().tg_linear_glu_device(self._ctx, ctypes.c_void_p(a.data_ptr()),
+        rc = _lib.lib().tg_linear_glu_device(self._ctx, _dev(a, "float32", "a"),
                                              a.numel() if a_len is None else a_len, m, w._handle,
-                                             ctypes.c_void_p(out.data_ptr()),
+                                             _dev(out, "float32", "out"),
                                              out.numel() if out_len is None else out_len, ldo, self._epi_dev(epi))
         _check(rc, self._ctx)
 
@@ -290,9 +298,9 @@ class Kernels:
         """matmul with BView::row_major(b, k, n, ldb) as the right-hand side: f32 GPU tensors, the
         reference's fused sums. b must hold whole 16-column panels, as the reference's view checks."""
         rc = _lib.lib().tg_matmul_rowmajor_device(
-            self._ctx, ctypes.c_void_p(a.data_ptr()), a.numel() if a_len is None else a_len, lda, m,
-            ctypes.c_void_p(b.data_ptr()), b.numel() if b_len is None else b_len, k, n, ldb,
-            ctypes.c_void_p(c.data_ptr()), c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
+            self._ctx, _dev(a, "float32", "a"), a.numel() if a_len is None else a_len, lda, m,
+            _dev(b, "float32", "b"), b.numel() if b_len is None else b_len, k, n, ldb,
+            _dev(c, "float32", "c"), c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
         _check(rc, self._ctx)
 
     def quant_bytes(self, m: int, k: int) -> int:
@@ -300,31 +308,31 @@ class Kernels:
 
     def quantize_rows_device(self, a, lda: int, m: int, k: int, qa, exps, a_len: Optional[int] = None):
         """Splits rows of a GPU tensor into the two-digit form (qa: uint8 tensor, exps: int32)."""
-        rc = _lib.lib().tg_quantize_rows_device(self._ctx, ctypes.c_void_p(a.data_ptr()),
+        rc = _lib.lib().tg_quantize_rows_device(self._ctx, _dev(a, "float32", "a"),
                                                 a.numel() if a_len is None else a_len, lda, m, k,
-                                                ctypes.c_void_p(qa.data_ptr()), qa.numel(),
-                                                ctypes.c_void_p(exps.data_ptr()))
+                                                _dev(qa, "uint8", "qa"), qa.numel(),
+                                                _dev(exps, "int32", "exps"))
         _check(rc, self._ctx)
 
     def matmul_quantized_device(self, qa, exps, m: int, w: PackedWeights, c, ldc: int,
                                 epi: Epilogue = Epilogue.PLAIN):
         """The MFMA GEMM alone over rows quantised by quantize_rows_device."""
-        rc = _lib.lib().tg_matmul_quantized_device(self._ctx, ctypes.c_void_p(qa.data_ptr()), qa.numel(),
-                                                   ctypes.c_void_p(exps.data_ptr()), m, w._handle,
-                                                   ctypes.c_void_p(c.data_ptr()), c.numel(), ldc,
+        rc = _lib.lib().tg_matmul_quantized_device(self._ctx, _dev(qa, "uint8", "qa"), qa.numel(),
+                                                   _dev(exps, "int32", "exps"), m, w._handle,
+                                                   _dev(c, "float32", "c"), c.numel(), ldc,
                                                    self._epi_dev(epi))
         _check(rc, self._ctx)
 
     def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int):
-        rc = _lib.lib().tg_glu_device(self._ctx, ctypes.c_void_p(x.data_ptr()), ldx, m, half,
-                                      ctypes.c_void_p(out.data_ptr()), ldo)
+        rc = _lib.lib().tg_glu_device(self._ctx, _dev(x, "float32", "x"), ldx, m, half,
+                                      _dev(out, "float32", "out"), ldo)
         _check(rc, self._ctx)
 
     def layer_norm_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, out, ldo: int):
         """LayerNorm of m rows of GPU tensor x (n values each) into out (may be x)."""
-        rc = _lib.lib().tg_layer_norm_device(self._ctx, ctypes.c_void_p(x.data_ptr()), ldx, m, n,
-                                             ctypes.c_void_p(gamma.data_ptr()), ctypes.c_void_p(beta.data_ptr()),
-                                             float(eps), ctypes.c_void_p(out.data_ptr()), ldo)
+        rc = _lib.lib().tg_layer_norm_device(self._ctx, _dev(x, "float32", "x"), ldx, m, n,
+                                             _dev(gamma, "float32", "gamma"), _dev(beta, "float32", "beta"),
+                                             float(eps), _dev(out, "float32", "out"), ldo)
         _check(rc, self._ctx)
 
     def dwconv1d_device(self, x, ldx: int, frames: int, channels: int, w, kernel: int, bias, out, ldo: int,
@@ -335,10 +343,10 @@ class Kernels:
         (rows output rows each) laid one after another are convolved each on its own."""
         rows = frames if rows is None else rows
         a = int(Act.NONE if act is None else act)
-        xp = ctypes.c_void_p(x.data_ptr()) if x is not None else None
+        xp = _dev(x, "float32", "x") if x is not None else None
         rc = _lib.lib().tg_dwconv1d_device(self._ctx, xp, ldx, frames, batch, channels,
-                                           ctypes.c_void_p(w.data_ptr()), kernel, ctypes.c_void_p(bias.data_ptr()),
-                                           t0, stride, rows, a, ctypes.c_void_p(out.data_ptr()), ldo)
+                                           _dev(w, "float32", "w"), kernel, _dev(bias, "float32", "bias"),
+                                           t0, stride, rows, a, _dev(out, "float32", "out"), ldo)
         _check(rc, self._ctx)
 
     def synchronize(self) -> None:
@@ -371,14 +379,14 @@ class TdtDecoder:
         desc.hidden, desc.vocab, desc.max_symbols, desc.layers = hidden, vocab, max_symbols, len(lstm)
         desc.durations = ctypes.cast(self._durs, ctypes.POINTER(ctypes.c_int32))
         desc.n_durations = len(self.durations)
-        desc.joint, desc.joint_bias = joint._handle, joint_bias.data_ptr()
-        desc.embedding = embedding.data_ptr()
+        desc.joint, desc.joint_bias = joint._handle, _dev(joint_bias, "float32", "joint_bias").value
+        desc.embedding = _dev(embedding, "float32", "embedding").value
         if len(lstm) > 4 or len(lstm) != len(lstm_bias):
             raise ValueError("1 to 4 LSTM layers, each with its bias")
         for i, (w, b) in enumerate(zip(lstm, lstm_bias)):
             desc.lstm[i] = w._handle
-            desc.lstm_bias[i] = b.data_ptr()
-        desc.proj, desc.proj_bias = proj._handle, proj_bias.data_ptr()
+            desc.lstm_bias[i] = _dev(b, "float32", "lstm_bias").value
+        desc.proj, desc.proj_bias = proj._handle, _dev(proj_bias, "float32", "proj_bias").value
         handle = ctypes.c_void_p()
         _check(_lib.lib().tg_tdt_create(kernels._ctx, ctypes.addressof(desc), ctypes.byref(handle)), kernels._ctx)
         self._handle = handle
@@ -391,21 +399,23 @@ class TdtDecoder:
         rows x layers x [h, c]), updated in place; preds (rows x h) gets the projection."""
         toks = (ctypes.c_int32 * max(len(tokens), 1))(*[int(t) for t in tokens])
         _check(_lib.lib().tg_tdt_predict_device(self._kernels._ctx, self._handle, ctypes.addressof(toks), len(tokens),
-                                                ctypes.c_void_p(states.data_ptr()),
-                                                ctypes.c_void_p(preds.data_ptr())), self._kernels._ctx)
+                                                _dev(states, "float32", "states"),
+                                                _dev(preds, "float32", "preds")), self._kernels._ctx)
 
     def decode(self, enc_proj, state, pred, frame: int = 0, on_frame: int = 0, cap: Optional[int] = None):
         """The greedy decode over the rows of enc_proj (GPU tensor, frames x >= h) from frame with
         on_frame tokens on it; state (layers x [h, c]) and pred (h) are updated in place. Returns
         (tokens, frame, on_frame)."""
+        if enc_proj.dim() != 2 or enc_proj.stride(1) != 1:
+            raise ValueError("enc_proj must be a 2-D tensor whose rows are contiguous")
         frames = enc_proj.shape[0]
         if cap is None:
             cap = max(frames - frame, 0) * max(self.max_symbols, 1)
         out = (_lib.Token * max(cap, 1))()
         f, o, n = ctypes.c_size_t(frame), ctypes.c_size_t(on_frame), ctypes.c_size_t(0)
-        rc = _lib.lib().tg_tdt_decode_device(self._kernels._ctx, self._handle, ctypes.c_void_p(enc_proj.data_ptr()),
-                                             enc_proj.stride(0), frames, ctypes.c_void_p(state.data_ptr()),
-                                             ctypes.c_void_p(pred.data_ptr()), ctypes.byref(f), ctypes.byref(o),
+        rc = _lib.lib().tg_tdt_decode_device(self._kernels._ctx, self._handle, _dev(enc_proj, "float32", "enc_proj"),
+                                             enc_proj.stride(0), frames, _dev(state, "float32", "state"),
+                                             _dev(pred, "float32", "pred"), ctypes.byref(f), ctypes.byref(o),
                                              ctypes.addressof(out), cap, ctypes.byref(n))
         _check(rc, self._kernels._ctx)
         return [Token(t.id, t.frame, t.duration) for t in out[:n.value]], f.value, o.value

@@ -104,3 +104,16 @@ def test_no_gpu_means_a_clean_error_not_a_fallback():
 
     with pytest.raises(TelmoError):
         Kernels()
+
+
+def test_gpu_tensors_are_checked_for_their_element_type_before_the_library_sees_them():
+    """The lengths passed with a device pointer count elements of the type the library reads, so a
+    half-precision or host tensor must never reach it: the wrapper refuses it first."""
+    import torch
+
+    from telmo_amd.kernels import _dev
+
+    with pytest.raises(TypeError, match="a must be a float32 GPU tensor"):
+        _dev(torch.zeros(4, dtype=torch.float32), "float32", "a")  # on the host
+    with pytest.raises(TypeError, match="qa must be a uint8 GPU tensor"):
+        _dev(torch.zeros(4, dtype=torch.int8), "uint8", "qa")
