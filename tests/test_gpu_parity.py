@@ -99,6 +99,40 @@ def test_fast_int8_is_bit_identical_to_its_integer_oracle(tk, orc, m, k, n):
         assert err <= 1e-3
 
 
+def _random_dispatch_shapes():
+    """Four seeded random shapes in each region of the int8 dispatch: the GEMV (m <= 16), the direct
+    kernel, the k-split kernel (at least 32 k-blocks, few tiles), the 64 x 64 LDS kernel (at least
+    2048 outputs), the 128 x 128 LDS kernel on narrow products (at least 256 of its tiles) and on
+    wide ones (at least 1024 tiles). Sizes are ragged on purpose."""
+    rng = np.random.default_rng(2024)
+    regions = [((1, 16), (1, 3000), (1, 5000)), ((17, 700), (1, 1800), (1, 1000)),
+               ((17, 500), (2048, 4200), (16, 1000)), ((17, 900), (1, 1500), (2048, 4000)),
+               ((4096, 6000), (1, 700), (900, 2032)), ((2000, 3000), (1, 200), (8192, 12000))]
+    out = []
+    for (m0, m1), (k0, k1), (n0, n1) in regions:
+        for _ in range(4):
+            out.append((int(rng.integers(m0, m1 + 1)), int(rng.integers(k0, k1 + 1)), int(rng.integers(n0, n1 + 1)),
+                        int(rng.integers(0, len(EPIS)))))
+    return out
+
+
+@pytest.mark.parametrize("m,k,n,e", _random_dispatch_shapes())
+def test_random_shapes_in_every_dispatch_region_match_the_integer_oracle(tk, orc, m, k, n, e):
+    """Whichever kernel the dispatch picks for a shape, the outputs are the integer oracle's bits."""
+    rng = np.random.default_rng(m * 131 + k * 17 + n)
+    a = normal(rng, m * k)
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    bias, c0 = normal(rng, n), normal(rng, m * n)
+    act, acc, with_bias = EPIS[e]
+    b = bias if with_bias else None
+    say("dispatch", m, k, n, act, acc, with_bias)
+    want = c0.copy()
+    assert orc.matmul_fast(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc) == 0
+    got = run_gpu(tk, a, k, m, values, scales, INT8, n, k, c0, n, b, act, acc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+
+
 def test_gemv_rows_equal_gemm_rows(tk):
     import telmo_amd
 
