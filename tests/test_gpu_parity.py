@@ -467,6 +467,37 @@ def test_fast_q8_0_is_bit_identical_to_its_integer_oracle(tk, orc, m, k, n):
     assert err <= 1e-3
 
 
+def _random_q8_shapes():
+    """Seeded random Q8_0 shapes (k a multiple of 32): the GEMV (m <= 16), the GEMM with 64 x 64
+    tiles and the GEMM on products with at least 1024 128 x 128 tiles."""
+    rng = np.random.default_rng(2025)
+    regions = [((1, 16), (1, 90), (1, 5000)), ((17, 900), (1, 80), (1, 3000)), ((2000, 2600), (1, 6), (8192, 10000))]
+    out = []
+    for (m0, m1), (b0, b1), (n0, n1) in regions:
+        for _ in range(3):
+            out.append((int(rng.integers(m0, m1 + 1)), 32 * int(rng.integers(b0, b1 + 1)), int(rng.integers(n0, n1 + 1)),
+                        int(rng.integers(0, len(EPIS)))))
+    return out
+
+
+@pytest.mark.parametrize("m,k,n,e", _random_q8_shapes())
+def test_random_q8_0_shapes_match_the_integer_oracle(tk, orc, m, k, n, e):
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(m * 131 + k * 17 + n + 1)
+    a = normal(rng, m * k)
+    q, d = q8_0_weights(rng, n, k, full_range=True)
+    values, scales = pack_q8_0(q, d)
+    bias, c0 = normal(rng, n), normal(rng, m * n)
+    act, acc, with_bias = EPIS[e]
+    b = bias if with_bias else None
+    say("dispatch-q8", m, k, n, act, acc, with_bias)
+    want = c0.copy()
+    assert orc.matmul_fast_q8(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc) == 0
+    got = run_gpu(tk, a, k, m, values, scales, Q8_0, n, k, c0, n, b, act, acc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+
+
 def test_fast_q8_0_unaligned_rows_take_the_gemm(tk, orc):
     from helpers import pack_q8_0, q8_0_weights
 
