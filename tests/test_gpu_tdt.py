@@ -6,7 +6,7 @@ math uses the GPU's expf / tanhf where the oracle (like the reference) uses the 
 gate output can differ by an ulp. That can move a rounding of the next product's two-digit input by
 one unit (1/32639 of the row's largest |value|), a step of about |q| s / 32639 in each output it
 feeds (1e-6 to 1e-5 here). States and predictions are therefore held to the fast path's own bound,
-1e-4 (absolute for states, row-normwise for predictions; the north-star bound is 1e-3), and the
+1e-4 (absolute for states, row-normwise for predictions; the parity bound for f32 outputs is 1e-3), and the
 emitted tokens, frames and durations must be identical.
 """
 import numpy as np
