@@ -144,17 +144,26 @@ void copy_rows(float *dst, size_t ldd, const float *src, size_t lds, size_t m, s
     for (size_t r = 0; r < m; r++) std::memcpy(dst + r * ldd, src + r * lds, cols * sizeof(float));
 }
 
+// (rows - 1) * ld + len, the elements a strided view of rows reads, or SIZE_MAX when that does not
+// fit in size_t: no buffer is that long, so the length check fails instead of wrapping.
+size_t span(size_t rows, size_t ld, size_t len) {
+    if (rows == 0) return 0;
+    if (ld != 0 && rows - 1 > (SIZE_MAX - len) / ld) return SIZE_MAX;
+    return (rows - 1) * ld + len;
+}
+
 // The checks of Kernels::matmul (src/kernels/mod.rs:669-677), in its order.
 int check_matmul(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w, float *c,
                  size_t c_len, size_t ldc, const tg_epilogue *epi) {
     const size_t k = w->d.k, n = w->d.n;
     if (lda < k || ldc < n) return fail(ctx, TG_ERR_SHAPE, "lda must be >= k and ldc >= n");
-    if (a_len < (m - 1) * lda + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
-    if (c_len < (m - 1) * ldc + n) return fail(ctx, TG_ERR_SHAPE, "c is too short");
+    if (a_len < span(m, lda, k)) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (c_len < span(m, ldc, n)) return fail(ctx, TG_ERR_SHAPE, "c is too short");
     if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
     if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
     if (!a && k > 0) return fail(ctx, TG_ERR_NULL, "a is null");
     if (!c) return fail(ctx, TG_ERR_NULL, "c is null");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
     return TG_OK;
 }
 
@@ -357,15 +366,15 @@ int tg_matmul_rowmajor_device(tg_ctx *ctx, const float *a, size_t a_len, size_t 
     if (!ctx) return TG_ERR_NULL;
     // BView::row_major's check (src/kernels/mod.rs:341-351): the view reads whole 16-column panels.
     if (n > 0 && k > 0) {
-        const size_t last = (tg::div_ceil(n, (size_t)tg::PANEL) - 1) * tg::PANEL + (k - 1) * ldb + tg::PANEL;
+        const size_t last = span(k, ldb, (tg::div_ceil(n, (size_t)tg::PANEL) - 1) * tg::PANEL + tg::PANEL);
         if (b_len < last) return fail(ctx, TG_ERR_SHAPE, "the matrix view reads past its buffer");
         if (!b) return fail(ctx, TG_ERR_NULL, "b is null");
     }
     if (m == 0 || n == 0) return TG_OK;
     // Kernels::matmul's checks (src/kernels/mod.rs:669-677), in its order.
     if (lda < k || ldc < n) return fail(ctx, TG_ERR_SHAPE, "lda must be >= k and ldc >= n");
-    if (a_len < (m - 1) * lda + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
-    if (c_len < (m - 1) * ldc + n) return fail(ctx, TG_ERR_SHAPE, "c is too short");
+    if (a_len < span(m, lda, k)) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (c_len < span(m, ldc, n)) return fail(ctx, TG_ERR_SHAPE, "c is too short");
     if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
     if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
     if (!a && k > 0) return fail(ctx, TG_ERR_NULL, "a is null");
@@ -438,7 +447,8 @@ int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t ld
     if (!ctx) return TG_ERR_NULL;
     if (m == 0) return TG_OK;
     if ((!a && k) || !qa || !exps) return fail(ctx, TG_ERR_NULL, "null buffer");
-    if (lda < k || a_len < (m - 1) * lda + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (lda < k || a_len < span(m, lda, k)) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
     if (qa_len < tg_quant_bytes(m, k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
     if (k > tg::MAX_K_INT) return fail(ctx, TG_ERR_UNSUPPORTED, "k beyond the integer path's limit");
     std::lock_guard<std::mutex> g(ctx->mu);
@@ -456,7 +466,8 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
         return fail(ctx, TG_ERR_UNSUPPORTED, "the staged path takes int8 or Q8_0 weights with k <= 65536");
     if (!qa || !exps || !c) return fail(ctx, TG_ERR_NULL, "null buffer");
     if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
-    if (ldc < n || c_len < (m - 1) * ldc + n) return fail(ctx, TG_ERR_SHAPE, "c is too short");
+    if (ldc < n || c_len < span(m, ldc, n)) return fail(ctx, TG_ERR_SHAPE, "c is too short");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
     if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
     if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
     if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
@@ -518,12 +529,13 @@ int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, co
     if (m == 0 || n == 0) return TG_OK;
     std::lock_guard<std::mutex> g(ctx->mu);
     // tg_linear_device's checks on a and the epilogue, then the GLU output's.
-    if (a_len < (m - 1) * k + k) return fail(ctx, TG_ERR_SHAPE, "a is too short");
+    if (a_len < span(m, k, k)) return fail(ctx, TG_ERR_SHAPE, "a is too short");
     if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
     if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
     if (!a && k > 0) return fail(ctx, TG_ERR_NULL, "a is null");
     if (ldo < half) return fail(ctx, TG_ERR_SHAPE, "ldo must be >= n / 2");
-    if (out_len < (m - 1) * ldo + half) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (out_len < span(m, ldo, half)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
     if (!out) return fail(ctx, TG_ERR_NULL, "out is null");
     if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
     TG_HIP(ctx, hipSetDevice(ctx->device));

@@ -740,3 +740,36 @@ def test_linear_glu_refuses_what_it_cannot_do(tk):
     with pytest.raises(telmo_amd.TelmoError, match="even"):
         tk.linear_glu_device(a, 40, w, out, 65)
     w.close()
+
+
+def test_strides_whose_span_wraps_size_t_are_refused_before_any_launch(tk):
+    """(m - 1) * lda + k is computed without wrapping: with lda = 2^63 and m = 3 it does not fit in
+    size_t, so no buffer is long enough and every entry point refuses the call on the host."""
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(5)
+    m, k, n = 3, 64, 32
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    a = torch.zeros(m * k, device="cuda")
+    c = torch.zeros(m * n, device="cuda")
+    huge = 1 << 63
+    say("span-wrap", m, k, n)
+    with pytest.raises(telmo_amd.TelmoError, match="a is too short"):
+        tk.matmul_device(a, huge, m, w, c, n)
+    with pytest.raises(telmo_amd.TelmoError, match="c is too short"):
+        tk.matmul_device(a, k, m, w, c, huge)
+    qa = torch.zeros(tk.quant_bytes(m, k), dtype=torch.uint8, device="cuda")
+    ex = torch.zeros(m, dtype=torch.int32, device="cuda")
+    with pytest.raises(telmo_amd.TelmoError, match="a is too short"):
+        tk.quantize_rows_device(a, huge, m, k, qa, ex)
+    with pytest.raises(telmo_amd.TelmoError, match="c is too short"):
+        tk.matmul_quantized_device(qa, ex, m, w, c, huge)
+    with pytest.raises(telmo_amd.TelmoError, match="out is too short"):
+        tk.linear_glu_device(a, m, w, c, ldo=huge)
+    tk.synchronize()
+    assert not c.any()
+    w.close()
