@@ -577,9 +577,12 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, s
         tg::div_ceil(rows, (size_t)8) * tg::div_ceil(channels, (size_t)256) * batch >= ((size_t)1 << 24))
         return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^24 channels, 65535 sequences or 2^35 outputs per call");
     if (frames > 0) {
-        const size_t xn = ((batch * frames - 1) * ldx + channels) * 4, on = ((batch * rows - 1) * ldo + channels) * 4;
+        // the bytes each view spans, saturated rather than wrapped
+        const size_t xs = span(batch * frames, ldx, channels), os = span(batch * rows, ldo, channels);
+        const size_t xn = xs > SIZE_MAX / 4 ? SIZE_MAX : xs * 4, on = os > SIZE_MAX / 4 ? SIZE_MAX : os * 4;
         const uintptr_t xb = reinterpret_cast<uintptr_t>(x), ob = reinterpret_cast<uintptr_t>(out);
-        if (ob < xb + xn && xb < ob + on) return fail(ctx, TG_ERR_ARG, "out must not overlap x");
+        if (xn && on && (ob >= xb ? ob - xb < xn : xb - ob < on))
+            return fail(ctx, TG_ERR_ARG, "out must not overlap x");
     }
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
