@@ -206,6 +206,9 @@ int upload(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *s
     if (!ctx || !out) return fail(ctx, TG_ERR_NULL, "null argument");
     *out = nullptr;
     if (!valid_precision(precision)) return fail(ctx, TG_ERR_ARG, "unknown precision");
+    // Sizes in which the panel byte count cannot wrap (and the kernels' 32-bit n and k hold).
+    if (n > (size_t)INT32_MAX || k > (size_t)INT32_MAX || (n && k > ((size_t)1 << 48) / n))
+        return fail(ctx, TG_ERR_UNSUPPORTED, "n and k must be < 2^31, with at most 2^48 weights");
     if (precision == TG_Q8_0 && k % tg::Q8_BLOCK) return fail(ctx, TG_ERR_ARG, "q8_0 needs k in multiples of 32");
     if (values_len != tg_panel_bytes(precision, n, k)) return fail(ctx, TG_ERR_ARG, "values have the wrong length");
     if (n_scales != tg_scale_count(precision, n, k)) return fail(ctx, TG_ERR_ARG, "scales have the wrong length");

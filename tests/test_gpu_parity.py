@@ -773,3 +773,16 @@ def test_strides_whose_span_wraps_size_t_are_refused_before_any_launch(tk):
     tk.synchronize()
     assert not c.any()
     w.close()
+
+
+def test_weight_sizes_whose_byte_count_would_wrap_are_refused(tk):
+    """n x k beyond 2^48 weights (or n, k beyond 2^31) is refused before the length check, so a panel
+    byte count that wraps size_t cannot match a short buffer."""
+    import telmo_amd
+
+    say("weights-wrap")
+    values = np.zeros(64, np.uint8)
+    scales = np.zeros(16, np.float32)
+    for n, k in ((1 << 40, 1 << 20), (16, 1 << 31), (1 << 31, 64)):
+        with pytest.raises(telmo_amd.TelmoError, match="n and k must be"):
+            telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
