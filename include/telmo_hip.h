@@ -100,7 +100,9 @@ int tg_synchronize(tg_ctx *ctx);
  * tg_panel_bytes gives, scales as tg_scale_count gives). Host pointers. The device copy is the
  * library's own and lives until tg_weights_free; int8 and Q8_0 values are re-laid out on the
  * device for the MFMA and dot4 kernels. Mirrors PackedWeights::from_parts, whose refusals
- * (wrong lengths, Q8_0 with k not a multiple of 32) give TG_ERR_ARG. */
+ * (wrong lengths, Q8_0 with k not a multiple of 32) give TG_ERR_ARG. n and k must be below 2^31
+ * with at most 2^48 weights (TG_ERR_UNSUPPORTED), checked before the lengths so that no byte
+ * count wraps. */
 int tg_weights_upload(tg_ctx *ctx, const uint8_t *values, size_t values_len, const float *scales,
                       size_t n_scales, uint32_t precision, size_t n, size_t k, tg_weights **out);
 /* The same with values and scales already in device memory (read during the call only). */
@@ -117,7 +119,9 @@ uint32_t tg_weights_precision(const tg_weights *w);
 
 /* c[m, n] = epilogue(a[m, k] * w^T) with a rows lda apart and c rows ldc apart. Host pointers;
  * copies a (and c when accumulating) to the device, runs, copies c back, and returns when done.
- * a_len and c_len are the lengths of the caller's slices, as the reference checks them. */
+ * a_len and c_len are the lengths of the caller's slices, as the reference checks them; a span
+ * (m - 1) * ld + k that does not fit in size_t counts as too long for any slice. m must be below
+ * 2^31 (TG_ERR_UNSUPPORTED). */
 int tg_matmul(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w, float *c,
               size_t c_len, size_t ldc, const tg_epilogue *epi);
 /* tg_matmul with lda = k and ldc = n. */
