@@ -54,6 +54,47 @@ LAYER = [
 ]
 
 
+# ---------------------------------------------------------------- synthetic inputs
+# Every input is drawn from telmo's test generator (src/kernels/mod.rs:795-805, exported as
+# telmo_amd.random): u in [-1, 1) and u01 = (u + 1) / 2. N(0, 1) activations by Box-Muller over
+# pairs of u01 (cos and sin of one pair give two values), int8 weights floor(u01 * 255) - 127 in
+# [-127, 127], scales 0.001 + 0.009 u01. Each tensor has a seed of its own.
+
+
+def synth_u01(length, seed):
+    import telmo_amd
+
+    return (telmo_amd.random(length, seed).astype(np.float64) + 1.0) * 0.5
+
+
+def synth_normal(shape, seed):
+    count = int(np.prod(shape))
+    u = synth_u01(2 * ((count + 1) // 2), seed).reshape(-1, 2)
+    r = np.sqrt(-2.0 * np.log1p(-u[:, 0]))
+    z = np.stack([r * np.cos(2.0 * np.pi * u[:, 1]), r * np.sin(2.0 * np.pi * u[:, 1])], axis=1).reshape(-1)
+    return z[:count].astype(np.float32).reshape(shape)
+
+
+def synth_int8(n, k, seed):
+    return (np.floor(synth_u01(n * k, seed) * 255.0) - 127.0).astype(np.int8).reshape(n, k)
+
+
+def synth_scales(n, seed):
+    return (0.001 + 0.009 * synth_u01(n, seed)).astype(np.float32)
+
+
+def panel_layout(q, s):
+    """int8 rows q [n, k] and scales s [n] in the panel layout (src/quant.rs:200-269)."""
+    n, k = q.shape
+    panels = -(-n // 16)
+    pad = np.zeros((panels * 16, k), np.int8)
+    pad[:n] = q
+    values = pad.reshape(panels, 16, k).transpose(0, 2, 1).reshape(-1).view(np.uint8).copy()
+    scales = np.zeros(panels * 16, np.float32)
+    scales[:n] = s
+    return values, scales
+
+
 def ops_of(m):
     return sum(2 * m * k * n for _, k, n, *_ in LAYER)
 
@@ -680,6 +721,41 @@ def cpu_tdt(net, enc_host, frames):
     return out, toks, oracle_toks
 
 
+def shape_leg(m, k, n, reps):
+    """One product shape alone, the program rocprofv3 runs for per-shape kernel statistics and
+    counters: rows quantised once, then `reps` launches of the MFMA GEMM alone
+    (tg_matmul_quantized_device) on the context's stream between HIP events on that stream. int8
+    weights and scales and N(0, 1) rows from telmo's test generator (seeds 1, 2 and 3)."""
+    import torch
+
+    import telmo_amd
+
+    values, scales = panel_layout(synth_int8(n, k, 1), synth_scales(n, 2))
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    w = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+    a = torch.from_numpy(synth_normal((m, k), 3)).cuda()
+    qa = torch.empty(kern.quant_bytes(m, k), dtype=torch.uint8, device="cuda")
+    exps = torch.empty(m, dtype=torch.int32, device="cuda")
+    c = torch.empty((m, n), device="cuda")
+    kern.quantize_rows_device(a, k, m, k, qa, exps)
+    for _ in range(3):
+        kern.matmul_quantized_device(qa, exps, m, w, c, n)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        kern.matmul_quantized_device(qa, exps, m, w, c, n)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    w.close()
+    kern.close()
+    return {"shape": [m, k, n], "reps": reps, "us_per_launch": round(us, 3),
+            "tops": round(2 * m * n * k / us / 1e6, 1)}
+
+
 def load_traffic():
     path = os.path.join(ROOT, "profiles", "gemm_layer_T750_traffic.json")
     if not os.path.exists(path):
@@ -700,9 +776,15 @@ def main():
     ap.add_argument("--no-encoder", action="store_true")
     ap.add_argument("--no-q8", action="store_true")
     ap.add_argument("--no-tdt", action="store_true")
+    ap.add_argument("--shape", type=int, nargs=3, metavar=("M", "K", "N"),
+                    help="time one product shape alone (the program for per-shape rocprofv3 runs) and exit")
+    ap.add_argument("--reps", type=int, default=20, help="launches timed with --shape")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU and has no multi-GPU path: run it with --gpus 1")
+    if args.shape:
+        print(json.dumps(shape_leg(*args.shape, args.reps)), flush=True)
+        return
 
     rng = np.random.default_rng(0)
     weights = make_weights(rng)

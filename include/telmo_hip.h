@@ -89,7 +89,8 @@ int tg_ctx_create(int device, void *stream, tg_ctx **out);
 void tg_ctx_destroy(tg_ctx *ctx);
 int tg_ctx_set_mode(tg_ctx *ctx, uint32_t mode);
 uint32_t tg_ctx_mode(const tg_ctx *ctx);
-/* The message of the last failed call on this context ("" if none). Valid until the next call. */
+/* The message of the last failed call on this context ("" if none), copied into storage of the
+ * calling thread: valid until that thread's next tg_last_error call. */
 const char *tg_last_error(const tg_ctx *ctx);
 /* Waits for all work queued on the context's stream. */
 int tg_synchronize(tg_ctx *ctx);
@@ -175,14 +176,19 @@ int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, co
 /* ---- row kernels -------------------------------------------------------------------------- */
 
 /* out[r, j] = x[r, j] * sigmoid(x[r, half + j]) for j < half (the GLU of a convolution module),
- * with the exp of the reference's SIMD kernels. Device pointers, queued on the stream. */
-int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo);
+ * with the exp of the reference's SIMD kernels. x_len and out_len are the buffers' lengths in
+ * floats, checked against the rows the call reads and writes (TG_ERR_SHAPE), as the reference
+ * asserts its slices (src/kernels/avx512.rs:412). Device pointers, queued on the stream. */
+int tg_glu_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t half, float *out,
+                  size_t out_len, size_t ldo);
 
 /* out[r, :] = LayerNorm(x[r, :]) * gamma + beta over n values per row, with the summation order of
- * the reference's AVX-512 layer_norm (src/kernels/avx512.rs:346-380). gamma and beta hold n device
- * floats; out may equal x. Device pointers, queued on the stream. */
-int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
-                         const float *beta, float eps, float *out, size_t ldo);
+ * the reference's AVX-512 layer_norm (src/kernels/avx512.rs:346-380). gamma and beta hold at least
+ * n floats and x and out (m - 1) ld + n, as the reference asserts (avx512.rs:348; TG_ERR_SHAPE
+ * otherwise); out may equal x. Device pointers, queued on the stream. */
+int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t n,
+                         const float *gamma, size_t gamma_len, const float *beta, size_t beta_len, float eps,
+                         float *out, size_t out_len, size_t ldo);
 
 /* Depthwise 1-D convolution of frames x channels rows, "same" zero padding: output row r is frame
  * t = t0 + r * stride, out[r, c] = bias[c] + sum over taps j in order of w[j * channels + c] *
@@ -195,9 +201,10 @@ int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size
  * may be laid one after another (sequence b: input rows b * frames .., output rows b * rows ..),
  * each convolved on its own; batch = 1 is the reference's call. out must not overlap x. Device
  * pointers, queued on the stream. */
-int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
-                       const float *w, size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows,
-                       uint32_t act, float *out, size_t ldo);
+int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t frames, size_t batch,
+                       size_t channels, const float *w, size_t w_len, size_t kernel, const float *bias,
+                       size_t bias_len, size_t t0, size_t stride, size_t rows, uint32_t act, float *out,
+                       size_t out_len, size_t ldo);
 
 /* ---- the TDT decoder (src/parakeet.rs:1412-1577) --------------------------------------------
  * Parakeet's prediction network (embedding, LSTM layers, projection) and joint, decoded greedily
@@ -222,6 +229,8 @@ typedef struct {
     const float *lstm_bias[4];     /* device, 4h */
     const tg_weights *proj;        /* h x h */
     const float *proj_bias;        /* device, h */
+    /* lengths in floats of the device buffers above, checked against what the network reads */
+    size_t joint_bias_len, embedding_len, lstm_bias_len[4], proj_bias_len;
 } tg_tdt_desc;
 /* One emitted token (parakeet.rs Token): its id, its frame (relative to enc_proj's first row) and
  * its duration. */
@@ -235,8 +244,10 @@ size_t tg_tdt_max_rows(const tg_tdt *tdt);
 /* predict_rows (src/parakeet.rs:1524-1577): for each row r, the token's embedding runs through the
  * LSTM layers with row r's state (states: rows x layers x [h, c] of h floats each, updated in place),
  * and preds[r] = proj(h_last) + bias. Gate math as the reference's: sigmoid = 1 / (1 + exp(-x)),
- * tanh, c = f c + i g, h = o tanh(c). Device pointers, 16-byte aligned; queued on the stream. */
-int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_t rows, float *states, float *preds);
+ * tanh, c = f c + i g, h = o tanh(c). states_len and preds_len (floats) must cover rows of each
+ * (TG_ERR_SHAPE). Device pointers, 16-byte aligned; queued on the stream. */
+int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_t rows, float *states,
+                          size_t states_len, float *preds, size_t preds_len);
 /* decode_inner (src/parakeet.rs:1412-1513) from frame *frame with *on_frame tokens already on it:
  * per frame t, logits = joint(relu(enc_proj[t] + pred)) + bias; the token and duration are the
  * argmaxes of the vocabulary and duration logits; a blank moves max(duration, 1) frames, a token
@@ -244,9 +255,11 @@ int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_
  * place) and moves by its duration, or after max_symbols tokens of duration 0 by one frame. Runs
  * until t >= frames and returns the emitted tokens (at most cap into tokens; *count is the number
  * emitted, TG_ERR_SHAPE when it exceeds cap) with *frame and *on_frame where the loop stopped.
- * enc_proj: frames rows of h floats at stride lde, on the device. Blocks until the decode ends. */
-int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t lde, size_t frames, float *state,
-                         float *pred, size_t *frame, size_t *on_frame, tg_token *tokens, size_t cap, size_t *count);
+ * enc_proj: frames rows of h floats at stride lde, on the device; enc_len, state_len and pred_len
+ * (floats) must cover what the decode reads (TG_ERR_SHAPE). Blocks until the decode ends. */
+int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t enc_len, size_t lde, size_t frames,
+                         float *state, size_t state_len, float *pred, size_t pred_len, size_t *frame,
+                         size_t *on_frame, tg_token *tokens, size_t cap, size_t *count);
 
 /* ---- packs: the reference's weight files (src/pack.rs) -------------------------------------
  * A pack is "TELMOPAK", a u32 version (1) and 4 zero bytes; entries' data at multiples of 64
@@ -301,6 +314,10 @@ int tg_fits(uint32_t precision, size_t k);
 /* quant::encode of row-major f32 rows w[n][k] (Rows::F32). */
 int tg_encode(const float *w, size_t n, size_t k, uint32_t precision, uint8_t *values, size_t values_len,
               float *scales, size_t n_scales);
+/* The reference's test generator, random(len, seed) (src/kernels/mod.rs:795-805): xorshift64
+ * (shifts 13, 7, 17) from the state seed * 0x9E3779B97F4A7C15 | 1, each step's top 24 bits mapped to
+ * [-1, 1). Not part of the product path: exported so that harnesses draw telmo's seeded inputs. */
+void tg_random(float *out, size_t len, uint64_t seed);
 /* quant::decode into row-major out[n][k]. */
 int tg_decode(const uint8_t *values, size_t values_len, const float *scales, size_t n_scales, uint32_t precision,
               size_t n, size_t k, float *out);

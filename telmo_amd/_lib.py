@@ -15,7 +15,8 @@ class TdtDesc(ctypes.Structure):
     """tg_tdt_desc."""
     _fields_ = [("hidden", _sz), ("vocab", _sz), ("durations", ctypes.POINTER(ctypes.c_int32)),
                 ("n_durations", _sz), ("max_symbols", _sz), ("layers", _sz), ("joint", _p), ("joint_bias", _p),
-                ("embedding", _p), ("lstm", _p * 4), ("lstm_bias", _p * 4), ("proj", _p), ("proj_bias", _p)]
+                ("embedding", _p), ("lstm", _p * 4), ("lstm_bias", _p * 4), ("proj", _p), ("proj_bias", _p),
+                ("joint_bias_len", _sz), ("embedding_len", _sz), ("lstm_bias_len", _sz * 4), ("proj_bias_len", _sz)]
 
 
 class Token(ctypes.Structure):
@@ -48,15 +49,18 @@ SIGNATURES = {
     "tg_quant_bytes": (_sz, [_sz, _sz]),
     "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
-    "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz]),
+    "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _sz]),
     "tg_linear_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _sz, _p]),
-    "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, ctypes.c_float, _p, _sz]),
-    "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, _sz, _sz, _u32, _p, _sz]),
+    "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, ctypes.c_float, _p, _sz,
+                                             _sz]),
+    "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p, _sz, _sz, _sz, _sz,
+                                           _u32, _p, _sz, _sz]),
     "tg_tdt_create": (ctypes.c_int, [_p, _p, ctypes.POINTER(_p)]),
     "tg_tdt_destroy": (None, [_p]),
     "tg_tdt_max_rows": (_sz, [_p]),
-    "tg_tdt_predict_device": (ctypes.c_int, [_p, _p, _p, _sz, _p, _p]),
-    "tg_tdt_decode_device": (ctypes.c_int, [_p, _p, _p, _sz, _sz, _p, _p, _szp, _szp, _p, _sz, _szp]),
+    "tg_tdt_predict_device": (ctypes.c_int, [_p, _p, _p, _sz, _p, _sz, _p, _sz]),
+    "tg_tdt_decode_device": (ctypes.c_int, [_p, _p, _p, _sz, _sz, _sz, _p, _sz, _p, _sz, _szp, _szp, _p, _sz,
+                                             _szp]),
     "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),
     "tg_pack_close": (None, [_p]),
@@ -74,6 +78,7 @@ SIGNATURES = {
     "tg_scale_count": (_sz, [_u32, _sz, _sz]),
     "tg_fits": (ctypes.c_int, [_u32, _sz]),
     "tg_encode": (ctypes.c_int, [_p, _sz, _sz, _u32, _p, _sz, _p, _sz]),
+    "tg_random": (None, [_p, _sz, ctypes.c_uint64]),
     "tg_decode": (ctypes.c_int, [_p, _sz, _p, _sz, _u32, _sz, _sz, _p]),
 }
 

@@ -25,7 +25,7 @@ struct tg_ctx {
     uint32_t mode = TG_MODE_FAST;
     std::mutex mu;
     // The last error message. Argument checks can fail before a call takes mu, so the message has
-    // a mutex of its own; a caller reading it while another thread calls on the context races.
+    // a mutex of its own; tg_last_error copies it under that mutex.
     std::mutex err_mu;
     std::string err;
     // Workspace of the quantised rows and their exponents, grown on demand.
@@ -313,7 +313,15 @@ int tg_ctx_set_mode(tg_ctx *ctx, uint32_t mode) {
 
 uint32_t tg_ctx_mode(const tg_ctx *ctx) { return ctx ? ctx->mode : TG_MODE_FAST; }
 
-const char *tg_last_error(const tg_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+const char *tg_last_error(const tg_ctx *ctx) {
+    // The message is copied under its lock into storage of the calling thread, so another thread
+    // failing or succeeding on the context meanwhile cannot free what the caller is reading.
+    thread_local std::string copy;
+    if (!ctx) return "null context";
+    std::lock_guard<std::mutex> g(const_cast<tg_ctx *>(ctx)->err_mu);
+    copy = ctx->err;
+    return copy.c_str();
+}
 
 int tg_synchronize(tg_ctx *ctx) {
     if (!ctx) return TG_ERR_NULL;
@@ -499,12 +507,17 @@ int tg_pack_upload_matrix(tg_ctx *ctx, const tg_pack *pack, const char *name, si
     return rc;
 }
 
-int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
-                         const float *beta, float eps, float *out, size_t ldo) {
+int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t n,
+                         const float *gamma, size_t gamma_len, const float *beta, size_t beta_len, float eps,
+                         float *out, size_t out_len, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;
     if (m == 0 || n == 0) return TG_OK;
     if (!x || !gamma || !beta || !out) return fail(ctx, TG_ERR_NULL, "null buffer");
     if (ldx < n || ldo < n) return fail(ctx, TG_ERR_SHAPE, "ldx and ldo must be >= n");
+    // The reference's assert (src/kernels/avx512.rs:348): out, gamma and beta hold the row's n values.
+    if (x_len < span(m, ldx, n)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (out_len < span(m, ldo, n)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (gamma_len < n || beta_len < n) return fail(ctx, TG_ERR_SHAPE, "gamma and beta must hold n values");
     if (n > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "rows longer than 2^31 values");
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
@@ -512,11 +525,16 @@ int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size
     return TG_OK;
 }
 
-int tg_glu_device(tg_ctx *ctx, const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo) {
+int tg_glu_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t half, float *out,
+                  size_t out_len, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;
     if (m == 0 || half == 0) return TG_OK;
     if (!x || !out) return fail(ctx, TG_ERR_NULL, "null buffer");
-    if (ldx < 2 * half || ldo < half) return fail(ctx, TG_ERR_SHAPE, "ldx must be >= 2 half and ldo >= half");
+    if (half > SIZE_MAX / 2 || ldx < 2 * half || ldo < half)
+        return fail(ctx, TG_ERR_SHAPE, "ldx must be >= 2 half and ldo >= half");
+    // The reference's assert (src/kernels/avx512.rs:412): both halves of each row are there.
+    if (x_len < span(m, ldx, 2 * half)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (out_len < span(m, ldo, half)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, tg::launch_glu(x, ldx, m, half, out, ldo, ctx->stream));
@@ -562,9 +580,10 @@ int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, co
     return TG_OK;
 }
 
-int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
-                       const float *w, size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows,
-                       uint32_t act, float *out, size_t ldo) {
+int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t frames, size_t batch,
+                       size_t channels, const float *w, size_t w_len, size_t kernel, const float *bias,
+                       size_t bias_len, size_t t0, size_t stride, size_t rows, uint32_t act, float *out,
+                       size_t out_len, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;
     if (act != TG_ACT_NONE && act != TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "act must be TG_ACT_NONE or TG_ACT_SILU");
     if (rows == 0 || channels == 0 || batch == 0) return TG_OK;
@@ -576,6 +595,14 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t ldx, size_t frames, s
         return fail(ctx, TG_ERR_UNSUPPORTED, "frames, t0 and stride must be < 2^40, rows < 2^26, kernel < 2^30");
     if (stride > 0 && rows - 1 > (lim - t0) / stride)
         return fail(ctx, TG_ERR_UNSUPPORTED, "the last row's frame t0 + (rows - 1) stride must be < 2^40");
+    // The slices dwconv1d_frame indexes (src/kernels/scalar.rs:174-182): the bias and each tap's
+    // channels, the input frames and the output rows.
+    if (bias_len < channels) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (kernel > 0 && (channels > SIZE_MAX / kernel || w_len < kernel * channels))
+        return fail(ctx, TG_ERR_SHAPE, "w is too short");
+    if (batch > SIZE_MAX / (frames > rows ? frames : rows)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (frames > 0 && x_len < span(batch * frames, ldx, channels)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (out_len < span(batch * rows, ldo, channels)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
     if (tg::div_ceil(channels, (size_t)256) >= 65536 || batch >= 65536 ||
         tg::div_ceil(rows, (size_t)8) * tg::div_ceil(channels, (size_t)256) * batch >= ((size_t)1 << 24))
         return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^24 channels, 65535 sequences or 2^35 outputs per call");
@@ -662,6 +689,10 @@ int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out) {
     rc = tdt_matrix(ctx, desc->proj, h, h, "proj");
     if (rc) return rc;
     if (!desc->joint_bias || !desc->embedding || !desc->proj_bias) return fail(ctx, TG_ERR_NULL, "null bias or embedding");
+    if (desc->joint_bias_len < vocab + ndur || desc->proj_bias_len < h || desc->embedding_len < vocab * h)
+        return fail(ctx, TG_ERR_SHAPE, "a bias or the embedding is too short");
+    for (size_t l = 0; l < layers; l++)
+        if (desc->lstm_bias_len[l] < 4 * h) return fail(ctx, TG_ERR_SHAPE, "an LSTM bias is too short");
     if (!aligned16(desc->embedding)) return fail(ctx, TG_ERR_ALIGN, "the embedding must be 16-byte aligned");
 
     std::lock_guard<std::mutex> g(ctx->mu);
@@ -733,13 +764,16 @@ void tg_tdt_destroy(tg_tdt *tdt) {
 
 size_t tg_tdt_max_rows(const tg_tdt *tdt) { return tdt ? tg::tdt_max_rows(*tdt->net.lstm[0]) : 0; }
 
-int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_t rows, float *states, float *preds) {
+int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_t rows, float *states,
+                          size_t states_len, float *preds, size_t preds_len) {
     if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
     if (rows == 0) return TG_OK;
     if (!tokens || !states || !preds) return fail(ctx, TG_ERR_NULL, "null tokens, states or preds");
     if (tdt->device != ctx->device) return fail(ctx, TG_ERR_ARG, "the network lives on another device");
     if (rows > tg::tdt_max_rows(*tdt->net.lstm[0]))
         return fail(ctx, TG_ERR_UNSUPPORTED, "more rows than tg_tdt_max_rows");
+    if (states_len < rows * tdt->net.layers * 2 * tdt->net.h) return fail(ctx, TG_ERR_SHAPE, "states is too short");
+    if (preds_len < rows * tdt->net.h) return fail(ctx, TG_ERR_SHAPE, "preds is too short");
     if (!aligned16(states) || !aligned16(preds)) return fail(ctx, TG_ERR_ALIGN, "states and preds must be 16-byte aligned");
     tg::TdtTokens toks{};
     for (size_t r = 0; r < rows; r++) {
@@ -756,8 +790,9 @@ int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_
     return TG_OK;
 }
 
-int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t lde, size_t frames, float *state,
-                         float *pred, size_t *frame, size_t *on_frame, tg_token *tokens, size_t cap, size_t *count) {
+int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t enc_len, size_t lde, size_t frames,
+                         float *state, size_t state_len, float *pred, size_t pred_len, size_t *frame,
+                         size_t *on_frame, tg_token *tokens, size_t cap, size_t *count) {
     if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
     if (!state || !pred || !frame || !on_frame || !count || (cap && !tokens))
         return fail(ctx, TG_ERR_NULL, "null argument");
@@ -768,6 +803,9 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
     if (*frame >= frames) return TG_OK;  // the reference's loop does not start
     if (!enc_proj) return fail(ctx, TG_ERR_NULL, "enc_proj is null");
     if (lde < net.h || lde % 4) return fail(ctx, TG_ERR_SHAPE, "lde must be >= hidden and a multiple of 4");
+    if (enc_len < span(frames, lde, net.h)) return fail(ctx, TG_ERR_SHAPE, "enc_proj is too short");
+    if (state_len < net.layers * 2 * net.h) return fail(ctx, TG_ERR_SHAPE, "state is too short");
+    if (pred_len < net.h) return fail(ctx, TG_ERR_SHAPE, "pred is too short");
     if (!aligned16(enc_proj) || !aligned16(state) || !aligned16(pred))
         return fail(ctx, TG_ERR_ALIGN, "enc_proj, state and pred must be 16-byte aligned");
     if (*on_frame > (size_t)INT32_MAX) return fail(ctx, TG_ERR_ARG, "on_frame out of range");

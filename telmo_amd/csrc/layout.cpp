@@ -34,45 +34,55 @@ float float_of(uint32_t b) {
     return f;
 }
 
-// Round to nearest even into IEEE half (src/quant.rs:91-127).
+// f32 to IEEE half, rounding to nearest even (src/quant.rs:91-127), worked out on the value
+// rather than its bits: a finite |x| with binary exponent E (x = f 2^E, 0.5 <= f < 1) sits on the
+// half grid of step 2^(E - 11), or 2^-24 below the normal range; rint (nearest, ties to even in the
+// default rounding mode) of |x| / step is exact in double, and the count m of steps gives the bits
+// directly: subnormals are m itself, normals (E + 14) << 10 plus m - 1024 (the biased exponent is
+// E + 14 = q + 25), where m = 2048 (a carry) lands on the next exponent's first value, and up to
+// infinity. Infinity keeps its sign; a
+// NaN keeps the top ten bits of its payload with the quiet bit set, as the reference writes it.
 uint16_t to_half(float x) {
     const uint32_t b = bits_of(x);
     const uint16_t sign = (uint16_t)((b >> 16) & 0x8000);
-    const int32_t exp = (int32_t)((b >> 23) & 0xff);
-    const uint32_t man = b & 0x7fffff;
-    if (exp == 0xff) return sign | 0x7c00 | (man ? (uint16_t)(0x200 | (man >> 13)) : 0);
-    const int32_t e = exp - 112;
-    if (e >= 0x1f) return sign | 0x7c00;
-    if (e <= 0) {
-        const uint32_t shift = (uint32_t)(126 - exp);
-        if (shift > 24) return sign;
-        const uint32_t full = man | 0x800000, half = 1u << (shift - 1);
-        uint32_t m = full >> shift;
-        const uint32_t rem = full & ((1u << shift) - 1);
-        if (rem > half || (rem == half && (m & 1))) m++;
-        return sign | (uint16_t)m;
-    }
-    uint32_t h = ((uint32_t)e << 10) | (man >> 13);
-    const uint32_t rem = man & 0x1fff;
-    if (rem > 0x1000 || (rem == 0x1000 && (h & 1))) h++;
-    return sign | (uint16_t)h;
+    if (std::isnan(x)) return sign | 0x7e00 | (uint16_t)((b & 0x7fffff) >> 13);
+    if (std::isinf(x)) return sign | 0x7c00;
+    const double v = std::fabs((double)x);
+    if (v == 0.0) return sign;
+    int E;
+    (void)std::frexp(v, &E);
+    const int q = E - 11 > -24 ? E - 11 : -24;  // the grid step's exponent
+    const double m = std::nearbyint(std::ldexp(v, -q));
+    if (q == -24 && m < 1024.0) return sign | (uint16_t)m;  // a subnormal (or zero) half
+    const double bits = (double)((q + 25) << 10) + (m - 1024.0);
+    return bits >= 0x7c00 ? (uint16_t)(sign | 0x7c00) : (uint16_t)(sign | (uint16_t)bits);
 }
 
+// IEEE half to f32, exactly: m 2^-24 below the normal range, (1024 + m) 2^(e - 25) above it; a
+// NaN becomes the quiet f32 NaN with the payload shifted into place.
 float from_half(uint16_t h) {
-    const uint32_t sign = (uint32_t)(h & 0x8000) << 16, exp = (h >> 10) & 0x1f, man = h & 0x3ff;
-    if (exp == 0) {
-        if (man == 0) return float_of(sign);
-        const float v = (float)man * (1.0f / 16777216.0f);
-        return sign ? -v : v;
-    }
-    if (exp == 0x1f) return float_of(sign | 0x7f800000u | (man ? 0x400000u | (man << 13) : 0u));
-    return float_of(sign | ((exp + 112) << 23) | (man << 13));
+    const uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    if (e == 0x1f) return float_of(sign | 0x7f800000u | (m ? 0x400000u | (m << 13) : 0u));
+    const double mag = e == 0 ? std::ldexp((double)m, -24) : std::ldexp((double)(1024 + m), (int)e - 25);
+    const float v = (float)mag;
+    return sign ? -v : v;
 }
 
+// f32 to bfloat16, nearest even (src/quant.rs:149-156): as for the half, the value is rounded to
+// the grid of 8 significant bits (step 2^(E - 8), or 2^-133 below the normal range) in double, and
+// the result, an f32 (infinity when it rounds past the largest one), keeps its top 16 bits. A NaN
+// gets the quiet bit.
 uint16_t to_bf16(float x) {
     const uint32_t b = bits_of(x);
     if (std::isnan(x)) return (uint16_t)((b >> 16) | 0x40);
-    return (uint16_t)((b + 0x7fff + ((b >> 16) & 1)) >> 16);
+    const double v = (double)x;
+    if (v == 0.0 || std::isinf(x)) return (uint16_t)(b >> 16);
+    int E;
+    (void)std::frexp(v, &E);
+    const int q = E - 8 > -133 ? E - 8 : -133;
+    const double r = std::ldexp(std::nearbyint(std::ldexp(v, -q)), q);
+    const float f = std::fabs(r) >= 0x1p128 ? (r > 0 ? INFINITY : -INFINITY) : (float)r;
+    return (uint16_t)(bits_of(f) >> 16);
 }
 
 // Rust's saturating `as i8` of an already rounded value.
@@ -123,6 +133,17 @@ size_t tg_scale_count(uint32_t precision, size_t n, size_t k) {
 }
 
 int tg_fits(uint32_t precision, size_t k) { return precision != TG_Q8_0 || k % Q8_BLOCK == 0; }
+
+void tg_random(float *out, size_t len, uint64_t seed) {
+    if (!out) return;
+    uint64_t s = seed * 0x9E3779B97F4A7C15ull | 1u;
+    for (size_t i = 0; i < len; i++) {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        out[i] = (float)(s >> 40) * (1.0f / 16777216.0f) * 2.0f - 1.0f;
+    }
+}
 
 int tg_encode(const float *w, size_t n, size_t k, uint32_t precision, uint8_t *values, size_t values_len,
               float *scales, size_t n_scales) {

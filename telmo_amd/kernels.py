@@ -100,6 +100,26 @@ def _dev(t, dtype: str, name: str) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _avail(t) -> int:
+    """Elements of t's storage from t's first element to the storage's end: all the library can
+    reach from t's address without leaving the allocation."""
+    return t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+
+
+def _len(t, given: Optional[int], name: str) -> int:
+    """The length in elements passed to the library beside tensor t: `given` when set, else t's
+    element count, which needs t contiguous (an expanded or overlapping view counts elements its
+    storage does not hold). Either way the length must stay inside t's storage."""
+    if given is None:
+        if not t.is_contiguous():
+            raise ValueError(f"{name} is not contiguous: pass the length the call may read or write")
+        given = t.numel()
+    if given < 0 or given > _avail(t):
+        raise ValueError(f"{name}: a length of {given} elements runs past the tensor's storage "
+                         f"({_avail(t)} elements from its start)")
+    return given
+
+
 def _check(code: int, ctx) -> None:
     if code != 0:
         msg = _lib.lib().tg_last_error(ctx).decode() if ctx else "error"
@@ -131,9 +151,11 @@ class PackedWeights:
     def from_device(kernels: "Kernels", n: int, k: int, precision: Precision, values, scales=None):
         """from_parts on GPU tensors (uint8 values, float32 scales) already in the panel layout."""
         out = ctypes.c_void_p()
-        rc = _lib.lib().tg_weights_upload_device(kernels._ctx, _dev(values, "uint8", "values"), values.numel(),
+        rc = _lib.lib().tg_weights_upload_device(kernels._ctx, _dev(values, "uint8", "values"),
+                                                 _len(values, None, "values"),
                                                  None if scales is None else _dev(scales, "float32", "scales"),
-                                                 0 if scales is None else scales.numel(), int(precision), n, k,
+                                                 0 if scales is None else _len(scales, None, "scales"),
+                                                 int(precision), n, k,
                                                  ctypes.byref(out))
         _check(rc, kernels._ctx)
         return PackedWeights(kernels, out, n, k, precision)
@@ -183,6 +205,14 @@ def encode(rows, n: int, k: int, precision: Precision):
                               scales.ctypes.data_as(ctypes.c_void_p), scales.size)
     _check(rc, None)
     return values, scales
+
+
+def random(length: int, seed: int) -> np.ndarray:
+    """The reference's test generator random(len, seed) (src/kernels/mod.rs:795-805): float32 values
+    in [-1, 1) from xorshift64, the same sequence for the same seed."""
+    out = np.empty(length, np.float32)
+    _lib.lib().tg_random(out.ctypes.data_as(ctypes.c_void_p), length, seed & (2**64 - 1))
+    return out
 
 
 def decode(values, scales, n: int, k: int, precision: Precision) -> np.ndarray:
@@ -264,16 +294,15 @@ class Kernels:
             return None
         e = _Epi()
         if epi.bias is not None:
-            e.bias, e.bias_len = _dev(epi.bias, "float32", "bias").value, epi.bias.numel()
+            e.bias, e.bias_len = _dev(epi.bias, "float32", "bias").value, _len(epi.bias, None, "bias")
         e.act, e.scale, e.accumulate = int(epi.act), float(epi.scale), int(bool(epi.accumulate))
         return ctypes.byref(e)
 
     def matmul_device(self, a, lda: int, m: int, w: PackedWeights, c, ldc: int, epi: Epilogue = Epilogue.PLAIN,
                       a_len: Optional[int] = None, c_len: Optional[int] = None):
         """Queues the product on GPU tensors (float32). a_len / c_len default to the tensors' sizes."""
-        rc = _lib.lib().tg_matmul_device(self._ctx, _dev(a, "float32", "a"), a.numel() if a_len is None
-                                         else a_len, lda, m, w._handle, _dev(c, "float32", "c"),
-                                         c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
+        rc = _lib.lib().tg_matmul_device(self._ctx, _dev(a, "float32", "a"), _len(a, a_len, "a"), lda, m, w._handle,
+                                         _dev(c, "float32", "c"), _len(c, c_len, "c"), ldc, self._epi_dev(epi))
         _check(rc, self._ctx)
 
     def linear_device(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
@@ -286,10 +315,9 @@ class Kernels:
         one GEMM for int8 weights in fast mode (n a multiple of 64). out is [m, ldo], ldo >= n / 2
         (default n / 2); epi must not accumulate."""
         ldo = w.n() // 2 if ldo is None else ldo
-        rc = _lib.lib().tg_linear_glu_device(self._ctx, _dev(a, "float32", "a"),
-                                             a.numel() if a_len is None else a_len, m, w._handle,
-                                             _dev(out, "float32", "out"),
-                                             out.numel() if out_len is None else out_len, ldo, self._epi_dev(epi))
+        rc = _lib.lib().tg_linear_glu_device(self._ctx, _dev(a, "float32", "a"), _len(a, a_len, "a"), m, w._handle,
+                                             _dev(out, "float32", "out"), _len(out, out_len, "out"), ldo,
+                                             self._epi_dev(epi))
         _check(rc, self._ctx)
 
     def matmul_rowmajor_device(self, a, lda: int, m: int, b, k: int, n: int, ldb: int, c, ldc: int,
@@ -298,9 +326,9 @@ class Kernels:
         """matmul with BView::row_major(b, k, n, ldb) as the right-hand side: f32 GPU tensors, the
         reference's fused sums. b must hold whole 16-column panels, as the reference's view checks."""
         rc = _lib.lib().tg_matmul_rowmajor_device(
-            self._ctx, _dev(a, "float32", "a"), a.numel() if a_len is None else a_len, lda, m,
-            _dev(b, "float32", "b"), b.numel() if b_len is None else b_len, k, n, ldb,
-            _dev(c, "float32", "c"), c.numel() if c_len is None else c_len, ldc, self._epi_dev(epi))
+            self._ctx, _dev(a, "float32", "a"), _len(a, a_len, "a"), lda, m,
+            _dev(b, "float32", "b"), _len(b, b_len, "b"), k, n, ldb,
+            _dev(c, "float32", "c"), _len(c, c_len, "c"), ldc, self._epi_dev(epi))
         _check(rc, self._ctx)
 
     def quant_bytes(self, m: int, k: int) -> int:
@@ -308,35 +336,42 @@ class Kernels:
 
     def quantize_rows_device(self, a, lda: int, m: int, k: int, qa, exps, a_len: Optional[int] = None):
         """Splits rows of a GPU tensor into the two-digit form (qa: uint8 tensor, exps: int32)."""
-        rc = _lib.lib().tg_quantize_rows_device(self._ctx, _dev(a, "float32", "a"),
-                                                a.numel() if a_len is None else a_len, lda, m, k,
-                                                _dev(qa, "uint8", "qa"), qa.numel(),
+        if _len(exps, None, "exps") < m:
+            raise ValueError("exps must hold m exponents")
+        rc = _lib.lib().tg_quantize_rows_device(self._ctx, _dev(a, "float32", "a"), _len(a, a_len, "a"), lda, m, k,
+                                                _dev(qa, "uint8", "qa"), _len(qa, None, "qa"),
                                                 _dev(exps, "int32", "exps"))
         _check(rc, self._ctx)
 
     def matmul_quantized_device(self, qa, exps, m: int, w: PackedWeights, c, ldc: int,
                                 epi: Epilogue = Epilogue.PLAIN):
         """The MFMA GEMM alone over rows quantised by quantize_rows_device."""
-        rc = _lib.lib().tg_matmul_quantized_device(self._ctx, _dev(qa, "uint8", "qa"), qa.numel(),
+        if _len(exps, None, "exps") < m:
+            raise ValueError("exps must hold m exponents")
+        rc = _lib.lib().tg_matmul_quantized_device(self._ctx, _dev(qa, "uint8", "qa"), _len(qa, None, "qa"),
                                                    _dev(exps, "int32", "exps"), m, w._handle,
-                                                   _dev(c, "float32", "c"), c.numel(), ldc,
+                                                   _dev(c, "float32", "c"), _len(c, None, "c"), ldc,
                                                    self._epi_dev(epi))
         _check(rc, self._ctx)
 
-    def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int):
-        rc = _lib.lib().tg_glu_device(self._ctx, _dev(x, "float32", "x"), ldx, m, half,
-                                      _dev(out, "float32", "out"), ldo)
+    def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int, x_len: Optional[int] = None,
+                   out_len: Optional[int] = None):
+        rc = _lib.lib().tg_glu_device(self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, m, half,
+                                      _dev(out, "float32", "out"), _len(out, out_len, "out"), ldo)
         _check(rc, self._ctx)
 
-    def layer_norm_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, out, ldo: int):
+    def layer_norm_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, out, ldo: int,
+                          x_len: Optional[int] = None, out_len: Optional[int] = None):
         """LayerNorm of m rows of GPU tensor x (n values each) into out (may be x)."""
-        rc = _lib.lib().tg_layer_norm_device(self._ctx, _dev(x, "float32", "x"), ldx, m, n,
-                                             _dev(gamma, "float32", "gamma"), _dev(beta, "float32", "beta"),
-                                             float(eps), _dev(out, "float32", "out"), ldo)
+        rc = _lib.lib().tg_layer_norm_device(self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, m, n,
+                                             _dev(gamma, "float32", "gamma"), _len(gamma, None, "gamma"),
+                                             _dev(beta, "float32", "beta"), _len(beta, None, "beta"),
+                                             float(eps), _dev(out, "float32", "out"), _len(out, out_len, "out"), ldo)
         _check(rc, self._ctx)
 
     def dwconv1d_device(self, x, ldx: int, frames: int, channels: int, w, kernel: int, bias, out, ldo: int,
-                        rows: int = None, t0: int = 0, stride: int = 1, act: "Act" = None, batch: int = 1):
+                        rows: int = None, t0: int = 0, stride: int = 1, act: "Act" = None, batch: int = 1,
+                        x_len: Optional[int] = None, out_len: Optional[int] = None):
         """Depthwise convolution of GPU tensor x (frames x channels) into out: row r is
         dwconv1d_frame at frame t0 + r * stride (rows defaults to frames), then SiLU when act is
         Act.SILU, as the conv module applies it. batch equal-length sequences of frames rows
@@ -344,9 +379,12 @@ class Kernels:
         rows = frames if rows is None else rows
         a = int(Act.NONE if act is None else act)
         xp = _dev(x, "float32", "x") if x is not None else None
-        rc = _lib.lib().tg_dwconv1d_device(self._ctx, xp, ldx, frames, batch, channels,
-                                           _dev(w, "float32", "w"), kernel, _dev(bias, "float32", "bias"),
-                                           t0, stride, rows, a, _dev(out, "float32", "out"), ldo)
+        xl = _len(x, x_len, "x") if x is not None else 0
+        rc = _lib.lib().tg_dwconv1d_device(self._ctx, xp, xl, ldx, frames, batch, channels,
+                                           _dev(w, "float32", "w"), _len(w, None, "w"), kernel,
+                                           _dev(bias, "float32", "bias"), _len(bias, None, "bias"),
+                                           t0, stride, rows, a, _dev(out, "float32", "out"),
+                                           _len(out, out_len, "out"), ldo)
         _check(rc, self._ctx)
 
     def synchronize(self) -> None:
@@ -380,13 +418,17 @@ class TdtDecoder:
         desc.durations = ctypes.cast(self._durs, ctypes.POINTER(ctypes.c_int32))
         desc.n_durations = len(self.durations)
         desc.joint, desc.joint_bias = joint._handle, _dev(joint_bias, "float32", "joint_bias").value
+        desc.joint_bias_len = _len(joint_bias, None, "joint_bias")
         desc.embedding = _dev(embedding, "float32", "embedding").value
+        desc.embedding_len = _len(embedding, None, "embedding")
         if len(lstm) > 4 or len(lstm) != len(lstm_bias):
             raise ValueError("1 to 4 LSTM layers, each with its bias")
         for i, (w, b) in enumerate(zip(lstm, lstm_bias)):
             desc.lstm[i] = w._handle
             desc.lstm_bias[i] = _dev(b, "float32", "lstm_bias").value
+            desc.lstm_bias_len[i] = _len(b, None, "lstm_bias")
         desc.proj, desc.proj_bias = proj._handle, _dev(proj_bias, "float32", "proj_bias").value
+        desc.proj_bias_len = _len(proj_bias, None, "proj_bias")
         handle = ctypes.c_void_p()
         _check(_lib.lib().tg_tdt_create(kernels._ctx, ctypes.addressof(desc), ctypes.byref(handle)), kernels._ctx)
         self._handle = handle
@@ -399,8 +441,9 @@ class TdtDecoder:
         rows x layers x [h, c]), updated in place; preds (rows x h) gets the projection."""
         toks = (ctypes.c_int32 * max(len(tokens), 1))(*[int(t) for t in tokens])
         _check(_lib.lib().tg_tdt_predict_device(self._kernels._ctx, self._handle, ctypes.addressof(toks), len(tokens),
-                                                _dev(states, "float32", "states"),
-                                                _dev(preds, "float32", "preds")), self._kernels._ctx)
+                                                _dev(states, "float32", "states"), _len(states, None, "states"),
+                                                _dev(preds, "float32", "preds"), _len(preds, None, "preds")),
+               self._kernels._ctx)
 
     def decode(self, enc_proj, state, pred, frame: int = 0, on_frame: int = 0, cap: Optional[int] = None):
         """The greedy decode over the rows of enc_proj (GPU tensor, frames x >= h) from frame with
@@ -413,10 +456,13 @@ class TdtDecoder:
             cap = max(frames - frame, 0) * max(self.max_symbols, 1)
         out = (_lib.Token * max(cap, 1))()
         f, o, n = ctypes.c_size_t(frame), ctypes.c_size_t(on_frame), ctypes.c_size_t(0)
+        enc_len = (frames - 1) * enc_proj.stride(0) + enc_proj.shape[1] if frames else 0
         rc = _lib.lib().tg_tdt_decode_device(self._kernels._ctx, self._handle, _dev(enc_proj, "float32", "enc_proj"),
-                                             enc_proj.stride(0), frames, _dev(state, "float32", "state"),
-                                             _dev(pred, "float32", "pred"), ctypes.byref(f), ctypes.byref(o),
-                                             ctypes.addressof(out), cap, ctypes.byref(n))
+                                             _len(enc_proj, enc_len, "enc_proj"), enc_proj.stride(0), frames,
+                                             _dev(state, "float32", "state"), _len(state, None, "state"),
+                                             _dev(pred, "float32", "pred"), _len(pred, None, "pred"),
+                                             ctypes.byref(f), ctypes.byref(o), ctypes.addressof(out), cap,
+                                             ctypes.byref(n))
         _check(rc, self._kernels._ctx)
         return [Token(t.id, t.frame, t.duration) for t in out[:n.value]], f.value, o.value
 

@@ -117,3 +117,78 @@ def test_gpu_tensors_are_checked_for_their_element_type_before_the_library_sees_
         _dev(torch.zeros(4, dtype=torch.float32), "float32", "a")  # on the host
     with pytest.raises(TypeError, match="qa must be a uint8 GPU tensor"):
         _dev(torch.zeros(4, dtype=torch.int8), "uint8", "qa")
+
+
+def test_half_and_bfloat16_encodings_match_the_oracle_over_many_bit_patterns(orc):
+    """layout.cpp rounds on the value (frexp, ldexp, nearbyint); the oracle follows the reference's
+    bit operations (src/quant.rs:91-156). They must agree on every f32 whose bits are drawn here:
+    all 65536 halves widened to f32 and nudged by one f32 ulp either way (the rounding ties and their
+    neighbours), every exponent with random significands, and the NaN payloads."""
+    from telmo_amd import Precision, encode
+
+    h = np.arange(65536, dtype=np.uint32)
+    widened = np.array([orc.f16_to_f32(int(x)) for x in h], np.float32).view(np.uint32)
+    rng = np.random.default_rng(6)
+    bits = np.concatenate([widened, widened + 1, widened - 1,
+                           rng.integers(0, 2**32, 400000, dtype=np.uint64).astype(np.uint32),
+                           (0x33000000 + np.arange(-4096, 4096)).astype(np.uint32),  # around 2^-25
+                           (0x477FF000 + np.arange(-4096, 4096)).astype(np.uint32),  # around 65520
+                           (0x7F800001 + rng.integers(0, 2**23 - 1, 2000)).astype(np.uint32)])
+    vals = bits.view(np.float32)
+    for p in (Precision.F16, Precision.BF16):
+        v1, _ = encode(vals, 1, vals.size, p)
+        v2, _ = orc.encode(vals, 1, vals.size, int(p))
+        assert np.array_equal(v1, v2), p
+
+
+def test_random_is_the_references_generator(orc):
+    """tg_random reproduces telmo's test generator (src/kernels/mod.rs:795-805), checked against a
+    plain-Python xorshift written from that source, and against the oracle's."""
+    from telmo_amd import random
+
+    def xorshift(length, seed):
+        mask = (1 << 64) - 1
+        s = (seed * 0x9E3779B97F4A7C15 & mask) | 1
+        out = []
+        for _ in range(length):
+            s ^= (s << 13) & mask
+            s ^= s >> 7
+            s ^= (s << 17) & mask
+            out.append(np.float32(np.float32(s >> 40) / np.float32(1 << 24)) * np.float32(2.0) - np.float32(1.0))
+        return np.array(out, np.float32)
+
+    for seed in (0, 1, 7, 2**63 + 5):
+        want = xorshift(700, seed)
+        assert np.array_equal(random(700, seed).view(np.uint32), want.view(np.uint32)), seed
+        assert np.array_equal(orc.random(700, seed % 2**64).view(np.uint32), want.view(np.uint32)), seed
+    # seed 0: the state starts at 1, and the first step is 1 ^ 1 << 13 = 0x2001, then ...
+    first = random(1, 0)[0]
+    s = 1
+    s ^= s << 13
+    s ^= s >> 7
+    s ^= (s << 17) & ((1 << 64) - 1)
+    assert first == np.float32((s >> 40) / 2**24 * 2 - 1)
+
+
+def test_device_lengths_stay_inside_the_tensor_storage():
+    """The wrappers pass a length beside every device pointer; it defaults to the element count only
+    for a contiguous tensor and never runs past the tensor's storage (an expanded or overlapping view
+    counts more elements than its storage holds)."""
+    import torch
+
+    from telmo_amd.kernels import _len
+
+    t = torch.zeros(100)
+    assert _len(t, None, "t") == 100
+    assert _len(t[10:], None, "t") == 90
+    assert _len(t[10:], 90, "t") == 90
+    with pytest.raises(ValueError, match="runs past"):
+        _len(t[10:], 91, "t")
+    with pytest.raises(ValueError, match="not contiguous"):
+        _len(torch.zeros(1).expand(50), None, "t")
+    with pytest.raises(ValueError, match="runs past"):
+        _len(torch.zeros(1).expand(50), 50, "t")
+    strided = torch.zeros(8, 12)[:, 4:]
+    with pytest.raises(ValueError, match="not contiguous"):
+        _len(strided, None, "v")
+    assert _len(strided, 7 * 12 + 8, "v") == 92

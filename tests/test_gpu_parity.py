@@ -572,8 +572,8 @@ def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
 @pytest.mark.parametrize("m,k,n,ldb", [(7, 128, 255, 255), (40, 128, 255, 256), (1, 33, 16, 20), (130, 300, 40, 64)])
 def test_rowmajor_right_hand_side_is_the_fused_reference(tk, orc, m, k, n, ldb):
     """BView::row_major (f32 activations as the right-hand side) gives the fused reference's bits: the
-    same values packed into panels through the oracle's fused matmul. Granite's packed rel product
-    is (m <= 128) x 128 -> 255."""
+    same values packed into panels through the oracle's fused matmul. The shapes include the
+    attention products' (m <= 128) x 128 -> 255."""
     import torch
 
     import telmo_amd
