@@ -92,7 +92,8 @@ uint32_t tg_ctx_mode(const tg_ctx *ctx);
 /* The message of the last failed call on this context ("" if none), copied into storage of the
  * calling thread: valid until that thread's next tg_last_error call. */
 const char *tg_last_error(const tg_ctx *ctx);
-/* Waits for all work queued on the context's stream. */
+/* Waits for all work queued on the context's stream; TG_ERR_HIP if a quantised-output product on it
+ * gave up waiting for its rows (tg_matmul_quantized_to_quant_device). */
 int tg_synchronize(tg_ctx *ctx);
 
 /* ---- weights ------------------------------------------------------------------------------ */
@@ -159,6 +160,21 @@ int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t ld
 int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                const tg_weights *w, float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
 
+/* The product of quantised rows whose outputs go out quantised in turn: epi(qa . w) as
+ * tg_matmul_quantized_device computes it, then the two-digit quantisation tg_quantize_rows_device
+ * makes of those f32 rows, into qa_out (tg_quant_bytes(m, n) bytes) and exps_out (m), bit-identical
+ * to the two calls; the f32 rows never reach memory. For a feed-forward block's first product,
+ * whose only reader is the second (src/parakeet.rs:1024-1060: ff_in with SiLU into s.big, then
+ * ff_out), which then takes qa_out through tg_matmul_quantized_device. int8 weights, fast mode, no
+ * accumulation (TG_ERR_ARG), n <= 65536. Each workgroup waits for the other column tiles of its
+ * rows, which the in-order dispatch of whole tile rows keeps short; a wait that runs out (about a
+ * second) marks the launch, and the next tg_synchronize on the context returns TG_ERR_HIP. Calls on
+ * one context share its rendezvous state, so they must not overlap on the device. Device pointers,
+ * queued on the stream. No counterpart in the reference, whose sums are all f32. */
+int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
+                                        const tg_weights *w, const tg_epilogue *epi, void *qa_out,
+                                        size_t qa_out_len, int32_t *exps_out, size_t exps_out_len);
+
 /* out = glu(epi(a . w)): the convolution module's pointwise_conv1 followed by its GLU
  * (src/parakeet.rs:1087-1104, src/granite.rs:881-899: Kernels::linear into [m, n], then
  * out[r, j] = g[r, j] * sigmoid(g[r, n / 2 + j]) for j < n / 2 through Kernels::glu), giving
@@ -189,6 +205,17 @@ int tg_glu_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t 
 int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t n,
                          const float *gamma, size_t gamma_len, const float *beta, size_t beta_len, float eps,
                          float *out, size_t out_len, size_t ldo);
+
+/* tg_layer_norm_device followed by tg_quantize_rows_device of its outputs, in one pass: the
+ * quantised rows (qa, tg_quant_bytes(m, n) bytes) and their m exponents (exps) that
+ * tg_matmul_quantized_device takes, bit-identical to the two calls. out, when not null, also gets
+ * the f32 LayerNorm (and may equal x); the reference's callers (src/parakeet.rs:1023, 1052, 1085,
+ * 1138) need only the product of the LayerNorm, so they pass null and the f32 rows never reach
+ * memory. n <= 65536. Device pointers, queued on the stream. */
+int tg_layer_norm_quant_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t n,
+                               const float *gamma, size_t gamma_len, const float *beta, size_t beta_len, float eps,
+                               float *out, size_t out_len, size_t ldo, void *qa, size_t qa_len, int32_t *exps,
+                               size_t exps_len);
 
 /* Depthwise 1-D convolution of frames x channels rows, "same" zero padding: output row r is frame
  * t = t0 + r * stride, out[r, c] = bias[c] + sum over taps j in order of w[j * channels + c] *

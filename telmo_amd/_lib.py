@@ -49,10 +49,13 @@ SIGNATURES = {
     "tg_quant_bytes": (_sz, [_sz, _sz]),
     "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
+    "tg_matmul_quantized_to_quant_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _p, _sz, _p, _sz]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _sz]),
     "tg_linear_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _sz, _p]),
     "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, ctypes.c_float, _p, _sz,
                                              _sz]),
+    "tg_layer_norm_quant_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, ctypes.c_float, _p,
+                                                   _sz, _sz, _p, _sz, _p, _sz]),
     "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p, _sz, _sz, _sz, _sz,
                                            _u32, _p, _sz, _sz]),
     "tg_tdt_create": (ctypes.c_int, [_p, _p, ctypes.POINTER(_p)]),

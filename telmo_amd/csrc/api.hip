@@ -42,6 +42,9 @@ struct tg_ctx {
     // The product before the GLU, when tg_linear_glu_device cannot fuse them.
     float *dg = nullptr;
     size_t dg_cap = 0;
+    // The row rendezvous of the quantised-output product (tg::QuantSync), zero between launches.
+    void *qsync = nullptr;
+    size_t qsync_cap = 0;
 };
 
 struct tg_weights {
@@ -296,7 +299,7 @@ void tg_ctx_destroy(tg_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (void *p : {(void *)ctx->qa, (void *)ctx->exps, (void *)ctx->da, (void *)ctx->dc, (void *)ctx->dbias,
-                    (void *)ctx->dg})
+                    (void *)ctx->dg, ctx->qsync})
         if (p) (void)hipFree(p);
     if (ctx->hst) (void)hipHostFree(ctx->hst);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -328,6 +331,18 @@ int tg_synchronize(tg_ctx *ctx) {
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->qsync) {
+        // A quantised-output product whose wait for its tile row ran out leaves its flag set (and
+        // its rendezvous state unknown): report it once and start the state over.
+        const tg::QuantSync q = tg::quant_sync_at(ctx->qsync, ctx->qsync_cap);
+        int32_t timed_out = 0;
+        TG_HIP(ctx, hipMemcpy(&timed_out, q.timeout, sizeof(timed_out), hipMemcpyDeviceToHost));
+        if (timed_out) {
+            TG_HIP(ctx, hipMemset(ctx->qsync, 0, tg::quant_sync_bytes(ctx->qsync_cap)));
+            return fail(ctx, TG_ERR_HIP, "a quantised-output product gave up waiting for its tile row; the quantised "
+                                         "rows it wrote are unusable");
+        }
+    }
     return TG_OK;
 }
 
@@ -489,6 +504,45 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
     return TG_OK;
 }
 
+int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
+                                        const tg_weights *w, const tg_epilogue *epi, void *qa_out,
+                                        size_t qa_out_len, int32_t *exps_out, size_t exps_out_len) {
+    if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
+    if (m == 0 || w->d.n == 0) return TG_OK;
+    const size_t n = w->d.n;
+    if (w->d.precision != TG_INT8 || w->d.k > tg::MAX_K_INT || ctx->mode != TG_MODE_FAST)
+        return fail(ctx, TG_ERR_UNSUPPORTED, "the quantised-output product takes int8 weights with k <= 65536 in fast mode");
+    if (n > tg::MAX_K_INT) return fail(ctx, TG_ERR_UNSUPPORTED, "outputs beyond the integer path's limit (65536)");
+    if (!qa || !exps || !qa_out || !exps_out) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (qa_out_len < tg_quant_bytes(m, n)) return fail(ctx, TG_ERR_SHAPE, "qa_out is too short");
+    if (exps_out_len < m) return fail(ctx, TG_ERR_SHAPE, "exps_out must hold m exponents");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
+    if (epi && epi->accumulate) return fail(ctx, TG_ERR_ARG, "quantised outputs are not accumulated");
+    if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
+    if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
+    if (qa == qa_out || exps == exps_out) return fail(ctx, TG_ERR_ARG, "the output must not overwrite the input");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    if (m > ctx->qsync_cap) {
+        // A larger rendezvous state, zeroed before any launch reads it.
+        TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->qsync) TG_HIP(ctx, hipFree(ctx->qsync));
+        ctx->qsync = nullptr;
+        ctx->qsync_cap = 0;
+        const size_t bytes = tg::quant_sync_bytes(m);
+        if (hipMalloc(&ctx->qsync, bytes) != hipSuccess) return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+        TG_HIP(ctx, hipMemset(ctx->qsync, 0, bytes));
+        ctx->qsync_cap = m;
+    }
+    TG_HIP(ctx, tg::launch_gemm_i8_qout(static_cast<const uint8_t *>(qa), exps, m, w->d, epi_args(epi, nullptr, false),
+                                        static_cast<uint8_t *>(qa_out), exps_out,
+                                        tg::quant_sync_at(ctx->qsync, ctx->qsync_cap), ctx->stream));
+    clear_error(ctx);
+    return TG_OK;
+}
+
 int tg_pack_upload_matrix(tg_ctx *ctx, const tg_pack *pack, const char *name, size_t n, size_t k,
                           tg_weights **out) {
     if (!ctx || !pack || !name || !out) return fail(ctx, TG_ERR_NULL, "null argument");
@@ -522,6 +576,30 @@ int tg_layer_norm_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, 
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, tg::launch_layer_norm(x, ldx, m, n, gamma, beta, eps, out, ldo, ctx->stream));
+    return TG_OK;
+}
+
+int tg_layer_norm_quant_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t n,
+                               const float *gamma, size_t gamma_len, const float *beta, size_t beta_len, float eps,
+                               float *out, size_t out_len, size_t ldo, void *qa, size_t qa_len, int32_t *exps,
+                               size_t exps_len) {
+    if (!ctx) return TG_ERR_NULL;
+    if (m == 0) return TG_OK;
+    if (!x || !gamma || !beta || !qa || !exps) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (n == 0) return fail(ctx, TG_ERR_SHAPE, "rows of no values have no LayerNorm to quantise");
+    if (ldx < n || (out && ldo < n)) return fail(ctx, TG_ERR_SHAPE, "ldx and ldo must be >= n");
+    if (x_len < span(m, ldx, n)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (out && out_len < span(m, ldo, n)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (gamma_len < n || beta_len < n) return fail(ctx, TG_ERR_SHAPE, "gamma and beta must hold n values");
+    if (qa_len < tg_quant_bytes(m, n)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (exps_len < m) return fail(ctx, TG_ERR_SHAPE, "exps must hold m exponents");
+    if (n > tg::MAX_K_INT) return fail(ctx, TG_ERR_UNSUPPORTED, "rows beyond the integer path's limit (65536)");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_layer_norm_quant(x, ldx, m, n, gamma, beta, eps, out, ldo, static_cast<uint8_t *>(qa), exps,
+                                            ctx->stream));
+    clear_error(ctx);
     return TG_OK;
 }
 

@@ -337,6 +337,152 @@ hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, con
     return hipGetLastError();
 }
 
+// LayerNorm of one 16-row block (one row block of the quantised layout) followed by the two-digit
+// quantisation of its outputs: the bits layer_norm_kernel writes, then those quantize_rows_regs_kernel
+// makes of them, in one launch. Pass 1 is layer_norm_kernel's: thread (r = tid / 16, j = tid % 16)
+// sums partial j of row r, the row's mean and rstd go to LDS. Pass 2 walks the runs of 16 inputs
+// the GEMM's A operand reads: run rho (rho = tid, tid + 256, ...) is k-block t = rho / 64 and operand
+// lane L = rho % 64, i.e. inputs 64 t + 16 (L / 16) + [0, 16) of row L % 16, so the 16 threads with
+// tid % 16 == r hold all of row r. Each computes its outputs (writing them to out when given) and
+// their largest magnitude; the row's largest gives its exponent, and pass 3 computes the outputs
+// again and writes each run's 16 hi and 16 lo digits as one 16-byte store each, lane L of the run's
+// 1 KB operand blocks. The inputs are read from memory once and from the caches after that. Digits
+// of rows past m and of inputs past n are zero. out may be x: every read of an input precedes the
+// write of its output in the same thread, and pass 1 ends at a barrier before any write.
+__global__ __launch_bounds__(256) void layer_norm_quant_kernel(const float *x, size_t ldx, size_t m, int n,
+                                                               const float *__restrict__ gamma,
+                                                               const float *__restrict__ beta, float eps, float *out,
+                                                               size_t ldo, uint8_t *__restrict__ qa,
+                                                               int32_t *__restrict__ exps, int kb, int vec) {
+    __shared__ float stat[16][2];
+    __shared__ float part_max[4][16];
+    __shared__ int part_bad[4][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t R = blockIdx.x, row0 = R * 16;
+    {
+        const int j = tid & 15, r = tid >> 4;
+        const size_t row = row0 + r;
+        const bool valid = row < m;
+        const float *xr = x + (valid ? row : 0) * ldx;
+        float s = 0.0f;
+        if (valid)
+            for (int i = j; i < n; i += 16) s = s + xr[i];
+        s = s + __shfl_xor(s, 8, 16);
+        s = s + __shfl_xor(s, 4, 16);
+        s = s + __shfl_xor(s, 2, 16);
+        s = s + __shfl_xor(s, 1, 16);
+        const float mean = s / (float)n;
+        float q = 0.0f;
+        if (valid)
+            for (int i = j; i < n; i += 16) {
+                const float d = xr[i] - mean;
+                q = __builtin_fmaf(d, d, q);
+            }
+        q = q + __shfl_xor(q, 8, 16);
+        q = q + __shfl_xor(q, 4, 16);
+        q = q + __shfl_xor(q, 2, 16);
+        q = q + __shfl_xor(q, 1, 16);
+        if (j == 0) {
+            stat[r][0] = mean;
+            stat[r][1] = 1.0f / __builtin_sqrtf(q / (float)n + eps);
+        }
+    }
+    __syncthreads();
+    const int r = tid & 15, runs = kb * 64;
+    const size_t row = row0 + r;
+    const bool valid = row < m;
+    const float mean = stat[r][0], rstd = stat[r][1];
+    const float *xr = x + (valid ? row : 0) * ldx;
+    // The outputs of run rho (zero past n) into y.
+    auto outputs = [&](int rho, float (&y)[16]) {
+        const int i0 = 64 * (rho >> 6) + 16 * ((rho & 63) >> 4);
+        if (vec && i0 + 16 <= n) {
+#pragma unroll
+            for (int c = 0; c < 16; c += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(xr + i0 + c);
+                const float4 g = *reinterpret_cast<const float4 *>(gamma + i0 + c);
+                const float4 b = *reinterpret_cast<const float4 *>(beta + i0 + c);
+                y[c] = __builtin_fmaf((v.x - mean) * rstd, g.x, b.x);
+                y[c + 1] = __builtin_fmaf((v.y - mean) * rstd, g.y, b.y);
+                y[c + 2] = __builtin_fmaf((v.z - mean) * rstd, g.z, b.z);
+                y[c + 3] = __builtin_fmaf((v.w - mean) * rstd, g.w, b.w);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                const int i = i0 + c;
+                y[c] = i < n ? __builtin_fmaf((xr[i] - mean) * rstd, gamma[i], beta[i]) : 0.0f;
+            }
+        }
+        return i0;
+    };
+    float amax = 0.0f;
+    int bad = 0;
+    if (valid) {
+        for (int rho = tid; rho < runs; rho += 256) {
+            float y[16];
+            const int i0 = outputs(rho, y);
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                bad |= !__builtin_isfinite(y[c]);
+                amax = fmaxf(amax, fabsf(y[c]));
+            }
+            if (out) {
+                float *orow = out + row * ldo;
+                if (vec && i0 + 16 <= n && ((reinterpret_cast<uintptr_t>(out) | ldo * sizeof(float)) % 16 == 0)) {
+#pragma unroll
+                    for (int c = 0; c < 16; c += 4)
+                        *reinterpret_cast<float4 *>(orow + i0 + c) = make_float4(y[c], y[c + 1], y[c + 2], y[c + 3]);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 16; c++)
+                        if (i0 + c < n) orow[i0 + c] = y[c];
+                }
+            }
+        }
+    }
+    // The row's threads: tid % 16 == r, four in each wavefront.
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    bad |= __shfl_xor(bad, 16, 64);
+    bad |= __shfl_xor(bad, 32, 64);
+    if (lane < 16) {
+        part_max[wave][lane] = amax;
+        part_bad[wave][lane] = bad;
+    }
+    __syncthreads();
+    amax = fmaxf(fmaxf(part_max[0][r], part_max[1][r]), fmaxf(part_max[2][r], part_max[3][r]));
+    bad = part_bad[0][r] | part_bad[1][r] | part_bad[2][r] | part_bad[3][r];
+    const int32_t e = bad ? EXP_NONFINITE : row_exponent_of(amax);
+    if (valid && tid < 16) exps[row] = e;
+    for (int rho = tid; rho < runs; rho += 256) {
+        uint4 hi = make_uint4(0, 0, 0, 0), lo = make_uint4(0, 0, 0, 0);
+        if (valid) {
+            float y[16];
+            outputs(rho, y);
+            digits4(y[0], y[1], y[2], y[3], e, hi.x, lo.x);
+            digits4(y[4], y[5], y[6], y[7], e, hi.y, lo.y);
+            digits4(y[8], y[9], y[10], y[11], e, hi.z, lo.z);
+            digits4(y[12], y[13], y[14], y[15], e, hi.w, lo.w);
+        }
+        uint8_t *blk = qa + ((R * kb + (rho >> 6)) * 2) * 1024 + (rho & 63) * 16;
+        *reinterpret_cast<uint4 *>(blk) = hi;
+        *reinterpret_cast<uint4 *>(blk + 1024) = lo;
+    }
+}
+
+hipError_t launch_layer_norm_quant(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                                   const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
+                                   hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    const size_t kb = div_ceil(n, KBLK);
+    const int vec = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
+                      reinterpret_cast<uintptr_t>(beta)) % 16 == 0);
+    hipLaunchKernelGGL(layer_norm_quant_kernel, dim3((unsigned)div_ceil(m, (size_t)16)), dim3(256), 0, s, x, ldx, m,
+                       (int)n, gamma, beta, eps, out, ldo, qa, exps, (int)kb, vec);
+    return hipGetLastError();
+}
+
 // Depthwise 1-D convolution with "same" zero padding, one output row per frame
 // t = t0 + r * stride, as the reference's dwconv1d_frame computes it (src/kernels/scalar.rs:164-187):
 // out[c] = bias[c], then for each tap j in order, out[c] = out[c] + w[j][c] * x[t + j - kernel/2][c]

@@ -354,6 +354,19 @@ class Kernels:
                                                    self._epi_dev(epi))
         _check(rc, self._ctx)
 
+    def matmul_quantized_to_quant_device(self, qa, exps, m: int, w: PackedWeights, qa_out, exps_out,
+                                         epi: Epilogue = Epilogue.PLAIN):
+        """The MFMA GEMM over quantised rows with its outputs epi(qa . w) quantised into qa_out and exps_out
+        (the f32 rows never reach memory); epi must not accumulate."""
+        for t, name, need in ((exps, "exps", m), (exps_out, "exps_out", m)):
+            if _len(t, None, name) < need:
+                raise ValueError(f"{name} must hold m exponents")
+        rc = _lib.lib().tg_matmul_quantized_to_quant_device(
+            self._ctx, _dev(qa, "uint8", "qa"), _len(qa, None, "qa"), _dev(exps, "int32", "exps"), m, w._handle,
+            self._epi_dev(epi), _dev(qa_out, "uint8", "qa_out"), _len(qa_out, None, "qa_out"),
+            _dev(exps_out, "int32", "exps_out"), _len(exps_out, None, "exps_out"))
+        _check(rc, self._ctx)
+
     def glu_device(self, x, ldx: int, m: int, half: int, out, ldo: int, x_len: Optional[int] = None,
                    out_len: Optional[int] = None):
         rc = _lib.lib().tg_glu_device(self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, m, half,
@@ -367,6 +380,18 @@ class Kernels:
                                              _dev(gamma, "float32", "gamma"), _len(gamma, None, "gamma"),
                                              _dev(beta, "float32", "beta"), _len(beta, None, "beta"),
                                              float(eps), _dev(out, "float32", "out"), _len(out, out_len, "out"), ldo)
+        _check(rc, self._ctx)
+
+    def layer_norm_quant_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, qa, exps, out=None,
+                                ldo: Optional[int] = None, x_len: Optional[int] = None, out_len: Optional[int] = None):
+        """LayerNorm of m rows of GPU tensor x, quantised into qa (uint8, quant_bytes(m, n)) and exps (int32,
+        m) for matmul_quantized_device; out (optional, may be x) also gets the f32 LayerNorm."""
+        ldo = n if ldo is None else ldo
+        rc = _lib.lib().tg_layer_norm_quant_device(
+            self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, m, n, _dev(gamma, "float32", "gamma"),
+            _len(gamma, None, "gamma"), _dev(beta, "float32", "beta"), _len(beta, None, "beta"), float(eps),
+            None if out is None else _dev(out, "float32", "out"), 0 if out is None else _len(out, out_len, "out"),
+            ldo, _dev(qa, "uint8", "qa"), _len(qa, None, "qa"), _dev(exps, "int32", "exps"), _len(exps, None, "exps"))
         _check(rc, self._ctx)
 
     def dwconv1d_device(self, x, ldx: int, frames: int, channels: int, w, kernel: int, bias, out, ldo: int,

@@ -20,3 +20,25 @@ def orc():
 
     oracle.lib()
     return oracle
+
+
+@pytest.fixture(scope="session")
+def gpu_stream():
+    """One stream for the GPU tests, made torch's current stream: tensors the tests create, fill and
+    read, and the library's kernels (a context bound to it), are ordered on it."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    yield stream
+    torch.cuda.synchronize()
+
+
+@pytest.fixture(scope="module")
+def tk(gpu_stream):
+    """A library context on the tests' stream."""
+    import telmo_amd
+
+    k = telmo_amd.Kernels(0, stream=gpu_stream.cuda_stream)
+    yield k
+    k.close()

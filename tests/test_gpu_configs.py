@@ -30,15 +30,6 @@ def say(*args):
     print("[case]", *args, flush=True)
 
 
-@pytest.fixture(scope="module")
-def tk():
-    import telmo_amd
-
-    k = telmo_amd.Kernels()
-    yield k
-    k.close()
-
-
 def weights(tk, n, k, seed):
     import telmo_amd
 

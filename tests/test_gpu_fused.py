@@ -1,0 +1,183 @@
+"""The fused row paths of the device layer against their unfused equivalents, through the C ABI, on an
+MI355X: each must write exactly the bytes of the calls it replaces.
+
+* tg_layer_norm_quant_device = tg_layer_norm_device then tg_quantize_rows_device (digits, exponents,
+  and the f32 LayerNorm when asked for, in place too);
+* tg_matmul_quantized_to_quant_device = tg_matmul_quantized_device into f32 rows then
+  tg_quantize_rows_device, for every launch of a sequence and every replay of a captured graph (its
+  row rendezvous state must come back to zero by itself).
+"""
+import numpy as np
+import pytest
+
+import bench
+from helpers import pack_int8, int8_weights, normal
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*args):
+    print("[case]", *args, flush=True)
+
+
+def same_floats(got, want):
+    """Bit-equal outside NaNs, NaN in the same places: which NaN an operation on two NaNs returns (and
+    so its sign bit) depends on the instruction the compiler picks, not on the arithmetic."""
+    import torch
+
+    nan = torch.isnan(want)
+    return torch.equal(torch.isnan(got), nan) and torch.equal(got[~nan].view(torch.int32), want[~nan].view(torch.int32))
+
+
+def quantised(tk, x, ldx, m, k):
+    """qa and exps of rows of x through the row quantiser, qa zero-filled first."""
+    import torch
+
+    qa = torch.zeros(tk.quant_bytes(m, k), dtype=torch.uint8, device="cuda")
+    ex = torch.zeros(m, dtype=torch.int32, device="cuda")
+    tk.quantize_rows_device(x, ldx, m, k, qa, ex, a_len=(m - 1) * ldx + k)
+    return qa, ex
+
+
+LN_CASES = [(750, 1024, 1024), (12000, 1024, 1024), (37, 1000, 1003), (5, 64, 64), (19, 100, 103), (3, 4096, 4096),
+            (16, 17, 17), (33, 2048, 2048), (1, 1, 4)]
+
+
+@pytest.mark.parametrize("m,n,ldx", LN_CASES)
+def test_layer_norm_quant_is_layer_norm_then_quantise(tk, m, n, ldx):
+    import torch
+
+    rng = np.random.default_rng(m + n)
+    x = (1.5 + 3.0 * rng.standard_normal((m, ldx))).astype(np.float32)
+    if m > 3:
+        x[2, min(5, n - 1)] = np.nan  # a non-finite row
+    gamma = (1.0 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    say("ln_quant", m, n, ldx)
+    xd, gd, bd = (torch.from_numpy(v).cuda() for v in (x, gamma, beta))
+    ln = torch.full((m, n), 3.0, device="cuda")
+    tk.layer_norm_device(xd, ldx, m, n, gd, bd, 1e-5, ln, n)
+    want_qa, want_ex = quantised(tk, ln, n, m, n)
+    qa = torch.zeros_like(want_qa)
+    ex = torch.zeros_like(want_ex)
+    out = torch.full((m, n), 3.0, device="cuda")
+    tk.layer_norm_quant_device(xd, ldx, m, n, gd, bd, 1e-5, qa, ex, out=out)
+    tk.synchronize()
+    assert same_floats(out, ln)
+    assert torch.equal(qa, want_qa)
+    assert torch.equal(ex, want_ex)
+    qa2 = torch.full_like(want_qa, 0)
+    tk.layer_norm_quant_device(xd, ldx, m, n, gd, bd, 1e-5, qa2, ex)  # no f32 output
+    if ldx == n:  # in place: x becomes its LayerNorm
+        tk.layer_norm_quant_device(xd, ldx, m, n, gd, bd, 1e-5, qa, ex, out=xd)
+        tk.synchronize()
+        assert same_floats(xd, ln)
+    tk.synchronize()
+    assert torch.equal(qa2, want_qa)
+
+
+QOUT_CASES = [  # m, k, n, act, with_bias
+    (750, 1024, 4096, 2, False), (12000, 1024, 4096, 2, False), (7500, 1024, 4096, 2, False),
+    (37, 200, 130, 0, True), (130, 64, 200, 1, True), (1, 100, 64, 2, False), (300, 1000, 1000, 1, True),
+    (5000, 256, 100, 0, False), (2100, 640, 4100, 2, True), (64, 4096, 1024, 0, False)]
+
+
+@pytest.mark.parametrize("m,k,n,act,with_bias", QOUT_CASES)
+def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, with_bias):
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(m * 3 + k + n)
+    a = normal(rng, (m, k))
+    if m > 10:
+        a[7, 3] = np.inf  # a row whose outputs are all NaN
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    bias = torch.from_numpy(normal(rng, n)).cuda() if with_bias else None
+    epi = telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act(act), scale=0.75)
+    say("qout", m, k, n, act, with_bias)
+    ad = torch.from_numpy(a).cuda()
+    qa, ex = quantised(tk, ad, k, m, k)
+    c = torch.zeros((m, n), device="cuda")
+    tk.matmul_quantized_device(qa, ex, m, w, c, n, epi)
+    want_qa, want_ex = quantised(tk, c, n, m, n)
+    for rep in range(3):  # the rendezvous state must be clean for every launch
+        got_qa = torch.zeros_like(want_qa)
+        got_ex = torch.zeros_like(want_ex)
+        tk.matmul_quantized_to_quant_device(qa, ex, m, w, got_qa, got_ex, epi)
+        tk.synchronize()
+        assert torch.equal(got_ex, want_ex), rep
+        assert torch.equal(got_qa, want_qa), rep
+    w.close()
+
+
+def test_quantised_output_product_replays_in_a_graph(tk):
+    """Captured in a HIP graph and replayed, with eager work and synchronisations between the replays,
+    the product gives the eager bytes every time."""
+    import torch
+
+    import telmo_amd
+
+    m, k, n = 750, 1024, 4096
+    rng = np.random.default_rng(9)
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    stream = torch.cuda.Stream()
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    w = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+    epi = telmo_amd.Epilogue(act=telmo_amd.Act.SILU)
+    with torch.cuda.stream(stream):
+        a = torch.from_numpy(normal(rng, (m, k))).cuda()
+        qa = torch.zeros(kern.quant_bytes(m, k), dtype=torch.uint8, device="cuda")
+        ex = torch.zeros(m, dtype=torch.int32, device="cuda")
+        kern.quantize_rows_device(a, k, m, k, qa, ex)
+        want_qa = torch.zeros(kern.quant_bytes(m, n), dtype=torch.uint8, device="cuda")
+        want_ex = torch.zeros(m, dtype=torch.int32, device="cuda")
+        kern.matmul_quantized_to_quant_device(qa, ex, m, w, want_qa, want_ex, epi)
+        got_qa, got_ex = torch.zeros_like(want_qa), torch.zeros_like(want_ex)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            kern.matmul_quantized_to_quant_device(qa, ex, m, w, got_qa, got_ex, epi)
+        for rep in range(4):
+            got_qa.zero_()
+            got_ex.zero_()
+            graph.replay()
+            kern.matmul_quantized_to_quant_device(qa, ex, m, w, want_qa, want_ex, epi)  # eager work between
+            stream.synchronize()
+            say("graph replay", rep)
+            assert torch.equal(got_qa, want_qa) and torch.equal(got_ex, want_ex), rep
+    kern.synchronize()
+    w.close()
+    kern.close()
+
+
+def test_quantised_output_refusals(tk):
+    import torch
+
+    import telmo_amd
+
+    m, k, n = 40, 64, 128
+    rng = np.random.default_rng(3)
+    q, s = int8_weights(rng, n, k)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, *pack_int8(q, s))
+    qa = torch.zeros(tk.quant_bytes(m, k), dtype=torch.uint8, device="cuda")
+    ex = torch.zeros(m, dtype=torch.int32, device="cuda")
+    qo = torch.zeros(tk.quant_bytes(m, n), dtype=torch.uint8, device="cuda")
+    eo = torch.zeros(m, dtype=torch.int32, device="cuda")
+    with pytest.raises(telmo_amd.TelmoError):
+        tk.matmul_quantized_to_quant_device(qa, ex, m, w, qo, eo, telmo_amd.Epilogue(accumulate=True))
+    with pytest.raises(telmo_amd.TelmoError):
+        tk.matmul_quantized_to_quant_device(qa, ex, m, w, qo[:-1], eo)
+    tk.set_mode(tk.EXACT)
+    try:
+        with pytest.raises(telmo_amd.TelmoError):
+            tk.matmul_quantized_to_quant_device(qa, ex, m, w, qo, eo)
+    finally:
+        tk.set_mode(tk.FAST)
+    with pytest.raises(telmo_amd.TelmoError):
+        tk.layer_norm_quant_device(torch.zeros((m, k), device="cuda"), k, m, k, torch.ones(k, device="cuda"),
+                                   torch.zeros(k, device="cuda"), 1e-5, qa[:-1], ex)
+    w.close()

@@ -23,15 +23,6 @@ def say(*args):
     print("[case]", *args, flush=True)
 
 
-@pytest.fixture(scope="module")
-def tk():
-    import telmo_amd
-
-    k = telmo_amd.Kernels()
-    yield k
-    k.close()
-
-
 def epi_of(telmo_amd, bias, act, accumulate, scale=0.5):
     return telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act(act), scale=scale, accumulate=accumulate)
 

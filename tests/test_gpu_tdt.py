@@ -23,15 +23,6 @@ def say(*args):
     print("[case]", *args, flush=True)
 
 
-@pytest.fixture(scope="module")
-def tk():
-    import telmo_amd
-
-    k = telmo_amd.Kernels()
-    yield k
-    k.close()
-
-
 def upload(tk, net, durations=None):
     import torch
 
