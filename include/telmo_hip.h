@@ -160,6 +160,13 @@ int tg_quantize_rows_device(tg_ctx *ctx, const float *a, size_t a_len, size_t ld
 int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                const tg_weights *w, float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
 
+/* tg_linear_glu_device on quantised rows: out = glu(epi(qa . w)), the GLU in the GEMM's epilogue,
+ * for a convolution module whose pointwise_conv1 input comes out of tg_layer_norm_quant_device.
+ * int8 weights, n a multiple of 64, fast mode (TG_ERR_UNSUPPORTED otherwise); no accumulation. */
+int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
+                                   const tg_weights *w, float *out, size_t out_len, size_t ldo,
+                                   const tg_epilogue *epi);
+
 /* The product of quantised rows whose outputs go out quantised in turn: epi(qa . w) as
  * tg_matmul_quantized_device computes it, then the two-digit quantisation tg_quantize_rows_device
  * makes of those f32 rows, into qa_out (tg_quant_bytes(m, n) bytes) and exps_out (m), bit-identical

@@ -49,6 +49,7 @@ SIGNATURES = {
     "tg_quant_bytes": (_sz, [_sz, _sz]),
     "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),
     "tg_matmul_quantized_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
+    "tg_matmul_quantized_glu_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_matmul_quantized_to_quant_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _p, _sz, _p, _sz]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _sz]),
     "tg_linear_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _sz, _p]),

@@ -504,6 +504,33 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
     return TG_OK;
 }
 
+int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
+                                   const tg_weights *w, float *out, size_t out_len, size_t ldo,
+                                   const tg_epilogue *epi) {
+    if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
+    const size_t n = w->d.n, half = n / 2;
+    if (n % 2) return fail(ctx, TG_ERR_SHAPE, "the product's outputs must be an even count");
+    if (epi && epi->accumulate) return fail(ctx, TG_ERR_ARG, "the GLU's input is not accumulated");
+    if (m == 0 || n == 0) return TG_OK;
+    if (w->d.precision != TG_INT8 || w->d.k > tg::MAX_K_INT || !tg::gemm_glu_fits(n) || ctx->mode != TG_MODE_FAST)
+        return fail(ctx, TG_ERR_UNSUPPORTED,
+                    "the quantised GLU product takes int8 weights, k <= 65536 and n a multiple of 64, in fast mode");
+    if (!qa || !exps || !out) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (ldo < half) return fail(ctx, TG_ERR_SHAPE, "ldo must be >= n / 2");
+    if (out_len < span(m, ldo, half)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
+    if (epi && epi->bias && epi->bias_len < n) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (epi && epi->act > TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "unknown activation");
+    if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_gemm_i8_glu(static_cast<const uint8_t *>(qa), exps, m, w->d, out, ldo,
+                                       epi_args(epi, nullptr, false), ctx->stream));
+    clear_error(ctx);
+    return TG_OK;
+}
+
 int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                         const tg_weights *w, const tg_epilogue *epi, void *qa_out,
                                         size_t qa_out_len, int32_t *exps_out, size_t exps_out_len) {

@@ -354,6 +354,18 @@ class Kernels:
                                                    self._epi_dev(epi))
         _check(rc, self._ctx)
 
+    def matmul_quantized_glu_device(self, qa, exps, m: int, w: PackedWeights, out, ldo: Optional[int] = None,
+                                    epi: Epilogue = Epilogue.PLAIN, out_len: Optional[int] = None):
+        """linear_glu_device on quantised rows: out = glu(epi(qa . w)) with the GLU in the GEMM's epilogue."""
+        ldo = w.n() // 2 if ldo is None else ldo
+        if _len(exps, None, "exps") < m:
+            raise ValueError("exps must hold m exponents")
+        rc = _lib.lib().tg_matmul_quantized_glu_device(self._ctx, _dev(qa, "uint8", "qa"), _len(qa, None, "qa"),
+                                                       _dev(exps, "int32", "exps"), m, w._handle,
+                                                       _dev(out, "float32", "out"), _len(out, out_len, "out"), ldo,
+                                                       self._epi_dev(epi))
+        _check(rc, self._ctx)
+
     def matmul_quantized_to_quant_device(self, qa, exps, m: int, w: PackedWeights, qa_out, exps_out,
                                          epi: Epilogue = Epilogue.PLAIN):
         """The MFMA GEMM over quantised rows with its outputs epi(qa . w) quantised into qa_out and exps_out

@@ -1,0 +1,72 @@
+"""Parakeet::layer (src/parakeet.rs:1011-1172) composed from the oracle's functions, the checker of the
+device layer (telmo_amd.conformer): LayerNorm rows (or_layer_norm), products (the integer oracle
+or_matmul_fast of the fast path, or the fused f32 reference or_matmul), the GLU, the depthwise
+convolution + SiLU per utterance, in the reference's order, with the V third of qkv standing in for
+the attention core as the device layer's default does."""
+import numpy as np
+
+import bench
+
+NONE, SILU = 0, 2
+INT8 = 3
+
+
+def synth_layer(d, ff, conv_kernel, seed):
+    """A layer's weights from telmo's generator: int8 matrices with scales, LayerNorms near (1, 0),
+    depthwise taps and bias. Returns {name: (values, scales, n, k)}, {norm: (gamma, beta)}, dw_w,
+    dw_b, all numpy."""
+    shapes = {"ff1_in": (ff, d), "ff1_out": (d, ff), "qkv": (3 * d, d), "out": (d, d), "pw1": (2 * d, d),
+              "pw2": (d, d), "ff2_in": (ff, d), "ff2_out": (d, ff)}
+    mats = {}
+    for i, (name, (n, k)) in enumerate(shapes.items()):
+        values, scales = bench.panel_layout(bench.synth_int8(n, k, seed + 10 * i), bench.synth_scales(n, seed + 10 * i + 1))
+        mats[name] = (values, scales, n, k)
+    norms = {}
+    for i, name in enumerate(("norm_ff1", "norm_att", "norm_conv", "norm_ff2", "norm_out")):
+        g = (1.0 + 0.1 * bench.synth_normal((d,), seed + 200 + 2 * i)).astype(np.float32)
+        b = (0.1 * bench.synth_normal((d,), seed + 201 + 2 * i)).astype(np.float32)
+        norms[name] = (g, b)
+    dw_w = (0.3 * bench.synth_normal((conv_kernel, d), seed + 300)).astype(np.float32)
+    dw_b = (0.1 * bench.synth_normal((d,), seed + 301)).astype(np.float32)
+    return mats, norms, dw_w, dw_b
+
+
+def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True):
+    """The layer on numpy rows x [t, d] (returned, x untouched): fast = True composes the integer
+    oracle (the device layer's bits), False the reference's fused f32 products."""
+    x = x.copy()
+    t, d = x.shape
+
+    def linear(a, lda, name, c, act=NONE, scale=1.0, accumulate=False):
+        values, scales, n, k = mats[name]
+        flat = np.ascontiguousarray(a).reshape(-1)
+        out = c.reshape(-1)
+        if fast:
+            rc = orc.matmul_fast(flat, lda, t, values, scales, n, k, out, n, None, act, scale, accumulate)
+        else:
+            rc = orc.matmul(True, flat, lda, t, values, scales, INT8, n, k, out, n, None, act, scale, accumulate)
+        assert rc == 0
+        return out.reshape(t, n)
+
+    def ln(rows, norm):
+        g, b = norms[norm]
+        return np.stack([orc.layer_norm(rows[r], g, b, 1e-5) for r in range(t)])
+
+    def feed_forward(norm, w_in, w_out):
+        h = ln(x, norm)
+        hid = linear(h, d, w_in, np.zeros((t, mats[w_in][2]), np.float32), SILU)
+        linear(hid, hid.shape[1], w_out, x, NONE, 0.5, True)
+
+    feed_forward("norm_ff1", "ff1_in", "ff1_out")
+    h = ln(x, "norm_att")
+    qkv = linear(h, d, "qkv", np.zeros((t, 3 * d), np.float32))
+    linear(qkv.reshape(-1)[2 * d:], 3 * d, "out", x, NONE, 1.0, True)
+    h = ln(x, "norm_conv")
+    g = linear(h, d, "pw1", np.zeros((t, 2 * d), np.float32))
+    u = np.stack([orc.glu(g[r, :d], g[r, d:]) for r in range(t)])
+    frames = t // utterances
+    conv = np.concatenate([orc.dwconv1d(u[s * frames:(s + 1) * frames], dw_w, dw_b, silu=True)
+                           for s in range(utterances)])
+    linear(conv, d, "pw2", x, NONE, 1.0, True)
+    feed_forward("norm_ff2", "ff2_in", "ff2_out")
+    return ln(x, "norm_out")
