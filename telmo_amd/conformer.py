@@ -5,7 +5,9 @@ GPU memory, with every int8 product on the library's fast path and the rows betw
 quantised wherever the product is their only reader:
 
     FF1   LayerNorm(norm_ff1)       -> quantised rows          tg_layer_norm_quant_device
-          ff1_in + SiLU             -> quantised hidden rows   tg_matmul_quantized_to_quant_device
+          ff1_in + SiLU             -> quantised hidden rows   tg_matmul_quantized_device + the row
+                                                               quantiser, or (quantised_hidden)
+                                                               tg_matmul_quantized_to_quant_device
           ff1_out, x += 0.5 * .                                tg_matmul_quantized_device
     att   LayerNorm(norm_att)       -> quantised rows
           qkv                       -> f32 q, k, v (the attention core reads them)
@@ -21,14 +23,16 @@ quantised wherever the product is their only reader:
 
 Each step writes exactly the bits the unfused calls write (LayerNorm then quantise, product then
 quantise), so the layer is the reference's sequence evaluated with the fast path's products: the
-integer oracle composed in the same order reproduces it bit for bit. Batches of equal-length
-utterances are stacked along the rows; only the depthwise convolution sees the boundaries."""
+integer oracle composed in the same order reproduces it bit for bit. Q8_0 matrices take the unfused
+steps where a fused kernel is int8-only (FF in, pw1 + GLU): their f32 rows go through memory.
+Batches of equal-length utterances are stacked along the rows; only the depthwise convolution sees
+the boundaries."""
 from __future__ import annotations
 
 from dataclasses import dataclass
 from typing import Callable, Dict, Optional
 
-from .kernels import Act, Epilogue, Kernels, PackedWeights
+from .kernels import Act, Epilogue, Kernels, PackedWeights, Precision
 
 # The layer's products (src/parakeet.rs:1011-1172): name -> (inputs, outputs) in units of d_model
 # (ff_mult for the feed-forward hidden width); pos is the attention's position projection.
@@ -51,10 +55,14 @@ class LayerWeights:
 class ConformerLayer:
     """Parakeet::layer on the device for up to `rows` frames of width d (ff hidden), on one context."""
 
-    def __init__(self, kern: Kernels, d: int, ff: int, conv_kernel: int, rows: int, eps: float = 1e-5):
+    def __init__(self, kern: Kernels, d: int, ff: int, conv_kernel: int, rows: int, eps: float = 1e-5,
+                 quantised_hidden: bool = False):
         import torch
 
         self.kern, self.d, self.ff, self.conv_kernel, self.rows, self.eps = kern, d, ff, conv_kernel, rows, eps
+        # FF in writes its hidden rows quantised (tg_matmul_quantized_to_quant_device) when set, else
+        # in f32 followed by the row quantiser: the same bits either way.
+        self.quantised_hidden = quantised_hidden
         dev = "cuda"
         u8 = lambda n: torch.empty(n, dtype=torch.uint8, device=dev)  # noqa: E731
         i32 = lambda n: torch.empty(n, dtype=torch.int32, device=dev)  # noqa: E731
@@ -64,6 +72,14 @@ class ConformerLayer:
         self.qkv = f32(rows, 3 * d)
         self.glu = f32(rows, d)
         self.conv = f32(rows, d)
+        self._f32 = {}  # f32 rows of the unfused steps (weights other than int8), made on first use
+
+    def _rows(self, name: str, width: int):
+        import torch
+
+        if name not in self._f32:
+            self._f32[name] = torch.empty((self.rows, width), dtype=torch.float32, device="cuda")
+        return self._f32[name]
 
     def forward(self, x, t: int, w: LayerWeights, utterances: int = 1,
                 attention: Optional[Callable] = None, pos=None, p_out=None) -> None:
@@ -83,8 +99,18 @@ class ConformerLayer:
         def feed_forward(norm, w_in, w_out):
             g, b = w.norms[norm]
             k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-            k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, m[w_in], self.qa_ff, self.ex_ff, silu)
-            k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
+            if m[w_in].precision() == Precision.INT8 and self.quantised_hidden:
+                k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, m[w_in], self.qa_ff, self.ex_ff, silu)
+                k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
+            elif m[w_in].precision() == Precision.INT8:
+                hid = self._rows("hid", ff)[:t]
+                k.matmul_quantized_device(self.qa_d, self.ex_d, t, m[w_in], hid, ff, silu)
+                k.quantize_rows_device(hid, ff, t, ff, self.qa_ff, self.ex_ff)
+                k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
+            else:  # the quantised-output product takes int8 weights: the hidden rows go through f32
+                hid = self._rows("hid", ff)[:t]
+                k.matmul_quantized_device(self.qa_d, self.ex_d, t, m[w_in], hid, ff, silu)
+                k.linear_device(hid, t, m[w_out], x, half_acc)
 
         feed_forward("norm_ff1", "ff1_in", "ff1_out")
         # self-attention: q, k, v in f32 for the attention core
@@ -103,7 +129,12 @@ class ConformerLayer:
         # convolution module
         g, b = w.norms["norm_conv"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-        k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], d)
+        if m["pw1"].precision() == Precision.INT8:
+            k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], d)
+        else:
+            g2 = self._rows("pw1", 2 * d)[:t]
+            k.matmul_quantized_device(self.qa_d, self.ex_d, t, m["pw1"], g2, 2 * d)
+            k.glu_device(g2, 2 * d, t, d, self.glu, d, out_len=t * d)
         k.dwconv1d_device(self.glu, d, t // utterances, d, w.dw_w, self.conv_kernel, w.dw_b, self.conv, d,
                           act=Act.SILU, batch=utterances, x_len=t * d, out_len=t * d)
         k.linear_device(self.conv[:t], t, m["pw2"], x, acc)

@@ -638,7 +638,8 @@ constexpr int QOUT_SPIN_LIMIT = 1 << 21;
 //  1. y = epi(sum) of each output, staged in LDS (zero past M or N), and each row's largest |y| bits
 //     over the wavefront's columns (16-lane reductions), then over the workgroup's (LDS);
 //  2. one fetch_max per row into sync.amax; the returned value is consumed before the barrier, so
-//     every row's max has reached the coherence point before thread 0 arrives;
+//     every row's max has been performed before thread 0 arrives (all atomics here are relaxed, at
+//     agent scope: no cache maintenance in the wait);
 //  3. thread 0 adds one to the tile row's arrival count and polls it until all gridDim.x column
 //     tiles have arrived. Tile rows are dispatched whole and in order (a row-major grid), so the
 //     tiles a workgroup waits for are running or done: the lowest tile row not done has every
@@ -709,9 +710,13 @@ __device__ __forceinline__ void qout_epilogue(float *staged, const v4i (&acc_hi)
     __syncthreads();
     if (tid == 0) {
         const int ncols = (int)gridDim.x;
-        __hip_atomic_fetch_add(&q.sync.arrive[by], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        // Relaxed atomics throughout: every value read across workgroups (amax, the counts) is itself
+        // an agent-scope atomic, and this workgroup's maxima are complete before the barrier above.
+        // Acquire or release orderings would add an L2 invalidation per poll and a write-back of the
+        // L2 per arrival, under every other workgroup on the XCD.
+        __hip_atomic_fetch_add(&q.sync.arrive[by], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int polls = 0;
-        while (__hip_atomic_load(&q.sync.arrive[by], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < ncols) {
+        while (__hip_atomic_load(&q.sync.arrive[by], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ncols) {
             __builtin_amdgcn_s_sleep(8);
             if (++polls == QOUT_SPIN_LIMIT) {
                 __hip_atomic_store(q.sync.timeout, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -732,7 +737,8 @@ __device__ __forceinline__ void qout_epilogue(float *staged, const v4i (&acc_hi)
     }
     __syncthreads();
     if (tid == 0) {
-        const int gone = __hip_atomic_fetch_add(&q.sync.depart[by], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        // the rows' maxima were read (atomically) and consumed before the barrier above
+        const int gone = __hip_atomic_fetch_add(&q.sync.depart[by], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last_s = gone == (int)gridDim.x - 1;
     }
     __syncthreads();

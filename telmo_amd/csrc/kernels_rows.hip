@@ -321,9 +321,14 @@ __global__ __launch_bounds__(256) void layer_norm_lds_kernel(const float *x, siz
     }
 }
 
+bool layer_norm4_fits(size_t n);
+hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+                              float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps, hipStream_t s);
+
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
+    if (layer_norm4_fits(n)) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
     if (n <= (size_t)LN_LDS_MAX) {
         // Up to sixteen rows and 64 KB of LDS per block.
         const int R = (int)min((size_t)16, (size_t)16384 / (n + LN_PAD));
@@ -471,10 +476,188 @@ __global__ __launch_bounds__(256) void layer_norm_quant_kernel(const float *x, s
     }
 }
 
+// LayerNorm of rows of n <= 1024 values, four rows per single-wavefront workgroup, with its outputs
+// written as f32 (out) and/or quantised (qa, exps). The arithmetic is layer_norm_kernel's:
+//  pass 1: lane (r = lane / 16, j = lane % 16) loads inputs j, j + 16, ... of row r into registers,
+//          all loads in flight at once, and sums partial j from them in order; the same registers
+//          give the squared deviations; 16-lane folds as the reference's (j + 8, + 4, + 2, + 1);
+//  the rows go to LDS (rows ROW_LDS floats apart, so the 64 lanes' stores hit 64 banks);
+//  pass 2: lane (c = lane / 4, r = lane % 4) takes runs c, c + 16, ... of 16 inputs of row r, the
+//          runs the GEMM's A operand reads (run rho: k-block rho / 4, operand lane group rho % 4),
+//          computes their outputs, writes them to out, and the row's largest magnitude (over the 16
+//          lanes holding row r) gives its exponent; each run's 16 hi and 16 lo digits go out as one
+//          16-byte store each. Rows past m write zero digits; out may be x (a lane reads a run of x
+//          before writing it, and pass 1 of the wavefront precedes every write).
+constexpr int LN4_MAX = 1024, LN4_ROW = LN4_MAX + 16;
+
+__global__ __launch_bounds__(64) void layer_norm4_kernel(const float *x, size_t ldx, size_t m, int n,
+                                                         const float *__restrict__ gamma,
+                                                         const float *__restrict__ beta, float eps, float *out,
+                                                         size_t ldo, uint8_t *__restrict__ qa,
+                                                         int32_t *__restrict__ exps, int kb, int vec) {
+    __shared__ __attribute__((aligned(16))) float rows_s[4 * LN4_ROW];
+    __shared__ float stat[4][2];
+    const int lane = threadIdx.x;
+    const size_t row0 = (size_t)blockIdx.x * 4;
+    {
+        const int r = lane >> 4, j = lane & 15;
+        const size_t row = row0 + r;
+        const bool valid = row < m;
+        const float *xr = x + (valid ? row : 0) * ldx;
+        // Every lane loads 64 values from valid addresses (indices past n read element 0, rows past
+        // m read row 0), so the loads are one straight run in flight together; the sums below take
+        // only the indices below n.
+        float v[LN4_MAX / 16];
+#pragma unroll
+        for (int i = 0; i < LN4_MAX / 16; i++) v[i] = xr[j + 16 * i < n ? j + 16 * i : 0];
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < LN4_MAX / 16; i++)
+            if (j + 16 * i < n) s = s + v[i];
+        s = s + __shfl_xor(s, 8, 16);
+        s = s + __shfl_xor(s, 4, 16);
+        s = s + __shfl_xor(s, 2, 16);
+        s = s + __shfl_xor(s, 1, 16);
+        const float mean = s / (float)n;
+        float q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < LN4_MAX / 16; i++)
+            if (j + 16 * i < n) {
+                const float d = v[i] - mean;
+                q = __builtin_fmaf(d, d, q);
+            }
+        q = q + __shfl_xor(q, 8, 16);
+        q = q + __shfl_xor(q, 4, 16);
+        q = q + __shfl_xor(q, 2, 16);
+        q = q + __shfl_xor(q, 1, 16);
+        if (j == 0) {
+            stat[r][0] = mean;
+            stat[r][1] = 1.0f / __builtin_sqrtf(q / (float)n + eps);
+        }
+#pragma unroll
+        for (int i = 0; i < LN4_MAX / 16; i++) rows_s[r * LN4_ROW + j + 16 * i] = v[i];
+    }
+    __syncthreads();
+    if (!qa) {
+        // f32 outputs only: lane (r = lane / 16, j = lane % 16) writes the float4s j, j + 16, ... of
+        // row r, so a row's 16 lanes store 256 contiguous bytes per instruction.
+        const int r = lane >> 4, j = lane & 15;
+        const size_t row = row0 + r;
+        if (row >= m) return;
+        const float mean = stat[r][0], rstd = stat[r][1];
+        const float *src = rows_s + r * LN4_ROW;
+        float *orow = out + row * ldo;
+        const bool v4 = vec && n % 4 == 0 && ((reinterpret_cast<uintptr_t>(out) | ldo * sizeof(float)) % 16 == 0);
+        if (v4) {
+            for (int i0 = 4 * j; i0 < n; i0 += 64) {
+                const float4 xv = *reinterpret_cast<const float4 *>(src + i0);
+                const float4 g = *reinterpret_cast<const float4 *>(gamma + i0);
+                const float4 b = *reinterpret_cast<const float4 *>(beta + i0);
+                float4 o;
+                o.x = __builtin_fmaf((xv.x - mean) * rstd, g.x, b.x);
+                o.y = __builtin_fmaf((xv.y - mean) * rstd, g.y, b.y);
+                o.z = __builtin_fmaf((xv.z - mean) * rstd, g.z, b.z);
+                o.w = __builtin_fmaf((xv.w - mean) * rstd, g.w, b.w);
+                *reinterpret_cast<float4 *>(orow + i0) = o;
+            }
+        } else {
+            for (int i = j; i < n; i += 16) orow[i] = __builtin_fmaf((src[i] - mean) * rstd, gamma[i], beta[i]);
+        }
+        return;
+    }
+    const int c = lane >> 2, r = lane & 3;
+    const size_t row = row0 + r;
+    const bool valid = row < m;
+    const float mean = stat[r][0], rstd = stat[r][1];
+    const int runs = (n + 15) / 16;  // runs holding inputs; runs up to kb * 4 hold zero digits
+    float y[LN4_MAX / 256][16];
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int u = 0; u < LN4_MAX / 256; u++) {
+        const int rho = c + 16 * u, i0 = 16 * rho;
+#pragma unroll
+        for (int e = 0; e < 16; e++) y[u][e] = 0.0f;
+        if (!valid || rho >= runs) continue;
+        const float *src = rows_s + r * LN4_ROW + i0;
+        if (vec && i0 + 16 <= n) {
+#pragma unroll
+            for (int e = 0; e < 16; e += 4) {
+                const float4 xv = *reinterpret_cast<const float4 *>(src + e);
+                const float4 g = *reinterpret_cast<const float4 *>(gamma + i0 + e);
+                const float4 b = *reinterpret_cast<const float4 *>(beta + i0 + e);
+                y[u][e] = __builtin_fmaf((xv.x - mean) * rstd, g.x, b.x);
+                y[u][e + 1] = __builtin_fmaf((xv.y - mean) * rstd, g.y, b.y);
+                y[u][e + 2] = __builtin_fmaf((xv.z - mean) * rstd, g.z, b.z);
+                y[u][e + 3] = __builtin_fmaf((xv.w - mean) * rstd, g.w, b.w);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                if (i0 + e < n) y[u][e] = __builtin_fmaf((src[e] - mean) * rstd, gamma[i0 + e], beta[i0 + e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            bad |= !__builtin_isfinite(y[u][e]);
+            amax = fmaxf(amax, fabsf(y[u][e]));
+        }
+        if (out) {
+            float *orow = out + row * ldo + i0;
+            if (vec && i0 + 16 <= n && ((reinterpret_cast<uintptr_t>(out) | ldo * sizeof(float)) % 16 == 0)) {
+#pragma unroll
+                for (int e = 0; e < 16; e += 4)
+                    *reinterpret_cast<float4 *>(orow + e) = make_float4(y[u][e], y[u][e + 1], y[u][e + 2], y[u][e + 3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (i0 + e < n) orow[e] = y[u][e];
+            }
+        }
+    }
+    // Row r's lanes are those with lane % 4 == r.
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        bad |= __shfl_xor(bad, off, 64);
+    }
+    const int32_t e = bad ? EXP_NONFINITE : row_exponent_of(amax);
+    if (valid && c == 0) exps[row] = e;
+    const size_t R = row / 16;
+#pragma unroll
+    for (int u = 0; u < LN4_MAX / 256; u++) {
+        const int rho = c + 16 * u;
+        if (rho >= kb * 4) continue;
+        uint4 hi = make_uint4(0, 0, 0, 0), lo = make_uint4(0, 0, 0, 0);
+        if (valid) {
+            digits4(y[u][0], y[u][1], y[u][2], y[u][3], e, hi.x, lo.x);
+            digits4(y[u][4], y[u][5], y[u][6], y[u][7], e, hi.y, lo.y);
+            digits4(y[u][8], y[u][9], y[u][10], y[u][11], e, hi.z, lo.z);
+            digits4(y[u][12], y[u][13], y[u][14], y[u][15], e, hi.w, lo.w);
+        }
+        uint8_t *blk = qa + ((R * kb + (rho >> 2)) * 2) * 1024 + (16 * (rho & 3) + row % 16) * 16;
+        *reinterpret_cast<uint4 *>(blk) = hi;
+        *reinterpret_cast<uint4 *>(blk + 1024) = lo;
+    }
+}
+
+bool layer_norm4_fits(size_t n) { return n > 0 && n <= (size_t)LN4_MAX; }
+
+hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+                              float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps, hipStream_t s) {
+    const size_t kb = div_ceil(n, KBLK);
+    const int vec = ((reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 == 0);
+    // Workgroups of four rows; a row block of 16 rows whose rows past m still get their zero digits.
+    const size_t groups = qa ? div_ceil(m, (size_t)16) * 4 : div_ceil(m, (size_t)4);
+    hipLaunchKernelGGL(layer_norm4_kernel, dim3((unsigned)groups), dim3(64), 0, s, x, ldx, m, (int)n, gamma, beta, eps,
+                       out, ldo, qa, exps, (int)kb, vec);
+    return hipGetLastError();
+}
+
 hipError_t launch_layer_norm_quant(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                    const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
                                    hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
+    if (layer_norm4_fits(n)) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
     const size_t kb = div_ceil(n, KBLK);
     const int vec = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
                       reinterpret_cast<uintptr_t>(beta)) % 16 == 0);

@@ -5,30 +5,8 @@ convolution + SiLU per utterance, in the reference's order, with the V third of 
 the attention core as the device layer's default does."""
 import numpy as np
 
-import bench
-
 NONE, SILU = 0, 2
 INT8 = 3
-
-
-def synth_layer(d, ff, conv_kernel, seed):
-    """A layer's weights from telmo's generator: int8 matrices with scales, LayerNorms near (1, 0),
-    depthwise taps and bias. Returns {name: (values, scales, n, k)}, {norm: (gamma, beta)}, dw_w,
-    dw_b, all numpy."""
-    shapes = {"ff1_in": (ff, d), "ff1_out": (d, ff), "qkv": (3 * d, d), "out": (d, d), "pw1": (2 * d, d),
-              "pw2": (d, d), "ff2_in": (ff, d), "ff2_out": (d, ff)}
-    mats = {}
-    for i, (name, (n, k)) in enumerate(shapes.items()):
-        values, scales = bench.panel_layout(bench.synth_int8(n, k, seed + 10 * i), bench.synth_scales(n, seed + 10 * i + 1))
-        mats[name] = (values, scales, n, k)
-    norms = {}
-    for i, name in enumerate(("norm_ff1", "norm_att", "norm_conv", "norm_ff2", "norm_out")):
-        g = (1.0 + 0.1 * bench.synth_normal((d,), seed + 200 + 2 * i)).astype(np.float32)
-        b = (0.1 * bench.synth_normal((d,), seed + 201 + 2 * i)).astype(np.float32)
-        norms[name] = (g, b)
-    dw_w = (0.3 * bench.synth_normal((conv_kernel, d), seed + 300)).astype(np.float32)
-    dw_b = (0.1 * bench.synth_normal((d,), seed + 301)).astype(np.float32)
-    return mats, norms, dw_w, dw_b
 
 
 def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True):

@@ -35,13 +35,13 @@ def device_layer(tk, mats, norms, dw_w, dw_b):
     return LayerWeights(W, {name: (dev(g), dev(b)) for name, (g, b) in norms.items()}, dev(dw_w), dev(dw_b))
 
 
-def run_device(tk, layers, x, utterances):
+def run_device(tk, layers, x, utterances, quantised_hidden=False):
     import torch
 
     from telmo_amd.conformer import ConformerLayer
 
     t = x.shape[0]
-    layer = ConformerLayer(tk, D, FF, K, t)
+    layer = ConformerLayer(tk, D, FF, K, t, quantised_hidden=quantised_hidden)
     xd = torch.from_numpy(x.copy()).cuda()
     for w in layers:
         layer.forward(xd, t, w, utterances=utterances)
@@ -55,12 +55,13 @@ def close(layers):
             m.close()
 
 
-def test_layer_at_750_frames(tk, orc):
-    mats, norms, dw_w, dw_b = layer_oracle.synth_layer(D, FF, K, 100)
+@pytest.mark.parametrize("quantised_hidden", [False, True])
+def test_layer_at_750_frames(tk, orc, quantised_hidden):
+    mats, norms, dw_w, dw_b = bench.layer_params(100)
     x = bench.synth_normal((750, D), 7)
-    say("layer", 750)
+    say("layer", 750, quantised_hidden)
     w = device_layer(tk, mats, norms, dw_w, dw_b)
-    got = run_device(tk, [w], x, 1)
+    got = run_device(tk, [w], x, 1, quantised_hidden)
     close([w])
     want = layer_oracle.oracle_layer(orc, x, mats, norms, dw_w, dw_b, fast=True)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -71,8 +72,8 @@ def test_layer_at_750_frames(tk, orc):
 
 
 def test_two_stacked_layers(tk, orc):
-    p1 = layer_oracle.synth_layer(D, FF, K, 400)
-    p2 = layer_oracle.synth_layer(D, FF, K, 700)
+    p1 = bench.layer_params(400)
+    p2 = bench.layer_params(700)
     x = bench.synth_normal((750, D), 8)
     say("two layers", 750)
     ws = [device_layer(tk, *p1), device_layer(tk, *p2)]
@@ -88,12 +89,12 @@ def test_two_stacked_layers(tk, orc):
 
 def test_batch_of_32_utterances(tk, orc):
     """M = 12000 rows: 32 utterances of 375 frames, each convolved on its own."""
-    mats, norms, dw_w, dw_b = layer_oracle.synth_layer(D, FF, K, 1000)
+    mats, norms, dw_w, dw_b = bench.layer_params(1000)
     frames, utt = 375, 32
     x = bench.synth_normal((frames * utt, D), 9)
     say("layer batch", frames * utt)
     w = device_layer(tk, mats, norms, dw_w, dw_b)
-    got = run_device(tk, [w], x, utt)
+    got = run_device(tk, [w], x, utt, quantised_hidden=True)
     close([w])
     for u in (0, 1, utt - 1):
         rows = slice(u * frames, (u + 1) * frames)
