@@ -137,6 +137,17 @@ int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size
 int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *c,
                      size_t c_len, const tg_epilogue *epi);
 
+/* tg_matmul_device without any allocation: no counterpart in the reference; for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The same checks, kernels and bits as tg_matmul_device; the quantised rows of a product that
+ * takes the GEMM go to a scratch array of the library's (16 MiB per GPU, held until the process
+ * ends) instead of the context's grown workspace. Products whose quantised rows exceed it
+ * (tg_quant_bytes(m, k) > 16 MiB - 64 KiB, or m > 16384) give TG_ERR_UNSUPPORTED. Every call on a
+ * GPU shares that GPU's scratch, so calls that overlap on one GPU (other contexts or streams)
+ * race: serialise them. Device pointers, queued on the stream. */
+int tg_matmul_device_noalloc(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w,
+                             float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
+
 /* c = epi(a . b) with b a row-major [k, ldb] f32 matrix whose first n columns are used: the
  * reference's BView::row_major right-hand side (src/kernels/mod.rs:320-339, the attention path's
  * f32 activations) through Kernels::matmul (657-688) / matmul_serial (732-765). The sums are the

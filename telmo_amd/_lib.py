@@ -45,6 +45,7 @@ SIGNATURES = {
     "tg_linear": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p]),
     "tg_matmul_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, _sz, _sz, _p]),
     "tg_linear_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p]),
+    "tg_matmul_device_noalloc": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _p, _sz, _sz, _p]),
     "tg_matmul_rowmajor_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _p, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p]),
     "tg_quant_bytes": (_sz, [_sz, _sz]),
     "tg_quantize_rows_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p]),

@@ -76,6 +76,41 @@ struct tg_tdt {
 
 constexpr int TDT_GRAPH_STEPS = 16;
 
+// The scratch of tg_matmul_device_noalloc, for callers that cannot allocate: the quantised rows of
+// one product (the first NOALLOC_QA_BYTES) and their row exponents (NOALLOC_ROWS int32 after them).
+// Each GPU the library runs on holds its own copy for the life of the process. Host code never uses
+// the array's name as an address: tg_ctx_create takes each device's address with
+// hipGetSymbolAddress, with that device current, and the kernels get that pointer.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+constexpr size_t NOALLOC_ROWS = 16384;
+constexpr size_t NOALLOC_QA_BYTES = NOALLOC_SCRATCH_BYTES - NOALLOC_ROWS * sizeof(int32_t);
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void *scratch_ptr[MAX_DEVICES] = {};  // device address of `scratch` per device, once taken
+hipError_t scratch_err[MAX_DEVICES] = {};
+
+// Takes the address of `scratch` on `device` (the current device) the first time; later calls
+// return it. hipSuccess with *out null never happens: a failure is returned and kept.
+hipError_t scratch_address(int device, void **out) {
+    *out = nullptr;
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(scratch_mu);
+    if (!scratch_ptr[device] && scratch_err[device] == hipSuccess) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) scratch_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+        else scratch_ptr[device] = p;
+    }
+    *out = scratch_ptr[device];
+    return scratch_err[device];
+}
+
+}  // namespace
+
 namespace {
 
 int fail(tg_ctx *ctx, int code, const std::string &msg) {
@@ -279,6 +314,10 @@ int tg_ctx_create(int device, void *stream, tg_ctx **out) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return TG_ERR_HIP;
     if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0) return TG_ERR_UNSUPPORTED;
+    // Set-up of the no-allocation scratch on this device, with the device current. A failure is
+    // kept and reported by tg_matmul_device_noalloc; nothing else needs the scratch.
+    void *scratch_dev = nullptr;
+    (void)scratch_address(device, &scratch_dev);
     tg_ctx *ctx = new tg_ctx();
     ctx->device = device;
     if (stream) {
@@ -384,6 +423,45 @@ int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size
     rc = run_device(ctx, a, lda, m, w, c, ldc, epi_args(epi, nullptr, false));
     if (rc == TG_OK) clear_error(ctx);
     return rc;
+}
+
+int tg_matmul_device_noalloc(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w,
+                             float *c, size_t c_len, size_t ldc, const tg_epilogue *epi) {
+    if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
+    if (m == 0 || w->d.n == 0) return TG_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int rc = check_matmul(ctx, a, a_len, lda, m, w, c, c_len, ldc, epi);
+    if (rc) return rc;
+    if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
+    const tg::DeviceWeights &d = w->d;
+    const bool int_path = ctx->mode == TG_MODE_FAST && (d.precision == TG_INT8 || d.precision == TG_Q8_0) &&
+                          d.k <= tg::MAX_K_INT;
+    const bool staged = int_path && !tg::gemv_fits(m, d.k, a, lda, d.precision);
+    if (staged && (m > NOALLOC_ROWS || tg::qa_bytes(m, d.k) > NOALLOC_QA_BYTES))
+        return fail(ctx, TG_ERR_UNSUPPORTED,
+                    "the product's quantised rows (" + std::to_string(tg::qa_bytes(m, d.k)) + " bytes, " +
+                        std::to_string(m) + " rows) exceed the no-allocation scratch (" +
+                        std::to_string(NOALLOC_QA_BYTES) + " bytes, " + std::to_string(NOALLOC_ROWS) + " rows)");
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    const tg::EpiArgs e = epi_args(epi, nullptr, false);
+    if (!int_path) {
+        TG_HIP(ctx, tg::launch_exact(a, lda, m, d, c, ldc, e, ctx->stream));
+    } else if (!staged) {
+        TG_HIP(ctx, tg::launch_gemv_i8(a, lda, m, d, c, ldc, e, ctx->stream));
+    } else {
+        void *base = nullptr;
+        const hipError_t se = scratch_address(ctx->device, &base);
+        if (se != hipSuccess) return hip_fail(ctx, se, "hipGetSymbolAddress of the no-allocation scratch");
+        // Every byte the GEMM reads into a stored output is written by the quantiser first (rows
+        // past m in the last 16-row block feed only outputs that are never stored), so nothing in
+        // the scratch needs clearing between calls.
+        uint8_t *qa = static_cast<uint8_t *>(base);
+        int32_t *exps = reinterpret_cast<int32_t *>(qa + NOALLOC_QA_BYTES);
+        TG_HIP(ctx, tg::launch_quantize_rows(a, lda, m, d.k, qa, exps, ctx->stream));
+        TG_HIP(ctx, tg::launch_gemm_i8(qa, exps, m, d, c, ldc, e, ctx->stream));
+    }
+    clear_error(ctx);
+    return TG_OK;
 }
 
 int tg_matmul_rowmajor_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const float *b,

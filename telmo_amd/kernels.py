@@ -305,6 +305,16 @@ class Kernels:
                                          _dev(c, "float32", "c"), _len(c, c_len, "c"), ldc, self._epi_dev(epi))
         _check(rc, self._ctx)
 
+    def matmul_device_noalloc(self, a, lda: int, m: int, w: PackedWeights, c, ldc: int,
+                              epi: Epilogue = Epilogue.PLAIN, a_len: Optional[int] = None,
+                              c_len: Optional[int] = None):
+        """matmul_device with no allocation: the quantised rows go to the library's per-GPU scratch
+        (16 MiB). Calls that overlap on one GPU race."""
+        rc = _lib.lib().tg_matmul_device_noalloc(self._ctx, _dev(a, "float32", "a"), _len(a, a_len, "a"), lda, m,
+                                                 w._handle, _dev(c, "float32", "c"), _len(c, c_len, "c"), ldc,
+                                                 self._epi_dev(epi))
+        _check(rc, self._ctx)
+
     def linear_device(self, a, m: int, w: PackedWeights, c, epi: Epilogue = Epilogue.PLAIN):
         self.matmul_device(a, w.k(), m, w, c, w.n(), epi)
 
