@@ -28,6 +28,19 @@ namespace {
 
 constexpr int THREADS = 256;
 
+// Whether every hi sum of the wavefront's RB x CB accumulators takes dequant_i32 (one vote).
+template <int RB, int CB>
+__device__ __forceinline__ bool wave_fits_i32(const v4i (&acc_hi)[RB][CB]) {
+    bool ok = true;
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) ok &= dequant_fits(acc_hi[r][cb][v]);
+    return __all(ok);
+}
+
 // The store of a wavefront's WM x WN tile of sums through the epilogue into c[m0.., n0..]. Lane l
 // owns the runs of four outputs at column 4 (l % (WN / 4)) of rows l / (WN / 4), + 64 / (WN / 4),
 // ...: per run one 16-byte load of the old outputs (when accumulating), one 16-byte LDS read of the
@@ -177,6 +190,34 @@ __device__ __forceinline__ void tile_of(int &bx, int &by) {
     }
 }
 
+// The wavefront's f32 sums staged in LDS (element v of lane l: row 4 (l / 16) + v, column l % 16 of
+// each 16 x 16 block, rows C_STRIDE floats apart), through dequant_i32 when the whole wavefront's
+// sums fit it, else dequant: the same values either way.
+template <int RB, int CB, int C_STRIDE>
+__device__ __forceinline__ void stage_sums(float *tile, const v4i (&acc_hi)[RB][CB], const v4i (&acc_lo)[RB][CB],
+                                           const int32_t (&e_row)[RB][4], const float (&s_col)[CB], int out_row,
+                                           int out_col) {
+    if (wave_fits_i32<RB, CB>(acc_hi)) {
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                        dequant_i32(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
+    } else {
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                        dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
+    }
+}
+
 template <int RB, int CB, int S, int OCC, int XCD, int G>
 __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__restrict__ qf,
                                                                const int32_t *__restrict__ exps, int M,
@@ -269,14 +310,7 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
     TileStore<WM, WN, C_STRIDE> out;
     out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     float *tile = staged[wave];
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-            for (int v = 0; v < 4; v++)
-                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
-                    dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
+    stage_sums<RB, CB, C_STRIDE>(tile, acc_hi, acc_lo, e_row, s_col, out_row, out_col);
     __syncthreads();
     out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
 }
@@ -422,12 +456,16 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *_
     // Epilogue: the strip (element v of lane l: row 4 (l / 16) + v, column l % 16 of each 16 x 16
     // block) is staged in the wavefront's own LDS area and stored in 16-byte runs.
     float *tile = reinterpret_cast<float *>(smem + PARTS + q * STAGE);
+    {
+        v4i hi1[1][CB], lo1[1][CB];
+        int32_t e1[1][4] = {{e_row[0], e_row[1], e_row[2], e_row[3]}};
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-            tile[(out_row + v) * C_STRIDE + cb * 16 + out_col] =
-                dequant(mine_hi[cb][v], mine_lo[cb][v], e_row[v], s_col[cb]);
+        for (int cb = 0; cb < CB; cb++) {
+            hi1[0][cb] = mine_hi[cb];
+            lo1[0][cb] = mine_lo[cb];
+        }
+        stage_sums<1, CB, C_STRIDE>(tile, hi1, lo1, e1, s_col, out_row, out_col);
+    }
     __syncthreads();
     out.finish(tile, c, ldc, m0 + q * 16, M, N, bias != nullptr, act, escale, accumulate);
 }
@@ -897,14 +935,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
 
     float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-            for (int v = 0; v < 4; v++)
-                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
-                    dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
+    stage_sums<RB, CB, C_STRIDE>(tile, acc_hi, acc_lo, e_row, s_col, out_row, out_col);
     __syncthreads();
     if constexpr (GLU) {
         // Wavefronts (wm, 0) and (wm, 1) hold the a and b halves of the same rows and columns; each

@@ -113,6 +113,17 @@ __device__ __forceinline__ float dequant(int32_t acc_hi, int32_t acc_lo, int32_t
     return __builtin_ldexpf(u, -e);
 }
 
+// dequant for sums with |acc_hi| < 2^22 (dequant_fits): S = 256 hi + lo then fits an int32 (|lo| <
+// 2^30 for k <= 65536), and its conversion to f32 is the same single rounding, with no f64
+// arithmetic. GEMM epilogues take this path when every sum of the wavefront fits (a wave-uniform
+// vote), which is all but certain for the sizes here: |hi| <= 127 * 127 * k.
+__device__ __forceinline__ bool dequant_fits(int32_t acc_hi) { return (uint32_t)(acc_hi + (1 << 22)) < (1u << 23); }
+__device__ __forceinline__ float dequant_i32(int32_t acc_hi, int32_t acc_lo, int32_t e, float scale) {
+    if (e == EXP_NONFINITE) return __builtin_nanf("");
+    const float u = (float)(acc_hi * 256 + acc_lo) * scale + 0.0f;
+    return __builtin_ldexpf(u, -e);
+}
+
 // The row exponent e: the largest with max|a| * 2^e <= DIGIT_MAX, from the bits of amax
 // (positive, finite) so that subnormals are handled exactly.
 __device__ __forceinline__ int32_t row_exponent_of(float amax) {
