@@ -245,6 +245,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, size_t 
 // are summed from LDS in the order above, and the outputs go out in 16-byte runs when out's rows
 // are aligned. Every input of the block is read before any output is written, so out may be x.
 constexpr int LN_PAD = 16, LN_LDS_MAX = 16384 - LN_PAD;  // one padded row fits 64 KB
+constexpr int LN4_MAX = 1024, LN4_ROW = LN4_MAX + 16;  // layer_norm4_kernel's rows
 
 __global__ __launch_bounds__(256) void layer_norm_lds_kernel(const float *x, size_t ldx, size_t m, int n, int R,
                                                              const float *__restrict__ gamma,
@@ -321,14 +322,20 @@ __global__ __launch_bounds__(256) void layer_norm_lds_kernel(const float *x, siz
     }
 }
 
-bool layer_norm4_fits(size_t n);
+bool layer_norm_quad_fits(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+                          const float *out, size_t ldo);
 hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                               float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps, hipStream_t s);
+hipError_t launch_layer_norm_quad(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                                  const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
+                                  hipStream_t s);
 
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
-    if (layer_norm4_fits(n)) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
+    if (layer_norm_quad_fits(x, ldx, m, n, gamma, beta, out, ldo))
+        return launch_layer_norm_quad(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
+    if (n <= (size_t)LN4_MAX) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
     if (n <= (size_t)LN_LDS_MAX) {
         // Up to sixteen rows and 64 KB of LDS per block.
         const int R = (int)min((size_t)16, (size_t)16384 / (n + LN_PAD));
@@ -488,8 +495,6 @@ __global__ __launch_bounds__(256) void layer_norm_quant_kernel(const float *x, s
 //          lanes holding row r) gives its exponent; each run's 16 hi and 16 lo digits go out as one
 //          16-byte store each. Rows past m write zero digits; out may be x (a lane reads a run of x
 //          before writing it, and pass 1 of the wavefront precedes every write).
-constexpr int LN4_MAX = 1024, LN4_ROW = LN4_MAX + 16;
-
 __global__ __launch_bounds__(64) void layer_norm4_kernel(const float *x, size_t ldx, size_t m, int n,
                                                          const float *__restrict__ gamma,
                                                          const float *__restrict__ beta, float eps, float *out,
@@ -640,12 +645,11 @@ __global__ __launch_bounds__(64) void layer_norm4_kernel(const float *x, size_t 
     }
 }
 
-bool layer_norm4_fits(size_t n) { return n > 0 && n <= (size_t)LN4_MAX; }
-
 hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                               float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps, hipStream_t s) {
     const size_t kb = div_ceil(n, KBLK);
-    const int vec = ((reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta)) % 16 == 0);
+    const int vec = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
+                      reinterpret_cast<uintptr_t>(beta)) % 16 == 0);
     // Workgroups of four rows; a row block of 16 rows whose rows past m still get their zero digits.
     const size_t groups = qa ? div_ceil(m, (size_t)16) * 4 : div_ceil(m, (size_t)4);
     hipLaunchKernelGGL(layer_norm4_kernel, dim3((unsigned)groups), dim3(64), 0, s, x, ldx, m, (int)n, gamma, beta, eps,
@@ -653,11 +657,171 @@ hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, co
     return hipGetLastError();
 }
 
+// LayerNorm of rows of n <= 1024 values (n % 4 == 0, rows and gamma, beta 16-byte aligned), four
+// rows per workgroup of four wavefronts, with its outputs written as f32 (out) and/or quantised
+// (qa, exps): layer_norm4_kernel's work spread over four times the wavefronts, for batches too
+// small to fill the chip with it. The arithmetic is layer_norm_kernel's, in three phases:
+//  1. wavefront w loads row w of the four: lane l takes inputs 4 (l + 64 i) + [0, 4) with 16-byte
+//     loads (one 1 KB run per instruction), keeps them in registers and copies them to LDS, zeros
+//     past n (rows LNQ_ROW floats apart, so that each half-wavefront's reads below hit 32 banks);
+//  2. wavefront 0 sums the partials of all four rows: lane (r = l / 16, p = l % 16) adds inputs
+//     p, p + 16, ... of row r in order (the zeros past n leave a sum unchanged, as it starts at +0
+//     and cannot become -0), and the squared deviations the same, a masked deviation of 0 past n;
+//     folds as the reference's (p + 8, + 4, + 2, + 1); mean and rstd go to LDS;
+//  3. wavefront w computes row w's outputs from its registers: out gets them as 16-byte stores; the
+//     row's largest magnitude gives its exponent, and a lane's four inputs are four consecutive
+//     bytes of one 16-byte run of the quantised layout (k-block t = 4 i + l / 16, operand lane
+//     16 ((l / 4) % 4) + row % 16, bytes 4 (l % 4) + [0, 4)), one 4-byte store per digit.
+// The chains of phase 2 are the only serial work: one instruction advances four rows. Rows past m
+// (up to the end of the last 16-row block) write zero digits. out may be x: a lane reads its inputs
+// before it writes their outputs, and no lane writes another's inputs.
+constexpr int LNQ_MAX = 1024, LNQ_ROW = LNQ_MAX + 16;
+
+template <bool FULL>  // FULL: n == LNQ_MAX, no masking in the chains
+__global__ __launch_bounds__(256) void layer_norm_quad_kernel(const float *x, size_t ldx, size_t m, int n,
+                                                              const float *__restrict__ gamma,
+                                                              const float *__restrict__ beta, float eps, float *out,
+                                                              size_t ldo, uint8_t *__restrict__ qa,
+                                                              int32_t *__restrict__ exps, int kb, size_t bpx) {
+    __shared__ __attribute__((aligned(16))) float rows_s[4 * LNQ_ROW];
+    __shared__ float stat[4][2];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const size_t xcd = blockIdx.x % 8, i = blockIdx.x / 8;
+    const size_t blk = xcd * bpx + i / 4;  // 16-row block
+    const size_t row0 = blk * 16 + (i % 4) * 4;
+    if (qa ? blk * 16 >= m : row0 >= m) return;  // uniform over the workgroup
+    const size_t row = row0 + w;
+    const bool valid = row < m;  // uniform over the wavefront
+    const float4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4 v[LNQ_MAX / 256];
+    {
+        const float4 *xr = reinterpret_cast<const float4 *>(x + (valid ? row : 0) * ldx);
+#pragma unroll
+        for (int i = 0; i < LNQ_MAX / 256; i++) {
+            const int c4 = lane + 64 * i;
+            v[i] = valid && (FULL || 4 * c4 < n) ? xr[c4] : zero;
+        }
+#pragma unroll
+        for (int i = 0; i < LNQ_MAX / 256; i++) reinterpret_cast<float4 *>(rows_s + w * LNQ_ROW)[lane + 64 * i] = v[i];
+    }
+    __syncthreads();
+    if (w == 0) {
+        const int r = lane >> 4, p = lane & 15;
+        const float *xr = rows_s + r * LNQ_ROW + p;
+        // The chains read LDS in batches of 16 (the scheduling barriers keep the batches apart, so
+        // that few registers are live and the workgroups fit eight wavefronts per SIMD).
+        float s = 0.0f;
+#pragma unroll
+        for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
+#pragma unroll
+            for (int q = q0; q < q0 + 16; q++) s = s + xr[16 * q];
+        }
+        s = s + __shfl_xor(s, 8, 16);
+        s = s + __shfl_xor(s, 4, 16);
+        s = s + __shfl_xor(s, 2, 16);
+        s = s + __shfl_xor(s, 1, 16);
+        const float mean = s / (float)n;
+        float sq = 0.0f;
+#pragma unroll
+        for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
+#pragma unroll
+            for (int q = q0; q < q0 + 16; q++) {
+                const float d = FULL || p + 16 * q < n ? xr[16 * q] - mean : 0.0f;
+                sq = __builtin_fmaf(d, d, sq);
+            }
+        }
+        sq = sq + __shfl_xor(sq, 8, 16);
+        sq = sq + __shfl_xor(sq, 4, 16);
+        sq = sq + __shfl_xor(sq, 2, 16);
+        sq = sq + __shfl_xor(sq, 1, 16);
+        if (p == 0) {
+            stat[r][0] = mean;
+            stat[r][1] = 1.0f / __builtin_sqrtf(sq / (float)n + eps);
+        }
+    }
+    __syncthreads();
+    if (!valid && !qa) return;
+    const float mean = stat[w][0], rstd = stat[w][1];
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < LNQ_MAX / 256; i++) {
+        const int c4 = lane + 64 * i;
+        if (valid && (FULL || 4 * c4 < n)) {
+            const float4 g = reinterpret_cast<const float4 *>(gamma)[c4];
+            const float4 b = reinterpret_cast<const float4 *>(beta)[c4];
+            float4 y;
+            y.x = __builtin_fmaf((v[i].x - mean) * rstd, g.x, b.x);
+            y.y = __builtin_fmaf((v[i].y - mean) * rstd, g.y, b.y);
+            y.z = __builtin_fmaf((v[i].z - mean) * rstd, g.z, b.z);
+            y.w = __builtin_fmaf((v[i].w - mean) * rstd, g.w, b.w);
+            v[i] = y;
+            if (out) reinterpret_cast<float4 *>(out + row * ldo)[c4] = y;
+            bad |= !__builtin_isfinite(y.x) | !__builtin_isfinite(y.y) | !__builtin_isfinite(y.z) |
+                   !__builtin_isfinite(y.w);
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(y.x), fabsf(y.y))), fmaxf(fabsf(y.z), fabsf(y.w)));
+        } else {
+            v[i] = zero;
+        }
+    }
+    if (!qa) return;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off));
+        bad |= __shfl_xor(bad, off);
+    }
+    const int32_t e = !valid ? 0 : (bad ? EXP_NONFINITE : row_exponent_of(amax));
+    if (valid && lane == 0) exps[row] = e;
+    uint8_t *base = qa + (row / 16) * (size_t)kb * 2048 + (16 * ((lane >> 2) & 3) + row % 16) * 16 + 4 * (lane & 3);
+#pragma unroll
+    for (int i = 0; i < LNQ_MAX / 256; i++) {
+        const int t = 4 * i + (lane >> 4);
+        if (t < kb) {
+            uint32_t hi = 0, lo = 0;
+            if (valid) digits4(v[i].x, v[i].y, v[i].z, v[i].w, e, hi, lo);
+            *reinterpret_cast<uint32_t *>(base + (size_t)t * 2048) = hi;
+            *reinterpret_cast<uint32_t *>(base + (size_t)t * 2048 + 1024) = lo;
+        }
+    }
+}
+
+// Whether layer_norm_quad_kernel takes these rows: fewer than LNQ_ROWS_MAX of them (beyond, the
+// single-wavefront layer_norm4_kernel fills the chip and costs fewer instructions per row), n <= 1024
+// and a multiple of 4, x, gamma, beta (and out when given) 16-byte aligned with row strides of
+// whole 16-byte units.
+constexpr size_t LNQ_ROWS_MAX = 2048;
+
+bool layer_norm_quad_fits(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+                          const float *out, size_t ldo) {
+    uintptr_t al = reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
+                   reinterpret_cast<uintptr_t>(beta);
+    if (out) al |= reinterpret_cast<uintptr_t>(out) | ldo * sizeof(float);
+    return m < LNQ_ROWS_MAX && n > 0 && n <= (size_t)LNQ_MAX && n % 4 == 0 && al % 16 == 0;
+}
+
+hipError_t launch_layer_norm_quad(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                                  const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
+                                  hipStream_t s) {
+    const size_t kb = div_ceil(n, KBLK);
+    // Four workgroups per 16-row block, bpx blocks per XCD.
+    const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
+    const unsigned groups = (unsigned)(8 * bpx * 4);
+    if (n == (size_t)LNQ_MAX)
+        hipLaunchKernelGGL(layer_norm_quad_kernel<true>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
+                           eps, out, ldo, qa, exps, (int)kb, bpx);
+    else
+        hipLaunchKernelGGL(layer_norm_quad_kernel<false>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
+                           eps, out, ldo, qa, exps, (int)kb, bpx);
+    return hipGetLastError();
+}
+
 hipError_t launch_layer_norm_quant(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                    const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
                                    hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
-    if (layer_norm4_fits(n)) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
+    if (layer_norm_quad_fits(x, ldx, m, n, gamma, beta, out, ldo))
+        return launch_layer_norm_quad(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
+    if (n <= (size_t)LN4_MAX) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
     const size_t kb = div_ceil(n, KBLK);
     const int vec = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
                       reinterpret_cast<uintptr_t>(beta)) % 16 == 0);

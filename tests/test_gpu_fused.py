@@ -40,7 +40,8 @@ def quantised(tk, x, ldx, m, k):
 
 
 LN_CASES = [(750, 1024, 1024), (12000, 1024, 1024), (37, 1000, 1003), (5, 64, 64), (19, 100, 103), (3, 4096, 4096),
-            (16, 17, 17), (33, 2048, 2048), (1, 1, 4)]
+            (16, 17, 17), (33, 2048, 2048), (1, 1, 4), (21, 100, 104), (40, 1020, 1020),
+            (2100, 1000, 1000)]
 
 
 @pytest.mark.parametrize("m,n,ldx", LN_CASES)

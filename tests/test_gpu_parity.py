@@ -319,9 +319,11 @@ def test_layer_norm_matches_the_reference_order(tk, orc):
     import torch
 
     rng = np.random.default_rng(17)
-    # 16-byte and unaligned rows, 1 to 16 rows per block, and rows past the LDS-staged kernel
+    # 16-byte and unaligned rows, 1 to 16 rows per block, rows past the LDS-staged kernel, and batches
+    # on both sides of the four-wavefront kernel's row limit
     for m, n, ldx in ((37, 1024, 1024), (5, 1000, 1003), (19, 17, 17), (3, 1, 4), (40, 4096, 4100),
-                      (33, 2048, 2048), (2, 16368, 16368), (3, 16369, 16369)):
+                      (33, 2048, 2048), (2, 16368, 16368), (3, 16369, 16369), (21, 100, 104), (6, 1020, 1024),
+                      (2050, 1024, 1024)):
         x = (2.0 + 3.0 * rng.standard_normal((m, ldx))).astype(np.float32)
         gamma = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
         beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
