@@ -388,11 +388,16 @@ def q8_leg(args):
     return out
 
 
+def gemv_kernel(m):
+    """The GEMV body the library runs for m aligned rows of int8 products."""
+    return "gemv_dot4" if m == 1 else "gemv_mfma"
+
+
 def gemv_leg(args):
-    """The TDT decode-step GEMVs (m = 1, 4, 8 streams) on the HBM roofline, for both decode kernels: the
-    MFMA GEMV (rows 16-byte aligned, the library's choice for them) and the dot4 GEMV with no MFMA
-    (the north star's sketch; the library takes it for rows that are not 16-byte aligned, so the
-    same call on rows starting one float in times it).
+    """The TDT decode-step GEMVs (m = 1, 4, 8 streams) on the HBM roofline, for the library's choice on
+    16-byte aligned rows ("gemv": the dot4 body with no MFMA for one row, the MFMA body for batches of
+    streams) and for the row-at-a-time dot4 kernel the library takes for rows that are not 16-byte
+    aligned ("dot4_rows": the same call on rows starting one float in).
 
     (i) each shape with its weights evicted: one pass over copies totalling more than 600 MB (twice
         the 256 MB Infinity Cache and more) is captured as a HIP graph and replayed, so every call
@@ -438,7 +443,7 @@ def gemv_leg(args):
         bias = torch.from_numpy(synth_normal((n,), 7200 + si)).cuda() if with_bias else None
         epi = Epilogue(bias=bias)
         for m in (1, 4, 8):
-            for kernel, aligned in (("mfma", True), ("dot4", False)):
+            for kernel, aligned in ((gemv_kernel(m), True), ("dot4_rows", False)):
                 a = rows(m, k, 7300 + m, aligned)
                 c = torch.empty(m, n, device="cuda")
                 alen = (m - 1) * k + k
@@ -457,7 +462,7 @@ def gemv_leg(args):
         w = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
         del values
         for m in (1, 4, 8):
-            for kernel, aligned in (("mfma", True), ("dot4", False)):
+            for kernel, aligned in ((gemv_kernel(m), True), ("dot4_rows", False)):
                 a = rows(m, k, 7600 + m, aligned)
                 c = torch.empty(m, n, device="cuda")
                 call = lambda i: kern.matmul_device(a, k, m, w, c, n, a_len=m * k)  # noqa: E731

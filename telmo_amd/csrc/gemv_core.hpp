@@ -1,8 +1,11 @@
-// The MFMA GEMV of the decode steps (m <= 16 rows, k <= 1984) as a device-function template over
-// where its input rows come from and where its outputs go, so the plain GEMV and the fused TDT step
-// share one body. The rows are read once into registers ahead of the weights, split into two int8
-// digits in LDS as 16 x 64 MFMA A operands, and every 1 KB weight block costs one 16-byte LDS read
-// per digit and two v_mfma_i32_16x16x64_i8 (Q8_0: four 16x16x32 MFMAs and a per-block f32 fold).
+// The GEMV of the decode steps (m <= 16 rows, k <= 1984) as a device-function template over where
+// its input rows come from and where its outputs go, so the plain GEMV and the fused TDT step share
+// one body. The rows are read once into registers ahead of the weights, split into two int8 digits
+// in LDS as 16 x 64 MFMA A operands, and every 1 KB weight block costs one 16-byte LDS read per digit
+// and two v_mfma_i32_16x16x64_i8 (Q8_0: four 16x16x32 MFMAs and a per-block f32 fold). With DOTR > 0
+// (int8 weights, at most DOTR rows) the block costs each row two 16-byte LDS reads and eight
+// v_dot4_i32_i8 instead, no MFMA, and the four 16-input groups of a column meet across the
+// wavefront after the k-loop; the sums, and so the outputs, are the same integers.
 // Workgroups stay resident and walk the panels, requesting the next panel's weights, scales, bias
 // and old outputs before the current panel's epilogue.
 #pragma once
@@ -122,7 +125,7 @@ __device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, in
 // last wavefront idle); wavefront w holds chunk wavefronts w + WAVES j (j < J) in registers. The
 // rows are read once, before the weights, so the weight loads stay in flight while the rows are
 // digitised.
-template <int WAVES, int KBC, int J, int Q8, class In, class Out>
+template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR = 0>
 __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
                                           const float *__restrict__ scales, int N, int P, int KB, int NB,
                                           const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
@@ -202,9 +205,16 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
     __syncthreads();
 
     const uint8_t *ap = sqa + lane * 16;
+    constexpr bool DOT = DOTR > 0 && !Q8;
+    // DOTR rows: lane (g = l / 16, j = l % 16) reads row r's operand lane 16 g + r (the digits of
+    // the inputs its weights multiply) and sums with v_dot4_i32_i8.
+    const uint8_t *dp = sqa + (lane >> 4) * 256;
     for (; p < P; p += step) {
         v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
         v4f accq = {0.0f, 0.0f, 0.0f, 0.0f};
+        int dh[DOTR > 0 ? DOTR : 1], dl[DOTR > 0 ? DOTR : 1];
+#pragma unroll
+        for (int r = 0; r < (DOTR > 0 ? DOTR : 1); r++) dh[r] = dl[r] = 0;
         const uint8_t *wp = wv + (size_t)p * panel_stride;
         for (int c0 = 0; c0 < KB; c0 += KBC) {
             if constexpr (Q8) {
@@ -236,12 +246,48 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
 #pragma unroll
                 for (int t = 0; t < KBC; t++) {
                     if (c0 + t < KB) {
-                        const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
-                        const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
-                        acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
-                        acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
+                        if constexpr (DOT) {
+#pragma unroll
+                            for (int r = 0; r < DOTR; r++) {
+                                const v4i ahi = *reinterpret_cast<const v4i *>(dp + (c0 + t) * 2048 + r * 16);
+                                const v4i alo = *reinterpret_cast<const v4i *>(dp + (c0 + t) * 2048 + 1024 + r * 16);
+                                int h = dh[r], l = dl[r];
+                                h = __builtin_amdgcn_sdot4(ahi.x, wr[t].x, h, false);
+                                h = __builtin_amdgcn_sdot4(ahi.y, wr[t].y, h, false);
+                                h = __builtin_amdgcn_sdot4(ahi.z, wr[t].z, h, false);
+                                h = __builtin_amdgcn_sdot4(ahi.w, wr[t].w, h, false);
+                                l = __builtin_amdgcn_sdot4(alo.x, wr[t].x, l, false);
+                                l = __builtin_amdgcn_sdot4(alo.y, wr[t].y, l, false);
+                                l = __builtin_amdgcn_sdot4(alo.z, wr[t].z, l, false);
+                                l = __builtin_amdgcn_sdot4(alo.w, wr[t].w, l, false);
+                                dh[r] = h;
+                                dl[r] = l;
+                            }
+                        } else {
+                            const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
+                            const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
+                            acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
+                            acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
+                        }
                     }
                 }
+            }
+        }
+        if constexpr (DOT) {
+            // The four input groups of a column meet (lanes j, j + 16, j + 32, j + 48); lane
+            // (g, j) then holds rows 4 g .. 4 g + 3 of column j as the MFMA's C operand would.
+#pragma unroll
+            for (int r = 0; r < DOTR; r++) {
+                dh[r] += __shfl_xor(dh[r], 16, 64);
+                dh[r] += __shfl_xor(dh[r], 32, 64);
+                dl[r] += __shfl_xor(dl[r], 16, 64);
+                dl[r] += __shfl_xor(dl[r], 32, 64);
+            }
+            const bool upper = DOTR > 4 && (lane >> 4) == 1;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                acc_hi[v] = upper ? dh[(4 + v) % DOTR] : dh[v % DOTR];
+                acc_lo[v] = upper ? dl[(4 + v) % DOTR] : dl[v % DOTR];
             }
         }
         const float sc0 = sc, bv0 = bv;

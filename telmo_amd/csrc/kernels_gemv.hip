@@ -5,7 +5,8 @@
 // weights in the MFMA layout: per k-block of 64 inputs of a 16-output panel, lane l = 16 g + j
 // loads 16 contiguous bytes (inputs 64 t + 16 g + [0, 16) of output j), 1 KB per wave, coalesced.
 //
-// gemv_mfma_kernel (m <= 16, k <= 1984, 16-byte aligned rows, k % 4 == 0): the digits sit in LDS as 16 x 64 MFMA A operands in lane
+// gemv_mfma_kernel (m <= 16, k <= 1984, 16-byte aligned rows, k % 4 == 0; one int8 row takes its
+// dot4 body, no MFMA): the digits sit in LDS as 16 x 64 MFMA A operands in lane
 // order, so each 1 KB weight block costs one 16-byte LDS read per digit and two
 // v_mfma_i32_16x16x64_i8, whatever m is. The rows are read once into registers ahead of the
 // weights; workgroups stay resident and walk the panels, so the rows are digitised once per
@@ -156,7 +157,7 @@ hipError_t launch_rows(const float *a, size_t lda, const DeviceWeights &w, float
 
 
 // Rows are read from a (row stride lda), outputs written to c: the GEMV of tg_matmul_device.
-template <int WAVES, int KBC, int J, int Q8>
+template <int WAVES, int KBC, int J, int Q8, int DOTR>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__restrict__ a, size_t lda, int m, int k,
                                                                const uint8_t *__restrict__ wv,
                                                                const float *__restrict__ scales, int N, int P, int KB,
@@ -167,9 +168,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];  // KB x (hi, lo) x 1 KB operands
     __shared__ uint32_t slot[WAVES * J];                           // max |x| bits per wavefront of chunks
     gemv::StoreC out{c, ldc};
-    gemv::mfma_body<WAVES, KBC, J, Q8>(gemv::RowsIn{a, lda}, out, m, k, wv, scales, N, P, KB, NB, c, ldc, bias, act,
-                                       escale, accumulate, panel_stride, blk_stride, sqa, slot);
+    gemv::mfma_body<WAVES, KBC, J, Q8, gemv::RowsIn, gemv::StoreC, DOTR>(gemv::RowsIn{a, lda}, out, m, k, wv, scales, N,
+                                                                      P, KB, NB, c, ldc, bias, act, escale, accumulate,
+                                                                      panel_stride, blk_stride, sqa, slot);
 }
+
+// A single decode row (m = 1, int8 weights) takes the dot4 variant of the body: the same row, panels
+// and epilogue, with v_dot4_i32_i8 in place of the MFMA and the four input groups summed across the
+// wavefront. From two rows on, the dot4 form is bound by its LDS operand reads and VALU work (each
+// row adds two 16-byte LDS reads and eight v_dot4 per 1 KB of weights, where one MFMA pair serves
+// up to 16 rows), so batches of streams take the MFMA.
+bool gemv_dot_rows(size_t m) { return m == 1; }
 
 constexpr int MFMA_MAX_KB = 31;       // digits within 62 KB of LDS
 constexpr size_t MFMA_MAX_WAVE_ROWS = 64;  // m * ceil(KB / 4): chunk wavefronts, at most 16 per thread of 256
@@ -185,25 +194,28 @@ bool mfma_fits(size_t m, size_t k, const float *a, size_t lda) {
 
 template <int WAVES, int KBC, int J>
 void launch_mfma_t(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
-                   const EpiArgs &epi, size_t blocks, hipStream_t s) {
-    const bool q8 = w.precision == Q8_0;
-    hipLaunchKernelGGL(q8 ? (gemv_mfma_kernel<WAVES, KBC, J, 1>) : (gemv_mfma_kernel<WAVES, KBC, J, 0>),
-                       dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a, lda, (int)m, (int)w.k, w.values,
-                       w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc,
-                       epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
+                   const EpiArgs &epi, size_t blocks, bool dot, hipStream_t s) {
+    void (*kernel)(const float *, size_t, int, int, const uint8_t *, const float *, int, int, int, int, float *,
+                   size_t, const float *, uint32_t, float, int, size_t, size_t);
+    if (w.precision == Q8_0) kernel = gemv_mfma_kernel<WAVES, KBC, J, 1, 0>;
+    else if (!dot) kernel = gemv_mfma_kernel<WAVES, KBC, J, 0, 0>;
+    else kernel = gemv_mfma_kernel<WAVES, KBC, J, 0, 1>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a, lda, (int)m, (int)w.k,
+                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc, epi.bias,
+                       epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
 }
 
 template <int WAVES, int KBC>
 void launch_mfma_j(size_t j, const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c,
-                   size_t ldc, const EpiArgs &epi, size_t blocks, hipStream_t s) {
-    if (j <= 1) launch_mfma_t<WAVES, KBC, 1>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else if (j <= 3) launch_mfma_t<WAVES, KBC, 3>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else if (j <= 6) launch_mfma_t<WAVES, KBC, 6>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12>(a, lda, m, w, c, ldc, epi, blocks, s);
-    else launch_mfma_t<WAVES, KBC, 16>(a, lda, m, w, c, ldc, epi, blocks, s);
+                   size_t ldc, const EpiArgs &epi, size_t blocks, bool dot, hipStream_t s) {
+    if (j <= 1) launch_mfma_t<WAVES, KBC, 1>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 3) launch_mfma_t<WAVES, KBC, 3>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 6) launch_mfma_t<WAVES, KBC, 6>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else launch_mfma_t<WAVES, KBC, 16>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
 }
 
 hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
@@ -219,12 +231,13 @@ hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights
     if (j > 16) return hipErrorInvalidValue;  // excluded by mfma_fits
     const size_t per_wave = div_ceil(w.panels, (size_t)waves * MFMA_MAX_GRID);
     const size_t blocks = div_ceil(w.panels, (size_t)waves * per_wave);
+    const bool dot = gemv_dot_rows(m) && w.precision == INT8;
     if (waves == 2) {
-        if (w.kb <= 10) launch_mfma_j<2, 10>(j, a, lda, m, w, c, ldc, epi, blocks, s);
-        else launch_mfma_j<2, 16>(j, a, lda, m, w, c, ldc, epi, blocks, s);
+        if (w.kb <= 10) launch_mfma_j<2, 10>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
+        else launch_mfma_j<2, 16>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
     } else {
-        if (w.kb <= 10) launch_mfma_j<4, 10>(j, a, lda, m, w, c, ldc, epi, blocks, s);
-        else launch_mfma_j<4, 16>(j, a, lda, m, w, c, ldc, epi, blocks, s);
+        if (w.kb <= 10) launch_mfma_j<4, 10>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
+        else launch_mfma_j<4, 16>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
     }
     return hipGetLastError();
 }
