@@ -53,16 +53,17 @@ __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
     return max(max(r0, r1), max(r2, r3));
 }
 
-// What one wavefront needs of panel p: its KBC first weight blocks, and for its lane's column the
-// scale, the bias and the old outputs of its four rows (when accumulating).
+// What one wavefront needs of panel p: its KBC first weight blocks (k-blocks kw, kw + ks, ...), and
+// for its lane's column the scale, the bias and the old outputs of its four rows (when accumulating).
 template <int KBC>
 __device__ __forceinline__ void fetch_panel(v4i (&wr)[KBC], float &sc, float &bv, float (&old)[4], int p, int lane,
                                             const uint8_t *wv, size_t panel_stride, size_t blk_stride, int KB,
                                             const float *scales, const float *bias, const float *c, size_t ldc,
-                                            int N, int m, int accumulate) {
+                                            int N, int m, int accumulate, int kw = 0, int ks = 1) {
     const uint8_t *wp = wv + (size_t)p * panel_stride + lane * 16;
 #pragma unroll
-    for (int t = 0; t < KBC; t++) wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(t, KB - 1) * blk_stride);
+    for (int t = 0; t < KBC; t++)
+        wr[t] = *reinterpret_cast<const v4i *>(wp + (size_t)min(kw + ks * t, KB - 1) * blk_stride);
     // Branch-free: loads that are not needed read a valid address and are discarded, so the
     // compiler's load counting stays exact and nothing here waits on earlier loads.
     const int col = p * PANEL + (lane & 15), orow = (lane >> 4) * 4;
@@ -125,7 +126,7 @@ __device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, in
 // last wavefront idle); wavefront w holds chunk wavefronts w + WAVES j (j < J) in registers. The
 // rows are read once, before the weights, so the weight loads stay in flight while the rows are
 // digitised.
-template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR = 0>
+template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR = 0, int KS = 1>
 __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
                                           const float *__restrict__ scales, int N, int P, int KB, int NB,
                                           const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
@@ -137,8 +138,15 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
     // uniform over the wavefront; q / spr is (q inv) >> 16, exact for q < 1024 and spr <= 8.
     const int spr = (KB + 3) / 4, inv = (65536 + spr - 1) / spr;
     const int wq = __builtin_amdgcn_readfirstlane(wave);
-    const int step = gridDim.x * WAVES;
-    int p = blockIdx.x * WAVES + wave;
+    // KS > 1 (int8, KS = WAVES): the workgroup's wavefronts share each panel, wavefront kw taking
+    // k-blocks kw, kw + KS, ...; their integer sums meet in LDS and wavefront 0 stores the panel.
+    // For products of few panels, where one wavefront per panel would leave most SIMDs idle and
+    // walk long rows of k-blocks alone.
+    static_assert(KS == 1 || (KS == WAVES && !Q8), "the k-split takes the whole workgroup, int8 weights");
+    const int kw = KS > 1 ? wave : 0;
+    const int nkb = KS > 1 ? (KB - kw + KS - 1) / KS : KB;  // this wavefront's k-blocks
+    const int step = KS > 1 ? gridDim.x : gridDim.x * WAVES;
+    int p = KS > 1 ? blockIdx.x : blockIdx.x * WAVES + wave;
 
     // One 16-byte load per chunk (rows 16-byte aligned, k % 4 == 0); chunks past the rows read
     // the zero chunk. Every load is unconditional and used as loaded, so the loads stay ahead of
@@ -162,7 +170,7 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
                             bias, c, ldc, N, m, accumulate);
     else
         fetch_panel<KBC>(wr, sc, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias, c,
-                         ldc, N, m, accumulate);
+                         ldc, N, m, accumulate, kw, KS);
 
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -209,6 +217,7 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
     // DOTR rows: lane (g = l / 16, j = l % 16) reads row r's operand lane 16 g + r (the digits of
     // the inputs its weights multiply) and sums with v_dot4_i32_i8.
     const uint8_t *dp = sqa + (lane >> 4) * 256;
+    int par = 0;
     for (; p < P; p += step) {
         v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
         v4f accq = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -216,7 +225,7 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
 #pragma unroll
         for (int r = 0; r < (DOTR > 0 ? DOTR : 1); r++) dh[r] = dl[r] = 0;
         const uint8_t *wp = wv + (size_t)p * panel_stride;
-        for (int c0 = 0; c0 < KB; c0 += KBC) {
+        for (int c0 = 0; c0 < nkb; c0 += KBC) {
             if constexpr (Q8) {
                 if (c0 > 0)
                     load_q8<KBC>(wh, sq, wp, scales + (size_t)p * NB * PANEL + (lane & 15), c0, KB, NB, blk_stride,
@@ -241,16 +250,18 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
                 if (c0 > 0) {
 #pragma unroll
                     for (int t = 0; t < KBC; t++)
-                        wr[t] = *reinterpret_cast<const v4i *>(wp + lane * 16 + (size_t)min(c0 + t, KB - 1) * blk_stride);
+                        wr[t] = *reinterpret_cast<const v4i *>(wp + lane * 16 +
+                                                               (size_t)min(kw + KS * (c0 + t), KB - 1) * blk_stride);
                 }
 #pragma unroll
                 for (int t = 0; t < KBC; t++) {
-                    if (c0 + t < KB) {
+                    if (c0 + t < nkb) {
+                        const int kt = kw + KS * (c0 + t);  // the k-block
                         if constexpr (DOT) {
 #pragma unroll
                             for (int r = 0; r < DOTR; r++) {
-                                const v4i ahi = *reinterpret_cast<const v4i *>(dp + (c0 + t) * 2048 + r * 16);
-                                const v4i alo = *reinterpret_cast<const v4i *>(dp + (c0 + t) * 2048 + 1024 + r * 16);
+                                const v4i ahi = *reinterpret_cast<const v4i *>(dp + kt * 2048 + r * 16);
+                                const v4i alo = *reinterpret_cast<const v4i *>(dp + kt * 2048 + 1024 + r * 16);
                                 int h = dh[r], l = dl[r];
                                 h = __builtin_amdgcn_sdot4(ahi.x, wr[t].x, h, false);
                                 h = __builtin_amdgcn_sdot4(ahi.y, wr[t].y, h, false);
@@ -264,8 +275,8 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
                                 dl[r] = l;
                             }
                         } else {
-                            const v4i ahi = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048);
-                            const v4i alo = *reinterpret_cast<const v4i *>(ap + (c0 + t) * 2048 + 1024);
+                            const v4i ahi = *reinterpret_cast<const v4i *>(ap + kt * 2048);
+                            const v4i alo = *reinterpret_cast<const v4i *>(ap + kt * 2048 + 1024);
                             acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wr[t], acc_hi, 0, 0, 0);
                             acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wr[t], acc_lo, 0, 0, 0);
                         }
@@ -290,18 +301,39 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
                 acc_lo[v] = upper ? dl[(4 + v) % DOTR] : dl[v % DOTR];
             }
         }
+        if constexpr (KS > 1) {
+            // Two sets of slots, alternating by panel: a set is rewritten two panels on, after a
+            // barrier that wavefront 0 reaches only once it has read the set.
+            __shared__ v4i part[2][KS][2][64];
+            v4i(*mine)[2][64] = part[par];
+            mine[kw][0][lane] = acc_hi;
+            mine[kw][1][lane] = acc_lo;
+            __syncthreads();
+            if (kw == 0) {
+#pragma unroll
+                for (int w = 1; w < KS; w++) {
+                    acc_hi += mine[w][0][lane];
+                    acc_lo += mine[w][1][lane];
+                }
+            }
+            par ^= 1;
+        }
         const float sc0 = sc, bv0 = bv;
         float old0[4];
 #pragma unroll
         for (int v = 0; v < 4; v++) old0[v] = old[v];
-        if constexpr (Q8)
-            fetch_panel_q8<KBC>(wh, sq, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, NB, off0,
-                                scales, bias, c, ldc, N, m, accumulate);
-        else
-            fetch_panel<KBC>(wr, sc, bv, old, min(p + step, P - 1), lane, wv, panel_stride, blk_stride, KB, scales,
-                             bias, c, ldc, N, m, accumulate);
+        // The next panel's operands, when there is one (a uniform branch: the last panel's wavefront
+        // leaves without loads still on the way).
+        if (p + step < P) {
+            if constexpr (Q8)
+                fetch_panel_q8<KBC>(wh, sq, bv, old, p + step, lane, wv, panel_stride, blk_stride, KB, NB, off0, scales,
+                                    bias, c, ldc, N, m, accumulate);
+            else
+                fetch_panel<KBC>(wr, sc, bv, old, p + step, lane, wv, panel_stride, blk_stride, KB, scales, bias, c,
+                                 ldc, N, m, accumulate, kw, KS);
+        }
         const int col = p * PANEL + ocol;
-        if (col < N) {
+        if (col < N && kw == 0) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 if (orow + v < m) {

@@ -157,7 +157,7 @@ hipError_t launch_rows(const float *a, size_t lda, const DeviceWeights &w, float
 
 
 // Rows are read from a (row stride lda), outputs written to c: the GEMV of tg_matmul_device.
-template <int WAVES, int KBC, int J, int Q8, int DOTR>
+template <int WAVES, int KBC, int J, int Q8, int DOTR, int KS>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__restrict__ a, size_t lda, int m, int k,
                                                                const uint8_t *__restrict__ wv,
                                                                const float *__restrict__ scales, int N, int P, int KB,
@@ -168,9 +168,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(const float *__re
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];  // KB x (hi, lo) x 1 KB operands
     __shared__ uint32_t slot[WAVES * J];                           // max |x| bits per wavefront of chunks
     gemv::StoreC out{c, ldc};
-    gemv::mfma_body<WAVES, KBC, J, Q8, gemv::RowsIn, gemv::StoreC, DOTR>(gemv::RowsIn{a, lda}, out, m, k, wv, scales, N,
-                                                                      P, KB, NB, c, ldc, bias, act, escale, accumulate,
-                                                                      panel_stride, blk_stride, sqa, slot);
+    gemv::mfma_body<WAVES, KBC, J, Q8, gemv::RowsIn, gemv::StoreC, DOTR, KS>(gemv::RowsIn{a, lda}, out, m, k, wv,
+                                                                          scales, N, P, KB, NB, c, ldc, bias, act,
+                                                                          escale, accumulate, panel_stride,
+                                                                          blk_stride, sqa, slot);
 }
 
 // A single decode row (m = 1, int8 weights) takes the dot4 variant of the body: the same row, panels
@@ -192,35 +193,47 @@ bool mfma_fits(size_t m, size_t k, const float *a, size_t lda) {
            lda % 4 == 0 && k % 4 == 0;
 }
 
-template <int WAVES, int KBC, int J>
+template <int WAVES, int KBC, int J, int KS>
 void launch_mfma_t(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                    const EpiArgs &epi, size_t blocks, bool dot, hipStream_t s) {
     void (*kernel)(const float *, size_t, int, int, const uint8_t *, const float *, int, int, int, int, float *,
                    size_t, const float *, uint32_t, float, int, size_t, size_t);
-    if (w.precision == Q8_0) kernel = gemv_mfma_kernel<WAVES, KBC, J, 1, 0>;
-    else if (!dot) kernel = gemv_mfma_kernel<WAVES, KBC, J, 0, 0>;
-    else kernel = gemv_mfma_kernel<WAVES, KBC, J, 0, 1>;
+    if constexpr (KS > 1) kernel = dot ? gemv_mfma_kernel<WAVES, KBC, J, 0, 1, KS> : gemv_mfma_kernel<WAVES, KBC, J, 0, 0, KS>;
+    else if (w.precision == Q8_0) kernel = gemv_mfma_kernel<WAVES, KBC, J, 1, 0, 1>;
+    else kernel = dot ? gemv_mfma_kernel<WAVES, KBC, J, 0, 1, 1> : gemv_mfma_kernel<WAVES, KBC, J, 0, 0, 1>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(WAVES * 64), w.kb * 2048, s, a, lda, (int)m, (int)w.k,
                        w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc, epi.bias,
                        epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
 }
 
-template <int WAVES, int KBC>
+template <int WAVES, int KBC, int KS>
 void launch_mfma_j(size_t j, const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c,
                    size_t ldc, const EpiArgs &epi, size_t blocks, bool dot, hipStream_t s) {
-    if (j <= 1) launch_mfma_t<WAVES, KBC, 1>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else if (j <= 3) launch_mfma_t<WAVES, KBC, 3>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else if (j <= 6) launch_mfma_t<WAVES, KBC, 6>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
-    else launch_mfma_t<WAVES, KBC, 16>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    if (j <= 1) launch_mfma_t<WAVES, KBC, 1, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 2) launch_mfma_t<WAVES, KBC, 2, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 3) launch_mfma_t<WAVES, KBC, 3, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 4) launch_mfma_t<WAVES, KBC, 4, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 6) launch_mfma_t<WAVES, KBC, 6, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 8) launch_mfma_t<WAVES, KBC, 8, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else if (j <= 12) launch_mfma_t<WAVES, KBC, 12, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
+    else launch_mfma_t<WAVES, KBC, 16, KS>(a, lda, m, w, c, ldc, epi, blocks, dot, s);
 }
 
 hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                        const EpiArgs &epi, hipStream_t s) {
     const size_t chunks = m * div_ceil(w.kb, (size_t)4) * 64;
+    const bool dot = gemv_dot_rows(m) && w.precision == INT8;
+    if (w.precision == INT8 && w.panels <= MFMA_MAX_GRID && m <= 8) {
+        // Few panels: one workgroup of four wavefronts per panel, its k-blocks split four ways, so
+        // that four times the SIMDs stream the weights and each walks a quarter of the row. (Past
+        // eight rows, digitising the rows once per panel costs more than the split saves.)
+        const size_t j = div_ceil(chunks, (size_t)256), kq = div_ceil(w.kb, (size_t)4);
+        if (j > 16) return hipErrorInvalidValue;  // excluded by mfma_fits
+        if (kq <= 3) launch_mfma_j<4, 3, 4>(j, a, lda, m, w, c, ldc, epi, w.panels, dot, s);
+        else if (kq <= 5) launch_mfma_j<4, 5, 4>(j, a, lda, m, w, c, ldc, epi, w.panels, dot, s);
+        else launch_mfma_j<4, 8, 4>(j, a, lda, m, w, c, ldc, epi, w.panels, dot, s);
+        return hipGetLastError();
+    }
     // Two-wave workgroups for short products, so they spread over more CUs.
     int waves = w.panels < 1024 ? 2 : 4;
     size_t j = div_ceil(chunks, (size_t)waves * 64);
@@ -231,13 +244,12 @@ hipError_t launch_mfma(const float *a, size_t lda, size_t m, const DeviceWeights
     if (j > 16) return hipErrorInvalidValue;  // excluded by mfma_fits
     const size_t per_wave = div_ceil(w.panels, (size_t)waves * MFMA_MAX_GRID);
     const size_t blocks = div_ceil(w.panels, (size_t)waves * per_wave);
-    const bool dot = gemv_dot_rows(m) && w.precision == INT8;
     if (waves == 2) {
-        if (w.kb <= 10) launch_mfma_j<2, 10>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
-        else launch_mfma_j<2, 16>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
+        if (w.kb <= 10) launch_mfma_j<2, 10, 1>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
+        else launch_mfma_j<2, 16, 1>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
     } else {
-        if (w.kb <= 10) launch_mfma_j<4, 10>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
-        else launch_mfma_j<4, 16>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
+        if (w.kb <= 10) launch_mfma_j<4, 10, 1>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
+        else launch_mfma_j<4, 16, 1>(j, a, lda, m, w, c, ldc, epi, blocks, dot, s);
     }
     return hipGetLastError();
 }

@@ -4,7 +4,8 @@
 //
 // Each kernel is the GEMV of gemv_core.hpp with its own input rows and outputs: the dot4 body for
 // the one-row products of int8 weights (the LSTM layers and the projection of a decode step), the
-// MFMA body for the joint's window of frames, for predictions of several rows and for Q8_0. No kernel
+// MFMA body for the joint's window of frames, for predictions of several rows and for Q8_0; int8
+// predictions of up to eight rows split each panel's k-blocks over a workgroup. No kernel
 // waits for, or counts, the workgroups of its own grid: what a step decides is computed from one
 // kernel's outputs by the next kernel, after the boundary between them has made them visible.
 //
@@ -336,7 +337,7 @@ __device__ __forceinline__ int decide_step(TdtCtl *ctl, const Decide &d, int *cu
 // State buffers of a prediction: a (rows x width) is read and b written when cur is 0, the other
 // way round when it is 1. mode 0: a standalone prediction (cur 0, tokens by value); 1: a later layer
 // of the decode (runs when a token was handed on); 2: layer 0 of the decode, which decides the step.
-template <int KBC, int J, int Q8, int DOTR = 0>
+template <int KBC, int J, int Q8, int DOTR = 0, int KS = 1>
 __global__ __launch_bounds__(TDT_THREADS) void tdt_lstm_kernel(TdtCtl *ctl, int mode, TdtTokens toks, Decide dec,
                                                                int m, int l, const float *__restrict__ emb,
                                                                float *sa, float *sb, size_t width, Weights w,
@@ -361,13 +362,13 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_lstm_kernel(TdtCtl *ctl, int 
     float *s_in = cur ? sb : sa, *s_out = cur ? sa : sb;
     const int h = w.k / 2;
     LstmOut out{s_in, s_out, width, h, l};
-    gemv::mfma_body<TDT_WAVES, KBC, J, Q8, LstmIn, LstmOut, DOTR>(LstmIn{emb, s_in, s_out, width, h, l, tok_s}, out, m,
+    gemv::mfma_body<TDT_WAVES, KBC, J, Q8, LstmIn, LstmOut, DOTR, KS>(LstmIn{emb, s_in, s_out, width, h, l, tok_s}, out, m,
                                                                   w.k, w.values, w.scales, w.n, w.P, w.KB, w.NB, s_out,
                                                                   width, bias, ACT_NONE, 1.0f, 0, w.panel_stride,
                                                                   w.blk_stride, sqa, slot);
 }
 
-template <int KBC, int J, int Q8, int DOTR = 0>
+template <int KBC, int J, int Q8, int DOTR = 0, int KS = 1>
 __global__ __launch_bounds__(TDT_THREADS) void tdt_proj_kernel(TdtCtl *ctl, int gated, int m, const float *sa,
                                                                const float *sb, size_t width, int layers, Weights w,
                                                                const float *__restrict__ bias, float *preds) {
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_proj_kernel(TdtCtl *ctl, int 
     const float *s_out = (gated && load_i(&ctl->cur)) ? sa : sb;
     const int h = w.k;
     gemv::StoreC out{preds, (size_t)h};
-    gemv::mfma_body<TDT_WAVES, KBC, J, Q8, gemv::RowsIn, gemv::StoreC, DOTR>(
+    gemv::mfma_body<TDT_WAVES, KBC, J, Q8, gemv::RowsIn, gemv::StoreC, DOTR, KS>(
         gemv::RowsIn{s_out + (size_t)(layers - 1) * 2 * h, width}, out, m, w.k, w.values, w.scales, w.n, w.P, w.KB,
         w.NB, preds, (size_t)h, bias, ACT_NONE, 1.0f, 0, w.panel_stride, w.blk_stride, sqa, slot);
 }
@@ -435,27 +436,33 @@ int j_of(size_t m, const DeviceWeights &d) {
         else hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 20, 1>) : (KERNEL<KBC, 20, 0>), g_, b_, lds_, s, __VA_ARGS__);                 \
     } while (0)
 
-// One-row products of int8 weights (DOT) take the dot4 body; Q8_0 and several rows the MFMA.
-#define TG_TDT_KBC_ROW(KERNEL, KBC, ...)                                                                      \
+// Predictions of int8 weights and up to eight rows: one workgroup per panel with the panel's
+// k-blocks split over its four wavefronts (the GEMV's k-split), the dot4 body for one row (ONE).
+// Q8_0 weights take the persistent MFMA grid of TG_TDT_DISPATCH.
+#define TG_TDT_KS_J(KERNEL, KBC, ...)                                                                         \
     do {                                                                                                      \
-        if (jj_ == 2) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 2, 1, 0>) : dot_ ? (KERNEL<KBC, 2, 0, 1>) : (KERNEL<KBC, 2, 0, 0>), g_, b_, lds_, s, __VA_ARGS__);       \
-        else if (jj_ == 4) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 4, 1, 0>) : dot_ ? (KERNEL<KBC, 4, 0, 1>) : (KERNEL<KBC, 4, 0, 0>), g_, b_, lds_, s, __VA_ARGS__);  \
-        else if (jj_ == 8) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 8, 1, 0>) : dot_ ? (KERNEL<KBC, 8, 0, 1>) : (KERNEL<KBC, 8, 0, 0>), g_, b_, lds_, s, __VA_ARGS__);  \
-        else if (jj_ == 12) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 12, 1, 0>) : dot_ ? (KERNEL<KBC, 12, 0, 1>) : (KERNEL<KBC, 12, 0, 0>), g_, b_, lds_, s, __VA_ARGS__); \
-        else if (jj_ == 16) hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 16, 1, 0>) : dot_ ? (KERNEL<KBC, 16, 0, 1>) : (KERNEL<KBC, 16, 0, 0>), g_, b_, lds_, s, __VA_ARGS__); \
-        else hipLaunchKernelGGL(q8_ ? (KERNEL<KBC, 20, 1, 0>) : dot_ ? (KERNEL<KBC, 20, 0, 1>) : (KERNEL<KBC, 20, 0, 0>), g_, b_, lds_, s, __VA_ARGS__);                \
+        if (jj_ == 2) hipLaunchKernelGGL(dot_ ? (KERNEL<KBC, 2, 0, 1, 4>) : (KERNEL<KBC, 2, 0, 0, 4>), g_, b_, lds_, s, __VA_ARGS__);        \
+        else if (jj_ == 4) hipLaunchKernelGGL(dot_ ? (KERNEL<KBC, 4, 0, 1, 4>) : (KERNEL<KBC, 4, 0, 0, 4>), g_, b_, lds_, s, __VA_ARGS__);   \
+        else if (jj_ == 8) hipLaunchKernelGGL(dot_ ? (KERNEL<KBC, 8, 0, 1, 4>) : (KERNEL<KBC, 8, 0, 0, 4>), g_, b_, lds_, s, __VA_ARGS__);   \
+        else if (jj_ == 12) hipLaunchKernelGGL(dot_ ? (KERNEL<KBC, 12, 0, 1, 4>) : (KERNEL<KBC, 12, 0, 0, 4>), g_, b_, lds_, s, __VA_ARGS__); \
+        else hipLaunchKernelGGL(dot_ ? (KERNEL<KBC, 16, 0, 1, 4>) : (KERNEL<KBC, 16, 0, 0, 4>), g_, b_, lds_, s, __VA_ARGS__);                \
     } while (0)
 
-#define TG_TDT_DISPATCH_ROW(KERNEL, JJ, D, ONE, ...)                     \
+#define TG_TDT_DISPATCH_KS(KERNEL, JJ, D, ONE, ...)                      \
     do {                                                                 \
-        const bool q8_ = (D).precision == Q8_0, dot_ = (ONE);            \
-        const size_t lds_ = (D).kb * 2048;                               \
-        const dim3 g_(grid_of(D)), b_(TDT_THREADS);                      \
+        const bool dot_ = (ONE);                                         \
+        const size_t lds_ = (D).kb * 2048, kq_ = div_ceil((D).kb, (size_t)4); \
+        const dim3 g_((unsigned)(D).panels), b_(TDT_THREADS);            \
         const int jj_ = (JJ);                                            \
-        if ((D).kb <= 10) TG_TDT_KBC_ROW(KERNEL, 10, __VA_ARGS__);       \
-        else if ((D).kb <= 20) TG_TDT_KBC_ROW(KERNEL, 20, __VA_ARGS__);  \
-        else TG_TDT_KBC_ROW(KERNEL, 16, __VA_ARGS__);                    \
+        if (kq_ <= 3) TG_TDT_KS_J(KERNEL, 3, __VA_ARGS__);               \
+        else if (kq_ <= 5) TG_TDT_KS_J(KERNEL, 5, __VA_ARGS__);          \
+        else TG_TDT_KS_J(KERNEL, 8, __VA_ARGS__);                        \
     } while (0)
+
+// Whether a prediction of m rows on these weights takes the k-split launch.
+bool tdt_split(size_t m, const DeviceWeights &d) {
+    return d.precision == INT8 && m <= 8 && d.panels <= (size_t)TDT_MAX_GRID && j_of(m, d) <= 16;
+}
 
 #define TG_TDT_DISPATCH(KERNEL, JJ, D, ...)                              \
     do {                                                                 \
@@ -492,12 +499,20 @@ hipError_t launch_tdt_predict(TdtCtl *ctl, const TdtTokens &toks, size_t m, cons
     const Decide none{};
     for (size_t l = 0; l < net.layers; l++) {
         const DeviceWeights &d = *net.lstm[l];
-        TG_TDT_DISPATCH_ROW(tdt_lstm_kernel, j_of(m, d), d, m == 1, ctl, 0, toks, none, (int)m, (int)l, net.emb, sa, sb,
-                            width, weights_of(d), net.lstm_b[l]);
+        if (tdt_split(m, d))
+            TG_TDT_DISPATCH_KS(tdt_lstm_kernel, j_of(m, d), d, m == 1, ctl, 0, toks, none, (int)m, (int)l, net.emb, sa,
+                               sb, width, weights_of(d), net.lstm_b[l]);
+        else
+            TG_TDT_DISPATCH(tdt_lstm_kernel, j_of(m, d), d, ctl, 0, toks, none, (int)m, (int)l, net.emb, sa, sb, width,
+                            weights_of(d), net.lstm_b[l]);
     }
     const DeviceWeights &p = *net.proj;
-    TG_TDT_DISPATCH_ROW(tdt_proj_kernel, j_of(m, p), p, m == 1, ctl, 0, (int)m, sa, sb, width, (int)net.layers,
-                        weights_of(p), net.proj_b, preds);
+    if (tdt_split(m, p))
+        TG_TDT_DISPATCH_KS(tdt_proj_kernel, j_of(m, p), p, m == 1, ctl, 0, (int)m, sa, sb, width, (int)net.layers,
+                           weights_of(p), net.proj_b, preds);
+    else
+        TG_TDT_DISPATCH(tdt_proj_kernel, j_of(m, p), p, ctl, 0, (int)m, sa, sb, width, (int)net.layers, weights_of(p),
+                        net.proj_b, preds);
     return hipGetLastError();
 }
 
@@ -512,12 +527,20 @@ hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, siz
     const size_t width = net.layers * 2 * net.h;
     for (size_t l = 0; l < net.layers; l++) {
         const DeviceWeights &w = *net.lstm[l];
-        TG_TDT_DISPATCH_ROW(tdt_lstm_kernel, j_of(1, w), w, true, ctl, l == 0 ? 2 : 1, TdtTokens{}, dec, 1, (int)l,
-                            net.emb, sa, sb, width, weights_of(w), net.lstm_b[l]);
+        if (tdt_split(1, w))
+            TG_TDT_DISPATCH_KS(tdt_lstm_kernel, j_of(1, w), w, true, ctl, l == 0 ? 2 : 1, TdtTokens{}, dec, 1, (int)l,
+                               net.emb, sa, sb, width, weights_of(w), net.lstm_b[l]);
+        else
+            TG_TDT_DISPATCH(tdt_lstm_kernel, j_of(1, w), w, ctl, l == 0 ? 2 : 1, TdtTokens{}, dec, 1, (int)l, net.emb,
+                            sa, sb, width, weights_of(w), net.lstm_b[l]);
     }
     const DeviceWeights &p = *net.proj;
-    TG_TDT_DISPATCH_ROW(tdt_proj_kernel, j_of(1, p), p, true, ctl, 1, 1, sa, sb, width, (int)net.layers,
-                        weights_of(p), net.proj_b, pred);
+    if (tdt_split(1, p))
+        TG_TDT_DISPATCH_KS(tdt_proj_kernel, j_of(1, p), p, true, ctl, 1, 1, sa, sb, width, (int)net.layers,
+                           weights_of(p), net.proj_b, pred);
+    else
+        TG_TDT_DISPATCH(tdt_proj_kernel, j_of(1, p), p, ctl, 1, 1, sa, sb, width, (int)net.layers, weights_of(p),
+                        net.proj_b, pred);
     return hipGetLastError();
 }
 
