@@ -791,6 +791,36 @@ def shape_leg(m, k, n, reps):
             "tops": round(2 * m * n * k / us / 1e6, 1)}
 
 
+def gemv_shape_leg(m, k, n, reps):
+    """One decode GEMV shape alone (tg_matmul_device on m rows of k inputs, the GEMV path), the
+    program rocprofv3 runs for the GEMV's kernel statistics and HBM byte counters: `reps` eager
+    launches rotating over copies of the weights totalling more than 600 MB (twice the 256 MB
+    Infinity Cache and more), so every launch streams its weights from HBM."""
+    import torch
+
+    import telmo_amd
+
+    values, scales = panel_layout(synth_int8(n, k, 7000), synth_scales(n, 7100))
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    one = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+    copies = [one] + [telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+                      for _ in range(int(600e6 // one.bytes()))]
+    a = torch.from_numpy(synth_normal((m, k), 7300 + m)).cuda()
+    c = torch.empty((m, n), device="cuda")
+    for w in copies[:3]:
+        kern.matmul_device(a, k, m, w, c, n)
+    ms = timed_on(stream, lambda i: kern.matmul_device(a, k, m, copies[i % len(copies)], c, n), reps)
+    wbytes = one.bytes()
+    for w in copies:
+        w.close()
+    kern.close()
+    return {"gemv_shape": [m, k, n], "reps": reps, "copies": len(copies), "weight_bytes": wbytes,
+            "us_per_launch": round(ms * 1e3, 3), "gb_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "note": "eager launches (the launch gaps included); rotating copies, weights from HBM"}
+
+
 def load_traffic():
     path = os.path.join(ROOT, "profiles", "layer_T750_traffic.json")
     if not os.path.exists(path):
@@ -813,12 +843,17 @@ def main():
     ap.add_argument("--no-tdt", action="store_true")
     ap.add_argument("--shape", type=int, nargs=3, metavar=("M", "K", "N"),
                     help="time one product shape alone (the program for per-shape rocprofv3 runs) and exit")
-    ap.add_argument("--reps", type=int, default=20, help="launches timed with --shape")
+    ap.add_argument("--gemv", type=int, nargs=3, metavar=("M", "K", "N"),
+                    help="time one decode GEMV shape over rotating weight copies (for rocprofv3 runs) and exit")
+    ap.add_argument("--reps", type=int, default=20, help="launches timed with --shape or --gemv")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU and has no multi-GPU path: run it with --gpus 1")
     if args.shape:
         print(json.dumps(shape_leg(*args.shape, args.reps)), flush=True)
+        return
+    if args.gemv:
+        print(json.dumps(gemv_shape_leg(*args.gemv, args.reps)), flush=True)
         return
 
     params = layer_params(100)
