@@ -876,6 +876,28 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         for (int cb = 0; cb < CB; cb++)
             fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
     };
+    // Row blocks [r0, r1) of this wavefront's A fragments (and, with b, its B fragments).
+    auto read_frags_rows = [&](const uint8_t *st, v4i (&fa)[RB][2], v4i (&fb)[CB], int r0, int r1, bool b) {
+        if (b) {
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+                fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            if (r < r0 || r >= r1) continue;
+            fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2) * 1024 + lane * 16);
+            fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2 + 1) * 1024 + lane * 16);
+        }
+    };
+#define TG_MMA_ROWS(fa, fb, r0, r1)                                                                    \
+    do {                                                                                               \
+        _Pragma("unroll") for (int r = (r0); r < (r1); r++)                                            \
+            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
+                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][0], (fb)[cb], acc_hi[r][cb], 0, 0, 0); \
+                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][1], (fb)[cb], acc_lo[r][cb], 0, 0, 0); \
+            }                                                                                          \
+    } while (0)
 #define TG_MMA(fa, fb)                                                                                 \
     do {                                                                                               \
         _Pragma("unroll") for (int r = 0; r < RB; r++)                                                 \
@@ -903,16 +925,31 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                 __syncthreads();
                 if (t + NS - 1 < KB) TG_ISSUE((s + NS - 1) % NS, t + NS - 1);
                 v4i fa[RB][2], fb[CB];
-                read_frags(smem + s * STAGE, fa, fb);
-                // All twelve reads are issued before the first MFMA, so that the LDS latency is
-                // waited out once per k-block, not once per row block.
-                __builtin_amdgcn_sched_barrier(0);
-                TG_MMA(fa, fb);
+                if constexpr (RB >= 4) {
+                    // The B fragments and the first half of the A fragments are read and waited
+                    // for; the second half's reads are issued before the first half's MFMAs, so
+                    // their LDS latency passes under those MFMAs.
+                    constexpr int H = RB / 2;
+                    read_frags_rows(smem + s * STAGE, fa, fb, 0, H, true);
+                    __builtin_amdgcn_sched_barrier(0);
+                    read_frags_rows(smem + s * STAGE, fa, fb, H, RB, false);
+                    __builtin_amdgcn_sched_barrier(0);
+                    TG_MMA_ROWS(fa, fb, 0, H);
+                    __builtin_amdgcn_sched_barrier(0);
+                    TG_MMA_ROWS(fa, fb, H, RB);
+                } else {
+                    read_frags(smem + s * STAGE, fa, fb);
+                    // All the reads are issued before the first MFMA, so that the LDS latency is
+                    // waited out once per k-block, not once per row block.
+                    __builtin_amdgcn_sched_barrier(0);
+                    TG_MMA(fa, fb);
+                }
             }
         }
     }
 #undef TG_ISSUE
 #undef TG_MMA
+#undef TG_MMA_ROWS
     // Row exponents and column scales are loaded after the k-loop, which leaves their registers
     // to the operand fragments.
     int32_t e_row[RB][4];
