@@ -92,8 +92,7 @@ uint32_t tg_ctx_mode(const tg_ctx *ctx);
 /* The message of the last failed call on this context ("" if none), copied into storage of the
  * calling thread: valid until that thread's next tg_last_error call. */
 const char *tg_last_error(const tg_ctx *ctx);
-/* Waits for all work queued on the context's stream; TG_ERR_HIP if a quantised-output product on it
- * gave up waiting for its rows (tg_matmul_quantized_to_quant_device). */
+/* Waits for all work queued on the context's stream; TG_ERR_HIP if the device reports an error. */
 int tg_synchronize(tg_ctx *ctx);
 
 /* ---- weights ------------------------------------------------------------------------------ */
@@ -181,14 +180,14 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
 /* The product of quantised rows whose outputs go out quantised in turn: epi(qa . w) as
  * tg_matmul_quantized_device computes it, then the two-digit quantisation tg_quantize_rows_device
  * makes of those f32 rows, into qa_out (tg_quant_bytes(m, n) bytes) and exps_out (m), bit-identical
- * to the two calls; the f32 rows never reach memory. For a feed-forward block's first product,
- * whose only reader is the second (src/parakeet.rs:1024-1060: ff_in with SiLU into s.big, then
- * ff_out), which then takes qa_out through tg_matmul_quantized_device. int8 weights, fast mode, no
- * accumulation (TG_ERR_ARG), n <= 65536. Each workgroup waits for the other column tiles of its
- * rows, which the in-order dispatch of whole tile rows keeps short; a wait that runs out (about a
- * second) marks the launch, and the next tg_synchronize on the context returns TG_ERR_HIP. Calls on
- * one context share its rendezvous state, so they must not overlap on the device. Device pointers,
- * queued on the stream. No counterpart in the reference, whose sums are all f32. */
+ * to the two calls. For a feed-forward block's first product, whose only reader is the second
+ * (src/parakeet.rs:1024-1060: ff_in with SiLU into s.big, then ff_out), which then takes qa_out
+ * through tg_matmul_quantized_device. The product also leaves each row's largest |y| per tile
+ * column, so the quantiser streams the f32 rows (kept in a context workspace of about 4 m n bytes,
+ * grown on first use) once, without a reduction. int8 weights, fast mode, no accumulation
+ * (TG_ERR_ARG), n <= 65536. Calls on one context share the workspace; they run in order on its
+ * stream. Device pointers, queued on the stream. No counterpart in the reference, whose sums are all
+ * f32. */
 int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                         const tg_weights *w, const tg_epilogue *epi, void *qa_out,
                                         size_t qa_out_len, int32_t *exps_out, size_t exps_out_len);

@@ -42,9 +42,11 @@ struct tg_ctx {
     // The product before the GLU, when tg_linear_glu_device cannot fuse them.
     float *dg = nullptr;
     size_t dg_cap = 0;
-    // The row rendezvous of the quantised-output product (tg::QuantSync), zero between launches.
-    void *qsync = nullptr;
-    size_t qsync_cap = 0;
+    // The quantised-output product's f32 rows and their per-tile row maxima, grown on demand.
+    float *hid = nullptr;
+    size_t hid_cap = 0;
+    uint32_t *tmax = nullptr;
+    size_t tmax_cap = 0;
 };
 
 struct tg_weights {
@@ -338,7 +340,7 @@ void tg_ctx_destroy(tg_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (void *p : {(void *)ctx->qa, (void *)ctx->exps, (void *)ctx->da, (void *)ctx->dc, (void *)ctx->dbias,
-                    (void *)ctx->dg, ctx->qsync})
+                    (void *)ctx->dg, (void *)ctx->hid, (void *)ctx->tmax})
         if (p) (void)hipFree(p);
     if (ctx->hst) (void)hipHostFree(ctx->hst);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -370,18 +372,6 @@ int tg_synchronize(tg_ctx *ctx) {
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
     TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->qsync) {
-        // A quantised-output product whose wait for its tile row ran out leaves its flag set (and
-        // its rendezvous state unknown): report it once and start the state over.
-        const tg::QuantSync q = tg::quant_sync_at(ctx->qsync, ctx->qsync_cap);
-        int32_t timed_out = 0;
-        TG_HIP(ctx, hipMemcpy(&timed_out, q.timeout, sizeof(timed_out), hipMemcpyDeviceToHost));
-        if (timed_out) {
-            TG_HIP(ctx, hipMemset(ctx->qsync, 0, tg::quant_sync_bytes(ctx->qsync_cap)));
-            return fail(ctx, TG_ERR_HIP, "a quantised-output product gave up waiting for its tile row; the quantised "
-                                         "rows it wrote are unusable");
-        }
-    }
     return TG_OK;
 }
 
@@ -630,20 +620,17 @@ int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_l
     if (qa == qa_out || exps == exps_out) return fail(ctx, TG_ERR_ARG, "the output must not overwrite the input");
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
-    if (m > ctx->qsync_cap) {
-        // A larger rendezvous state, zeroed before any launch reads it.
-        TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        if (ctx->qsync) TG_HIP(ctx, hipFree(ctx->qsync));
-        ctx->qsync = nullptr;
-        ctx->qsync_cap = 0;
-        const size_t bytes = tg::quant_sync_bytes(m);
-        if (hipMalloc(&ctx->qsync, bytes) != hipSuccess) return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
-        TG_HIP(ctx, hipMemset(ctx->qsync, 0, bytes));
-        ctx->qsync_cap = m;
-    }
+    // The f32 rows (row stride kb * 64, so every 16-byte load of the quantiser stays inside) and
+    // the row maxima, grown before any launch reads them; every element read is written first.
+    const size_t ldh = tg::div_ceil(n, (size_t)tg::KBLK) * tg::KBLK;
+    const int strips = tg::gemm_qout_strips(m, w->d);
+    int rc;
+    if ((rc = grow(ctx, ctx->hid, ctx->hid_cap, m * ldh * sizeof(float)))) return rc;
+    if ((rc = grow(ctx, ctx->tmax, ctx->tmax_cap, m * (size_t)strips * sizeof(uint32_t)))) return rc;
     TG_HIP(ctx, tg::launch_gemm_i8_qout(static_cast<const uint8_t *>(qa), exps, m, w->d, epi_args(epi, nullptr, false),
-                                        static_cast<uint8_t *>(qa_out), exps_out,
-                                        tg::quant_sync_at(ctx->qsync, ctx->qsync_cap), ctx->stream));
+                                        ctx->hid, ldh, ctx->tmax, ctx->stream));
+    TG_HIP(ctx, tg::launch_quantize_known(ctx->hid, ldh, m, n, ctx->tmax, strips, static_cast<uint8_t *>(qa_out),
+                                          exps_out, ctx->stream));
     clear_error(ctx);
     return TG_OK;
 }

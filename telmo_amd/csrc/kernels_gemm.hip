@@ -95,17 +95,29 @@ struct TileStore {
         }
     }
 
+    // With rmax, also each run's largest |y| over its columns below N, as unsigned bits (all ones
+    // for a NaN or an infinity; 0 for rows past M).
     __device__ __forceinline__ void finish(const float *tile, float *__restrict__ c, size_t ldc, int m0, int M, int N,
-                                           bool has_bias, uint32_t act, float escale, int accumulate) {
+                                           bool has_bias, uint32_t act, float escale, int accumulate,
+                                           uint32_t *rmax = nullptr) {
         if constexpr (!EARLY) load_old(c, ldc, m0, M, N, accumulate);
 #pragma unroll
         for (int u = 0; u < PER; u++) {
             const int row = m0 + r0 + u * STEP;
+            if (rmax) rmax[u] = 0u;
             if (row >= M) continue;
             v4f v = *reinterpret_cast<const v4f *>(tile + (r0 + u * STEP) * C_STRIDE + 4 * cr);
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 v[j] = epilogue_vals(v[j], has_bias, b[j], act, escale, accumulate != 0, old[u][j]);
+            if (rmax) {
+                uint32_t mx = 0u;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (col + j < N)
+                        mx = max(mx, __builtin_isfinite(v[j]) ? __float_as_uint(fabsf(v[j])) : 0xffffffffu);
+                rmax[u] = mx;
+            }
             float *dst = c + (size_t)row * ldc + col;
             if (vec) {
                 __builtin_nontemporal_store(v, reinterpret_cast<v4f *>(dst));
@@ -658,159 +670,14 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     }
 }
 
-// The quantised output of gemm_lds_kernel<..., QOUT = 1>: the digit layout qo (kbo k-blocks per
-// row block), the row exponents eo and the rendezvous state.
-struct QOut {
-    uint8_t *qo;
-    int32_t *eo;
-    int kbo;
-    QuantSync sync;
+// The row maxima of gemm_lds_kernel<..., QOUT = 1>: for each row and workgroup column bx, the
+// largest |y| over the workgroup's columns as unsigned bits (all ones when one of them is a NaN or
+// an infinity), at tmax[row * strips + bx]; the streaming quantiser (launch_quantize_known) takes
+// the row's exponent from them.
+struct TileMax {
+    uint32_t *tmax;
+    int strips;
 };
-
-// Polls of a tile row's arrival counter before a workgroup gives up (about 1 s of s_sleep 8).
-constexpr int QOUT_SPIN_LIMIT = 1 << 21;
-
-// The epilogue of a GEMM whose outputs go out as quantised rows (QuantSync in tg_internal.hpp). The
-// workgroup's tile is TM row blocks by TN panels (columns n0g = bx TN 16 on, contiguous); wavefront
-// (wm, wn) holds rows wm WM + [0, WM) and columns wn WN + [0, WN) of it.
-//  1. y = epi(sum) of each output, staged in LDS (zero past M or N), and each row's largest |y| bits
-//     over the wavefront's columns (16-lane reductions), then over the workgroup's (LDS);
-//  2. one fetch_max per row into sync.amax; the returned value is consumed before the barrier, so
-//     every row's max has been performed before thread 0 arrives (all atomics here are relaxed, at
-//     agent scope: no cache maintenance in the wait);
-//  3. thread 0 adds one to the tile row's arrival count and polls it until all gridDim.x column
-//     tiles have arrived. Tile rows are dispatched whole and in order (a row-major grid), so the
-//     tiles a workgroup waits for are running or done: the lowest tile row not done has every
-//     tile dispatched, the slots holding earlier-dispatched tiles being far more than a tile row;
-//  4. each row's exponent from its amax (row_exponent_of, or EXP_NONFINITE), eo from column tile 0;
-//  5. the departure count: the last workgroup of the tile row zeroes its rows' amax and both counts;
-//  6. the digits: the tile is TM row blocks by TN / 4 k-blocks of the quantised layout; slot L of a
-//     block's 64 operand lanes holds inputs 64 t + 16 (L / 16) + [0, 16) of row L % 16, read as
-//     four 16-byte LDS loads and written as one 16-byte store per digit.
-// The arithmetic per output is TileStore's (dequant then epilogue_vals), and the digits are those
-// digits4 makes of it with the row's exponent, so the result is the row quantiser's on the f32
-// outputs the plain GEMM writes.
-template <int TM, int TN, int WM, int WN, int C_STRIDE, int RB, int CB>
-__device__ __forceinline__ void qout_epilogue(float *staged, const v4i (&acc_hi)[RB][CB], const v4i (&acc_lo)[RB][CB],
-                                              const int32_t (&e_row)[RB][4], const float (&s_col)[CB], int tid,
-                                              int lane, int wave, int wm, int wn, int bx, int by, int m0, int n0,
-                                              int M, int N, const float *__restrict__ bias, uint32_t act,
-                                              float escale, const QOut &q) {
-    constexpr int ROWS = TM * 16;
-    __shared__ uint32_t row_bits[2][ROWS];
-    __shared__ int32_t row_e[ROWS];
-    __shared__ int last_s;
-    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
-    float bcol[CB];
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) {
-        const int col = n0 + cb * 16 + out_col;
-        bcol[cb] = bias && col < N ? bias[col] : 0.0f;
-    }
-    __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
-    float *tile = staged + wave * WM * C_STRIDE;
-    uint32_t rb[RB][4];
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            rb[r][v] = 0u;
-            const int row = m0 + r * 16 + out_row + v;
-#pragma unroll
-            for (int cb = 0; cb < CB; cb++) {
-                const int col = n0 + cb * 16 + out_col;
-                float y = epilogue_vals(dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]),
-                                        bias != nullptr, bcol[cb], act, escale, false, 0.0f);
-                if (row >= M || col >= N) y = 0.0f;
-                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] = y;
-                rb[r][v] = max(rb[r][v], __float_as_uint(fabsf(y)));
-            }
-        }
-    // Lanes l and l ^ 1, 2, 4, 8 hold the same rows (out_row) in other columns.
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) rb[r][v] = max(rb[r][v], (uint32_t)__shfl_xor((int)rb[r][v], off, 16));
-            if (out_col == 0) row_bits[wn][wm * WM + r * 16 + out_row + v] = rb[r][v];
-        }
-    __syncthreads();
-    const int row0 = by * ROWS;
-    for (int rr = tid; rr < ROWS; rr += THREADS) {
-        const int row = row0 + rr;
-        uint32_t seen = 0;
-        if (row < M)
-            seen = __hip_atomic_fetch_max(&q.sync.amax[row], max(row_bits[0][rr], row_bits[1][rr]), __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        row_bits[0][rr] = seen;  // consuming the returned value waits for the atomic to complete
-    }
-    __syncthreads();
-    if (tid == 0) {
-        const int ncols = (int)gridDim.x;
-        // Relaxed atomics throughout: every value read across workgroups (amax, the counts) is itself
-        // an agent-scope atomic, and this workgroup's maxima are complete before the barrier above.
-        // Acquire or release orderings would add an L2 invalidation per poll and a write-back of the
-        // L2 per arrival, under every other workgroup on the XCD.
-        __hip_atomic_fetch_add(&q.sync.arrive[by], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int polls = 0;
-        while (__hip_atomic_load(&q.sync.arrive[by], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ncols) {
-            __builtin_amdgcn_s_sleep(8);
-            if (++polls == QOUT_SPIN_LIMIT) {
-                __hip_atomic_store(q.sync.timeout, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-    for (int rr = tid; rr < ROWS; rr += THREADS) {
-        const int row = row0 + rr;
-        int32_t e = 0;
-        if (row < M) {
-            const uint32_t bits = __hip_atomic_load(&q.sync.amax[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            e = bits >= 0x7f800000u ? EXP_NONFINITE : row_exponent_of(__uint_as_float(bits));
-            if (bx == 0) q.eo[row] = e;
-        }
-        row_e[rr] = e;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        // the rows' maxima were read (atomically) and consumed before the barrier above
-        const int gone = __hip_atomic_fetch_add(&q.sync.depart[by], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_s = gone == (int)gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last_s) {
-        // Every workgroup of the tile row has read the rows' maxima: clear the state for the next launch.
-        for (int rr = tid; rr < ROWS; rr += THREADS)
-            if (row0 + rr < M) __hip_atomic_store(&q.sync.amax[row0 + rr], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (tid == 0) {
-            __hip_atomic_store(&q.sync.arrive[by], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&q.sync.depart[by], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    // The digits, block (row block by TM + i, k-block bx TN / 4 + j), operand slot L.
-    constexpr int KBT = TN / 4, SLOTS = TM * KBT * 64;
-    const int row_blocks = (M + 15) / 16;
-    for (int sl = tid; sl < SLOTS; sl += THREADS) {
-        const int blk = sl >> 6, L = sl & 63, i = blk % TM, j = blk / TM;
-        const int R = by * TM + i, t = bx * KBT + j;
-        if (R >= row_blocks || t >= q.kbo) continue;
-        const int rr = i * 16 + (L & 15), cc = j * 64 + (L >> 4) * 16;
-        const float *src = staged + ((rr / WM) + 2 * (cc / WN)) * WM * C_STRIDE + (rr % WM) * C_STRIDE + cc % WN;
-        const v4f y0 = *reinterpret_cast<const v4f *>(src), y1 = *reinterpret_cast<const v4f *>(src + 4);
-        const v4f y2 = *reinterpret_cast<const v4f *>(src + 8), y3 = *reinterpret_cast<const v4f *>(src + 12);
-        const int32_t e = row_e[rr];
-        uint4 hi, lo;
-        digits4(y0[0], y0[1], y0[2], y0[3], e, hi.x, lo.x);
-        digits4(y1[0], y1[1], y1[2], y1[3], e, hi.y, lo.y);
-        digits4(y2[0], y2[1], y2[2], y2[3], e, hi.z, lo.z);
-        digits4(y3[0], y3[1], y3[2], y3[3], e, hi.w, lo.w);
-        uint8_t *dst = q.qo + (((size_t)R * q.kbo + t) * 2) * 1024 + L * 16;
-        *reinterpret_cast<uint4 *>(dst) = hi;
-        *reinterpret_cast<uint4 *>(dst + 1024) = lo;
-    }
-}
 
 template <int TM, int TN, int NS, int XCD, int G, int GLU, int QOUT = 0>
 __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__restrict__ qf,
@@ -820,7 +687,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
                                                               float *__restrict__ c, size_t ldc,
                                                               const float *__restrict__ bias, uint32_t act,
                                                               float escale, int accumulate, size_t b_panel,
-                                                              size_t b_blk, int hp, QOut qout) {
+                                                              size_t b_blk, int hp, TileMax tmx) {
     constexpr int RB = TM / 2, CB = TN / 2;  // 16 x 16 blocks per wavefront
     constexpr int CH = 2 * TM + TN;          // 1 KB chunks per stage
     static_assert(CH % 4 == 0, "the chunks split evenly over four wavefronts");
@@ -960,13 +827,6 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
 #pragma unroll
     for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(panel_of(wn * CB + cb) * 16 + out_col, P * 16 - 1)];
-    if constexpr (QOUT) {
-        static_assert(!GLU && TN % 4 == 0 && WN % 16 == 0, "whole k-blocks of contiguous columns");
-        qout_epilogue<TM, TN, WM, WN, C_STRIDE, RB, CB>(reinterpret_cast<float *>(smem), acc_hi, acc_lo, e_row, s_col,
-                                                        tid, lane, wave, wm, wn, bx, by, m0, n0, M, N, bias, act,
-                                                        escale, qout);
-        return;
-    }
     TileStore<WM, WN, C_STRIDE> out;
     if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
@@ -980,6 +840,25 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         const float *ta = reinterpret_cast<const float *>(smem) + wm * WM * C_STRIDE + wn * (WM / 2) * C_STRIDE;
         glu_store<WM / 2, WN, C_STRIDE>(ta, ta + 2 * WM * C_STRIDE, lane, c, ldc, m0 + wn * (WM / 2), bx * WN, M,
                                         hp * 16, bias, act, escale);
+    } else if constexpr (QOUT) {
+        // The outputs as usual, and each row's largest |y| over the workgroup's columns: over the
+        // RPR lanes holding a row's runs, then over the two wavefronts of the row (LDS).
+        __shared__ uint32_t smax[2][TM * 16];
+        constexpr int PER = TileStore<WM, WN, C_STRIDE>::PER, RPR = TileStore<WM, WN, C_STRIDE>::RPR,
+                      STEP = TileStore<WM, WN, C_STRIDE>::STEP;
+        uint32_t rmax[PER];
+        out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate, rmax);
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+#pragma unroll
+            for (int off = 1; off < RPR; off <<= 1) rmax[u] = max(rmax[u], (uint32_t)__shfl_xor((int)rmax[u], off, 64));
+            if (lane % RPR == 0) smax[wn][wm * WM + lane / RPR + u * STEP] = rmax[u];
+        }
+        __syncthreads();
+        for (int rr = tid; rr < TM * 16; rr += THREADS) {
+            const int row = by * TM * 16 + rr;
+            if (row < M) tmx.tmax[(size_t)row * tmx.strips + bx] = max(smax[0][rr], smax[1][rr]);
+        }
     } else {
         out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
     }
@@ -987,8 +866,8 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
 
 template <int TM, int TN, int NS, int XCD, int G, int GLU = 0, int QOUT = 0>
 hipError_t launch_lds(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
-                      const EpiArgs &epi, hipStream_t s, const QOut &q = QOut{}) {
-    static_assert(!QOUT || (XCD == 0 && G == 0), "the quantised output needs tile rows dispatched whole, in order");
+                      const EpiArgs &epi, hipStream_t s, const TileMax &q = TileMax{}) {
+    static_assert(!QOUT || !GLU, "row maxima of plain products");
     // GLU: a workgroup column covers TN / 2 panels of each half (the launcher checks that they
     // divide the half's panels).
     const size_t hp = w.panels / 2, cols = GLU ? hp / (TN / 2) : div_ceil(w.panels, (size_t)TN);
@@ -1031,36 +910,19 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 
-size_t quant_sync_bytes(size_t m) {
-    const size_t rows = div_ceil(m, (size_t)16) * 16, blocks = div_ceil(m, (size_t)16);
-    return (rows + 2 * blocks + 1) * 4;
+// The product's f32 outputs and their row maxima per workgroup column (TileMax), on the tiles
+// launch_gemm_i8 would pick: 128 x 128 when they fill the chip twice over, else 64 x 64.
+int gemm_qout_strips(size_t m, const DeviceWeights &w) {
+    return (int)div_ceil(w.panels, (size_t)(gemm_tile_choice(m, w.panels) == 0 ? 8 : 4));
 }
 
-QuantSync quant_sync_at(void *base, size_t m) {
-    const size_t rows = div_ceil(m, (size_t)16) * 16, blocks = div_ceil(m, (size_t)16);
-    uint32_t *p = static_cast<uint32_t *>(base);
-    QuantSync q;
-    q.amax = p;
-    q.arrive = reinterpret_cast<int32_t *>(p + rows);
-    q.depart = q.arrive + blocks;
-    q.timeout = q.depart + blocks;
-    return q;
-}
-
-// The product with its outputs quantised (QuantSync): 128 x 128 tiles when they fill the chip twice
-// over, else 64 x 64, both walked in row-major order so that tile rows are dispatched whole.
 hipError_t launch_gemm_i8_qout(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w,
-                               const EpiArgs &epi, uint8_t *qa_out, int32_t *exps_out, const QuantSync &sync,
-                               hipStream_t s) {
+                               const EpiArgs &epi, float *h, size_t ldh, uint32_t *tmax, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
     if (w.precision != INT8 || epi.accumulate) return hipErrorInvalidValue;
-    QOut q;
-    q.qo = qa_out;
-    q.eo = exps_out;
-    q.kbo = (int)div_ceil(w.n, (size_t)KBLK);
-    q.sync = sync;
-    if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 0, 0, 0, 1>(qf, exps, m, w, nullptr, 0, epi, s, q);
-    return launch_lds<4, 4, 3, 0, 0, 0, 1>(qf, exps, m, w, nullptr, 0, epi, s, q);
+    const TileMax q{tmax, gemm_qout_strips(m, w)};
+    if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0, 0, 1>(qf, exps, m, w, h, ldh, epi, s, q);
+    return launch_lds<4, 4, 3, 0, 4, 0, 1>(qf, exps, m, w, h, ldh, epi, s, q);
 }
 
 // The GLU-fused product: 128 x 128 tiles (four panels of each half) when they fill the chip twice

@@ -176,6 +176,69 @@ hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, 
     return hipGetLastError();
 }
 
+// The row quantiser for rows whose largest magnitudes are known already: h holds m rows of n f32
+// values (row stride ldh, a multiple of 64, 16-byte aligned rows; values past n are ignored), and
+// tmax the largest |value| of each row over strips column ranges as unsigned bits, all ones for a
+// range holding a NaN or an infinity (tmax[row * strips + s], as gemm_lds_kernel<..., QOUT = 1>
+// leaves them). Workgroup (R, y) takes 16-row block R and k-blocks QK_CH y .. QK_CH y + QK_CH - 1.
+// Thread (r = tid / 16, c = tid % 16) folds row r's maxima c, c + 16, ... over its 16 lanes into the
+// row exponent, the one quantize_rows_regs_kernel computes from the values, then writes the digits
+// of inputs 64 t + 4 c + [0, 4) as one hi and one lo dword at operand lane 16 (c / 4) + r, bytes
+// 4 (c % 4), so that each k-block's 2 KB of digits of the block's 16 rows goes out as one
+// contiguous run, and every input is read once with a 16-byte load. Inputs past n and rows past m
+// get zero digits.
+constexpr int QK_CH = 4;
+
+__global__ __launch_bounds__(256) void quantize_known_kernel(const float *__restrict__ h, size_t ldh, size_t m, int n,
+                                                             int kb, const uint32_t *__restrict__ tmax, int strips,
+                                                             uint8_t *__restrict__ qa, int32_t *__restrict__ exps) {
+    const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+    const size_t R = blockIdx.x, row = R * 16 + r;
+    const int t0 = blockIdx.y * QK_CH;
+    const bool valid = row < m;
+    const float *hr = h + (valid ? row : 0) * ldh;
+    float4 v[QK_CH];
+#pragma unroll
+    for (int j = 0; j < QK_CH; j++) {
+        const int i0 = (t0 + j) * KBLK + 4 * c;
+        v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (valid && t0 + j < kb) {
+            const float4 x = *reinterpret_cast<const float4 *>(hr + i0);
+            v[j].x = i0 < n ? x.x : 0.0f;
+            v[j].y = i0 + 1 < n ? x.y : 0.0f;
+            v[j].z = i0 + 2 < n ? x.z : 0.0f;
+            v[j].w = i0 + 3 < n ? x.w : 0.0f;
+        }
+    }
+    uint32_t mx = 0u;
+    if (valid)
+        for (int st = c; st < strips; st += 16) mx = max(mx, tmax[row * (size_t)strips + st]);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 16));
+    const int32_t e = !valid ? 0 : (mx >= 0x7f800000u ? EXP_NONFINITE : row_exponent_of(__uint_as_float(mx)));
+    if (valid && blockIdx.y == 0 && c == 0) exps[row] = e;
+#pragma unroll
+    for (int j = 0; j < QK_CH; j++) {
+        const int t = t0 + j;
+        if (t >= kb) break;
+        uint32_t hi = 0u, lo = 0u;
+        if (valid) digits4(v[j].x, v[j].y, v[j].z, v[j].w, e, hi, lo);
+        uint8_t *blk = qa + ((R * kb + t) * 2) * 1024 + (16 * (c >> 2) + r) * 16 + 4 * (c & 3);
+        *reinterpret_cast<uint32_t *>(blk) = hi;
+        *reinterpret_cast<uint32_t *>(blk + 1024) = lo;
+    }
+}
+
+hipError_t launch_quantize_known(const float *h, size_t ldh, size_t m, size_t n, const uint32_t *tmax, int strips,
+                                 uint8_t *qa, int32_t *exps, hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    const size_t kb = div_ceil(n, KBLK);
+    if (ldh % KBLK != 0 || ldh < kb * KBLK || reinterpret_cast<uintptr_t>(h) % 16 != 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)div_ceil(m, (size_t)16), (unsigned)div_ceil(kb, (size_t)QK_CH));
+    hipLaunchKernelGGL(quantize_known_kernel, grid, dim3(256), 0, s, h, ldh, m, (int)n, (int)kb, tmax, strips, qa, exps);
+    return hipGetLastError();
+}
+
 // out = a * sigmoid(b) as the reference's SIMD glu computes it: a / (1 + exp(0 - b))
 // (src/kernels/avx512.rs:410-430).
 __global__ __launch_bounds__(256) void glu_kernel(const float *__restrict__ x, size_t ldx, size_t m, size_t half,

@@ -205,26 +205,18 @@ bool gemm_glu_fits(size_t n);
 hipError_t launch_gemm_i8_glu(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *out,
                               size_t ldo, const EpiArgs &epi, hipStream_t s);
 
-// A GEMM that writes its outputs y = epi(sum) as quantised rows (the layout and exponents the row
-// quantiser writes) instead of f32: each workgroup folds its tile's per-row largest |y| into amax
-// (bits of |y| as unsigned integers, so a NaN or an infinity is above every finite value), arrives
-// at its tile row's counter, waits until every column tile of that row has arrived, reads the rows'
-// exponents and writes its digits. The last workgroup of a tile row to leave zeroes the row's state,
-// so it is all zero between launches (set so at allocation). A wait that runs past its bound sets
-// *timeout and gives up; the digits of that launch are then unusable.
-struct QuantSync {
-    uint32_t *amax;   // [rows], padded to whole 16-row blocks
-    int32_t *arrive;  // [16-row blocks]
-    int32_t *depart;  // [16-row blocks]
-    int32_t *timeout; // [1]
-};
-// Bytes of the state for up to m rows (amax, arrive, depart, timeout, in that order).
-size_t quant_sync_bytes(size_t m);
-QuantSync quant_sync_at(void *base, size_t m);
+// The FFN hidden rows' quantisation in two launches, bit-identical to the product into f32 rows
+// followed by the row quantiser: the GEMM writes its outputs y = epi(sum) into h (row stride ldh)
+// and, per row and workgroup column, the largest |y| as unsigned bits (all ones for a NaN or an
+// infinity) into tmax[row * strips + column], strips = gemm_qout_strips(m, w); then the streaming
+// quantiser turns h into the digit layout and row exponents, each row's exponent from its maxima.
 // int8 weights, fast mode, no accumulation (epi.accumulate must be 0); m >= 1.
+int gemm_qout_strips(size_t m, const DeviceWeights &w);
 hipError_t launch_gemm_i8_qout(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w,
-                               const EpiArgs &epi, uint8_t *qa_out, int32_t *exps_out, const QuantSync &sync,
-                               hipStream_t s);
+                               const EpiArgs &epi, float *h, size_t ldh, uint32_t *tmax, hipStream_t s);
+// h: ldh a multiple of 64 and at least n rounded up to 64, 16-byte aligned.
+hipError_t launch_quantize_known(const float *h, size_t ldh, size_t m, size_t n, const uint32_t *tmax, int strips,
+                                 uint8_t *qa, int32_t *exps, hipStream_t s);
 
 // The decode GEMVs (quantise the rows themselves; int8 and Q8_0 weights): the MFMA GEMV for
 // m <= 16 rows of k <= 1984 inputs (m * ceil(k / 256) <= 64; 16-byte aligned rows, k % 4 == 0),

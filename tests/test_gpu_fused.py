@@ -5,7 +5,7 @@ MI355X: each must write exactly the bytes of the calls it replaces.
   and the f32 LayerNorm when asked for, in place too);
 * tg_matmul_quantized_to_quant_device = tg_matmul_quantized_device into f32 rows then
   tg_quantize_rows_device, for every launch of a sequence and every replay of a captured graph (its
-  row rendezvous state must come back to zero by itself).
+  workspace of f32 rows and row maxima is rewritten by every launch).
 """
 import numpy as np
 import pytest
@@ -104,7 +104,7 @@ def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, wit
     c = torch.zeros((m, n), device="cuda")
     tk.matmul_quantized_device(qa, ex, m, w, c, n, epi)
     want_qa, want_ex = quantised(tk, c, n, m, n)
-    for rep in range(3):  # the rendezvous state must be clean for every launch
+    for rep in range(3):  # every launch rewrites the workspace it reads
         got_qa = torch.zeros_like(want_qa)
         got_ex = torch.zeros_like(want_ex)
         tk.matmul_quantized_to_quant_device(qa, ex, m, w, got_qa, got_ex, epi)
