@@ -56,12 +56,13 @@ class ConformerLayer:
     """Parakeet::layer on the device for up to `rows` frames of width d (ff hidden), on one context."""
 
     def __init__(self, kern: Kernels, d: int, ff: int, conv_kernel: int, rows: int, eps: float = 1e-5,
-                 quantised_hidden: bool = False):
+                 quantised_hidden: bool = True):
         import torch
 
         self.kern, self.d, self.ff, self.conv_kernel, self.rows, self.eps = kern, d, ff, conv_kernel, rows, eps
-        # FF in writes its hidden rows quantised (tg_matmul_quantized_to_quant_device) when set, else
-        # in f32 followed by the row quantiser: the same bits either way.
+        # FF in writes its hidden rows quantised (tg_matmul_quantized_to_quant_device) when set (as
+        # fast at 750 rows, 7% faster from 3000), else in f32 followed by the row quantiser: the same
+        # bits either way.
         self.quantised_hidden = quantised_hidden
         dev = "cuda"
         u8 = lambda n: torch.empty(n, dtype=torch.uint8, device=dev)  # noqa: E731

@@ -599,6 +599,10 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
     return TG_OK;
 }
 
+// Rows from which the quantised-output product leaves its activation to the quantiser (measured:
+// 212 against 228 us at 12000 x 1024 -> 4096 with SiLU, 25.4 against 23.9 us at 750 rows).
+constexpr size_t QOUT_ACT_ROWS = 2048;
+
 int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                         const tg_weights *w, const tg_epilogue *epi, void *qa_out,
                                         size_t qa_out_len, int32_t *exps_out, size_t exps_out_len) {
@@ -624,13 +628,26 @@ int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_l
     // the row maxima, grown before any launch reads them; every element read is written first.
     const size_t ldh = tg::div_ceil(n, (size_t)tg::KBLK) * tg::KBLK;
     const int strips = tg::gemm_qout_strips(m, w->d);
+    const tg::EpiArgs ea = epi_args(epi, nullptr, false);
     int rc;
     if ((rc = grow(ctx, ctx->hid, ctx->hid_cap, m * ldh * sizeof(float)))) return rc;
-    if ((rc = grow(ctx, ctx->tmax, ctx->tmax_cap, m * (size_t)strips * sizeof(uint32_t)))) return rc;
-    TG_HIP(ctx, tg::launch_gemm_i8_qout(static_cast<const uint8_t *>(qa), exps, m, w->d, epi_args(epi, nullptr, false),
-                                        ctx->hid, ldh, ctx->tmax, ctx->stream));
-    TG_HIP(ctx, tg::launch_quantize_known(ctx->hid, ldh, m, n, ctx->tmax, strips, static_cast<uint8_t *>(qa_out),
-                                          exps_out, ctx->stream));
+    if ((ea.act != tg::ACT_NONE || ea.scale != 1.0f) && m >= QOUT_ACT_ROWS) {
+        // The activation and the scale are VALU work that the product's epilogue adds to its MFMA
+        // loop, where it is not hidden at this many rows; the quantiser applies them to each input
+        // as it loads it (the same f32 operations on the same values), under its HBM time, and the
+        // product writes only the biased sums.
+        const tg::EpiArgs biased{ea.bias, tg::ACT_NONE, 1.0f, 0};
+        TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, ctx->hid, ldh, biased,
+                                       ctx->stream));
+        TG_HIP(ctx, tg::launch_quantize_rows(ctx->hid, ldh, m, n, static_cast<uint8_t *>(qa_out), exps_out,
+                                             ctx->stream, tg::RowAct{ea.act, ea.scale}));
+    } else {
+        if ((rc = grow(ctx, ctx->tmax, ctx->tmax_cap, m * (size_t)strips * sizeof(uint32_t)))) return rc;
+        TG_HIP(ctx, tg::launch_gemm_i8_qout(static_cast<const uint8_t *>(qa), exps, m, w->d, ea, ctx->hid, ldh,
+                                            ctx->tmax, ctx->stream));
+        TG_HIP(ctx, tg::launch_quantize_known(ctx->hid, ldh, m, n, ctx->tmax, strips, static_cast<uint8_t *>(qa_out),
+                                              exps_out, ctx->stream));
+    }
     clear_error(ctx);
     return TG_OK;
 }

@@ -53,11 +53,12 @@ __device__ __forceinline__ int wave_or(int v) {
 // One wavefront per row: the largest magnitude (and any NaN or infinity) over the row's k
 // inputs, the row exponent, then the digits of each input into the fragment-major QA.
 __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ ar, size_t k, size_t kb,
-                                                     uint8_t *__restrict__ qa, size_t row, int lane) {
+                                                     uint8_t *__restrict__ qa, size_t row, int lane,
+                                                     const RowAct &f) {
     float amax = 0.0f;
     int bad = 0;
     for (size_t i = lane; i < k; i += 64) {
-        float x = ar[i];
+        float x = f(ar[i]);
         bad |= !__builtin_isfinite(x);
         amax = fmaxf(amax, fabsf(x));
     }
@@ -67,7 +68,7 @@ __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ a
     for (size_t t = 0; t < kb; t++) {
         const size_t i = t * KBLK + lane;
         int8_t hi = 0, lo = 0;
-        if (i < k) digits_of(ar[i], e, hi, lo);
+        if (i < k) digits_of(f(ar[i]), e, hi, lo);
         const size_t at = qa_offset(row, t, 0, kb) + (lane >> 4) * 256 + (lane & 15);
         qa[at] = (uint8_t)hi;
         qa[at + 1024] = (uint8_t)lo;
@@ -77,11 +78,11 @@ __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ a
 
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restrict__ a, size_t lda, size_t m,
                                                             size_t k, size_t kb, uint8_t *__restrict__ qa,
-                                                            int32_t *__restrict__ exps) {
+                                                            int32_t *__restrict__ exps, RowAct f) {
     const int lane = threadIdx.x & 63;
     const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= m) return;
-    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa, row, lane);
+    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa, row, lane, f);
     if (lane == 0) exps[row] = e;
 }
 
@@ -98,7 +99,7 @@ template <int J>
 __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__restrict__ a, size_t lda, int k,
                                                                  int kb, uint8_t *__restrict__ qa,
                                                                  int32_t *__restrict__ exps, int vec, size_t m,
-                                                                 size_t bpx) {
+                                                                 size_t bpx, RowAct f) {
     __shared__ float s_max[4];
     __shared__ int s_bad[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -119,6 +120,12 @@ __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__
             v[j].y = k0 + 1 < k ? ar[k0 + 1] : 0.0f;
             v[j].z = k0 + 2 < k ? ar[k0 + 2] : 0.0f;
             v[j].w = k0 + 3 < k ? ar[k0 + 3] : 0.0f;
+        }
+        if (f.act != ACT_NONE || f.scale != 1.0f) {
+            if (k0 < k) v[j].x = f(v[j].x);
+            if (k0 + 1 < k) v[j].y = f(v[j].y);
+            if (k0 + 2 < k) v[j].z = f(v[j].z);
+            if (k0 + 3 < k) v[j].w = f(v[j].w);
         }
         bad |= !__builtin_isfinite(v[j].x) | !__builtin_isfinite(v[j].y) | !__builtin_isfinite(v[j].z) |
                !__builtin_isfinite(v[j].w);
@@ -152,27 +159,27 @@ __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__
 
 template <int J>
 void launch_regs(const float *a, size_t lda, size_t m, size_t k, size_t kb, uint8_t *qa, int32_t *exps, int vec,
-                 hipStream_t s) {
+                 const RowAct &f, hipStream_t s) {
     const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
     hipLaunchKernelGGL(quantize_rows_regs_kernel<J>, dim3((unsigned)(8 * bpx * 16)), dim3(256), 0, s, a, lda, (int)k,
-                       (int)kb, qa, exps, vec, m, bpx);
+                       (int)kb, qa, exps, vec, m, bpx, f);
 }
 
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
-                                hipStream_t s) {
+                                hipStream_t s, RowAct f) {
     if (m == 0) return hipSuccess;
     const size_t kb = div_ceil(k, KBLK);
     // 16-byte loads need every row 16-byte aligned.
     const int vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (lda % 4 == 0);
     const size_t j = div_ceil(kb * 16, 256);  // 4-input chunks per thread
-    if (j <= 1) launch_regs<1>(a, lda, m, k, kb, qa, exps, vec, s);
-    else if (j <= 2) launch_regs<2>(a, lda, m, k, kb, qa, exps, vec, s);
-    else if (j <= 4) launch_regs<4>(a, lda, m, k, kb, qa, exps, vec, s);
-    else if (j <= 8) launch_regs<8>(a, lda, m, k, kb, qa, exps, vec, s);
-    else if (j <= 16) launch_regs<16>(a, lda, m, k, kb, qa, exps, vec, s);
+    if (j <= 1) launch_regs<1>(a, lda, m, k, kb, qa, exps, vec, f, s);
+    else if (j <= 2) launch_regs<2>(a, lda, m, k, kb, qa, exps, vec, f, s);
+    else if (j <= 4) launch_regs<4>(a, lda, m, k, kb, qa, exps, vec, f, s);
+    else if (j <= 8) launch_regs<8>(a, lda, m, k, kb, qa, exps, vec, f, s);
+    else if (j <= 16) launch_regs<16>(a, lda, m, k, kb, qa, exps, vec, f, s);
     else
         hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)div_ceil(m, 4)), dim3(256), 0, s, a, lda, m, k, kb,
-                           qa, exps);
+                           qa, exps, f);
     return hipGetLastError();
 }
 

@@ -176,9 +176,19 @@ struct EpiArgs {
 // Re-lays int8 / Q8_0 panel values (device, telmo's layout) into w's MFMA layout.
 hipError_t launch_repack_i8(const uint8_t *src, const DeviceWeights &w, hipStream_t s);
 
-// Per-row digits and exponents of a[m][lda] (k inputs) into qa (fragment-major) / exps.
+// The map the row quantiser applies to each input before quantising it: the activation, then the
+// scale (the order of epilogue_vals without bias and accumulation). The identity by default.
+struct RowAct {
+    uint32_t act = ACT_NONE;
+    float scale = 1.0f;
+    __device__ __forceinline__ float operator()(float v) const {
+        return epilogue_vals(v, false, 0.0f, act, scale, false, 0.0f);
+    }
+};
+
+// Per-row digits and exponents of f(a[m][lda]) (k inputs) into qa (fragment-major) / exps.
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
-                                hipStream_t s);
+                                hipStream_t s, RowAct f = RowAct{});
 
 // out[r][j] = x[r][j] * sigmoid(x[r][half + j]).
 hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s);

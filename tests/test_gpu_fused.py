@@ -77,14 +77,18 @@ def test_layer_norm_quant_is_layer_norm_then_quantise(tk, m, n, ldx):
     assert torch.equal(qa2, want_qa)
 
 
-QOUT_CASES = [  # m, k, n, act, with_bias
-    (750, 1024, 4096, 2, False), (12000, 1024, 4096, 2, False), (7500, 1024, 4096, 2, False),
-    (37, 200, 130, 0, True), (130, 64, 200, 1, True), (1, 100, 64, 2, False), (300, 1000, 1000, 1, True),
-    (5000, 256, 100, 0, False), (2100, 640, 4100, 2, True), (64, 4096, 1024, 0, False)]
+# m, k, n, act, with_bias, scale. An activation or a scale other than 1 is applied by the quantiser as
+# it loads the product's biased sums; the identity map takes the row maxima from the product.
+QOUT_CASES = [
+    (750, 1024, 4096, 2, False, 1.0), (12000, 1024, 4096, 2, False, 1.0), (7500, 1024, 4096, 2, False, 0.75),
+    (750, 1024, 4096, 0, True, 1.0), (12000, 1024, 4096, 0, False, 1.0),
+    (37, 200, 130, 0, True, 0.75), (37, 200, 130, 0, True, 1.0), (130, 64, 200, 1, True, 0.75),
+    (1, 100, 64, 2, False, -2.0), (300, 1000, 1000, 1, True, 1.0), (5000, 256, 100, 0, False, 1.0),
+    (2100, 640, 4100, 2, True, 0.75), (64, 4096, 1024, 0, False, 1.0), (5, 64, 17000, 2, True, 1.0)]
 
 
-@pytest.mark.parametrize("m,k,n,act,with_bias", QOUT_CASES)
-def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, with_bias):
+@pytest.mark.parametrize("m,k,n,act,with_bias,scale", QOUT_CASES)
+def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, with_bias, scale):
     import torch
 
     import telmo_amd
@@ -97,8 +101,8 @@ def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, wit
     values, scales = pack_int8(q, s)
     w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
     bias = torch.from_numpy(normal(rng, n)).cuda() if with_bias else None
-    epi = telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act(act), scale=0.75)
-    say("qout", m, k, n, act, with_bias)
+    epi = telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act(act), scale=scale)
+    say("qout", m, k, n, act, with_bias, scale)
     ad = torch.from_numpy(a).cuda()
     qa, ex = quantised(tk, ad, k, m, k)
     c = torch.zeros((m, n), device="cuda")
