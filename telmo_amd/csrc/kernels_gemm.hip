@@ -710,6 +710,20 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         return P0 + cc;
     };
 
+    // The epilogue's row exponents and column scales, one per thread, loaded before the k-loop so
+    // that their latency passes under it, and handed over through LDS after it. Rows and columns
+    // past the edge read the last valid one and are never stored.
+    constexpr int NPRE = TM * 16 + TN * 16;
+    static_assert(NPRE <= THREADS, "one exponent or scale per thread");
+    __shared__ uint32_t s_pre[NPRE];
+    uint32_t pre = 0u;
+    if (tid < TM * 16) {
+        pre = (uint32_t)exps[min(by * TM * 16 + tid, M - 1)];
+    } else if (tid < NPRE) {
+        const int j = tid - TM * 16;
+        pre = __float_as_uint(scales[min(panel_of(j >> 4) * 16 + (j & 15), P * 16 - 1)]);
+    }
+
     // This wavefront's copies: chunk ch = wave + 4 i is row block R0 + ch / 2, digit ch % 2 when
     // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one.
     const uint8_t *g[CPW];
@@ -817,19 +831,18 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
 #undef TG_ISSUE
 #undef TG_MMA
 #undef TG_MMA_ROWS
-    // Row exponents and column scales are loaded after the k-loop, which leaves their registers
-    // to the operand fragments.
+    if (tid < NPRE) s_pre[tid] = pre;
+    TileStore<WM, WN, C_STRIDE> out;
+    if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
     int32_t e_row[RB][4];
     float s_col[CB];
 #pragma unroll
     for (int r = 0; r < RB; r++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
+        for (int v = 0; v < 4; v++) e_row[r][v] = (int32_t)s_pre[wm * WM + r * 16 + out_row + v];
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(panel_of(wn * CB + cb) * 16 + out_col, P * 16 - 1)];
-    TileStore<WM, WN, C_STRIDE> out;
-    if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
-    __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
+    for (int cb = 0; cb < CB; cb++) s_col[cb] = __uint_as_float(s_pre[TM * 16 + (wn * CB + cb) * 16 + out_col]);
 
     float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
     stage_sums<RB, CB, C_STRIDE>(tile, acc_hi, acc_lo, e_row, s_col, out_row, out_col);
