@@ -30,6 +30,8 @@ The JSON line also carries:
   encoder       24 layers at M = 12000 (32 utterances of 30 s) and M = 7500 (one 600 s utterance):
                 audio-seconds per second.
   gemv, tdt     the decoder's GEMVs on the HBM roofline and the greedy TDT decode.
+  vendor        the same product shapes on hipBLASLt (int8 over both digit planes: the same MFMA work)
+                and torch's bf16 / f16 GEMMs, for scale.
   cpu_baseline  the C++ port of telmo's SIMD tile + thread pool (oracle/cpu_baseline.cpp,
                 bit-identical to the fused oracle) on the host's cores, on the same bytes.
 """
@@ -275,6 +277,9 @@ def gpu_leg(args, params, x0_host):
                                                                                        qa_o, ex_o, silu),
         "dwconv1d + SiLU": lambda i: kern.dwconv1d_device(glu, D, T, D, w.dw_w, DW_KERNEL, w.dw_b, dw_out, D,
                                                           act=Act.SILU),
+        "dwconv1d + SiLU, quantised output": lambda i: kern.dwconv1d_quant_device(glu, D, T, D, w.dw_w, DW_KERNEL,
+                                                                                  w.dw_b, qa_d, ex_d, act=Act.SILU),
+        "quantize_rows (conv output)": lambda i: kern.quantize_rows_device(dw_out, D, T, D, qa_d, ex_d),
         "layer_norm (in place)": lambda i: kern.layer_norm_device(dw_out, D, T, D, g, b, 1e-5, dw_out, D),
     }
     row_us = {}
@@ -791,6 +796,65 @@ def shape_leg(m, k, n, reps):
             "tops": round(2 * m * n * k / us / 1e6, 1)}
 
 
+VENDOR_SHAPES = [(750, 1024, 4096), (750, 4096, 1024), (750, 1024, 1024), (12000, 1024, 4096), (12000, 4096, 1024),
+                 (12000, 1024, 1024)]
+
+
+def vendor_leg(reps=20):
+    """The same products on the vendor library, for scale. For each shape: this library's product on
+    quantised rows (tg_matmul_quantized_device, f32 out), hipBLASLt's int8 GEMM through
+    torch._int_mm on both digit planes stacked (2m x k int8 times k x n int8, int32 out: the same
+    MFMA work as the two-digit product, without its dequantisation), on one digit plane (m rows:
+    a plain int8 GEMM, which misses the 1e-3 gate) and torch's bf16 and f16 GEMMs (m x k times
+    k x n). All timed with HIP events over `reps` launches after 3 untimed ones."""
+    import torch
+
+    import telmo_amd
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+
+    def us_of(fn):
+        for _ in range(3):
+            fn(0)
+        return timed_on(stream, fn, reps) * 1e3
+
+    out = []
+    for m, k, n in VENDOR_SHAPES:
+        values, scales = panel_layout(synth_int8(n, k, 1), synth_scales(n, 2))
+        w = telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, values, scales)
+        a = torch.from_numpy(synth_normal((m, k), 3)).cuda()
+        qa = torch.empty(kern.quant_bytes(m, k), dtype=torch.uint8, device="cuda")
+        exps = torch.empty(m, dtype=torch.int32, device="cuda")
+        c = torch.empty((m, n), device="cuda")
+        kern.quantize_rows_device(a, k, m, k, qa, exps)
+        ours = us_of(lambda i: kern.matmul_quantized_device(qa, exps, m, w, c, n))
+        w.close()
+        del qa, exps, c
+        a8 = torch.randint(-127, 128, (2 * m, k), dtype=torch.int8, device="cuda")
+        b8 = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda").t()
+        two = us_of(lambda i: torch._int_mm(a8, b8))
+        one = us_of(lambda i: torch._int_mm(a8[:m], b8))
+        del a8, b8
+        row = {"shape": [m, k, n], "ours_us": round(ours, 2), "hipblaslt_int8_two_planes_us": round(two, 2),
+               "hipblaslt_int8_one_plane_us": round(one, 2)}
+        for name, dt in (("torch_bf16_us", torch.bfloat16), ("torch_f16_us", torch.float16)):
+            x = a.to(dt)
+            y = torch.randn(k, n, dtype=dt, device="cuda")
+            row[name] = round(us_of(lambda i: x @ y), 2)
+            del x, y
+        row["ours_vs_hipblaslt_two_planes"] = round(two / ours, 3)
+        out.append(row)
+        del a
+    kern.close()
+    torch.cuda.synchronize()
+    return {"note": "vendor GEMMs on the same shapes: hipBLASLt int8 over both digit planes is the two-digit "
+                    "product's MFMA work (int32 out, no epilogue); bf16 misses the 1e-3 gate, f16 passes it "
+                    "without exact integer sums",
+            "shapes": out}
+
+
 def gemv_shape_leg(m, k, n, reps):
     """One decode GEMV shape alone (tg_matmul_device on m rows of k inputs, the GEMV path), the
     program rocprofv3 runs for the GEMV's kernel statistics and HBM byte counters: `reps` eager
@@ -841,6 +905,7 @@ def main():
     ap.add_argument("--no-encoder", action="store_true")
     ap.add_argument("--no-q8", action="store_true")
     ap.add_argument("--no-tdt", action="store_true")
+    ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--shape", type=int, nargs=3, metavar=("M", "K", "N"),
                     help="time one product shape alone (the program for per-shape rocprofv3 runs) and exit")
     ap.add_argument("--gemv", type=int, nargs=3, metavar=("M", "K", "N"),
@@ -887,6 +952,7 @@ def main():
         net = tdt_network()
         enc = synth_normal((T_FRAMES, TDT_H), 22)
         tdt, gpu_toks = tdt_leg(args, net, enc)
+    vendor = None if args.no_vendor else vendor_leg()
     cpu = None if args.no_cpu else cpu_leg(params, x0, args.cpu_seconds)
     if cpu is not None and tdt is not None:
         cpu["tdt_decode"], port_toks, oracle_toks = cpu_tdt(net, enc, 150)
@@ -916,6 +982,7 @@ def main():
         "encoder": encoder,
         "q8_0": q8,
         "tdt": tdt,
+        "vendor": vendor,
     }
     print(json.dumps(line))
 

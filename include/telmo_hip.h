@@ -252,6 +252,20 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, si
                        size_t bias_len, size_t t0, size_t stride, size_t rows, uint32_t act, float *out,
                        size_t out_len, size_t ldo);
 
+/* The conv module's depthwise convolution + SiLU whose output only the next pointwise product reads
+ * (Parakeet::layer, src/parakeet.rs:1105-1134: dwconv1d_frame for every frame, silu, then
+ * conv_pw2): tg_dwconv1d_device over whole sequences (t0 = 0, stride = 1, rows = frames) whose
+ * output rows are written quantised, qa and exps holding exactly what tg_quantize_rows_device
+ * writes for those rows (k = channels), ready for tg_matmul_quantized_device. out (nullable) also
+ * receives the f32 rows. Sequences are stacked along the rows (batch of them, frames rows each);
+ * qa_len >= tg_quant_bytes(batch * frames, channels), exps_len >= batch * frames. channels 1 ..
+ * 2048 and kernel 1 .. 32, else TG_ERR_UNSUPPORTED (the caller then makes the two calls). No
+ * reference counterpart of its own: the fusion of two calls the reference makes in a row. */
+int tg_dwconv1d_quant_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t frames, size_t batch,
+                             size_t channels, const float *w, size_t w_len, size_t kernel, const float *bias,
+                             size_t bias_len, uint32_t act, float *out, size_t out_len, size_t ldo, void *qa,
+                             size_t qa_len, int32_t *exps, size_t exps_len);
+
 /* ---- the TDT decoder (src/parakeet.rs:1412-1577) --------------------------------------------
  * Parakeet's prediction network (embedding, LSTM layers, projection) and joint, decoded greedily
  * with every step on the device. The matrices are tg_weights of int8 or Q8_0 values. The network

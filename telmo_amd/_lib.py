@@ -60,6 +60,8 @@ SIGNATURES = {
                                                    _sz, _sz, _p, _sz, _p, _sz]),
     "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p, _sz, _sz, _sz, _sz,
                                            _u32, _p, _sz, _sz]),
+    "tg_dwconv1d_quant_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p, _sz, _u32, _p,
+                                                 _sz, _sz, _p, _sz, _p, _sz]),
     "tg_tdt_create": (ctypes.c_int, [_p, _p, ctypes.POINTER(_p)]),
     "tg_tdt_destroy": (None, [_p]),
     "tg_tdt_max_rows": (_sz, [_p]),

@@ -16,8 +16,9 @@ quantised wherever the product is their only reader:
           out, x += .                                          tg_matmul_device (quantises att)
     conv  LayerNorm(norm_conv)      -> quantised rows
           pw1 + GLU                 -> f32                     tg_matmul_quantized_glu_device
-          depthwise conv + SiLU     -> f32 (each utterance on its own)
-          pw2, x += .                                          tg_matmul_device
+          depthwise conv + SiLU     -> quantised rows (each       tg_dwconv1d_quant_device
+                                       utterance on its own)
+          pw2, x += .                                          tg_matmul_quantized_device
     FF2   as FF1 with norm_ff2, ff2_in, ff2_out
     out   LayerNorm(norm_out), in place
 
@@ -136,9 +137,15 @@ class ConformerLayer:
             g2 = self._rows("pw1", 2 * d)[:t]
             k.matmul_quantized_device(self.qa_d, self.ex_d, t, m["pw1"], g2, 2 * d)
             k.glu_device(g2, 2 * d, t, d, self.glu, d, out_len=t * d)
-        k.dwconv1d_device(self.glu, d, t // utterances, d, w.dw_w, self.conv_kernel, w.dw_b, self.conv, d,
-                          act=Act.SILU, batch=utterances, x_len=t * d, out_len=t * d)
-        k.linear_device(self.conv[:t], t, m["pw2"], x, acc)
+        # the convolution writes its rows quantised for pw2 when the fused kernel takes the shape
+        if m["pw2"].precision() in (Precision.INT8, Precision.Q8_0) and k.dwconv1d_quant_device(
+                self.glu, d, t // utterances, d, w.dw_w, self.conv_kernel, w.dw_b, self.qa_d, self.ex_d,
+                act=Act.SILU, batch=utterances, x_len=t * d):
+            k.matmul_quantized_device(self.qa_d, self.ex_d, t, m["pw2"], x, d, acc)
+        else:
+            k.dwconv1d_device(self.glu, d, t // utterances, d, w.dw_w, self.conv_kernel, w.dw_b, self.conv, d,
+                              act=Act.SILU, batch=utterances, x_len=t * d, out_len=t * d)
+            k.linear_device(self.conv[:t], t, m["pw2"], x, acc)
         feed_forward("norm_ff2", "ff2_in", "ff2_out")
         g, b = w.norms["norm_out"]
         k.layer_norm_device(x, d, t, d, g, b, eps, x, d)

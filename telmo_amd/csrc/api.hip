@@ -808,6 +808,40 @@ int tg_dwconv1d_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, si
     return TG_OK;
 }
 
+int tg_dwconv1d_quant_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t frames, size_t batch,
+                             size_t channels, const float *w, size_t w_len, size_t kernel, const float *bias,
+                             size_t bias_len, uint32_t act, float *out, size_t out_len, size_t ldo, void *qa,
+                             size_t qa_len, int32_t *exps, size_t exps_len) {
+    if (!ctx) return TG_ERR_NULL;
+    if (act != TG_ACT_NONE && act != TG_ACT_SILU) return fail(ctx, TG_ERR_ARG, "act must be TG_ACT_NONE or TG_ACT_SILU");
+    if (frames == 0 || channels == 0 || batch == 0) return TG_OK;
+    if (!x || !w || !bias || !qa || !exps) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (!tg::dwconv_quant_fits(channels, kernel))
+        return fail(ctx, TG_ERR_UNSUPPORTED, "channels must be 1 .. 2048 and kernel 1 .. 32");
+    if (ldx < channels || (out && ldo < channels)) return fail(ctx, TG_ERR_SHAPE, "ldx and ldo must be >= channels");
+    if (frames > (size_t)INT32_MAX || batch > (size_t)INT32_MAX / frames)
+        return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
+    const size_t total = frames * batch;
+    if (bias_len < channels) return fail(ctx, TG_ERR_SHAPE, "bias is too short");
+    if (w_len < kernel * channels) return fail(ctx, TG_ERR_SHAPE, "w is too short");
+    if (x_len < span(total, ldx, channels)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (out && out_len < span(total, ldo, channels)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    if (qa_len < tg_quant_bytes(total, channels)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (exps_len < total) return fail(ctx, TG_ERR_SHAPE, "exps is too short");
+    if (out) {
+        // the bytes each view spans (each span is below 2^31 rows of at most ldx or ldo floats)
+        const size_t xs = span(total, ldx, channels), os = span(total, ldo, channels);
+        const size_t xn = xs > SIZE_MAX / 4 ? SIZE_MAX : xs * 4, on = os > SIZE_MAX / 4 ? SIZE_MAX : os * 4;
+        const uintptr_t xb = reinterpret_cast<uintptr_t>(x), ob = reinterpret_cast<uintptr_t>(out);
+        if (ob >= xb ? ob - xb < xn : xb - ob < on) return fail(ctx, TG_ERR_ARG, "out must not overlap x");
+    }
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_dwconv_quant(x, ldx, frames, batch, channels, w, kernel, bias, act == TG_ACT_SILU, out, ldo,
+                                        static_cast<uint8_t *>(qa), exps, ctx->stream));
+    return TG_OK;
+}
+
 /* ---- the TDT decode -------------------------------------------------------------------------- */
 
 namespace {

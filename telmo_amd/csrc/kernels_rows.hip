@@ -1024,6 +1024,190 @@ void launch_dwconv_reg(const float *x, size_t ldx, size_t frames, size_t batch, 
                        total);
 }
 
+// The depthwise convolution of whole sequences (output row r of a sequence = frame r, stride 1) with
+// its output rows quantised as the row quantiser would (tg_dwconv1d_quant_device): the same f32
+// values as dwconv1d_reg_kernel, then the same exponents and digits as quantize_rows_regs_kernel.
+// Workgroup b takes output rows R b .. R b + R - 1 of the stacked sequences (so its rows may hold the
+// end of one sequence and the start of the next) over all channels, one channel per thread and
+// slice of 1024: R = 16 (a whole QA row block) for large batches, R = 4 (a quarter of one, four
+// times the workgroups) for short ones, where the per-row arithmetic and not the memory bounds the
+// time. Each thread loads the SPAN input rows its R outputs reach (clamped to the input) and the
+// taps into registers, sums taps in order from the bias (a tap whose input row lies outside its
+// output row's sequence is skipped, not added as zero), applies the SiLU, and stages the row in LDS
+// (row stride CWS floats, 16 bytes past a multiple of 256 so the digit pass reads without bank
+// conflicts). The R row maxima and non-finite flags are reduced over the workgroup; then each
+// thread packs the digits of 16 inputs of one row into a 16-byte hi and a 16-byte lo store (item
+// (t, g, i): k-block t, 16-input group g, row i, rows fastest, so a wavefront's stores are runs of
+// R x 16 contiguous bytes of the operand layout). Channels past the last and rows past the last get
+// zero digits; their f32 values are not stored.
+template <int R, int KMAX, int SL>
+__global__ __launch_bounds__(1024) void dwconv_quant_kernel(const float *__restrict__ x, size_t ldx, int64_t frames,
+                                                            int64_t total, int channels,
+                                                            const float *__restrict__ w, int kernel,
+                                                            const float *__restrict__ bias, int silu,
+                                                            float *__restrict__ out, size_t ldo,
+                                                            uint8_t *__restrict__ qa, int32_t *__restrict__ exps,
+                                                            int kb, size_t bpx) {
+    static_assert(16 % R == 0, "whole QA row blocks split evenly");
+    constexpr int SPAN = R - 1 + KMAX, CWS = 1024 * SL + 4, WAVES = 16;
+    __shared__ __attribute__((aligned(16))) float tile[R * CWS];
+    __shared__ float s_max[WAVES][R];
+    __shared__ int s_bad[WAVES];
+    __shared__ int32_t s_e[R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Workgroup L runs on XCD L % 8; each XCD takes a contiguous run of row groups.
+    const size_t grp = (blockIdx.x % 8) * bpx + blockIdx.x / 8;
+    const int64_t g0 = (int64_t)grp * R;
+    if (g0 >= total) return;  // uniform over the workgroup
+    const int half = kernel / 2;
+    const int64_t first = g0 - half;  // the input row of window slot 0
+    // The first row of each output row's sequence, as a window slot: lo[i] = start - first, in
+    // [i + half + 1 - frames, i + half] (wave-uniform).
+    int32_t lo[R];
+    {
+        int64_t s = (g0 / frames) * frames;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            while (g0 + i >= s + frames) s += frames;
+            lo[i] = (int32_t)(s - first);
+        }
+    }
+    // The whole window inside row 0's sequence: every row of the group is in it and every tap valid.
+    const bool inner = lo[0] <= 0 && (R - 1) + (kernel - 1) < lo[0] + frames;
+    float rmax[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rmax[i] = 0.0f;
+    int rbad = 0;
+#pragma unroll 1
+    for (int sl = 0; sl < SL; sl++) {
+        const int c = sl * 1024 + tid;
+        const int cc = c < channels ? c : channels - 1;  // idle lanes load a valid column and store nothing
+        float acc[R];
+        {
+            float v[SPAN], wr[KMAX];
+#pragma unroll
+            for (int s = 0; s < SPAN; s++) {
+                const int64_t f = first + s;
+                const int64_t fc = f < 0 ? 0 : (f >= total ? total - 1 : f);
+                v[s] = x[(size_t)fc * ldx + cc];
+            }
+#pragma unroll
+            for (int j = 0; j < KMAX; j++) wr[j] = w[(size_t)(j < kernel ? j : kernel - 1) * channels + cc];
+            const float b = bias[cc];
+#pragma unroll
+            for (int i = 0; i < R; i++) acc[i] = b;
+            if (inner) {
+#pragma unroll
+                for (int j = 0; j < KMAX; j++) {
+                    if (j < kernel) {
+#pragma unroll
+                        for (int i = 0; i < R; i++) acc[i] = acc[i] + wr[j] * v[i + j];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < KMAX; j++) {
+                    if (j < kernel) {
+#pragma unroll
+                        for (int i = 0; i < R; i++) {
+                            const float nv = acc[i] + wr[j] * v[i + j];
+                            acc[i] = (uint32_t)(i + j - lo[i]) < (uint32_t)frames ? nv : acc[i];
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            float o = acc[i];
+            if (silu) o = o / (1.0f + exp_simd(0.0f - o));
+            const bool ok = c < channels && g0 + i < total;
+            tile[i * CWS + c] = ok ? o : 0.0f;
+            if (ok) {
+                if (out) out[(size_t)(g0 + i) * ldo + c] = o;
+                rmax[i] = fmaxf(rmax[i], fabsf(o));
+                rbad |= (!__builtin_isfinite(o)) << i;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        const float m = wave_max(rmax[i]);
+        if (lane == 0) s_max[wave][i] = m;
+    }
+    rbad = wave_or(rbad);
+    if (lane == 0) s_bad[wave] = rbad;
+    __syncthreads();
+    if (tid < R) {
+        float m = 0.0f;
+        int b = 0;
+#pragma unroll
+        for (int q = 0; q < WAVES; q++) {
+            m = fmaxf(m, s_max[q][tid]);
+            b |= s_bad[q];
+        }
+        const bool valid = g0 + tid < total;
+        const int32_t e = !valid ? 0 : (((b >> tid) & 1) ? EXP_NONFINITE : row_exponent_of(m));
+        s_e[tid] = e;
+        if (valid) exps[g0 + tid] = e;
+    }
+    __syncthreads();
+    const size_t blk = (size_t)(g0 / 16);
+    const int r0 = (int)(g0 % 16);
+    for (int item = tid; item < 4 * R * kb; item += 1024) {
+        const int i = item % R, g = (item / R) % 4, t = item / (4 * R);
+        const float4 *src = reinterpret_cast<const float4 *>(tile + i * CWS + 64 * t + 16 * g);
+        const int32_t e = s_e[i];
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 a = src[q];
+            digits4(a.x, a.y, a.z, a.w, e, h[q], l[q]);
+        }
+        uint8_t *dst = qa + ((blk * (size_t)kb + t) * 2) * 1024 + (16 * g + r0 + i) * 16;
+        *reinterpret_cast<uint4 *>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<uint4 *>(dst + 1024) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+}
+
+bool dwconv_quant_fits(size_t channels, size_t kernel) {
+    return channels >= 1 && channels <= 2048 && kernel >= 1 && kernel <= 32;
+}
+
+// Rows below which the four-row workgroups take the call (fewer than two 16-row workgroups per CU).
+constexpr size_t DQ_SMALL = 8192;
+
+hipError_t launch_dwconv_quant(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
+                               const float *w, size_t kernel, const float *bias, int silu, float *out, size_t ldo,
+                               uint8_t *qa, int32_t *exps, hipStream_t s) {
+    const size_t total = frames * batch;
+    if (total == 0 || channels == 0) return hipSuccess;
+    if (!dwconv_quant_fits(channels, kernel)) return hipErrorInvalidValue;
+    const size_t kb = div_ceil(channels, (size_t)KBLK);
+    const size_t rows = total < DQ_SMALL ? 4 : 16;
+    const size_t bpx = div_ceil(div_ceil(total, rows), (size_t)8);
+    const dim3 grid((unsigned)(8 * bpx));
+#define TG_DQ(R_, KM, SL_)                                                                                       \
+    hipLaunchKernelGGL((dwconv_quant_kernel<R_, KM, SL_>), grid, dim3(1024), 0, s, x, ldx, (int64_t)frames,       \
+                       (int64_t)total, (int)channels, w, (int)kernel, bias, silu, out, ldo, qa, exps, (int)kb, bpx)
+#define TG_DQ_K(R_, SL_)                         \
+    do {                                         \
+        if (kernel <= 9) TG_DQ(R_, 9, SL_);      \
+        else if (kernel <= 16) TG_DQ(R_, 16, SL_); \
+        else TG_DQ(R_, 32, SL_);                 \
+    } while (0)
+    if (rows == 4) {
+        if (channels <= 1024) TG_DQ_K(4, 1);
+        else TG_DQ_K(4, 2);
+    } else {
+        if (channels <= 1024) TG_DQ_K(16, 1);
+        else TG_DQ_K(16, 2);
+    }
+#undef TG_DQ_K
+#undef TG_DQ
+    return hipGetLastError();
+}
+
 hipError_t launch_dwconv1d(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels, const float *w,
                            size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows, int silu,
                            float *out, size_t ldo, hipStream_t s) {

@@ -197,6 +197,13 @@ hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *
 hipError_t launch_dwconv1d(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels, const float *w,
                            size_t kernel, const float *bias, size_t t0, size_t stride, size_t rows, int silu,
                            float *out, size_t ldo, hipStream_t s);
+// The depthwise convolution of whole sequences (t0 = 0, stride 1, rows = frames) with its output
+// rows quantised (qa, exps as launch_quantize_rows writes them for k = channels); out may be null.
+// channels <= 2048 and 1 <= kernel <= 32 (dwconv_quant_fits).
+bool dwconv_quant_fits(size_t channels, size_t kernel);
+hipError_t launch_dwconv_quant(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
+                               const float *w, size_t kernel, const float *bias, int silu, float *out, size_t ldo,
+                               uint8_t *qa, int32_t *exps, hipStream_t s);
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s);
 // LayerNorm then the two-digit quantisation of its outputs (qa, exps); out (may be null, may be x)

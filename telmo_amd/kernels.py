@@ -26,6 +26,10 @@ import numpy as np
 from . import _lib
 
 
+# The library's status for a precision, mode or size it does not run (TG_ERR_UNSUPPORTED).
+TG_ERR_UNSUPPORTED = -5
+
+
 class TelmoError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"{message} (status {code})")
@@ -433,6 +437,26 @@ class Kernels:
                                            t0, stride, rows, a, _dev(out, "float32", "out"),
                                            _len(out, out_len, "out"), ldo)
         _check(rc, self._ctx)
+
+    def dwconv1d_quant_device(self, x, ldx: int, frames: int, channels: int, w, kernel: int, bias, qa, exps,
+                              act: "Act" = None, batch: int = 1, out=None, ldo: int = 0,
+                              x_len: Optional[int] = None, out_len: Optional[int] = None) -> bool:
+        """dwconv1d_device of whole sequences (rows = frames, t0 = 0, stride 1) writing its output
+        rows quantised into qa / exps, as quantize_rows_device would write them (k = channels);
+        out (optional) also receives the f32 rows. Returns False, with nothing queued, when the
+        fused kernel does not take the shape (channels beyond 2048 or kernel beyond 32): the caller
+        then makes the two calls."""
+        a = int(Act.NONE if act is None else act)
+        rc = _lib.lib().tg_dwconv1d_quant_device(
+            self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, frames, batch, channels,
+            _dev(w, "float32", "w"), _len(w, None, "w"), kernel, _dev(bias, "float32", "bias"),
+            _len(bias, None, "bias"), a, _dev(out, "float32", "out") if out is not None else None,
+            _len(out, out_len, "out") if out is not None else 0, ldo, _dev(qa, "uint8", "qa"),
+            _len(qa, None, "qa"), _dev(exps, "int32", "exps"), _len(exps, None, "exps"))
+        if rc == TG_ERR_UNSUPPORTED:
+            return False
+        _check(rc, self._ctx)
+        return True
 
     def synchronize(self) -> None:
         _check(_lib.lib().tg_synchronize(self._ctx), self._ctx)

@@ -5,7 +5,9 @@ MI355X: each must write exactly the bytes of the calls it replaces.
   and the f32 LayerNorm when asked for, in place too);
 * tg_matmul_quantized_to_quant_device = tg_matmul_quantized_device into f32 rows then
   tg_quantize_rows_device, for every launch of a sequence and every replay of a captured graph (its
-  workspace of f32 rows and row maxima is rewritten by every launch).
+  workspace of f32 rows and row maxima is rewritten by every launch);
+* tg_dwconv1d_quant_device = tg_dwconv1d_device then tg_quantize_rows_device, the f32 rows also
+  bit-identical to the oracle's dwconv1d_frame loop.
 """
 import numpy as np
 import pytest
@@ -186,3 +188,73 @@ def test_quantised_output_refusals(tk):
         tk.layer_norm_quant_device(torch.zeros((m, k), device="cuda"), k, m, k, torch.ones(k, device="cuda"),
                                    torch.zeros(k, device="cuda"), 1e-5, qa[:-1], ex)
     w.close()
+
+
+# batch, frames, channels, kernel, silu, with_out, ldx. Row blocks of 16 that straddle sequences
+# (375, 20, 7 frames), sequences shorter than a block, channels past 1024 (two slices) and not a
+# multiple of 64, 9 / 16 / 31 taps, a NaN and an infinity in the input.
+DWQ_CASES = [(1, 750, 1024, 9, True, False, 1024), (32, 375, 1024, 9, True, False, 1024),
+             (5, 20, 64, 9, True, True, 64), (9, 7, 100, 16, False, True, 104), (3, 40, 1000, 31, True, True, 1000),
+             (2, 33, 2048, 9, True, True, 2048), (4, 16, 1500, 5, False, False, 1504), (1, 1, 3, 3, True, True, 3),
+             (2, 50, 130, 1, True, False, 130)]
+
+
+@pytest.mark.parametrize("case", DWQ_CASES)
+def test_dwconv_quant_is_dwconv_then_quantise(tk, orc, case):
+    import torch
+
+    from telmo_amd import Act
+
+    batch, frames, channels, kernel, silu, with_out, ldx = case
+    total = batch * frames
+    rng = np.random.default_rng(total + channels + kernel)
+    x = (2.0 * rng.standard_normal((total, ldx))).astype(np.float32)
+    if total > 40 and channels > 20:
+        x[30, 11] = np.nan
+        x[total - 2, channels - 1] = np.inf
+    w = (0.3 * rng.standard_normal((kernel, channels))).astype(np.float32)
+    bias = rng.standard_normal(channels).astype(np.float32)
+    say("dwconv_quant", case)
+    act = Act.SILU if silu else Act.NONE
+    xd, wd, bd = (torch.from_numpy(v).cuda() for v in (x, w, bias))
+    conv = torch.full((total, channels), 9.5, device="cuda")
+    tk.dwconv1d_device(xd, ldx, frames, channels, wd, kernel, bd, conv, channels, act=act, batch=batch,
+                       x_len=(total - 1) * ldx + channels)
+    want_qa, want_ex = quantised(tk, conv, channels, total, channels)
+    qa = torch.zeros_like(want_qa)
+    ex = torch.zeros_like(want_ex)
+    out = torch.full((total, channels), 9.5, device="cuda") if with_out else None
+    assert tk.dwconv1d_quant_device(xd, ldx, frames, channels, wd, kernel, bd, qa, ex, act=act, batch=batch,
+                                    out=out, ldo=channels, x_len=(total - 1) * ldx + channels)
+    tk.synchronize()
+    assert torch.equal(ex, want_ex)
+    assert torch.equal(qa, want_qa)
+    if with_out:
+        assert same_floats(out, conv)
+    want = np.concatenate([orc.dwconv1d(x[b * frames:(b + 1) * frames, :channels], w, bias, silu=silu)
+                           for b in range(batch)])
+    got = conv.cpu().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_dwconv_quant_refusals_and_fallback(tk):
+    import torch
+
+    import telmo_amd
+
+    xx = torch.zeros((16, 16), device="cuda")
+    x = xx[:8]
+    w = torch.zeros((3, 16), device="cuda")
+    b = torch.zeros(16, device="cuda")
+    qa = torch.zeros(tk.quant_bytes(8, 16), dtype=torch.uint8, device="cuda")
+    ex = torch.zeros(8, dtype=torch.int32, device="cuda")
+    with pytest.raises(telmo_amd.TelmoError):  # qa too short for 16 rows
+        tk.dwconv1d_quant_device(xx, 16, 8, 16, w, 3, b, qa, ex, batch=2)
+    with pytest.raises(telmo_amd.TelmoError):  # out overlaps x
+        tk.dwconv1d_quant_device(x, 16, 8, 16, w, 3, b, qa, ex, out=xx[4:12], ldo=16)
+    with pytest.raises(telmo_amd.TelmoError):  # ldx < channels
+        tk.dwconv1d_quant_device(x, 8, 8, 16, w, 3, b, qa, ex)
+    w33 = torch.zeros((33, 16), device="cuda")
+    assert not tk.dwconv1d_quant_device(x, 16, 8, 16, w33, 33, b, qa, ex)  # 33 taps: the caller's two calls
