@@ -122,16 +122,67 @@ __device__ __forceinline__ int32_t exponent_from_slots(const uint32_t *slots, in
     return mx == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(mx));
 }
 
+// A wavefront's operands of one panel in registers: the first KBC weight blocks (int8: whole
+// 16-byte operands and one scale per column; Q8_0: 8-byte halves and block scales), the bias and
+// the old outputs of its column.
+template <int KBC, int Q8>
+struct Panel {
+    v4i wr[Q8 ? 1 : KBC];
+    long wh[Q8 ? KBC : 1][2];
+    float sq[Q8 ? KBC : 1][2];
+    float sc, bv, old[4];
+};
+
+// The first panel mfma_body<WAVES, ..., KS> gives this wavefront, fetched as its body would fetch it:
+// for callers whose input rows depend on loads of their own (a control block, another kernel's
+// outputs), so that the weights are requested first and arrive while those loads resolve. The panel
+// fetch is unconditional (a wavefront past the last panel re-reads panel P - 1 and never uses it).
+template <int WAVES, int KBC, int Q8, int KS = 1>
+__device__ __forceinline__ void fetch_first(Panel<KBC, Q8> &pn, int m, const uint8_t *__restrict__ wv,
+                                            const float *__restrict__ scales, int N, int P, int KB, int NB,
+                                            const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
+                                            int accumulate, size_t panel_stride, size_t blk_stride) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kw = KS > 1 ? wave : 0;
+    const int p = KS > 1 ? blockIdx.x : blockIdx.x * WAVES + wave;
+    const int off0 = (16 * ((lane >> 4) >> 1) + (lane & 15)) * 16 + 8 * ((lane >> 4) & 1);
+    pn.sc = 0.0f;
+    if constexpr (Q8)
+        fetch_panel_q8<KBC>(pn.wh, pn.sq, pn.bv, pn.old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, NB,
+                            off0, scales, bias, c, ldc, N, m, accumulate);
+    else
+        fetch_panel<KBC>(pn.wr, pn.sc, pn.bv, pn.old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales,
+                         bias, c, ldc, N, m, accumulate, kw, KS);
+}
+
+// The chunks of the input rows this thread holds in mfma_body: rows are split into 4-input chunks,
+// ceil(KB / 4) wavefronts of them per row (the tail of the last wavefront idle); wavefront w holds
+// chunk wavefronts w + WAVES j (j < J). Chunk wavefront q = wave + WAVES j covers chunks
+// 64 (q - r spr) + [0, 64) of row r = q / spr, spr = ceil(KB / 4); q / spr is (q inv) >> 16, exact
+// for q < 1024 and spr <= 8. One 16-byte load per chunk (rows 16-byte aligned, k % 4 == 0); chunks
+// past the rows read the zero chunk. Every load is unconditional.
+template <int WAVES, int J, class In>
+__device__ __forceinline__ void load_rows(const In &in, v4f (&x)[J], int m, int k, int KB) {
+    const int lane = threadIdx.x & 63;
+    const int spr = (KB + 3) / 4, inv = (65536 + spr - 1) / spr;
+    const int wq = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int q = wq + WAVES * j, r = (q * inv) >> 16;
+        x[j] = in.load(r, ((q - r * spr) * 64 + lane) * 4, m, k);
+    }
+}
+
 // Rows are split into 4-input chunks, ceil(KB / 4) wavefronts of them per row (the tail of the
 // last wavefront idle); wavefront w holds chunk wavefronts w + WAVES j (j < J) in registers. The
 // rows are read once, before the weights, so the weight loads stay in flight while the rows are
-// digitised.
-template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR = 0, int KS = 1>
-__device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
-                                          const float *__restrict__ scales, int N, int P, int KB, int NB,
-                                          const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
-                                          uint32_t act, float escale, int accumulate, size_t panel_stride,
-                                          size_t blk_stride, uint8_t *sqa, uint32_t *slot) {
+// digitised. With PRE, pn holds the first panel already (fetch_first, called before the rows).
+template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR, int KS, bool PRE>
+__device__ __forceinline__ void mfma_body_impl(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
+                                               const float *__restrict__ scales, int N, int P, int KB, int NB,
+                                               const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
+                                               uint32_t act, float escale, int accumulate, size_t panel_stride,
+                                               size_t blk_stride, uint8_t *sqa, uint32_t *slot, Panel<KBC, Q8> &pn) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Chunk wavefront q = wave + WAVES j covers chunks 64 (q - r spr) + [0, 64) of row
     // r = q / spr, where spr = ceil(KB / 4) wavefronts cover a row (its tail idle). All of it is
@@ -148,29 +199,28 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
     const int step = KS > 1 ? gridDim.x : gridDim.x * WAVES;
     int p = KS > 1 ? blockIdx.x : blockIdx.x * WAVES + wave;
 
-    // One 16-byte load per chunk (rows 16-byte aligned, k % 4 == 0); chunks past the rows read
-    // the zero chunk. Every load is unconditional and used as loaded, so the loads stay ahead of
-    // the weight loads and waiting for them never waits for the weights.
+    // The rows' loads are used as loaded and issued ahead of the weight loads, so waiting for them
+    // never waits for the weights.
     v4f x[J];
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-        const int q = wq + WAVES * j, r = (q * inv) >> 16;
-        x[j] = in.load(r, ((q - r * spr) * 64 + lane) * 4, m, k);
-    }
+    load_rows<WAVES, J>(in, x, m, k, KB);
     // Panel fetches are unconditional (a wavefront past the last panel re-reads panel P - 1 and
     // never uses it): under a branch the compiler's load counting would wait for them early.
     // int8: whole 16-byte operands and one scale per column. Q8_0: 8-byte halves and block scales.
     const int off0 = (16 * ((lane >> 4) >> 1) + (lane & 15)) * 16 + 8 * ((lane >> 4) & 1);
-    v4i wr[Q8 ? 1 : KBC];
-    long wh[Q8 ? KBC : 1][2];
-    float sq[Q8 ? KBC : 1][2];
-    float sc = 0.0f, bv, old[4];
-    if constexpr (Q8)
-        fetch_panel_q8<KBC>(wh, sq, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, NB, off0, scales,
-                            bias, c, ldc, N, m, accumulate);
-    else
-        fetch_panel<KBC>(wr, sc, bv, old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB, scales, bias, c,
-                         ldc, N, m, accumulate, kw, KS);
+    if constexpr (!PRE) {
+        pn.sc = 0.0f;
+        if constexpr (Q8)
+            fetch_panel_q8<KBC>(pn.wh, pn.sq, pn.bv, pn.old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB,
+                                NB, off0, scales, bias, c, ldc, N, m, accumulate);
+        else
+            fetch_panel<KBC>(pn.wr, pn.sc, pn.bv, pn.old, min(p, P - 1), lane, wv, panel_stride, blk_stride, KB,
+                             scales, bias, c, ldc, N, m, accumulate, kw, KS);
+    }
+    auto &wr = pn.wr;
+    auto &wh = pn.wh;
+    auto &sq = pn.sq;
+    float &sc = pn.sc, &bv = pn.bv;
+    auto &old = pn.old;
 
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -348,6 +398,31 @@ __device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, 
             }
         }
     }
+}
+
+// The GEMV body, fetching its first panel after the rows.
+template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR = 0, int KS = 1>
+__device__ __forceinline__ void mfma_body(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
+                                          const float *__restrict__ scales, int N, int P, int KB, int NB,
+                                          const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
+                                          uint32_t act, float escale, int accumulate, size_t panel_stride,
+                                          size_t blk_stride, uint8_t *sqa, uint32_t *slot) {
+    Panel<KBC, Q8> pn;
+    mfma_body_impl<WAVES, KBC, J, Q8, In, Out, DOTR, KS, false>(in, out, m, k, wv, scales, N, P, KB, NB, c, ldc, bias,
+                                                                act, escale, accumulate, panel_stride, blk_stride,
+                                                                sqa, slot, pn);
+}
+
+// The GEMV body on a first panel the caller fetched with fetch_first<WAVES, KBC, Q8, KS>.
+template <int WAVES, int KBC, int J, int Q8, class In, class Out, int DOTR = 0, int KS = 1>
+__device__ __forceinline__ void mfma_body_pre(const In &in, Out &out, int m, int k, const uint8_t *__restrict__ wv,
+                                              const float *__restrict__ scales, int N, int P, int KB, int NB,
+                                              const float *__restrict__ c, size_t ldc, const float *__restrict__ bias,
+                                              uint32_t act, float escale, int accumulate, size_t panel_stride,
+                                              size_t blk_stride, uint8_t *sqa, uint32_t *slot, Panel<KBC, Q8> &pn) {
+    mfma_body_impl<WAVES, KBC, J, Q8, In, Out, DOTR, KS, true>(in, out, m, k, wv, scales, N, P, KB, NB, c, ldc, bias,
+                                                               act, escale, accumulate, panel_stride, blk_stride,
+                                                               sqa, slot, pn);
 }
 
 }  // namespace gemv

@@ -162,11 +162,16 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_joint_kernel(TdtCtl *ctl, con
     __shared__ Best red[TDT_WAVES][TDT_ROWS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool lead = blockIdx.x == 0 && tid == 0;
-    if (load_i(&ctl->done)) {
+    // The control values head the chain: they are requested first, the weights (which do not depend
+    // on them) right after, so that waiting for the control values never waits for the weights.
+    const int done = load_i(&ctl->done), t = load_i(&ctl->t), rows = load_i(&ctl->rows);
+    gemv::Panel<KBC, Q8> pn;
+    gemv::fetch_first<TDT_WAVES, KBC, Q8>(pn, 1, w.values, w.scales, w.n, w.P, w.KB, w.NB, extras, 0, bias, 0,
+                                          w.panel_stride, w.blk_stride);
+    if (done) {
         if (lead) store_i(&ctl->snap.valid, 0);
         return;
     }
-    const int t = load_i(&ctl->t), rows = load_i(&ctl->rows);
     if (t >= frames) {
         // Only the last prediction's state flip is left: the decode ends here.
         if (lead) {
@@ -192,9 +197,9 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_joint_kernel(TdtCtl *ctl, con
         out.bv[v] = __builtin_nanf("");
         out.bi[v] = INT32_MAX;
     }
-    gemv::mfma_body<TDT_WAVES, KBC, J, Q8>(JointIn{enc, lde, pred, t, frames}, out, rows, w.k, w.values, w.scales,
+    gemv::mfma_body_pre<TDT_WAVES, KBC, J, Q8>(JointIn{enc, lde, pred, t, frames}, out, rows, w.k, w.values, w.scales,
                                            w.n, w.P, w.KB, w.NB, extras, 0, bias, ACT_NONE, 1.0f, 0,
-                                           w.panel_stride, w.blk_stride, sqa, slot);
+                                           w.panel_stride, w.blk_stride, sqa, slot, pn);
     // Lanes 16 g .. 16 g + 15 hold 16 columns of rows 4 g .. 4 g + 3: fold them, then the wavefronts.
 #pragma unroll
     for (int v = 0; v < 4; v++) {
@@ -231,27 +236,45 @@ struct Decide {
 };
 
 // The step's decision, computed alike in every workgroup of the kernel after the joint (so it needs
-// no communication between them). Returns the token handed to the prediction network, or -1; the
-// state buffer to read is left in *cur. Workgroup 0 publishes the new control values.
+// no communication between them). Every load it makes is independent of the others (the snapshot,
+// the joint's partials, the first and duration logits of all TDT_ROWS rows, the durations), so they
+// are all issued before any is used: one memory round trip. Returns the token handed to the
+// prediction network, -1 when the step hands none on, or -2 when the joint made no step (the
+// decode had ended); the state buffer to read is left in *cur. Workgroup 0 publishes the new
+// control values.
 __device__ __forceinline__ int decide_step(TdtCtl *ctl, const Decide &d, int *cur) {
     __shared__ int tok_s[TDT_ROWS], dur_s[TDT_ROWS], durs[TDT_MAX_DURATIONS], result;
     __shared__ float dlog[TDT_ROWS][TDT_MAX_DURATIONS];
     const int tid = threadIdx.x;
-    const int t = load_i(&ctl->snap.t), rows = load_i(&ctl->snap.rows);
-    *cur = load_i(&ctl->snap.cur) ^ load_i(&ctl->snap.active);  // the last prediction wrote the other buffer
-    if (tid < d.ndur) durs[tid] = d.durations[tid];
-    {
-        // Thread (r, s) takes row r's partials of workgroups s, s + 16, ... (sixteen loads per round,
-        // one round up to 256 joint workgroups), with the row's first and duration logits.
-        const int r = tid >> 4, s = tid & 15, nb = d.joint_grid;
-        const float *ex = d.extras + (size_t)min(r, rows - 1) * TDT_EXTRA;
-        const float first = ex[0];
-        float dl[4];
+    // Thread (r, s) takes row r's partials of workgroups s, s + 16, ... (sixteen loads per round,
+    // one round up to 256 joint workgroups), with the row's first and duration logits. Rows the
+    // window does not hold are read as well (the buffers hold TDT_ROWS rows) and never used. The
+    // partials and logits are requested first, the snapshot after them: a wait for a snapshot value
+    // then covers only loads the decision needs anyway.
+    const int r = tid >> 4, s = tid & 15, nb = d.joint_grid;
+    const float *ex = d.extras + (size_t)r * TDT_EXTRA;
+    Best x0[16];
 #pragma unroll
-        for (int q = 0; q < 4; q++) dl[q] = ex[1 + min(s + 16 * q, d.ndur - 1)];
+    for (int u = 0; u < 16; u++) x0[u] = d.partials[(size_t)min(s + 16 * u, nb - 1) * TDT_ROWS + r];
+    const float first = ex[0];
+    float dl[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) dl[q] = ex[1 + min(s + 16 * q, d.ndur - 1)];
+    const int dur_v = d.durations[min(tid, d.ndur - 1)];
+    const int valid = load_i(&ctl->snap.valid);
+    const int t = load_i(&ctl->snap.t), rows = load_i(&ctl->snap.rows);
+    const int snap_cur = load_i(&ctl->snap.cur), snap_active = load_i(&ctl->snap.active);
+    const int snap_on = load_i(&ctl->snap.on_frame), snap_ntok = load_i(&ctl->snap.ntok);
+    {
         float bv = __builtin_nanf("");
         int bi = INT32_MAX;
-        for (int b0 = s; b0 < nb; b0 += 16 * 16) {
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (s + 16 * u < nb && before(x0[u].v, x0[u].i, bv, bi)) {
+                bv = x0[u].v;
+                bi = x0[u].i;
+            }
+        for (int b0 = s + 16 * 16; b0 < nb; b0 += 16 * 16) {
             Best x[16];
 #pragma unroll
             for (int u = 0; u < 16; u++) x[u] = d.partials[(size_t)min(b0 + 16 * u, nb - 1) * TDT_ROWS + r];
@@ -271,11 +294,14 @@ __device__ __forceinline__ int decide_step(TdtCtl *ctl, const Decide &d, int *cu
                 bi = oi;
             }
         }
+        if (tid < d.ndur) durs[tid] = dur_v;
 #pragma unroll
         for (int q = 0; q < 4; q++)
             if (s + 16 * q < d.ndur) dlog[r][s + 16 * q] = dl[q];
         if (s == 0) tok_s[r] = __builtin_isnan(first) || bi == INT32_MAX ? 0 : bi;  // a NaN first is never beaten
     }
+    if (!valid) return -2;  // uniform: the joint made no step
+    *cur = snap_cur ^ snap_active;  // the last prediction wrote the other buffer
     __syncthreads();
     if (tid < TDT_ROWS) {
         int k = 0;
@@ -285,7 +311,7 @@ __device__ __forceinline__ int decide_step(TdtCtl *ctl, const Decide &d, int *cu
     }
     __syncthreads();
     if (tid == 0) {
-        int tc = t, on = load_i(&ctl->snap.on_frame), ntok = load_i(&ctl->snap.ntok), token = -1, done = 0;
+        int tc = t, on = snap_on, ntok = snap_ntok, token = -1, done = 0;
         // The next window: after a token, twice the frames this one walked (at least 4); after a
         // window of blanks, the most.
         int next = TDT_ROWS;
@@ -345,22 +371,21 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_lstm_kernel(TdtCtl *ctl, int 
     extern __shared__ __attribute__((aligned(16))) uint8_t sqa[];
     __shared__ uint32_t slot[TDT_WAVES * J];
     __shared__ int tok_s[TDT_ROWS];
+    const int h = w.k / 2;
     int cur = 0;
+    if (mode == 1) {
+        if (!load_i(&ctl->active)) return;
+        cur = load_i(&ctl->cur);
+    }
     if (mode == 2) {
-        if (!load_i(&ctl->snap.valid)) return;
         const int token = decide_step(ctl, dec, &cur);
         if (token < 0) return;
         if (threadIdx.x == 0) tok_s[0] = token;
-    } else {
-        if (mode == 1) {
-            if (!load_i(&ctl->active)) return;
-            cur = load_i(&ctl->cur);
-        }
+    } else if (mode == 0) {
         if (threadIdx.x < TDT_ROWS) tok_s[threadIdx.x] = toks.tok[threadIdx.x];
     }
     __syncthreads();
     float *s_in = cur ? sb : sa, *s_out = cur ? sa : sb;
-    const int h = w.k / 2;
     LstmOut out{s_in, s_out, width, h, l};
     gemv::mfma_body<TDT_WAVES, KBC, J, Q8, LstmIn, LstmOut, DOTR, KS>(LstmIn{emb, s_in, s_out, width, h, l, tok_s}, out, m,
                                                                   w.k, w.values, w.scales, w.n, w.P, w.KB, w.NB, s_out,
