@@ -7,16 +7,18 @@
 //
 // Both the quantised rows (fragment-major QA) and the weights (MFMA layout) store each 16 x 64
 // MFMA operand as 1 KB in lane order, so one 16-byte load per lane is one operand, fully coalesced.
-// Three kernels share that layout and the epilogue (TileStore):
+// Three kernels share that layout:
 //   gemm_lds_kernel    operands copied from global memory straight into an LDS ring
 //                      (global_load_lds_dwordx4), one copy per workgroup: 128 x 128 tiles when
 //                      they fill the chip twice over, 64 x 64 tiles for products of >= 2048 outputs;
+//                      the sums come out transposed and are stored from registers (store_transposed);
 //   gemm_i8_kernel     2 x 2 independent wavefronts loading their operands straight into a
 //                      register ring (no LDS, no barriers in the loop): narrower products;
 //   gemm_i8_kq_kernel  the narrower products with long inputs: each wavefront takes the whole
 //                      64 x 64 tile over a quarter of the k-blocks, and the integer partial sums
 //                      meet in LDS.
-// launch_gemm_i8 at the end picks one by shape.
+// The other two stage their sums in LDS and store them through TileStore. launch_gemm_i8 at the
+// end picks one by shape.
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -228,6 +230,112 @@ __device__ __forceinline__ void stage_sums(float *tile, const v4i (&acc_hi)[RB][
                     tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
                         dequant(acc_hi[r][cb][v], acc_lo[r][cb][v], e_row[r][v], s_col[cb]);
     }
+}
+
+// The epilogue of a wavefront whose MFMAs took the weights as the first operand and the rows as
+// the second, so that the accumulators hold the transposed blocks: element v of lane l in block
+// (r, cb) is the sum of row m0 + 16 r + l % 16, column n0 + 16 cb + 4 (l / 16) + v. Each lane then
+// owns runs of four consecutive outputs and stores them from registers (16-byte nontemporal
+// stores), with no staging in LDS and no barrier (the 12000 x 1024 -> 4096 product takes 140 us
+// against 150 us with its sums staged in LDS). e[r] is the exponent of the lane's row in row block
+// r, sc[cb] the scales of its four columns in block cb. With rmax, also each row block's largest
+// |y| over the wavefront's columns below N (all ones for a NaN or an infinity, 0 past M), the same
+// in the 16 lanes l % 16 of a row. Rows past M are skipped.
+//
+// FAST (a wave-uniform choice): every column of the wavefront lies below N and c, ldc and bias
+// are 16-byte aligned, so the bias, the old outputs and the outputs move 16 bytes at a time with
+// no column checks. Otherwise they move one output at a time, columns past N skipped.
+template <bool FAST, int RB, int CB>
+__device__ __forceinline__ void store_transposed_as(const v4i (&acc_hi)[RB][CB], const v4i (&acc_lo)[RB][CB],
+                                                    const int32_t (&e)[RB], const v4f (&sc)[CB], int lane,
+                                                    float *__restrict__ c, size_t ldc, int m0, int n0, int M, int N,
+                                                    const float *__restrict__ bias, uint32_t act, float escale,
+                                                    int accumulate, uint32_t *rmax) {
+    const int mr = lane & 15, nq = 4 * (lane >> 4);
+    v4f b[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) {
+        b[cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        const int col = n0 + 16 * cb + nq;
+        if (bias) {
+            if constexpr (FAST) {
+                b[cb] = *reinterpret_cast<const v4f *>(bias + col);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) b[cb][j] = col + j < N ? bias[col + j] : 0.0f;
+            }
+        }
+    }
+    const bool fits = wave_fits_i32<RB, CB>(acc_hi);
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+        const int row = m0 + 16 * r + mr;
+        float *dst = c + (size_t)row * ldc + n0 + nq;
+        uint32_t mx = 0u;
+        if (row < M) {
+            v4f old[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) {
+                old[cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                const int col = n0 + 16 * cb + nq;
+                if (accumulate) {
+                    if constexpr (FAST) {
+                        old[cb] = *reinterpret_cast<const v4f *>(dst + 16 * cb);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            if (col + j < N) old[cb][j] = dst[16 * cb + j];
+                    }
+                }
+            }
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) {
+                const int col = n0 + 16 * cb + nq;
+                v4f v;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float d = fits ? dequant_i32(acc_hi[r][cb][j], acc_lo[r][cb][j], e[r], sc[cb][j])
+                                         : dequant(acc_hi[r][cb][j], acc_lo[r][cb][j], e[r], sc[cb][j]);
+                    v[j] = epilogue_vals(d, bias != nullptr, b[cb][j], act, escale, accumulate != 0, old[cb][j]);
+                    if (rmax && (FAST || col + j < N))
+                        mx = max(mx, __builtin_isfinite(v[j]) ? __float_as_uint(fabsf(v[j])) : 0xffffffffu);
+                }
+                if constexpr (FAST) {
+                    __builtin_nontemporal_store(v, reinterpret_cast<v4f *>(dst + 16 * cb));
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (col + j < N) dst[16 * cb + j] = v[j];
+                }
+            }
+        }
+        if (rmax) {
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 16, 64));
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 32, 64));
+            rmax[r] = mx;
+        }
+    }
+}
+
+// EDGE = 0: the launcher has checked that every wavefront is FAST (16-byte aligned c, ldc and bias,
+// and N a multiple of the workgroup's columns), so the kernel carries the FAST code alone: an
+// instruction footprint that fits the instruction cache (the kernel with both variants runs the
+// 12000 x 1024 -> 2048 product 7% slower). EDGE = 1: each wavefront picks.
+template <int EDGE, int RB, int CB>
+__device__ __forceinline__ void store_transposed(const v4i (&acc_hi)[RB][CB], const v4i (&acc_lo)[RB][CB],
+                                                 const int32_t (&e)[RB], const v4f (&sc)[CB], int lane,
+                                                 float *__restrict__ c, size_t ldc, int m0, int n0, int M, int N,
+                                                 const float *__restrict__ bias, uint32_t act, float escale,
+                                                 int accumulate, uint32_t *rmax = nullptr) {
+    const bool fast = !EDGE || (((reinterpret_cast<uintptr_t>(c) | ldc * sizeof(float) |
+                                  reinterpret_cast<uintptr_t>(bias)) % 16) == 0 &&
+                                n0 + 16 * CB <= N);
+    if (fast)
+        store_transposed_as<true>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale, accumulate,
+                                  rmax);
+    else
+        store_transposed_as<false>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale, accumulate,
+                                   rmax);
 }
 
 template <int RB, int CB, int S, int OCC, int XCD, int G>
@@ -637,17 +745,19 @@ hipError_t launch_q8(const uint8_t *qf, const int32_t *exps, size_t m, const Dev
 // fill the chip twice over; 64 x 64 tiles grouped four tile-rows at a time for mid-size products
 // of at least 2048 outputs.
 
-// 64 lanes x 16 bytes from g (per lane) to LDS at lds (the wavefront's base; lane l's bytes land at
-// lds + 16 l). M0 holds the LDS address; it is set before every copy and nothing else here uses it.
+// The LDS address of p (the offset within the workgroup's LDS).
 __device__ __forceinline__ uint32_t lds_address(const void *p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
 }
 
-__device__ __forceinline__ void copy_to_lds(const uint8_t *g, uint8_t *lds) {
-    const uint32_t a = __builtin_amdgcn_readfirstlane(lds_address(lds));
+// 64 lanes x 16 bytes from base + voff (a wave-uniform base address in scalar registers plus each
+// lane's byte offset) to LDS at lds (the wave-uniform LDS address; lane l's bytes land at lds +
+// 16 l when voff = 16 l). M0 holds the LDS address; it is set before every copy and nothing else
+// here uses it.
+__device__ __forceinline__ void copy_to_lds_s(const uint8_t *base, uint32_t voff, uint32_t lds) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(a), "v"(g) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory", "m0");
 #pragma clang diagnostic pop
 }
 
@@ -679,7 +789,7 @@ struct TileMax {
     int strips;
 };
 
-template <int TM, int TN, int NS, int XCD, int G, int GLU, int QOUT = 0>
+template <int TM, int TN, int NS, int XCD, int G, int GLU, int QOUT, int EDGE>
 __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__restrict__ qf,
                                                               const int32_t *__restrict__ exps, int M,
                                                               const uint8_t *__restrict__ wv,
@@ -691,11 +801,12 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
     constexpr int RB = TM / 2, CB = TN / 2;  // 16 x 16 blocks per wavefront
     constexpr int CH = 2 * TM + TN;          // 1 KB chunks per stage
     static_assert(CH % 4 == 0, "the chunks split evenly over four wavefronts");
+    static_assert(NS >= 3, "block t + 1 lands while block t is multiplied, block t - 1's buffer refills");
     constexpr int CPW = CH / 4, STAGE = CH * 1024;
     constexpr int WM = RB * 16, WN = CB * 16, C_STRIDE = WN + 4;
     static_assert(4 * WM * C_STRIDE * 4 <= NS * STAGE, "the epilogue reuses the ring");
     __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     int bx, by;
     tile_of<XCD, G>(bx, by);
@@ -715,7 +826,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
     // past the edge read the last valid one and are never stored.
     constexpr int NPRE = TM * 16 + TN * 16;
     static_assert(NPRE <= THREADS, "one exponent or scale per thread");
-    __shared__ uint32_t s_pre[NPRE];
+    __shared__ __attribute__((aligned(16))) uint32_t s_pre[NPRE];
     uint32_t pre = 0u;
     if (tid < TM * 16) {
         pre = (uint32_t)exps[min(by * TM * 16 + tid, M - 1)];
@@ -725,115 +836,123 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
     }
 
     // This wavefront's copies: chunk ch = wave + 4 i is row block R0 + ch / 2, digit ch % 2 when
-    // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one.
+    // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one. The
+    // bases are wave-uniform (scalar registers); each lane adds its 16 bytes' offset.
     const uint8_t *g[CPW];
     size_t gs[CPW];
 #pragma unroll
     for (int i = 0; i < CPW; i++) {
         const int ch = wave + 4 * i;
         if (ch < 2 * TM) {
-            g[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024 + lane * 16;
+            g[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024;
             gs[i] = 2048;
         } else {
-            g[i] = wv + (size_t)min(panel_of(ch - 2 * TM), P - 1) * b_panel + lane * 16;
+            g[i] = wv + (size_t)min(panel_of(ch - 2 * TM), P - 1) * b_panel;
             gs[i] = b_blk;
         }
     }
-#define TG_ISSUE(buf, tt)                                                                              \
-    do {                                                                                               \
-        uint8_t *st_ = smem + (buf) * STAGE;                                                           \
-        const size_t t_ = (size_t)(tt);                                                                \
-        _Pragma("unroll") for (int i = 0; i < CPW; i++) copy_to_lds(g[i] + t_ * gs[i], st_ + (wave + 4 * i) * 1024); \
-    } while (0)
-    // This wavefront's operands of one k-block from the stage at st: row blocks wm * RB + r (hi and
-    // lo digits) and panels wn * CB + cb.
-    auto read_frags = [&](const uint8_t *st, v4i (&fa)[RB][2], v4i (&fb)[CB]) {
+    const uint32_t voff = lane * 16, lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    auto issue = [&](int buf, int tt) {
 #pragma unroll
-        for (int r = 0; r < RB; r++) {
-            fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2) * 1024 + lane * 16);
-            fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2 + 1) * 1024 + lane * 16);
-        }
+        for (int i = 0; i < CPW; i++)
+            copy_to_lds_s(g[i] + (size_t)tt * gs[i], voff, lds0 + buf * STAGE + (wave + 4 * i) * 1024);
+    };
+    // This wavefront's operands of one k-block from LDS buffer buf: row blocks wm * RB + r (hi and lo
+    // digits) and panels wn * CB + cb.
+    auto read_frags = [&](int buf, v4i (&fa)[RB][2], v4i (&fb)[CB]) {
+        const uint8_t *st = smem + buf * STAGE;
 #pragma unroll
         for (int cb = 0; cb < CB; cb++)
             fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
-    };
-    // Row blocks [r0, r1) of this wavefront's A fragments (and, with b, its B fragments).
-    auto read_frags_rows = [&](const uint8_t *st, v4i (&fa)[RB][2], v4i (&fb)[CB], int r0, int r1, bool b) {
-        if (b) {
-#pragma unroll
-            for (int cb = 0; cb < CB; cb++)
-                fb[cb] = *reinterpret_cast<const v4i *>(st + 2 * TM * 1024 + (wn * CB + cb) * 1024 + lane * 16);
-        }
 #pragma unroll
         for (int r = 0; r < RB; r++) {
-            if (r < r0 || r >= r1) continue;
             fa[r][0] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2) * 1024 + lane * 16);
             fa[r][1] = *reinterpret_cast<const v4i *>(st + ((wm * RB + r) * 2 + 1) * 1024 + lane * 16);
         }
     };
-#define TG_MMA_ROWS(fa, fb, r0, r1)                                                                    \
-    do {                                                                                               \
-        _Pragma("unroll") for (int r = (r0); r < (r1); r++)                                            \
-            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
-                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][0], (fb)[cb], acc_hi[r][cb], 0, 0, 0); \
-                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][1], (fb)[cb], acc_lo[r][cb], 0, 0, 0); \
-            }                                                                                          \
-    } while (0)
-#define TG_MMA(fa, fb)                                                                                 \
-    do {                                                                                               \
-        _Pragma("unroll") for (int r = 0; r < RB; r++)                                                 \
-            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
-                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][0], (fb)[cb], acc_hi[r][cb], 0, 0, 0); \
-                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8((fa)[r][1], (fb)[cb], acc_lo[r][cb], 0, 0, 0); \
-            }                                                                                          \
-    } while (0)
-
+    // TR (every product but the GLU): the weights are the first MFMA operand, so the accumulators
+    // hold the transposed blocks that store_transposed writes out from registers. The GLU pairs
+    // the two halves' sums through LDS and keeps the rows first.
+    constexpr bool TR = !GLU;
     v4i acc_hi[RB][CB], acc_lo[RB][CB];
 #pragma unroll
     for (int i = 0; i < RB; i++)
 #pragma unroll
         for (int j = 0; j < CB; j++) acc_hi[i][j] = acc_lo[i][j] = v4i{0, 0, 0, 0};
+    auto mma = [&](const v4i (&fa)[RB][2], const v4i (&fb)[CB]) {
 #pragma unroll
-    for (int s = 0; s < NS - 1; s++)
-        if (s < KB) TG_ISSUE(s, s);
-    for (int t0 = 0; t0 < KB; t0 += NS) {
+        for (int r = 0; r < RB; r++)
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            const int t = t0 + s;
-            if (t < KB) {
-                // k-block t sits in buffer s; up to NS - 2 later k-blocks may still be on the way.
-                wait_stages<CPW, NS - 2>(min(NS - 2, KB - 1 - t));
-                __syncthreads();
-                if (t + NS - 1 < KB) TG_ISSUE((s + NS - 1) % NS, t + NS - 1);
-                v4i fa[RB][2], fb[CB];
-                if constexpr (RB >= 4) {
-                    // The B fragments and the first half of the A fragments are read and waited
-                    // for; the second half's reads are issued before the first half's MFMAs, so
-                    // their LDS latency passes under those MFMAs.
-                    constexpr int H = RB / 2;
-                    read_frags_rows(smem + s * STAGE, fa, fb, 0, H, true);
-                    __builtin_amdgcn_sched_barrier(0);
-                    read_frags_rows(smem + s * STAGE, fa, fb, H, RB, false);
-                    __builtin_amdgcn_sched_barrier(0);
-                    TG_MMA_ROWS(fa, fb, 0, H);
-                    __builtin_amdgcn_sched_barrier(0);
-                    TG_MMA_ROWS(fa, fb, H, RB);
+            for (int cb = 0; cb < CB; cb++) {
+                if constexpr (TR) {
+                    acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb], fa[r][0], acc_hi[r][cb], 0, 0, 0);
+                    acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb], fa[r][1], acc_lo[r][cb], 0, 0, 0);
                 } else {
-                    read_frags(smem + s * STAGE, fa, fb);
-                    // All the reads are issued before the first MFMA, so that the LDS latency is
-                    // waited out once per k-block, not once per row block.
-                    __builtin_amdgcn_sched_barrier(0);
-                    TG_MMA(fa, fb);
+                    acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[r][0], fb[cb], acc_hi[r][cb], 0, 0, 0);
+                    acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[r][1], fb[cb], acc_lo[r][cb], 0, 0, 0);
                 }
             }
+    };
+
+    // k-block t sits in buffer t % NS. Two register sets of fragments: while the MFMAs of block t
+    // run on one, block t + 1's fragments are read into the other, so the LDS latency passes under
+    // the MFMAs. Iteration t waits for block t + 1's copies, and after the barrier (every
+    // wavefront has consumed block t - 1's fragments) reuses block t - 1's buffer for block
+    // t + NS - 1.
+    v4i fa0[RB][2], fb0[CB], fa1[RB][2], fb1[CB];
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < KB) issue(s, s);
+    wait_stages<CPW, NS - 2>(min(NS - 2, KB - 1));
+    __syncthreads();
+    read_frags(0, fa0, fb0);
+    auto step = [&](int t, const v4i (&ca)[RB][2], const v4i (&cb)[CB], v4i (&na)[RB][2], v4i (&nb)[CB]) {
+        if (t + 1 < KB) {
+            wait_stages<CPW, NS - 3>(min(NS - 3, KB - 2 - t));
+            __syncthreads();
+            if (t + NS - 1 < KB) issue((t + NS - 1) % NS, t + NS - 1);
+            read_frags((t + 1) % NS, na, nb);
         }
+        mma(ca, cb);
+    };
+    int t = 0;
+    for (; t + 1 < KB; t += 2) {
+        step(t, fa0, fb0, fa1, fb1);
+        step(t + 1, fa1, fb1, fa0, fb0);
     }
-#undef TG_ISSUE
-#undef TG_MMA
-#undef TG_MMA_ROWS
+    if (t < KB) step(t, fa0, fb0, fa1, fb1);
     if (tid < NPRE) s_pre[tid] = pre;
-    TileStore<WM, WN, C_STRIDE> out;
-    if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    if constexpr (TR) {
+        __syncthreads();  // s_pre
+        int32_t e[RB];
+        v4f sc[CB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) e[r] = (int32_t)s_pre[wm * WM + r * 16 + (lane & 15)];
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+            sc[cb] = *reinterpret_cast<const v4f *>(s_pre + TM * 16 + (wn * CB + cb) * 16 + 4 * (lane >> 4));
+        if constexpr (QOUT) {
+            // Each row's largest |y| over the workgroup's columns: over this wavefront's (the lanes
+            // of a row), then over the two wavefronts of the row (LDS).
+            __shared__ uint32_t smax[2][TM * 16];
+            uint32_t rmax[RB];
+            store_transposed<EDGE, RB, CB>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale,
+                                           accumulate, rmax);
+            if (lane < 16) {
+#pragma unroll
+                for (int r = 0; r < RB; r++) smax[wn][wm * WM + r * 16 + lane] = rmax[r];
+            }
+            __syncthreads();
+            for (int rr = tid; rr < TM * 16; rr += THREADS) {
+                const int row = by * TM * 16 + rr;
+                if (row < M) tmx.tmax[(size_t)row * tmx.strips + bx] = max(smax[0][rr], smax[1][rr]);
+            }
+        } else {
+            store_transposed<EDGE, RB, CB>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale,
+                                           accumulate);
+        }
+        return;
+    }
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
     int32_t e_row[RB][4];
     float s_col[CB];
@@ -853,27 +972,6 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_lds_kernel(const uint8_t *__r
         const float *ta = reinterpret_cast<const float *>(smem) + wm * WM * C_STRIDE + wn * (WM / 2) * C_STRIDE;
         glu_store<WM / 2, WN, C_STRIDE>(ta, ta + 2 * WM * C_STRIDE, lane, c, ldc, m0 + wn * (WM / 2), bx * WN, M,
                                         hp * 16, bias, act, escale);
-    } else if constexpr (QOUT) {
-        // The outputs as usual, and each row's largest |y| over the workgroup's columns: over the
-        // RPR lanes holding a row's runs, then over the two wavefronts of the row (LDS).
-        __shared__ uint32_t smax[2][TM * 16];
-        constexpr int PER = TileStore<WM, WN, C_STRIDE>::PER, RPR = TileStore<WM, WN, C_STRIDE>::RPR,
-                      STEP = TileStore<WM, WN, C_STRIDE>::STEP;
-        uint32_t rmax[PER];
-        out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate, rmax);
-#pragma unroll
-        for (int u = 0; u < PER; u++) {
-#pragma unroll
-            for (int off = 1; off < RPR; off <<= 1) rmax[u] = max(rmax[u], (uint32_t)__shfl_xor((int)rmax[u], off, 64));
-            if (lane % RPR == 0) smax[wn][wm * WM + lane / RPR + u * STEP] = rmax[u];
-        }
-        __syncthreads();
-        for (int rr = tid; rr < TM * 16; rr += THREADS) {
-            const int row = by * TM * 16 + rr;
-            if (row < M) tmx.tmax[(size_t)row * tmx.strips + bx] = max(smax[0][rr], smax[1][rr]);
-        }
-    } else {
-        out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
     }
 }
 
@@ -885,9 +983,18 @@ hipError_t launch_lds(const uint8_t *qf, const int32_t *exps, size_t m, const De
     // divide the half's panels).
     const size_t hp = w.panels / 2, cols = GLU ? hp / (TN / 2) : div_ceil(w.panels, (size_t)TN);
     const dim3 grid((unsigned)cols, (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
-    hipLaunchKernelGGL((gemm_lds_kernel<TM, TN, NS, XCD, G, GLU, QOUT>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
-                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
-                       epi.accumulate, w.panel_stride, w.blk_stride, (int)hp, q);
+    // The FAST-only kernel when every tile is whole in columns and the outputs and bias are 16-byte
+    // aligned; the GLU stores through LDS and has one kernel.
+    auto kernel = &gemm_lds_kernel<TM, TN, NS, XCD, G, GLU, QOUT, 0>;
+    if constexpr (!GLU) {
+        const bool fast = ((reinterpret_cast<uintptr_t>(c) | ldc * sizeof(float) |
+                            reinterpret_cast<uintptr_t>(epi.bias)) % 16) == 0 &&
+                          w.n % (TN * PANEL) == 0;
+        if (!fast) kernel = &gemm_lds_kernel<TM, TN, NS, XCD, G, GLU, QOUT, 1>;
+    }
+    hipLaunchKernelGGL(kernel, grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values, w.scales, (int)w.n,
+                       (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride,
+                       w.blk_stride, (int)hp, q);
     return hipGetLastError();
 }
 

@@ -562,6 +562,38 @@ def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
 
 
+@pytest.mark.parametrize("m,k,n,ldc,bias_off", [(4100, 64, 4100, 4103, 0), (4100, 64, 4096, 4096, 1),
+                                                 (2100, 128, 2050, 2051, 0), (2100, 128, 2048, 2048, 3)])
+def test_large_products_with_unaligned_rows_or_bias(tk, orc, m, k, n, ldc, bias_off):
+    """The LDS-staged GEMM's outputs go 16 bytes at a time only when c's rows and the bias are
+    16-byte aligned; an odd ldc or a bias starting one or three floats into its buffer takes the
+    output-at-a-time path on every tile. 128 x 128 tiles (4100 x 4100) and 64 x 64 tiles
+    (2100 x 2050); bias, accumulation and the columns past n left alone, bit-identical to the
+    integer oracle."""
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(m + n + ldc + bias_off)
+    a = normal(rng, (m, k))
+    q, s = int8_weights(rng, n, k)
+    values, scales = pack_int8(q, s)
+    bias_buf = normal(rng, n + bias_off)
+    bias = bias_buf[bias_off:]
+    c0 = normal(rng, m * ldc)
+    want = c0.copy()
+    orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, want, ldc, bias, SILU, 0.5, True)
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, values, scales)
+    cd = torch.from_numpy(c0.copy()).cuda()
+    bd = torch.from_numpy(bias_buf).cuda()[bias_off:]
+    say("unaligned", m, k, n, ldc, bias_off)
+    tk.matmul_device(torch.from_numpy(a).cuda(), k, m, w, cd, ldc,
+                     telmo_amd.Epilogue(bias=bd, act=telmo_amd.Act.SILU, scale=0.5, accumulate=True))
+    tk.synchronize()
+    assert np.array_equal(cd.cpu().numpy().view(np.uint32), want.view(np.uint32)), (m, k, n, ldc, bias_off)
+    w.close()
+
+
 @pytest.mark.parametrize("m,k,n,ldb", [(7, 128, 255, 255), (40, 128, 255, 256), (1, 33, 16, 20), (130, 300, 40, 64)])
 def test_rowmajor_right_hand_side_is_the_fused_reference(tk, orc, m, k, n, ldb):
     """BView::row_major (f32 activations as the right-hand side) gives the fused reference's bits: the
