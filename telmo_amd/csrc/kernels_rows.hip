@@ -1170,12 +1170,219 @@ __global__ __launch_bounds__(1024) void dwconv_quant_kernel(const float *__restr
     }
 }
 
+// The largest |o| of each of a lane's N rows (N a power of two up to 16) over the wavefront by
+// recursive halving: at each step a lane keeps half of its rows, sends the other half to its
+// partner and takes the partner's copy of the half it keeps (N - 1 + 6 - log2 N shuffles against
+// 6 N for one reduction per row). On return m[0] of lane l is the wavefront's maximum of row
+// sum_k b_(5-k) 2^(log2 N - 1 - k), b_i bit i of l (wave_max_row).
+template <int N>
+__device__ __forceinline__ void wave_max_rows(float (&m)[N], int lane) {
+    static_assert(N >= 1 && N <= 16 && (N & (N - 1)) == 0, "a power of two up to 16");
+#pragma unroll
+    for (int h = N / 2, off = 32; h >= 1; h >>= 1, off >>= 1) {
+        const bool up = lane & off;
+#pragma unroll
+        for (int k = 0; k < h; k++) {
+            const float send = up ? m[k] : m[k + h];
+            const float keep = up ? m[k + h] : m[k];
+            m[k] = fmaxf(keep, __shfl_xor(send, off, 64));
+        }
+    }
+    constexpr int LOG = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : 4;
+#pragma unroll
+    for (int off = 32 >> LOG; off >= 1; off >>= 1) m[0] = fmaxf(m[0], __shfl_xor(m[0], off, 64));
+}
+
+template <int N>
+__device__ __forceinline__ int wave_max_row(int lane) {
+    constexpr int LOG = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : 4;
+    return (lane >> (6 - LOG)) & (N - 1);  // the top LOG bits of the lane, bit 5 the highest
+}
+
+// The taps of dwconv_quant_block_kernel for R output rows: acc[i] (starting at the bias) += w[j] *
+// input slot i + j, for j in order. The input rows are read in batches of B, a batch's loads all
+// issued before its first use, so the wavefront waits out the memory latency once per batch.
+// FULL: every tap of every output lies inside the output's sequence and kernel = KMAX, so the taps
+// are added unconditionally from the unclamped rows; otherwise rows are clamped to the input and a
+// tap is skipped when its input row lies outside its output row's sequence or j >= kernel.
+template <bool FULL, int R, int KMAX>
+__device__ __forceinline__ void block_taps(float4 (&acc)[R], const float4 (&wr)[KMAX], const float *__restrict__ x,
+                                           size_t ldx, int64_t first, int64_t total, int cc, int kernel,
+                                           const int32_t (&lo)[R], int64_t frames) {
+    constexpr int SPAN = R - 1 + KMAX, B = 8;
+    const float *base = x + cc;
+#pragma unroll
+    for (int s0 = 0; s0 < SPAN; s0 += B) {
+        float4 v[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            if (s0 + u < SPAN) {
+                const int64_t f = first + s0 + u;
+                const int64_t fc = FULL ? f : (f < 0 ? 0 : (f >= total ? total - 1 : f));
+                v[u] = *reinterpret_cast<const float4 *>(base + (size_t)fc * ldx);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const int sl = s0 + u;
+            if (sl >= SPAN) break;
+#pragma unroll
+            for (int i = (sl - KMAX + 1 > 0 ? sl - KMAX + 1 : 0); i < (sl < R ? sl + 1 : R); i++) {
+                const int j = sl - i;  // tap j of output i; taps of one output arrive in order
+                if (FULL || (j < kernel && (uint32_t)(sl - lo[i]) < (uint32_t)frames)) {
+                    acc[i].x = acc[i].x + wr[j].x * v[u].x;
+                    acc[i].y = acc[i].y + wr[j].y * v[u].y;
+                    acc[i].z = acc[i].z + wr[j].z * v[u].z;
+                    acc[i].w = acc[i].w + wr[j].w * v[u].w;
+                }
+            }
+        }
+    }
+}
+
+// dwconv_quant_kernel for whole QA row blocks of 4 to 1024 channels (a multiple of 4) with 16-byte
+// aligned rows, taps and bias, and kernel <= 9. Workgroup b takes output rows 16 b .. 16 b + 15:
+// 16 / RT groups of W threads (W = 16 kb rounded up to whole wavefronts, kb the k-blocks of a
+// row), thread j of group q taking channels 4 j .. 4 j + 3 of rows RT q .. RT q + RT - 1 (threads
+// past the last channel hold zeros). The thread reads each of the RT + kernel - 1 input rows its
+// outputs reach once (a 16-byte load) and adds it into the outputs it feeds, tap j of output i
+// being input slot i + j, so every output still sums its taps in order from the bias (a tap
+// outside its output row's sequence skipped); the outputs stay in registers (no LDS tile). After
+// the SiLU, the row maxima and non-finite flags are reduced over the workgroup, each thread packs
+// the digits of its four channels of each of its rows into LDS (rows 16 kb + 4 dwords apart: hi
+// rows, then lo rows), and the workgroup copies the row block's QA bytes (kb x 2 KB, contiguous)
+// out in 16-byte stores, consecutive lanes writing consecutive bytes. The same values, exponents
+// and digits as dwconv_quant_kernel.
+template <int RT, int KMAX>
+__global__ __launch_bounds__(1024) void dwconv_quant_block_kernel(const float *__restrict__ x, size_t ldx,
+                                                                  int64_t frames, int64_t total, int channels,
+                                                                  const float *__restrict__ w, int kernel,
+                                                                  const float *__restrict__ bias, int silu,
+                                                                  float *__restrict__ out, size_t ldo,
+                                                                  uint8_t *__restrict__ qa,
+                                                                  int32_t *__restrict__ exps, int kb, size_t bpx) {
+    constexpr int R = 16, G = R / RT;
+    static_assert(R % RT == 0, "whole row groups");
+    extern __shared__ __attribute__((aligned(16))) uint32_t stage[];  // [2][R][16 kb + 4]
+    __shared__ float s_max[16][R];
+    __shared__ int s_bad[16];
+    __shared__ int32_t s_e[R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int W = (int)(blockDim.x / G), wpg = W >> 6;  // threads and wavefronts per row group
+    const int cq = tid % W, rq = tid / W;                // rq is wave-uniform
+    const int rs = 16 * kb + 4;                          // staged row stride, dwords
+    // Workgroup L runs on XCD L % 8; each XCD takes a contiguous run of row blocks.
+    const size_t blk = (blockIdx.x % 8) * bpx + blockIdx.x / 8;
+    const int64_t g0 = (int64_t)blk * R;
+    if (g0 >= total) return;  // uniform over the workgroup
+    const int64_t r0 = g0 + RT * rq;  // this thread's first output row
+    const int half = kernel / 2;
+    const int64_t first = r0 - half;  // the input row of window slot 0
+    // The first row of each output row's sequence as a window slot (wave-uniform).
+    int32_t lo[RT];
+    {
+        int64_t s = (r0 / frames) * frames;
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            while (r0 + i >= s + frames) s += frames;
+            lo[i] = (int32_t)(s - first);
+        }
+    }
+    const bool inner = lo[0] <= 0 && (RT - 1) + (kernel - 1) < lo[0] + frames;
+    const int c = 4 * cq;
+    const bool live = c < channels;
+    const int cc = live ? c : channels - 4;  // idle lanes read valid channels and keep nothing
+    float4 wr[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; j++)
+        wr[j] = *reinterpret_cast<const float4 *>(w + (size_t)(j < kernel ? j : kernel - 1) * channels + cc);
+    float4 acc[RT];
+    {
+        const float4 b = *reinterpret_cast<const float4 *>(bias + cc);
+#pragma unroll
+        for (int i = 0; i < RT; i++) acc[i] = b;
+    }
+    if (inner && kernel == KMAX)
+        block_taps<true>(acc, wr, x, ldx, first, total, cc, kernel, lo, frames);
+    else
+        block_taps<false>(acc, wr, x, ldx, first, total, cc, kernel, lo, frames);
+    float m[RT];
+    int rbad = 0;
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        float4 o = acc[i];
+        if (silu) {
+            o.x = o.x / (1.0f + exp_simd(0.0f - o.x));
+            o.y = o.y / (1.0f + exp_simd(0.0f - o.y));
+            o.z = o.z / (1.0f + exp_simd(0.0f - o.z));
+            o.w = o.w / (1.0f + exp_simd(0.0f - o.w));
+        }
+        const bool ok = live && r0 + i < total;
+        if (ok && out) *reinterpret_cast<float4 *>(out + (size_t)(r0 + i) * ldo + c) = o;
+        acc[i] = ok ? o : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        m[i] = fmaxf(fmaxf(fabsf(acc[i].x), fabsf(acc[i].y)), fmaxf(fabsf(acc[i].z), fabsf(acc[i].w)));
+        const bool fin = __builtin_isfinite(acc[i].x) && __builtin_isfinite(acc[i].y) &&
+                         __builtin_isfinite(acc[i].z) && __builtin_isfinite(acc[i].w);
+        rbad |= (int)!fin << i;
+    }
+    wave_max_rows<RT>(m, lane);
+    rbad = wave_or(rbad);
+    {
+        constexpr int LOG = RT == 1 ? 0 : RT == 2 ? 1 : RT == 4 ? 2 : RT == 8 ? 3 : 4;
+        if ((lane & ((64 >> LOG) - 1)) == 0) s_max[wave][RT * rq + wave_max_row<RT>(lane)] = m[0];
+    }
+    if (lane == 0) s_bad[wave] = rbad;
+    __syncthreads();
+    if (tid < R) {
+        // row tid: the wavefronts of its row group
+        const int q0 = (tid / RT) * wpg;
+        float mx = 0.0f;
+        int b = 0;
+        for (int q = q0; q < q0 + wpg; q++) {
+            mx = fmaxf(mx, s_max[q][tid]);
+            b |= s_bad[q];
+        }
+        const bool valid = g0 + tid < total;
+        const int32_t e = !valid ? 0 : (((b >> (tid % RT)) & 1) ? EXP_NONFINITE : row_exponent_of(mx));
+        s_e[tid] = e;
+        if (valid) exps[g0 + tid] = e;
+    }
+    __syncthreads();
+    if (cq < 16 * kb) {
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const int row = RT * rq + i;
+            uint32_t h, l;
+            digits4(acc[i].x, acc[i].y, acc[i].z, acc[i].w, s_e[row], h, l);
+            stage[row * rs + cq] = h;
+            stage[(R + row) * rs + cq] = l;
+        }
+    }
+    __syncthreads();
+    // Chunk q of the row block's QA bytes (16 bytes at q * 16): k-block t = q / 128, digit
+    // d = q / 64 % 2, 16-input group g = q / 16 % 4, row r = q % 16.
+    uint8_t *dst = qa + (size_t)blk * kb * 2048;
+    for (int q = tid; q < 128 * kb; q += blockDim.x) {
+        const int r = q & 15, g = (q >> 4) & 3, d = (q >> 6) & 1, t = q >> 7;
+        const uint4 v = *reinterpret_cast<const uint4 *>(stage + (d * R + r) * rs + 16 * t + 4 * g);
+        *reinterpret_cast<uint4 *>(dst + (size_t)q * 16) = v;
+    }
+}
+
 bool dwconv_quant_fits(size_t channels, size_t kernel) {
     return channels >= 1 && channels <= 2048 && kernel >= 1 && kernel <= 32;
 }
 
 // Rows below which the four-row workgroups take the call (fewer than two 16-row workgroups per CU).
 constexpr size_t DQ_SMALL = 8192;
+// Rows from which dwconv_quant_block_kernel takes the calls it fits, and from which it runs eight
+// rows per thread (two workgroups per CU) rather than four (one). 1024 x 9 taps with SiLU, in us:
+//   rows         750   1500   3000   7500   12000
+//   row slices   8.5   12.3   17.7   36.4    58.6   (dwconv_quant_kernel)
+//   4 per thread 10.1  10.7   11.7   22.5    33.3
+//   8 per thread 11.1  12.6   13.7   21.5    30.7
+constexpr size_t DQ_BLOCK_ROWS = 1024, DQ_RT8_ROWS = 6144;
 
 hipError_t launch_dwconv_quant(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels,
                                const float *w, size_t kernel, const float *bias, int silu, float *out, size_t ldo,
@@ -1184,6 +1391,23 @@ hipError_t launch_dwconv_quant(const float *x, size_t ldx, size_t frames, size_t
     if (total == 0 || channels == 0) return hipSuccess;
     if (!dwconv_quant_fits(channels, kernel)) return hipErrorInvalidValue;
     const size_t kb = div_ceil(channels, (size_t)KBLK);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                           reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(out)) % 16) == 0 &&
+                         ldx % 4 == 0 && (!out || ldo % 4 == 0);
+    if (total >= DQ_BLOCK_ROWS && kernel <= 9 && channels % 4 == 0 && channels <= 1024 && aligned) {
+        const size_t bpx = div_ceil(div_ceil(total, (size_t)16), (size_t)8);
+        const size_t lds = 2 * 16 * (16 * kb + 4) * sizeof(uint32_t);  // at most 33 KB
+        const unsigned wg = (unsigned)div_ceil(16 * kb, (size_t)64) * 64;  // a row group, whole wavefronts
+        if (total >= DQ_RT8_ROWS)
+            hipLaunchKernelGGL((dwconv_quant_block_kernel<8, 9>), dim3((unsigned)(8 * bpx)), dim3(2 * wg), lds, s, x,
+                               ldx, (int64_t)frames, (int64_t)total, (int)channels, w, (int)kernel, bias, silu, out,
+                               ldo, qa, exps, (int)kb, bpx);
+        else
+            hipLaunchKernelGGL((dwconv_quant_block_kernel<4, 9>), dim3((unsigned)(8 * bpx)), dim3(4 * wg), lds, s, x,
+                               ldx, (int64_t)frames, (int64_t)total, (int)channels, w, (int)kernel, bias, silu, out,
+                               ldo, qa, exps, (int)kb, bpx);
+        return hipGetLastError();
+    }
     const size_t rows = total < DQ_SMALL ? 4 : 16;
     const size_t bpx = div_ceil(div_ceil(total, rows), (size_t)8);
     const dim3 grid((unsigned)(8 * bpx));

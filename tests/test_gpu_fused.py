@@ -193,10 +193,23 @@ def test_quantised_output_refusals(tk):
 # batch, frames, channels, kernel, silu, with_out, ldx. Row blocks of 16 that straddle sequences
 # (375, 20, 7 frames), sequences shorter than a block, channels past 1024 (two slices) and not a
 # multiple of 64, 9 / 16 / 31 taps, a NaN and an infinity in the input.
-DWQ_CASES = [(1, 750, 1024, 9, True, False, 1024), (32, 375, 1024, 9, True, False, 1024),
-             (5, 20, 64, 9, True, True, 64), (9, 7, 100, 16, False, True, 104), (3, 40, 1000, 31, True, True, 1000),
+# batch, frames, channels, kernel, silu, with_out, ldx. From 1024 rows, calls with channels a
+# multiple of 4 up to 1024, kernel <= 9 and 16-byte aligned rows take the whole-block kernel, four
+# rows per thread below 6144 rows and eight from there: the second group (sequences straddling
+# blocks, 5 taps with an f32 output and a padded stride, a single tap, sequences of two frames
+# under nine taps, an even kernel on 64 channels) and the third (12000 rows; sequences of nine
+# frames, shorter than a block, with an f32 output). The rest take the row-slice kernel: four-row
+# workgroups below 8192 rows, the last case 16-row ones.
+DWQ_CASES = [(1, 750, 1024, 9, True, False, 1024), (5, 20, 64, 9, True, True, 64),
+
+             (4, 375, 1024, 9, True, False, 1024), (30, 45, 1000, 5, False, True, 1004),
+             (100, 13, 256, 1, True, False, 256), (520, 2, 512, 9, True, True, 516), (40, 30, 64, 4, True, False, 68),
+
+             (32, 375, 1024, 9, True, False, 1024), (700, 9, 128, 9, True, True, 132),
+
+             (9, 7, 100, 16, False, True, 104), (3, 40, 1000, 31, True, True, 1000),
              (2, 33, 2048, 9, True, True, 2048), (4, 16, 1500, 5, False, False, 1504), (1, 1, 3, 3, True, True, 3),
-             (2, 50, 130, 1, True, False, 130)]
+             (2, 50, 130, 1, True, False, 130), (40, 210, 1500, 9, True, False, 1500)]
 
 
 @pytest.mark.parametrize("case", DWQ_CASES)
