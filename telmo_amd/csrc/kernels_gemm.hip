@@ -244,8 +244,11 @@ __device__ __forceinline__ void stage_sums(float *tile, const v4i (&acc_hi)[RB][
 //
 // FAST (a wave-uniform choice): every column of the wavefront lies below N and c, ldc and bias
 // are 16-byte aligned, so the bias, the old outputs and the outputs move 16 bytes at a time with
-// no column checks. Otherwise they move one output at a time, columns past N skipped.
-template <bool FAST, int RB, int CB>
+// no column checks. Otherwise they move one output at a time, columns past N skipped. FITS: every
+// sum of the wavefront takes dequant_i32 (else dequant); ACT: the activation (ACT_ANY: act).
+// Both are wave-uniform and chosen once before the unrolled loops, which then hold no branch per
+// output: with the choices inside, the epilogue of a 128 x 128 tile ran 700 branches.
+template <bool FAST, bool FITS, uint32_t ACT, int RB, int CB>
 __device__ __forceinline__ void store_transposed_as(const v4i (&acc_hi)[RB][CB], const v4i (&acc_lo)[RB][CB],
                                                     const int32_t (&e)[RB], const v4f (&sc)[CB], int lane,
                                                     float *__restrict__ c, size_t ldc, int m0, int n0, int M, int N,
@@ -266,7 +269,6 @@ __device__ __forceinline__ void store_transposed_as(const v4i (&acc_hi)[RB][CB],
             }
         }
     }
-    const bool fits = wave_fits_i32<RB, CB>(acc_hi);
 #pragma unroll
     for (int r = 0; r < RB; r++) {
         const int row = m0 + 16 * r + mr;
@@ -294,9 +296,9 @@ __device__ __forceinline__ void store_transposed_as(const v4i (&acc_hi)[RB][CB],
                 v4f v;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float d = fits ? dequant_i32(acc_hi[r][cb][j], acc_lo[r][cb][j], e[r], sc[cb][j])
+                    const float d = FITS ? dequant_i32(acc_hi[r][cb][j], acc_lo[r][cb][j], e[r], sc[cb][j])
                                          : dequant(acc_hi[r][cb][j], acc_lo[r][cb][j], e[r], sc[cb][j]);
-                    v[j] = epilogue_vals(d, bias != nullptr, b[cb][j], act, escale, accumulate != 0, old[cb][j]);
+                    v[j] = epilogue_sel<ACT>(d, bias != nullptr, b[cb][j], act, escale, accumulate != 0, old[cb][j]);
                     if (rmax && (FAST || col + j < N))
                         mx = max(mx, __builtin_isfinite(v[j]) ? __float_as_uint(fabsf(v[j])) : 0xffffffffu);
                 }
@@ -330,12 +332,21 @@ __device__ __forceinline__ void store_transposed(const v4i (&acc_hi)[RB][CB], co
     const bool fast = !EDGE || (((reinterpret_cast<uintptr_t>(c) | ldc * sizeof(float) |
                                   reinterpret_cast<uintptr_t>(bias)) % 16) == 0 &&
                                 n0 + 16 * CB <= N);
-    if (fast)
-        store_transposed_as<true>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale, accumulate,
-                                  rmax);
-    else
-        store_transposed_as<false>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale, accumulate,
-                                   rmax);
+    const bool fits = wave_fits_i32<RB, CB>(acc_hi);
+#define TG_ST(F, I, A)                                                                                          \
+    store_transposed_as<F, I, A>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale, accumulate, \
+                                 rmax)
+#define TG_ST_ACTS(F)                              \
+    do {                                           \
+        if (!fits) TG_ST(F, false, ACT_ANY);       \
+        else if (act == ACT_NONE) TG_ST(F, true, ACT_NONE); \
+        else if (act == ACT_RELU) TG_ST(F, true, ACT_RELU); \
+        else TG_ST(F, true, ACT_SILU);             \
+    } while (0)
+    if (fast) TG_ST_ACTS(true);
+    else TG_ST_ACTS(false);
+#undef TG_ST_ACTS
+#undef TG_ST
 }
 
 template <int RB, int CB, int S, int OCC, int XCD, int G>

@@ -96,6 +96,26 @@ __device__ __forceinline__ float epilogue_vals(float v, bool has_bias, float b, 
     return v;
 }
 
+// epilogue_vals with the activation fixed at compile time (ACT <= ACT_SILU; ACT = ACT_ANY reads act)
+// and the bias and accumulation taken by selects rather than branches, so that an unrolled
+// epilogue over many outputs has no branch per output. The same operations in the same order.
+constexpr uint32_t ACT_ANY = 3;
+template <uint32_t ACT>
+__device__ __forceinline__ float epilogue_sel(float v, bool has_bias, float b, uint32_t act, float scale,
+                                              bool accumulate, float old) {
+    const float vb = v + b;
+    v = has_bias ? vb : v;
+    const uint32_t a = ACT == ACT_ANY ? act : ACT;
+    if (a == ACT_RELU) {
+        v = v > 0.0f ? v : 0.0f;
+    } else if (a == ACT_SILU) {
+        v = v / (1.0f + exp_simd(0.0f - v));
+    }
+    v = v * scale;
+    const float va = old + v;
+    return accumulate ? va : v;
+}
+
 __device__ __forceinline__ float epilogue(float v, const float *bias, size_t col, uint32_t act, float scale,
                                           bool accumulate, const float *cptr) {
     return epilogue_vals(v, bias != nullptr, bias ? bias[col] : 0.0f, act, scale, accumulate,
