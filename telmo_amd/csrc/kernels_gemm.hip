@@ -98,10 +98,12 @@ struct TileStore {
     }
 
     // With rmax, also each run's largest |y| over its columns below N, as unsigned bits (all ones
-    // for a NaN or an infinity; 0 for rows past M).
-    __device__ __forceinline__ void finish(const float *tile, float *__restrict__ c, size_t ldc, int m0, int M, int N,
-                                           bool has_bias, uint32_t act, float escale, int accumulate,
-                                           uint32_t *rmax = nullptr) {
+    // for a NaN or an infinity; 0 for rows past M). ACT: the activation, fixed at compile time
+    // (finish() dispatches on act once) so that the unrolled runs hold no branch per output.
+    template <uint32_t ACT>
+    __device__ __forceinline__ void finish_act(const float *tile, float *__restrict__ c, size_t ldc, int m0, int M,
+                                               int N, bool has_bias, float escale, int accumulate,
+                                               uint32_t *rmax) {
         if constexpr (!EARLY) load_old(c, ldc, m0, M, N, accumulate);
 #pragma unroll
         for (int u = 0; u < PER; u++) {
@@ -111,7 +113,7 @@ struct TileStore {
             v4f v = *reinterpret_cast<const v4f *>(tile + (r0 + u * STEP) * C_STRIDE + 4 * cr);
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                v[j] = epilogue_vals(v[j], has_bias, b[j], act, escale, accumulate != 0, old[u][j]);
+                v[j] = epilogue_sel<ACT>(v[j], has_bias, b[j], ACT, escale, accumulate != 0, old[u][j]);
             if (rmax) {
                 uint32_t mx = 0u;
 #pragma unroll
@@ -130,6 +132,14 @@ struct TileStore {
             }
         }
     }
+
+    __device__ __forceinline__ void finish(const float *tile, float *__restrict__ c, size_t ldc, int m0, int M, int N,
+                                           bool has_bias, uint32_t act, float escale, int accumulate,
+                                           uint32_t *rmax = nullptr) {
+        if (act == ACT_NONE) finish_act<ACT_NONE>(tile, c, ldc, m0, M, N, has_bias, escale, accumulate, rmax);
+        else if (act == ACT_RELU) finish_act<ACT_RELU>(tile, c, ldc, m0, M, N, has_bias, escale, accumulate, rmax);
+        else finish_act<ACT_SILU>(tile, c, ldc, m0, M, N, has_bias, escale, accumulate, rmax);
+    }
 };
 
 // The GLU of a pair of staged tiles, the a and b halves of the same rows and columns (rows
@@ -137,10 +147,10 @@ struct TileStore {
 // the epilogue (bias, activation, scale; no accumulation), the values tg_linear_device writes and
 // tg_glu_device then combines. The b half's bias sits Nh columns on. Runs of four outputs per lane
 // as TileStore, 16-byte nontemporal stores when out's rows are 16-byte aligned.
-template <int WM, int WN, int C_STRIDE>
-__device__ __forceinline__ void glu_store(const float *ta, const float *tb, int lane, float *__restrict__ out,
-                                          size_t ldo, int m0, int n0, int M, int Nh, const float *__restrict__ bias,
-                                          uint32_t act, float escale) {
+template <uint32_t ACT, int WM, int WN, int C_STRIDE>
+__device__ __forceinline__ void glu_store_act(const float *ta, const float *tb, int lane, float *__restrict__ out,
+                                              size_t ldo, int m0, int n0, int M, int Nh, const float *__restrict__ bias,
+                                              float escale) {
     constexpr int RPR = WN / 4, STEP = 64 / RPR, PER = WM / STEP;
     static_assert(WN % 4 == 0 && 64 % RPR == 0 && WM % STEP == 0, "whole runs per lane");
     const int cr = lane % RPR, r0 = lane / RPR, col = n0 + 4 * cr;
@@ -163,8 +173,8 @@ __device__ __forceinline__ void glu_store(const float *ta, const float *tb, int 
         v4f o;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const float va = epilogue_vals(a[j], bias != nullptr, ba[j], act, escale, false, 0.0f);
-            const float vb = epilogue_vals(b[j], bias != nullptr, bb[j], act, escale, false, 0.0f);
+            const float va = epilogue_sel<ACT>(a[j], bias != nullptr, ba[j], ACT, escale, false, 0.0f);
+            const float vb = epilogue_sel<ACT>(b[j], bias != nullptr, bb[j], ACT, escale, false, 0.0f);
             o[j] = va / (1.0f + exp_simd(0.0f - vb));
         }
         float *dst = out + (size_t)row * ldo + col;
@@ -176,6 +186,18 @@ __device__ __forceinline__ void glu_store(const float *ta, const float *tb, int 
                 if (col + j < Nh) dst[j] = o[j];
         }
     }
+}
+
+// glu_store_act with the activation chosen once.
+template <int WM, int WN, int C_STRIDE>
+__device__ __forceinline__ void glu_store(const float *ta, const float *tb, int lane, float *__restrict__ out,
+                                          size_t ldo, int m0, int n0, int M, int Nh, const float *__restrict__ bias,
+                                          uint32_t act, float escale) {
+#define TG_GLU(A) glu_store_act<A, WM, WN, C_STRIDE>(ta, tb, lane, out, ldo, m0, n0, M, Nh, bias, escale)
+    if (act == ACT_NONE) TG_GLU(ACT_NONE);
+    else if (act == ACT_RELU) TG_GLU(ACT_RELU);
+    else TG_GLU(ACT_SILU);
+#undef TG_GLU
 }
 
 // Order in which workgroups take tiles. Workgroup L of a launch goes to XCD L % 8 (each XCD has
