@@ -95,11 +95,16 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restr
 // XCD L % 8 and takes row 16 (x bpx + i / 16) + i % 16 with x = L % 8, i = L / 8, bpx = row blocks
 // per XCD. The row block's lines are then filled in one L2 instead of written back in pieces by
 // several. Workgroups past the last row exit at once.
-template <int J>
+//
+// MODE: 0 the identity; otherwise f = RowAct{act, scale} with act ACT_NONE (1), ACT_RELU (2) or
+// ACT_SILU (3) fixed at compile time and applied to every value of a chunk with no branch (the
+// chunk's values past k are zeros, which every f maps to a zero digit); a runtime act inside the
+// unrolled chunks cost a branch per value.
+template <int J, int MODE>
 __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__restrict__ a, size_t lda, int k,
                                                                  int kb, uint8_t *__restrict__ qa,
                                                                  int32_t *__restrict__ exps, int vec, size_t m,
-                                                                 size_t bpx, RowAct f) {
+                                                                 size_t bpx, float scale) {
     __shared__ float s_max[4];
     __shared__ int s_bad[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -121,11 +126,12 @@ __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__
             v[j].z = k0 + 2 < k ? ar[k0 + 2] : 0.0f;
             v[j].w = k0 + 3 < k ? ar[k0 + 3] : 0.0f;
         }
-        if (f.act != ACT_NONE || f.scale != 1.0f) {
-            if (k0 < k) v[j].x = f(v[j].x);
-            if (k0 + 1 < k) v[j].y = f(v[j].y);
-            if (k0 + 2 < k) v[j].z = f(v[j].z);
-            if (k0 + 3 < k) v[j].w = f(v[j].w);
+        if constexpr (MODE != 0) {
+            constexpr uint32_t A = MODE == 1 ? ACT_NONE : MODE == 2 ? ACT_RELU : ACT_SILU;
+            v[j].x = epilogue_sel<A>(v[j].x, false, 0.0f, A, scale, false, 0.0f);
+            v[j].y = epilogue_sel<A>(v[j].y, false, 0.0f, A, scale, false, 0.0f);
+            v[j].z = epilogue_sel<A>(v[j].z, false, 0.0f, A, scale, false, 0.0f);
+            v[j].w = epilogue_sel<A>(v[j].w, false, 0.0f, A, scale, false, 0.0f);
         }
         bad |= !__builtin_isfinite(v[j].x) | !__builtin_isfinite(v[j].y) | !__builtin_isfinite(v[j].z) |
                !__builtin_isfinite(v[j].w);
@@ -161,8 +167,13 @@ template <int J>
 void launch_regs(const float *a, size_t lda, size_t m, size_t k, size_t kb, uint8_t *qa, int32_t *exps, int vec,
                  const RowAct &f, hipStream_t s) {
     const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
-    hipLaunchKernelGGL(quantize_rows_regs_kernel<J>, dim3((unsigned)(8 * bpx * 16)), dim3(256), 0, s, a, lda, (int)k,
-                       (int)kb, qa, exps, vec, m, bpx, f);
+    const int mode = f.act == ACT_NONE ? (f.scale == 1.0f ? 0 : 1) : f.act == ACT_RELU ? 2 : 3;
+    auto kernel = &quantize_rows_regs_kernel<J, 0>;
+    if (mode == 1) kernel = &quantize_rows_regs_kernel<J, 1>;
+    else if (mode == 2) kernel = &quantize_rows_regs_kernel<J, 2>;
+    else if (mode == 3) kernel = &quantize_rows_regs_kernel<J, 3>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)(8 * bpx * 16)), dim3(256), 0, s, a, lda, (int)k, (int)kb, qa, exps,
+                       vec, m, bpx, f.scale);
 }
 
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,

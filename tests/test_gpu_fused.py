@@ -79,14 +79,16 @@ def test_layer_norm_quant_is_layer_norm_then_quantise(tk, m, n, ldx):
     assert torch.equal(qa2, want_qa)
 
 
-# m, k, n, act, with_bias, scale. An activation or a scale other than 1 is applied by the quantiser as
-# it loads the product's biased sums; the identity map takes the row maxima from the product.
+# m, k, n, act, with_bias, scale. From 2048 rows an activation or a scale other than 1 is applied by
+# the quantiser as it loads the product's biased sums (SiLU, ReLU with a scale, a negative scale
+# alone); otherwise the quantiser takes the row maxima from the product.
 QOUT_CASES = [
     (750, 1024, 4096, 2, False, 1.0), (12000, 1024, 4096, 2, False, 1.0), (7500, 1024, 4096, 2, False, 0.75),
     (750, 1024, 4096, 0, True, 1.0), (12000, 1024, 4096, 0, False, 1.0),
     (37, 200, 130, 0, True, 0.75), (37, 200, 130, 0, True, 1.0), (130, 64, 200, 1, True, 0.75),
     (1, 100, 64, 2, False, -2.0), (300, 1000, 1000, 1, True, 1.0), (5000, 256, 100, 0, False, 1.0),
-    (2100, 640, 4100, 2, True, 0.75), (64, 4096, 1024, 0, False, 1.0), (5, 64, 17000, 2, True, 1.0)]
+    (2100, 640, 4100, 2, True, 0.75), (64, 4096, 1024, 0, False, 1.0), (5, 64, 17000, 2, True, 1.0),
+    (3000, 128, 640, 1, True, 0.5), (2500, 64, 300, 0, True, -1.5)]
 
 
 @pytest.mark.parametrize("m,k,n,act,with_bias,scale", QOUT_CASES)
