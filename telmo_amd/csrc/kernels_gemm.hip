@@ -13,12 +13,15 @@
 //                      they fill the chip twice over, 64 x 64 tiles for products of >= 2048 outputs;
 //                      the sums come out transposed and are stored from registers (store_transposed);
 //   gemm_i8_kernel     2 x 2 independent wavefronts loading their operands straight into a
-//                      register ring (no LDS, no barriers in the loop): narrower products;
+//                      register ring (no LDS, no barriers): narrower products; its sums come out
+//                      transposed and are stored from registers too (750 x 1024 -> 1024:
+//                      7.5 -> 6.7 us);
 //   gemm_i8_kq_kernel  the narrower products with long inputs: each wavefront takes the whole
 //                      64 x 64 tile over a quarter of the k-blocks, and the integer partial sums
 //                      meet in LDS.
-// The other two stage their sums in LDS and store them through TileStore. launch_gemm_i8 at the
-// end picks one by shape.
+// The k-split kernel, whose partial sums meet in LDS anyway, stages its sums there and stores them
+// through TileStore (the register-stored form was 0.5 us slower on it). launch_gemm_i8 at the end
+// picks one by shape.
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -381,26 +384,25 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
                                                                float escale, int accumulate, size_t b_panel,
                                                                size_t b_blk) {
     constexpr int WM = RB * 16, WN = CB * 16;
-    constexpr int C_STRIDE = WN + 4;  // f32 per row of a wavefront's staged tile
-    __shared__ __attribute__((aligned(16))) float staged[4][WM * C_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     int bx, by;
     tile_of<XCD, G>(bx, by);
     const int m0 = by * 2 * WM + wm * WM, n0 = bx * 2 * WN + wn * WN;
     const int R0 = m0 / 16, P0 = n0 / 16, RLAST = (M + 15) / 16 - 1;
-    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
 
-    // The epilogue's row exponents and column scales, fetched first so their latency hides under
-    // the main loop. Rows and columns past the edge read the last valid one and are never stored.
-    int32_t e_row[RB][4];
-    float s_col[CB];
+    // The epilogue's row exponents and column scales (the transposed blocks' layout: lane l holds
+    // row l % 16 and columns 4 (l / 16) + [0, 4) of each block), fetched first so their latency
+    // hides under the main loop. Rows and columns past the edge read the last valid one and are
+    // never stored.
+    int32_t e[RB];
+    v4f sc[CB];
 #pragma unroll
-    for (int r = 0; r < RB; r++)
+    for (int r = 0; r < RB; r++) e[r] = exps[min(m0 + r * 16 + (lane & 15), M - 1)];
 #pragma unroll
-        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
+    for (int cb = 0; cb < CB; cb++)
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
+        for (int v = 0; v < 4; v++) sc[cb][v] = scales[min(n0 + cb * 16 + 4 * (lane >> 4) + v, P * 16 - 1)];
 
     // Operand blocks of this wavefront: row block R of the QA at (R * KB + t) * 2048 (+1024 for
     // the lo digits), panel p of the weights at p * b_panel + t * b_blk.
@@ -432,8 +434,8 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
     do {                                                                                               \
         _Pragma("unroll") for (int r = 0; r < RB; r++)                                                 \
             _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                        \
-                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[st][r][0], fb[st][cb], acc_hi[r][cb], 0, 0, 0); \
-                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[st][r][1], fb[st][cb], acc_lo[r][cb], 0, 0, 0); \
+                acc_hi[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[st][cb], fa[st][r][0], acc_hi[r][cb], 0, 0, 0); \
+                acc_lo[r][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[st][cb], fa[st][r][1], acc_lo[r][cb], 0, 0, 0); \
             }                                                                                          \
     } while (0)
 
@@ -458,14 +460,9 @@ __global__ __launch_bounds__(THREADS, OCC) void gemm_i8_kernel(const uint8_t *__
 #undef TG_LOAD
 #undef TG_MMA
 
-    // Epilogue: the wavefront stages its f32 sums in LDS (element v of lane l holds row
-    // 4 (l / 16) + v, column l % 16 of its 16 x 16 block), then stores them in 16-byte runs.
-    TileStore<WM, WN, C_STRIDE> out;
-    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
-    float *tile = staged[wave];
-    stage_sums<RB, CB, C_STRIDE>(tile, acc_hi, acc_lo, e_row, s_col, out_row, out_col);
-    __syncthreads();
-    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+    // Epilogue: the weights were the MFMAs' first operand, so each lane holds four consecutive
+    // columns of one row per block and stores them from registers.
+    store_transposed<1, RB, CB>(acc_hi, acc_lo, e, sc, lane, c, ldc, m0, n0, M, N, bias, act, escale, accumulate);
 }
 
 template <int RB, int CB, int S, int OCC, int XCD, int G>
