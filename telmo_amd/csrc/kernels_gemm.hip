@@ -17,8 +17,8 @@
 //                      transposed and are stored from registers too (750 x 1024 -> 1024:
 //                      7.5 -> 6.7 us);
 //   gemm_i8_kq_kernel  the narrower products with long inputs: each wavefront takes the whole
-//                      64 x 64 tile over a quarter of the k-blocks, and the integer partial sums
-//                      meet in LDS.
+//                      48 x 64 or 64 x 64 tile over a quarter of the k-blocks, and the integer
+//                      partial sums meet in LDS.
 // The k-split kernel, whose partial sums meet in LDS anyway, stages its sums there and stores them
 // through TileStore (the register-stored form was 0.5 us slower on it). launch_gemm_i8 at the end
 // picks one by shape.
@@ -32,6 +32,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int THREADS = 256;
+constexpr size_t GFX950_CUS = 256;  // compute units of an MI355X
 
 // Whether every hi sum of the wavefront's RB x CB accumulators takes dequant_i32 (one vote).
 template <int RB, int CB>
@@ -483,7 +484,7 @@ hipError_t launch_tile(const uint8_t *qf, const int32_t *exps, size_t m, const D
 // the 2 x 2 kernel loads each twice. The four integer partial sums are then combined through LDS:
 // wavefront q keeps row block q, receives the other three wavefronts' sums for it and stores its
 // 16 x 64 strip. The sums are exact integers, so the split changes no result.
-template <int S, int XCD, int G>
+template <int RB, int S, int XCD, int G>
 __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *__restrict__ qf,
                                                                 const int32_t *__restrict__ exps, int M,
                                                                 const uint8_t *__restrict__ wv,
@@ -492,7 +493,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *_
                                                                 const float *__restrict__ bias, uint32_t act,
                                                                 float escale, int accumulate, size_t b_panel,
                                                                 size_t b_blk) {
-    constexpr int RB = 4, CB = 4, WN = CB * 16, C_STRIDE = WN + 4;
+    static_assert(RB == 3 || RB == 4, "three or four row blocks: wavefront q < RB stores row block q");
+    constexpr int CB = 4, WN = CB * 16, C_STRIDE = WN + 4;
     constexpr int SLOT = CB * 2 * 64;          // v4i per partial strip (one row block, hi and lo)
     constexpr int PARTS = RB * 3 * SLOT * 16;  // bytes: three strips for each row block
     constexpr int STAGE = 16 * C_STRIDE * 4;   // bytes of one wavefront's staged strip
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *_
     int32_t e_row[4];
     float s_col[CB];
 #pragma unroll
-    for (int v = 0; v < 4; v++) e_row[v] = exps[min(m0 + q * 16 + out_row + v, M - 1)];
+    for (int v = 0; v < 4; v++) e_row[v] = exps[min(m0 + min(q, RB - 1) * 16 + out_row + v, M - 1)];
 #pragma unroll
     for (int cb = 0; cb < CB; cb++) s_col[cb] = scales[min(n0 + cb * 16 + out_col, P * 16 - 1)];
 
@@ -565,8 +567,12 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *_
 #undef TG_LOAD
 #undef TG_MMA
 
+    // Wavefront q stores row block q; with three row blocks the fourth only contributes partials
+    // (it still takes part in every barrier), its rows clamped to the tile's end, never stored.
+    const bool stores = q < RB;
+    const int mq = stores ? m0 + q * 16 : M;
     TileStore<16, WN, C_STRIDE> out;
-    out.begin(lane, c, ldc, m0 + q * 16, n0, M, N, bias, accumulate);
+    out.begin(lane, c, ldc, mq, n0, M, N, bias, accumulate);
 
     // Row block r's strip from wavefront w != r goes to slot (r, w - (w > r)).
     v4i *part = reinterpret_cast<v4i *>(smem);
@@ -595,7 +601,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *_
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < 3; w++) {
-        const v4i *slot = part + (q * 3 + w) * SLOT;
+        const v4i *slot = part + (min(q, RB - 1) * 3 + w) * SLOT;
 #pragma unroll
         for (int cb = 0; cb < CB; cb++) {
             mine_hi[cb] += slot[(cb * 2) * 64 + lane];
@@ -617,14 +623,14 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_i8_kq_kernel(const uint8_t *_
         stage_sums<1, CB, C_STRIDE>(tile, hi1, lo1, e1, s_col, out_row, out_col);
     }
     __syncthreads();
-    out.finish(tile, c, ldc, m0 + q * 16, M, N, bias != nullptr, act, escale, accumulate);
+    out.finish(tile, c, ldc, mq, M, N, bias != nullptr, act, escale, accumulate);
 }
 
-template <int S, int XCD, int G>
+template <int RB, int S, int XCD, int G>
 hipError_t launch_kq(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                      const EpiArgs &epi, hipStream_t s) {
-    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)4), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)4));
-    hipLaunchKernelGGL((gemm_i8_kq_kernel<S, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
+    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)4), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)RB));
+    hipLaunchKernelGGL((gemm_i8_kq_kernel<RB, S, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m, w.values,
                        w.scales, (int)w.n, (int)w.panels, (int)w.kb, c, ldc, epi.bias, epi.act, epi.scale,
                        epi.accumulate, w.panel_stride, w.blk_stride);
     return hipGetLastError();
@@ -1055,8 +1061,15 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     if (w.panels >= 128) return launch_lds<4, 4, 3, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
     if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 256)
         return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
-    if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512)
-        return launch_kq<5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512) {
+        // 48-row tiles when their workgroups (one per CU) fit the chip in one round: every CU
+        // busy and a quarter less work each (750 x 4096 -> 1024: 192 -> 256 workgroups, 15.7 ->
+        // 14.2 us); else 64-row tiles (at 1000 rows 336 workgroups would take two rounds: 25
+        // against 16.4 us).
+        if (div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
+            return launch_kq<3, 5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_kq<4, 5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    }
     return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 

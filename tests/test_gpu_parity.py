@@ -64,9 +64,11 @@ def test_exact_mode_is_bit_identical_to_the_fused_reference(tk, orc, p):
         tk.set_mode(tk.FAST)
 
 
+# (700, 2048, 1000) and (1300, 2048, 700) take the k-split kernel with 48- and 64-row tiles.
 FAST_SHAPES = [(1, 1, 1), (3, 7, 5), (8, 64, 16), (9, 64, 16), (13, 100, 50), (64, 128, 96), (130, 1000, 255),
                (200, 640, 8198), (257, 2048, 130), (1, 4096, 1024), (8, 1280, 2560), (16, 2048, 100),
-               (4, 2112, 300), (16, 2049, 77), (2, 64, 140000), (11, 700, 20000)]
+               (4, 2112, 300), (16, 2049, 77), (2, 64, 140000), (11, 700, 20000), (700, 2048, 1000),
+               (1300, 2048, 700)]
 
 
 @pytest.mark.parametrize("m,k,n", FAST_SHAPES)
