@@ -1070,7 +1070,13 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
             return launch_kq<3, 5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
         return launch_kq<4, 5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
     }
-    return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    // The direct kernel: 64 x 64 tiles when they give about one workgroup per CU (161 to 256 of
+    // them), else 32 x 64 tiles, four workgroups per CU: more of them on small grids, shorter
+    // ones on large (750 x 1024 -> 640: 6.3 -> 4.9 us; 300 x 1024 -> 1000: 6.9 -> 5.4 us;
+    // 1500 x 1024 -> 1024: 10.7 -> 9.7 us; 750 x 1024 -> 1024 keeps 64 x 64, 6.6 against 7.3 us).
+    const size_t tiles64 = div_ceil(m, (size_t)64) * div_ceil(w.n, (size_t)64);
+    if (tiles64 > 160 && tiles64 <= GFX950_CUS) return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    return launch_tile<1, 2, 6, 4, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
 }
 
 // The product's f32 outputs and their row maxima per workgroup column (TileMax), on the tiles
