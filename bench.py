@@ -706,14 +706,26 @@ def tdt_leg(args, net, enc_host):
     pred0 = torch.zeros(h, device="cuda")
     dec.predict_rows([vocab - 1], state0.view(1, -1), pred0.view(1, -1))
     kern.synchronize()
-    times, toks = [], None
-    for _ in range(6):
-        state, pred = state0.clone(), pred0.clone()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        toks, frame, _ = dec.decode(enc, state, pred)
-        times.append(time.perf_counter() - t0)
-    ms = float(np.median(times[1:])) * 1e3
+
+    def timed():
+        times, toks, state = [], None, None
+        for _ in range(6):
+            state, pred = state0.clone(), pred0.clone()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            toks, frame, _ = dec.decode(enc, state, pred)
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times[1:])) * 1e3, toks, state.cpu().numpy()
+
+    resident = dec.resident
+    ms, toks, state_r = timed()
+    steps_ms = None
+    if resident:  # the same decode as a graph of step kernels, for comparison
+        dec.set_resident(False)
+        steps_ms, steps_toks, state_s = timed()
+        if steps_toks != toks or np.max(np.abs(state_s - state_r)) > 1e-4:
+            raise RuntimeError("the resident and step-kernel decodes differ")
+        dec.set_resident(True)
     frames = enc_host.shape[0]
     weight_bytes = joint.bytes() + sum(w.bytes() for w in lstm) + proj.bytes()
     out = {"workload": f"greedy TDT decode, {frames} frames (60 s audio), h={h}, vocab {vocab} + "
@@ -721,7 +733,11 @@ def tdt_leg(args, net, enc_host):
            "frames": frames, "tokens": len(toks), "tokens_per_frame": round(len(toks) / frames, 3),
            "ms_per_decode": round(ms, 3), "us_per_token": round(ms * 1e3 / max(len(toks), 1), 2),
            "audio_s_per_s": round(60.0 / (ms * 1e-3), 1), "decoder_weight_mb": round(weight_bytes / 1e6, 2),
-           "timing": "wall clock around tg_tdt_decode_device (blocks until the decode ends), median of 5"}
+           "resident": resident,
+           "step_kernels_ms_per_decode": None if steps_ms is None else round(steps_ms, 3),
+           "step_kernels_us_per_token": None if steps_ms is None else round(steps_ms * 1e3 / max(len(toks), 1), 2),
+           "timing": "wall clock around tg_tdt_decode_device (blocks until the decode ends), median of 5; "
+                     "resident: one launch with the matrices in LDS; step kernels: four kernels per step as a graph"}
     dec.close()
     kern.close()
     return out, toks

@@ -320,6 +320,15 @@ int tg_tdt_predict_device(tg_ctx *ctx, tg_tdt *tdt, const int32_t *tokens, size_
 int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t enc_len, size_t lde, size_t frames,
                          float *state, size_t state_len, float *pred, size_t pred_len, size_t *frame,
                          size_t *on_frame, tg_token *tokens, size_t cap, size_t *count);
+/* How tg_tdt_decode_device runs its steps (no counterpart in the reference, whose decode loop runs
+ * on the host). Resident (the default where the network allows it: int8 matrices, vocab < 65535,
+ * the panels fit the workgroups' LDS and the device takes cooperative launches): one launch makes
+ * the steps with the matrices held in LDS across the device's CUs. Otherwise each step is four
+ * kernels, replayed as a graph. Both give the same tokens, states and predictions.
+ * tg_tdt_set_resident(on = 1) fails with TG_ERR_UNSUPPORTED when the network cannot run resident;
+ * on = 0 selects the step kernels. tg_tdt_is_resident returns 1 when decodes run resident. */
+int tg_tdt_set_resident(tg_ctx *ctx, tg_tdt *tdt, int on);
+int tg_tdt_is_resident(const tg_tdt *tdt);
 
 /* ---- packs: the reference's weight files (src/pack.rs) -------------------------------------
  * A pack is "TELMOPAK", a u32 version (1) and 4 zero bytes; entries' data at multiples of 64

@@ -68,6 +68,8 @@ SIGNATURES = {
     "tg_tdt_predict_device": (ctypes.c_int, [_p, _p, _p, _sz, _p, _sz, _p, _sz]),
     "tg_tdt_decode_device": (ctypes.c_int, [_p, _p, _p, _sz, _sz, _sz, _p, _sz, _p, _sz, _szp, _szp, _p, _sz,
                                              _szp]),
+    "tg_tdt_set_resident": (ctypes.c_int, [_p, _p, ctypes.c_int]),
+    "tg_tdt_is_resident": (ctypes.c_int, [_p]),
     "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),
     "tg_pack_close": (None, [_p]),

@@ -74,9 +74,17 @@ struct tg_tdt {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     uintptr_t key[7] = {};
+    // The resident decode: its plan (valid when can_resident), whether decodes use it, its
+    // hand-over words and the longest wait of one workgroup for another (wall-clock ticks).
+    tg::TdtPlan plan;
+    bool can_resident = false, use_resident = false;
+    uint64_t *words = nullptr;
+    uint64_t wait_ticks = 0;
 };
 
 constexpr int TDT_GRAPH_STEPS = 16;
+// Steps per resident launch: the host looks at the control block between launches.
+constexpr int TDT_RESIDENT_STEPS = 16384;
 
 // The scratch of tg_matmul_device_noalloc, for callers that cannot allocate: the quantised rows of
 // one product (the first NOALLOC_QA_BYTES) and their row exponents (NOALLOC_ROWS int32 after them).
@@ -868,6 +876,7 @@ void tdt_release(tg_tdt *t) {
     if (t->scratch) (void)hipFree(t->scratch);
     if (t->partials) (void)hipFree(t->partials);
     if (t->tokens) (void)hipFree(t->tokens);
+    if (t->words) (void)hipFree(t->words);
     delete t;
 }
 
@@ -883,6 +892,24 @@ int tdt_matrix(tg_ctx *ctx, const tg_weights *w, size_t n, size_t k, const char 
         return fail(ctx, TG_ERR_SHAPE, std::string(what) + " is " + std::to_string(w->d.n) + " x " +
                                            std::to_string(w->d.k) + ", and the network needs " + std::to_string(n) +
                                            " x " + std::to_string(k));
+    return TG_OK;
+}
+
+// The decode's outputs from the control block: frame, on_frame, the token count and the tokens.
+int tdt_results(tg_ctx *ctx, tg_tdt *tdt, const tg::TdtCtl *hc, size_t *frame, size_t *on_frame, tg_token *tokens,
+                size_t cap, size_t *count) {
+    const size_t n = (size_t)hc->ntok;
+    *frame = (size_t)hc->t;
+    *on_frame = (size_t)hc->on_frame;
+    *count = n;
+    const size_t copy = n < cap ? n : cap;
+    if (copy) {
+        std::vector<int32_t> buf(copy * 3);
+        TG_HIP(ctx, hipMemcpy(buf.data(), tdt->tokens, copy * 3 * sizeof(int32_t), hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < copy; i++)
+            tokens[i] = tg_token{(uint32_t)buf[3 * i], (uint32_t)buf[3 * i + 1], (uint32_t)buf[3 * i + 2]};
+    }
+    if (n > cap) return fail(ctx, TG_ERR_SHAPE, "tokens holds " + std::to_string(cap) + " entries and the decode emitted " + std::to_string(n));
     return TG_OK;
 }
 
@@ -963,6 +990,18 @@ int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out) {
         }
     }
     net.durations = t->durations;
+    if (tg::tdt_resident_plan(net, t->plan)) {
+        if (hipMalloc(&t->words, tg::tdt_resident_words(net) * sizeof(uint64_t)) != hipSuccess) {
+            tdt_release(t);
+            return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+        }
+        int khz = 0;
+        if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device) != hipSuccess || khz <= 0)
+            khz = 100000;
+        t->wait_ticks = (uint64_t)khz * 1000;  // one second
+        t->can_resident = t->use_resident = true;
+    }
+    (void)hipGetLastError();  // a refused LDS attribute or occupancy query leaves the step kernels
     std::memset(t->ctl_host, 0, sizeof(tg::TdtCtl));
     hipError_t e = hipMemcpyAsync(t->ctl, t->ctl_host, sizeof(tg::TdtCtl), hipMemcpyHostToDevice, ctx->stream);
     if (e == hipSuccess)
@@ -1054,6 +1093,23 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
     hc->on_frame = (int32_t)*on_frame;
     hc->rows = tg::TDT_ROWS;
     TG_HIP(ctx, hipMemcpyAsync(tdt->ctl, hc, sizeof(*hc), hipMemcpyHostToDevice, ctx->stream));
+    const size_t limit = (frames - *frame) * (per_frame + 1) + 1;
+    if (tdt->use_resident) {
+        TG_HIP(ctx, tg::launch_tdt_resident_init(net, tdt->words, state, pred, ctx->stream));
+        size_t steps = 0;
+        while (true) {
+            TG_HIP(ctx, tg::launch_tdt_resident(tdt->ctl, net, tdt->plan, tdt->words, enc_proj, lde, (int)frames, state,
+                                                pred, tdt->tokens, (int)most, TDT_RESIDENT_STEPS, tdt->wait_ticks,
+                                                ctx->stream));
+            TG_HIP(ctx, hipMemcpyAsync(hc, tdt->ctl, sizeof(*hc), hipMemcpyDeviceToHost, ctx->stream));
+            TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            if (hc->err) return fail(ctx, TG_ERR_HIP, "the resident decode: a workgroup's wait passed its deadline");
+            if (hc->done) break;
+            steps += TDT_RESIDENT_STEPS;
+            if (steps > limit) return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
+        }
+        return tdt_results(ctx, tdt, hc, frame, on_frame, tokens, cap, count);
+    }
     // Steps run as a captured graph of TDT_GRAPH_STEPS steps, replayed in growing batches between
     // looks at the control block; a step after the end returns at once. Every step emits a token
     // or moves at least one frame, so (frames - frame) (per_frame + 1) steps always suffice.
@@ -1076,7 +1132,6 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
         TG_HIP(ctx, hipGraphInstantiate(&tdt->exec, g, nullptr, nullptr, 0));
         std::memcpy(tdt->key, key, sizeof(key));
     }
-    const size_t limit = (frames - *frame) * (per_frame + 1) + 1;
     size_t steps = 0, graphs = 1;
     while (true) {
         for (size_t i = 0; i < graphs; i++) TG_HIP(ctx, hipGraphLaunch(tdt->exec, ctx->stream));
@@ -1090,19 +1145,19 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
     if (hc->cur)  // the last prediction left the state in the scratch buffer
         TG_HIP(ctx, hipMemcpyAsync(state, tdt->scratch, net.layers * 2 * net.h * sizeof(float),
                                    hipMemcpyDeviceToDevice, ctx->stream));
-    const size_t n = (size_t)hc->ntok;
-    *frame = (size_t)hc->t;
-    *on_frame = (size_t)hc->on_frame;
-    *count = n;
-    const size_t copy = n < cap ? n : cap;
-    if (copy) {
-        std::vector<int32_t> buf(copy * 3);
-        TG_HIP(ctx, hipMemcpy(buf.data(), tdt->tokens, copy * 3 * sizeof(int32_t), hipMemcpyDeviceToHost));
-        for (size_t i = 0; i < copy; i++)
-            tokens[i] = tg_token{(uint32_t)buf[3 * i], (uint32_t)buf[3 * i + 1], (uint32_t)buf[3 * i + 2]};
-    }
-    if (n > cap) return fail(ctx, TG_ERR_SHAPE, "tokens holds " + std::to_string(cap) + " entries and the decode emitted " + std::to_string(n));
+    return tdt_results(ctx, tdt, hc, frame, on_frame, tokens, cap, count);
+}
+
+int tg_tdt_set_resident(tg_ctx *ctx, tg_tdt *tdt, int on) {
+    if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
+    if (on && !tdt->can_resident)
+        return fail(ctx, TG_ERR_UNSUPPORTED,
+                    "the network does not run resident (int8 matrices, vocab < 65535, the panels in LDS, cooperative launch)");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    tdt->use_resident = on != 0;
     return TG_OK;
 }
+
+int tg_tdt_is_resident(const tg_tdt *tdt) { return tdt && tdt->use_resident ? 1 : 0; }
 
 }  // extern "C"

@@ -25,6 +25,8 @@
 //   and the cell update happens in the epilogue. The state is read from one buffer and written to
 //   the other (the decode flips between them), so no workgroup reads a state another has replaced.
 // * tdt_proj_kernel writes pred = W_p h_last + b_p.
+#include <algorithm>
+
 #include "gemv_core.hpp"
 
 namespace tg {
@@ -226,6 +228,55 @@ __global__ __launch_bounds__(TDT_THREADS) void tdt_joint_kernel(TdtCtl *ctl, con
     }
 }
 
+// Where a window's walk leaves the decode: the frame, tokens on it, tokens emitted, the token handed
+// to the prediction network (-1: none), the next window's rows and whether the frames are used up.
+struct Walked {
+    int t, on, ntok, token, rows, done;
+};
+
+// The reference's loop over the window's rows (src/parakeet.rs:1412-1577): a blank skips
+// max(duration, 1) frames; a token is recorded (when record is set and the buffer has room), handed
+// to the prediction network and moves the frame by its duration, or counts towards max_symbols on
+// its frame. The walk stops at the first token, at the end of the window or of the frames. The next
+// window: after a token, twice the frames this one walked (at least 4); after a window of blanks,
+// the most.
+__device__ __forceinline__ Walked walk_window(int t, int rows, int on, int ntok, const int *tok_s, const int *dur_s,
+                                              int blank, int frames, int max_symbols, int32_t *tokens, int cap,
+                                              bool record) {
+    int tc = t, token = -1, done = 0, next = TDT_ROWS;
+    while (true) {
+        const int r = tc - t;
+        if (r >= rows) break;  // the next window scores the frames from tc
+        const int tok = tok_s[r], dur = dur_s[r];
+        if (tok == blank) {
+            tc += max(dur, 1);
+            on = 0;
+            if (tc >= frames) {
+                done = 1;
+                break;
+            }
+            continue;
+        }
+        if (record && ntok < cap) {
+            tokens[3 * ntok] = tok;
+            tokens[3 * ntok + 1] = tc;
+            tokens[3 * ntok + 2] = dur;
+        }
+        ntok++;
+        token = tok;
+        next = min(TDT_ROWS, max(4, 2 * (r + 1)));
+        if (dur > 0) {
+            tc += dur;
+            on = 0;
+        } else if (++on >= max_symbols) {
+            tc += 1;
+            on = 0;
+        }
+        break;
+    }
+    return Walked{tc, on, ntok, token, next, done};
+}
+
 // What the decider of a step reads besides the control block.
 struct Decide {
     const Best *partials;
@@ -311,50 +362,18 @@ __device__ __forceinline__ int decide_step(TdtCtl *ctl, const Decide &d, int *cu
     }
     __syncthreads();
     if (tid == 0) {
-        int tc = t, on = snap_on, ntok = snap_ntok, token = -1, done = 0;
-        // The next window: after a token, twice the frames this one walked (at least 4); after a
-        // window of blanks, the most.
-        int next = TDT_ROWS;
-        while (true) {
-            const int r = tc - t;
-            if (r >= rows) break;  // the next window scores the frames from tc
-            const int tok = tok_s[r], dur = dur_s[r];
-            if (tok == d.blank) {
-                tc += max(dur, 1);
-                on = 0;
-                if (tc >= d.frames) {
-                    done = 1;
-                    break;
-                }
-                continue;
-            }
-            if (blockIdx.x == 0 && ntok < d.cap) {
-                d.tokens[3 * ntok] = tok;
-                d.tokens[3 * ntok + 1] = tc;
-                d.tokens[3 * ntok + 2] = dur;
-            }
-            ntok++;
-            token = tok;
-            next = min(TDT_ROWS, max(4, 2 * (r + 1)));
-            if (dur > 0) {
-                tc += dur;
-                on = 0;
-            } else if (++on >= d.max_symbols) {
-                tc += 1;
-                on = 0;
-            }
-            break;
-        }
+        const Walked w = walk_window(t, rows, snap_on, snap_ntok, tok_s, dur_s, d.blank, d.frames, d.max_symbols,
+                                     d.tokens, d.cap, blockIdx.x == 0);
         if (blockIdx.x == 0) {
-            store_i(&ctl->t, tc);
-            store_i(&ctl->on_frame, on);
-            store_i(&ctl->ntok, ntok);
-            store_i(&ctl->rows, next);
+            store_i(&ctl->t, w.t);
+            store_i(&ctl->on_frame, w.on);
+            store_i(&ctl->ntok, w.ntok);
+            store_i(&ctl->rows, w.rows);
             store_i(&ctl->cur, *cur);
-            store_i(&ctl->active, token >= 0);
-            store_i(&ctl->done, done);
+            store_i(&ctl->active, w.token >= 0);
+            store_i(&ctl->done, w.done);
         }
-        result = token;
+        result = w.token;
     }
     __syncthreads();
     return result;
@@ -500,6 +519,628 @@ bool tdt_split(size_t m, const DeviceWeights &d) {
         else TG_TDT_KBC(KERNEL, 16, __VA_ARGS__);                        \
     } while (0)
 
+// ------------------------------------------------------------------------------ the resident decode
+//
+// One cooperative launch makes up to ResArgs::steps decode steps with every matrix held in LDS: each
+// workgroup copies its panels of the joint, of every LSTM layer and of the projection once, and a
+// step then reads only the rows it scores. The step's stages are those of the kernels above (the
+// joint over a window of frames, the decision in every workgroup alike, the LSTM layers with the
+// cell update, the projection), with the same integer sums and the same f32 epilogues.
+//
+// Workgroups hand each other values through 8-byte words: a value and the tag of the step or
+// prediction that wrote it, stored and loaded as one agent-scope atomic. A reader waits until every
+// word it needs carries the tag it expects; no counter or barrier spans workgroups. Each kind of word
+// has two buffers, alternating with the tag's parity, and a buffer is rewritten two tags on: every
+// workgroup writes a joint word for every row of every step after its previous decision, and a
+// decision needs all of them, so no buffer is rewritten while a reader still needs its values. Every
+// wait has a deadline (and watches the error flag): a wait that passes it sets the flag and ends the
+// launch, so every workgroup exits.
+
+constexpr int RES_WAVES = 4;
+constexpr int RES_THREADS = RES_WAVES * 64;
+constexpr int RES_MAX_PANELS = 8;  // panels of one matrix per workgroup
+constexpr int RES_MAX_GRID = 256;  // workgroups: a row's sixteen decider threads read sixteen words each
+constexpr uint32_t TAG_NONE = 0xffffffffu;
+
+struct ResMat {
+    const uint8_t *values;
+    const float *scales, *bias;
+    size_t panel_stride, blk_stride;
+    int n, KB, P;
+};
+
+struct ResArgs {
+    ResMat joint, proj, lstm[TDT_MAX_LAYERS];
+    const float *emb, *enc;
+    size_t lde;
+    const int32_t *durations;
+    int32_t *tokens;
+    TdtCtl *ctl;
+    float *state, *pred;
+    // Hand-over words: the prediction [2][h], the LSTM outputs h [layers][2][h], the joint's best
+    // entries [2][TDT_ROWS][RES_MAX_GRID] and its first and duration logits [2][TDT_ROWS][TDT_EXTRA].
+    uint64_t *w_pred, *w_h, *w_part, *w_ext;
+    int h, vocab, ndur, layers, blank, max_symbols, frames, cap;
+    int JP, GJ, LP, GL, PP, GP, poff, grid;
+    int steps;
+    uint64_t wait_ticks;  // the longest wait, in wall-clock ticks
+};
+
+__device__ __forceinline__ uint64_t word_load(const uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void word_store(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
+    return ((uint64_t)tag << 32) | __float_as_uint(v);
+}
+__device__ __forceinline__ float word_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+// A workgroup's best entry of a joint row: the low 16 bits of the step, the index (0xffff: none,
+// so vocab < 65535) and the value.
+__device__ __forceinline__ uint64_t tagged_best(Best x, uint32_t step) {
+    const uint32_t i = x.i == INT32_MAX ? 0xffffu : (uint32_t)x.i;
+    return ((uint64_t)(step & 0xffffu) << 48) | ((uint64_t)i << 32) | __float_as_uint(x.v);
+}
+__device__ __forceinline__ Best best_of(uint64_t w) {
+    const uint32_t i = (uint32_t)(w >> 32) & 0xffffu;
+    return Best{word_value(w), i == 0xffffu ? INT32_MAX : (int)i};
+}
+
+// Waits until word i (bit i of need) carries tag[i], reloading the words still pending each round.
+// False when the deadline passes or another workgroup has set the error flag.
+template <int N>
+__device__ __forceinline__ bool wait_words(const uint64_t *const (&p)[N], uint32_t need, const uint32_t (&tag)[N],
+                                           uint64_t (&w)[N], const int32_t *err, uint64_t deadline) {
+    for (int round = 0;; round++) {
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if (need >> i & 1) w[i] = word_load(p[i]);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if ((need >> i & 1) && (uint32_t)(w[i] >> 32) == tag[i]) need &= ~(1u << i);
+        if (!need) return true;
+        if ((round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(err) != 0)) return false;
+    }
+}
+
+// Copies np panels from p0 on of a matrix into LDS, panel pi's k-block t at (pi KB + t) * 1024.
+__device__ __forceinline__ void copy_panels(uint8_t *dst, const ResMat &m, int p0, int np) {
+    const int per = m.KB * 64, total = np * per;
+    for (int i0 = 0; i0 < total; i0 += RES_THREADS * 8) {
+        gemv::v4i v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = min(i0 + u * RES_THREADS + (int)threadIdx.x, total - 1);
+            const int pi = i / per, rem = i - pi * per;
+            v[u] = *reinterpret_cast<const gemv::v4i *>(m.values + (size_t)(p0 + pi) * m.panel_stride +
+                                                        (size_t)(rem >> 6) * m.blk_stride + (rem & 63) * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * RES_THREADS + (int)threadIdx.x;
+            if (i < total) {
+                const int pi = i / per, rem = i - pi * per;
+                *reinterpret_cast<gemv::v4i *>(dst + ((size_t)pi * m.KB + (rem >> 6)) * 1024 + (rem & 63) * 16) = v[u];
+            }
+        }
+    }
+}
+
+// The LDS of a resident workgroup besides its panels.
+struct ResShared {
+    float js[RES_MAX_PANELS * PANEL], jbias[RES_MAX_PANELS * PANEL];
+    float ps[RES_MAX_PANELS * PANEL], pbias[RES_MAX_PANELS * PANEL], pst[RES_MAX_PANELS * PANEL];
+    float ls[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL], lbias[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL];
+    float hst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4], cst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4];
+    __attribute__((aligned(16))) float pin[TDT_MAX_H];  // the prediction the joint adds
+    float dlog[TDT_ROWS][TDT_MAX_DURATIONS];
+    Best red[RES_WAVES][TDT_ROWS];
+    int32_t kpart[RES_WAVES][2][PANEL];
+    int32_t erow[TDT_ROWS];
+    uint32_t slot[RES_WAVES];
+    int tok_s[TDT_ROWS], dur_s[TDT_ROWS], durs[TDT_MAX_DURATIONS];
+    int dec[6];
+    int abort;
+};
+
+__device__ __forceinline__ void res_fail(const ResArgs &a, ResShared &sh) {
+    sh.abort = 1;
+    store_i(&a.ctl->err, 1);
+}
+
+// The exponent of a row from the workgroup's four wavefront maxima in sh.slot.
+__device__ __forceinline__ int32_t res_exponent(const ResShared &sh) {
+    const uint32_t m = max(max(sh.slot[0], sh.slot[1]), max(sh.slot[2], sh.slot[3]));
+    return m == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(m));
+}
+
+// The largest |x| of a chunk as bits, all ones for a non-finite input (as the GEMV's row maxima).
+__device__ __forceinline__ uint32_t chunk_max(v4f v) {
+    const bool bad = !__builtin_isfinite(v.x) | !__builtin_isfinite(v.y) | !__builtin_isfinite(v.z) |
+                     !__builtin_isfinite(v.w);
+    const float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    return bad ? 0xffffffffu : __float_as_uint(mx);
+}
+
+// One row of k = 4 CK inputs whose chunk c (inputs 4c .. 4c + 3) thread c % 256 holds in x[c / 256]:
+// the row exponent, then the digits in the one-row layout (k-block t, 16-input group g: hi at
+// sq + 128 t + 16 g, lo 64 bytes on), zero past the row up to KB k-blocks.
+template <int NC>
+__device__ __forceinline__ int32_t row_digits(const v4f (&x)[NC], int CK, int KB, uint8_t *sq, ResShared &sh) {
+    const int tid = threadIdx.x;
+    uint32_t mx = 0;
+#pragma unroll
+    for (int i = 0; i < NC; i++)
+        if (tid + RES_THREADS * i < CK) mx = max(mx, chunk_max(x[i]));
+    const uint32_t m = gemv::wave_max_u(mx);
+    if ((tid & 63) == 0) sh.slot[tid >> 6] = m;
+    __syncthreads();
+    const int32_t e = res_exponent(sh);
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+        const int c = tid + RES_THREADS * i;
+        if (c < KB * 16) {
+            const v4f v = c < CK ? x[i] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            uint32_t hi, lo;
+            digits4(v.x, v.y, v.z, v.w, e, hi, lo);
+            uint8_t *d = sq + (c >> 4) * 128 + ((c & 15) >> 2) * 16 + (c & 3) * 4;
+            *reinterpret_cast<uint32_t *>(d) = hi;
+            *reinterpret_cast<uint32_t *>(d + 64) = lo;
+        }
+    }
+    __syncthreads();
+    return e;
+}
+
+// The integer sums of one row (digits in sq, one-row layout) with panel pw (KB k-blocks in LDS): the
+// four wavefronts take k-blocks w, w + 4, ...; v_dot4_i32_i8 per 16-input group, the groups meet
+// across the wavefront and the wavefronts in sh.kpart. Lanes j < 16 of wavefront 0 read column j's
+// sums (hi, lo) after the barrier that ends this call.
+__device__ __forceinline__ void row_sums(const uint8_t *pw, int KB, const uint8_t *sq, ResShared &sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int dh = 0, dl = 0;
+    for (int t = wave; t < KB; t += RES_WAVES) {
+        const gemv::v4i ahi = *reinterpret_cast<const gemv::v4i *>(sq + t * 128 + (lane >> 4) * 16);
+        const gemv::v4i alo = *reinterpret_cast<const gemv::v4i *>(sq + t * 128 + 64 + (lane >> 4) * 16);
+        const gemv::v4i wv = *reinterpret_cast<const gemv::v4i *>(pw + (size_t)t * 1024 + lane * 16);
+        dh = __builtin_amdgcn_sdot4(ahi.x, wv.x, dh, false);
+        dh = __builtin_amdgcn_sdot4(ahi.y, wv.y, dh, false);
+        dh = __builtin_amdgcn_sdot4(ahi.z, wv.z, dh, false);
+        dh = __builtin_amdgcn_sdot4(ahi.w, wv.w, dh, false);
+        dl = __builtin_amdgcn_sdot4(alo.x, wv.x, dl, false);
+        dl = __builtin_amdgcn_sdot4(alo.y, wv.y, dl, false);
+        dl = __builtin_amdgcn_sdot4(alo.z, wv.z, dl, false);
+        dl = __builtin_amdgcn_sdot4(alo.w, wv.w, dl, false);
+    }
+    dh += __shfl_xor(dh, 16, 64);
+    dh += __shfl_xor(dh, 32, 64);
+    dl += __shfl_xor(dl, 16, 64);
+    dl += __shfl_xor(dl, 32, 64);
+    if (lane < PANEL) {
+        sh.kpart[wave][0][lane] = dh;
+        sh.kpart[wave][1][lane] = dl;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ ResShared sh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x;
+    const int h = a.h, NJ = a.joint.n, KBJ = a.joint.KB, KBL = a.lstm[0].KB, KBP = a.proj.KB;
+    const int pj0 = b * a.JP, npj = b < a.GJ ? min(a.JP, a.joint.P - pj0) : 0;
+    const int pl0 = b * a.LP, npl = b < a.GL ? min(a.LP, a.lstm[0].P - pl0) : 0;
+    const int bp = b - a.poff, pp0 = bp * a.PP, npp = bp >= 0 && bp < a.GP ? min(a.PP, a.proj.P - pp0) : 0;
+    uint8_t *wj = lds;
+    uint8_t *wl = wj + (size_t)a.JP * KBJ * 1024;
+    uint8_t *wp = wl + (size_t)a.layers * a.LP * KBL * 1024;
+    uint8_t *sq = wp + (size_t)a.PP * KBP * 1024;
+
+    copy_panels(wj, a.joint, pj0, npj);
+    for (int l = 0; l < a.layers; l++) copy_panels(wl + (size_t)l * a.LP * KBL * 1024, a.lstm[l], pl0, npl);
+    copy_panels(wp, a.proj, pp0, npp);
+    if (tid < npj * PANEL) {
+        const int c = min(pj0 * PANEL + tid, NJ - 1);
+        sh.js[tid] = a.joint.scales[c];
+        sh.jbias[tid] = a.joint.bias[c];
+    }
+    if (tid < npl * PANEL) {
+        for (int l = 0; l < a.layers; l++) {
+            sh.ls[l][tid] = a.lstm[l].scales[pl0 * PANEL + tid];
+            sh.lbias[l][tid] = a.lstm[l].bias[pl0 * PANEL + tid];
+        }
+    }
+    if (tid < npl * 4) {
+        const int u = pl0 * 4 + tid;
+        for (int l = 0; l < a.layers; l++) {
+            sh.hst[l][tid] = a.state[(size_t)l * 2 * h + u];
+            sh.cst[l][tid] = a.state[(size_t)l * 2 * h + h + u];
+        }
+    }
+    if (tid < npp * PANEL) {
+        const int c = min(pp0 * PANEL + tid, h - 1);
+        sh.ps[tid] = a.proj.scales[c];
+        sh.pbias[tid] = a.proj.bias[c];
+        sh.pst[tid] = a.pred[c];
+    }
+    if (tid < a.ndur) sh.durs[tid] = a.durations[tid];
+    if (tid == 0) sh.abort = 0;
+    int t = a.ctl->t, on = a.ctl->on_frame, ntok = a.ctl->ntok, rows = a.ctl->rows, done = a.ctl->done;
+    uint32_t s = a.ctl->step, n = a.ctl->preds, pin_n = TAG_NONE;
+    const uint32_t s_end = s + (uint32_t)a.steps;
+    const int CH = h >> 2;  // 4-input chunks of h inputs
+    __syncthreads();
+
+    while (!done && s != s_end) {
+        if (t >= a.frames) {
+            done = 1;
+            break;
+        }
+        const uint32_t par = s & 1;
+        uint64_t *ext = a.w_ext + (size_t)par * TDT_ROWS * TDT_EXTRA;
+        // ---- The joint over rows t .. t + rows - 1: z = relu(enc_proj[min(t + r, frames - 1)] + pred).
+        if (npj > 0) {
+            // Wavefront w holds rows w + 4 j, lane l chunks l + 64 i (h <= 992: at most 248 chunks).
+            // The encoder rows are requested before the wait for the prediction.
+            v4f e[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = wave + 4 * j, f = min(t + r, a.frames - 1);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int c = lane + 64 * i;
+                    const bool ok = r < rows && c < CH;
+                    e[j][i] = *reinterpret_cast<const v4f *>(ok ? a.enc + (size_t)f * a.lde + 4 * c : gemv::ZERO_CHUNK);
+                }
+            }
+            if (pin_n != n) {
+                const uint64_t *p[4];
+                uint32_t tag[4];
+                uint64_t w[4];
+                uint32_t need = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int i = tid + RES_THREADS * q;
+                    p[q] = a.w_pred + (size_t)(n & 1) * h + min(i, h - 1);
+                    tag[q] = n;
+                    if (i < h) need |= 1u << q;
+                }
+                if (!wait_words<4>(p, need, tag, w, &a.ctl->err, (uint64_t)wall_clock64() + a.wait_ticks)) res_fail(a, sh);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (need >> q & 1) sh.pin[tid + RES_THREADS * q] = word_value(w[q]);
+                pin_n = n;
+                __syncthreads();
+                if (sh.abort) break;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = wave + 4 * j;
+                if (r < rows) {
+                    v4f z[4];
+                    uint32_t mx = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int c = lane + 64 * i;
+                        const v4f pv = c < CH ? *reinterpret_cast<const v4f *>(sh.pin + 4 * c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                        z[i].x = fmaxf(e[j][i].x + pv.x, 0.0f);
+                        z[i].y = fmaxf(e[j][i].y + pv.y, 0.0f);
+                        z[i].z = fmaxf(e[j][i].z + pv.z, 0.0f);
+                        z[i].w = fmaxf(e[j][i].w + pv.w, 0.0f);
+                        if (c < CH) mx = max(mx, chunk_max(z[i]));
+                    }
+                    const uint32_t m = gemv::wave_max_u(mx);
+                    const int32_t ex = m == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(m));
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int c = lane + 64 * i;
+                        if (c < KBJ * 16) {
+                            uint32_t hi, lo;
+                            digits4(z[i].x, z[i].y, z[i].z, z[i].w, ex, hi, lo);
+                            uint8_t *d = sq + (c >> 4) * 2048 + ((c & 15) >> 2) * 256 + r * 16 + (c & 3) * 4;
+                            *reinterpret_cast<uint32_t *>(d) = hi;
+                            *reinterpret_cast<uint32_t *>(d + 1024) = lo;
+                        }
+                    }
+                    if (lane == 0) sh.erow[r] = ex;
+                }
+            }
+            __syncthreads();
+            // Wavefront w scores panels w, w + 4, ... of this workgroup: element v of lane l is row
+            // 4 (l / 16) + v, column l % 16.
+            Best mine[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) mine[v] = Best{__builtin_nanf(""), INT32_MAX};
+            const int orow = (lane >> 4) * 4, j16 = lane & 15;
+            for (int pi = wave; pi < npj; pi += RES_WAVES) {
+                gemv::v4i hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+                const uint8_t *wb = wj + (size_t)pi * KBJ * 1024 + lane * 16;
+                for (int tk = 0; tk < KBJ; tk++) {
+                    const gemv::v4i ahi = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + lane * 16);
+                    const gemv::v4i alo = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + 1024 + lane * 16);
+                    const gemv::v4i wv = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)tk * 1024);
+                    hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wv, hi, 0, 0, 0);
+                    lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wv, lo, 0, 0, 0);
+                }
+                const int col = (pj0 + pi) * PANEL + j16;
+                const float sc = sh.js[pi * PANEL + j16], bs = sh.jbias[pi * PANEL + j16];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = orow + v;
+                    if (r < rows && col < NJ) {
+                        const float val =
+                            epilogue_vals(dequant(hi[v], lo[v], sh.erow[r], sc), true, bs, ACT_NONE, 1.0f, false, 0.0f);
+                        if (col < a.vocab) {
+                            if (before(val, col, mine[v].v, mine[v].i)) mine[v] = Best{val, col};
+                            if (col == 0) word_store(ext + (size_t)r * TDT_EXTRA, tagged(val, s));
+                        } else {
+                            word_store(ext + (size_t)r * TDT_EXTRA + 1 + (col - a.vocab), tagged(val, s));
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float bv = mine[v].v;
+                int bi = mine[v].i;
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    const float ov = __shfl_xor(bv, off, 64);
+                    const int oi = __shfl_xor(bi, off, 64);
+                    if (before(ov, oi, bv, bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                if (j16 == 0) sh.red[wave][orow + v] = Best{bv, bi};
+            }
+        }
+        __syncthreads();
+        // Every workgroup's word for every row of the step (none from those without joint panels).
+        if (tid < TDT_ROWS) {
+            Best x{__builtin_nanf(""), INT32_MAX};
+            if (npj > 0) {
+#pragma unroll
+                for (int q = 0; q < RES_WAVES; q++)
+                    if (before(sh.red[q][tid].v, sh.red[q][tid].i, x.v, x.i)) x = sh.red[q][tid];
+            }
+            word_store(a.w_part + ((size_t)par * TDT_ROWS + tid) * RES_MAX_GRID + b, tagged_best(x, s));
+        }
+        // ---- The decision, alike in every workgroup. Thread (r, q) waits for row r's words of
+        // workgroups q, q + 16, ... and its logits q, q + 16, ... (the first, then the durations).
+        {
+            const int r = tid >> 4, q = tid & 15;
+            const bool live = r < rows;
+            const uint64_t *pb = a.w_part + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + q;
+            const uint64_t *pe = ext + (size_t)r * TDT_EXTRA;
+            uint64_t pw[16], ew[5];
+            uint32_t pneed = 0, eneed = 0;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (live && q + 16 * u < a.grid) pneed |= 1u << u;
+#pragma unroll
+            for (int v = 0; v < 5; v++)
+                if (live && q + 16 * v <= a.ndur) eneed |= 1u << v;
+            const uint64_t deadline = (uint64_t)wall_clock64() + a.wait_ticks;
+            for (int round = 0;; round++) {
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (pneed >> u & 1) pw[u] = word_load(pb + 16 * u);
+#pragma unroll
+                for (int v = 0; v < 5; v++)
+                    if (eneed >> v & 1) ew[v] = word_load(pe + min(q + 16 * v, a.ndur));
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if ((pneed >> u & 1) && (uint32_t)(pw[u] >> 48) == (s & 0xffffu)) pneed &= ~(1u << u);
+#pragma unroll
+                for (int v = 0; v < 5; v++)
+                    if ((eneed >> v & 1) && (uint32_t)(ew[v] >> 32) == s) eneed &= ~(1u << v);
+                if (!(pneed | eneed)) break;
+                if ((round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(&a.ctl->err) != 0)) {
+                    res_fail(a, sh);
+                    break;
+                }
+            }
+            Best x{__builtin_nanf(""), INT32_MAX};
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                if (live && q + 16 * u < a.grid) {
+                    const Best y = best_of(pw[u]);
+                    if (before(y.v, y.i, x.v, x.i)) x = y;
+                }
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                const float ov = __shfl_xor(x.v, off, 64);
+                const int oi = __shfl_xor(x.i, off, 64);
+                if (before(ov, oi, x.v, x.i)) x = Best{ov, oi};
+            }
+            if (live) {
+#pragma unroll
+                for (int v = 0; v < 5; v++) {
+                    const int qq = q + 16 * v;
+                    if (qq >= 1 && qq <= a.ndur) sh.dlog[r][qq - 1] = word_value(ew[v]);
+                }
+                if (q == 0) {
+                    const float first = word_value(ew[0]);  // a NaN first is never beaten
+                    sh.tok_s[r] = __builtin_isnan(first) || x.i == INT32_MAX ? 0 : x.i;
+                }
+            }
+        }
+        __syncthreads();
+        if (sh.abort) break;
+        if (tid < rows) {
+            int k = 0;
+            for (int i = 1; i < a.ndur; i++)
+                if (sh.dlog[tid][i] > sh.dlog[tid][k]) k = i;
+            sh.dur_s[tid] = sh.durs[k];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            const Walked wk = walk_window(t, rows, on, ntok, sh.tok_s, sh.dur_s, a.blank, a.frames, a.max_symbols,
+                                          a.tokens, a.cap, b == 0);
+            sh.dec[0] = wk.t;
+            sh.dec[1] = wk.on;
+            sh.dec[2] = wk.ntok;
+            sh.dec[3] = wk.token;
+            sh.dec[4] = wk.rows;
+            sh.dec[5] = wk.done;
+        }
+        __syncthreads();
+        t = sh.dec[0];
+        on = sh.dec[1];
+        ntok = sh.dec[2];
+        const int token = sh.dec[3];
+        rows = sh.dec[4];
+        done = sh.dec[5];
+        s++;
+        if (token < 0) continue;
+
+        // ---- The prediction for the token: the LSTM layers (input [x; h_l], x the embedding row or
+        // the layer below's new h; tags n + 1 for the new values, n for the old), then the projection.
+        const uint32_t nn = n + 1;
+        bool stop = false;
+        for (int l = 0; l < a.layers && !stop; l++) {
+            if (npl == 0) continue;
+            const uint8_t *wlay = wl + (size_t)l * a.LP * KBL * 1024;
+            const uint64_t *hnew = a.w_h + ((size_t)(l - 1) * 2 + (nn & 1)) * h;  // used for l >= 1
+            const uint64_t *hold = a.w_h + ((size_t)l * 2 + (n & 1)) * h;
+            v4f x[2];
+            const uint64_t *p[8];
+            uint32_t tag[8];
+            uint64_t w[8];
+            uint32_t need = 0;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int c = tid + RES_THREADS * i;
+                x[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                const bool first = c < CH, second = !first && c < 2 * CH;
+                if (first && l == 0) x[i] = *reinterpret_cast<const v4f *>(a.emb + (size_t)token * h + 4 * c);
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) {
+                    p[4 * i + qq] = first ? hnew + min(4 * c + qq, h - 1) : hold + min(4 * (c - CH) + qq, h - 1);
+                    tag[4 * i + qq] = first ? nn : n;
+                    if ((first && l > 0) || second) need |= 1u << (4 * i + qq);
+                }
+            }
+            if (!wait_words<8>(p, need, tag, w, &a.ctl->err, (uint64_t)wall_clock64() + a.wait_ticks)) res_fail(a, sh);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                if (need >> (4 * i) & 1)
+                    x[i] = v4f{word_value(w[4 * i]), word_value(w[4 * i + 1]), word_value(w[4 * i + 2]),
+                               word_value(w[4 * i + 3])};
+            const int32_t e = row_digits<2>(x, 2 * CH, KBL, sq, sh);
+            if (sh.abort) {
+                stop = true;
+                break;
+            }
+            for (int pi = 0; pi < npl; pi++) {
+                row_sums(wlay + (size_t)pi * KBL * 1024, KBL, sq, sh);
+                if (wave == 0) {
+                    const int j = lane & 15;
+                    const int32_t shi = sh.kpart[0][0][j] + sh.kpart[1][0][j] + sh.kpart[2][0][j] + sh.kpart[3][0][j];
+                    const int32_t slo = sh.kpart[0][1][j] + sh.kpart[1][1][j] + sh.kpart[2][1][j] + sh.kpart[3][1][j];
+                    const float v = epilogue_vals(dequant(shi, slo, e, sh.ls[l][pi * PANEL + j]), true,
+                                                  sh.lbias[l][pi * PANEL + j], ACT_NONE, 1.0f, false, 0.0f);
+                    // Output 4 u + q is gate q (i, f, g, o) of unit u: the quad's lane 0 updates the
+                    // cell (src/parakeet.rs:1549-1562): c = f c + i g, h = o tanh(c).
+                    const float gi = quad_lane<0>(v), gf = quad_lane<1>(v), gg = quad_lane<2>(v), go = quad_lane<3>(v);
+                    if (lane < PANEL && (j & 3) == 0) {
+                        const int ul = pi * 4 + (j >> 2), u = pl0 * 4 + ul;
+                        const float ig = sigmoid(gi), fg = sigmoid(gf), g = tanhf(gg), og = sigmoid(go);
+                        const float c = fg * sh.cst[l][ul] + ig * g;
+                        const float hn = og * tanhf(c);
+                        sh.cst[l][ul] = c;
+                        sh.hst[l][ul] = hn;
+                        word_store(a.w_h + ((size_t)l * 2 + (nn & 1)) * h + u, tagged(hn, nn));
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        if (stop) break;
+        if (npp > 0) {
+            const uint64_t *hl = a.w_h + ((size_t)(a.layers - 1) * 2 + (nn & 1)) * h;
+            v4f x[1];
+            const uint64_t *p[4];
+            uint32_t tag[4];
+            uint64_t w[4];
+            uint32_t need = 0;
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                p[qq] = hl + min(4 * tid + qq, h - 1);
+                tag[qq] = nn;
+                if (tid < CH) need |= 1u << qq;
+            }
+            if (!wait_words<4>(p, need, tag, w, &a.ctl->err, (uint64_t)wall_clock64() + a.wait_ticks)) res_fail(a, sh);
+            x[0] = tid < CH ? v4f{word_value(w[0]), word_value(w[1]), word_value(w[2]), word_value(w[3])}
+                            : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const int32_t e = row_digits<1>(x, CH, KBP, sq, sh);
+            if (sh.abort) break;
+            for (int pi = 0; pi < npp; pi++) {
+                row_sums(wp + (size_t)pi * KBP * 1024, KBP, sq, sh);
+                if (wave == 0 && lane < PANEL) {
+                    const int col = (pp0 + pi) * PANEL + lane;
+                    const int32_t shi = sh.kpart[0][0][lane] + sh.kpart[1][0][lane] + sh.kpart[2][0][lane] + sh.kpart[3][0][lane];
+                    const int32_t slo = sh.kpart[0][1][lane] + sh.kpart[1][1][lane] + sh.kpart[2][1][lane] + sh.kpart[3][1][lane];
+                    const float v = epilogue_vals(dequant(shi, slo, e, sh.ps[pi * PANEL + lane]), true,
+                                                  sh.pbias[pi * PANEL + lane], ACT_NONE, 1.0f, false, 0.0f);
+                    if (col < h) {
+                        sh.pst[pi * PANEL + lane] = v;
+                        word_store(a.w_pred + (size_t)(nn & 1) * h + col, tagged(v, nn));
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        n = nn;
+    }
+
+    // The state, the prediction and the position for the caller (or the next launch).
+    if (tid < npl * 4) {
+        const int u = pl0 * 4 + tid;
+        for (int l = 0; l < a.layers; l++) {
+            a.state[(size_t)l * 2 * h + u] = sh.hst[l][tid];
+            a.state[(size_t)l * 2 * h + h + u] = sh.cst[l][tid];
+        }
+    }
+    if (tid < npp * PANEL && pp0 * PANEL + tid < h) a.pred[pp0 * PANEL + tid] = sh.pst[tid];
+    if (b == 0 && tid == 0) {
+        a.ctl->t = t;
+        a.ctl->on_frame = on;
+        a.ctl->ntok = ntok;
+        a.ctl->rows = rows;
+        a.ctl->done = done;
+        a.ctl->step = s;
+        a.ctl->preds = n;
+    }
+}
+
+// The hand-over words at the start of a decode: the prediction and each layer's h with tag 0 in
+// buffer 0, buffer 1 and the logits with no tag, the joint words with the low 16 bits of steps
+// -2 and -1 (which no step of the decode reaches before rewriting them).
+__global__ void tdt_resident_init_kernel(uint64_t *words, int h, int layers, const float *state, const float *pred) {
+    const size_t np = 2 * (size_t)h, nh = (size_t)layers * 2 * h, nb = 2 * (size_t)TDT_ROWS * RES_MAX_GRID,
+                 ne = 2 * (size_t)TDT_ROWS * TDT_EXTRA;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < np + nh + nb + ne;
+         i += (size_t)gridDim.x * blockDim.x) {
+        uint64_t v;
+        if (i < np) {
+            v = i < (size_t)h ? tagged(pred[i], 0) : tagged(0.0f, TAG_NONE);
+        } else if (i < np + nh) {
+            const size_t k = i - np, l = k / (2 * h), par = (k / h) % 2, u = k % h;
+            v = par == 0 ? tagged(state[l * 2 * h + u], 0) : tagged(0.0f, TAG_NONE);
+        } else if (i < np + nh + nb) {
+            const size_t par = (i - np - nh) / ((size_t)TDT_ROWS * RES_MAX_GRID);
+            v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
+        } else {
+            v = tagged(0.0f, TAG_NONE);
+        }
+        words[i] = v;
+    }
+}
+
 }  // namespace
 
 size_t tdt_max_rows(const DeviceWeights &lstm) {
@@ -570,5 +1211,103 @@ hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, siz
 }
 
 size_t tdt_extras_bytes() { return (size_t)TDT_ROWS * TDT_EXTRA * sizeof(float); }
+
+size_t tdt_resident_words(const TdtNet &net) {
+    return 2 * net.h + net.layers * 2 * net.h + 2 * (size_t)TDT_ROWS * RES_MAX_GRID + 2 * (size_t)TDT_ROWS * TDT_EXTRA;
+}
+
+bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
+    plan = TdtPlan{};
+    if (net.joint->precision != INT8 || net.proj->precision != INT8) return false;
+    for (size_t l = 0; l < net.layers; l++)
+        if (net.lstm[l]->precision != INT8) return false;
+    if (net.vocab >= 0xffff || net.h > TDT_MAX_H || net.ndur > (size_t)TDT_MAX_DURATIONS) return false;
+    int dev = 0, cus = 0, coop = 0, max_lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return false;
+    if (cus < 1 || !coop) return false;
+    // Panels spread over at most one workgroup per CU (up to RES_MAX_GRID); the projection's
+    // workgroups follow the LSTM's when both fit.
+    const size_t G = (size_t)std::min(cus, RES_MAX_GRID);
+    const size_t PJ = net.joint->panels, PL = net.lstm[0]->panels, PP = net.proj->panels;
+    TdtPlan p;
+    p.JP = (int)div_ceil(PJ, G);
+    p.GJ = (int)div_ceil(PJ, (size_t)p.JP);
+    p.LP = (int)div_ceil(PL, G);
+    p.GL = (int)div_ceil(PL, (size_t)p.LP);
+    p.PP = (int)div_ceil(PP, G);
+    p.GP = (int)div_ceil(PP, (size_t)p.PP);
+    p.poff = (size_t)(p.GL + p.GP) <= G ? p.GL : 0;
+    p.grid = std::max(p.GJ, std::max(p.GL, p.poff + p.GP));
+    if (p.JP > RES_MAX_PANELS || p.LP > RES_MAX_PANELS || p.PP > RES_MAX_PANELS) return false;
+    const size_t KBJ = net.joint->kb, KBL = net.lstm[0]->kb, KBP = net.proj->kb;
+    p.lds = ((size_t)p.JP * KBJ + net.layers * p.LP * KBL + (size_t)p.PP * KBP) * 1024 +
+            std::max(KBJ * 2048, std::max(KBL, KBP) * 128);
+    const void *f = reinterpret_cast<const void *>(&tdt_resident_kernel);
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, f) != hipSuccess || p.lds + fa.sharedSizeBytes > (size_t)max_lds) return false;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds) != hipSuccess) return false;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, RES_THREADS, p.lds) != hipSuccess || per_cu < 1 ||
+        (size_t)p.grid > (size_t)per_cu * cus)
+        return false;
+    plan = p;
+    return true;
+}
+
+hipError_t launch_tdt_resident_init(const TdtNet &net, uint64_t *words, const float *state, const float *pred,
+                                    hipStream_t s) {
+    hipLaunchKernelGGL(tdt_resident_init_kernel, dim3(64), dim3(256), 0, s, words, (int)net.h, (int)net.layers, state,
+                       pred);
+    return hipGetLastError();
+}
+
+hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &plan, uint64_t *words,
+                               const float *enc, size_t lde, int frames, float *state, float *pred, int32_t *tokens,
+                               int cap, int steps, uint64_t wait_ticks, hipStream_t s) {
+    auto mat = [](const DeviceWeights &d, const float *bias) {
+        return ResMat{d.values, d.scales, bias, d.panel_stride, d.blk_stride, (int)d.n, (int)d.kb, (int)d.panels};
+    };
+    ResArgs a{};
+    a.joint = mat(*net.joint, net.joint_b);
+    a.proj = mat(*net.proj, net.proj_b);
+    for (size_t l = 0; l < net.layers; l++) a.lstm[l] = mat(*net.lstm[l], net.lstm_b[l]);
+    a.emb = net.emb;
+    a.enc = enc;
+    a.lde = lde;
+    a.durations = net.durations;
+    a.tokens = tokens;
+    a.ctl = ctl;
+    a.state = state;
+    a.pred = pred;
+    a.w_pred = words;
+    a.w_h = a.w_pred + 2 * net.h;
+    a.w_part = a.w_h + net.layers * 2 * net.h;
+    a.w_ext = a.w_part + 2 * (size_t)TDT_ROWS * RES_MAX_GRID;
+    a.h = (int)net.h;
+    a.vocab = (int)net.vocab;
+    a.ndur = (int)net.ndur;
+    a.layers = (int)net.layers;
+    a.blank = (int)net.blank;
+    a.max_symbols = (int)net.max_symbols;
+    a.frames = frames;
+    a.cap = cap;
+    a.JP = plan.JP;
+    a.GJ = plan.GJ;
+    a.LP = plan.LP;
+    a.GL = plan.GL;
+    a.PP = plan.PP;
+    a.GP = plan.GP;
+    a.poff = plan.poff;
+    a.grid = plan.grid;
+    a.steps = steps;
+    a.wait_ticks = wait_ticks;
+    void *args[] = {&a};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&tdt_resident_kernel), dim3((unsigned)plan.grid),
+                                      dim3(RES_THREADS), args, (unsigned)plan.lds, s);
+}
 
 }  // namespace tg

@@ -286,6 +286,10 @@ struct TdtCtl {
     int32_t cur;                // the state buffer holding the current LSTM state (0: the caller's)
     int32_t rows;               // frames the next joint scores (1 .. TDT_ROWS)
     TdtSnap snap;
+    // The resident decode's position: steps made and predictions run (the tags of its hand-over
+    // words), and whether a wait passed its deadline.
+    uint32_t step, preds;
+    int32_t err;
 };
 struct TdtTokens {
     int32_t tok[TDT_ROWS];
@@ -307,5 +311,27 @@ hipError_t launch_tdt_predict(TdtCtl *ctl, const TdtTokens &toks, size_t m, cons
 hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, size_t lde, int frames, float *sa,
                            float *sb, float *pred, void *partials, float *extras, int32_t *tokens, int cap,
                            hipStream_t s);
+
+// The resident decode: one cooperative launch makes many steps with the network's matrices held in
+// LDS, the workgroups handing each other values through tagged words.
+constexpr size_t TDT_MAX_H = 992;
+struct TdtPlan {
+    int grid = 0;              // workgroups
+    int JP = 0, GJ = 0;        // joint panels per workgroup, workgroups holding them
+    int LP = 0, GL = 0;        // LSTM panels (of every layer) per workgroup, workgroups holding them
+    int PP = 0, GP = 0, poff = 0;  // projection panels per workgroup, workgroups, the first of them
+    size_t lds = 0;            // dynamic LDS bytes per workgroup
+};
+// Whether the resident decode takes this network on the current device; fills plan and sets the
+// kernel's LDS limit. Needs int8 matrices, vocab < 65535, a cooperative launch and the panels in LDS.
+bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan);
+size_t tdt_resident_words(const TdtNet &net);  // 8-byte hand-over words
+// Writes the hand-over words for a decode from state and pred (tags 0; the other buffers none).
+hipError_t launch_tdt_resident_init(const TdtNet &net, uint64_t *words, const float *state, const float *pred,
+                                    hipStream_t s);
+// Up to steps steps from the position in ctl (written by the host), which the launch updates.
+hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &plan, uint64_t *words,
+                               const float *enc, size_t lde, int frames, float *state, float *pred, int32_t *tokens,
+                               int cap, int steps, uint64_t wait_ticks, hipStream_t s);
 
 }  // namespace tg

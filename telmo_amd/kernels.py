@@ -516,6 +516,15 @@ class TdtDecoder:
                                                 _dev(preds, "float32", "preds"), _len(preds, None, "preds")),
                self._kernels._ctx)
 
+    @property
+    def resident(self) -> bool:
+        """Whether decode runs resident: one launch for the steps, the matrices held in LDS."""
+        return bool(_lib.lib().tg_tdt_is_resident(self._handle))
+
+    def set_resident(self, on: bool) -> None:
+        """Resident decode (raises where the network cannot run it) or one graph of step kernels."""
+        _check(_lib.lib().tg_tdt_set_resident(self._kernels._ctx, self._handle, 1 if on else 0), self._kernels._ctx)
+
     def decode(self, enc_proj, state, pred, frame: int = 0, on_frame: int = 0, cap: Optional[int] = None):
         """The greedy decode over the rows of enc_proj (GPU tensor, frames x >= h) from frame with
         on_frame tokens on it; state (layers x [h, c]) and pred (h) are updated in place. Returns
