@@ -540,6 +540,9 @@ constexpr int RES_WAVES = 4;
 constexpr int RES_THREADS = RES_WAVES * 64;
 constexpr int RES_MAX_PANELS = 8;  // panels of one matrix per workgroup
 constexpr int RES_MAX_GRID = 256;  // workgroups: a row's sixteen decider threads read sixteen words each
+// Copies of every hand-over word: workgroup b reads copy b % RES_COPIES (its XCD, as workgroups are
+// dealt to the eight XCDs in turn), so each word's line has about an eighth of the readers.
+constexpr int RES_COPIES = 8;
 constexpr uint32_t TAG_NONE = 0xffffffffu;
 
 struct ResMat {
@@ -557,11 +560,16 @@ struct ResArgs {
     int32_t *tokens;
     TdtCtl *ctl;
     float *state, *pred;
-    // Hand-over words: the prediction [2][h], the LSTM outputs h [layers][2][h], the joint's best
-    // entries [2][TDT_ROWS][RES_MAX_GRID] and its first and duration logits [2][TDT_ROWS][TDT_EXTRA].
-    uint64_t *w_pred, *w_h, *w_part, *w_ext;
+    // Hand-over words in RES_COPIES copies, cs words apart, of: the prediction [2][h], the LSTM
+    // outputs h [layers][2][h], each workgroup's best vocabulary entry per joint row
+    // [2][TDT_ROWS][RES_MAX_GRID] and the duration-holding joint workgroups' best duration entries
+    // [2][TDT_ROWS][TDT_ROWS].
+    uint64_t *w_pred, *w_h, *w_part, *w_dur;
+    size_t cs;
     int h, vocab, ndur, layers, blank, max_symbols, frames, cap;
-    int JP, GJ, LP, GL, PP, GP, poff, grid;
+    // Workgroups 0 .. GP - 1 hold the projection's panels, PP each; workgroups qoff + j hold joint
+    // panels (j < GJ, JP each) and LSTM panels (j < GL, LP of every layer each).
+    int JP, GJ, LP, GL, PP, GP, qoff, grid;
     int steps;
     uint64_t wait_ticks;  // the longest wait, in wall-clock ticks
 };
@@ -571,6 +579,11 @@ __device__ __forceinline__ uint64_t word_load(const uint64_t *p) {
 }
 __device__ __forceinline__ void word_store(uint64_t *p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Stores v into every copy of a word.
+__device__ __forceinline__ void word_store_all(uint64_t *p, size_t stride, uint64_t v) {
+#pragma unroll
+    for (int c = 0; c < RES_COPIES; c++) word_store(p + c * stride, v);
 }
 __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
     return ((uint64_t)tag << 32) | __float_as_uint(v);
@@ -585,6 +598,35 @@ __device__ __forceinline__ uint64_t tagged_best(Best x, uint32_t step) {
 __device__ __forceinline__ Best best_of(uint64_t w) {
     const uint32_t i = (uint32_t)(w >> 32) & 0xffffu;
     return Best{word_value(w), i == 0xffffu ? INT32_MAX : (int)i};
+}
+
+// One step of the best-entry fold across lanes (DPP control CTRL, within rows of 16 lanes).
+template <int CTRL>
+__device__ __forceinline__ void best_step(float &v, int &i) {
+    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
+    if (before(ov, oi, v, i)) {
+        v = ov;
+        i = oi;
+    }
+}
+// The best entry of each row of 16 lanes, left in all 16: quad_perm [1,0,3,2], [2,3,0,1], then
+// row_half_mirror and row_mirror pair every lane with one of each other group in turn (the order
+// is a total one, so any pairing that reaches every lane gives the same entry).
+__device__ __forceinline__ void best16(float &v, int &i) {
+    best_step<0xB1>(v, i);
+    best_step<0x4E>(v, i);
+    best_step<0x141>(v, i);
+    best_step<0x140>(v, i);
+}
+// v summed over lanes l, l ^ 16, l ^ 32, l ^ 48: v_permlane16_swap / v_permlane32_swap exchange
+// rows 1 and 3 of one operand with rows 0 and 2 (halves 1 and 0) of the other; with both operands
+// v, the two results of each lane are its own value and its partner's.
+__device__ __forceinline__ int sum_groups(int v) {
+    const auto a = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    v = (int)(a[0] + a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)(b[0] + b[1]);
 }
 
 // Waits until word i (bit i of need) carries tag[i], reloading the words still pending each round.
@@ -634,8 +676,7 @@ struct ResShared {
     float ls[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL], lbias[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL];
     float hst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4], cst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4];
     __attribute__((aligned(16))) float pin[TDT_MAX_H];  // the prediction the joint adds
-    float dlog[TDT_ROWS][TDT_MAX_DURATIONS];
-    Best red[RES_WAVES][TDT_ROWS];
+    Best red[RES_WAVES][TDT_ROWS], dred[RES_WAVES][TDT_ROWS];
     int32_t kpart[RES_WAVES][2][PANEL];
     int32_t erow[TDT_ROWS];
     uint32_t slot[RES_WAVES];
@@ -713,10 +754,8 @@ __device__ __forceinline__ void row_sums(const uint8_t *pw, int KB, const uint8_
         dl = __builtin_amdgcn_sdot4(alo.z, wv.z, dl, false);
         dl = __builtin_amdgcn_sdot4(alo.w, wv.w, dl, false);
     }
-    dh += __shfl_xor(dh, 16, 64);
-    dh += __shfl_xor(dh, 32, 64);
-    dl += __shfl_xor(dl, 16, 64);
-    dl += __shfl_xor(dl, 32, 64);
+    dh = sum_groups(dh);
+    dl = sum_groups(dl);
     if (lane < PANEL) {
         sh.kpart[wave][0][lane] = dh;
         sh.kpart[wave][1][lane] = dl;
@@ -728,10 +767,14 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ ResShared sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x;
+    const size_t rc = (size_t)(b % RES_COPIES) * a.cs;  // the copy this workgroup reads
     const int h = a.h, NJ = a.joint.n, KBJ = a.joint.KB, KBL = a.lstm[0].KB, KBP = a.proj.KB;
-    const int pj0 = b * a.JP, npj = b < a.GJ ? min(a.JP, a.joint.P - pj0) : 0;
-    const int pl0 = b * a.LP, npl = b < a.GL ? min(a.LP, a.lstm[0].P - pl0) : 0;
-    const int bp = b - a.poff, pp0 = bp * a.PP, npp = bp >= 0 && bp < a.GP ? min(a.PP, a.proj.P - pp0) : 0;
+    const int bq = b - a.qoff;  // among the joint and LSTM workgroups
+    const int pj0 = bq * a.JP, npj = bq >= 0 && bq < a.GJ ? min(a.JP, a.joint.P - pj0) : 0;
+    const int pl0 = bq * a.LP, npl = bq >= 0 && bq < a.GL ? min(a.LP, a.lstm[0].P - pl0) : 0;
+    const int pp0 = b * a.PP, npp = b < a.GP ? min(a.PP, a.proj.P - pp0) : 0;
+    // The joint workgroups holding duration columns: nd of them from jd0 (at most 5 for 64 durations).
+    const int jd0 = (a.vocab / PANEL) / a.JP, nd = ((NJ - 1) / PANEL) / a.JP - jd0 + 1;
     uint8_t *wj = lds;
     uint8_t *wl = wj + (size_t)a.JP * KBJ * 1024;
     uint8_t *wp = wl + (size_t)a.layers * a.LP * KBL * 1024;
@@ -778,7 +821,6 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             break;
         }
         const uint32_t par = s & 1;
-        uint64_t *ext = a.w_ext + (size_t)par * TDT_ROWS * TDT_EXTRA;
         // ---- The joint over rows t .. t + rows - 1: z = relu(enc_proj[min(t + r, frames - 1)] + pred).
         if (npj > 0) {
             // Wavefront w holds rows w + 4 j, lane l chunks l + 64 i (h <= 992: at most 248 chunks).
@@ -802,7 +844,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const int i = tid + RES_THREADS * q;
-                    p[q] = a.w_pred + (size_t)(n & 1) * h + min(i, h - 1);
+                    p[q] = a.w_pred + rc + (size_t)(n & 1) * h + min(i, h - 1);
                     tag[q] = n;
                     if (i < h) need |= 1u << q;
                 }
@@ -848,20 +890,34 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             }
             __syncthreads();
             // Wavefront w scores panels w, w + 4, ... of this workgroup: element v of lane l is row
-            // 4 (l / 16) + v, column l % 16.
-            Best mine[4];
+            // 4 (l / 16) + v, column l % 16. Each row keeps its best vocabulary entry and its best
+            // duration entry (index d for column vocab + d). A NaN first logit (column 0) is never
+            // beaten in the reference's argmax: it enters as (+inf, 0), which nothing comes before;
+            // a NaN first duration logit likewise.
+            Best mine[4], dmine[4];
 #pragma unroll
-            for (int v = 0; v < 4; v++) mine[v] = Best{__builtin_nanf(""), INT32_MAX};
+            for (int v = 0; v < 4; v++) mine[v] = dmine[v] = Best{__builtin_nanf(""), INT32_MAX};
             const int orow = (lane >> 4) * 4, j16 = lane & 15;
             for (int pi = wave; pi < npj; pi += RES_WAVES) {
                 gemv::v4i hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
                 const uint8_t *wb = wj + (size_t)pi * KBJ * 1024 + lane * 16;
-                for (int tk = 0; tk < KBJ; tk++) {
-                    const gemv::v4i ahi = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + lane * 16);
-                    const gemv::v4i alo = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + 1024 + lane * 16);
-                    const gemv::v4i wv = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)tk * 1024);
-                    hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, wv, hi, 0, 0, 0);
-                    lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, wv, lo, 0, 0, 0);
+                // Four k-blocks' operands are read before their MFMAs.
+                for (int t0 = 0; t0 < KBJ; t0 += 4) {
+                    gemv::v4i ah[4], al[4], wv[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int tk = min(t0 + u, KBJ - 1);
+                        ah[u] = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + lane * 16);
+                        al[u] = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + 1024 + lane * 16);
+                        wv[u] = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)tk * 1024);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        if (t0 + u < KBJ) {
+                            hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[u], wv[u], hi, 0, 0, 0);
+                            lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[u], wv[u], lo, 0, 0, 0);
+                        }
+                    }
                 }
                 const int col = (pj0 + pi) * PANEL + j16;
                 const float sc = sh.js[pi * PANEL + j16], bs = sh.jbias[pi * PANEL + j16];
@@ -869,80 +925,74 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                 for (int v = 0; v < 4; v++) {
                     const int r = orow + v;
                     if (r < rows && col < NJ) {
-                        const float val =
+                        float val =
                             epilogue_vals(dequant(hi[v], lo[v], sh.erow[r], sc), true, bs, ACT_NONE, 1.0f, false, 0.0f);
-                        if (col < a.vocab) {
-                            if (before(val, col, mine[v].v, mine[v].i)) mine[v] = Best{val, col};
-                            if (col == 0) word_store(ext + (size_t)r * TDT_EXTRA, tagged(val, s));
-                        } else {
-                            word_store(ext + (size_t)r * TDT_EXTRA + 1 + (col - a.vocab), tagged(val, s));
-                        }
+                        const bool voc = col < a.vocab;
+                        const int idx = voc ? col : col - a.vocab;
+                        if (idx == 0 && __builtin_isnan(val)) val = __builtin_inff();
+                        Best &m = voc ? mine[v] : dmine[v];
+                        if (before(val, idx, m.v, m.i)) m = Best{val, idx};
                     }
                 }
             }
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                float bv = mine[v].v;
-                int bi = mine[v].i;
-#pragma unroll
-                for (int off = 1; off < 16; off <<= 1) {
-                    const float ov = __shfl_xor(bv, off, 64);
-                    const int oi = __shfl_xor(bi, off, 64);
-                    if (before(ov, oi, bv, bi)) {
-                        bv = ov;
-                        bi = oi;
-                    }
+                best16(mine[v].v, mine[v].i);
+                best16(dmine[v].v, dmine[v].i);
+                if (j16 == 0) {
+                    sh.red[wave][orow + v] = mine[v];
+                    sh.dred[wave][orow + v] = dmine[v];
                 }
-                if (j16 == 0) sh.red[wave][orow + v] = Best{bv, bi};
             }
         }
         __syncthreads();
-        // Every workgroup's word for every row of the step (none from those without joint panels).
-        if (tid < TDT_ROWS) {
-            Best x{__builtin_nanf(""), INT32_MAX};
+        // Every workgroup's word for every row of the step (none from those without joint panels),
+        // thread (c, r) writing copy c of row r's; the joint workgroups holding duration columns also
+        // write their best duration entries.
+        if (tid < TDT_ROWS * RES_COPIES) {
+            const int r = tid & (TDT_ROWS - 1), c = tid / TDT_ROWS;
+            Best x{__builtin_nanf(""), INT32_MAX}, xd{__builtin_nanf(""), INT32_MAX};
             if (npj > 0) {
 #pragma unroll
-                for (int q = 0; q < RES_WAVES; q++)
-                    if (before(sh.red[q][tid].v, sh.red[q][tid].i, x.v, x.i)) x = sh.red[q][tid];
+                for (int q = 0; q < RES_WAVES; q++) {
+                    if (before(sh.red[q][r].v, sh.red[q][r].i, x.v, x.i)) x = sh.red[q][r];
+                    if (before(sh.dred[q][r].v, sh.dred[q][r].i, xd.v, xd.i)) xd = sh.dred[q][r];
+                }
             }
-            word_store(a.w_part + ((size_t)par * TDT_ROWS + tid) * RES_MAX_GRID + b, tagged_best(x, s));
+            word_store(a.w_part + c * a.cs + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + b, tagged_best(x, s));
+            if (bq >= jd0 && bq < jd0 + nd)
+                word_store(a.w_dur + c * a.cs + ((size_t)par * TDT_ROWS + r) * TDT_ROWS + (bq - jd0), tagged_best(xd, s));
         }
         // ---- The decision, alike in every workgroup. Thread (r, q) waits for row r's words of
-        // workgroups q, q + 16, ... and its logits q, q + 16, ... (the first, then the durations).
+        // workgroups q, q + 16, ... and for duration word q.
         {
             const int r = tid >> 4, q = tid & 15;
             const bool live = r < rows;
-            const uint64_t *pb = a.w_part + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + q;
-            const uint64_t *pe = ext + (size_t)r * TDT_EXTRA;
-            uint64_t pw[16], ew[5];
-            uint32_t pneed = 0, eneed = 0;
+            const uint64_t *pb = a.w_part + rc + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + q;
+            const uint64_t *pd = a.w_dur + rc + ((size_t)par * TDT_ROWS + r) * TDT_ROWS + q;
+            uint64_t pw[16], dw = 0;
+            uint32_t pneed = 0;
+            bool dneed = live && q < nd;
 #pragma unroll
             for (int u = 0; u < 16; u++)
                 if (live && q + 16 * u < a.grid) pneed |= 1u << u;
-#pragma unroll
-            for (int v = 0; v < 5; v++)
-                if (live && q + 16 * v <= a.ndur) eneed |= 1u << v;
             const uint64_t deadline = (uint64_t)wall_clock64() + a.wait_ticks;
             for (int round = 0;; round++) {
 #pragma unroll
                 for (int u = 0; u < 16; u++)
                     if (pneed >> u & 1) pw[u] = word_load(pb + 16 * u);
-#pragma unroll
-                for (int v = 0; v < 5; v++)
-                    if (eneed >> v & 1) ew[v] = word_load(pe + min(q + 16 * v, a.ndur));
+                if (dneed) dw = word_load(pd);
 #pragma unroll
                 for (int u = 0; u < 16; u++)
                     if ((pneed >> u & 1) && (uint32_t)(pw[u] >> 48) == (s & 0xffffu)) pneed &= ~(1u << u);
-#pragma unroll
-                for (int v = 0; v < 5; v++)
-                    if ((eneed >> v & 1) && (uint32_t)(ew[v] >> 32) == s) eneed &= ~(1u << v);
-                if (!(pneed | eneed)) break;
+                if (dneed && (uint32_t)(dw >> 48) == (s & 0xffffu)) dneed = false;
+                if (!pneed && !dneed) break;
                 if ((round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(&a.ctl->err) != 0)) {
                     res_fail(a, sh);
                     break;
                 }
             }
-            Best x{__builtin_nanf(""), INT32_MAX};
+            Best x{__builtin_nanf(""), INT32_MAX}, xd{__builtin_nanf(""), INT32_MAX};
 #pragma unroll
             for (int u = 0; u < 16; u++) {
                 if (live && q + 16 * u < a.grid) {
@@ -950,33 +1000,16 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                     if (before(y.v, y.i, x.v, x.i)) x = y;
                 }
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-                const float ov = __shfl_xor(x.v, off, 64);
-                const int oi = __shfl_xor(x.i, off, 64);
-                if (before(ov, oi, x.v, x.i)) x = Best{ov, oi};
-            }
-            if (live) {
-#pragma unroll
-                for (int v = 0; v < 5; v++) {
-                    const int qq = q + 16 * v;
-                    if (qq >= 1 && qq <= a.ndur) sh.dlog[r][qq - 1] = word_value(ew[v]);
-                }
-                if (q == 0) {
-                    const float first = word_value(ew[0]);  // a NaN first is never beaten
-                    sh.tok_s[r] = __builtin_isnan(first) || x.i == INT32_MAX ? 0 : x.i;
-                }
+            if (live && q < nd) xd = best_of(dw);
+            best16(x.v, x.i);
+            best16(xd.v, xd.i);
+            if (live && q == 0) {
+                sh.tok_s[r] = x.i == INT32_MAX ? 0 : x.i;
+                sh.dur_s[r] = sh.durs[xd.i == INT32_MAX ? 0 : xd.i];
             }
         }
         __syncthreads();
         if (sh.abort) break;
-        if (tid < rows) {
-            int k = 0;
-            for (int i = 1; i < a.ndur; i++)
-                if (sh.dlog[tid][i] > sh.dlog[tid][k]) k = i;
-            sh.dur_s[tid] = sh.durs[k];
-        }
-        __syncthreads();
         if (tid == 0) {
             const Walked wk = walk_window(t, rows, on, ntok, sh.tok_s, sh.dur_s, a.blank, a.frames, a.max_symbols,
                                           a.tokens, a.cap, b == 0);
@@ -1004,8 +1037,8 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
         for (int l = 0; l < a.layers && !stop; l++) {
             if (npl == 0) continue;
             const uint8_t *wlay = wl + (size_t)l * a.LP * KBL * 1024;
-            const uint64_t *hnew = a.w_h + ((size_t)(l - 1) * 2 + (nn & 1)) * h;  // used for l >= 1
-            const uint64_t *hold = a.w_h + ((size_t)l * 2 + (n & 1)) * h;
+            const uint64_t *hnew = a.w_h + rc + ((size_t)(l - 1) * 2 + (nn & 1)) * h;  // used for l >= 1
+            const uint64_t *hold = a.w_h + rc + ((size_t)l * 2 + (n & 1)) * h;
             v4f x[2];
             const uint64_t *p[8];
             uint32_t tag[8];
@@ -1053,7 +1086,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                         const float hn = og * tanhf(c);
                         sh.cst[l][ul] = c;
                         sh.hst[l][ul] = hn;
-                        word_store(a.w_h + ((size_t)l * 2 + (nn & 1)) * h + u, tagged(hn, nn));
+                        word_store_all(a.w_h + ((size_t)l * 2 + (nn & 1)) * h + u, a.cs, tagged(hn, nn));
                     }
                 }
                 __syncthreads();
@@ -1061,7 +1094,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
         }
         if (stop) break;
         if (npp > 0) {
-            const uint64_t *hl = a.w_h + ((size_t)(a.layers - 1) * 2 + (nn & 1)) * h;
+            const uint64_t *hl = a.w_h + rc + ((size_t)(a.layers - 1) * 2 + (nn & 1)) * h;
             v4f x[1];
             const uint64_t *p[4];
             uint32_t tag[4];
@@ -1088,7 +1121,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                                                   sh.pbias[pi * PANEL + lane], ACT_NONE, 1.0f, false, 0.0f);
                     if (col < h) {
                         sh.pst[pi * PANEL + lane] = v;
-                        word_store(a.w_pred + (size_t)(nn & 1) * h + col, tagged(v, nn));
+                        word_store_all(a.w_pred + (size_t)(nn & 1) * h + col, a.cs, tagged(v, nn));
                     }
                 }
                 __syncthreads();
@@ -1118,13 +1151,15 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
 }
 
 // The hand-over words at the start of a decode: the prediction and each layer's h with tag 0 in
-// buffer 0, buffer 1 and the logits with no tag, the joint words with the low 16 bits of steps
-// -2 and -1 (which no step of the decode reaches before rewriting them).
+// buffer 0 and no tag in buffer 1; the joint's best-entry words (vocabulary and duration) with the
+// low 16 bits of steps -2 and -1, which no step reaches before rewriting them (every step rewrites
+// every such word of its buffer).
 __global__ void tdt_resident_init_kernel(uint64_t *words, int h, int layers, const float *state, const float *pred) {
     const size_t np = 2 * (size_t)h, nh = (size_t)layers * 2 * h, nb = 2 * (size_t)TDT_ROWS * RES_MAX_GRID,
-                 ne = 2 * (size_t)TDT_ROWS * TDT_EXTRA;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < np + nh + nb + ne;
-         i += (size_t)gridDim.x * blockDim.x) {
+                 nd = 2 * (size_t)TDT_ROWS * TDT_ROWS, per = np + nh + nb + nd;
+    for (size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x; j < RES_COPIES * per;
+         j += (size_t)gridDim.x * blockDim.x) {
+        const size_t i = j % per;
         uint64_t v;
         if (i < np) {
             v = i < (size_t)h ? tagged(pred[i], 0) : tagged(0.0f, TAG_NONE);
@@ -1135,9 +1170,10 @@ __global__ void tdt_resident_init_kernel(uint64_t *words, int h, int layers, con
             const size_t par = (i - np - nh) / ((size_t)TDT_ROWS * RES_MAX_GRID);
             v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
         } else {
-            v = tagged(0.0f, TAG_NONE);
+            const size_t par = (i - np - nh - nb) / ((size_t)TDT_ROWS * TDT_ROWS);
+            v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
         }
-        words[i] = v;
+        words[j] = v;
     }
 }
 
@@ -1212,9 +1248,12 @@ hipError_t launch_tdt_step(TdtCtl *ctl, const TdtNet &net, const float *enc, siz
 
 size_t tdt_extras_bytes() { return (size_t)TDT_ROWS * TDT_EXTRA * sizeof(float); }
 
-size_t tdt_resident_words(const TdtNet &net) {
-    return 2 * net.h + net.layers * 2 * net.h + 2 * (size_t)TDT_ROWS * RES_MAX_GRID + 2 * (size_t)TDT_ROWS * TDT_EXTRA;
+// Words of one copy of the hand-over buffers.
+static size_t words_per_copy(const TdtNet &net) {
+    return 2 * net.h + net.layers * 2 * net.h + 2 * (size_t)TDT_ROWS * RES_MAX_GRID + 2 * (size_t)TDT_ROWS * TDT_ROWS;
 }
+
+size_t tdt_resident_words(const TdtNet &net) { return RES_COPIES * words_per_copy(net); }
 
 bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
     plan = TdtPlan{};
@@ -1229,8 +1268,9 @@ bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
         hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
         return false;
     if (cus < 1 || !coop) return false;
-    // Panels spread over at most one workgroup per CU (up to RES_MAX_GRID); the projection's
-    // workgroups follow the LSTM's when both fit.
+    // Panels spread over at most one workgroup per CU (up to RES_MAX_GRID). The projection's
+    // workgroups come first and hold nothing else when the grid has room (their joint would start
+    // late, after the projection); the joint and the LSTM share the rest.
     const size_t G = (size_t)std::min(cus, RES_MAX_GRID);
     const size_t PJ = net.joint->panels, PL = net.lstm[0]->panels, PP = net.proj->panels;
     TdtPlan p;
@@ -1240,9 +1280,12 @@ bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
     p.GL = (int)div_ceil(PL, (size_t)p.LP);
     p.PP = (int)div_ceil(PP, G);
     p.GP = (int)div_ceil(PP, (size_t)p.PP);
-    p.poff = (size_t)(p.GL + p.GP) <= G ? p.GL : 0;
-    p.grid = std::max(p.GJ, std::max(p.GL, p.poff + p.GP));
+    p.qoff = (size_t)(p.GP + std::max(p.GJ, p.GL)) <= G ? p.GP : 0;
+    p.grid = std::max(p.GP, p.qoff + std::max(p.GJ, p.GL));
     if (p.JP > RES_MAX_PANELS || p.LP > RES_MAX_PANELS || p.PP > RES_MAX_PANELS) return false;
+    // The joint workgroups holding duration columns write one word each per row: at most TDT_ROWS.
+    const size_t nd = (((net.vocab + net.ndur - 1) / PANEL) / p.JP) - ((net.vocab / PANEL) / p.JP) + 1;
+    if (nd > (size_t)TDT_ROWS) return false;
     const size_t KBJ = net.joint->kb, KBL = net.lstm[0]->kb, KBP = net.proj->kb;
     p.lds = ((size_t)p.JP * KBJ + net.layers * p.LP * KBL + (size_t)p.PP * KBP) * 1024 +
             std::max(KBJ * 2048, std::max(KBL, KBP) * 128);
@@ -1260,7 +1303,7 @@ bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
 
 hipError_t launch_tdt_resident_init(const TdtNet &net, uint64_t *words, const float *state, const float *pred,
                                     hipStream_t s) {
-    hipLaunchKernelGGL(tdt_resident_init_kernel, dim3(64), dim3(256), 0, s, words, (int)net.h, (int)net.layers, state,
+    hipLaunchKernelGGL(tdt_resident_init_kernel, dim3(256), dim3(256), 0, s, words, (int)net.h, (int)net.layers, state,
                        pred);
     return hipGetLastError();
 }
@@ -1286,7 +1329,8 @@ hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &pl
     a.w_pred = words;
     a.w_h = a.w_pred + 2 * net.h;
     a.w_part = a.w_h + net.layers * 2 * net.h;
-    a.w_ext = a.w_part + 2 * (size_t)TDT_ROWS * RES_MAX_GRID;
+    a.w_dur = a.w_part + 2 * (size_t)TDT_ROWS * RES_MAX_GRID;
+    a.cs = words_per_copy(net);
     a.h = (int)net.h;
     a.vocab = (int)net.vocab;
     a.ndur = (int)net.ndur;
@@ -1301,7 +1345,7 @@ hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &pl
     a.GL = plan.GL;
     a.PP = plan.PP;
     a.GP = plan.GP;
-    a.poff = plan.poff;
+    a.qoff = plan.qoff;
     a.grid = plan.grid;
     a.steps = steps;
     a.wait_ticks = wait_ticks;

@@ -319,7 +319,8 @@ struct TdtPlan {
     int grid = 0;              // workgroups
     int JP = 0, GJ = 0;        // joint panels per workgroup, workgroups holding them
     int LP = 0, GL = 0;        // LSTM panels (of every layer) per workgroup, workgroups holding them
-    int PP = 0, GP = 0, poff = 0;  // projection panels per workgroup, workgroups, the first of them
+    int PP = 0, GP = 0;        // projection panels per workgroup, workgroups (the first GP)
+    int qoff = 0;              // the first joint / LSTM workgroup
     size_t lds = 0;            // dynamic LDS bytes per workgroup
 };
 // Whether the resident decode takes this network on the current device; fills plan and sets the
