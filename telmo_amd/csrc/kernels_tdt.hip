@@ -543,6 +543,7 @@ constexpr int RES_MAX_GRID = 256;  // workgroups: a row's sixteen decider thread
 // Copies of every hand-over word: workgroup b reads copy b % RES_COPIES (its XCD, as workgroups are
 // dealt to the eight XCDs in turn), so each word's line has about an eighth of the readers.
 constexpr int RES_COPIES = 8;
+constexpr int RES_DEC = 6;  // words of a decision: frame, tokens on it, tokens emitted, token, rows, done
 constexpr uint32_t TAG_NONE = 0xffffffffu;
 
 struct ResMat {
@@ -561,10 +562,11 @@ struct ResArgs {
     TdtCtl *ctl;
     float *state, *pred;
     // Hand-over words in RES_COPIES copies, cs words apart, of: the prediction [2][h], the LSTM
-    // outputs h [layers][2][h], each workgroup's best vocabulary entry per joint row
-    // [2][TDT_ROWS][RES_MAX_GRID] and the duration-holding joint workgroups' best duration entries
-    // [2][TDT_ROWS][TDT_ROWS].
-    uint64_t *w_pred, *w_h, *w_part, *w_dur;
+    // outputs h [layers][2][h] and the decision [2][RES_DEC]; in the first copy only, each
+    // workgroup's best vocabulary entry per joint row [2][TDT_ROWS][RES_MAX_GRID] and the
+    // duration-holding joint workgroups' best duration entries [2][TDT_ROWS][TDT_ROWS], which only
+    // workgroup 0 reads.
+    uint64_t *w_pred, *w_h, *w_part, *w_dur, *w_dec;
     size_t cs;
     int h, vocab, ndur, layers, blank, max_symbols, frames, cap;
     // Workgroups 0 .. GP - 1 hold the projection's panels, PP each; workgroups qoff + j hold joint
@@ -677,6 +679,7 @@ struct ResShared {
     float hst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4], cst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4];
     __attribute__((aligned(16))) float pin[TDT_MAX_H];  // the prediction the joint adds
     Best red[RES_WAVES][TDT_ROWS], dred[RES_WAVES][TDT_ROWS];
+    Best cand[RES_THREADS / 16], dcand[RES_THREADS / 16];  // the decider's 16-lane group bests
     int32_t kpart[RES_WAVES][2][PANEL];
     int32_t erow[TDT_ROWS];
     uint32_t slot[RES_WAVES];
@@ -946,41 +949,47 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             }
         }
         __syncthreads();
-        // Every workgroup's word for every row of the step (none from those without joint panels),
-        // thread (c, r) writing copy c of row r's; the joint workgroups holding duration columns also
-        // write their best duration entries.
-        if (tid < TDT_ROWS * RES_COPIES) {
-            const int r = tid & (TDT_ROWS - 1), c = tid / TDT_ROWS;
+        // Every workgroup's word for every row of the step (none from those without joint panels);
+        // the joint workgroups holding duration columns also write their best duration entries.
+        if (tid < TDT_ROWS) {
             Best x{__builtin_nanf(""), INT32_MAX}, xd{__builtin_nanf(""), INT32_MAX};
             if (npj > 0) {
 #pragma unroll
                 for (int q = 0; q < RES_WAVES; q++) {
-                    if (before(sh.red[q][r].v, sh.red[q][r].i, x.v, x.i)) x = sh.red[q][r];
-                    if (before(sh.dred[q][r].v, sh.dred[q][r].i, xd.v, xd.i)) xd = sh.dred[q][r];
+                    if (before(sh.red[q][tid].v, sh.red[q][tid].i, x.v, x.i)) x = sh.red[q][tid];
+                    if (before(sh.dred[q][tid].v, sh.dred[q][tid].i, xd.v, xd.i)) xd = sh.dred[q][tid];
                 }
             }
-            word_store(a.w_part + c * a.cs + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + b, tagged_best(x, s));
+            word_store(a.w_part + ((size_t)par * TDT_ROWS + tid) * RES_MAX_GRID + b, tagged_best(x, s));
             if (bq >= jd0 && bq < jd0 + nd)
-                word_store(a.w_dur + c * a.cs + ((size_t)par * TDT_ROWS + r) * TDT_ROWS + (bq - jd0), tagged_best(xd, s));
+                word_store(a.w_dur + ((size_t)par * TDT_ROWS + tid) * TDT_ROWS + (bq - jd0), tagged_best(xd, s));
         }
-        // ---- The decision, alike in every workgroup. Thread (r, q) waits for row r's words of
-        // workgroups q, q + 16, ... and for duration word q.
-        {
-            const int r = tid >> 4, q = tid & 15;
+        // ---- The decision. Workgroup 0 (a projection workgroup, idle during the joint when the grid
+        // has room for both) gathers the words, walks the window, records the token and publishes the
+        // outcome in RES_COPIES copies; the others wait for their copy (a few words on one line,
+        // where every workgroup reading every joint word would queue thousands of line requests). Thread (r, q) of workgroup 0 waits for row r's words of workgroups q,
+        // q + 16, ... and for duration word q.
+        if (b == 0) {
+            // The window's rows rounded up to a power of two, R, share the threads: g = 256 / R per
+            // row, thread j of row r reading the words of workgroups j, j + g, ... and, for j < nd,
+            // duration word j. Coherent loads of one wavefront are served about one after another,
+            // so the words are spread over all four wavefronts rather than stacked in one.
+            const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : TDT_ROWS;
+            const int g = RES_THREADS / R, r = tid / g, j = tid - r * g;
             const bool live = r < rows;
-            const uint64_t *pb = a.w_part + rc + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + q;
-            const uint64_t *pd = a.w_dur + rc + ((size_t)par * TDT_ROWS + r) * TDT_ROWS + q;
+            const uint64_t *pb = a.w_part + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + j;
+            const uint64_t *pd = a.w_dur + ((size_t)par * TDT_ROWS + r) * TDT_ROWS + min(j, TDT_ROWS - 1);
             uint64_t pw[16], dw = 0;
             uint32_t pneed = 0;
-            bool dneed = live && q < nd;
+            bool dneed = live && j < nd;
 #pragma unroll
             for (int u = 0; u < 16; u++)
-                if (live && q + 16 * u < a.grid) pneed |= 1u << u;
+                if (live && j + g * u < a.grid) pneed |= 1u << u;
             const uint64_t deadline = (uint64_t)wall_clock64() + a.wait_ticks;
             for (int round = 0;; round++) {
 #pragma unroll
                 for (int u = 0; u < 16; u++)
-                    if (pneed >> u & 1) pw[u] = word_load(pb + 16 * u);
+                    if (pneed >> u & 1) pw[u] = word_load(pb + g * u);
                 if (dneed) dw = word_load(pd);
 #pragma unroll
                 for (int u = 0; u < 16; u++)
@@ -992,35 +1001,60 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                     break;
                 }
             }
+            // Each group of 16 lanes (inside one row's threads, g >= 16) folds its entries; thread r
+            // then takes the best of its row's g / 16 groups, and the duration entry of its first.
             Best x{__builtin_nanf(""), INT32_MAX}, xd{__builtin_nanf(""), INT32_MAX};
 #pragma unroll
             for (int u = 0; u < 16; u++) {
-                if (live && q + 16 * u < a.grid) {
+                if (live && j + g * u < a.grid) {
                     const Best y = best_of(pw[u]);
                     if (before(y.v, y.i, x.v, x.i)) x = y;
                 }
             }
-            if (live && q < nd) xd = best_of(dw);
+            if (live && j < nd) xd = best_of(dw);
             best16(x.v, x.i);
             best16(xd.v, xd.i);
-            if (live && q == 0) {
-                sh.tok_s[r] = x.i == INT32_MAX ? 0 : x.i;
-                sh.dur_s[r] = sh.durs[xd.i == INT32_MAX ? 0 : xd.i];
+            if ((lane & 15) == 0) {
+                sh.cand[tid >> 4] = x;
+                sh.dcand[tid >> 4] = xd;
             }
+            __syncthreads();
+            if (tid < rows) {
+                const int k0 = tid * (g / 16);
+                Best bx = sh.cand[k0];
+                for (int k = 1; k < g / 16; k++)
+                    if (before(sh.cand[k0 + k].v, sh.cand[k0 + k].i, bx.v, bx.i)) bx = sh.cand[k0 + k];
+                const Best bd = sh.dcand[k0];
+                sh.tok_s[tid] = bx.i == INT32_MAX ? 0 : bx.i;
+                sh.dur_s[tid] = sh.durs[bd.i == INT32_MAX ? 0 : bd.i];
+            }
+            __syncthreads();
+            if (sh.abort) break;
+            if (tid == 0) {
+                const Walked wk = walk_window(t, rows, on, ntok, sh.tok_s, sh.dur_s, a.blank, a.frames, a.max_symbols,
+                                              a.tokens, a.cap, true);
+                sh.dec[0] = wk.t;
+                sh.dec[1] = wk.on;
+                sh.dec[2] = wk.ntok;
+                sh.dec[3] = wk.token;
+                sh.dec[4] = wk.rows;
+                sh.dec[5] = wk.done;
+            }
+            __syncthreads();
+            if (tid < RES_DEC * RES_COPIES)
+                word_store(a.w_dec + (size_t)(tid / RES_DEC) * a.cs + par * RES_DEC + tid % RES_DEC,
+                           tagged(__int_as_float(sh.dec[tid % RES_DEC]), s));
+        } else {
+            if (tid < RES_DEC) {
+                const uint64_t *p[1] = {a.w_dec + rc + par * RES_DEC + tid};
+                const uint32_t tag[1] = {s};
+                uint64_t w[1];
+                if (!wait_words<1>(p, 1u, tag, w, &a.ctl->err, (uint64_t)wall_clock64() + a.wait_ticks)) res_fail(a, sh);
+                sh.dec[tid] = __float_as_int(word_value(w[0]));
+            }
+            __syncthreads();
+            if (sh.abort) break;
         }
-        __syncthreads();
-        if (sh.abort) break;
-        if (tid == 0) {
-            const Walked wk = walk_window(t, rows, on, ntok, sh.tok_s, sh.dur_s, a.blank, a.frames, a.max_symbols,
-                                          a.tokens, a.cap, b == 0);
-            sh.dec[0] = wk.t;
-            sh.dec[1] = wk.on;
-            sh.dec[2] = wk.ntok;
-            sh.dec[3] = wk.token;
-            sh.dec[4] = wk.rows;
-            sh.dec[5] = wk.done;
-        }
-        __syncthreads();
         t = sh.dec[0];
         on = sh.dec[1];
         ntok = sh.dec[2];
@@ -1156,7 +1190,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
 // every such word of its buffer).
 __global__ void tdt_resident_init_kernel(uint64_t *words, int h, int layers, const float *state, const float *pred) {
     const size_t np = 2 * (size_t)h, nh = (size_t)layers * 2 * h, nb = 2 * (size_t)TDT_ROWS * RES_MAX_GRID,
-                 nd = 2 * (size_t)TDT_ROWS * TDT_ROWS, per = np + nh + nb + nd;
+                 nd = 2 * (size_t)TDT_ROWS * TDT_ROWS, per = np + nh + nb + nd + 2 * RES_DEC;
     for (size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x; j < RES_COPIES * per;
          j += (size_t)gridDim.x * blockDim.x) {
         const size_t i = j % per;
@@ -1169,9 +1203,11 @@ __global__ void tdt_resident_init_kernel(uint64_t *words, int h, int layers, con
         } else if (i < np + nh + nb) {
             const size_t par = (i - np - nh) / ((size_t)TDT_ROWS * RES_MAX_GRID);
             v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
-        } else {
+        } else if (i < np + nh + nb + nd) {
             const size_t par = (i - np - nh - nb) / ((size_t)TDT_ROWS * TDT_ROWS);
             v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
+        } else {
+            v = tagged(0.0f, TAG_NONE);
         }
         words[j] = v;
     }
@@ -1250,7 +1286,8 @@ size_t tdt_extras_bytes() { return (size_t)TDT_ROWS * TDT_EXTRA * sizeof(float);
 
 // Words of one copy of the hand-over buffers.
 static size_t words_per_copy(const TdtNet &net) {
-    return 2 * net.h + net.layers * 2 * net.h + 2 * (size_t)TDT_ROWS * RES_MAX_GRID + 2 * (size_t)TDT_ROWS * TDT_ROWS;
+    return 2 * net.h + net.layers * 2 * net.h + 2 * (size_t)TDT_ROWS * RES_MAX_GRID +
+           2 * (size_t)TDT_ROWS * TDT_ROWS + 2 * RES_DEC;
 }
 
 size_t tdt_resident_words(const TdtNet &net) { return RES_COPIES * words_per_copy(net); }
@@ -1330,6 +1367,7 @@ hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &pl
     a.w_h = a.w_pred + 2 * net.h;
     a.w_part = a.w_h + net.layers * 2 * net.h;
     a.w_dur = a.w_part + 2 * (size_t)TDT_ROWS * RES_MAX_GRID;
+    a.w_dec = a.w_dur + 2 * (size_t)TDT_ROWS * TDT_ROWS;
     a.cs = words_per_copy(net);
     a.h = (int)net.h;
     a.vocab = (int)net.vocab;
