@@ -938,10 +938,11 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                     }
                 }
             }
+            const bool has_dur = bq >= jd0 && bq < jd0 + nd;  // uniform: only these hold duration columns
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 best16(mine[v].v, mine[v].i);
-                best16(dmine[v].v, dmine[v].i);
+                if (has_dur) best16(dmine[v].v, dmine[v].i);
                 if (j16 == 0) {
                     sh.red[wave][orow + v] = mine[v];
                     sh.dred[wave][orow + v] = dmine[v];
