@@ -591,36 +591,46 @@ __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
     return ((uint64_t)tag << 32) | __float_as_uint(v);
 }
 __device__ __forceinline__ float word_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
-// A workgroup's best entry of a joint row: the low 16 bits of the step, the index (0xffff: none,
-// so vocab < 65535) and the value.
-__device__ __forceinline__ uint64_t tagged_best(Best x, uint32_t step) {
-    const uint32_t i = x.i == INT32_MAX ? 0xffffu : (uint32_t)x.i;
-    return ((uint64_t)(step & 0xffffu) << 48) | ((uint64_t)i << 32) | __float_as_uint(x.v);
+// A candidate of the resident decode's argmaxes as integers: k orders the values (larger k, larger
+// value; 0 for NaN, which never wins, and for no entry), i is the index (0xffffffff: none). The
+// reference's scan keeps the first of equal largest values: the larger k wins, then the smaller i.
+struct Key {
+    uint32_t k, i;
+};
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    if (__builtin_isnan(v)) return 0u;
+    if (u == 0x80000000u) return 0x80000000u;  // -0 equals +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-__device__ __forceinline__ Best best_of(uint64_t w) {
+__device__ __forceinline__ bool better(Key a, Key b) { return a.k > b.k || (a.k == b.k && a.i < b.i); }
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// The best candidate of each row of 16 lanes, in all 16: the largest k (a DPP max over quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the smallest i among the lanes holding it.
+__device__ __forceinline__ Key fold16(Key x) {
+    uint32_t m = x.k;
+    m = max(m, dpp_u32<0xB1>(m));
+    m = max(m, dpp_u32<0x4E>(m));
+    m = max(m, dpp_u32<0x141>(m));
+    m = max(m, dpp_u32<0x140>(m));
+    uint32_t i = x.k == m ? x.i : 0xffffffffu;
+    i = min(i, dpp_u32<0xB1>(i));
+    i = min(i, dpp_u32<0x4E>(i));
+    i = min(i, dpp_u32<0x141>(i));
+    i = min(i, dpp_u32<0x140>(i));
+    return Key{m, i};
+}
+__device__ __forceinline__ uint64_t tagged_key(Key x, uint32_t step) {
+    return ((uint64_t)(step & 0xffffu) << 48) | ((uint64_t)(x.i & 0xffffu) << 32) | x.k;
+}
+__device__ __forceinline__ Key key_of(uint64_t w) {
     const uint32_t i = (uint32_t)(w >> 32) & 0xffffu;
-    return Best{word_value(w), i == 0xffffu ? INT32_MAX : (int)i};
+    return Key{(uint32_t)w, i == 0xffffu ? 0xffffffffu : i};
 }
 
-// One step of the best-entry fold across lanes (DPP control CTRL, within rows of 16 lanes).
-template <int CTRL>
-__device__ __forceinline__ void best_step(float &v, int &i) {
-    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
-    if (before(ov, oi, v, i)) {
-        v = ov;
-        i = oi;
-    }
-}
-// The best entry of each row of 16 lanes, left in all 16: quad_perm [1,0,3,2], [2,3,0,1], then
-// row_half_mirror and row_mirror pair every lane with one of each other group in turn (the order
-// is a total one, so any pairing that reaches every lane gives the same entry).
-__device__ __forceinline__ void best16(float &v, int &i) {
-    best_step<0xB1>(v, i);
-    best_step<0x4E>(v, i);
-    best_step<0x141>(v, i);
-    best_step<0x140>(v, i);
-}
 // v summed over lanes l, l ^ 16, l ^ 32, l ^ 48: v_permlane16_swap / v_permlane32_swap exchange
 // rows 1 and 3 of one operand with rows 0 and 2 (halves 1 and 0) of the other; with both operands
 // v, the two results of each lane are its own value and its partner's.
@@ -678,8 +688,8 @@ struct ResShared {
     float ls[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL], lbias[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL];
     float hst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4], cst[TDT_MAX_LAYERS][RES_MAX_PANELS * 4];
     __attribute__((aligned(16))) float pin[TDT_MAX_H];  // the prediction the joint adds
-    Best red[RES_WAVES][TDT_ROWS], dred[RES_WAVES][TDT_ROWS];
-    Best cand[RES_THREADS / 16], dcand[RES_THREADS / 16];  // the decider's 16-lane group bests
+    Key red[RES_WAVES][TDT_ROWS], dred[RES_WAVES][TDT_ROWS];
+    Key cand[RES_THREADS / 16], dcand[RES_THREADS / 16];  // the decider's 16-lane group bests
     int32_t kpart[RES_WAVES][2][PANEL];
     int32_t erow[TDT_ROWS];
     uint32_t slot[RES_WAVES];
@@ -897,9 +907,9 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             // duration entry (index d for column vocab + d). A NaN first logit (column 0) is never
             // beaten in the reference's argmax: it enters as (+inf, 0), which nothing comes before;
             // a NaN first duration logit likewise.
-            Best mine[4], dmine[4];
+            Key mine[4], dmine[4];
 #pragma unroll
-            for (int v = 0; v < 4; v++) mine[v] = dmine[v] = Best{__builtin_nanf(""), INT32_MAX};
+            for (int v = 0; v < 4; v++) mine[v] = dmine[v] = Key{0u, 0xffffffffu};
             const int orow = (lane >> 4) * 4, j16 = lane & 15;
             for (int pi = wave; pi < npj; pi += RES_WAVES) {
                 gemv::v4i hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
@@ -933,16 +943,18 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                         const bool voc = col < a.vocab;
                         const int idx = voc ? col : col - a.vocab;
                         if (idx == 0 && __builtin_isnan(val)) val = __builtin_inff();
-                        Best &m = voc ? mine[v] : dmine[v];
-                        if (before(val, idx, m.v, m.i)) m = Best{val, idx};
+                        // A lane meets its columns in increasing order: the strictly larger wins.
+                        const uint32_t key = order_key(val);
+                        Key &m = voc ? mine[v] : dmine[v];
+                        if (key > m.k) m = Key{key, (uint32_t)idx};
                     }
                 }
             }
             const bool has_dur = bq >= jd0 && bq < jd0 + nd;  // uniform: only these hold duration columns
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                best16(mine[v].v, mine[v].i);
-                if (has_dur) best16(dmine[v].v, dmine[v].i);
+                mine[v] = fold16(mine[v]);
+                if (has_dur) dmine[v] = fold16(dmine[v]);
                 if (j16 == 0) {
                     sh.red[wave][orow + v] = mine[v];
                     sh.dred[wave][orow + v] = dmine[v];
@@ -953,17 +965,17 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
         // Every workgroup's word for every row of the step (none from those without joint panels);
         // the joint workgroups holding duration columns also write their best duration entries.
         if (tid < TDT_ROWS) {
-            Best x{__builtin_nanf(""), INT32_MAX}, xd{__builtin_nanf(""), INT32_MAX};
+            Key x{0u, 0xffffffffu}, xd{0u, 0xffffffffu};
             if (npj > 0) {
 #pragma unroll
                 for (int q = 0; q < RES_WAVES; q++) {
-                    if (before(sh.red[q][tid].v, sh.red[q][tid].i, x.v, x.i)) x = sh.red[q][tid];
-                    if (before(sh.dred[q][tid].v, sh.dred[q][tid].i, xd.v, xd.i)) xd = sh.dred[q][tid];
+                    if (better(sh.red[q][tid], x)) x = sh.red[q][tid];
+                    if (better(sh.dred[q][tid], xd)) xd = sh.dred[q][tid];
                 }
             }
-            word_store(a.w_part + ((size_t)par * TDT_ROWS + tid) * RES_MAX_GRID + b, tagged_best(x, s));
+            word_store(a.w_part + ((size_t)par * TDT_ROWS + tid) * RES_MAX_GRID + b, tagged_key(x, s));
             if (bq >= jd0 && bq < jd0 + nd)
-                word_store(a.w_dur + ((size_t)par * TDT_ROWS + tid) * TDT_ROWS + (bq - jd0), tagged_best(xd, s));
+                word_store(a.w_dur + ((size_t)par * TDT_ROWS + tid) * TDT_ROWS + (bq - jd0), tagged_key(xd, s));
         }
         // ---- The decision. Workgroup 0 (a projection workgroup, idle during the joint when the grid
         // has room for both) gathers the words, walks the window, records the token and publishes the
@@ -1004,17 +1016,17 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             }
             // Each group of 16 lanes (inside one row's threads, g >= 16) folds its entries; thread r
             // then takes the best of its row's g / 16 groups, and the duration entry of its first.
-            Best x{__builtin_nanf(""), INT32_MAX}, xd{__builtin_nanf(""), INT32_MAX};
+            Key x{0u, 0xffffffffu}, xd{0u, 0xffffffffu};
 #pragma unroll
             for (int u = 0; u < 16; u++) {
                 if (live && j + g * u < a.grid) {
-                    const Best y = best_of(pw[u]);
-                    if (before(y.v, y.i, x.v, x.i)) x = y;
+                    const Key y = key_of(pw[u]);
+                    if (better(y, x)) x = y;
                 }
             }
-            if (live && j < nd) xd = best_of(dw);
-            best16(x.v, x.i);
-            best16(xd.v, xd.i);
+            if (live && j < nd) xd = key_of(dw);
+            x = fold16(x);
+            xd = fold16(xd);
             if ((lane & 15) == 0) {
                 sh.cand[tid >> 4] = x;
                 sh.dcand[tid >> 4] = xd;
@@ -1022,12 +1034,12 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             __syncthreads();
             if (tid < rows) {
                 const int k0 = tid * (g / 16);
-                Best bx = sh.cand[k0];
+                Key bx = sh.cand[k0];
                 for (int k = 1; k < g / 16; k++)
-                    if (before(sh.cand[k0 + k].v, sh.cand[k0 + k].i, bx.v, bx.i)) bx = sh.cand[k0 + k];
-                const Best bd = sh.dcand[k0];
-                sh.tok_s[tid] = bx.i == INT32_MAX ? 0 : bx.i;
-                sh.dur_s[tid] = sh.durs[bd.i == INT32_MAX ? 0 : bd.i];
+                    if (better(sh.cand[k0 + k], bx)) bx = sh.cand[k0 + k];
+                const Key bd = sh.dcand[k0];
+                sh.tok_s[tid] = bx.i == 0xffffffffu ? 0 : (int)bx.i;
+                sh.dur_s[tid] = sh.durs[bd.i == 0xffffffffu ? 0 : bd.i];
             }
             __syncthreads();
             if (sh.abort) break;
