@@ -631,6 +631,11 @@ __device__ __forceinline__ Key key_of(uint64_t w) {
     return Key{(uint32_t)w, i == 0xffffu ? 0xffffffffu : i};
 }
 
+// dequant, through its int32 form when the wavefront voted that every hi sum fits (the same value).
+__device__ __forceinline__ float dequant_w(int32_t hi, int32_t lo, int32_t e, float sc, bool fits) {
+    return fits ? dequant_i32(hi, lo, e, sc) : dequant(hi, lo, e, sc);
+}
+
 // v summed over lanes l, l ^ 16, l ^ 32, l ^ 48: v_permlane16_swap / v_permlane32_swap exchange
 // rows 1 and 3 of one operand with rows 0 and 2 (halves 1 and 0) of the other; with both operands
 // v, the two results of each lane are its own value and its partner's.
@@ -934,12 +939,14 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                 }
                 const int col = (pj0 + pi) * PANEL + j16;
                 const float sc = sh.js[pi * PANEL + j16], bs = sh.jbias[pi * PANEL + j16];
+                const bool fits = __all(dequant_fits(hi[0]) & dequant_fits(hi[1]) & dequant_fits(hi[2]) &
+                                        dequant_fits(hi[3]));
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int r = orow + v;
                     if (r < rows && col < NJ) {
-                        float val =
-                            epilogue_vals(dequant(hi[v], lo[v], sh.erow[r], sc), true, bs, ACT_NONE, 1.0f, false, 0.0f);
+                        float val = epilogue_vals(dequant_w(hi[v], lo[v], sh.erow[r], sc, fits), true, bs, ACT_NONE,
+                                                  1.0f, false, 0.0f);
                         const bool voc = col < a.vocab;
                         const int idx = voc ? col : col - a.vocab;
                         if (idx == 0 && __builtin_isnan(val)) val = __builtin_inff();
@@ -1121,7 +1128,8 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                     const int j = lane & 15;
                     const int32_t shi = sh.kpart[0][0][j] + sh.kpart[1][0][j] + sh.kpart[2][0][j] + sh.kpart[3][0][j];
                     const int32_t slo = sh.kpart[0][1][j] + sh.kpart[1][1][j] + sh.kpart[2][1][j] + sh.kpart[3][1][j];
-                    const float v = epilogue_vals(dequant(shi, slo, e, sh.ls[l][pi * PANEL + j]), true,
+                    const bool fits = __all(dequant_fits(shi));
+                    const float v = epilogue_vals(dequant_w(shi, slo, e, sh.ls[l][pi * PANEL + j], fits), true,
                                                   sh.lbias[l][pi * PANEL + j], ACT_NONE, 1.0f, false, 0.0f);
                     // Output 4 u + q is gate q (i, f, g, o) of unit u: the quad's lane 0 updates the
                     // cell (src/parakeet.rs:1549-1562): c = f c + i g, h = o tanh(c).
@@ -1164,7 +1172,8 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                     const int col = (pp0 + pi) * PANEL + lane;
                     const int32_t shi = sh.kpart[0][0][lane] + sh.kpart[1][0][lane] + sh.kpart[2][0][lane] + sh.kpart[3][0][lane];
                     const int32_t slo = sh.kpart[0][1][lane] + sh.kpart[1][1][lane] + sh.kpart[2][1][lane] + sh.kpart[3][1][lane];
-                    const float v = epilogue_vals(dequant(shi, slo, e, sh.ps[pi * PANEL + lane]), true,
+                    const bool fits = __all(dequant_fits(shi));  // over the 16 active lanes
+                    const float v = epilogue_vals(dequant_w(shi, slo, e, sh.ps[pi * PANEL + lane], fits), true,
                                                   sh.pbias[pi * PANEL + lane], ACT_NONE, 1.0f, false, 0.0f);
                     if (col < h) {
                         sh.pst[pi * PANEL + lane] = v;
