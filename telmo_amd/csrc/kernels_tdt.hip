@@ -986,14 +986,12 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
         }
         // ---- The decision. Workgroup 0 (a projection workgroup, idle during the joint when the grid
         // has room for both) gathers the words, walks the window, records the token and publishes the
-        // outcome in RES_COPIES copies; the others wait for their copy (a few words on one line,
-        // where every workgroup reading every joint word would queue thousands of line requests). Thread (r, q) of workgroup 0 waits for row r's words of workgroups q,
-        // q + 16, ... and for duration word q.
+        // outcome in RES_COPIES copies; the others wait for their copy (six words on one line, where
+        // every workgroup reading every joint word would queue thousands of line requests).
         if (b == 0) {
             // The window's rows rounded up to a power of two, R, share the threads: g = 256 / R per
             // row, thread j of row r reading the words of workgroups j, j + g, ... and, for j < nd,
-            // duration word j. Coherent loads of one wavefront are served about one after another,
-            // so the words are spread over all four wavefronts rather than stacked in one.
+            // duration word j; the loads are spread over all four wavefronts.
             const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 8 ? 8 : TDT_ROWS;
             const int g = RES_THREADS / R, r = tid / g, j = tid - r * g;
             const bool live = r < rows;
