@@ -787,6 +787,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x;
     const size_t rc = (size_t)(b % RES_COPIES) * a.cs;  // the copy this workgroup reads
     const int h = a.h, NJ = a.joint.n, KBJ = a.joint.KB, KBL = a.lstm[0].KB, KBP = a.proj.KB;
+    const int KBJ4 = (KBJ + 3) & ~3;  // the joint's k-blocks padded with zero digits to whole groups of four
     const int bq = b - a.qoff;  // among the joint and LSTM workgroups
     const int pj0 = bq * a.JP, npj = bq >= 0 && bq < a.GJ ? min(a.JP, a.joint.P - pj0) : 0;
     const int pl0 = bq * a.LP, npl = bq >= 0 && bq < a.GL ? min(a.LP, a.lstm[0].P - pl0) : 0;
@@ -895,7 +896,7 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int c = lane + 64 * i;
-                        if (c < KBJ * 16) {
+                        if (c < KBJ4 * 16) {  // zero digits past the row (z is 0 there)
                             uint32_t hi, lo;
                             digits4(z[i].x, z[i].y, z[i].z, z[i].w, ex, hi, lo);
                             uint8_t *d = sq + (c >> 4) * 2048 + ((c & 15) >> 2) * 256 + r * 16 + (c & 3) * 4;
@@ -919,22 +920,20 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             for (int pi = wave; pi < npj; pi += RES_WAVES) {
                 gemv::v4i hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
                 const uint8_t *wb = wj + (size_t)pi * KBJ * 1024 + lane * 16;
-                // Four k-blocks' operands are read before their MFMAs.
-                for (int t0 = 0; t0 < KBJ; t0 += 4) {
+                // Four k-blocks' operands are read before their MFMAs, with no branch between: past
+                // KBJ the digits are zero (the weights read are the last block's, adding nothing).
+                for (int t0 = 0; t0 < KBJ4; t0 += 4) {
                     gemv::v4i ah[4], al[4], wv[4];
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
-                        const int tk = min(t0 + u, KBJ - 1);
-                        ah[u] = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + lane * 16);
-                        al[u] = *reinterpret_cast<const gemv::v4i *>(sq + tk * 2048 + 1024 + lane * 16);
-                        wv[u] = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)tk * 1024);
+                        ah[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + lane * 16);
+                        al[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + 1024 + lane * 16);
+                        wv[u] = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)min(t0 + u, KBJ - 1) * 1024);
                     }
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
-                        if (t0 + u < KBJ) {
-                            hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[u], wv[u], hi, 0, 0, 0);
-                            lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[u], wv[u], lo, 0, 0, 0);
-                        }
+                        hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[u], wv[u], hi, 0, 0, 0);
+                        lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[u], wv[u], lo, 0, 0, 0);
                     }
                 }
                 const int col = (pj0 + pi) * PANEL + j16;
@@ -1345,7 +1344,7 @@ bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
     if (nd > (size_t)TDT_ROWS) return false;
     const size_t KBJ = net.joint->kb, KBL = net.lstm[0]->kb, KBP = net.proj->kb;
     p.lds = ((size_t)p.JP * KBJ + net.layers * p.LP * KBL + (size_t)p.PP * KBP) * 1024 +
-            std::max(KBJ * 2048, std::max(KBL, KBP) * 128);
+            std::max(((KBJ + 3) & ~(size_t)3) * 2048, std::max(KBL, KBP) * 128);
     const void *f = reinterpret_cast<const void *>(&tdt_resident_kernel);
     hipFuncAttributes fa;
     if (hipFuncGetAttributes(&fa, f) != hipSuccess || p.lds + fa.sharedSizeBytes > (size_t)max_lds) return false;
