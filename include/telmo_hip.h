@@ -130,7 +130,12 @@ int tg_linear(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weig
               const tg_epilogue *epi);
 
 /* The same on device pointers, queued on the context's stream and returning at once. Buffers
- * must stay valid until the stream reaches the work (tg_synchronize). a and c must not overlap. */
+ * must stay valid until the stream reaches the work (tg_synchronize). a and c must not overlap.
+ * Captured graphs: a call that takes the GEMM quantises a into the context's workspace, which a
+ * later call needing more of it frees and reallocates. A HIP graph captured around a call keeps the
+ * workspace's address, so once any call on that context has grown the workspace the graph must not
+ * be replayed (it would write freed memory): capture after the largest call, or capture
+ * tg_matmul_device_noalloc or the staged calls below on buffers of the caller's. */
 int tg_matmul_device(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w,
                      float *c, size_t c_len, size_t ldc, const tg_epilogue *epi);
 int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *c,
@@ -329,6 +334,21 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
  * on = 0 selects the step kernels. tg_tdt_is_resident returns 1 when decodes run resident. */
 int tg_tdt_set_resident(tg_ctx *ctx, tg_tdt *tdt, int on);
 int tg_tdt_is_resident(const tg_tdt *tdt);
+/* A resident launch holds most of the GPU's CUs until the decode ends, and two of them cannot be
+ * resident on one GPU at once: within a process, one resident decode runs per device at a time,
+ * and a decode that starts while another holds the device runs on the step kernels instead (same
+ * results). Separate processes must not run resident decodes on the same GPU; give each process
+ * its own GPU or call tg_tdt_set_resident(ctx, tdt, 0) in all but one.
+ * tg_tdt_last_resident: 1 when the last tg_tdt_decode_device on this network ran resident, 0 when
+ * it ran on the step kernels, -1 before the first. */
+int tg_tdt_last_resident(const tg_tdt *tdt);
+/* Limits of the resident decode (no counterpart in the reference; for tests and tuning): the most
+ * steps one launch makes before the host looks at the control block and relaunches (1 to 16384; 0
+ * restores 16384), and the longest one workgroup waits for another, in microseconds (0 restores
+ * one second). A wait that passes its limit ends the launch in every workgroup; the decode then
+ * fails with TG_ERR_HIP and leaves state and pred as they were passed (*frame, *on_frame and the
+ * tokens untouched), so the call can be repeated, resident or on the step kernels. */
+int tg_tdt_set_resident_limits(tg_ctx *ctx, tg_tdt *tdt, uint32_t steps_per_launch, uint64_t wait_us);
 
 /* ---- packs: the reference's weight files (src/pack.rs) -------------------------------------
  * A pack is "TELMOPAK", a u32 version (1) and 4 zero bytes; entries' data at multiples of 64

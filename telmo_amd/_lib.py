@@ -70,6 +70,8 @@ SIGNATURES = {
                                              _szp]),
     "tg_tdt_set_resident": (ctypes.c_int, [_p, _p, ctypes.c_int]),
     "tg_tdt_is_resident": (ctypes.c_int, [_p]),
+    "tg_tdt_last_resident": (ctypes.c_int, [_p]),
+    "tg_tdt_set_resident_limits": (ctypes.c_int, [_p, _p, _u32, ctypes.c_uint64]),
     "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),
     "tg_pack_close": (None, [_p]),

@@ -54,6 +54,10 @@ struct tg_weights {
     int device;
 };
 
+constexpr int TDT_GRAPH_STEPS = 16;
+// Steps per resident launch: the host looks at the control block between launches.
+constexpr int TDT_RESIDENT_STEPS = 16384;
+
 // A TDT prediction network and joint on the device (the joint, projection, biases and embedding
 // stay the caller's), with the interleaved LSTM copies and the buffers of its decode steps.
 struct tg_tdt {
@@ -80,11 +84,12 @@ struct tg_tdt {
     bool can_resident = false, use_resident = false;
     uint64_t *words = nullptr;
     uint64_t wait_ticks = 0;
+    uint64_t clock_khz = 100000;  // the device's wall clock, for tg_tdt_set_resident_limits
+    int launch_steps = TDT_RESIDENT_STEPS;  // steps per resident launch
+    // Whether the last tg_tdt_decode_device ran resident (1), by the step kernels (0), or none yet (-1).
+    int last_resident = -1;
 };
 
-constexpr int TDT_GRAPH_STEPS = 16;
-// Steps per resident launch: the host looks at the control block between launches.
-constexpr int TDT_RESIDENT_STEPS = 16384;
 
 // The scratch of tg_matmul_device_noalloc, for callers that cannot allocate: the quantised rows of
 // one product (the first NOALLOC_QA_BYTES) and their row exponents (NOALLOC_ROWS int32 after them).
@@ -99,6 +104,10 @@ static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 namespace {
 
 constexpr int MAX_DEVICES = 64;
+// A resident decode holds most of a GPU's CUs for its whole launch, and two resident launches on one
+// GPU cannot both be resident: one decode per device at a time holds this lock (try_lock); a decode
+// that finds it taken runs on the step kernels, which share the GPU with it.
+std::mutex resident_mu[MAX_DEVICES];
 std::mutex scratch_mu;
 void *scratch_ptr[MAX_DEVICES] = {};  // device address of `scratch` per device, once taken
 hipError_t scratch_err[MAX_DEVICES] = {};
@@ -998,7 +1007,9 @@ int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out) {
         int khz = 0;
         if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device) != hipSuccess || khz <= 0)
             khz = 100000;
+        t->clock_khz = (uint64_t)khz;
         t->wait_ticks = (uint64_t)khz * 1000;  // one second
+        t->launch_steps = TDT_RESIDENT_STEPS;
         t->can_resident = t->use_resident = true;
     }
     (void)hipGetLastError();  // a refused LDS attribute or occupancy query leaves the step kernels
@@ -1094,19 +1105,47 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
     hc->rows = tg::TDT_ROWS;
     TG_HIP(ctx, hipMemcpyAsync(tdt->ctl, hc, sizeof(*hc), hipMemcpyHostToDevice, ctx->stream));
     const size_t limit = (frames - *frame) * (per_frame + 1) + 1;
-    if (tdt->use_resident) {
+    // The resident decode when the network takes it and no other resident decode holds this device;
+    // the lock is held until its last launch has ended (each launch is followed by a synchronize).
+    std::unique_lock<std::mutex> rlock;
+    if (tdt->use_resident && ctx->device >= 0 && ctx->device < MAX_DEVICES)
+        rlock = std::unique_lock<std::mutex>(resident_mu[ctx->device], std::try_to_lock);
+    tdt->last_resident = rlock.owns_lock() ? 1 : 0;
+    if (rlock.owns_lock()) {
+        // state and pred as the caller passed them, in the scratch rows (layers x 2h, then h), put
+        // back if a launch fails: the launches write their state back even when a wait gave up.
+        const size_t sw = net.layers * 2 * net.h;
+        TG_HIP(ctx, hipMemcpyAsync(tdt->scratch, state, sw * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+        TG_HIP(ctx, hipMemcpyAsync(tdt->scratch + sw, pred, net.h * sizeof(float), hipMemcpyDeviceToDevice,
+                                   ctx->stream));
+        auto restore = [&]() {
+            (void)hipMemcpyAsync(state, tdt->scratch, sw * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+            (void)hipMemcpyAsync(pred, tdt->scratch + sw, net.h * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+            (void)hipStreamSynchronize(ctx->stream);
+        };
         TG_HIP(ctx, tg::launch_tdt_resident_init(net, tdt->words, state, pred, ctx->stream));
         size_t steps = 0;
         while (true) {
-            TG_HIP(ctx, tg::launch_tdt_resident(tdt->ctl, net, tdt->plan, tdt->words, enc_proj, lde, (int)frames, state,
-                                                pred, tdt->tokens, (int)most, TDT_RESIDENT_STEPS, tdt->wait_ticks,
-                                                ctx->stream));
+            const hipError_t e = tg::launch_tdt_resident(tdt->ctl, net, tdt->plan, tdt->words, enc_proj, lde,
+                                                         (int)frames, state, pred, tdt->tokens, (int)most,
+                                                         tdt->launch_steps, tdt->wait_ticks, ctx->stream);
+            if (e != hipSuccess) {
+                restore();
+                return hip_fail(ctx, e, "the resident decode's launch");
+            }
             TG_HIP(ctx, hipMemcpyAsync(hc, tdt->ctl, sizeof(*hc), hipMemcpyDeviceToHost, ctx->stream));
             TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
-            if (hc->err) return fail(ctx, TG_ERR_HIP, "the resident decode: a workgroup's wait passed its deadline");
+            if (hc->err) {
+                restore();
+                return fail(ctx, TG_ERR_HIP,
+                            "the resident decode: a workgroup's wait passed its deadline (state and pred restored)");
+            }
             if (hc->done) break;
-            steps += TDT_RESIDENT_STEPS;
-            if (steps > limit) return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
+            steps += (size_t)tdt->launch_steps;
+            if (steps > limit) {
+                restore();
+                return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
+            }
         }
         return tdt_results(ctx, tdt, hc, frame, on_frame, tokens, cap, count);
     }
@@ -1159,5 +1198,19 @@ int tg_tdt_set_resident(tg_ctx *ctx, tg_tdt *tdt, int on) {
 }
 
 int tg_tdt_is_resident(const tg_tdt *tdt) { return tdt && tdt->use_resident ? 1 : 0; }
+
+int tg_tdt_last_resident(const tg_tdt *tdt) { return tdt ? tdt->last_resident : -1; }
+
+int tg_tdt_set_resident_limits(tg_ctx *ctx, tg_tdt *tdt, uint32_t steps_per_launch, uint64_t wait_us) {
+    if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
+    if (steps_per_launch > (uint32_t)TDT_RESIDENT_STEPS)
+        return fail(ctx, TG_ERR_ARG, "at most 16384 steps per resident launch");
+    if (wait_us > (uint64_t)60 * 1000 * 1000) return fail(ctx, TG_ERR_ARG, "a wait of at most 60 s");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    tdt->launch_steps = steps_per_launch ? (int)steps_per_launch : TDT_RESIDENT_STEPS;
+    const uint64_t ticks = wait_us ? wait_us * tdt->clock_khz / 1000 : tdt->clock_khz * 1000;
+    tdt->wait_ticks = ticks ? ticks : 1;
+    return TG_OK;
+}
 
 }  // extern "C"

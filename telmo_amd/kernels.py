@@ -525,6 +525,20 @@ class TdtDecoder:
         """Resident decode (raises where the network cannot run it) or one graph of step kernels."""
         _check(_lib.lib().tg_tdt_set_resident(self._kernels._ctx, self._handle, 1 if on else 0), self._kernels._ctx)
 
+    @property
+    def last_resident(self) -> Optional[bool]:
+        """Whether the last decode ran resident (False: on the step kernels; None before the first).
+        A decode falls back to the step kernels while another one holds the device resident."""
+        v = int(_lib.lib().tg_tdt_last_resident(self._handle))
+        return None if v < 0 else bool(v)
+
+    def set_resident_limits(self, steps_per_launch: int = 0, wait_us: int = 0) -> None:
+        """The resident decode's steps per launch (0: 16384) and longest wait between workgroups in
+        microseconds (0: one second); a wait past it fails the decode and leaves state and pred as
+        they were passed."""
+        _check(_lib.lib().tg_tdt_set_resident_limits(self._kernels._ctx, self._handle, steps_per_launch, wait_us),
+               self._kernels._ctx)
+
     def decode(self, enc_proj, state, pred, frame: int = 0, on_frame: int = 0, cap: Optional[int] = None):
         """The greedy decode over the rows of enc_proj (GPU tensor, frames x >= h) from frame with
         on_frame tokens on it; state (layers x [h, c]) and pred (h) are updated in place. Returns

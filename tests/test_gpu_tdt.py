@@ -197,3 +197,171 @@ def test_decode_fixture(tk):
     assert [frame, on] == list(g["end"])
     assert np.max(np.abs(state.cpu().numpy() - g["state"])) <= TOL
     dec.close()
+
+
+def zero_joint_network(rng, token, duration, h=32, vocab=20, durs=(0, 1, 2, 3, 4), max_symbols=3):
+    """A network whose joint weights are zero, so every logit is its bias: the decode emits `token`
+    with `duration` at every step (the closed form of decode_inner's loop)."""
+    net = tdt_network(rng, h, vocab, list(durs), layers=2, max_symbols=max_symbols)
+    net["joint"] = (np.zeros_like(net["joint"][0]), net["joint"][1])
+    b = np.zeros(vocab + len(durs), np.float32)
+    b[token] = 5.0
+    b[vocab + list(durs).index(duration)] = 5.0
+    net["joint_b"] = b
+    return net
+
+
+def test_resident_decode_crosses_the_relaunch_boundary(tk):
+    """More steps than one resident launch makes (16384): 6000 frames of three duration-0 tokens each
+    are 18000 steps, so the host relaunches from the control block once; tokens are the closed form,
+    and state and prediction equal the step kernels' run of the same decode."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    net = zero_joint_network(rng, 7, 0)
+    frames = 6000
+    enc = torch.from_numpy(rng.standard_normal((frames, 32)).astype(np.float32)).cuda()
+    dec = upload(tk, net)
+    results = []
+    for resident in (True, False):
+        dec.set_resident(resident)
+        state, pred = torch.zeros(2 * 2 * 32, device="cuda"), torch.zeros(32, device="cuda")
+        say("decode across the relaunch boundary", "resident" if resident else "steps")
+        toks, frame, on = dec.decode(enc, state, pred)
+        assert dec.last_resident == resident
+        assert [tuple(t) for t in toks] == [(7, t, 0) for t in range(frames) for _ in range(3)]
+        assert (frame, on) == (frames, 0)
+        results.append((state.cpu().numpy(), pred.cpu().numpy()))
+    assert np.max(np.abs(results[0][0] - results[1][0])) <= TOL
+    assert np.max(np.abs(results[0][1] - results[1][1])) <= TOL
+    dec.close()
+
+
+@pytest.mark.parametrize("steps", [1, 3, 16])
+def test_resident_decode_relaunches_every_few_steps(tk, orc, steps):
+    """The same decodes with a relaunch every `steps` steps: every launch resumes from the control
+    block, the hand-over words and the state the previous one wrote back; the oracle's tokens."""
+    import torch
+
+    for case in (DECODE_CASES[0], DECODE_CASES[2]):
+        h, vocab, durs, layers, p, frames, blank_bias, ms = case
+        rng = np.random.default_rng(frames + h + layers)
+        net = tdt_network(rng, h, vocab, durs, layers=layers, precision=p, max_symbols=ms, blank_bias=blank_bias)
+        dec = upload(tk, net)
+        dec.set_resident_limits(steps_per_launch=steps)
+        enc = rng.standard_normal((frames, h)).astype(np.float32)
+        state = (0.3 * rng.standard_normal(layers * 2 * h)).astype(np.float32)
+        pred = (0.3 * rng.standard_normal(h)).astype(np.float32)
+        sd, pdv = torch.from_numpy(state.copy()).cuda(), torch.from_numpy(pred.copy()).cuda()
+        say("decode relaunching every", steps, "steps", case)
+        toks, frame, on = dec.decode(torch.from_numpy(enc).cuda(), sd, pdv)
+        assert dec.last_resident
+        want, wframe, won = orc.tdt_decode(net, enc, state, pred)
+        assert [tuple(t) for t in toks] == want
+        assert (frame, on) == (wframe, won)
+        assert np.max(np.abs(sd.cpu().numpy() - state)) <= TOL
+        assert rel_norm_err(pdv.cpu().numpy()[None], pred[None]) <= TOL
+        dec.close()
+
+
+def test_resident_decode_past_its_deadline_leaves_the_state_as_passed(tk, orc):
+    """A one-microsecond limit on every wait between workgroups (forced from the host; every wait
+    still ends, at its deadline): the decode fails with an error, and state and prediction are the
+    caller's values, not a mix of the steps the workgroups had reached. With the default limit the
+    same call then gives the oracle's decode."""
+    import torch
+
+    import telmo_amd
+
+    h, vocab, durs, layers, p, frames, blank_bias, ms = DECODE_CASES[0]
+    rng = np.random.default_rng(frames + h + layers)
+    net = tdt_network(rng, h, vocab, durs, layers=layers, precision=p, max_symbols=ms, blank_bias=blank_bias)
+    dec = upload(tk, net)
+    enc = rng.standard_normal((frames, h)).astype(np.float32)
+    state = (0.3 * rng.standard_normal(layers * 2 * h)).astype(np.float32)
+    pred = (0.3 * rng.standard_normal(h)).astype(np.float32)
+    encd = torch.from_numpy(enc).cuda()
+    sd, pdv = torch.from_numpy(state.copy()).cuda(), torch.from_numpy(pred.copy()).cuda()
+    dec.set_resident_limits(wait_us=1)
+    say("resident decode with a 1 us wait limit")
+    with pytest.raises(telmo_amd.TelmoError):
+        dec.decode(encd, sd, pdv)
+    tk.synchronize()
+    assert np.array_equal(sd.cpu().numpy(), state)
+    assert np.array_equal(pdv.cpu().numpy(), pred)
+    dec.set_resident_limits()
+    say("the same decode with the default limits")
+    toks, frame, on = dec.decode(encd, sd, pdv)
+    assert dec.last_resident
+    want, wframe, won = orc.tdt_decode(net, enc, state, pred)
+    assert [tuple(t) for t in toks] == want
+    assert (frame, on) == (wframe, won)
+    assert np.max(np.abs(sd.cpu().numpy() - state)) <= TOL
+    dec.close()
+
+
+def test_concurrent_decodes_on_two_contexts_share_the_device(orc, gpu_stream):
+    """Two threads, each with its own context, stream and network, decode at the same time, five
+    times each: one resident decode holds the device at a time, the other runs on the step kernels,
+    and every decode equals the oracle's. The threads touch only their own streams (no device-wide
+    synchronisation), so their decodes overlap."""
+    import threading
+
+    import torch
+
+    import telmo_amd
+
+    h, vocab, durs, layers, p, frames, blank_bias, ms = DECODE_CASES[4]
+    reps = 5
+    cases = []
+    for i in range(2):
+        rng = np.random.default_rng(300 + i)
+        net = tdt_network(rng, h, vocab, durs, layers=layers, precision=p, max_symbols=ms, blank_bias=blank_bias)
+        enc = rng.standard_normal((frames, h)).astype(np.float32)
+        state = (0.3 * rng.standard_normal(layers * 2 * h)).astype(np.float32)
+        pred = (0.3 * rng.standard_normal(h)).astype(np.float32)
+        ws, wp = state.copy(), pred.copy()
+        want = orc.tdt_decode(net, enc, ws, wp)
+        cases.append((net, enc, state, pred, want, ws))
+    kerns = [telmo_amd.Kernels(0) for _ in range(2)]
+    decs = [upload(k, c[0]) for k, c in zip(kerns, cases)]
+    encs = [torch.from_numpy(c[1]).cuda() for c in cases]
+    ins = [[(torch.from_numpy(c[2].copy()).cuda(), torch.from_numpy(c[3].copy()).cuda()) for _ in range(reps)]
+           for c in cases]
+    torch.cuda.synchronize()
+    start = threading.Barrier(2)
+    results = [[], []]
+    errors = []
+
+    def run(i):
+        try:
+            start.wait()
+            for r in range(reps):
+                sd, pdv = ins[i][r]
+                toks, frame, on = decs[i].decode(encs[i], sd, pdv)
+                results[i].append(([tuple(t) for t in toks], frame, on, decs[i].last_resident))
+            kerns[i].synchronize()
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    say("two concurrent decodes")
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for i in range(2):
+        want, wframe, won = cases[i][4]
+        assert len(results[i]) == reps
+        for r, (toks, frame, on, _) in enumerate(results[i]):
+            assert toks == want and (frame, on) == (wframe, won)
+            assert np.max(np.abs(ins[i][r][0].cpu().numpy() - cases[i][5])) <= TOL
+    ran = [r[3] for i in range(2) for r in results[i]]
+    print("[case] resident decodes:", sum(ran), "of", len(ran), flush=True)
+    for d in decs:
+        d.close()
+    for k in kerns:
+        k.close()
