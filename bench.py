@@ -153,6 +153,54 @@ def layer_params(seed, precision=3):
     return mats, norms, dw_w, dw_b
 
 
+# Granite Speech 5's encoder shapes (src/granite.rs:1153-1170): d_model 1024, feed-forward 4096,
+# 2048 convolution channels (expansion 2), kernel 7, vocabulary 16384; blocks 0 and 1 are strided.
+G_D, G_FF, G_CC, G_KERNEL, G_VOCAB = 1024, 4096, 2048, 7, 16384
+G_PRODUCTS = [("ff1_up", G_D, G_FF), ("ff1_down", G_FF, G_D), ("qkv", G_D, 3 * G_D), ("out", G_D, G_D),
+              ("pw1", G_D, 2 * G_CC), ("pw2", G_CC, G_D), ("ff2_up", G_D, G_FF), ("ff2_down", G_FF, G_D)]
+G_NORMS = ("ff1_norm", "norm_att", "norm_conv", "ff2_norm", "norm_out")
+
+
+def granite_block_params(seed, strided):
+    """One Granite block's parameters from telmo's generator, on the host: int8 matrices {name:
+    (values, scales, n, k)} with scales U(0.001, 0.01), biases N(0, 0.1^2) (qkv has none), LayerNorms
+    near (1, 0), depthwise taps [7, 2048] and bias [2048], and the stride flag."""
+    mats, biases, norms = {}, {}, {}
+    for i, (name, k, n) in enumerate(G_PRODUCTS):
+        mats[name] = panel_layout(synth_int8(n, k, seed + 10 * i), synth_scales(n, seed + 10 * i + 1)) + (n, k)
+        if name != "qkv":
+            biases[name] = (0.1 * synth_normal((n,), seed + 10 * i + 2)).astype(np.float32)
+    for i, name in enumerate(G_NORMS):
+        norms[name] = ((1.0 + 0.1 * synth_normal((G_D,), seed + 200 + 2 * i)).astype(np.float32),
+                       (0.1 * synth_normal((G_D,), seed + 201 + 2 * i)).astype(np.float32))
+    dw_w = (0.3 * synth_normal((G_KERNEL, G_CC), seed + 300)).astype(np.float32)
+    dw_b = (0.1 * synth_normal((G_CC,), seed + 301)).astype(np.float32)
+    return mats, biases, norms, dw_w, dw_b, strided
+
+
+def granite_head_params(seed):
+    """The CTC head (vocab x d) and out_mid (d x vocab) with their biases, int8 as above."""
+    head = panel_layout(synth_int8(G_VOCAB, G_D, seed), synth_scales(G_VOCAB, seed + 1)) + (G_VOCAB, G_D)
+    mid = panel_layout(synth_int8(G_D, G_VOCAB, seed + 2), synth_scales(G_D, seed + 3)) + (G_D, G_VOCAB)
+    head_b = (0.1 * synth_normal((G_VOCAB,), seed + 4)).astype(np.float32)
+    mid_b = (0.1 * synth_normal((G_D,), seed + 5)).astype(np.float32)
+    return head, head_b, mid, mid_b
+
+
+def upload_granite_block(kern, params):
+    import torch
+
+    import telmo_amd
+    from telmo_amd.granite import BlockWeights
+
+    mats, biases, norms, dw_w, dw_b, strided = params
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    W = {name: telmo_amd.PackedWeights.from_parts(kern, n, k, telmo_amd.Precision.INT8, v, s)
+         for name, (v, s, n, k) in mats.items()}
+    return BlockWeights(W, {name: dev(b) for name, b in biases.items()},
+                        {name: (dev(g), dev(b)) for name, (g, b) in norms.items()}, dev(dw_w), dev(dw_b), strided)
+
+
 def upload_layer(kern, params, precision=3):
     import torch
 

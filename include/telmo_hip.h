@@ -222,6 +222,22 @@ int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, co
 int tg_glu_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t half, float *out,
                   size_t out_len, size_t ldo);
 
+/* softmax of each of m rows of n values, in place: Kernels::softmax as the reference's AVX-512
+ * kernel computes it (src/kernels/mod.rs:460, src/kernels/avx512.rs:382-407): the row maximum,
+ * e = exp(x - max) with the SIMD exp, sixteen partial sums of e (partial j over e[j], e[j + 16], ...
+ * in order) folded by halves, then e * (1 / sum). Granite's self-conditioning applies it to the CTC
+ * head's logits (src/granite.rs:1040-1069). x holds (m - 1) ldx + n floats (TG_ERR_SHAPE
+ * otherwise). Device pointer, queued on the stream. */
+int tg_softmax_device(tg_ctx *ctx, float *x, size_t x_len, size_t ldx, size_t m, size_t n);
+
+/* Granite's strided-block pooling (src/granite.rs:918-931, the "pool" step of block_span): for each
+ * of batch equal-length sequences of frames rows of x, output row r < frames / 2 of that sequence
+ * (row b (frames / 2) + r of out) is (x[b frames + 2 r] + x[b frames + 2 r + 1]) / 2 over n values,
+ * a last odd frame dropped. out must not overlap x (TG_ERR_ARG). Device pointers, queued on the
+ * stream. */
+int tg_average_pairs_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t frames, size_t batch,
+                            size_t n, float *out, size_t out_len, size_t ldo);
+
 /* out[r, :] = LayerNorm(x[r, :]) * gamma + beta over n values per row, with the summation order of
  * the reference's AVX-512 layer_norm (src/kernels/avx512.rs:346-380). gamma and beta hold at least
  * n floats and x and out (m - 1) ld + n, as the reference asserts (avx512.rs:348; TG_ERR_SHAPE

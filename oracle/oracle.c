@@ -20,6 +20,9 @@
  *   or_exp_simd           src/kernels/avx512.rs:279-304 == avx2.rs:305-331 (same steps)
  *   or_glu                src/kernels/avx512.rs:410-430
  *   or_layer_norm         src/kernels/avx512.rs:346-380 (AVX-512 summation order)
+ *   or_softmax            src/kernels/avx512.rs:382-407 (AVX-512 order; the bits of rows holding a
+ *                         NaN depend on the register maximum's fold, which the reference leaves to
+ *                         the compiler: those rows are parity unpinned)
  *   or_dwconv1d_frame     src/kernels/scalar.rs:164-187 (== avx512.rs:445-459, the same loop)
  *   or_dwconv1d           src/parakeet.rs:1107-1122, src/granite.rs:900-915 (one frame per
  *                         output row, then silu, avx512.rs:308-311 and 432-443)
@@ -343,6 +346,28 @@ void or_layer_norm(const float *x, size_t n, float *out, const float *gamma, con
         const float d = (x[i] - mean) * rstd;
         out[i] = fmaf(d, gamma[i], beta[i]);
     }
+}
+
+/* softmax of one row in place, AVX-512 (src/kernels/avx512.rs:382-407): sixteen lane maxima from
+ * -inf (x86 MAXPS, masked tail lanes loading -inf), folded by halves with the lower lane first;
+ * e = exp_simd(x - max) stored over x; sixteen partial sums of e from +0 in steps of 16 (masked
+ * tail lanes keep their partial), reduced as reduce16; inv = 1 / sum; x = e * inv. */
+void or_softmax(float *x, size_t n) {
+    float mx[16], s[16] = {0};
+    for (int j = 0; j < 16; j++) mx[j] = -INFINITY;
+    for (size_t i = 0; i < n; i += 16)
+        for (size_t j = 0; j < 16; j++) mx[j] = x86_max(mx[j], i + j < n ? x[i + j] : -INFINITY);
+    for (int h = 8; h >= 1; h >>= 1)
+        for (int j = 0; j < h; j++) mx[j] = x86_max(mx[j], mx[j + h]);
+    const float vmax = mx[0];
+    for (size_t i = 0; i < n; i += 16)
+        for (size_t j = 0; j < 16 && i + j < n; j++) {
+            const float e = or_exp_simd(x[i + j] - vmax);
+            x[i + j] = e;
+            s[j] = s[j] + e;
+        }
+    const float inv = 1.0f / reduce16(s);
+    for (size_t i = 0; i < n; i++) x[i] = x[i] * inv;
 }
 
 /* One output frame of the depthwise convolution (src/kernels/scalar.rs:164-187): out = bias, then

@@ -69,6 +69,7 @@ def lib():
         L.or_silu_simd.restype = ctypes.c_float
         L.or_glu.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.or_layer_norm.argtypes = [_f32p, _sz, _f32p, _f32p, _f32p, ctypes.c_float]
+        L.or_softmax.argtypes = [_f32p, _sz]
         _vp = ctypes.c_void_p
         L.or_tdt_predict.argtypes = [ctypes.c_int, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]
         L.or_tdt_decode.argtypes = [ctypes.c_int, _sz, _sz, _sz, _vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -218,6 +219,17 @@ def layer_norm(x, gamma, beta, eps):
     lib().or_layer_norm(x, x.size, out, np.ascontiguousarray(gamma, np.float32),
                         np.ascontiguousarray(beta, np.float32), float(eps))
     return out
+
+
+def softmax(x):
+    """One row (or each row of a 2-D array), the reference's AVX-512 softmax; returns a copy."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    rows = x.reshape(-1, x.shape[-1]) if x.ndim > 1 else x.reshape(1, -1)
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        lib().or_softmax(row, row.size)
+        rows[r] = row
+    return rows.reshape(x.shape)
 
 
 def dwconv1d_frame(x, t, w, bias):

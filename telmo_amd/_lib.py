@@ -53,6 +53,8 @@ SIGNATURES = {
     "tg_matmul_quantized_glu_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _sz, _sz, _p]),
     "tg_matmul_quantized_to_quant_device": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _p, _p, _p, _sz, _p, _sz]),
     "tg_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _sz]),
+    "tg_softmax_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz]),
+    "tg_average_pairs_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz]),
     "tg_linear_glu_device": (ctypes.c_int, [_p, _p, _sz, _sz, _p, _p, _sz, _sz, _p]),
     "tg_layer_norm_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, ctypes.c_float, _p, _sz,
                                              _sz]),

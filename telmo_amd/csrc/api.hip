@@ -745,6 +745,41 @@ int tg_glu_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t 
     return TG_OK;
 }
 
+int tg_softmax_device(tg_ctx *ctx, float *x, size_t x_len, size_t ldx, size_t m, size_t n) {
+    if (!ctx) return TG_ERR_NULL;
+    if (m == 0 || n == 0) return TG_OK;
+    if (!x) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (ldx < n) return fail(ctx, TG_ERR_SHAPE, "ldx must be >= n");
+    if (x_len < span(m, ldx, n)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (n > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "rows longer than 2^31 values");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_softmax(x, ldx, m, n, ctx->stream));
+    return TG_OK;
+}
+
+int tg_average_pairs_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t frames, size_t batch,
+                            size_t n, float *out, size_t out_len, size_t ldo) {
+    if (!ctx) return TG_ERR_NULL;
+    const size_t rows = frames / 2;
+    if (rows == 0 || batch == 0 || n == 0) return TG_OK;
+    if (!x || !out) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (ldx < n || ldo < n) return fail(ctx, TG_ERR_SHAPE, "ldx and ldo must be >= n");
+    if (frames > SIZE_MAX / batch || rows * batch > SIZE_MAX / n)
+        return fail(ctx, TG_ERR_SHAPE, "frames x batch x n overflows");
+    // Rows b frames + 2 r + 1 for r < frames / 2 are read; a last odd frame is not.
+    const size_t last_in = (batch - 1) * frames + 2 * rows;
+    if (x_len < span(last_in, ldx, n)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (out_len < span(rows * batch, ldo, n)) return fail(ctx, TG_ERR_SHAPE, "out is too short");
+    const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), o0 = reinterpret_cast<uintptr_t>(out);
+    if (x0 < o0 + span(rows * batch, ldo, n) * sizeof(float) && o0 < x0 + span(last_in, ldx, n) * sizeof(float))
+        return fail(ctx, TG_ERR_ARG, "out must not overlap x");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_average_pairs(x, ldx, frames, batch, n, out, ldo, ctx->stream));
+    return TG_OK;
+}
+
 int tg_linear_glu_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const tg_weights *w, float *out,
                          size_t out_len, size_t ldo, const tg_epilogue *epi) {
     if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");

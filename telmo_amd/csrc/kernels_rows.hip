@@ -278,6 +278,121 @@ hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *
     return hipGetLastError();
 }
 
+// softmax of each row in place as the reference's AVX-512 kernel computes it
+// (src/kernels/avx512.rs:382-407): the row maximum; e = exp(x - max) with the SIMD exp, stored;
+// sixteen partial sums, partial j adding e[j], e[j + 16], ... in order from +0, folded by halves
+// (j + 8, j + 4, j + 2, j + 1); inv = 1 / sum; x = e * inv. One workgroup per row. The maximum of
+// a row without NaN is the same in any order, so the workgroup reduces it at once; a row holding a
+// NaN takes the reference's lane order (x86 MAXPS per lane from -inf, then the halving fold with
+// the lower lane first). The sums are the serial part: the row goes through LDS in chunks of
+// SM_CH values, transposed so that lane j of wavefront 0 reads its partial's inputs contiguously,
+// and lanes 0..15 continue their sixteen chains chunk after chunk. Every thread reads back only
+// the e values it stored itself.
+constexpr int SM_CH = 4096, SM_LD = SM_CH / 16 + 4;
+
+__device__ __forceinline__ float x86_maxf(float a, float b) { return a > b ? a : b; }
+
+__global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ x, size_t ldx, size_t m, int n) {
+    __shared__ float eT[16 * SM_LD];
+    __shared__ float red[4];
+    __shared__ int nan_s[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (size_t row = blockIdx.x; row < m; row += gridDim.x) {
+        float *p = x + row * ldx;
+        float mx = -INFINITY;
+        int nan = 0;
+        for (int i = tid; i < n; i += 256) {
+            const float v = p[i];
+            nan |= v != v;
+            mx = v > mx ? v : mx;
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float y = __shfl_xor(mx, o);
+            mx = y > mx ? y : mx;
+            nan |= __shfl_xor(nan, o);
+        }
+        if (lane == 0) {
+            red[wave] = mx;
+            nan_s[wave] = nan;
+        }
+        __syncthreads();
+        mx = x86_maxf(x86_maxf(red[0], red[1]), x86_maxf(red[2], red[3]));
+        if (nan_s[0] | nan_s[1] | nan_s[2] | nan_s[3]) {
+            // The reference's lane order: partial j folds x[j], x[j + 16], ... into -inf.
+            float pm = -INFINITY;
+            if (wave == 0 && lane < 16)
+                for (int i = lane; i < n; i += 16) pm = x86_maxf(pm, p[i]);
+            for (int o = 8; o >= 1; o >>= 1) {
+                const float y = __shfl_down(pm, o, 16);
+                pm = x86_maxf(pm, y);  // lanes j < o: lower lane j first, upper lane j + o second
+            }
+            if (tid == 0) red[0] = pm;
+            __syncthreads();
+            mx = red[0];
+        }
+        float part = 0.0f;
+        for (int c0 = 0; c0 < n; c0 += SM_CH) {
+            const int len = min(SM_CH, n - c0);
+            __syncthreads();  // the previous chunk's sums are done with eT
+            for (int i = tid; i < len; i += 256) {
+                const float e = exp_simd(p[c0 + i] - mx);
+                p[c0 + i] = e;
+                eT[(i & 15) * SM_LD + (i >> 4)] = e;
+            }
+            __syncthreads();
+            if (wave == 0 && lane < 16) {
+                const float *col = eT + lane * SM_LD;
+                const int cnt = (len - lane + 15) >> 4;  // inputs j + 16 t < len of this partial
+                for (int t = 0; t < cnt; t++) part = part + col[t];
+            }
+        }
+        if (wave == 0) {
+            float s = part;
+            s = s + __shfl_xor(s, 8, 16);
+            s = s + __shfl_xor(s, 4, 16);
+            s = s + __shfl_xor(s, 2, 16);
+            s = s + __shfl_xor(s, 1, 16);
+            if (lane == 0) red[0] = 1.0f / s;
+        }
+        __syncthreads();
+        const float inv = red[0];
+        for (int i = tid; i < n; i += 256) p[i] = p[i] * inv;
+        __syncthreads();  // red is rewritten by the next row
+    }
+}
+
+hipError_t launch_softmax(float *x, size_t ldx, size_t m, size_t n, hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    const size_t blocks = m < 65536 ? m : 65536;
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, ldx, m, (int)n);
+    return hipGetLastError();
+}
+
+// Granite's strided-block pooling (src/granite.rs:918-931): output row r of sequence b is
+// (x[b frames + 2 r] + x[b frames + 2 r + 1]) / 2, a rounded sum then an exact halving, for
+// r < frames / 2 (a last odd frame dropped).
+__global__ __launch_bounds__(256) void average_pairs_kernel(const float *__restrict__ x, size_t ldx, size_t frames,
+                                                            size_t rows, size_t total, size_t n,
+                                                            float *__restrict__ out, size_t ldo) {
+    const size_t cells = total * n;
+    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < cells; idx += (size_t)gridDim.x * 256) {
+        const size_t r = idx / n, c = idx - r * n;
+        const size_t b = r / rows, src = b * frames + 2 * (r - b * rows);
+        out[r * ldo + c] = (x[src * ldx + c] + x[(src + 1) * ldx + c]) / 2.0f;
+    }
+}
+
+hipError_t launch_average_pairs(const float *x, size_t ldx, size_t frames, size_t batch, size_t n, float *out,
+                                size_t ldo, hipStream_t s) {
+    const size_t rows = frames / 2, total = rows * batch;
+    if (total == 0 || n == 0) return hipSuccess;
+    size_t blocks = div_ceil(total * n, 256);
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(average_pairs_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, ldx, frames, rows, total, n,
+                       out, ldo);
+    return hipGetLastError();
+}
+
 // LayerNorm of rows of n values as the reference's AVX-512 kernel computes it
 // (src/kernels/avx512.rs:346-380): sixteen partial sums, partial j adding inputs j, j + 16, ... in
 // order, folded by halves (j + 8, j + 4, j + 2, j + 1) into the row sum; mean = sum / n; the same

@@ -212,6 +212,11 @@ hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, 
 
 // out[r][j] = x[r][j] * sigmoid(x[r][half + j]).
 hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s);
+// softmax of m rows of n values in place (the reference's AVX-512 order).
+hipError_t launch_softmax(float *x, size_t ldx, size_t m, size_t n, hipStream_t s);
+// out[b (frames / 2) + r] = (x[b frames + 2 r] + x[b frames + 2 r + 1]) / 2 over n values per row.
+hipError_t launch_average_pairs(const float *x, size_t ldx, size_t frames, size_t batch, size_t n, float *out,
+                                size_t ldo, hipStream_t s);
 
 // LayerNorm of m rows of n values (the reference's AVX-512 summation order).
 hipError_t launch_dwconv1d(const float *x, size_t ldx, size_t frames, size_t batch, size_t channels, const float *w,

@@ -399,6 +399,21 @@ class Kernels:
                                       _dev(out, "float32", "out"), _len(out, out_len, "out"), ldo)
         _check(rc, self._ctx)
 
+    def softmax_device(self, x, ldx: int, m: int, n: int, x_len: Optional[int] = None):
+        """Kernels::softmax (src/kernels/avx512.rs:382-407) of m rows of n values of GPU tensor x, in
+        place."""
+        rc = _lib.lib().tg_softmax_device(self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, m, n)
+        _check(rc, self._ctx)
+
+    def average_pairs_device(self, x, ldx: int, frames: int, n: int, out, ldo: int, batch: int = 1,
+                             x_len: Optional[int] = None, out_len: Optional[int] = None):
+        """Granite's strided-block pooling (src/granite.rs:918-931): row r of each of batch sequences
+        of frames rows becomes (x[2 r] + x[2 r + 1]) / 2 in out (frames // 2 rows per sequence)."""
+        rc = _lib.lib().tg_average_pairs_device(self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx,
+                                                frames, batch, n, _dev(out, "float32", "out"),
+                                                _len(out, out_len, "out"), ldo)
+        _check(rc, self._ctx)
+
     def layer_norm_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, out, ldo: int,
                           x_len: Optional[int] = None, out_len: Optional[int] = None):
         """LayerNorm of m rows of GPU tensor x (n values each) into out (may be x)."""
