@@ -89,6 +89,18 @@ int tg_ctx_create(int device, void *stream, tg_ctx **out);
 void tg_ctx_destroy(tg_ctx *ctx);
 int tg_ctx_set_mode(tg_ctx *ctx, uint32_t mode);
 uint32_t tg_ctx_mode(const tg_ctx *ctx);
+/* The accuracy guard of the product entry points (tg_matmul, tg_linear and their _device and
+ * _noalloc forms) in fast mode, on by default; no counterpart in the reference, whose f32 sums have
+ * no data-dependent error. The fast path keeps 15 bits of each row relative to its largest value.
+ * When a product takes the GEMM (not the decode GEMV of a few aligned rows), its quantiser also
+ * measures what the two digits drop: with x = a 2^e the scaled inputs, v = rint(x) and d =
+ * rint(256 (x - v)), a row whose 256 sum d^2 exceeds sum v^2 (a relative rounding of the row above
+ * 2^-12, where the fast path's row-normwise error could approach 1e-3: an outlier far above the
+ * rest of a long row) is flagged, and the exact kernel rewrites that row's outputs with the
+ * reference's fused sums (its bits), the epilogue accumulating onto the row as it was before the
+ * call. Unflagged rows keep the fast path's bits. Off: every row takes the fast path. */
+int tg_ctx_set_guard(tg_ctx *ctx, int on);
+int tg_ctx_guard(const tg_ctx *ctx);
 /* The message of the last failed call on this context ("" if none), copied into storage of the
  * calling thread: valid until that thread's next tg_last_error call. */
 const char *tg_last_error(const tg_ctx *ctx);
@@ -145,8 +157,10 @@ int tg_linear_device(tg_ctx *ctx, const float *a, size_t a_len, size_t m, const 
  * cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * The same checks, kernels and bits as tg_matmul_device; the quantised rows of a product that
  * takes the GEMM go to a scratch array of the library's (16 MiB per GPU, held until the process
- * ends) instead of the context's grown workspace. Products whose quantised rows exceed it
- * (tg_quant_bytes(m, k) > 16 MiB - 64 KiB, or m > 16384) give TG_ERR_UNSUPPORTED. Every call on a
+ * ends) instead of the context's grown workspace, and so do the accuracy guard's flags and, for an
+ * accumulating product, its rows' old outputs (m n floats after the quantised rows). Products whose
+ * quantised rows exceed it (tg_quant_bytes(m, k) > 16 MiB - 128 KiB, or m > 16384), or with the guard
+ * on whose old outputs do not fit beside them, give TG_ERR_UNSUPPORTED. Every call on a
  * GPU shares that GPU's scratch, so calls that overlap on one GPU (other contexts or streams)
  * race: serialise them. Device pointers, queued on the stream. */
 int tg_matmul_device_noalloc(tg_ctx *ctx, const float *a, size_t a_len, size_t lda, size_t m, const tg_weights *w,

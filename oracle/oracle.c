@@ -508,6 +508,24 @@ int32_t or_row_exponent(const float *a, size_t k) {
     return e;
 }
 
+/* The accuracy guard's flag of one row (telmo_amd's fast path; no reference counterpart): with e
+ * the row exponent, x = ldexp(a, e), v = rint(x) (the two digits' value) and d = rint(256 (x - v))
+ * (the next eight bits), the row is flagged when 256 sum d^2 > sum v^2, summed as exact integers.
+ * Rows holding a NaN or an infinity are not flagged. A flagged row's outputs are the fused
+ * reference's (or_matmul). */
+int or_guard_flag(const float *a, size_t k) {
+    const int32_t e = or_row_exponent(a, k);
+    if (e == OR_EXP_NONFINITE) return 0;
+    int64_t vv = 0, dd = 0;
+    for (size_t i = 0; i < k; i++) {
+        const float x = ldexpf(a[i], e), v = rintf(x);
+        const int64_t d = (int64_t)rintf((x - v) * 256.0f), iv = (int64_t)v;
+        vv += iv * iv;
+        dd += d * d;
+    }
+    return 256 * dd > vv;
+}
+
 /* Digits of rows a[m][lda] into hi/lo [m][k] and exponents [m]. */
 void or_quantize_rows(const float *a, size_t lda, size_t m, size_t k, int8_t *hi, int8_t *lo, int32_t *ex) {
     for (size_t r = 0; r < m; r++) {

@@ -88,6 +88,8 @@ def lib():
                                      ctypes.c_void_p, _sz, ctypes.c_int, ctypes.c_float, ctypes.c_int]
         L.or_matmul_fast_q8.argtypes = L.or_matmul_fast.argtypes
         L.or_row_exponent.argtypes = [_f32p, _sz]
+        L.or_guard_flag.argtypes = [_f32p, _sz]
+        L.or_guard_flag.restype = ctypes.c_int
         L.or_row_exponent.restype = ctypes.c_int32
         L.or_quantize_rows.argtypes = [_f32p, _sz, _sz, _sz, _i8p, _i8p, _i32p]
         L.or_int_products.argtypes = [_i8p, _i8p, _sz, _sz, _i8p, _sz, _i32p, _i32p]
@@ -352,16 +354,49 @@ def matmul(fused, a, lda, m, values, scales, p, n, k, c, ldc, bias=None, act=NON
                            _ptr(bias), 0 if bias is None else bias.size, act, scale, int(accumulate))
 
 
-def matmul_fast(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, scale=1.0, accumulate=False):
-    """The integer oracle of the fast int8 path, in place on `c`."""
-    return lib().or_matmul_fast(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc, _ptr(bias),
-                                0 if bias is None else bias.size, act, scale, int(accumulate))
+def guard_flags(a, lda, m, k):
+    """The accuracy guard's flag of each of m rows of a (rows lda apart)."""
+    a = np.ascontiguousarray(a, np.float32)
+    return np.array([lib().or_guard_flag(np.ascontiguousarray(a[r * lda:r * lda + k]) if k else
+                                         np.zeros(1, np.float32), k) for r in range(m)], np.int32)
 
 
-def matmul_fast_q8(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, scale=1.0, accumulate=False):
-    """The integer oracle of the fast Q8_0 path (block sums scaled in block order), in place on `c`."""
-    return lib().or_matmul_fast_q8(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc, _ptr(bias),
-                                   0 if bias is None else bias.size, act, scale, int(accumulate))
+def _guarded(fast, a, lda, m, values, scales, p, n, k, c, ldc, bias, act, scale, accumulate, guard):
+    """A fast-path oracle with the accuracy guard: flagged rows take the fused reference (or_matmul)
+    on their own, accumulating onto the row as it was before the call."""
+    if not guard or m == 0 or n == 0:
+        return fast()
+    flags = guard_flags(a, lda, m, k)
+    old = {r: c[r * ldc:r * ldc + n].copy() for r in np.flatnonzero(flags)}
+    rc = fast()
+    if rc:
+        return rc
+    for r, row_c in old.items():
+        ar = np.ascontiguousarray(a[r * lda:r * lda + k]) if k else np.zeros(1, np.float32)
+        rc = matmul(True, ar, k, 1, values, scales, p, n, k, row_c, n, bias, act, scale, accumulate)
+        if rc:
+            return rc
+        c[r * ldc:r * ldc + n] = row_c
+    return 0
+
+
+def matmul_fast(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, scale=1.0, accumulate=False,
+                guard=False):
+    """The integer oracle of the fast int8 path, in place on `c`; guard: the product entry points'
+    accuracy guard (rows it flags take the fused reference)."""
+    fast = lambda: lib().or_matmul_fast(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc,  # noqa: E731
+                                        _ptr(bias), 0 if bias is None else bias.size, act, scale, int(accumulate))
+    return _guarded(fast, a, lda, m, values, scales, INT8, n, k, c, ldc, bias, act, scale, accumulate, guard)
+
+
+def matmul_fast_q8(a, lda, m, values, scales, n, k, c, ldc, bias=None, act=NONE, scale=1.0, accumulate=False,
+                   guard=False):
+    """The integer oracle of the fast Q8_0 path (block sums scaled in block order), in place on `c`;
+    guard as matmul_fast."""
+    fast = lambda: lib().or_matmul_fast_q8(a, a.size, lda, m, values, scales, n, k, c, c.size, ldc,  # noqa: E731
+                                           _ptr(bias), 0 if bias is None else bias.size, act, scale,
+                                           int(accumulate))
+    return _guarded(fast, a, lda, m, values, scales, Q8_0, n, k, c, ldc, bias, act, scale, accumulate, guard)
 
 
 def row_exponent(row):

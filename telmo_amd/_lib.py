@@ -32,6 +32,8 @@ SIGNATURES = {
     "tg_ctx_destroy": (None, [_p]),
     "tg_ctx_set_mode": (ctypes.c_int, [_p, _u32]),
     "tg_ctx_mode": (_u32, [_p]),
+    "tg_ctx_set_guard": (ctypes.c_int, [_p, ctypes.c_int]),
+    "tg_ctx_guard": (ctypes.c_int, [_p]),
     "tg_last_error": (ctypes.c_char_p, [_p]),
     "tg_synchronize": (ctypes.c_int, [_p]),
     "tg_weights_upload": (ctypes.c_int, [_p, _p, _sz, _p, _sz, _u32, _sz, _sz, ctypes.POINTER(_p)]),

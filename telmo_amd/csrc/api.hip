@@ -47,6 +47,13 @@ struct tg_ctx {
     size_t hid_cap = 0;
     uint32_t *tmax = nullptr;
     size_t tmax_cap = 0;
+    // The accuracy guard of the product entry points (tg::RowGuard): on unless turned off; its row
+    // flags and the flagged rows' old outputs, grown on demand.
+    bool guard = true;
+    int32_t *flags = nullptr;
+    size_t flags_cap = 0;
+    float *save = nullptr;
+    size_t save_cap = 0;
 };
 
 struct tg_weights {
@@ -92,13 +99,15 @@ struct tg_tdt {
 
 
 // The scratch of tg_matmul_device_noalloc, for callers that cannot allocate: the quantised rows of
-// one product (the first NOALLOC_QA_BYTES) and their row exponents (NOALLOC_ROWS int32 after them).
+// one product (the first NOALLOC_QA_BYTES; with the accuracy guard on and an accumulating
+// epilogue, the flagged rows' old outputs after them), their row exponents (NOALLOC_ROWS int32
+// after that region) and the guard's row flags (NOALLOC_ROWS int32 after the exponents).
 // Each GPU the library runs on holds its own copy for the life of the process. Host code never uses
 // the array's name as an address: tg_ctx_create takes each device's address with
 // hipGetSymbolAddress, with that device current, and the kernels get that pointer.
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
 constexpr size_t NOALLOC_ROWS = 16384;
-constexpr size_t NOALLOC_QA_BYTES = NOALLOC_SCRATCH_BYTES - NOALLOC_ROWS * sizeof(int32_t);
+constexpr size_t NOALLOC_QA_BYTES = NOALLOC_SCRATCH_BYTES - 2 * NOALLOC_ROWS * sizeof(int32_t);
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -253,8 +262,24 @@ int run_device(tg_ctx *ctx, const float *a, size_t lda, size_t m, const tg_weigh
     if (rc) return rc;
     rc = grow(ctx, ctx->exps, ctx->exps_cap, m * sizeof(int32_t));
     if (rc) return rc;
-    TG_HIP(ctx, tg::launch_quantize_rows(a, lda, m, d.k, ctx->qa, ctx->exps, ctx->stream));
+    // The accuracy guard: the quantiser flags the rows whose two digits drop too much (keeping their
+    // old outputs when the epilogue accumulates), the GEMM runs on every row, then the exact kernel
+    // rewrites the flagged rows with the reference's fused sums.
+    tg::RowGuard g;
+    if (ctx->guard) {
+        if ((rc = grow(ctx, ctx->flags, ctx->flags_cap, m * sizeof(int32_t)))) return rc;
+        g.flags = ctx->flags;
+        if (epi.accumulate) {
+            if ((rc = grow(ctx, ctx->save, ctx->save_cap, m * d.n * sizeof(float)))) return rc;
+            g.c = c;
+            g.ldc = ldc;
+            g.n = d.n;
+            g.save = ctx->save;
+        }
+    }
+    TG_HIP(ctx, tg::launch_quantize_rows(a, lda, m, d.k, ctx->qa, ctx->exps, ctx->stream, tg::RowAct{}, g));
     TG_HIP(ctx, tg::launch_gemm_i8(ctx->qa, ctx->exps, m, d, c, ldc, epi, ctx->stream));
+    if (ctx->guard) TG_HIP(ctx, tg::launch_exact_rows(a, lda, m, d, c, ldc, epi, g.flags, g.save, ctx->stream));
     return TG_OK;
 }
 
@@ -357,7 +382,7 @@ void tg_ctx_destroy(tg_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (void *p : {(void *)ctx->qa, (void *)ctx->exps, (void *)ctx->da, (void *)ctx->dc, (void *)ctx->dbias,
-                    (void *)ctx->dg, (void *)ctx->hid, (void *)ctx->tmax})
+                    (void *)ctx->dg, (void *)ctx->hid, (void *)ctx->tmax, (void *)ctx->flags, (void *)ctx->save})
         if (p) (void)hipFree(p);
     if (ctx->hst) (void)hipHostFree(ctx->hst);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -373,6 +398,15 @@ int tg_ctx_set_mode(tg_ctx *ctx, uint32_t mode) {
 }
 
 uint32_t tg_ctx_mode(const tg_ctx *ctx) { return ctx ? ctx->mode : TG_MODE_FAST; }
+
+int tg_ctx_set_guard(tg_ctx *ctx, int on) {
+    if (!ctx) return TG_ERR_NULL;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    ctx->guard = on != 0;
+    return TG_OK;
+}
+
+int tg_ctx_guard(const tg_ctx *ctx) { return ctx && ctx->guard ? 1 : 0; }
 
 const char *tg_last_error(const tg_ctx *ctx) {
     // The message is copied under its lock into storage of the calling thread, so another thread
@@ -449,6 +483,15 @@ int tg_matmul_device_noalloc(tg_ctx *ctx, const float *a, size_t a_len, size_t l
                     "the product's quantised rows (" + std::to_string(tg::qa_bytes(m, d.k)) + " bytes, " +
                         std::to_string(m) + " rows) exceed the no-allocation scratch (" +
                         std::to_string(NOALLOC_QA_BYTES) + " bytes, " + std::to_string(NOALLOC_ROWS) + " rows)");
+    // With the guard on, an accumulating product keeps its flagged rows' old outputs (m n floats)
+    // after the quantised rows.
+    const size_t qa_round = (tg::qa_bytes(m, d.k) + 255) / 256 * 256;
+    const bool keep = staged && ctx->guard && epi && epi->accumulate;
+    if (keep && (d.n > (NOALLOC_QA_BYTES - qa_round) / sizeof(float) / m))
+        return fail(ctx, TG_ERR_UNSUPPORTED,
+                    "with the accuracy guard on, an accumulating product keeps m x n floats beside its quantised "
+                    "rows, which exceed the no-allocation scratch (" + std::to_string(NOALLOC_QA_BYTES) +
+                        " bytes); turn the guard off (tg_ctx_set_guard) or split the rows");
     TG_HIP(ctx, hipSetDevice(ctx->device));
     const tg::EpiArgs e = epi_args(epi, nullptr, false);
     if (!int_path) {
@@ -464,8 +507,19 @@ int tg_matmul_device_noalloc(tg_ctx *ctx, const float *a, size_t a_len, size_t l
         // the scratch needs clearing between calls.
         uint8_t *qa = static_cast<uint8_t *>(base);
         int32_t *exps = reinterpret_cast<int32_t *>(qa + NOALLOC_QA_BYTES);
-        TG_HIP(ctx, tg::launch_quantize_rows(a, lda, m, d.k, qa, exps, ctx->stream));
+        tg::RowGuard g;
+        if (ctx->guard) {
+            g.flags = exps + NOALLOC_ROWS;
+            if (keep) {
+                g.c = c;
+                g.ldc = ldc;
+                g.n = d.n;
+                g.save = reinterpret_cast<float *>(qa + qa_round);
+            }
+        }
+        TG_HIP(ctx, tg::launch_quantize_rows(a, lda, m, d.k, qa, exps, ctx->stream, tg::RowAct{}, g));
         TG_HIP(ctx, tg::launch_gemm_i8(qa, exps, m, d, c, ldc, e, ctx->stream));
+        if (ctx->guard) TG_HIP(ctx, tg::launch_exact_rows(a, lda, m, d, c, ldc, e, g.flags, g.save, ctx->stream));
     }
     clear_error(ctx);
     return TG_OK;

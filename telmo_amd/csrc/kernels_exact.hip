@@ -56,6 +56,41 @@ __global__ __launch_bounds__(256) void exact_kernel(const float *__restrict__ a,
     *cp = epilogue(acc, bias, (size_t)col, act, escale, accumulate != 0, cp);
 }
 
+// The accuracy guard's fix-up (RowGuard): the exact kernel's sums and epilogue for the flagged rows
+// of a product the fast path has just written, over every output column. Workgroup (x, y) takes the
+// 64 columns 64 x .. and the rows of chunk y; its wavefronts read the chunk's flags 64 at a time and
+// take the flagged rows in turn (wavefront w the w-th, w + 4-th, ... of each group of 64). A flagged
+// row's old outputs come from save (kept by the quantiser) when the epilogue accumulates.
+__global__ __launch_bounds__(256) void exact_rows_kernel(const float *__restrict__ a, size_t lda, int m, int k,
+                                                         const uint8_t *__restrict__ wv,
+                                                         const float *__restrict__ scales, uint32_t prec, int N,
+                                                         size_t ps, size_t bs, float *__restrict__ c, size_t ldc,
+                                                         const float *__restrict__ bias, uint32_t act, float escale,
+                                                         int accumulate, const int32_t *__restrict__ flags,
+                                                         const float *__restrict__ save, int chunk) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    const int r0 = blockIdx.y * chunk, r1 = min(m, r0 + chunk);
+    const size_t p = (size_t)(col < N ? col : N - 1) / PANEL;
+    const int j = (col < N ? col : N - 1) % PANEL;
+    for (int base = r0; base < r1; base += 64) {
+        const int f = base + lane < r1 ? flags[base + lane] : 0;
+        uint64_t mask = __ballot(f != 0);
+        for (int nth = 0; mask; nth++, mask &= mask - 1) {
+            if ((nth & 3) != wave) continue;
+            const int row = base + __builtin_ctzll(mask);
+            if (col >= N) continue;
+            const float *ar = a + (size_t)row * lda;
+            float acc = 0.0f;
+            for (int i = 0; i < k; i++)
+                acc = __builtin_fmaf(ar[i], widen_one(wv, scales, prec, k, ps, bs, p, j, i), acc);
+            const float old = accumulate ? save[(size_t)row * N + col] : 0.0f;
+            c[(size_t)row * ldc + col] = epilogue_vals(acc, bias != nullptr, bias ? bias[col] : 0.0f, act, escale,
+                                                       accumulate != 0, old);
+        }
+    }
+}
+
 // BView::row_major as the right-hand side (src/kernels/mod.rs:320-339): column col of input i is
 // b[i ldb + col], read straight from the row-major f32 matrix, summed as the exact kernel sums.
 __global__ __launch_bounds__(256) void rowmajor_kernel(const float *__restrict__ a, size_t lda, int m, int k,
@@ -90,6 +125,21 @@ hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeight
     hipLaunchKernelGGL(exact_kernel, grid, dim3(256), 0, s, a, lda, (int)m, (int)w.k, w.values, w.scales,
                        w.precision, (int)w.n, w.panel_stride, w.blk_stride, c, ldc, epi.bias, epi.act, epi.scale,
                        epi.accumulate);
+    return hipGetLastError();
+}
+
+hipError_t launch_exact_rows(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                             const EpiArgs &epi, const int32_t *flags, const float *save, hipStream_t s) {
+    if (m == 0 || w.n == 0) return hipSuccess;
+    // About 2048 workgroups: the column groups times row chunks of whole groups of 64 rows.
+    const size_t cols = div_ceil(w.n, 64), groups = div_ceil(m, 64);
+    size_t chunks = 2048 / cols;
+    chunks = chunks < 1 ? 1 : (chunks > groups ? groups : chunks);
+    const size_t chunk = div_ceil(groups, chunks) * 64;
+    dim3 grid((unsigned)cols, (unsigned)div_ceil(m, chunk));
+    hipLaunchKernelGGL(exact_rows_kernel, grid, dim3(256), 0, s, a, lda, (int)m, (int)w.k, w.values, w.scales,
+                       w.precision, (int)w.n, w.panel_stride, w.blk_stride, c, ldc, epi.bias, epi.act, epi.scale,
+                       epi.accumulate, flags, save, (int)chunk);
     return hipGetLastError();
 }
 

@@ -52,9 +52,31 @@ __device__ __forceinline__ int wave_or(int v) {
 
 // One wavefront per row: the largest magnitude (and any NaN or infinity) over the row's k
 // inputs, the row exponent, then the digits of each input into the fragment-major QA.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// The guard's flag of a row (RowGuard) from the two sums of every input; with a save buffer, a
+// flagged row's outputs as they are before the product are copied there by the workgroup's
+// `threads` threads (thread t copies columns t, t + threads, ...).
+__device__ __forceinline__ void guard_store(const RowGuard &g, size_t row, int32_t flag, int t, int threads) {
+    if (t == 0) g.flags[row] = flag;
+    if (flag && g.save) {
+        const float *cr = g.c + row * g.ldc;
+        float *sr = g.save + row * g.n;
+        for (size_t j = t; j < g.n; j += threads) sr[j] = cr[j];
+    }
+}
+
 __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ ar, size_t k, size_t kb,
                                                      uint8_t *__restrict__ qa, size_t row, int lane,
-                                                     const RowAct &f) {
+                                                     const RowAct &f, int32_t *flag = nullptr) {
     float amax = 0.0f;
     int bad = 0;
     for (size_t i = lane; i < k; i += 64) {
@@ -65,25 +87,34 @@ __device__ __forceinline__ int32_t quantize_row_wave(const float *__restrict__ a
     amax = wave_max(amax);
     bad = wave_or(bad);
     const int32_t e = bad ? EXP_NONFINITE : row_exponent_of(amax);
+    double vv = 0.0;
+    int32_t dd = 0;
     for (size_t t = 0; t < kb; t++) {
         const size_t i = t * KBLK + lane;
         int8_t hi = 0, lo = 0;
-        if (i < k) digits_of(f(ar[i]), e, hi, lo);
+        if (i < k) {
+            const float x = f(ar[i]);
+            digits_of(x, e, hi, lo);
+            if (flag && e != EXP_NONFINITE) guard_terms(x, e, vv, dd);
+        }
         const size_t at = qa_offset(row, t, 0, kb) + (lane >> 4) * 256 + (lane & 15);
         qa[at] = (uint8_t)hi;
         qa[at + 1024] = (uint8_t)lo;
     }
+    if (flag) *flag = guard_flag(e, wave_sum_f64(vv), wave_sum_i32(dd));
     return e;
 }
 
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restrict__ a, size_t lda, size_t m,
                                                             size_t k, size_t kb, uint8_t *__restrict__ qa,
-                                                            int32_t *__restrict__ exps, RowAct f) {
+                                                            int32_t *__restrict__ exps, RowAct f, RowGuard g) {
     const int lane = threadIdx.x & 63;
     const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= m) return;
-    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa, row, lane, f);
+    int32_t flag = 0;
+    int32_t e = quantize_row_wave(a + row * lda, k, kb, qa, row, lane, f, g.flags ? &flag : nullptr);
     if (lane == 0) exps[row] = e;
+    if (g.flags) guard_store(g, row, flag, lane, 64);
 }
 
 // One workgroup per row, the row held in registers: thread t owns the 4-input chunks t + 256 j
@@ -100,13 +131,18 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float *__restr
 // ACT_SILU (3) fixed at compile time and applied to every value of a chunk with no branch (the
 // chunk's values past k are zeros, which every f maps to a zero digit); a runtime act inside the
 // unrolled chunks cost a branch per value.
-template <int J, int MODE>
+//
+// GUARD: the row's flag of the accuracy guard (RowGuard) from the inputs held in registers, after
+// the digits are stored, and a flagged row's old outputs saved.
+template <int J, int MODE, bool GUARD>
 __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__restrict__ a, size_t lda, int k,
                                                                  int kb, uint8_t *__restrict__ qa,
                                                                  int32_t *__restrict__ exps, int vec, size_t m,
-                                                                 size_t bpx, float scale) {
+                                                                 size_t bpx, float scale, RowGuard g) {
     __shared__ float s_max[4];
     __shared__ int s_bad[4];
+    __shared__ double s_vv[4];
+    __shared__ int32_t s_dd[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t x = blockIdx.x % 8, i = blockIdx.x / 8;
     const size_t row = (x * bpx + i / 16) * 16 + i % 16;
@@ -161,36 +197,61 @@ __global__ __launch_bounds__(256) void quantize_rows_regs_kernel(const float *__
             *reinterpret_cast<uint32_t *>(qa + at + 1024) = lo;
         }
     }
+    if constexpr (GUARD) {
+        // Chunks past k hold zeros, whose v and d are zero.
+        double vv = 0.0;
+        int32_t dd = 0;
+        if (e != EXP_NONFINITE) {
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                guard_terms(v[j].x, e, vv, dd);
+                guard_terms(v[j].y, e, vv, dd);
+                guard_terms(v[j].z, e, vv, dd);
+                guard_terms(v[j].w, e, vv, dd);
+            }
+        }
+        vv = wave_sum_f64(vv);
+        dd = wave_sum_i32(dd);
+        if (lane == 0) {
+            s_vv[wave] = vv;
+            s_dd[wave] = dd;
+        }
+        __syncthreads();
+        const int32_t flag = guard_flag(e, ((s_vv[0] + s_vv[1]) + s_vv[2]) + s_vv[3], s_dd[0] + s_dd[1] + s_dd[2] + s_dd[3]);
+        guard_store(g, row, flag, tid, 256);
+    }
 }
 
 template <int J>
 void launch_regs(const float *a, size_t lda, size_t m, size_t k, size_t kb, uint8_t *qa, int32_t *exps, int vec,
-                 const RowAct &f, hipStream_t s) {
+                 const RowAct &f, const RowGuard &g, hipStream_t s) {
     const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
     const int mode = f.act == ACT_NONE ? (f.scale == 1.0f ? 0 : 1) : f.act == ACT_RELU ? 2 : 3;
-    auto kernel = &quantize_rows_regs_kernel<J, 0>;
-    if (mode == 1) kernel = &quantize_rows_regs_kernel<J, 1>;
-    else if (mode == 2) kernel = &quantize_rows_regs_kernel<J, 2>;
-    else if (mode == 3) kernel = &quantize_rows_regs_kernel<J, 3>;
+    auto kernel = &quantize_rows_regs_kernel<J, 0, false>;
+    if (g.flags) kernel = &quantize_rows_regs_kernel<J, 0, true>;  // the product entry points: no activation
+    else if (mode == 1) kernel = &quantize_rows_regs_kernel<J, 1, false>;
+    else if (mode == 2) kernel = &quantize_rows_regs_kernel<J, 2, false>;
+    else if (mode == 3) kernel = &quantize_rows_regs_kernel<J, 3, false>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)(8 * bpx * 16)), dim3(256), 0, s, a, lda, (int)k, (int)kb, qa, exps,
-                       vec, m, bpx, f.scale);
+                       vec, m, bpx, f.scale, g);
 }
 
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
-                                hipStream_t s, RowAct f) {
+                                hipStream_t s, RowAct f, const RowGuard &g) {
+    if (g.flags && (f.act != ACT_NONE || f.scale != 1.0f)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const size_t kb = div_ceil(k, KBLK);
     // 16-byte loads need every row 16-byte aligned.
     const int vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) && (lda % 4 == 0);
     const size_t j = div_ceil(kb * 16, 256);  // 4-input chunks per thread
-    if (j <= 1) launch_regs<1>(a, lda, m, k, kb, qa, exps, vec, f, s);
-    else if (j <= 2) launch_regs<2>(a, lda, m, k, kb, qa, exps, vec, f, s);
-    else if (j <= 4) launch_regs<4>(a, lda, m, k, kb, qa, exps, vec, f, s);
-    else if (j <= 8) launch_regs<8>(a, lda, m, k, kb, qa, exps, vec, f, s);
-    else if (j <= 16) launch_regs<16>(a, lda, m, k, kb, qa, exps, vec, f, s);
+    if (j <= 1) launch_regs<1>(a, lda, m, k, kb, qa, exps, vec, f, g, s);
+    else if (j <= 2) launch_regs<2>(a, lda, m, k, kb, qa, exps, vec, f, g, s);
+    else if (j <= 4) launch_regs<4>(a, lda, m, k, kb, qa, exps, vec, f, g, s);
+    else if (j <= 8) launch_regs<8>(a, lda, m, k, kb, qa, exps, vec, f, g, s);
+    else if (j <= 16) launch_regs<16>(a, lda, m, k, kb, qa, exps, vec, f, g, s);
     else
         hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)div_ceil(m, 4)), dim3(256), 0, s, a, lda, m, k, kb,
-                           qa, exps, f);
+                           qa, exps, f, g);
     return hipGetLastError();
 }
 

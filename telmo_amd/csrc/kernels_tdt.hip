@@ -938,8 +938,8 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                 }
                 const int col = (pj0 + pi) * PANEL + j16;
                 const float sc = sh.js[pi * PANEL + j16], bs = sh.jbias[pi * PANEL + j16];
-                const bool fits = __all(dequant_fits(hi[0]) & dequant_fits(hi[1]) & dequant_fits(hi[2]) &
-                                        dequant_fits(hi[3]));
+                const bool fits = __all((int)dequant_fits(hi[0]) & (int)dequant_fits(hi[1]) &
+                                        (int)dequant_fits(hi[2]) & (int)dequant_fits(hi[3]));
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int r = orow + v;

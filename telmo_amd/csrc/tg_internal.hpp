@@ -184,6 +184,21 @@ __device__ __forceinline__ void digits4(float x0, float x1, float x2, float x3, 
     hi = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
 }
 
+// The guard's two sums over one input (RowGuard): v^2 and d^2 of x = a 2^e, v = rint(x),
+// d = rint(256 (x - v)). x - v is exact (|x - v| <= 1/2 and both are f32 near each other), and so is
+// the scaling by 256, so d is an integer in [-128, 128].
+__device__ __forceinline__ void guard_terms(float a, int32_t e, double &vv, int32_t &dd) {
+    const float x = __builtin_ldexpf(a, e);
+    const float v = __builtin_rintf(x);
+    const int32_t d = (int32_t)__builtin_rintf((x - v) * 256.0f);
+    vv += (double)v * (double)v;
+    dd += d * d;
+}
+// The flag of a row from its two sums (RowGuard).
+__device__ __forceinline__ int32_t guard_flag(int32_t e, double vv, int32_t dd) {
+    return e != EXP_NONFINITE && 256.0 * (double)dd > vv ? 1 : 0;
+}
+
 // ---------------------------------------------------------------------------- launchers
 
 struct EpiArgs {
@@ -206,9 +221,26 @@ struct RowAct {
     }
 };
 
-// Per-row digits and exponents of f(a[m][lda]) (k inputs) into qa (fragment-major) / exps.
+// The accuracy guard of a product's quantised rows. Under its exponent e a row's inputs become
+// x = a 2^e, v = rint(x) (the two digits' value) and d = rint(256 (x - v)) (the next eight bits);
+// the row is flagged when 256 sum d^2 > sum v^2, that is when the relative size of what the two
+// digits drop, rho = |x - v| / |x| ~ sqrt(sum d^2 / 65536) / sqrt(sum v^2), exceeds 2^-12. Both
+// sums are exact integers (sum v^2 < 2^53 in f64, sum d^2 < 2^31), so the flag does not depend on
+// the order of the sums. The fast path's row-normwise error measures 0.7 to 2.1 rho, so an unflagged
+// row stays within about 5e-4 of the reference; N(0, 1) rows have rho near 3.5e-5. Rows with a NaN
+// or an infinity are not flagged (their outputs are NaN, as without the guard).
+struct RowGuard {
+    int32_t *flags = nullptr;  // per row, 1 when flagged; null: no guard
+    const float *c = nullptr;  // the product's output rows before it runs, kept for flagged rows
+    size_t ldc = 0;            // when the epilogue accumulates: c[r ldc + j] -> save[r n + j], j < n
+    size_t n = 0;
+    float *save = nullptr;  // null when the epilogue does not accumulate
+};
+
+// Per-row digits and exponents of f(a[m][lda]) (k inputs) into qa (fragment-major) / exps, and
+// the guard's flags (and saved output rows) when g.flags is set.
 hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, uint8_t *qa, int32_t *exps,
-                                hipStream_t s, RowAct f = RowAct{});
+                                hipStream_t s, RowAct f = RowAct{}, const RowGuard &g = RowGuard{});
 
 // out[r][j] = x[r][j] * sigmoid(x[r][half + j]).
 hipError_t launch_glu(const float *x, size_t ldx, size_t m, size_t half, float *out, size_t ldo, hipStream_t s);
@@ -271,6 +303,10 @@ hipError_t launch_gemv_i8(const float *a, size_t lda, size_t m, const DeviceWeig
 // The exact kernel: the reference's fused sums in input order, any precision.
 hipError_t launch_exact(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
                         const EpiArgs &epi, hipStream_t s);
+// The guard's fix-up: the exact kernel's outputs for the rows flagged in flags[m] only, the epilogue
+// accumulating onto save[r n + j] (the rows as they were before the product) when it accumulates.
+hipError_t launch_exact_rows(const float *a, size_t lda, size_t m, const DeviceWeights &w, float *c, size_t ldc,
+                             const EpiArgs &epi, const int32_t *flags, const float *save, hipStream_t s);
 // A row-major f32 right-hand side [k, ldb], the exact kernel's sums (kernels_exact.hip).
 hipError_t launch_rowmajor(const float *a, size_t lda, size_t m, size_t k, const float *b, size_t ldb, size_t n,
                            float *c, size_t ldc, const EpiArgs &epi, hipStream_t s);

@@ -257,6 +257,14 @@ class Kernels:
     def mode(self) -> int:
         return _lib.lib().tg_ctx_mode(self._ctx)
 
+    def set_guard(self, on: bool) -> None:
+        """The fast path's accuracy guard (on by default): rows whose two digits drop more than 2^-12
+        of them take the reference's fused sums (tg_ctx_set_guard)."""
+        _check(_lib.lib().tg_ctx_set_guard(self._ctx, int(bool(on))), self._ctx)
+
+    def guard(self) -> bool:
+        return bool(_lib.lib().tg_ctx_guard(self._ctx))
+
     def close(self) -> None:
         if self._ctx:
             _lib.lib().tg_ctx_destroy(self._ctx)

@@ -2,7 +2,9 @@
 device layer (telmo_amd.conformer): LayerNorm rows (or_layer_norm), products (the integer oracle
 or_matmul_fast of the fast path, or the fused f32 reference or_matmul), the GLU, the depthwise
 convolution + SiLU per utterance, in the reference's order, with the V third of qkv standing in for
-the attention core as the device layer's default does."""
+the attention core as the device layer's default does. Products the device makes through
+tg_matmul_device (the attention output's, which quantises f32 rows itself) take the integer oracle
+with the entry point's accuracy guard; the staged products of quantised rows take it without."""
 import numpy as np
 
 NONE, SILU = 0, 2
@@ -15,12 +17,13 @@ def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True):
     x = x.copy()
     t, d = x.shape
 
-    def linear(a, lda, name, c, act=NONE, scale=1.0, accumulate=False):
+    def linear(a, lda, name, c, act=NONE, scale=1.0, accumulate=False, guard=False):
         values, scales, n, k = mats[name]
         flat = np.ascontiguousarray(a).reshape(-1)
         out = c.reshape(-1)
         if fast:
-            rc = orc.matmul_fast(flat, lda, t, values, scales, n, k, out, n, None, act, scale, accumulate)
+            rc = orc.matmul_fast(flat, lda, t, values, scales, n, k, out, n, None, act, scale, accumulate,
+                                 guard=guard)
         else:
             rc = orc.matmul(True, flat, lda, t, values, scales, INT8, n, k, out, n, None, act, scale, accumulate)
         assert rc == 0
@@ -38,7 +41,7 @@ def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True):
     feed_forward("norm_ff1", "ff1_in", "ff1_out")
     h = ln(x, "norm_att")
     qkv = linear(h, d, "qkv", np.zeros((t, 3 * d), np.float32))
-    linear(qkv.reshape(-1)[2 * d:], 3 * d, "out", x, NONE, 1.0, True)
+    linear(qkv.reshape(-1)[2 * d:], 3 * d, "out", x, NONE, 1.0, True, guard=True)  # tg_matmul_device
     h = ln(x, "norm_conv")
     g = linear(h, d, "pw1", np.zeros((t, 2 * d), np.float32))
     u = np.stack([orc.glu(g[r, :d], g[r, d:]) for r in range(t)])
@@ -57,14 +60,15 @@ def oracle_granite_block(orc, x, mats, biases, norms, dw_w, dw_b, strided, utter
     x = x.copy()
     t, d = x.shape
 
-    def linear(a, rows, name, c, act=NONE, scale=1.0, accumulate=False, lda=None):
+    def linear(a, rows, name, c, act=NONE, scale=1.0, accumulate=False, lda=None, guard=False):
         values, scales, n, k = mats[name]
         flat = np.ascontiguousarray(a).reshape(-1)
         out = c.reshape(-1)
         bias = biases.get(name)
         lda = k if lda is None else lda
         if fast:
-            rc = orc.matmul_fast(flat, lda, rows, values, scales, n, k, out, n, bias, act, scale, accumulate)
+            rc = orc.matmul_fast(flat, lda, rows, values, scales, n, k, out, n, bias, act, scale, accumulate,
+                                 guard=guard)
         else:
             rc = orc.matmul(True, flat, lda, rows, values, scales, INT8, n, k, out, n, bias, act, scale,
                             accumulate)
@@ -84,7 +88,7 @@ def oracle_granite_block(orc, x, mats, biases, norms, dw_w, dw_b, strided, utter
     feed_forward(x, "ff1")
     h = ln(x, "norm_att")
     qkv = linear(h, t, "qkv", np.zeros((t, 3 * d), np.float32))
-    linear(qkv.reshape(-1)[2 * d:], t, "out", x, NONE, 1.0, True, lda=3 * d)
+    linear(qkv.reshape(-1)[2 * d:], t, "out", x, NONE, 1.0, True, lda=3 * d, guard=True)  # tg_matmul_device
     h = ln(x, "norm_conv")
     cc = mats["pw2"][3]
     g = linear(h, t, "pw1", np.zeros((t, 2 * cc), np.float32))
@@ -117,8 +121,8 @@ def oracle_self_conditioning(orc, x, head, head_b, mid, mid_b, fast=True):
         values, scales, n, k = name_mat
         flat = np.ascontiguousarray(a).reshape(-1)
         out = c.reshape(-1)
-        if fast:
-            rc = orc.matmul_fast(flat, k, t, values, scales, n, k, out, n, bias, NONE, 1.0, accumulate)
+        if fast:  # both products go through tg_matmul_device, whose guard applies
+            rc = orc.matmul_fast(flat, k, t, values, scales, n, k, out, n, bias, NONE, 1.0, accumulate, guard=True)
         else:
             rc = orc.matmul(True, flat, k, t, values, scales, INT8, n, k, out, n, bias, NONE, 1.0, accumulate)
         assert rc == 0

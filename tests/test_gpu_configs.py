@@ -208,16 +208,21 @@ def test_parakeet_subsampling_pw1_shape(tk, orc):
 # so the error of an output grows with kappa = max|a| sqrt(k) / ||a||_2 of its row: about 3.4 for
 # N(0, 1) rows, up to sqrt(k) for a row that is one spike. Measured on random int8 weights, the
 # row-normwise error stays below FAST_ERR_PER_KAPPA * kappa (1.4e-5 to 3.3e-5 over k = 1024 to
-# 16384 and spikes of 10 to 1000 sigma). The 1e-3 gate therefore holds up to kappa of about 28;
-# rows beyond need the exact mode (Kernels.EXACT), which gives the reference's bits.
+# 16384 and spikes of 10 to 1000 sigma), so without a guard the 1e-3 gate holds up to kappa of
+# about 28. The product entry points' accuracy guard (on by default) flags the rows whose two digits
+# drop more than 2^-12 of the row and gives them the fused reference's sums: every row then meets
+# the gate.
 FAST_ERR_PER_KAPPA = 3.5e-5
 
 
-@pytest.mark.parametrize("k,spike", [(4096, 300.0), (16384, 30.0), (16384, 300.0), (1024, 1000.0)])
-def test_rows_with_a_spike_follow_the_stated_error_bound(tk, orc, k, spike):
-    """Heavy-tailed rows (one input of `spike` sigma per row, the rest N(0, 1)): the fast path still
-    gives the integer oracle's bits, each row's error against the fused reference stays within
-    FAST_ERR_PER_KAPPA * kappa, and the exact mode gives the fused reference's bits."""
+@pytest.mark.parametrize("k,spike,epi", [(4096, 300.0, 0), (16384, 30.0, 0), (16384, 300.0, 0), (1024, 1000.0, 0),
+                                         (4096, 300.0, 1), (16384, 300.0, 1), (4096, 25.0, 0), (16384, 12.0, 1)])
+def test_rows_with_a_spike_meet_the_gate_under_the_guard(tk, orc, k, spike, epi):
+    """Heavy-tailed rows (one input of `spike` sigma per row, the rest N(0, 1)), kappa up to sqrt(k):
+    with the guard every row is within 1e-3 of the fused reference, the flagged ones bit-equal to it,
+    and the whole product equals the guarded integer oracle; with the guard off the product equals
+    the integer oracle and each row stays within FAST_ERR_PER_KAPPA * kappa; the exact mode gives the
+    fused reference's bits. epi 1: bias, SiLU, scale 0.5 and accumulation onto nonzero rows."""
     import torch
 
     import telmo_amd
@@ -227,30 +232,101 @@ def test_rows_with_a_spike_follow_the_stated_error_bound(tk, orc, k, spike):
     a = bench.synth_normal((m, k), 6000 + k)
     a[np.arange(m), rng.integers(0, k, m)] = np.float32(spike) * np.sign(rng.standard_normal(m)).astype(np.float32)
     values, scales, w = weights(tk, n, k, 6100)
-    say("spike", m, k, n, spike)
+    c0 = bench.synth_normal((m, n), 6200) if epi else np.zeros((m, n), np.float32)
+    bias = bench.synth_normal((n,), 6300) if epi else None
+    act, scale, acc = (2, 0.5, True) if epi else (0, 1.0, False)
+    e = telmo_amd.Epilogue(bias=None if bias is None else torch.from_numpy(bias).cuda(), act=telmo_amd.Act(act),
+                           scale=scale, accumulate=acc)
+    say("spike", m, k, n, spike, epi)
     ad = torch.from_numpy(a).cuda()
-    c = torch.zeros((m, n), device="cuda")
-    tk.linear_device(ad, m, w, c)
-    tk.synchronize()
-    got = c.cpu().numpy()
-    want = np.zeros(m * n, np.float32)
-    orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, want, n)
-    assert np.array_equal(got.reshape(-1).view(np.uint32), want.view(np.uint32))
-    ref = np.zeros(m * n, np.float32)
-    orc.matmul(True, a.reshape(-1), k, m, values, scales, INT8, n, k, ref, n)
+
+    def run():
+        c = torch.from_numpy(c0.copy()).cuda()
+        tk.linear_device(ad, m, w, c, e)
+        tk.synchronize()
+        return c.cpu().numpy()
+
+    def oracle(guard):
+        out = c0.copy().reshape(-1)
+        assert orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, out, n, bias, act, scale, acc,
+                               guard=guard) == 0
+        return out.reshape(m, n)
+
+    ref = c0.copy().reshape(-1)
+    orc.matmul(True, a.reshape(-1), k, m, values, scales, INT8, n, k, ref, n, bias, act, scale, acc)
     ref = ref.reshape(m, n)
+    flags = orc.guard_flags(a.reshape(-1), k, m, k).astype(bool)
     kappa = np.abs(a).max(axis=1) * np.sqrt(k) / np.linalg.norm(a.astype(np.float64), axis=1)
+
+    assert tk.guard()
+    got = run()
+    assert np.array_equal(got.view(np.uint32), oracle(True).view(np.uint32))
+    assert np.array_equal(got[flags].view(np.uint32), ref[flags].view(np.uint32))
     per_row = np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
-    print(f"[err] k={k} spike={spike}: max err {per_row.max():.2e}, kappa {kappa.min():.1f}-{kappa.max():.1f}, "
-          f"max err/kappa {(per_row / kappa).max():.2e}", flush=True)
-    assert np.all(per_row <= FAST_ERR_PER_KAPPA * kappa)
+    print(f"[err] k={k} spike={spike} epi={epi}: {flags.sum()} of {m} rows flagged (kappa "
+          f"{kappa[flags].min() if flags.any() else 0:.1f}+), max err {per_row.max():.2e}, unflagged kappa up to "
+          f"{kappa[~flags].max() if (~flags).any() else 0:.1f}", flush=True)
+    assert per_row.max() <= 1e-3
+
+    tk.set_guard(False)
+    try:
+        got = run()
+    finally:
+        tk.set_guard(True)
+    assert np.array_equal(got.view(np.uint32), oracle(False).view(np.uint32))
+    if not epi:
+        per_row = np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
+        assert np.all(per_row <= FAST_ERR_PER_KAPPA * kappa)
+
     tk.set_mode(tk.EXACT)
     try:
-        tk.linear_device(ad, m, w, c)
-        tk.synchronize()
+        got = run()
     finally:
         tk.set_mode(tk.FAST)
-    assert np.array_equal(c.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    w.close()
+
+
+def test_guard_on_the_host_and_no_allocation_entry_points(tk, orc):
+    """The host-pointer tg_linear and tg_matmul_device_noalloc apply the same guard: the guarded
+    oracle's bits, with accumulation. Rows of the decode GEMV (here 8 aligned rows of 640) are not
+    guarded: the unguarded oracle's bits."""
+    import torch
+
+    import telmo_amd
+
+    m, k, n = 64, 4096, 512
+    a = bench.synth_normal((m, k), 6400)
+    a[::3, 7] = np.float32(500.0)
+    values, scales, w = weights(tk, n, k, 6500)
+    c0 = bench.synth_normal((m, n), 6600)
+    want = c0.copy().reshape(-1)
+    orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, want, n, None, 0, 1.0, True, guard=True)
+    flags = orc.guard_flags(a.reshape(-1), k, m, k)
+    assert 0 < flags.sum() < m
+    say("guard host", m, k, n)
+    got = c0.copy()
+    tk.linear(a, m, w, got, telmo_amd.Epilogue(accumulate=True))
+    assert np.array_equal(got.reshape(-1).view(np.uint32), want.view(np.uint32))
+    say("guard noalloc", m, k, n)
+    cd = torch.from_numpy(c0.copy()).cuda()
+    tk.matmul_device_noalloc(torch.from_numpy(a).cuda(), k, m, w, cd, n, telmo_amd.Epilogue(accumulate=True))
+    tk.synchronize()
+    assert np.array_equal(cd.cpu().numpy().reshape(-1).view(np.uint32), want.view(np.uint32))
+    w.close()
+
+    m, k, n = 8, 640, 256
+    a = bench.synth_normal((m, k), 6700)
+    a[:, 5] = np.float32(3000.0)
+    values, scales, w = weights(tk, n, k, 6800)
+    assert orc.guard_flags(a.reshape(-1), k, m, k).all()
+    say("guard gemv", m, k, n)
+    cd = torch.zeros((m, n), device="cuda")
+    tk.linear_device(torch.from_numpy(a).cuda(), m, w, cd)
+    tk.synchronize()
+    want = np.zeros(m * n, np.float32)
+    orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, want, n)
+    assert np.array_equal(cd.cpu().numpy().reshape(-1).view(np.uint32), want.view(np.uint32))
     w.close()
 
 

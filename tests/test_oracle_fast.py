@@ -198,3 +198,52 @@ def test_a_misplaced_block_scale_is_caught(orc):
     assert not np.array_equal(good, bad)
     assert np.array_equal(good.reshape(m, n).view(np.uint32),
                           q8_fast_by_parts(orc, a.reshape(m, k), m, k, q, d, n).view(np.uint32))
+
+
+def test_guard_flag_threshold_is_exact(orc):
+    # e = 0 for a row whose largest value is 32639; each 0.25 has v = 0 and d = 64 (d^2 = 4096), so
+    # the row is flagged once 256 * 4096 * count > 32639^2 = 1065304321, that is from 1016 quarters.
+    for count, flagged in ((1015, 0), (1016, 1)):
+        row = np.full(1 + count, 0.25, np.float32)
+        row[0] = 32639.0
+        assert orc.row_exponent(row) == 0
+        assert orc.guard_flags(row, row.size, 1, row.size)[0] == flagged, count
+    # integers below 32640 keep every bit (d = 0): never flagged, however spiky
+    row = np.zeros(4096, np.float32)
+    row[3] = 32639.0
+    row[100:110] = 1.0
+    assert orc.guard_flags(row, row.size, 1, row.size)[0] == 0
+    # rows with a NaN or an infinity are not flagged
+    row = np.full(64, 0.3, np.float32)
+    row[1] = np.inf
+    assert orc.guard_flags(row, 64, 1, 64)[0] == 0
+
+
+def test_guard_flags_the_rows_whose_error_could_pass_the_gate(orc):
+    """The flag against the fast path's measured error: every unflagged row of spikes up to
+    sqrt(k) x is within 6e-4 of the fused reference (the gate is 1e-3); N(0, 1) rows are not
+    flagged; the guarded oracle gives flagged rows the fused reference's bits and the others the
+    integer oracle's."""
+    rng = np.random.default_rng(21)
+    for k in (1024, 4096, 16384):
+        n, m = 256, 32
+        q, s = int8_weights(rng, n, k)
+        values, scales = pack_int8(q, s)
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        spikes = [0, 0, 3, 10, 30, 100, 300, 1000] * 4
+        for r, sp in enumerate(spikes):
+            if sp:
+                a[r, rng.integers(k)] = sp * (r + 1)
+        flags = orc.guard_flags(a.reshape(-1), k, m, k).astype(bool)
+        assert not flags[0] and not flags[1]
+        fast = np.zeros(m * n, np.float32)
+        guarded = np.zeros(m * n, np.float32)
+        ref = np.zeros(m * n, np.float32)
+        orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, fast, n)
+        orc.matmul_fast(a.reshape(-1), k, m, values, scales, n, k, guarded, n, guard=True)
+        orc.matmul(True, a.reshape(-1), k, m, values, scales, 3, n, k, ref, n)
+        fast, guarded, ref = fast.reshape(m, n), guarded.reshape(m, n), ref.reshape(m, n)
+        err = np.abs(fast - ref).max(axis=1) / np.abs(ref).max(axis=1)
+        assert flags.any() and err[~flags].max() <= 6e-4, (k, err[~flags].max())
+        assert np.array_equal(guarded[flags].view(np.uint32), ref[flags].view(np.uint32))
+        assert np.array_equal(guarded[~flags].view(np.uint32), fast[~flags].view(np.uint32))
