@@ -8,24 +8,28 @@ with the entry point's accuracy guard; the staged products of quantised rows tak
 import numpy as np
 
 NONE, SILU = 0, 2
-INT8 = 3
+INT8, Q8_0 = 3, 4
 
 
-def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True):
+def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True, precision=INT8):
     """The layer on numpy rows x [t, d] (returned, x untouched): fast = True composes the integer
-    oracle (the device layer's bits), False the reference's fused f32 products."""
+    oracle (the device layer's bits), False the reference's fused f32 products. precision Q8_0 (4):
+    the matrices are Q8_0 and the feed-forward's second product goes through tg_linear_device (the
+    hidden rows in f32), as the device layer runs it."""
     x = x.copy()
     t, d = x.shape
+    q8 = precision == Q8_0
 
     def linear(a, lda, name, c, act=NONE, scale=1.0, accumulate=False, guard=False):
         values, scales, n, k = mats[name]
         flat = np.ascontiguousarray(a).reshape(-1)
         out = c.reshape(-1)
         if fast:
-            rc = orc.matmul_fast(flat, lda, t, values, scales, n, k, out, n, None, act, scale, accumulate,
-                                 guard=guard)
+            rc = (orc.matmul_fast_q8 if q8 else orc.matmul_fast)(flat, lda, t, values, scales, n, k, out, n, None,
+                                                                 act, scale, accumulate, guard=guard)
         else:
-            rc = orc.matmul(True, flat, lda, t, values, scales, INT8, n, k, out, n, None, act, scale, accumulate)
+            rc = orc.matmul(True, flat, lda, t, values, scales, precision, n, k, out, n, None, act, scale,
+                            accumulate)
         assert rc == 0
         return out.reshape(t, n)
 
@@ -36,7 +40,7 @@ def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True):
     def feed_forward(norm, w_in, w_out):
         h = ln(x, norm)
         hid = linear(h, d, w_in, np.zeros((t, mats[w_in][2]), np.float32), SILU)
-        linear(hid, hid.shape[1], w_out, x, NONE, 0.5, True)
+        linear(hid, hid.shape[1], w_out, x, NONE, 0.5, True, guard=q8)
 
     feed_forward("norm_ff1", "ff1_in", "ff1_out")
     h = ln(x, "norm_att")

@@ -23,14 +23,14 @@ def say(*args):
     print("[case]", *args, flush=True)
 
 
-def device_layer(tk, mats, norms, dw_w, dw_b):
+def device_layer(tk, mats, norms, dw_w, dw_b, precision=3):
     import torch
 
     import telmo_amd
     from telmo_amd.conformer import LayerWeights
 
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
-    W = {name: telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.INT8, v, s)
+    W = {name: telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision(precision), v, s)
          for name, (v, s, n, k) in mats.items()}
     return LayerWeights(W, {name: (dev(g), dev(b)) for name, (g, b) in norms.items()}, dev(dw_w), dev(dw_b))
 
@@ -100,3 +100,80 @@ def test_batch_of_32_utterances(tk, orc):
         rows = slice(u * frames, (u + 1) * frames)
         want = layer_oracle.oracle_layer(orc, x[rows], mats, norms, dw_w, dw_b, fast=True)
         assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32)), u
+        ref = layer_oracle.oracle_layer(orc, x[rows], mats, norms, dw_w, dw_b, fast=False)
+        err = rel_norm_err(got[rows], ref)
+        print(f"[err] utterance {u} of the 32 x 375-frame batch against the f32 reference: {err:.3e}", flush=True)
+        assert err <= 1e-3
+
+
+def test_one_600_s_utterance(tk, orc):
+    """M = 7500 rows of one utterance (config 4's layer: the 16-row-block convolution with eight rows
+    per thread, the four-row LayerNorm at 7500 rows). Only the depthwise convolution mixes rows (four
+    on either side), so windows of the output are checked against the oracle run on the window's
+    rows and four more on each side: the first, a middle and the last 256 rows."""
+    mats, norms, dw_w, dw_b = bench.layer_params(1200)
+    t, half = 7500, K // 2
+    x = bench.synth_normal((t, D), 10)
+    say("layer one utterance", t)
+    w = device_layer(tk, mats, norms, dw_w, dw_b)
+    got = run_device(tk, [w], x, 1, quantised_hidden=True)
+    close([w])
+    for r0, r1 in ((0, 256), (3700, 3956), (t - 256, t)):
+        lo, hi = max(0, r0 - half), min(t, r1 + half)
+        want = layer_oracle.oracle_layer(orc, x[lo:hi], mats, norms, dw_w, dw_b, fast=True)[r0 - lo:r1 - lo]
+        assert np.array_equal(got[r0:r1].view(np.uint32), want.view(np.uint32)), (r0, r1)
+        ref = layer_oracle.oracle_layer(orc, x[lo:hi], mats, norms, dw_w, dw_b, fast=False)[r0 - lo:r1 - lo]
+        err = rel_norm_err(got[r0:r1], ref)
+        print(f"[err] rows {r0}-{r1} of one 7500-frame utterance against the f32 reference: {err:.3e}", flush=True)
+        assert err <= 1e-3
+
+
+def test_q8_0_layer_at_750_frames(tk, orc):
+    """The layer with Q8_0 matrices (Parakeet's recommended precision): the unfused feed-forward
+    (hidden rows in f32, the second product through tg_linear_device) and pw1 + GLU (two calls), the
+    Q8_0 GEMM everywhere, against the oracle composition with the Q8_0 integer oracle."""
+    mats, norms, dw_w, dw_b = bench.layer_params(1400, precision=4)
+    x = bench.synth_normal((750, D), 15)
+    say("layer q8_0", 750)
+    w = device_layer(tk, mats, norms, dw_w, dw_b, precision=4)
+    got = run_device(tk, [w], x, 1, quantised_hidden=True)
+    close([w])
+    want = layer_oracle.oracle_layer(orc, x, mats, norms, dw_w, dw_b, fast=True, precision=4)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    ref = layer_oracle.oracle_layer(orc, x, mats, norms, dw_w, dw_b, fast=False, precision=4)
+    err = rel_norm_err(got, ref)
+    print(f"[err] the Q8_0 layer at T=750 against the f32 reference: {err:.3e}", flush=True)
+    assert err <= 1e-3
+
+
+def test_position_projection(tk, orc):
+    """The attention's position projection (Parakeet::layer's pos_proj of the relative positions,
+    conformer.py's pos branch): p_out = pos . W through tg_linear_device, with the accuracy guard."""
+    import torch
+
+    import telmo_amd
+    from telmo_amd.conformer import ConformerLayer
+
+    mats, norms, dw_w, dw_b = bench.layer_params(1600)
+    t = 300
+    q, sc = bench.synth_int8(D, D, 1650), bench.synth_scales(D, 1651)
+    pv, ps = bench.panel_layout(q, sc)
+    mats = dict(mats, pos=(pv, ps, D, D))
+    x = bench.synth_normal((t, D), 16)
+    pos = bench.synth_normal((2 * t - 1, D), 17)
+    say("layer pos", t)
+    w = device_layer(tk, mats, norms, dw_w, dw_b)
+    layer = ConformerLayer(tk, D, FF, K, t)
+    xd = torch.from_numpy(x.copy()).cuda()
+    p_out = torch.zeros((2 * t - 1, D), device="cuda")
+    layer.forward(xd, t, w, pos=torch.from_numpy(pos).cuda(), p_out=p_out)
+    tk.synchronize()
+    close([w])
+    want = np.zeros((2 * t - 1) * D, np.float32)
+    assert orc.matmul_fast(pos.reshape(-1), D, 2 * t - 1, pv, ps, D, D, want, D, guard=True) == 0
+    assert np.array_equal(p_out.cpu().numpy().reshape(-1).view(np.uint32), want.view(np.uint32))
+    # the layer's own output is unchanged by the projection
+    mats.pop("pos")
+    want_x = layer_oracle.oracle_layer(orc, x, mats, norms, dw_w, dw_b, fast=True)
+    assert np.array_equal(xd.cpu().numpy().view(np.uint32), want_x.view(np.uint32))
+    assert telmo_amd.Precision.INT8 == 3
