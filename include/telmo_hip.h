@@ -191,7 +191,9 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
 
 /* tg_linear_glu_device on quantised rows: out = glu(epi(qa . w)), the GLU in the GEMM's epilogue,
  * for a convolution module whose pointwise_conv1 input comes out of tg_layer_norm_quant_device.
- * int8 weights, n a multiple of 64, fast mode (TG_ERR_UNSUPPORTED otherwise); no accumulation. */
+ * int8 weights with n a multiple of 64; Q8_0 weights (any even n) run the product into a context
+ * buffer and then the GLU kernel, the bits of the two calls. Fast mode (TG_ERR_UNSUPPORTED
+ * otherwise); no accumulation. */
 int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                    const tg_weights *w, float *out, size_t out_len, size_t ldo,
                                    const tg_epilogue *epi);
@@ -205,7 +207,8 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
  * bytes, grown on first use. Without activation or scale the product also leaves each row's largest
  * |y| per tile column, so the quantiser streams the rows once without a reduction; from 2048 rows an
  * activation and scale are applied by the quantiser as it loads the product's biased sums, off the
- * MFMA loop. int8 weights, fast mode, no accumulation
+ * MFMA loop. Q8_0 weights run the product and then the row quantiser. int8 or Q8_0 weights, fast
+ * mode, no accumulation
  * (TG_ERR_ARG), n <= 65536. Calls on one context share the workspace; they run in order on its
  * stream. Device pointers, queued on the stream. No counterpart in the reference, whose sums are all
  * f32. */

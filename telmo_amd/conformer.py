@@ -24,8 +24,9 @@ quantised wherever the product is their only reader:
 
 Each step writes exactly the bits the unfused calls write (LayerNorm then quantise, product then
 quantise), so the layer is the reference's sequence evaluated with the fast path's products: the
-integer oracle composed in the same order reproduces it bit for bit. Q8_0 matrices take the unfused
-steps where a fused kernel is int8-only (FF in, pw1 + GLU): their f32 rows go through memory.
+integer oracle composed in the same order reproduces it bit for bit. Q8_0 matrices take the same
+entry points; for them the quantised-output product and the quantised GLU run the product into a
+context buffer and then the quantiser or the GLU kernel (the same bits as the two calls).
 Batches of equal-length utterances are stacked along the rows; only the depthwise convolution sees
 the boundaries."""
 from __future__ import annotations
@@ -101,7 +102,7 @@ class ConformerLayer:
         def feed_forward(norm, w_in, w_out):
             g, b = w.norms[norm]
             k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-            if m[w_in].precision() == Precision.INT8 and self.quantised_hidden:
+            if m[w_in].precision() in (Precision.INT8, Precision.Q8_0) and self.quantised_hidden:
                 k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, m[w_in], self.qa_ff, self.ex_ff, silu)
                 k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
             elif m[w_in].precision() == Precision.INT8:
@@ -109,7 +110,7 @@ class ConformerLayer:
                 k.matmul_quantized_device(self.qa_d, self.ex_d, t, m[w_in], hid, ff, silu)
                 k.quantize_rows_device(hid, ff, t, ff, self.qa_ff, self.ex_ff)
                 k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
-            else:  # the quantised-output product takes int8 weights: the hidden rows go through f32
+            else:  # other precisions: the hidden rows go through f32 and tg_linear_device
                 hid = self._rows("hid", ff)[:t]
                 k.matmul_quantized_device(self.qa_d, self.ex_d, t, m[w_in], hid, ff, silu)
                 k.linear_device(hid, t, m[w_out], x, half_acc)
@@ -131,7 +132,7 @@ class ConformerLayer:
         # convolution module
         g, b = w.norms["norm_conv"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-        if m["pw1"].precision() == Precision.INT8:
+        if m["pw1"].precision() in (Precision.INT8, Precision.Q8_0):
             k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], d)
         else:
             g2 = self._rows("pw1", 2 * d)[:t]

@@ -651,9 +651,12 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
     if (n % 2) return fail(ctx, TG_ERR_SHAPE, "the product's outputs must be an even count");
     if (epi && epi->accumulate) return fail(ctx, TG_ERR_ARG, "the GLU's input is not accumulated");
     if (m == 0 || n == 0) return TG_OK;
-    if (w->d.precision != TG_INT8 || w->d.k > tg::MAX_K_INT || !tg::gemm_glu_fits(n) || ctx->mode != TG_MODE_FAST)
+    const bool q8 = w->d.precision == TG_Q8_0;
+    if ((w->d.precision != TG_INT8 && !q8) || w->d.k > tg::MAX_K_INT || (!q8 && !tg::gemm_glu_fits(n)) ||
+        ctx->mode != TG_MODE_FAST)
         return fail(ctx, TG_ERR_UNSUPPORTED,
-                    "the quantised GLU product takes int8 weights, k <= 65536 and n a multiple of 64, in fast mode");
+                    "the quantised GLU product takes int8 weights with n a multiple of 64, or Q8_0 weights, k <= "
+                    "65536, in fast mode");
     if (!qa || !exps || !out) return fail(ctx, TG_ERR_NULL, "null buffer");
     if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
     if (ldo < half) return fail(ctx, TG_ERR_SHAPE, "ldo must be >= n / 2");
@@ -664,8 +667,18 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
     if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
-    TG_HIP(ctx, tg::launch_gemm_i8_glu(static_cast<const uint8_t *>(qa), exps, m, w->d, out, ldo,
+    if (q8) {
+        // Q8_0: the product's [m, n] rows through the context's buffer, then the GLU kernel (the
+        // bits of tg_matmul_quantized_device followed by tg_glu_device).
+        int rc = grow(ctx, ctx->dg, ctx->dg_cap, m * n * sizeof(float));
+        if (rc) return rc;
+        TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, ctx->dg, n,
                                        epi_args(epi, nullptr, false), ctx->stream));
+        TG_HIP(ctx, tg::launch_glu(ctx->dg, n, m, half, out, ldo, ctx->stream));
+    } else {
+        TG_HIP(ctx, tg::launch_gemm_i8_glu(static_cast<const uint8_t *>(qa), exps, m, w->d, out, ldo,
+                                           epi_args(epi, nullptr, false), ctx->stream));
+    }
     clear_error(ctx);
     return TG_OK;
 }
@@ -680,8 +693,10 @@ int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_l
     if (!ctx || !w) return fail(ctx, TG_ERR_NULL, "null context or weights");
     if (m == 0 || w->d.n == 0) return TG_OK;
     const size_t n = w->d.n;
-    if (w->d.precision != TG_INT8 || w->d.k > tg::MAX_K_INT || ctx->mode != TG_MODE_FAST)
-        return fail(ctx, TG_ERR_UNSUPPORTED, "the quantised-output product takes int8 weights with k <= 65536 in fast mode");
+    const bool q8 = w->d.precision == TG_Q8_0;
+    if ((w->d.precision != TG_INT8 && !q8) || w->d.k > tg::MAX_K_INT || ctx->mode != TG_MODE_FAST)
+        return fail(ctx, TG_ERR_UNSUPPORTED,
+                    "the quantised-output product takes int8 or Q8_0 weights with k <= 65536 in fast mode");
     if (n > tg::MAX_K_INT) return fail(ctx, TG_ERR_UNSUPPORTED, "outputs beyond the integer path's limit (65536)");
     if (!qa || !exps || !qa_out || !exps_out) return fail(ctx, TG_ERR_NULL, "null buffer");
     if (qa_len < tg_quant_bytes(m, w->d.k)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
@@ -702,7 +717,16 @@ int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_l
     const tg::EpiArgs ea = epi_args(epi, nullptr, false);
     int rc;
     if ((rc = grow(ctx, ctx->hid, ctx->hid_cap, m * ldh * sizeof(float)))) return rc;
-    if ((ea.act != tg::ACT_NONE || ea.scale != 1.0f) && m >= QOUT_ACT_ROWS) {
+    if (q8) {
+        // Q8_0: the product's rows, then the row quantiser; the activation and scale go to the
+        // quantiser from QOUT_ACT_ROWS rows as for int8.
+        const bool later = (ea.act != tg::ACT_NONE || ea.scale != 1.0f) && m >= QOUT_ACT_ROWS;
+        const tg::EpiArgs first = later ? tg::EpiArgs{ea.bias, tg::ACT_NONE, 1.0f, 0} : ea;
+        TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, ctx->hid, ldh, first,
+                                       ctx->stream));
+        TG_HIP(ctx, tg::launch_quantize_rows(ctx->hid, ldh, m, n, static_cast<uint8_t *>(qa_out), exps_out,
+                                             ctx->stream, later ? tg::RowAct{ea.act, ea.scale} : tg::RowAct{}));
+    } else if ((ea.act != tg::ACT_NONE || ea.scale != 1.0f) && m >= QOUT_ACT_ROWS) {
         // The activation and the scale are VALU work that the product's epilogue adds to its MFMA
         // loop, where it is not hidden at this many rows; the quantiser applies them to each input
         // as it loads it (the same f32 operations on the same values), under its HBM time, and the

@@ -96,10 +96,10 @@ class GraniteBlock:
         k.layer_norm_quant_device(x, d, t, d, g, b, self.eps, self.qa_d, self.ex_d)
         silu = Epilogue(bias=w.biases[which + "_up"], act=Act.SILU)
         half_acc = Epilogue(bias=w.biases[which + "_down"], scale=0.5, accumulate=True)
-        if up.precision() == Precision.INT8:
+        if up.precision() in (Precision.INT8, Precision.Q8_0):
             k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, up, self.qa_ff, self.ex_ff, silu)
             k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, down, x, d, half_acc)
-        else:  # the quantised-output product takes int8 weights: the hidden rows go through f32
+        else:  # other precisions: the hidden rows go through f32 and tg_linear_device
             hid = self._rows("hid", ff)[:t]
             k.matmul_quantized_device(self.qa_d, self.ex_d, t, up, hid, ff, silu)
             k.linear_device(hid, t, down, x, half_acc)
@@ -136,7 +136,7 @@ class GraniteBlock:
         g, b = w.norms["norm_conv"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
         pw1 = Epilogue(bias=w.biases["pw1"])
-        if m["pw1"].precision() == Precision.INT8:
+        if m["pw1"].precision() in (Precision.INT8, Precision.Q8_0):
             k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], cc, epi=pw1)
         else:
             g2 = self._rows("pw1", 2 * cc)[:t]

@@ -14,8 +14,7 @@ INT8, Q8_0 = 3, 4
 def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True, precision=INT8):
     """The layer on numpy rows x [t, d] (returned, x untouched): fast = True composes the integer
     oracle (the device layer's bits), False the reference's fused f32 products. precision Q8_0 (4):
-    the matrices are Q8_0 and the feed-forward's second product goes through tg_linear_device (the
-    hidden rows in f32), as the device layer runs it."""
+    the matrices are Q8_0 (the Q8_0 integer oracle)."""
     x = x.copy()
     t, d = x.shape
     q8 = precision == Q8_0
@@ -40,7 +39,7 @@ def oracle_layer(orc, x, mats, norms, dw_w, dw_b, utterances=1, fast=True, preci
     def feed_forward(norm, w_in, w_out):
         h = ln(x, norm)
         hid = linear(h, d, w_in, np.zeros((t, mats[w_in][2]), np.float32), SILU)
-        linear(hid, hid.shape[1], w_out, x, NONE, 0.5, True, guard=q8)
+        linear(hid, hid.shape[1], w_out, x, NONE, 0.5, True)
 
     feed_forward("norm_ff1", "ff1_in", "ff1_out")
     h = ln(x, "norm_att")

@@ -122,6 +122,39 @@ def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, wit
     w.close()
 
 
+@pytest.mark.parametrize("m,k,n,act,with_bias,scale", [(750, 1024, 4096, 2, True, 1.0), (2500, 1024, 640, 2, True, 0.5),
+                                                      (37, 96, 130, 0, False, 1.0)])
+def test_q8_0_quantised_output_and_glu_are_the_two_calls(tk, m, k, n, act, with_bias, scale):
+    """Q8_0 weights through the quantised-output product and the quantised GLU product: the product's
+    rows then the quantiser, and the product's rows then the GLU kernel, bit for bit."""
+    import torch
+
+    import telmo_amd
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(m + k + n + 5)
+    a = normal(rng, (m, k))
+    values, scales = pack_q8_0(*q8_0_weights(rng, n, k))
+    w = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.Q8_0, values, scales)
+    bias = torch.from_numpy(normal(rng, n)).cuda() if with_bias else None
+    epi = telmo_amd.Epilogue(bias=bias, act=telmo_amd.Act(act), scale=scale)
+    say("q8 qout / glu", m, k, n, act)
+    qa, ex = quantised(tk, torch.from_numpy(a).cuda(), k, m, k)
+    c = torch.zeros((m, n), device="cuda")
+    tk.matmul_quantized_device(qa, ex, m, w, c, n, epi)
+    want_qa, want_ex = quantised(tk, c, n, m, n)
+    got_qa, got_ex = torch.zeros_like(want_qa), torch.zeros_like(want_ex)
+    tk.matmul_quantized_to_quant_device(qa, ex, m, w, got_qa, got_ex, epi)
+    want_glu = torch.zeros((m, n // 2), device="cuda")
+    tk.glu_device(c, n, m, n // 2, want_glu, n // 2)
+    got_glu = torch.zeros((m, n // 2), device="cuda")
+    tk.matmul_quantized_glu_device(qa, ex, m, w, got_glu, epi=epi)
+    tk.synchronize()
+    assert torch.equal(got_ex, want_ex) and torch.equal(got_qa, want_qa)
+    assert torch.equal(got_glu.view(torch.int32), want_glu.view(torch.int32))
+    w.close()
+
+
 def test_quantised_output_product_replays_in_a_graph(tk):
     """Captured in a HIP graph and replayed, with eager work and synchronisations between the replays,
     the product gives the eager bytes every time."""

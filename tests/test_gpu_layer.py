@@ -129,9 +129,9 @@ def test_one_600_s_utterance(tk, orc):
 
 
 def test_q8_0_layer_at_750_frames(tk, orc):
-    """The layer with Q8_0 matrices (Parakeet's recommended precision): the unfused feed-forward
-    (hidden rows in f32, the second product through tg_linear_device) and pw1 + GLU (two calls), the
-    Q8_0 GEMM everywhere, against the oracle composition with the Q8_0 integer oracle."""
+    """The layer with Q8_0 matrices (Parakeet's recommended precision), the Q8_0 GEMM everywhere, the
+    quantised-output feed-forward and the quantised GLU product included, against the oracle
+    composition with the Q8_0 integer oracle."""
     mats, norms, dw_w, dw_b = bench.layer_params(1400, precision=4)
     x = bench.synth_normal((750, D), 15)
     say("layer q8_0", 750)
