@@ -359,7 +359,8 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
                          float *state, size_t state_len, float *pred, size_t pred_len, size_t *frame,
                          size_t *on_frame, tg_token *tokens, size_t cap, size_t *count);
 /* How tg_tdt_decode_device runs its steps (no counterpart in the reference, whose decode loop runs
- * on the host). Resident (the default where the network allows it: int8 matrices, vocab < 65535,
+ * on the host). Resident (the default where the network allows it: every matrix int8, or every one
+ * Q8_0, vocab < 65535,
  * the panels fit the workgroups' LDS and the device takes cooperative launches): one launch makes
  * the steps with the matrices held in LDS across the device's CUs. Otherwise each step is four
  * kernels, replayed as a graph. Both give the same tokens, states and predictions.

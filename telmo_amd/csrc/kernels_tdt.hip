@@ -551,6 +551,7 @@ struct ResMat {
     const float *scales, *bias;
     size_t panel_stride, blk_stride;
     int n, KB, P;
+    int NB;  // Q8_0: 32-input blocks (k / 32); scales [(p NB + b) 16 + j]
 };
 
 struct ResArgs {
@@ -752,6 +753,43 @@ __device__ __forceinline__ int32_t row_digits(const v4f (&x)[NC], int CK, int KB
     return e;
 }
 
+// Copies the Q8_0 block scales of np panels from p0 on into LDS (panel pi's at (pi NB + b) 16 + j).
+__device__ __forceinline__ void copy_q8_scales(float *dst, const ResMat &m, int p0, int np) {
+    const int total = np * m.NB * PANEL;
+    for (int i = threadIdx.x; i < total; i += RES_THREADS) dst[i] = m.scales[(size_t)p0 * m.NB * PANEL + i];
+}
+
+// row_sums for Q8_0 weights: the sums of each 32-input block b (k-block t = b / 2, lane groups 2 (b %
+// 2) and 2 (b % 2) + 1) as T = 256 H + L, left in tq[b 16 + j]; lanes j < 16 of wavefront 0 then fold
+// F = fmaf(d_b, T_b, F) over the NB blocks in order from +0 (the integer oracle's order) and return
+// F (other lanes: 0). ds holds the panel's block scales.
+__device__ __forceinline__ float row_fold_q8(const uint8_t *pw, int KB, int NB, const float *ds, const uint8_t *sq,
+                                             int32_t *tq) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int t = wave; t < KB; t += RES_WAVES) {
+        const gemv::v4i ahi = *reinterpret_cast<const gemv::v4i *>(sq + t * 128 + (lane >> 4) * 16);
+        const gemv::v4i alo = *reinterpret_cast<const gemv::v4i *>(sq + t * 128 + 64 + (lane >> 4) * 16);
+        const gemv::v4i wv = *reinterpret_cast<const gemv::v4i *>(pw + (size_t)t * 1024 + lane * 16);
+        int dh = 0, dl = 0;
+        dh = __builtin_amdgcn_sdot4(ahi.x, wv.x, dh, false);
+        dh = __builtin_amdgcn_sdot4(ahi.y, wv.y, dh, false);
+        dh = __builtin_amdgcn_sdot4(ahi.z, wv.z, dh, false);
+        dh = __builtin_amdgcn_sdot4(ahi.w, wv.w, dh, false);
+        dl = __builtin_amdgcn_sdot4(alo.x, wv.x, dl, false);
+        dl = __builtin_amdgcn_sdot4(alo.y, wv.y, dl, false);
+        dl = __builtin_amdgcn_sdot4(alo.z, wv.z, dl, false);
+        dl = __builtin_amdgcn_sdot4(alo.w, wv.w, dl, false);
+        dh += __shfl_xor(dh, 16, 64);  // groups 2 h' and 2 h' + 1: the 32 inputs of block 2 t + h'
+        dl += __shfl_xor(dl, 16, 64);
+        if (((lane >> 4) & 1) == 0) tq[(2 * t + (lane >> 5)) * PANEL + (lane & 15)] = dh * 256 + dl;
+    }
+    __syncthreads();
+    float f = 0.0f;
+    if (wave == 0 && lane < PANEL)
+        for (int b = 0; b < NB; b++) f = __builtin_fmaf(ds[b * PANEL + lane], (float)tq[b * PANEL + lane], f);
+    return f;
+}
+
 // The integer sums of one row (digits in sq, one-row layout) with panel pw (KB k-blocks in LDS): the
 // four wavefronts take k-blocks w, w + 4, ...; v_dot4_i32_i8 per 16-input group, the groups meet
 // across the wavefront and the wavefronts in sh.kpart. Lanes j < 16 of wavefront 0 read column j's
@@ -781,6 +819,11 @@ __device__ __forceinline__ void row_sums(const uint8_t *pw, int KB, const uint8_
     __syncthreads();
 }
 
+// Q8: every matrix is Q8_0. Its block scales sit in LDS after the digit staging (joint, each LSTM
+// layer, projection), then the one-row products' block sums (tq); the joint runs a 16x16x32 MFMA per
+// 32-input half and folds each block's sums into f32 in block order, the one-row products fold
+// theirs in row_fold_q8.
+template <bool Q8>
 __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ ResShared sh;
@@ -798,10 +841,20 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
     uint8_t *wl = wj + (size_t)a.JP * KBJ * 1024;
     uint8_t *wp = wl + (size_t)a.layers * a.LP * KBL * 1024;
     uint8_t *sq = wp + (size_t)a.PP * KBP * 1024;
+    const int NBJ = a.joint.NB, NBL = a.lstm[0].NB, NBP = a.proj.NB;
+    float *qsj = reinterpret_cast<float *>(sq + (size_t)max(KBJ4 * 2048, max(KBL, KBP) * 128));
+    float *qsl = qsj + (size_t)a.JP * NBJ * PANEL;
+    float *qsp = qsl + (size_t)a.layers * a.LP * NBL * PANEL;
+    int32_t *tq = reinterpret_cast<int32_t *>(qsp + (size_t)a.PP * NBP * PANEL);
 
     copy_panels(wj, a.joint, pj0, npj);
     for (int l = 0; l < a.layers; l++) copy_panels(wl + (size_t)l * a.LP * KBL * 1024, a.lstm[l], pl0, npl);
     copy_panels(wp, a.proj, pp0, npp);
+    if constexpr (Q8) {
+        copy_q8_scales(qsj, a.joint, pj0, npj);
+        for (int l = 0; l < a.layers; l++) copy_q8_scales(qsl + (size_t)l * a.LP * NBL * PANEL, a.lstm[l], pl0, npl);
+        copy_q8_scales(qsp, a.proj, pp0, npp);
+    }
     if (tid < npj * PANEL) {
         const int c = min(pj0 * PANEL + tid, NJ - 1);
         sh.js[tid] = a.joint.scales[c];
@@ -919,21 +972,49 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             const int orow = (lane >> 4) * 4, j16 = lane & 15;
             for (int pi = wave; pi < npj; pi += RES_WAVES) {
                 gemv::v4i hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-                const uint8_t *wb = wj + (size_t)pi * KBJ * 1024 + lane * 16;
-                // Four k-blocks' operands are read before their MFMAs, with no branch between: past
-                // KBJ the digits are zero (the weights read are the last block's, adding nothing).
-                for (int t0 = 0; t0 < KBJ4; t0 += 4) {
-                    gemv::v4i ah[4], al[4], wv[4];
+                float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (Q8) {
+                    // Half hh of k-block t is block 2 t + hh: lane 16 g + x reads 8 bytes of layout
+                    // lane 16 (2 hh + g / 2) + x, the same inputs for the digits and the weights.
+                    const uint8_t *wb = wj + (size_t)pi * KBJ * 1024;
+                    const float *ds = qsj + (size_t)pi * NBJ * PANEL + j16;
+                    const int g = lane >> 4, off0 = (16 * (g >> 1) + j16) * 16 + 8 * (g & 1);
+                    for (int t = 0; t < KBJ; t++) {
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        ah[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + lane * 16);
-                        al[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + 1024 + lane * 16);
-                        wv[u] = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)min(t0 + u, KBJ - 1) * 1024);
+                        for (int hh = 0; hh < 2; hh++) {
+                            const int bk = 2 * t + hh;
+                            if (bk < NBJ) {
+                                const int off = off0 + hh * 512;
+                                const long ah = *reinterpret_cast<const long *>(sq + t * 2048 + off);
+                                const long al = *reinterpret_cast<const long *>(sq + t * 2048 + 1024 + off);
+                                const long wv = *reinterpret_cast<const long *>(wb + (size_t)t * 1024 + off);
+                                const gemv::v4i H = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, wv, gemv::v4i{0, 0, 0, 0},
+                                                                                         0, 0, 0);
+                                const gemv::v4i L = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, wv, gemv::v4i{0, 0, 0, 0},
+                                                                                         0, 0, 0);
+                                const float d = ds[bk * PANEL];
+#pragma unroll
+                                for (int v = 0; v < 4; v++) fq[v] = __builtin_fmaf(d, (float)(H[v] * 256 + L[v]), fq[v]);
+                            }
+                        }
                     }
+                } else {
+                    const uint8_t *wb = wj + (size_t)pi * KBJ * 1024 + lane * 16;
+                    // Four k-blocks' operands are read before their MFMAs, with no branch between: past
+                    // KBJ the digits are zero (the weights read are the last block's, adding nothing).
+                    for (int t0 = 0; t0 < KBJ4; t0 += 4) {
+                        gemv::v4i ah[4], al[4], wv[4];
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[u], wv[u], hi, 0, 0, 0);
-                        lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[u], wv[u], lo, 0, 0, 0);
+                        for (int u = 0; u < 4; u++) {
+                            ah[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + lane * 16);
+                            al[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + 1024 + lane * 16);
+                            wv[u] = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)min(t0 + u, KBJ - 1) * 1024);
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[u], wv[u], hi, 0, 0, 0);
+                            lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[u], wv[u], lo, 0, 0, 0);
+                        }
                     }
                 }
                 const int col = (pj0 + pi) * PANEL + j16;
@@ -944,8 +1025,10 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                 for (int v = 0; v < 4; v++) {
                     const int r = orow + v;
                     if (r < rows && col < NJ) {
-                        float val = epilogue_vals(dequant_w(hi[v], lo[v], sh.erow[r], sc, fits), true, bs, ACT_NONE,
-                                                  1.0f, false, 0.0f);
+                        const int32_t er = sh.erow[r];
+                        const float dq = Q8 ? (er == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(fq[v], -er))
+                                            : dequant_w(hi[v], lo[v], er, sc, fits);
+                        float val = epilogue_vals(dq, true, bs, ACT_NONE, 1.0f, false, 0.0f);
                         const bool voc = col < a.vocab;
                         const int idx = voc ? col : col - a.vocab;
                         if (idx == 0 && __builtin_isnan(val)) val = __builtin_inff();
@@ -1120,14 +1203,26 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                 break;
             }
             for (int pi = 0; pi < npl; pi++) {
-                row_sums(wlay + (size_t)pi * KBL * 1024, KBL, sq, sh);
+                float fq = 0.0f;
+                if constexpr (Q8)
+                    fq = row_fold_q8(wlay + (size_t)pi * KBL * 1024, KBL, NBL,
+                                     qsl + ((size_t)l * a.LP + pi) * NBL * PANEL, sq, tq);
+                else
+                    row_sums(wlay + (size_t)pi * KBL * 1024, KBL, sq, sh);
                 if (wave == 0) {
                     const int j = lane & 15;
-                    const int32_t shi = sh.kpart[0][0][j] + sh.kpart[1][0][j] + sh.kpart[2][0][j] + sh.kpart[3][0][j];
-                    const int32_t slo = sh.kpart[0][1][j] + sh.kpart[1][1][j] + sh.kpart[2][1][j] + sh.kpart[3][1][j];
-                    const bool fits = __all(dequant_fits(shi));
-                    const float v = epilogue_vals(dequant_w(shi, slo, e, sh.ls[l][pi * PANEL + j], fits), true,
-                                                  sh.lbias[l][pi * PANEL + j], ACT_NONE, 1.0f, false, 0.0f);
+                    float dq;
+                    if constexpr (Q8) {
+                        dq = e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(fq, -e);
+                    } else {
+                        const int32_t shi =
+                            sh.kpart[0][0][j] + sh.kpart[1][0][j] + sh.kpart[2][0][j] + sh.kpart[3][0][j];
+                        const int32_t slo =
+                            sh.kpart[0][1][j] + sh.kpart[1][1][j] + sh.kpart[2][1][j] + sh.kpart[3][1][j];
+                        const bool fits = __all(dequant_fits(shi));
+                        dq = dequant_w(shi, slo, e, sh.ls[l][pi * PANEL + j], fits);
+                    }
+                    const float v = epilogue_vals(dq, true, sh.lbias[l][pi * PANEL + j], ACT_NONE, 1.0f, false, 0.0f);
                     // Output 4 u + q is gate q (i, f, g, o) of unit u: the quad's lane 0 updates the
                     // cell (src/parakeet.rs:1549-1562): c = f c + i g, h = o tanh(c).
                     const float gi = quad_lane<0>(v), gf = quad_lane<1>(v), gg = quad_lane<2>(v), go = quad_lane<3>(v);
@@ -1164,14 +1259,25 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
             const int32_t e = row_digits<1>(x, CH, KBP, sq, sh);
             if (sh.abort) break;
             for (int pi = 0; pi < npp; pi++) {
-                row_sums(wp + (size_t)pi * KBP * 1024, KBP, sq, sh);
+                float fq = 0.0f;
+                if constexpr (Q8)
+                    fq = row_fold_q8(wp + (size_t)pi * KBP * 1024, KBP, NBP, qsp + (size_t)pi * NBP * PANEL, sq, tq);
+                else
+                    row_sums(wp + (size_t)pi * KBP * 1024, KBP, sq, sh);
                 if (wave == 0 && lane < PANEL) {
                     const int col = (pp0 + pi) * PANEL + lane;
-                    const int32_t shi = sh.kpart[0][0][lane] + sh.kpart[1][0][lane] + sh.kpart[2][0][lane] + sh.kpart[3][0][lane];
-                    const int32_t slo = sh.kpart[0][1][lane] + sh.kpart[1][1][lane] + sh.kpart[2][1][lane] + sh.kpart[3][1][lane];
-                    const bool fits = __all(dequant_fits(shi));  // over the 16 active lanes
-                    const float v = epilogue_vals(dequant_w(shi, slo, e, sh.ps[pi * PANEL + lane], fits), true,
-                                                  sh.pbias[pi * PANEL + lane], ACT_NONE, 1.0f, false, 0.0f);
+                    float dq;
+                    if constexpr (Q8) {
+                        dq = e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(fq, -e);
+                    } else {
+                        const int32_t shi =
+                            sh.kpart[0][0][lane] + sh.kpart[1][0][lane] + sh.kpart[2][0][lane] + sh.kpart[3][0][lane];
+                        const int32_t slo =
+                            sh.kpart[0][1][lane] + sh.kpart[1][1][lane] + sh.kpart[2][1][lane] + sh.kpart[3][1][lane];
+                        const bool fits = __all(dequant_fits(shi));  // over the 16 active lanes
+                        dq = dequant_w(shi, slo, e, sh.ps[pi * PANEL + lane], fits);
+                    }
+                    const float v = epilogue_vals(dq, true, sh.pbias[pi * PANEL + lane], ACT_NONE, 1.0f, false, 0.0f);
                     if (col < h) {
                         sh.pst[pi * PANEL + lane] = v;
                         word_store_all(a.w_pred + (size_t)(nn & 1) * h + col, a.cs, tagged(v, nn));
@@ -1313,9 +1419,11 @@ size_t tdt_resident_words(const TdtNet &net) { return RES_COPIES * words_per_cop
 
 bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
     plan = TdtPlan{};
-    if (net.joint->precision != INT8 || net.proj->precision != INT8) return false;
+    const uint32_t prec = net.joint->precision;
+    if ((prec != INT8 && prec != Q8_0) || net.proj->precision != prec) return false;
     for (size_t l = 0; l < net.layers; l++)
-        if (net.lstm[l]->precision != INT8) return false;
+        if (net.lstm[l]->precision != prec) return false;
+    const bool q8 = prec == Q8_0;
     if (net.vocab >= 0xffff || net.h > TDT_MAX_H || net.ndur > (size_t)TDT_MAX_DURATIONS) return false;
     int dev = 0, cus = 0, coop = 0, max_lds = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1345,7 +1453,15 @@ bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan) {
     const size_t KBJ = net.joint->kb, KBL = net.lstm[0]->kb, KBP = net.proj->kb;
     p.lds = ((size_t)p.JP * KBJ + net.layers * p.LP * KBL + (size_t)p.PP * KBP) * 1024 +
             std::max(((KBJ + 3) & ~(size_t)3) * 2048, std::max(KBL, KBP) * 128);
-    const void *f = reinterpret_cast<const void *>(&tdt_resident_kernel);
+    p.q8 = q8;
+    if (q8) {
+        // The block scales of the workgroup's panels, then a one-row product's block sums.
+        const size_t NBJ = net.joint->k / Q8_BLOCK, NBL = net.lstm[0]->k / Q8_BLOCK, NBP = net.proj->k / Q8_BLOCK;
+        p.lds += ((size_t)p.JP * NBJ + net.layers * p.LP * NBL + (size_t)p.PP * NBP) * PANEL * sizeof(float) +
+                 2 * std::max(KBL, KBP) * PANEL * sizeof(int32_t);
+    }
+    const void *f = q8 ? reinterpret_cast<const void *>(&tdt_resident_kernel<true>)
+                       : reinterpret_cast<const void *>(&tdt_resident_kernel<false>);
     hipFuncAttributes fa;
     if (hipFuncGetAttributes(&fa, f) != hipSuccess || p.lds + fa.sharedSizeBytes > (size_t)max_lds) return false;
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds) != hipSuccess) return false;
@@ -1368,7 +1484,8 @@ hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &pl
                                const float *enc, size_t lde, int frames, float *state, float *pred, int32_t *tokens,
                                int cap, int steps, uint64_t wait_ticks, hipStream_t s) {
     auto mat = [](const DeviceWeights &d, const float *bias) {
-        return ResMat{d.values, d.scales, bias, d.panel_stride, d.blk_stride, (int)d.n, (int)d.kb, (int)d.panels};
+        return ResMat{d.values, d.scales, bias, d.panel_stride, d.blk_stride, (int)d.n, (int)d.kb, (int)d.panels,
+                      (int)(d.k / Q8_BLOCK)};
     };
     ResArgs a{};
     a.joint = mat(*net.joint, net.joint_b);
@@ -1407,8 +1524,9 @@ hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &pl
     a.steps = steps;
     a.wait_ticks = wait_ticks;
     void *args[] = {&a};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&tdt_resident_kernel), dim3((unsigned)plan.grid),
-                                      dim3(RES_THREADS), args, (unsigned)plan.lds, s);
+    const void *f = plan.q8 ? reinterpret_cast<const void *>(&tdt_resident_kernel<true>)
+                            : reinterpret_cast<const void *>(&tdt_resident_kernel<false>);
+    return hipLaunchCooperativeKernel(f, dim3((unsigned)plan.grid), dim3(RES_THREADS), args, (unsigned)plan.lds, s);
 }
 
 }  // namespace tg

@@ -363,9 +363,11 @@ struct TdtPlan {
     int PP = 0, GP = 0;        // projection panels per workgroup, workgroups (the first GP)
     int qoff = 0;              // the first joint / LSTM workgroup
     size_t lds = 0;            // dynamic LDS bytes per workgroup
+    bool q8 = false;           // Q8_0 matrices (their block scales in LDS too), else int8
 };
 // Whether the resident decode takes this network on the current device; fills plan and sets the
-// kernel's LDS limit. Needs int8 matrices, vocab < 65535, a cooperative launch and the panels in LDS.
+// kernel's LDS limit. Needs every matrix int8, or every one Q8_0, vocab < 65535, a cooperative
+// launch and the panels in LDS.
 bool tdt_resident_plan(const TdtNet &net, TdtPlan &plan);
 size_t tdt_resident_words(const TdtNet &net);  // 8-byte hand-over words
 // Writes the hand-over words for a decode from state and pred (tags 0; the other buffers none).

@@ -73,17 +73,15 @@ DECODE_CASES = [  # h, vocab, durations, layers, precision, frames, blank_bias, 
 @pytest.mark.parametrize("resident", [True, False], ids=["resident", "steps"])
 @pytest.mark.parametrize("case", DECODE_CASES)
 def test_decode_matches_the_oracle(tk, orc, case, resident):
-    """Both ways of running the steps: resident (int8 networks) and the graph of step kernels."""
+    """Both ways of running the steps: resident and the graph of step kernels, int8 and Q8_0."""
     import torch
 
     h, vocab, durs, layers, p, frames, blank_bias, ms = case
-    if resident and p != INT8_P:
-        pytest.skip("the resident decode takes int8 matrices")
     rng = np.random.default_rng(frames + h + layers)
     net = tdt_network(rng, h, vocab, durs, layers=layers, precision=p, max_symbols=ms, blank_bias=blank_bias)
     dec = upload(tk, net)
-    # int8 networks run resident unless told otherwise; Q8_0 ones cannot.
-    assert dec.resident == (p == INT8_P)
+    # networks run resident unless told otherwise
+    assert dec.resident
     dec.set_resident(resident)
     assert dec.resident == resident
     enc = rng.standard_normal((frames, h)).astype(np.float32)
@@ -92,6 +90,7 @@ def test_decode_matches_the_oracle(tk, orc, case, resident):
     sd, pdv = torch.from_numpy(state.copy()).cuda(), torch.from_numpy(pred.copy()).cuda()
     say("decode", case, "resident" if resident else "steps")
     toks, frame, on = dec.decode(torch.from_numpy(enc).cuda(), sd, pdv)
+    assert dec.last_resident == resident
     want, wframe, won = orc.tdt_decode(net, enc, state, pred)
     assert [tuple(t) for t in toks] == want
     assert (frame, on) == (wframe, won)
