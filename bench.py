@@ -29,6 +29,8 @@ The JSON line also carries:
                 profiles/ (FETCH_SIZE and WRITE_SIZE scaled by a copy kernel's reading).
   encoder       24 layers at M = 12000 (32 utterances of 30 s) and M = 7500 (one 600 s utterance):
                 audio-seconds per second.
+  granite       Granite's 16-block encoder (blocks 0 and 1 strided, the self-conditioning) on 60 s.
+  timed_s_total the seconds inside every timed region of the run (HIP events).
   gemv, tdt     the decoder's GEMVs on the HBM roofline and the greedy TDT decode.
   vendor        the same product shapes on hipBLASLt (int8 over both digit planes: the same MFMA work)
                 and torch's bf16 / f16 GEMMs, for scale.
@@ -219,6 +221,10 @@ def close_layer(w):
         m.close()
 
 
+# Seconds inside every timed region of the run (HIP events), reported as timed_s_total.
+TIMED_S = [0.0]
+
+
 def timed_on(stream, fn, reps):
     """Mean ms per call of fn over reps calls, HIP events on `stream` around them."""
     import torch
@@ -230,6 +236,7 @@ def timed_on(stream, fn, reps):
         fn(i)
     e1.record(stream)
     torch.cuda.synchronize()
+    TIMED_S[0] += e0.elapsed_time(e1) * 1e-3
     return e0.elapsed_time(e1) / reps
 
 
@@ -298,14 +305,15 @@ def gpu_leg(args, params, x0_host):
     glu = torch.zeros((T, D), device="cuda")
     silu, half_acc, acc = Epilogue(act=Act.SILU), Epilogue(scale=0.5, accumulate=True), Epilogue(accumulate=True)
     hid = torch.zeros((T, FF), device="cuda")
+    # FF in as the step runs it: the quantised-output product (the product, then the quantiser of its rows).
     launches = {
-        "ff1_in": lambda i: kern.matmul_quantized_device(qa_d, ex_d, T, m["ff1_in"], hid, FF, silu),
+        "ff1_in": lambda i: kern.matmul_quantized_to_quant_device(qa_d, ex_d, T, m["ff1_in"], qa_o, ex_o, silu),
         "ff1_out": lambda i: kern.matmul_quantized_device(qa_h, ex_h, T, m["ff1_out"], c, D, half_acc),
         "qkv": lambda i: kern.matmul_quantized_device(qa_d, ex_d, T, m["qkv"], qkv, 3 * D),
         "out": lambda i: kern.matmul_quantized_device(qa_d, ex_d, T, m["out"], c, D, acc),
         "pw1": lambda i: kern.matmul_quantized_glu_device(qa_d, ex_d, T, m["pw1"], glu, D),
         "pw2": lambda i: kern.matmul_quantized_device(qa_d, ex_d, T, m["pw2"], c, D, acc),
-        "ff2_in": lambda i: kern.matmul_quantized_device(qa_d, ex_d, T, m["ff2_in"], hid, FF, silu),
+        "ff2_in": lambda i: kern.matmul_quantized_to_quant_device(qa_d, ex_d, T, m["ff2_in"], qa_o, ex_o, silu),
         "ff2_out": lambda i: kern.matmul_quantized_device(qa_h, ex_h, T, m["ff2_out"], c, D, half_acc),
     }
     per_shape = []
@@ -360,7 +368,8 @@ def encoder_leg(args):
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
-    layers = [upload_layer(kern, layer_params(5000 + 97 * i)) for i in range(ENC_LAYERS)]
+    host = [layer_params(5000 + 97 * i) for i in range(ENC_LAYERS)]
+    layers = [upload_layer(kern, p) for p in host]
     wbytes = sum(m.bytes() for w in layers for m in w.mats.values())
     stack = ConformerLayer(kern, D, FF, DW_KERNEL, max(rows for _, rows, _, _ in ENC_CASES))
     out = []
@@ -386,6 +395,83 @@ def encoder_leg(args):
         del x0, x
     for w in layers:
         close_layer(w)
+    kern.close()
+    return out, host
+
+
+# Granite Speech 5's encoder (src/granite.rs:606-650): 16 blocks, 0 and 1 strided, the
+# self-conditioning after block 7 (layers / 2 - 1). 60 s of audio: 3000 rows into block 0, 750 out.
+G_BLOCKS, G_STRIDED, G_SELFCOND, G_ROWS = 16, (0, 1), 7, 3000
+
+
+def granite_ops(rows):
+    """2 m n k of one pass's products: the blocks at their row counts and the self-conditioning."""
+    ops, t = 0, rows
+    for i in range(G_BLOCKS):
+        n = t // 2 if i in G_STRIDED else t
+        for name, k, nout in G_PRODUCTS:
+            m = n if name in ("pw2", "ff2_up", "ff2_down") else t
+            ops += 2 * m * k * nout
+        if i == G_SELFCOND:
+            ops += 2 * 2 * n * G_D * G_VOCAB
+        t = n
+    return ops
+
+
+def granite_leg(args):
+    """Granite's encoder on the device (telmo_amd.granite): 16 blocks with their own int8 weights from
+    telmo's generator (blocks 0 and 1 strided), the self-conditioning after block 7, over 3000 rows
+    (60 s of audio) of N(0, 1) input; the attention core is the V third of qkv as in the Parakeet
+    leg. One pass timed eagerly (the strided blocks allocate their outputs), median of 5."""
+    import torch
+
+    import telmo_amd
+    from telmo_amd.granite import GraniteBlock, self_conditioning
+
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    kern = telmo_amd.Kernels(0, stream=stream.cuda_stream)
+    blocks = [upload_granite_block(kern, granite_block_params(9000 + 53 * i, i in G_STRIDED))
+              for i in range(G_BLOCKS)]
+    head, head_b, mid, mid_b = granite_head_params(9900)
+    H = telmo_amd.PackedWeights.from_parts(kern, head[2], head[3], telmo_amd.Precision.INT8, head[0], head[1])
+    M = telmo_amd.PackedWeights.from_parts(kern, mid[2], mid[3], telmo_amd.Precision.INT8, mid[0], mid[1])
+    hb, mb = torch.from_numpy(head_b).cuda(), torch.from_numpy(mid_b).cuda()
+    blk = GraniteBlock(kern, G_D, G_FF, G_CC, G_KERNEL, G_ROWS)
+    x0 = torch.from_numpy(synth_normal((G_ROWS, G_D), 9950)).cuda()
+    bufs = [torch.empty((G_ROWS // 2, G_D), device="cuda"), torch.empty((G_ROWS // 4, G_D), device="cuda")]
+    logits = torch.empty(G_ROWS // 4 * G_VOCAB, device="cuda")
+    x = torch.empty_like(x0)
+
+    def run(_):
+        x.copy_(x0)
+        cur, t = x, G_ROWS
+        for i, w in enumerate(blocks):
+            cur, t = blk.forward(cur, t, w, out=bufs[i] if i in G_STRIDED else None)
+            if i == G_SELFCOND:
+                self_conditioning(kern, cur, t, H, hb, M, mb, logits)
+        return cur
+
+    for i in range(2):
+        run(i)
+    times = [timed_on(stream, run, 1) for _ in range(5)]
+    ms = float(np.median(times))
+    y = run(0)
+    kern.synchronize()
+    if not torch.isfinite(y).all():
+        raise RuntimeError("the Granite encoder output is not finite")
+    ops = granite_ops(G_ROWS)
+    wbytes = sum(m.bytes() for w in blocks for m in w.mats.values()) + H.bytes() + M.bytes()
+    out = {"workload": f"Granite encoder, {G_BLOCKS} blocks (0, 1 strided) and the self-conditioning, "
+                       f"{G_ROWS} input rows (60 s audio), d {G_D}, ff {G_FF}, conv {G_CC}, vocab {G_VOCAB}, int8",
+           "ms_per_pass": round(ms, 3), "audio_s_per_s": round(60.0 / (ms * 1e-3), 1),
+           "tops": round(ops / (ms * 1e-3) / 1e12, 1), "frac_int8_peak": round(ops / (ms * 1e-3) / PEAK_INT8, 4),
+           "ops_per_pass": ops, "weights_mb": round(wbytes / 1e6, 1),
+           "timing": "HIP events around one eager pass, median of 5"}
+    for w in blocks:
+        close_layer(w)
+    H.close()
+    M.close()
     kern.close()
     return out
 
@@ -603,10 +689,12 @@ def host_cpu():
     return {"model": model, "logical_cpus_usable": len(os.sched_getaffinity(0)), "isa_flags": isa}
 
 
-def cpu_leg(params, x0_host, budget_s):
+def cpu_leg(params, x0_host, budget_s, enc_params=None):
     """telmo's SIMD + pool path (the C++ port) on the same bytes: the eight products of the layer on
-    every host core and on one thread (best of 5 rounds each), and the decode joint GEMV (m = 1) on
-    all cores with its weights rotated over copies larger than the host's caches."""
+    every host core and on one thread (best of 5 rounds each), the decode joint GEMV (m = 1) on all
+    cores with its weights rotated over copies larger than the host's caches, and (enc_params: the 24
+    layers' parameters of the GPU encoder leg) one pass of the 24 layers' products over 750 rows,
+    best of 3."""
     from oracle import oracle as orc
 
     L = orc.cpubase()
@@ -629,8 +717,8 @@ def cpu_leg(params, x0_host, budget_s):
     srcs = {"ff1_in": x, "ff1_out": h, "qkv": x, "pw1": x, "pw2": u, "ff2_in": x, "ff2_out": h}
     p = lambda arr: arr.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
 
-    def gemm(pool, name, act, scale, accumulate):
-        values, scales, n, k = mats[name]
+    def gemm(pool, name, act, scale, accumulate, mats_of=None):
+        values, scales, n, k = (mats_of or mats)[name]
         if name == "out":  # the V third of QKV: rows 3D apart, starting at column 2D
             a_ptr, lda = ctypes.c_void_p(qkv.ctypes.data + 4 * 2 * D), 3 * D
         else:
@@ -640,9 +728,9 @@ def cpu_leg(params, x0_host, budget_s):
                          out.size, n, None, 0, 2 if act == "silu" else 0, scale, int(accumulate))
         assert rc == 0, rc
 
-    def layer(pool):
+    def layer(pool, mats_of=None):
         for name, k, n, act, scale, accumulate in PRODUCTS:
-            gemm(pool, name, act, scale, accumulate)
+            gemm(pool, name, act, scale, accumulate, mats_of)
 
     # Bit-identity with the fused oracle before timing (FF1 in on the layer input).
     pool = L.cb_pool_new(cores)
@@ -688,6 +776,15 @@ def cpu_leg(params, x0_host, budget_s):
         for cv in copies:
             L.cb_matmul(pool, isa, p(a), k, k, 1, p(cv), p(js), 3, n, k, p(c), n, n, None, 0, 0, 1.0, 0)
         gemv_best = min(gemv_best, (time.perf_counter() - t0) / len(copies))
+    enc = None
+    if enc_params:
+        enc = float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            x[:] = x0_host
+            for lp in enc_params:
+                layer(pool, lp[0])
+            enc = min(enc, time.perf_counter() - t0)
     L.cb_pool_free(pool)
     return {"value": round(ops_of(T) / best / 1e12, 4), "unit": "TOPS", "cores": cores,
             "kind": "port", "isa": "avx512" if isa == 2 else "avx2", "host": host_cpu(),
@@ -701,9 +798,12 @@ def cpu_leg(params, x0_host, budget_s):
             "gemv_rotating": {"gemv": "joint 640 -> 8198, m = 1", "copies": len(copies),
                               "copy_mb": round(jbytes / 1e6, 2), "us": round(gemv_best * 1e6, 1),
                               "gb_s": round(jbytes / gemv_best / 1e9, 2), "cores": cores},
-            "encoder_audio_s_per_s": round(T * 0.08 / (ENC_LAYERS * best), 1),
-            "encoder_note": f"{ENC_LAYERS} layers of these products per {T} frames (80 ms each): the CPU path's "
-                            "encoder audio-seconds per second, GEMMs only, scaled from the sample"}
+            "encoder_audio_s_per_s": None if enc is None else round(T * 0.08 / enc, 1),
+            "encoder_ms_per_pass": None if enc is None else round(enc * 1e3, 1),
+            "encoder_note": f"one pass of {ENC_LAYERS} layers' products (each layer its own weights, those of the "
+                            f"GPU encoder leg) over {T} frames (80 ms each, 60 s of audio) on {cores} threads, best "
+                            "of 3, measured: the CPU path's encoder audio-seconds per second, GEMMs only (the "
+                            "LayerNorms, GLU and convolution are not ported)"}
 
 
 # The TDT decoder of Parakeet: h = 640, vocab 8193 (blank last) + 5 durations, 2 LSTM layers.
@@ -711,20 +811,26 @@ TDT_H, TDT_VOCAB, TDT_DURS, TDT_MAX_SYMBOLS = 640, 8193, [0, 1, 2, 3, 4], 10
 TDT_BLANK_BIAS = 28.0  # on random weights: blank runs between tokens
 
 
-def tdt_network(seed=21):
-    """A random int8 network of Parakeet's decoder shapes in the panel layout (numpy), from telmo's
-    generator: int8 weights with per-output scales in [lo, hi), N(0, 1) biases and embedding."""
+def tdt_network(seed=21, precision=3):
+    """A random network of Parakeet's decoder shapes in the panel layout (numpy), from telmo's
+    generator: int8 weights with per-output scales in [lo, hi) (precision 3), or the same int8 values
+    with f16-exact scales in [lo, hi) per 32 inputs of each output (Q8_0, precision 4); N(0, 1)
+    biases and embedding."""
     h, vocab = TDT_H, TDT_VOCAB
     seeds = iter(range(seed * 100, seed * 100 + 100))
 
     def mat(n, k, lo, hi):
         q = synth_int8(n, k, next(seeds))
+        if precision == 4:
+            values, _ = panel_layout(q, np.ones(n, np.float32))
+            d = lo + (hi - lo) * synth_u01(-(-n // 16) * 16 * (k // 32), next(seeds))
+            return values, d.astype(np.float16).astype(np.float32)
         return panel_layout(q, (lo + (hi - lo) * synth_u01(n, next(seeds))).astype(np.float32))
 
     outputs = vocab + len(TDT_DURS)
     joint_b = (0.5 * synth_normal((outputs,), next(seeds))).astype(np.float32)
     joint_b[vocab - 1] += TDT_BLANK_BIAS
-    return {"p": 3, "h": h, "vocab": vocab, "durations": TDT_DURS, "max_symbols": TDT_MAX_SYMBOLS,
+    return {"p": precision, "h": h, "vocab": vocab, "durations": TDT_DURS, "max_symbols": TDT_MAX_SYMBOLS,
             "joint": mat(outputs, h, 0.001, 0.01), "joint_b": joint_b,
             "emb": (0.5 * synth_normal((vocab, h), next(seeds))).astype(np.float32),
             "lstm": [mat(4 * h, 2 * h, 0.0004, 0.0008) for _ in range(2)],
@@ -742,7 +848,7 @@ def tdt_leg(args, net, enc_host):
 
     kern = telmo_amd.Kernels(0)
     h, vocab = net["h"], net["vocab"]
-    P = telmo_amd.Precision.INT8
+    P = telmo_amd.Precision(net["p"])
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
     joint = telmo_amd.PackedWeights.from_parts(kern, vocab + len(TDT_DURS), h, P, *net["joint"])
     lstm = [telmo_amd.PackedWeights.from_parts(kern, 4 * h, 2 * h, P, *w) for w in net["lstm"]]
@@ -777,7 +883,7 @@ def tdt_leg(args, net, enc_host):
     frames = enc_host.shape[0]
     weight_bytes = joint.bytes() + sum(w.bytes() for w in lstm) + proj.bytes()
     out = {"workload": f"greedy TDT decode, {frames} frames (60 s audio), h={h}, vocab {vocab} + "
-                       f"{len(TDT_DURS)} durations, 2 LSTM layers, int8",
+                       f"{len(TDT_DURS)} durations, 2 LSTM layers, {'Q8_0' if net['p'] == 4 else 'int8'}",
            "frames": frames, "tokens": len(toks), "tokens_per_frame": round(len(toks) / frames, 3),
            "ms_per_decode": round(ms, 3), "us_per_token": round(ms * 1e3 / max(len(toks), 1), 2),
            "audio_s_per_s": round(60.0 / (ms * 1e-3), 1), "decoder_weight_mb": round(weight_bytes / 1e6, 2),
@@ -970,6 +1076,7 @@ def main():
     ap.add_argument("--no-q8", action="store_true")
     ap.add_argument("--no-tdt", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
+    ap.add_argument("--no-granite", action="store_true")
     ap.add_argument("--shape", type=int, nargs=3, metavar=("M", "K", "N"),
                     help="time one product shape alone (the program for per-shape rocprofv3 runs) and exit")
     ap.add_argument("--gemv", type=int, nargs=3, metavar=("M", "K", "N"),
@@ -1000,7 +1107,8 @@ def main():
                 "traffic": traffic.get("traffic_bytes_per_launch") if traffic else None,
                 "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of these launches, committed in "
                                   "profiles/layer_T750_traffic.json (not measured in this run)" if traffic else None,
-                "kernel": "the eight products' GEMM kernels of the layer step, each launched alone",
+                "kernel": "the eight products of the layer step as it runs them, each launched alone (FF in: the "
+                          "quantised-output product and its row quantiser)",
                 "dominant": dominant["product"],
                 "avg_launch_us": round(gemm_us / len(per_shape), 3), "ops_per_launch_avg": ops / len(per_shape),
                 "note": "two int8 digits per activation: the MFMAs execute 2x the algorithmic ops, so the "
@@ -1009,15 +1117,18 @@ def main():
                 "per_shape": per_shape, "row_kernels_us": row_us}
     gemv = None if args.no_gemv else gemv_leg(args)
     host = host_leg(params, x0)
-    encoder = None if args.no_encoder else encoder_leg(args)
+    encoder, enc_params = (None, None) if args.no_encoder else encoder_leg(args)
+    granite = None if args.no_granite else granite_leg(args)
     q8 = None if args.no_q8 else q8_leg(args)
     tdt = None
     if not args.no_tdt:
         net = tdt_network()
         enc = synth_normal((T_FRAMES, TDT_H), 22)
         tdt, gpu_toks = tdt_leg(args, net, enc)
+        if q8 is not None:
+            q8["tdt"], _ = tdt_leg(args, tdt_network(precision=4), enc)
     vendor = None if args.no_vendor else vendor_leg()
-    cpu = None if args.no_cpu else cpu_leg(params, x0, args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_leg(params, x0, args.cpu_seconds, enc_params)
     if cpu is not None and tdt is not None:
         cpu["tdt_decode"], port_toks, oracle_toks = cpu_tdt(net, enc, 150)
         if port_toks is not None:
@@ -1044,9 +1155,11 @@ def main():
         "gemv": gemv,
         "pcie_inclusive": host,
         "encoder": encoder,
+        "granite": granite,
         "q8_0": q8,
         "tdt": tdt,
         "vendor": vendor,
+        "timed_s_total": round(TIMED_S[0], 3),
     }
     print(json.dumps(line))
 
