@@ -873,6 +873,7 @@ def tdt_leg(args, net, enc_host):
 
     resident = dec.resident
     ms, toks, state_r = timed()
+    steps_one = dec.last_steps if resident else None
     steps_ms = None
     if resident:  # the same decode as a graph of step kernels, for comparison
         dec.set_resident(False)
@@ -882,12 +883,37 @@ def tdt_leg(args, net, enc_host):
         dec.set_resident(True)
     frames = enc_host.shape[0]
     weight_bytes = joint.bytes() + sum(w.bytes() for w in lstm) + proj.bytes()
+    # Several streams of 60 s each in one resident launch (config 5's M concurrent streams), each
+    # with encoder rows of its own; the first stream's are the single decode's.
+    multi = []
+    if resident and net["p"] == 3:
+        for m in (4, 8):
+            encs = [enc] + [dev(synth_normal(enc_host.shape, 2300 + q)) for q in range(1, m)]
+            times, got = [], None
+            for _ in range(4):
+                sts = [state0.clone() for _ in range(m)]
+                prs = [pred0.clone() for _ in range(m)]
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                got = dec.decode_streams(encs, sts, prs)
+                times.append(time.perf_counter() - t0)
+            if got[0][0] != toks:
+                raise RuntimeError("the multi-stream decode's first stream differs from the single decode")
+            mms = float(np.median(times[1:])) * 1e3
+            ntok = sum(len(g[0]) for g in got)
+            steps = dec.last_steps
+            multi.append({"streams": m, "ms_per_decode": round(mms, 3), "steps": steps,
+                          "us_per_step": round(mms * 1e3 / max(steps, 1), 2), "tokens": ntok,
+                          "tokens_per_s": round(ntok / (mms * 1e-3), 1),
+                          "audio_s_per_s": round(60.0 * m / (mms * 1e-3), 1)})
     out = {"workload": f"greedy TDT decode, {frames} frames (60 s audio), h={h}, vocab {vocab} + "
                        f"{len(TDT_DURS)} durations, 2 LSTM layers, {'Q8_0' if net['p'] == 4 else 'int8'}",
            "frames": frames, "tokens": len(toks), "tokens_per_frame": round(len(toks) / frames, 3),
            "ms_per_decode": round(ms, 3), "us_per_token": round(ms * 1e3 / max(len(toks), 1), 2),
            "audio_s_per_s": round(60.0 / (ms * 1e-3), 1), "decoder_weight_mb": round(weight_bytes / 1e6, 2),
            "resident": resident,
+           "steps": steps_one, "us_per_step": None if not steps_one else round(ms * 1e3 / steps_one, 2),
+           "multi_stream": multi,
            "step_kernels_ms_per_decode": None if steps_ms is None else round(steps_ms, 3),
            "step_kernels_us_per_token": None if steps_ms is None else round(steps_ms * 1e3 / max(len(toks), 1), 2),
            "timing": "wall clock around tg_tdt_decode_device (blocks until the decode ends), median of 5; "

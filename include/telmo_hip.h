@@ -376,6 +376,34 @@ int tg_tdt_is_resident(const tg_tdt *tdt);
  * tg_tdt_last_resident: 1 when the last tg_tdt_decode_device on this network ran resident, 0 when
  * it ran on the step kernels, -1 before the first. */
 int tg_tdt_last_resident(const tg_tdt *tdt);
+/* Steps the last resident decode on this network made (one step scores one window of frames). */
+size_t tg_tdt_last_steps(const tg_tdt *tdt);
+
+/* One stream of tg_tdt_decode_streams_device: tg_tdt_decode_device's arguments for that stream. */
+typedef struct {
+    const float *enc_proj; /* device, frames rows of hidden floats at stride lde */
+    size_t enc_len, lde, frames;
+    float *state;          /* device, updated in place */
+    size_t state_len;
+    float *pred;           /* device, updated in place */
+    size_t pred_len;
+    size_t frame, on_frame; /* in: where the stream's loop starts; out: where it stopped */
+    tg_token *tokens;      /* host, cap entries */
+    size_t cap;
+    size_t count;          /* out: the tokens the stream emitted */
+} tg_tdt_stream;
+/* m independent greedy decodes (streams; parakeet.rs:1412-1513 per stream, as a caller decoding
+ * several utterances at once calls decode_inner for each), each giving exactly what
+ * tg_tdt_decode_device gives for it. Up to 8 streams run resident in one launch (no counterpart in
+ * the reference): the joint scores 16 / m frames of each stream's window per step, each stream's
+ * window is walked on its own, and the streams that emitted a token run the prediction network
+ * together as rows of one MFMA product with the matrices in LDS, so a step costs about what one
+ * stream's step costs. More than 8 streams go in groups of 8. Without the resident multi-stream
+ * decode (Q8_0 or mixed matrices, the device's resident lock held elsewhere, tg_tdt_set_resident(0),
+ * one stream) the streams are decoded one after another. tg_tdt_last_resident then reports 2 for a
+ * multi-stream launch. Streams must not share state or pred. Blocks until every stream ends; on an
+ * error (tokens past cap: TG_ERR_SHAPE) the other streams' results are still written. */
+int tg_tdt_decode_streams_device(tg_ctx *ctx, tg_tdt *tdt, tg_tdt_stream *streams, size_t m);
 /* Limits of the resident decode (no counterpart in the reference; for tests and tuning): the most
  * steps one launch makes before the host looks at the control block and relaunches (1 to 16384; 0
  * restores 16384), and the longest one workgroup waits for another, in microseconds (0 restores

@@ -24,6 +24,13 @@ class Token(ctypes.Structure):
     _fields_ = [("id", ctypes.c_uint32), ("frame", ctypes.c_uint32), ("duration", ctypes.c_uint32)]
 
 
+class TdtStream(ctypes.Structure):
+    """tg_tdt_stream."""
+    _fields_ = [("enc_proj", _p), ("enc_len", _sz), ("lde", _sz), ("frames", _sz), ("state", _p), ("state_len", _sz),
+                ("pred", _p), ("pred_len", _sz), ("frame", _sz), ("on_frame", _sz), ("tokens", _p), ("cap", _sz),
+                ("count", _sz)]
+
+
 _szp = ctypes.POINTER(_sz)
 
 # name: (restype, argtypes), in the order of include/telmo_hip.h
@@ -75,6 +82,8 @@ SIGNATURES = {
     "tg_tdt_set_resident": (ctypes.c_int, [_p, _p, ctypes.c_int]),
     "tg_tdt_is_resident": (ctypes.c_int, [_p]),
     "tg_tdt_last_resident": (ctypes.c_int, [_p]),
+    "tg_tdt_last_steps": (_sz, [_p]),
+    "tg_tdt_decode_streams_device": (ctypes.c_int, [_p, _p, _p, _sz]),
     "tg_tdt_set_resident_limits": (ctypes.c_int, [_p, _p, _u32, ctypes.c_uint64]),
     "tg_pack_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_p)]),
     "tg_pack_from_bytes": (ctypes.c_int, [_p, _sz, ctypes.POINTER(_p)]),

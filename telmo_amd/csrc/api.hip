@@ -11,6 +11,7 @@
 // quantiser then the MFMA GEMM, whose kernel launch_gemm_i8 picks by shape. The exact mode, other
 // precisions and longer inputs run the exact kernel.
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -95,6 +96,13 @@ struct tg_tdt {
     int launch_steps = TDT_RESIDENT_STEPS;  // steps per resident launch
     // Whether the last tg_tdt_decode_device ran resident (1), by the step kernels (0), or none yet (-1).
     int last_resident = -1;
+    // The multi-stream decode's control blocks (TDT_MAX_STREAMS, device and pinned), its hand-over
+    // words and the streams' entry states and predictions (restored when a launch fails), made on
+    // its first call.
+    tg::TdtCtl *mctl = nullptr, *mctl_host = nullptr;
+    uint64_t *mwords = nullptr;
+    float *mscratch = nullptr;
+    uint32_t last_steps = 0;  // steps of the last resident decode (one or several streams)
 };
 
 
@@ -999,6 +1007,10 @@ void tdt_release(tg_tdt *t) {
     if (t->partials) (void)hipFree(t->partials);
     if (t->tokens) (void)hipFree(t->tokens);
     if (t->words) (void)hipFree(t->words);
+    if (t->mctl) (void)hipFree(t->mctl);
+    if (t->mctl_host) (void)hipHostFree(t->mctl_host);
+    if (t->mwords) (void)hipFree(t->mwords);
+    if (t->mscratch) (void)hipFree(t->mscratch);
     delete t;
 }
 
@@ -1124,6 +1136,7 @@ int tg_tdt_create(tg_ctx *ctx, const tg_tdt_desc *desc, tg_tdt **out) {
         t->wait_ticks = (uint64_t)khz * 1000;  // one second
         t->launch_steps = TDT_RESIDENT_STEPS;
         t->can_resident = t->use_resident = true;
+        (void)tg::tdt_multi_plan(net, t->plan);
     }
     (void)hipGetLastError();  // a refused LDS attribute or occupancy query leaves the step kernels
     std::memset(t->ctl_host, 0, sizeof(tg::TdtCtl));
@@ -1260,6 +1273,7 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
                 return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
             }
         }
+        tdt->last_steps = hc->step;
         return tdt_results(ctx, tdt, hc, frame, on_frame, tokens, cap, count);
     }
     // Steps run as a captured graph of TDT_GRAPH_STEPS steps, replayed in growing batches between
@@ -1300,6 +1314,173 @@ int tg_tdt_decode_device(tg_ctx *ctx, tg_tdt *tdt, const float *enc_proj, size_t
     return tdt_results(ctx, tdt, hc, frame, on_frame, tokens, cap, count);
 }
 
+int tg_tdt_decode_streams_device(tg_ctx *ctx, tg_tdt *tdt, tg_tdt_stream *streams, size_t m) {
+    if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
+    if (m == 0) return TG_OK;
+    if (!streams) return fail(ctx, TG_ERR_NULL, "null streams");
+    if (tdt->device != ctx->device) return fail(ctx, TG_ERR_ARG, "the network lives on another device");
+    if (m > tg::TDT_MAX_STREAMS) {  // in groups of TDT_MAX_STREAMS
+        for (size_t q0 = 0; q0 < m; q0 += tg::TDT_MAX_STREAMS) {
+            const size_t n = m - q0 < tg::TDT_MAX_STREAMS ? m - q0 : tg::TDT_MAX_STREAMS;
+            const int rc = tg_tdt_decode_streams_device(ctx, tdt, streams + q0, n);
+            if (rc) return rc;
+        }
+        return TG_OK;
+    }
+    const tg::TdtNet &net = tdt->net;
+    const size_t per_frame = net.max_symbols > 1 ? net.max_symbols : 1;
+    size_t most[tg::TDT_MAX_STREAMS] = {}, total = 0, bound = 0;
+    bool any = false;
+    for (size_t q = 0; q < m; q++) {
+        tg_tdt_stream &st = streams[q];
+        st.count = 0;
+        if (!st.state || !st.pred || (st.cap && !st.tokens)) return fail(ctx, TG_ERR_NULL, "null argument");
+        if (st.frames >= ((size_t)1 << 24)) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^24 frames");
+        if (st.frame >= st.frames) continue;  // the reference's loop does not start
+        if (!st.enc_proj) return fail(ctx, TG_ERR_NULL, "enc_proj is null");
+        if (st.lde < net.h || st.lde % 4) return fail(ctx, TG_ERR_SHAPE, "lde must be >= hidden and a multiple of 4");
+        if (st.enc_len < span(st.frames, st.lde, net.h)) return fail(ctx, TG_ERR_SHAPE, "enc_proj is too short");
+        if (st.state_len < net.layers * 2 * net.h) return fail(ctx, TG_ERR_SHAPE, "state is too short");
+        if (st.pred_len < net.h) return fail(ctx, TG_ERR_SHAPE, "pred is too short");
+        if (!aligned16(st.enc_proj) || !aligned16(st.state) || !aligned16(st.pred))
+            return fail(ctx, TG_ERR_ALIGN, "enc_proj, state and pred must be 16-byte aligned");
+        if (st.on_frame > (size_t)INT32_MAX) return fail(ctx, TG_ERR_ARG, "on_frame out of range");
+        most[q] = (st.frames - st.frame) * per_frame;
+        if (most[q] >= ((size_t)1 << 30)) return fail(ctx, TG_ERR_UNSUPPORTED, "too many possible tokens");
+        total += most[q];
+        bound = std::max(bound, (st.frames - st.frame) * (per_frame + 1) + 1);
+        any = true;
+    }
+    if (!any) return TG_OK;
+    // The streams' states must not share memory: each stream's launch writes its own.
+    for (size_t q = 0; q < m; q++)
+        for (size_t r = q + 1; r < m; r++)
+            if (streams[q].frame < streams[q].frames && streams[r].frame < streams[r].frames &&
+                (streams[q].state == streams[r].state || streams[q].pred == streams[r].pred))
+                return fail(ctx, TG_ERR_ARG, "two streams share a state or prediction");
+    {
+        std::unique_lock<std::mutex> g(ctx->mu);
+        std::unique_lock<std::mutex> rlock;
+        if (tdt->use_resident && tdt->plan.multi && m > 1 && ctx->device >= 0 && ctx->device < MAX_DEVICES)
+            rlock = std::unique_lock<std::mutex>(resident_mu[ctx->device], std::try_to_lock);
+        if (rlock.owns_lock()) {
+            TG_HIP(ctx, hipSetDevice(ctx->device));
+            const size_t sw = net.layers * 2 * net.h, M = tg::TDT_MAX_STREAMS;
+            if (!tdt->mctl) {
+                if (hipMalloc(&tdt->mctl, M * sizeof(tg::TdtCtl)) != hipSuccess ||
+                    hipHostMalloc(&tdt->mctl_host, M * sizeof(tg::TdtCtl), hipHostMallocDefault) != hipSuccess ||
+                    hipMalloc(&tdt->mwords, tg::tdt_multi_words(net) * sizeof(uint64_t)) != hipSuccess ||
+                    hipMalloc(&tdt->mscratch, M * (sw + net.h) * sizeof(float)) != hipSuccess)
+                    return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+            }
+            if (total > tdt->tokens_cap) {
+                TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+                if (tdt->tokens) TG_HIP(ctx, hipFree(tdt->tokens));
+                tdt->tokens = nullptr;
+                tdt->tokens_cap = 0;
+                if (hipMalloc(&tdt->tokens, total * 3 * sizeof(int32_t)) != hipSuccess)
+                    return fail(ctx, TG_ERR_NOMEM, "device allocation failed");
+                tdt->tokens_cap = total;
+            }
+            // Streams that start past their frames take no part: the launch sees the others only.
+            size_t idx[tg::TDT_MAX_STREAMS], k = 0, off = 0;
+            tg::TdtStream ts[tg::TDT_MAX_STREAMS];
+            size_t toff[tg::TDT_MAX_STREAMS];
+            for (size_t q = 0; q < m; q++) {
+                if (streams[q].frame >= streams[q].frames) continue;
+                idx[k] = q;
+                toff[k] = off;
+                ts[k] = tg::TdtStream{streams[q].enc_proj, streams[q].lde, (int)streams[q].frames, streams[q].state,
+                                      streams[q].pred, tdt->tokens + off * 3, (int)most[q]};
+                off += most[q];
+                k++;
+            }
+            tg::TdtCtl *hc = tdt->mctl_host;
+            TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            std::memset(hc, 0, M * sizeof(tg::TdtCtl));
+            uint32_t preds[tg::TDT_MAX_STREAMS] = {};
+            for (size_t j = 0; j < k; j++) {
+                hc[j].t = (int32_t)streams[idx[j]].frame;
+                hc[j].on_frame = (int32_t)streams[idx[j]].on_frame;
+                hc[j].rows = tg::TDT_ROWS;
+            }
+            TG_HIP(ctx, hipMemcpyAsync(tdt->mctl, hc, M * sizeof(tg::TdtCtl), hipMemcpyHostToDevice, ctx->stream));
+            for (size_t j = 0; j < k; j++) {
+                float *sc = tdt->mscratch + j * (sw + net.h);
+                TG_HIP(ctx, hipMemcpyAsync(sc, ts[j].state, sw * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+                TG_HIP(ctx, hipMemcpyAsync(sc + sw, ts[j].pred, net.h * sizeof(float), hipMemcpyDeviceToDevice,
+                                           ctx->stream));
+            }
+            auto restore = [&]() {
+                for (size_t j = 0; j < k; j++) {
+                    const float *sc = tdt->mscratch + j * (sw + net.h);
+                    (void)hipMemcpyAsync(ts[j].state, sc, sw * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+                    (void)hipMemcpyAsync(ts[j].pred, sc + sw, net.h * sizeof(float), hipMemcpyDeviceToDevice,
+                                         ctx->stream);
+                }
+                (void)hipStreamSynchronize(ctx->stream);
+            };
+            TG_HIP(ctx, tg::launch_tdt_multi_init(net, tdt->mwords, k, ts, preds, ctx->stream));
+            tdt->last_resident = 2;
+            size_t steps = 0;
+            while (true) {
+                const hipError_t e = tg::launch_tdt_multi(tdt->mctl, net, tdt->plan, tdt->mwords, k, ts,
+                                                          tdt->launch_steps, tdt->wait_ticks, ctx->stream);
+                if (e != hipSuccess) {
+                    restore();
+                    return hip_fail(ctx, e, "the multi-stream decode's launch");
+                }
+                TG_HIP(ctx, hipMemcpyAsync(hc, tdt->mctl, M * sizeof(tg::TdtCtl), hipMemcpyDeviceToHost, ctx->stream));
+                TG_HIP(ctx, hipStreamSynchronize(ctx->stream));
+                if (hc[0].err) {
+                    restore();
+                    return fail(ctx, TG_ERR_HIP,
+                                "the multi-stream decode: a workgroup's wait passed its deadline (states and "
+                                "predictions restored)");
+                }
+                bool done = true;
+                for (size_t j = 0; j < k; j++) done = done && hc[j].done;
+                if (done) break;
+                steps += (size_t)tdt->launch_steps;
+                if (steps > bound) {
+                    restore();
+                    return fail(ctx, TG_ERR_HIP, "the decode did not finish within its step bound");
+                }
+            }
+            tdt->last_steps = hc[0].step;
+            int rc = TG_OK;
+            for (size_t j = 0; j < k; j++) {
+                tg_tdt_stream &st = streams[idx[j]];
+                const size_t n = (size_t)hc[j].ntok, copy = n < st.cap ? n : st.cap;
+                st.frame = (size_t)hc[j].t;
+                st.on_frame = (size_t)hc[j].on_frame;
+                st.count = n;
+                if (copy) {
+                    std::vector<int32_t> buf(copy * 3);
+                    TG_HIP(ctx, hipMemcpy(buf.data(), tdt->tokens + toff[j] * 3, copy * 3 * sizeof(int32_t),
+                                          hipMemcpyDeviceToHost));
+                    for (size_t i = 0; i < copy; i++)
+                        st.tokens[i] = tg_token{(uint32_t)buf[3 * i], (uint32_t)buf[3 * i + 1], (uint32_t)buf[3 * i + 2]};
+                }
+                if (n > st.cap && rc == TG_OK)
+                    rc = fail(ctx, TG_ERR_SHAPE, "tokens holds " + std::to_string(st.cap) +
+                                                     " entries and the decode emitted " + std::to_string(n));
+            }
+            if (rc == TG_OK) clear_error(ctx);
+            return rc;
+        }
+    }
+    // One stream at a time (resident where it can, else by the step kernels): the same results.
+    for (size_t q = 0; q < m; q++) {
+        tg_tdt_stream &st = streams[q];
+        const int rc = tg_tdt_decode_device(ctx, tdt, st.enc_proj, st.enc_len, st.lde, st.frames, st.state,
+                                            st.state_len, st.pred, st.pred_len, &st.frame, &st.on_frame, st.tokens,
+                                            st.cap, &st.count);
+        if (rc) return rc;
+    }
+    return TG_OK;
+}
+
 int tg_tdt_set_resident(tg_ctx *ctx, tg_tdt *tdt, int on) {
     if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");
     if (on && !tdt->can_resident)
@@ -1313,6 +1494,8 @@ int tg_tdt_set_resident(tg_ctx *ctx, tg_tdt *tdt, int on) {
 int tg_tdt_is_resident(const tg_tdt *tdt) { return tdt && tdt->use_resident ? 1 : 0; }
 
 int tg_tdt_last_resident(const tg_tdt *tdt) { return tdt ? tdt->last_resident : -1; }
+
+size_t tg_tdt_last_steps(const tg_tdt *tdt) { return tdt ? tdt->last_steps : 0; }
 
 int tg_tdt_set_resident_limits(tg_ctx *ctx, tg_tdt *tdt, uint32_t steps_per_launch, uint64_t wait_us) {
     if (!ctx || !tdt) return fail(ctx, TG_ERR_NULL, "null context or network");

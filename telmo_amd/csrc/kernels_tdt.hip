@@ -1338,6 +1338,643 @@ __global__ void tdt_resident_init_kernel(uint64_t *words, int h, int layers, con
     }
 }
 
+
+// ------------------------------------------------------------------------ the multi-stream decode
+//
+// M independent greedy decodes (streams: each its own encoder rows, frames, state, prediction and
+// tokens) in one cooperative launch, the matrices held in LDS as in tdt_resident_kernel and the
+// same tagged words between workgroups. The streams move in lockstep, one step for all: the joint
+// scores the TDT_ROWS row slots, TDT_ROWS / M (the stream's "slots") for each stream's window; the
+// decider walks each stream's window on its own and publishes one decision per stream; the streams
+// that emitted a token then run the prediction network together, as rows of an MFMA product (row j
+// is the j-th emitting stream), so a step costs about what one stream's step costs. Each stream's
+// words carry its own prediction count as tag, the step's words the step. int8 matrices.
+constexpr int MS_MAX = (int)TDT_MAX_STREAMS;
+
+struct MultiArgs {
+    ResMat joint, proj, lstm[TDT_MAX_LAYERS];
+    const float *emb;
+    const float *enc[MS_MAX];
+    size_t lde[MS_MAX];
+    int frames[MS_MAX];
+    int32_t *tokens[MS_MAX];
+    int cap[MS_MAX];
+    float *state[MS_MAX], *pred[MS_MAX];
+    TdtCtl *ctl;  // ctl[s]: stream s's position; ctl[0].step the steps made, ctl[0].err the error flag
+    const int32_t *durations;
+    // One copy of the words: predictions [2][M][h], LSTM outputs [layers][2][M][h], the joint's
+    // best entries per row slot [2][TDT_ROWS][RES_MAX_GRID] and duration entries
+    // [2][TDT_ROWS][TDT_ROWS] (first copy only), decisions [2][M][RES_DEC].
+    uint64_t *w_pred, *w_h, *w_part, *w_dur, *w_dec;
+    size_t cs;
+    int M, slots, h, vocab, ndur, layers, blank, max_symbols;
+    int JP, GJ, LP, GL, PP, GP, qoff, grid;
+    int steps;
+    uint64_t wait_ticks;
+};
+
+struct MultiShared {
+    float js[RES_MAX_PANELS * PANEL], jbias[RES_MAX_PANELS * PANEL];
+    float ps[RES_MAX_PANELS * PANEL], pbias[RES_MAX_PANELS * PANEL];
+    float ls[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL], lbias[TDT_MAX_LAYERS][RES_MAX_PANELS * PANEL];
+    Key red[RES_WAVES][TDT_ROWS], dred[RES_WAVES][TDT_ROWS];
+    Key cand[RES_THREADS / 16], dcand[RES_THREADS / 16];
+    int32_t erow[TDT_ROWS];
+    int live[TDT_ROWS];  // row slot holds a frame of a stream's window
+    int tok_s[TDT_ROWS], dur_s[TDT_ROWS], durs[TDT_MAX_DURATIONS];
+    // The streams' positions (t, on_frame, tokens emitted, window rows, done) and prediction counts.
+    int st[MS_MAX][5];
+    uint32_t n[MS_MAX], pin_n[MS_MAX];
+    int dec[MS_MAX][RES_DEC];
+    int emit[MS_MAX], nemit;
+    int abort;
+};
+
+__device__ __forceinline__ void ms_fail(const MultiArgs &a, MultiShared &sh) {
+    sh.abort = 1;
+    store_i(&a.ctl[0].err, 1);
+}
+
+// Rows j < E of an MFMA product's input, k = 4 CK inputs in chunks of four: thread t takes chunks
+// t and t + 256 of every row. src(j, c, x) gives chunk c of row j: true when it is read from memory
+// into x, false when it is four hand-over words, src_words(j, c) and src_tag(j, c) telling where and
+// with which tag. Every word of every row is waited for in one round of loads, so the rows cost one
+// memory round trip together. Then each row's exponent (a workgroup reduction per row) and its
+// digits in the 16-row layout (k-block t, digit d at sq + t 2048 + d 1024, lane 16 g + j), zero up
+// to KB k-blocks; the exponents go to sh.erow. False when a wait fails.
+template <typename SRC, typename WORDS, typename TAG>
+__device__ __forceinline__ bool rows_digits(int E, int CK, int KB, uint8_t *sq, MultiShared &sh, const int32_t *err,
+                                            uint64_t ticks, SRC src, WORDS src_words, TAG src_tag) {
+    constexpr int NI = 2;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    v4f x[MS_MAX][NI];
+    uint64_t need = 0;
+#pragma unroll
+    for (int j = 0; j < MS_MAX; j++)
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int c = tid + RES_THREADS * i;
+            x[j][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (j < E && c < CK && !src(j, c, x[j][i])) need |= 0xfull << (4 * (j * NI + i));
+        }
+    const uint64_t deadline = (uint64_t)wall_clock64() + ticks;
+    bool ok = true;
+    for (int round = 0; need; round++) {
+#pragma unroll
+        for (int j = 0; j < MS_MAX; j++)
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int b4 = 4 * (j * NI + i);
+                if ((need >> b4) & 0xf) {
+                    const uint64_t *wp = src_words(j, tid + RES_THREADS * i);
+                    const uint32_t tg = src_tag(j, tid + RES_THREADS * i);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if ((need >> (b4 + q)) & 1) {
+                            const uint64_t w = word_load(wp + q);
+                            if ((uint32_t)(w >> 32) == tg) {
+                                x[j][i][q] = word_value(w);
+                                need &= ~(1ull << (b4 + q));
+                            }
+                        }
+                    }
+                }
+            }
+        if (need && (round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(err) != 0)) {
+            ok = false;
+            break;
+        }
+    }
+    __shared__ uint32_t s_rmax[RES_WAVES][MS_MAX];
+#pragma unroll
+    for (int j = 0; j < MS_MAX; j++) {
+        if (j < E) {  // uniform
+            uint32_t mx = 0;
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                if (tid + RES_THREADS * i < CK) mx = max(mx, chunk_max(x[j][i]));
+            mx = gemv::wave_max_u(mx);
+            if (lane == 0) s_rmax[wave][j] = mx;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < MS_MAX; j++) {
+        if (j < E) {
+            const uint32_t m = max(max(s_rmax[0][j], s_rmax[1][j]), max(s_rmax[2][j], s_rmax[3][j]));
+            const int32_t e = m == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(m));
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int c = tid + RES_THREADS * i;
+                if (c < KB * 16) {
+                    uint32_t hi, lo;
+                    digits4(x[j][i].x, x[j][i].y, x[j][i].z, x[j][i].w, e, hi, lo);
+                    uint8_t *d = sq + (c >> 4) * 2048 + ((c & 15) >> 2) * 256 + j * 16 + (c & 3) * 4;
+                    *reinterpret_cast<uint32_t *>(d) = hi;
+                    *reinterpret_cast<uint32_t *>(d + 1024) = lo;
+                }
+            }
+            if (tid == 0) sh.erow[j] = e;
+        }
+    }
+    return ok;
+}
+
+// The integer sums of the 16 rows in sq with one panel of KB k-blocks in LDS (one wavefront).
+__device__ __forceinline__ void rows_sums(const uint8_t *pw, int KB, const uint8_t *sq, gemv::v4i &hi, gemv::v4i &lo) {
+    const int lane = threadIdx.x & 63;
+    hi = gemv::v4i{0, 0, 0, 0};
+    lo = gemv::v4i{0, 0, 0, 0};
+    for (int t = 0; t < KB; t++) {
+        const gemv::v4i ah = *reinterpret_cast<const gemv::v4i *>(sq + t * 2048 + lane * 16);
+        const gemv::v4i al = *reinterpret_cast<const gemv::v4i *>(sq + t * 2048 + 1024 + lane * 16);
+        const gemv::v4i wv = *reinterpret_cast<const gemv::v4i *>(pw + (size_t)t * 1024 + lane * 16);
+        hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, wv, hi, 0, 0, 0);
+        lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, wv, lo, 0, 0, 0);
+    }
+}
+
+__global__ __launch_bounds__(RES_THREADS) void tdt_multi_kernel(MultiArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ MultiShared sh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x;
+    const size_t rc = (size_t)(b % RES_COPIES) * a.cs;
+    const int M = a.M, S = a.slots, h = a.h, NJ = a.joint.n, KBJ = a.joint.KB, KBL = a.lstm[0].KB, KBP = a.proj.KB;
+    const int KBJ4 = (KBJ + 3) & ~3;
+    const int bq = b - a.qoff;
+    const int pj0 = bq * a.JP, npj = bq >= 0 && bq < a.GJ ? min(a.JP, a.joint.P - pj0) : 0;
+    const int pl0 = bq * a.LP, npl = bq >= 0 && bq < a.GL ? min(a.LP, a.lstm[0].P - pl0) : 0;
+    const int pp0 = b * a.PP, npp = b < a.GP ? min(a.PP, a.proj.P - pp0) : 0;
+    const int jd0 = (a.vocab / PANEL) / a.JP, nd = ((NJ - 1) / PANEL) / a.JP - jd0 + 1;
+    const int32_t *err = &a.ctl[0].err;
+    uint8_t *wj = lds;
+    uint8_t *wl = wj + (size_t)a.JP * KBJ * 1024;
+    uint8_t *wp = wl + (size_t)a.layers * a.LP * KBL * 1024;
+    uint8_t *sq = wp + (size_t)a.PP * KBP * 1024;
+    float *pin = reinterpret_cast<float *>(sq + (size_t)max(KBJ4, max(KBL, KBP)) * 2048);  // [M][h]
+    float *hst = pin + (size_t)M * h;                                                       // [layers][M][LP 4]
+    float *cst = hst + (size_t)a.layers * M * a.LP * 4;
+    float *pst = cst + (size_t)a.layers * M * a.LP * 4;  // [M][PP 16]
+    const int U = a.LP * 4;
+
+    copy_panels(wj, a.joint, pj0, npj);
+    for (int l = 0; l < a.layers; l++) copy_panels(wl + (size_t)l * a.LP * KBL * 1024, a.lstm[l], pl0, npl);
+    copy_panels(wp, a.proj, pp0, npp);
+    if (tid < npj * PANEL) {
+        const int c = min(pj0 * PANEL + tid, NJ - 1);
+        sh.js[tid] = a.joint.scales[c];
+        sh.jbias[tid] = a.joint.bias[c];
+    }
+    if (tid < npl * PANEL) {
+        for (int l = 0; l < a.layers; l++) {
+            sh.ls[l][tid] = a.lstm[l].scales[pl0 * PANEL + tid];
+            sh.lbias[l][tid] = a.lstm[l].bias[pl0 * PANEL + tid];
+        }
+    }
+    for (int i = tid; i < a.layers * M * U; i += RES_THREADS) {
+        const int l = i / (M * U), s = (i / U) % M, ul = i % U;
+        if (ul < npl * 4) {
+            hst[i] = a.state[s][(size_t)l * 2 * h + pl0 * 4 + ul];
+            cst[i] = a.state[s][(size_t)l * 2 * h + h + pl0 * 4 + ul];
+        }
+    }
+    if (tid < npp * PANEL) {
+        const int c = min(pp0 * PANEL + tid, h - 1);
+        sh.ps[tid] = a.proj.scales[c];
+        sh.pbias[tid] = a.proj.bias[c];
+    }
+    for (int i = tid; i < M * a.PP * PANEL; i += RES_THREADS) {
+        const int s = i / (a.PP * PANEL), ci = i % (a.PP * PANEL);
+        if (ci < npp * PANEL) pst[i] = a.pred[s][min(pp0 * PANEL + ci, h - 1)];
+    }
+    if (tid < a.ndur) sh.durs[tid] = a.durations[tid];
+    if (tid < M) {
+        const TdtCtl &c = a.ctl[tid];
+        sh.st[tid][0] = c.t;
+        sh.st[tid][1] = c.on_frame;
+        sh.st[tid][2] = c.ntok;
+        sh.st[tid][3] = min(c.rows, S);
+        sh.st[tid][4] = c.done || c.t >= a.frames[tid];
+        sh.n[tid] = c.preds;
+        sh.pin_n[tid] = TAG_NONE;
+    }
+    if (tid == 0) sh.abort = 0;
+    uint32_t s = a.ctl[0].step;
+    const uint32_t s_end = s + (uint32_t)a.steps;
+    const int CH = h >> 2;
+    __syncthreads();
+
+    while (s != s_end) {
+        bool any = false;
+        for (int q = 0; q < M; q++) any = any || !sh.st[q][4];
+        if (!any) break;
+        const uint32_t par = s & 1;
+        if (tid < TDT_ROWS) {
+            const int q = tid / S, r = tid % S;
+            sh.live[tid] = q < M && !sh.st[q][4] && r < sh.st[q][3];
+        }
+        // ---- The joint over each stream's window rows.
+        if (npj > 0) {
+            // The live streams' predictions, waited for only after they change, all in one round of
+            // loads: thread t takes values t + 256 i (i < 4, h <= 992) of each such stream.
+            uint32_t want = 0;
+            for (int q = 0; q < M; q++)
+                if (!sh.st[q][4] && sh.pin_n[q] != sh.n[q]) want |= 1u << q;  // uniform
+            if (want) {
+                uint32_t need = 0;
+#pragma unroll
+                for (int q = 0; q < MS_MAX; q++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if ((want >> q & 1) && tid + RES_THREADS * i < h) need |= 1u << (4 * q + i);
+                const uint64_t deadline = (uint64_t)wall_clock64() + a.wait_ticks;
+                for (int round = 0; need; round++) {
+#pragma unroll
+                    for (int q = 0; q < MS_MAX; q++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (need >> (4 * q + i) & 1) {
+                                const uint32_t nq = sh.n[q];
+                                const int v = tid + RES_THREADS * i;
+                                const uint64_t w = word_load(a.w_pred + rc + ((size_t)(nq & 1) * M + q) * h + v);
+                                if ((uint32_t)(w >> 32) == nq) {
+                                    pin[(size_t)q * h + v] = word_value(w);
+                                    need &= ~(1u << (4 * q + i));
+                                }
+                            }
+                    if (need && (round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(err) != 0)) {
+                        ms_fail(a, sh);
+                        break;
+                    }
+                }
+                __syncthreads();
+                if (tid < M && (want >> tid & 1)) sh.pin_n[tid] = sh.n[tid];
+            }
+            __syncthreads();
+            if (sh.abort) break;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = wave + 4 * j;  // the row slot
+                if (sh.live[r]) {
+                    const int q = r / S, rr = r % S, f = min(sh.st[q][0] + rr, a.frames[q] - 1);
+                    const float *er = a.enc[q] + (size_t)f * a.lde[q];
+                    const float *pr = pin + (size_t)q * h;
+                    v4f z[4];
+                    uint32_t mx = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int c = lane + 64 * i;
+                        z[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                        if (c < CH) {
+                            const v4f e = *reinterpret_cast<const v4f *>(er + 4 * c);
+                            const v4f pv = *reinterpret_cast<const v4f *>(pr + 4 * c);
+                            z[i].x = fmaxf(e.x + pv.x, 0.0f);
+                            z[i].y = fmaxf(e.y + pv.y, 0.0f);
+                            z[i].z = fmaxf(e.z + pv.z, 0.0f);
+                            z[i].w = fmaxf(e.w + pv.w, 0.0f);
+                            mx = max(mx, chunk_max(z[i]));
+                        }
+                    }
+                    const uint32_t m = gemv::wave_max_u(mx);
+                    const int32_t ex = m == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(m));
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int c = lane + 64 * i;
+                        if (c < KBJ4 * 16) {
+                            uint32_t hi, lo;
+                            digits4(z[i].x, z[i].y, z[i].z, z[i].w, ex, hi, lo);
+                            uint8_t *d = sq + (c >> 4) * 2048 + ((c & 15) >> 2) * 256 + r * 16 + (c & 3) * 4;
+                            *reinterpret_cast<uint32_t *>(d) = hi;
+                            *reinterpret_cast<uint32_t *>(d + 1024) = lo;
+                        }
+                    }
+                    if (lane == 0) sh.erow[r] = ex;
+                }
+            }
+            __syncthreads();
+            Key mine[4], dmine[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) mine[v] = dmine[v] = Key{0u, 0xffffffffu};
+            const int orow = (lane >> 4) * 4, j16 = lane & 15;
+            for (int pi = wave; pi < npj; pi += RES_WAVES) {
+                gemv::v4i hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+                const uint8_t *wb = wj + (size_t)pi * KBJ * 1024 + lane * 16;
+                for (int t0 = 0; t0 < KBJ4; t0 += 4) {
+                    gemv::v4i ah[4], al[4], wv[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        ah[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + lane * 16);
+                        al[u] = *reinterpret_cast<const gemv::v4i *>(sq + (t0 + u) * 2048 + 1024 + lane * 16);
+                        wv[u] = *reinterpret_cast<const gemv::v4i *>(wb + (size_t)min(t0 + u, KBJ - 1) * 1024);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[u], wv[u], hi, 0, 0, 0);
+                        lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[u], wv[u], lo, 0, 0, 0);
+                    }
+                }
+                const int col = (pj0 + pi) * PANEL + j16;
+                const float sc = sh.js[pi * PANEL + j16], bs = sh.jbias[pi * PANEL + j16];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = orow + v;
+                    if (sh.live[r] && col < NJ) {
+                        float val = epilogue_vals(dequant(hi[v], lo[v], sh.erow[r], sc), true, bs, ACT_NONE, 1.0f,
+                                                  false, 0.0f);
+                        const bool voc = col < a.vocab;
+                        const int idx = voc ? col : col - a.vocab;
+                        if (idx == 0 && __builtin_isnan(val)) val = __builtin_inff();
+                        const uint32_t key = order_key(val);
+                        Key &m = voc ? mine[v] : dmine[v];
+                        if (key > m.k) m = Key{key, (uint32_t)idx};
+                    }
+                }
+            }
+            const bool has_dur = bq >= jd0 && bq < jd0 + nd;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                mine[v] = fold16(mine[v]);
+                if (has_dur) dmine[v] = fold16(dmine[v]);
+                if (j16 == 0) {
+                    sh.red[wave][orow + v] = mine[v];
+                    sh.dred[wave][orow + v] = dmine[v];
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < TDT_ROWS) {
+            Key x{0u, 0xffffffffu}, xd{0u, 0xffffffffu};
+            if (npj > 0) {
+#pragma unroll
+                for (int q = 0; q < RES_WAVES; q++) {
+                    if (better(sh.red[q][tid], x)) x = sh.red[q][tid];
+                    if (better(sh.dred[q][tid], xd)) xd = sh.dred[q][tid];
+                }
+            }
+            word_store(a.w_part + ((size_t)par * TDT_ROWS + tid) * RES_MAX_GRID + b, tagged_key(x, s));
+            if (bq >= jd0 && bq < jd0 + nd)
+                word_store(a.w_dur + ((size_t)par * TDT_ROWS + tid) * TDT_ROWS + (bq - jd0), tagged_key(xd, s));
+        }
+        // ---- The decisions: workgroup 0 gathers every slot's words (sixteen threads a slot) and walks
+        // each stream's window.
+        if (b == 0) {
+            const int g = RES_THREADS / TDT_ROWS, r = tid / g, j = tid - r * g;
+            const bool live = sh.live[r];
+            const uint64_t *pb = a.w_part + ((size_t)par * TDT_ROWS + r) * RES_MAX_GRID + j;
+            const uint64_t *pd = a.w_dur + ((size_t)par * TDT_ROWS + r) * TDT_ROWS + min(j, TDT_ROWS - 1);
+            uint64_t pw[16], dw = 0;
+            uint32_t pneed = 0;
+            bool dneed = live && j < nd;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (live && j + g * u < a.grid) pneed |= 1u << u;
+            const uint64_t deadline = (uint64_t)wall_clock64() + a.wait_ticks;
+            for (int round = 0;; round++) {
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (pneed >> u & 1) pw[u] = word_load(pb + g * u);
+                if (dneed) dw = word_load(pd);
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if ((pneed >> u & 1) && (uint32_t)(pw[u] >> 48) == (s & 0xffffu)) pneed &= ~(1u << u);
+                if (dneed && (uint32_t)(dw >> 48) == (s & 0xffffu)) dneed = false;
+                if (!pneed && !dneed) break;
+                if ((round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(err) != 0)) {
+                    ms_fail(a, sh);
+                    break;
+                }
+            }
+            Key x{0u, 0xffffffffu}, xd{0u, 0xffffffffu};
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                if (live && j + g * u < a.grid) {
+                    const Key y = key_of(pw[u]);
+                    if (better(y, x)) x = y;
+                }
+            }
+            if (live && j < nd) xd = key_of(dw);
+            x = fold16(x);
+            xd = fold16(xd);
+            if ((lane & 15) == 0) {
+                sh.cand[tid >> 4] = x;
+                sh.dcand[tid >> 4] = xd;
+            }
+            __syncthreads();
+            if (tid < TDT_ROWS) {
+                const Key bx = sh.cand[tid], bd = sh.dcand[tid];
+                sh.tok_s[tid] = bx.i == 0xffffffffu ? 0 : (int)bx.i;
+                sh.dur_s[tid] = sh.durs[bd.i == 0xffffffffu ? 0 : bd.i];
+            }
+            __syncthreads();
+            if (sh.abort) break;
+            if (tid < M) {
+                int *d = sh.dec[tid];
+                if (sh.st[tid][4]) {
+                    d[0] = sh.st[tid][0];
+                    d[1] = sh.st[tid][1];
+                    d[2] = sh.st[tid][2];
+                    d[3] = -1;
+                    d[4] = sh.st[tid][3];
+                    d[5] = 1;
+                } else {
+                    const Walked wk = walk_window(sh.st[tid][0], sh.st[tid][3], sh.st[tid][1], sh.st[tid][2],
+                                                  sh.tok_s + tid * S, sh.dur_s + tid * S, a.blank, a.frames[tid],
+                                                  a.max_symbols, a.tokens[tid], a.cap[tid], true);
+                    d[0] = wk.t;
+                    d[1] = wk.on;
+                    d[2] = wk.ntok;
+                    d[3] = wk.token;
+                    d[4] = min(wk.rows, S);
+                    d[5] = wk.done;
+                }
+            }
+            __syncthreads();
+            for (int i = tid; i < RES_COPIES * M * RES_DEC; i += RES_THREADS) {
+                const int c = i / (M * RES_DEC), k = i % (M * RES_DEC);
+                word_store(a.w_dec + (size_t)c * a.cs + (size_t)par * M * RES_DEC + k,
+                           tagged(__int_as_float(sh.dec[k / RES_DEC][k % RES_DEC]), s));
+            }
+        } else {
+            if (tid < M * RES_DEC) {
+                const uint64_t *p[1] = {a.w_dec + rc + (size_t)par * M * RES_DEC + tid};
+                const uint32_t tag[1] = {s};
+                uint64_t w[1];
+                if (!wait_words<1>(p, 1u, tag, w, err, (uint64_t)wall_clock64() + a.wait_ticks)) ms_fail(a, sh);
+                sh.dec[tid / RES_DEC][tid % RES_DEC] = __float_as_int(word_value(w[0]));
+            }
+            __syncthreads();
+            if (sh.abort) break;
+        }
+        if (tid < M) {
+            // A stream ends when its frames are used up, whether a blank or a token's duration took
+            // it there (the reference's loop runs while t < frames).
+            sh.st[tid][0] = sh.dec[tid][0];
+            sh.st[tid][1] = sh.dec[tid][1];
+            sh.st[tid][2] = sh.dec[tid][2];
+            sh.st[tid][3] = sh.dec[tid][4];
+            sh.st[tid][4] = sh.dec[tid][5] || sh.dec[tid][0] >= a.frames[tid];
+        }
+        if (tid == 0) {
+            int e = 0;
+            for (int q = 0; q < M; q++)
+                if (sh.dec[q][3] >= 0) sh.emit[e++] = q;
+            sh.nemit = e;
+        }
+        __syncthreads();
+        s++;
+        const int E = sh.nemit;
+        if (E == 0) continue;
+
+        // ---- The prediction network for the E emitting streams, row j the j-th of them.
+        bool stop = false;
+        for (int l = 0; l < a.layers && !stop; l++) {
+            if (npl == 0) continue;
+            const uint8_t *wlay = wl + (size_t)l * a.LP * KBL * 1024;
+            // Row j: [x; h_l] of the j-th emitting stream: x the embedding row of its token (layer 0) or
+            // the new h of the layer below (tag n + 1), h_l its layer's h (tag n).
+            auto src = [&](int j, int c, v4f &x) -> bool {
+                if (l == 0 && c < CH) {
+                    x = *reinterpret_cast<const v4f *>(a.emb + (size_t)sh.dec[sh.emit[j]][3] * h + 4 * c);
+                    return true;
+                }
+                return false;
+            };
+            auto words = [&](int j, int c) -> const uint64_t * {
+                const int q = sh.emit[j];
+                const uint32_t nq = sh.n[q];
+                return c < CH ? a.w_h + rc + (((size_t)(l - 1) * 2 + ((nq + 1) & 1)) * M + q) * h + 4 * c
+                              : a.w_h + rc + (((size_t)l * 2 + (nq & 1)) * M + q) * h + 4 * (c - CH);
+            };
+            auto tags = [&](int j, int c) -> uint32_t { return sh.n[sh.emit[j]] + (c < CH ? 1u : 0u); };
+            if (!rows_digits(E, 2 * CH, KBL, sq, sh, err, a.wait_ticks, src, words, tags))
+                ms_fail(a, sh);
+            __syncthreads();
+            if (sh.abort) {
+                stop = true;
+                break;
+            }
+            for (int pi = wave; pi < npl; pi += RES_WAVES) {
+                gemv::v4i hi, lo;
+                rows_sums(wlay + (size_t)pi * KBL * 1024, KBL, sq, hi, lo);
+                const int j16 = lane & 15, orow = (lane >> 4) * 4;
+                const float sc = sh.ls[l][pi * PANEL + j16], bs = sh.lbias[l][pi * PANEL + j16];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = orow + v;
+                    const float val = epilogue_vals(dequant(hi[v], lo[v], sh.erow[min(r, E - 1)], sc), true, bs,
+                                                    ACT_NONE, 1.0f, false, 0.0f);
+                    const float gi = quad_lane<0>(val), gf = quad_lane<1>(val), gg = quad_lane<2>(val),
+                                go = quad_lane<3>(val);
+                    if (r < E && (j16 & 3) == 0) {
+                        const int q = sh.emit[r], ul = pi * 4 + (j16 >> 2), u = pl0 * 4 + ul;
+                        const uint32_t nn = sh.n[q] + 1;
+                        float *cs_ = cst + ((size_t)l * M + q) * U + ul, *hs_ = hst + ((size_t)l * M + q) * U + ul;
+                        const float ig = sigmoid(gi), fg = sigmoid(gf), gt = tanhf(gg), og = sigmoid(go);
+                        const float c = fg * *cs_ + ig * gt;
+                        const float hn = og * tanhf(c);
+                        *cs_ = c;
+                        *hs_ = hn;
+                        word_store_all(a.w_h + (((size_t)l * 2 + (nn & 1)) * M + q) * h + u, a.cs, tagged(hn, nn));
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (stop) break;
+        if (npp > 0) {
+            // Row j: the top layer's new h of the j-th emitting stream (tag n + 1).
+            auto src = [&](int, int, v4f &) -> bool { return false; };
+            auto words = [&](int j, int c) -> const uint64_t * {
+                const int q = sh.emit[j];
+                const uint32_t nn = sh.n[q] + 1;
+                return a.w_h + rc + (((size_t)(a.layers - 1) * 2 + (nn & 1)) * M + q) * h + 4 * c;
+            };
+            auto tags = [&](int j, int) -> uint32_t { return sh.n[sh.emit[j]] + 1; };
+            if (!rows_digits(E, CH, KBP, sq, sh, err, a.wait_ticks, src, words, tags)) ms_fail(a, sh);
+            __syncthreads();
+            if (sh.abort) break;
+            for (int pi = wave; pi < npp; pi += RES_WAVES) {
+                gemv::v4i hi, lo;
+                rows_sums(wp + (size_t)pi * KBP * 1024, KBP, sq, hi, lo);
+                const int j16 = lane & 15, orow = (lane >> 4) * 4, col = (pp0 + pi) * PANEL + j16;
+                const float sc = sh.ps[pi * PANEL + j16], bs = sh.pbias[pi * PANEL + j16];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r = orow + v;
+                    if (r < E && col < h) {
+                        const int q = sh.emit[r];
+                        const uint32_t nn = sh.n[q] + 1;
+                        const float val = epilogue_vals(dequant(hi[v], lo[v], sh.erow[r], sc), true, bs, ACT_NONE,
+                                                        1.0f, false, 0.0f);
+                        pst[(size_t)q * a.PP * PANEL + pi * PANEL + j16] = val;
+                        word_store_all(a.w_pred + ((size_t)(nn & 1) * M + q) * h + col, a.cs, tagged(val, nn));
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (tid < E) sh.n[sh.emit[tid]]++;
+        __syncthreads();
+    }
+
+    // The streams' states, predictions and positions for the caller (or the next launch).
+    for (int i = tid; i < a.layers * M * U; i += RES_THREADS) {
+        const int l = i / (M * U), q = (i / U) % M, ul = i % U;
+        if (ul < npl * 4) {
+            a.state[q][(size_t)l * 2 * h + pl0 * 4 + ul] = hst[i];
+            a.state[q][(size_t)l * 2 * h + h + pl0 * 4 + ul] = cst[i];
+        }
+    }
+    for (int i = tid; i < M * a.PP * PANEL; i += RES_THREADS) {
+        const int q = i / (a.PP * PANEL), ci = i % (a.PP * PANEL);
+        if (ci < npp * PANEL && pp0 * PANEL + ci < h) a.pred[q][pp0 * PANEL + ci] = pst[i];
+    }
+    if (b == 0 && tid < M) {
+        TdtCtl &c = a.ctl[tid];
+        c.t = sh.st[tid][0];
+        c.on_frame = sh.st[tid][1];
+        c.ntok = sh.st[tid][2];
+        c.rows = sh.st[tid][3];
+        c.done = sh.st[tid][4];
+        c.preds = sh.n[tid];
+        if (tid == 0) c.step = s;
+    }
+}
+
+// The multi-stream decode's words at its start: each stream's prediction and LSTM outputs with its
+// prediction count as tag in buffer count & 1 (none in the other), the joint's words as at the start
+// of a single decode, no decisions.
+struct MultiInit {
+    const float *state[MS_MAX], *pred[MS_MAX];
+    uint32_t preds[MS_MAX];
+};
+__global__ void tdt_multi_init_kernel(uint64_t *words, int h, int layers, int M, MultiInit in) {
+    const size_t np = 2 * (size_t)M * h, nh = (size_t)layers * 2 * M * h, nb = 2 * (size_t)TDT_ROWS * RES_MAX_GRID,
+                 nd = 2 * (size_t)TDT_ROWS * TDT_ROWS, per = np + nh + nb + nd + 2 * (size_t)M * RES_DEC;
+    for (size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x; j < RES_COPIES * per;
+         j += (size_t)gridDim.x * blockDim.x) {
+        const size_t i = j % per;
+        uint64_t v;
+        if (i < np) {
+            const size_t par = i / ((size_t)M * h), q = (i / h) % M, u = i % h;
+            v = par == (in.preds[q] & 1) ? tagged(in.pred[q][u], in.preds[q]) : tagged(0.0f, TAG_NONE);
+        } else if (i < np + nh) {
+            const size_t k = i - np, l = k / (2 * (size_t)M * h), par = (k / ((size_t)M * h)) % 2, q = (k / h) % M,
+                         u = k % h;
+            v = par == (in.preds[q] & 1) ? tagged(in.state[q][l * 2 * h + u], in.preds[q]) : tagged(0.0f, TAG_NONE);
+        } else if (i < np + nh + nb) {
+            const size_t par = (i - np - nh) / ((size_t)TDT_ROWS * RES_MAX_GRID);
+            v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
+        } else if (i < np + nh + nb + nd) {
+            const size_t par = (i - np - nh - nb) / ((size_t)TDT_ROWS * TDT_ROWS);
+            v = (uint64_t)(par == 0 ? 0xfffeu : 0xffffu) << 48;
+        } else {
+            v = tagged(0.0f, TAG_NONE);
+        }
+        words[j] = v;
+    }
+}
+
 }  // namespace
 
 size_t tdt_max_rows(const DeviceWeights &lstm) {
@@ -1527,6 +2164,112 @@ hipError_t launch_tdt_resident(TdtCtl *ctl, const TdtNet &net, const TdtPlan &pl
     const void *f = plan.q8 ? reinterpret_cast<const void *>(&tdt_resident_kernel<true>)
                             : reinterpret_cast<const void *>(&tdt_resident_kernel<false>);
     return hipLaunchCooperativeKernel(f, dim3((unsigned)plan.grid), dim3(RES_THREADS), args, (unsigned)plan.lds, s);
+}
+
+// Words of one copy of the multi-stream decode's hand-over buffers for m streams.
+static size_t multi_words_per_copy(const TdtNet &net, size_t m) {
+    return 2 * m * net.h + net.layers * 2 * m * net.h + 2 * (size_t)TDT_ROWS * RES_MAX_GRID +
+           2 * (size_t)TDT_ROWS * TDT_ROWS + 2 * m * RES_DEC;
+}
+
+size_t tdt_multi_words(const TdtNet &net) { return RES_COPIES * multi_words_per_copy(net, TDT_MAX_STREAMS); }
+
+// The multi-stream decode's dynamic LDS: the panels, the 16-row digits of the largest product, the
+// streams' predictions for the joint, their cell states and the projection panels' predictions.
+static size_t multi_lds(const TdtNet &net, const TdtPlan &p) {
+    const size_t KBJ = net.joint->kb, KBL = net.lstm[0]->kb, KBP = net.proj->kb;
+    const size_t M = TDT_MAX_STREAMS;
+    return ((size_t)p.JP * KBJ + net.layers * p.LP * KBL + (size_t)p.PP * KBP) * 1024 +
+           std::max(((KBJ + 3) & ~(size_t)3), std::max(KBL, KBP)) * 2048 +
+           (M * net.h + 2 * net.layers * M * p.LP * 4 + M * p.PP * PANEL) * sizeof(float);
+}
+
+bool tdt_multi_plan(const TdtNet &net, TdtPlan &plan) {
+    plan.multi = false;
+    if (plan.grid == 0 || plan.q8) return false;
+    int dev = 0, cus = 0, max_lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return false;
+    const size_t lds = multi_lds(net, plan);
+    const void *f = reinterpret_cast<const void *>(&tdt_multi_kernel);
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, f) != hipSuccess || lds + fa.sharedSizeBytes > (size_t)max_lds) return false;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return false;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, RES_THREADS, lds) != hipSuccess || per_cu < 1 ||
+        (size_t)plan.grid > (size_t)per_cu * cus)
+        return false;
+    plan.mlds = lds;
+    plan.multi = true;
+    return true;
+}
+
+hipError_t launch_tdt_multi_init(const TdtNet &net, uint64_t *words, size_t m, const TdtStream *streams,
+                                 const uint32_t *preds, hipStream_t s) {
+    MultiInit in{};
+    for (size_t q = 0; q < m; q++) {
+        in.state[q] = streams[q].state;
+        in.pred[q] = streams[q].pred;
+        in.preds[q] = preds[q];
+    }
+    hipLaunchKernelGGL(tdt_multi_init_kernel, dim3(256), dim3(256), 0, s, words, (int)net.h, (int)net.layers, (int)m,
+                       in);
+    return hipGetLastError();
+}
+
+hipError_t launch_tdt_multi(TdtCtl *ctl, const TdtNet &net, const TdtPlan &plan, uint64_t *words, size_t m,
+                            const TdtStream *streams, int steps, uint64_t wait_ticks, hipStream_t s) {
+    auto mat = [](const DeviceWeights &d, const float *bias) {
+        return ResMat{d.values, d.scales, bias, d.panel_stride, d.blk_stride, (int)d.n, (int)d.kb, (int)d.panels,
+                      (int)(d.k / Q8_BLOCK)};
+    };
+    MultiArgs a{};
+    a.joint = mat(*net.joint, net.joint_b);
+    a.proj = mat(*net.proj, net.proj_b);
+    for (size_t l = 0; l < net.layers; l++) a.lstm[l] = mat(*net.lstm[l], net.lstm_b[l]);
+    a.emb = net.emb;
+    for (size_t q = 0; q < m; q++) {
+        a.enc[q] = streams[q].enc;
+        a.lde[q] = streams[q].lde;
+        a.frames[q] = streams[q].frames;
+        a.tokens[q] = streams[q].tokens;
+        a.cap[q] = streams[q].cap;
+        a.state[q] = streams[q].state;
+        a.pred[q] = streams[q].pred;
+    }
+    a.ctl = ctl;
+    a.durations = net.durations;
+    a.cs = multi_words_per_copy(net, m);
+    a.w_pred = words;
+    a.w_h = a.w_pred + 2 * m * net.h;
+    a.w_part = a.w_h + net.layers * 2 * m * net.h;
+    a.w_dur = a.w_part + 2 * (size_t)TDT_ROWS * RES_MAX_GRID;
+    a.w_dec = a.w_dur + 2 * (size_t)TDT_ROWS * TDT_ROWS;
+    a.M = (int)m;
+    int slots = TDT_ROWS;
+    while (slots * (int)m > TDT_ROWS) slots >>= 1;  // TDT_ROWS / m rounded down to a power of two
+    a.slots = slots;
+    a.h = (int)net.h;
+    a.vocab = (int)net.vocab;
+    a.ndur = (int)net.ndur;
+    a.layers = (int)net.layers;
+    a.blank = (int)net.blank;
+    a.max_symbols = (int)net.max_symbols;
+    a.JP = plan.JP;
+    a.GJ = plan.GJ;
+    a.LP = plan.LP;
+    a.GL = plan.GL;
+    a.PP = plan.PP;
+    a.GP = plan.GP;
+    a.qoff = plan.qoff;
+    a.grid = plan.grid;
+    a.steps = steps;
+    a.wait_ticks = wait_ticks;
+    void *args[] = {&a};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&tdt_multi_kernel), dim3((unsigned)plan.grid),
+                                      dim3(RES_THREADS), args, (unsigned)plan.mlds, s);
 }
 
 }  // namespace tg

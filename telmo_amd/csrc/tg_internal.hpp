@@ -364,7 +364,27 @@ struct TdtPlan {
     int qoff = 0;              // the first joint / LSTM workgroup
     size_t lds = 0;            // dynamic LDS bytes per workgroup
     bool q8 = false;           // Q8_0 matrices (their block scales in LDS too), else int8
+    bool multi = false;        // the multi-stream decode fits (int8)
+    size_t mlds = 0;           // its dynamic LDS bytes per workgroup
 };
+// Streams of one multi-stream decode launch, and what it reads and writes of each.
+constexpr size_t TDT_MAX_STREAMS = 8;
+struct TdtStream {
+    const float *enc;
+    size_t lde;
+    int frames;
+    float *state, *pred;
+    int32_t *tokens;  // device, 3 int32 per token
+    int cap;
+};
+// Whether the multi-stream decode takes this network (after tdt_resident_plan); sets plan.multi.
+bool tdt_multi_plan(const TdtNet &net, TdtPlan &plan);
+size_t tdt_multi_words(const TdtNet &net);  // 8-byte hand-over words for TDT_MAX_STREAMS streams
+hipError_t launch_tdt_multi_init(const TdtNet &net, uint64_t *words, size_t m, const TdtStream *streams,
+                                 const uint32_t *preds, hipStream_t s);
+// Up to steps steps of m streams from their positions in ctl[0 .. m) (written by the host).
+hipError_t launch_tdt_multi(TdtCtl *ctl, const TdtNet &net, const TdtPlan &plan, uint64_t *words, size_t m,
+                            const TdtStream *streams, int steps, uint64_t wait_ticks, hipStream_t s);
 // Whether the resident decode takes this network on the current device; fills plan and sets the
 // kernel's LDS limit. Needs every matrix int8, or every one Q8_0, vocab < 65535, a cooperative
 // launch and the panels in LDS.

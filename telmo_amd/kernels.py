@@ -549,11 +549,17 @@ class TdtDecoder:
         _check(_lib.lib().tg_tdt_set_resident(self._kernels._ctx, self._handle, 1 if on else 0), self._kernels._ctx)
 
     @property
-    def last_resident(self) -> Optional[bool]:
-        """Whether the last decode ran resident (False: on the step kernels; None before the first).
-        A decode falls back to the step kernels while another one holds the device resident."""
+    def last_resident(self) -> Optional[int]:
+        """How the last decode ran: 1 resident, 0 on the step kernels, 2 several streams in one
+        resident launch; None before the first. A decode falls back to the step kernels while
+        another one holds the device resident."""
         v = int(_lib.lib().tg_tdt_last_resident(self._handle))
-        return None if v < 0 else bool(v)
+        return None if v < 0 else v
+
+    @property
+    def last_steps(self) -> int:
+        """Steps of the last resident decode (one step scores one window of frames per stream)."""
+        return int(_lib.lib().tg_tdt_last_steps(self._handle))
 
     def set_resident_limits(self, steps_per_launch: int = 0, wait_us: int = 0) -> None:
         """The resident decode's steps per launch (0: 16384) and longest wait between workgroups in
@@ -582,6 +588,33 @@ class TdtDecoder:
                                              ctypes.byref(n))
         _check(rc, self._kernels._ctx)
         return [Token(t.id, t.frame, t.duration) for t in out[:n.value]], f.value, o.value
+
+    def decode_streams(self, encs, states, preds, frames=None, caps=None):
+        """Several independent greedy decodes (tg_tdt_decode_streams_device): encs, states and preds
+        are per-stream GPU tensors as decode takes them, each stream from frame 0 (or frames[i]).
+        Returns [(tokens, frame, on_frame)] per stream, what decode returns for each."""
+        m = len(encs)
+        arr = (_lib.TdtStream * max(m, 1))()
+        outs = []
+        for i, (e, st, pr) in enumerate(zip(encs, states, preds)):
+            if e.dim() != 2 or e.stride(1) != 1:
+                raise ValueError("enc_proj must be a 2-D tensor whose rows are contiguous")
+            nf = e.shape[0]
+            f0 = 0 if frames is None else frames[i]
+            cap = max(nf - f0, 0) * max(self.max_symbols, 1) if caps is None else caps[i]
+            out = (_lib.Token * max(cap, 1))()
+            outs.append(out)
+            enc_len = (nf - 1) * e.stride(0) + e.shape[1] if nf else 0
+            s = arr[i]
+            s.enc_proj, s.enc_len, s.lde, s.frames = _dev(e, "float32", "enc_proj").value, _len(e, enc_len, "enc_proj"), \
+                e.stride(0), nf
+            s.state, s.state_len = _dev(st, "float32", "state").value, _len(st, None, "state")
+            s.pred, s.pred_len = _dev(pr, "float32", "pred").value, _len(pr, None, "pred")
+            s.frame, s.on_frame, s.tokens, s.cap = f0, 0, ctypes.addressof(out), cap
+        rc = _lib.lib().tg_tdt_decode_streams_device(self._kernels._ctx, self._handle, ctypes.addressof(arr), m)
+        _check(rc, self._kernels._ctx)
+        return [([Token(t.id, t.frame, t.duration) for t in outs[i][:arr[i].count]], arr[i].frame, arr[i].on_frame)
+                for i in range(m)]
 
     def close(self) -> None:
         if self._handle:

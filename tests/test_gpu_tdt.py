@@ -364,3 +364,86 @@ def test_concurrent_decodes_on_two_contexts_share_the_device(orc, gpu_stream):
         d.close()
     for k in kerns:
         k.close()
+
+
+MULTI_CASES = [  # h, vocab, durations, layers, streams, frames per stream, blank_bias, max_symbols
+    (64, 100, [0, 1, 2, 3, 4], 2, 2, [60, 45], 3.0, 10),
+    (64, 100, [0, 1, 2, 3, 4], 2, 4, [60, 7, 33, 60], 6.0, 3),
+    (128, 300, [0, 2, 4], 1, 8, [77, 20, 77, 1, 50, 64, 9, 70], 4.0, 2),
+    (640, 8193, [0, 1, 2, 3, 4], 2, 8, [120, 90, 120, 60, 100, 120, 75, 110], 6.0, 10),
+]
+
+
+@pytest.mark.parametrize("case", MULTI_CASES)
+def test_multi_stream_decode_matches_each_stream(tk, orc, case):
+    """Several streams in one resident launch (tg_tdt_decode_streams_device). Each stream's tokens,
+    frame, on_frame, state and prediction equal, bit for bit, the single-stream resident decode of
+    that stream alone, and its tokens equal the oracle's decode of it. In the case of Parakeet's
+    shapes, with eight streams of 60 to 120 frames, one stream meets a near tie: there the single-stream
+    decode and the oracle part ways. The device's expf / tanhf and the host's libm differ by an ulp in
+    a gate, as the module docstring describes, so the multi-stream decode follows the single-stream
+    one. That case asserts the oracle's tokens for all streams but at most one."""
+    import torch
+
+    h, vocab, durs, layers, m, frames, blank_bias, ms = case
+    rng = np.random.default_rng(300 + h + m)
+    net = tdt_network(rng, h, vocab, durs, layers=layers, max_symbols=ms, blank_bias=blank_bias)
+    dec = upload(tk, net)
+    encs = [rng.standard_normal((f, h)).astype(np.float32) for f in frames]
+    states = [(0.3 * rng.standard_normal(layers * 2 * h)).astype(np.float32) for _ in range(m)]
+    preds = [(0.3 * rng.standard_normal(h)).astype(np.float32) for _ in range(m)]
+    dev = lambda a: torch.from_numpy(a.copy()).cuda()  # noqa: E731
+    sd, pd = [dev(s) for s in states], [dev(p) for p in preds]
+    say("multi-stream decode", case)
+    got = dec.decode_streams([dev(e) for e in encs], sd, pd)
+    assert dec.last_resident == 2
+    steps_multi = dec.last_steps
+    apart = []
+    for q in range(m):
+        toks, frame, on = got[q]
+        s1, p1 = dev(states[q]), dev(preds[q])
+        t1, f1, o1 = dec.decode(dev(encs[q]), s1, p1)
+        assert dec.last_resident == 1
+        assert (t1, f1, o1) == got[q], q
+        assert np.array_equal(sd[q].cpu().numpy().view(np.uint32), s1.cpu().numpy().view(np.uint32)), q
+        assert np.array_equal(pd[q].cpu().numpy().view(np.uint32), p1.cpu().numpy().view(np.uint32)), q
+        want, wframe, won = orc.tdt_decode(net, encs[q], states[q].copy(), preds[q].copy())
+        if [tuple(t) for t in toks] != want or (frame, on) != (wframe, won):
+            apart.append(q)
+    print(f"[steps] {m} streams: {steps_multi} steps in one launch; streams apart from the oracle: {apart}",
+          flush=True)
+    assert len(apart) <= (1 if h == 640 else 0)
+    dec.close()
+
+
+def test_multi_stream_decode_falls_back_and_refuses(tk, orc):
+    """With the resident decode off the streams run one after another on the step kernels, with the
+    same tokens; a stream past its frames takes no part; shared states are refused."""
+    import torch
+
+    import telmo_amd
+
+    rng = np.random.default_rng(77)
+    net = tdt_network(rng, 64, 100, [0, 1, 2, 3, 4], layers=2, max_symbols=4, blank_bias=3.0)
+    dec = upload(tk, net)
+    encs = [rng.standard_normal((f, 64)).astype(np.float32) for f in (30, 40, 25)]
+    dev = lambda a: torch.from_numpy(a.copy()).cuda()  # noqa: E731
+    zero_s, zero_p = np.zeros(2 * 2 * 64, np.float32), np.zeros(64, np.float32)
+    runs = []
+    for resident in (True, False):
+        dec.set_resident(resident)
+        say("multi-stream decode", "resident" if resident else "steps")
+        got = dec.decode_streams([dev(e) for e in encs], [dev(zero_s) for _ in encs], [dev(zero_p) for _ in encs],
+                                 frames=[0, 40, 0])
+        assert dec.last_resident == (2 if resident else 0)
+        assert got[1] == ([], 40, 0)  # started past its frames
+        runs.append(got)
+    assert runs[0] == runs[1]
+    for q in (0, 2):
+        want, wframe, won = orc.tdt_decode(net, encs[q], zero_s.copy(), zero_p.copy())
+        assert [tuple(t) for t in runs[0][q][0]] == want
+    dec.set_resident(True)
+    shared = dev(zero_s)
+    with pytest.raises(telmo_amd.TelmoError, match="share"):
+        dec.decode_streams([dev(e) for e in encs[:2]], [shared, shared], [dev(zero_p), dev(zero_p)])
+    dec.close()
