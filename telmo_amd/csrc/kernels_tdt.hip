@@ -1395,87 +1395,40 @@ __device__ __forceinline__ void ms_fail(const MultiArgs &a, MultiShared &sh) {
     store_i(&a.ctl[0].err, 1);
 }
 
-// Rows j < E of an MFMA product's input, k = 4 CK inputs in chunks of four: thread t takes chunks
-// t and t + 256 of every row. src(j, c, x) gives chunk c of row j: true when it is read from memory
-// into x, false when it is four hand-over words, src_words(j, c) and src_tag(j, c) telling where and
-// with which tag. Every word of every row is waited for in one round of loads, so the rows cost one
-// memory round trip together. Then each row's exponent (a workgroup reduction per row) and its
-// digits in the 16-row layout (k-block t, digit d at sq + t 2048 + d 1024, lane 16 g + j), zero up
-// to KB k-blocks; the exponents go to sh.erow. False when a wait fails.
-template <typename SRC, typename WORDS, typename TAG>
-__device__ __forceinline__ bool rows_digits(int E, int CK, int KB, uint8_t *sq, MultiShared &sh, const int32_t *err,
-                                            uint64_t ticks, SRC src, WORDS src_words, TAG src_tag) {
-    constexpr int NI = 2;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    v4f x[MS_MAX][NI];
-    uint64_t need = 0;
-#pragma unroll
-    for (int j = 0; j < MS_MAX; j++)
-#pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const int c = tid + RES_THREADS * i;
-            x[j][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (j < E && c < CK && !src(j, c, x[j][i])) need |= 0xfull << (4 * (j * NI + i));
-        }
-    const uint64_t deadline = (uint64_t)wall_clock64() + ticks;
+// Rows j < E of an MFMA product's input from wavefront w = j % 4 (chunk c of 4 inputs in lane c % 64):
+// x = [first CA inputs; the rest], each chunk given by ld(j, c), then the row exponent and the digits
+// in the 16-row layout (k-block t, digit d at sq + t 2048 + d 1024, lane 16 g + j), zero up to KB
+// k-blocks. Returns false when a wait fails.
+template <typename LD>
+__device__ __forceinline__ bool rows_digits(int E, int CK, int KB, uint8_t *sq, MultiShared &sh, LD ld) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     bool ok = true;
-    for (int round = 0; need; round++) {
+    for (int j = wave; j < E; j += RES_WAVES) {
+        v4f x[8];
+        uint32_t mx = 0;
 #pragma unroll
-        for (int j = 0; j < MS_MAX; j++)
-#pragma unroll
-            for (int i = 0; i < NI; i++) {
-                const int b4 = 4 * (j * NI + i);
-                if ((need >> b4) & 0xf) {
-                    const uint64_t *wp = src_words(j, tid + RES_THREADS * i);
-                    const uint32_t tg = src_tag(j, tid + RES_THREADS * i);
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        if ((need >> (b4 + q)) & 1) {
-                            const uint64_t w = word_load(wp + q);
-                            if ((uint32_t)(w >> 32) == tg) {
-                                x[j][i][q] = word_value(w);
-                                need &= ~(1ull << (b4 + q));
-                            }
-                        }
-                    }
-                }
+        for (int q = 0; q < 8; q++) {
+            const int c = lane + 64 * q;
+            x[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (c < CK) {
+                ok = ld(j, c, x[q]) && ok;
+                mx = max(mx, chunk_max(x[q]));
             }
-        if (need && (round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(err) != 0)) {
-            ok = false;
-            break;
         }
-    }
-    __shared__ uint32_t s_rmax[RES_WAVES][MS_MAX];
+        const uint32_t m = gemv::wave_max_u(mx);
+        const int32_t e = m == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(m));
 #pragma unroll
-    for (int j = 0; j < MS_MAX; j++) {
-        if (j < E) {  // uniform
-            uint32_t mx = 0;
-#pragma unroll
-            for (int i = 0; i < NI; i++)
-                if (tid + RES_THREADS * i < CK) mx = max(mx, chunk_max(x[j][i]));
-            mx = gemv::wave_max_u(mx);
-            if (lane == 0) s_rmax[wave][j] = mx;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < MS_MAX; j++) {
-        if (j < E) {
-            const uint32_t m = max(max(s_rmax[0][j], s_rmax[1][j]), max(s_rmax[2][j], s_rmax[3][j]));
-            const int32_t e = m == 0xffffffffu ? EXP_NONFINITE : row_exponent_of(__uint_as_float(m));
-#pragma unroll
-            for (int i = 0; i < NI; i++) {
-                const int c = tid + RES_THREADS * i;
-                if (c < KB * 16) {
-                    uint32_t hi, lo;
-                    digits4(x[j][i].x, x[j][i].y, x[j][i].z, x[j][i].w, e, hi, lo);
-                    uint8_t *d = sq + (c >> 4) * 2048 + ((c & 15) >> 2) * 256 + j * 16 + (c & 3) * 4;
-                    *reinterpret_cast<uint32_t *>(d) = hi;
-                    *reinterpret_cast<uint32_t *>(d + 1024) = lo;
-                }
+        for (int q = 0; q < 8; q++) {
+            const int c = lane + 64 * q;
+            if (c < KB * 16) {
+                uint32_t hi, lo;
+                digits4(x[q].x, x[q].y, x[q].z, x[q].w, e, hi, lo);
+                uint8_t *d = sq + (c >> 4) * 2048 + ((c & 15) >> 2) * 256 + j * 16 + (c & 3) * 4;
+                *reinterpret_cast<uint32_t *>(d) = hi;
+                *reinterpret_cast<uint32_t *>(d + 1024) = lo;
             }
-            if (tid == 0) sh.erow[j] = e;
         }
+        if (lane == 0) sh.erow[j] = e;
     }
     return ok;
 }
@@ -1492,6 +1445,16 @@ __device__ __forceinline__ void rows_sums(const uint8_t *pw, int KB, const uint8
         hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, wv, hi, 0, 0, 0);
         lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, wv, lo, 0, 0, 0);
     }
+}
+
+// Waits for the four words of chunk c at p (the value of each word its float), tag tg.
+__device__ __forceinline__ bool wait_chunk(const uint64_t *p, uint32_t tg, const int32_t *err, uint64_t ticks, v4f &x) {
+    const uint64_t *pp[4] = {p, p + 1, p + 2, p + 3};
+    const uint32_t tag[4] = {tg, tg, tg, tg};
+    uint64_t w[4];
+    const bool ok = wait_words<4>(pp, 0xfu, tag, w, err, (uint64_t)wall_clock64() + ticks);
+    x = v4f{word_value(w[0]), word_value(w[1]), word_value(w[2]), word_value(w[3])};
+    return ok;
 }
 
 __global__ __launch_bounds__(RES_THREADS) void tdt_multi_kernel(MultiArgs a) {
@@ -1575,40 +1538,19 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_multi_kernel(MultiArgs a) {
         }
         // ---- The joint over each stream's window rows.
         if (npj > 0) {
-            // The live streams' predictions, waited for only after they change, all in one round of
-            // loads: thread t takes values t + 256 i (i < 4, h <= 992) of each such stream.
-            uint32_t want = 0;
-            for (int q = 0; q < M; q++)
-                if (!sh.st[q][4] && sh.pin_n[q] != sh.n[q]) want |= 1u << q;  // uniform
-            if (want) {
-                uint32_t need = 0;
-#pragma unroll
-                for (int q = 0; q < MS_MAX; q++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        if ((want >> q & 1) && tid + RES_THREADS * i < h) need |= 1u << (4 * q + i);
-                const uint64_t deadline = (uint64_t)wall_clock64() + a.wait_ticks;
-                for (int round = 0; need; round++) {
-#pragma unroll
-                    for (int q = 0; q < MS_MAX; q++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            if (need >> (4 * q + i) & 1) {
-                                const uint32_t nq = sh.n[q];
-                                const int v = tid + RES_THREADS * i;
-                                const uint64_t w = word_load(a.w_pred + rc + ((size_t)(nq & 1) * M + q) * h + v);
-                                if ((uint32_t)(w >> 32) == nq) {
-                                    pin[(size_t)q * h + v] = word_value(w);
-                                    need &= ~(1u << (4 * q + i));
-                                }
-                            }
-                    if (need && (round & 15) == 15 && ((uint64_t)wall_clock64() > deadline || load_i(err) != 0)) {
-                        ms_fail(a, sh);
-                        break;
-                    }
+            // The live streams' predictions (waited for only after they change).
+            for (int q = 0; q < M; q++) {
+                if (sh.st[q][4] || sh.pin_n[q] == sh.n[q]) continue;  // uniform
+                const uint32_t nq = sh.n[q];
+                for (int i = tid; i < h; i += RES_THREADS) {
+                    const uint64_t *p[1] = {a.w_pred + rc + ((size_t)(nq & 1) * M + q) * h + i};
+                    const uint32_t tag[1] = {nq};
+                    uint64_t w[1];
+                    if (!wait_words<1>(p, 1u, tag, w, err, (uint64_t)wall_clock64() + a.wait_ticks)) ms_fail(a, sh);
+                    pin[(size_t)q * h + i] = word_value(w[0]);
                 }
                 __syncthreads();
-                if (tid < M && (want >> tid & 1)) sh.pin_n[tid] = sh.n[tid];
+                if (tid == 0) sh.pin_n[q] = nq;
             }
             __syncthreads();
             if (sh.abort) break;
@@ -1830,24 +1772,21 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_multi_kernel(MultiArgs a) {
         for (int l = 0; l < a.layers && !stop; l++) {
             if (npl == 0) continue;
             const uint8_t *wlay = wl + (size_t)l * a.LP * KBL * 1024;
-            // Row j: [x; h_l] of the j-th emitting stream: x the embedding row of its token (layer 0) or
-            // the new h of the layer below (tag n + 1), h_l its layer's h (tag n).
-            auto src = [&](int j, int c, v4f &x) -> bool {
-                if (l == 0 && c < CH) {
-                    x = *reinterpret_cast<const v4f *>(a.emb + (size_t)sh.dec[sh.emit[j]][3] * h + 4 * c);
-                    return true;
-                }
-                return false;
-            };
-            auto words = [&](int j, int c) -> const uint64_t * {
+            auto ld = [&](int j, int c, v4f &x) -> bool {
                 const int q = sh.emit[j];
                 const uint32_t nq = sh.n[q];
-                return c < CH ? a.w_h + rc + (((size_t)(l - 1) * 2 + ((nq + 1) & 1)) * M + q) * h + 4 * c
-                              : a.w_h + rc + (((size_t)l * 2 + (nq & 1)) * M + q) * h + 4 * (c - CH);
+                if (c < CH) {
+                    if (l == 0) {
+                        x = *reinterpret_cast<const v4f *>(a.emb + (size_t)sh.dec[q][3] * h + 4 * c);
+                        return true;
+                    }
+                    return wait_chunk(a.w_h + rc + (((size_t)(l - 1) * 2 + ((nq + 1) & 1)) * M + q) * h + 4 * c, nq + 1,
+                                      err, a.wait_ticks, x);
+                }
+                return wait_chunk(a.w_h + rc + (((size_t)l * 2 + (nq & 1)) * M + q) * h + 4 * (c - CH), nq, err,
+                                  a.wait_ticks, x);
             };
-            auto tags = [&](int j, int c) -> uint32_t { return sh.n[sh.emit[j]] + (c < CH ? 1u : 0u); };
-            if (!rows_digits(E, 2 * CH, KBL, sq, sh, err, a.wait_ticks, src, words, tags))
-                ms_fail(a, sh);
+            if (!rows_digits(E, 2 * CH, KBL, sq, sh, ld)) ms_fail(a, sh);
             __syncthreads();
             if (sh.abort) {
                 stop = true;
@@ -1882,15 +1821,13 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_multi_kernel(MultiArgs a) {
         }
         if (stop) break;
         if (npp > 0) {
-            // Row j: the top layer's new h of the j-th emitting stream (tag n + 1).
-            auto src = [&](int, int, v4f &) -> bool { return false; };
-            auto words = [&](int j, int c) -> const uint64_t * {
+            auto ld = [&](int j, int c, v4f &x) -> bool {
                 const int q = sh.emit[j];
                 const uint32_t nn = sh.n[q] + 1;
-                return a.w_h + rc + (((size_t)(a.layers - 1) * 2 + (nn & 1)) * M + q) * h + 4 * c;
+                return wait_chunk(a.w_h + rc + (((size_t)(a.layers - 1) * 2 + (nn & 1)) * M + q) * h + 4 * c, nn, err,
+                                  a.wait_ticks, x);
             };
-            auto tags = [&](int j, int) -> uint32_t { return sh.n[sh.emit[j]] + 1; };
-            if (!rows_digits(E, CH, KBP, sq, sh, err, a.wait_ticks, src, words, tags)) ms_fail(a, sh);
+            if (!rows_digits(E, CH, KBP, sq, sh, ld)) ms_fail(a, sh);
             __syncthreads();
             if (sh.abort) break;
             for (int pi = wave; pi < npp; pi += RES_WAVES) {
