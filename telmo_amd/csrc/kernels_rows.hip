@@ -289,9 +289,18 @@ __global__ __launch_bounds__(256) void quantize_known_kernel(const float *__rest
             v[j].w = i0 + 3 < n ? x.w : 0.0f;
         }
     }
+    // The row's strip maxima: the first 128 strips' loads all issued before any is used, so they cost
+    // one memory round trip.
     uint32_t mx = 0u;
-    if (valid)
-        for (int st = c; st < strips; st += 16) mx = max(mx, tmax[row * (size_t)strips + st]);
+    if (valid) {
+        const uint32_t *tr = tmax + row * (size_t)strips;
+        uint32_t sm[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) sm[u] = c + 16 * u < strips ? tr[c + 16 * u] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; u++) mx = max(mx, sm[u]);
+        for (int st = c + 128; st < strips; st += 16) mx = max(mx, tr[st]);
+    }
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 16));
     const int32_t e = !valid ? 0 : (mx >= 0x7f800000u ? EXP_NONFINITE : row_exponent_of(__uint_as_float(mx)));
@@ -579,19 +588,19 @@ __global__ __launch_bounds__(256) void layer_norm_lds_kernel(const float *x, siz
     }
 }
 
-bool layer_norm_quad_fits(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+bool layer_norm_row_fits(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                           const float *out, size_t ldo);
 hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                               float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps, hipStream_t s);
-hipError_t launch_layer_norm_quad(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+hipError_t launch_layer_norm_row(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                   const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
                                   hipStream_t s);
 
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
-    if (layer_norm_quad_fits(x, ldx, m, n, gamma, beta, out, ldo))
-        return launch_layer_norm_quad(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
+    if (layer_norm_row_fits(x, ldx, m, n, gamma, beta, out, ldo))
+        return launch_layer_norm_row(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
     if (n <= (size_t)LN4_MAX) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, nullptr, nullptr, s);
     if (n <= (size_t)LN_LDS_MAX) {
         // Up to sixteen rows and 64 KB of LDS per block.
@@ -914,59 +923,51 @@ hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, co
     return hipGetLastError();
 }
 
-// LayerNorm of rows of n <= 1024 values (n % 4 == 0, rows and gamma, beta 16-byte aligned), four
-// rows per workgroup of four wavefronts, with its outputs written as f32 (out) and/or quantised
-// (qa, exps): layer_norm4_kernel's work spread over four times the wavefronts, for batches too
-// small to fill the chip with it. The arithmetic is layer_norm_kernel's, in three phases:
-//  1. wavefront w loads row w of the four: lane l takes inputs 4 (l + 64 i) + [0, 4) with 16-byte
-//     loads (one 1 KB run per instruction), keeps them in registers and copies them to LDS, zeros
-//     past n (rows LNQ_ROW floats apart, so that each half-wavefront's reads below hit 32 banks);
-//  2. wavefront 0 sums the partials of all four rows: lane (r = l / 16, p = l % 16) adds inputs
-//     p, p + 16, ... of row r in order (the zeros past n leave a sum unchanged, as it starts at +0
-//     and cannot become -0), and the squared deviations the same, a masked deviation of 0 past n;
-//     folds as the reference's (p + 8, + 4, + 2, + 1); mean and rstd go to LDS;
-//  3. wavefront w computes row w's outputs from its registers: out gets them as 16-byte stores; the
-//     row's largest magnitude gives its exponent, and a lane's four inputs are four consecutive
-//     bytes of one 16-byte run of the quantised layout (k-block t = 4 i + l / 16, operand lane
-//     16 ((l / 4) % 4) + row % 16, bytes 4 (l % 4) + [0, 4)), one 4-byte store per digit.
-// The chains of phase 2 are the only serial work: one instruction advances four rows. Rows past m
-// (up to the end of the last 16-row block) write zero digits. out may be x: a lane reads its inputs
-// before it writes their outputs, and no lane writes another's inputs.
-constexpr int LNQ_MAX = 1024, LNQ_ROW = LNQ_MAX + 16;
+constexpr int LNQ_MAX = 1024;
 
+// LayerNorm of a row of n <= 1024 values (n % 4 == 0, rows and gamma, beta 16-byte aligned) per
+// workgroup of 256 threads, with its outputs written as f32 (out) and/or quantised (qa, exps). The
+// arithmetic is layer_norm_kernel's:
+//  1. thread t loads inputs 4 t + [0, 4) (zeros past n) with one 16-byte load, keeps them in
+//     registers and copies them to LDS; gamma and beta are loaded with them;
+//  2. lanes p < 16 of wavefront 0 run the row's two chains in the reference's order: lane p adds
+//     inputs p, p + 16, ... in order (the zeros past n leave a sum unchanged, as it starts at +0 and
+//     cannot become -0), then the squared deviations the same, a masked deviation of 0 past n; both
+//     fold as the reference's (p + 8, + 4, + 2, + 1); mean and rstd go to LDS;
+//  3. after one barrier every thread writes its four outputs (16-byte stores to out) and, with the
+//     row maximum reduced over the workgroup, their digits: chunk t is k-block t / 16, operand lane
+//     16 ((t % 16) / 4) + row % 16, bytes 4 (t % 4) + [0, 4).
+// Rows are spread over the XCDs in 16-row blocks as quantize_rows_regs_kernel spreads them; rows past
+// m up to the end of the last 16-row block get zero digits when qa is given. out may be x: a thread
+// reads its inputs before it writes their outputs, and no thread writes another's inputs.
 template <bool FULL>  // FULL: n == LNQ_MAX, no masking in the chains
-__global__ __launch_bounds__(256) void layer_norm_quad_kernel(const float *x, size_t ldx, size_t m, int n,
-                                                              const float *__restrict__ gamma,
-                                                              const float *__restrict__ beta, float eps, float *out,
-                                                              size_t ldo, uint8_t *__restrict__ qa,
-                                                              int32_t *__restrict__ exps, int kb, size_t bpx) {
-    __shared__ __attribute__((aligned(16))) float rows_s[4 * LNQ_ROW];
-    __shared__ float stat[4][2];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const size_t xcd = blockIdx.x % 8, i = blockIdx.x / 8;
-    const size_t blk = xcd * bpx + i / 4;  // 16-row block
-    const size_t row0 = blk * 16 + (i % 4) * 4;
-    if (qa ? blk * 16 >= m : row0 >= m) return;  // uniform over the workgroup
-    const size_t row = row0 + w;
-    const bool valid = row < m;  // uniform over the wavefront
+__global__ __launch_bounds__(256) void layer_norm_row_kernel(const float *x, size_t ldx, size_t m, int n,
+                                                             const float *__restrict__ gamma,
+                                                             const float *__restrict__ beta, float eps, float *out,
+                                                             size_t ldo, uint8_t *__restrict__ qa,
+                                                             int32_t *__restrict__ exps, int kb, size_t bpx) {
+    __shared__ __attribute__((aligned(16))) float row_s[LNQ_MAX];
+    __shared__ float stat[2];
+    __shared__ float s_max[4];
+    __shared__ int s_bad[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t xg = blockIdx.x % 8, i = blockIdx.x / 8;
+    const size_t row = (xg * bpx + i / 16) * 16 + i % 16;
+    const bool valid = row < m;
+    if (!valid && (!qa || row >= (m + 15) / 16 * 16)) return;  // uniform over the workgroup
     const float4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    float4 v[LNQ_MAX / 256];
-    {
-        const float4 *xr = reinterpret_cast<const float4 *>(x + (valid ? row : 0) * ldx);
-#pragma unroll
-        for (int i = 0; i < LNQ_MAX / 256; i++) {
-            const int c4 = lane + 64 * i;
-            v[i] = valid && (FULL || 4 * c4 < n) ? xr[c4] : zero;
-        }
-#pragma unroll
-        for (int i = 0; i < LNQ_MAX / 256; i++) reinterpret_cast<float4 *>(rows_s + w * LNQ_ROW)[lane + 64 * i] = v[i];
+    const bool in = valid && (FULL || 4 * tid < n);
+    float4 v = zero, g = zero, b = zero;
+    if (in) {
+        v = reinterpret_cast<const float4 *>(x + row * ldx)[tid];
+        g = reinterpret_cast<const float4 *>(gamma)[tid];
+        b = reinterpret_cast<const float4 *>(beta)[tid];
     }
+    reinterpret_cast<float4 *>(row_s)[tid] = v;
     __syncthreads();
-    if (w == 0) {
-        const int r = lane >> 4, p = lane & 15;
-        const float *xr = rows_s + r * LNQ_ROW + p;
-        // The chains read LDS in batches of 16 (the scheduling barriers keep the batches apart, so
-        // that few registers are live and the workgroups fit eight wavefronts per SIMD).
+    if (tid < 16) {
+        const int p = tid;
+        const float *xr = row_s + p;
         float s = 0.0f;
 #pragma unroll
         for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
@@ -992,63 +993,50 @@ __global__ __launch_bounds__(256) void layer_norm_quad_kernel(const float *x, si
         sq = sq + __shfl_xor(sq, 2, 16);
         sq = sq + __shfl_xor(sq, 1, 16);
         if (p == 0) {
-            stat[r][0] = mean;
-            stat[r][1] = 1.0f / __builtin_sqrtf(sq / (float)n + eps);
+            stat[0] = mean;
+            stat[1] = 1.0f / __builtin_sqrtf(sq / (float)n + eps);
         }
     }
     __syncthreads();
-    if (!valid && !qa) return;
-    const float mean = stat[w][0], rstd = stat[w][1];
-    float amax = 0.0f;
-    int bad = 0;
-#pragma unroll
-    for (int i = 0; i < LNQ_MAX / 256; i++) {
-        const int c4 = lane + 64 * i;
-        if (valid && (FULL || 4 * c4 < n)) {
-            const float4 g = reinterpret_cast<const float4 *>(gamma)[c4];
-            const float4 b = reinterpret_cast<const float4 *>(beta)[c4];
-            float4 y;
-            y.x = __builtin_fmaf((v[i].x - mean) * rstd, g.x, b.x);
-            y.y = __builtin_fmaf((v[i].y - mean) * rstd, g.y, b.y);
-            y.z = __builtin_fmaf((v[i].z - mean) * rstd, g.z, b.z);
-            y.w = __builtin_fmaf((v[i].w - mean) * rstd, g.w, b.w);
-            v[i] = y;
-            if (out) reinterpret_cast<float4 *>(out + row * ldo)[c4] = y;
-            bad |= !__builtin_isfinite(y.x) | !__builtin_isfinite(y.y) | !__builtin_isfinite(y.z) |
-                   !__builtin_isfinite(y.w);
-            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(y.x), fabsf(y.y))), fmaxf(fabsf(y.z), fabsf(y.w)));
-        } else {
-            v[i] = zero;
-        }
+    const float mean = stat[0], rstd = stat[1];
+    float4 y = zero;
+    if (in) {
+        y.x = __builtin_fmaf((v.x - mean) * rstd, g.x, b.x);
+        y.y = __builtin_fmaf((v.y - mean) * rstd, g.y, b.y);
+        y.z = __builtin_fmaf((v.z - mean) * rstd, g.z, b.z);
+        y.w = __builtin_fmaf((v.w - mean) * rstd, g.w, b.w);
+        if (out) reinterpret_cast<float4 *>(out + row * ldo)[tid] = y;
     }
-    if (!qa) return;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off));
-        bad |= __shfl_xor(bad, off);
+    if (!qa) return;  // uniform
+    float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+    int bad = !__builtin_isfinite(y.x) | !__builtin_isfinite(y.y) | !__builtin_isfinite(y.z) | !__builtin_isfinite(y.w);
+    amax = wave_max(amax);
+    bad = wave_or(bad);
+    if (lane == 0) {
+        s_max[wave] = amax;
+        s_bad[wave] = bad;
     }
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    bad = s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3];
     const int32_t e = !valid ? 0 : (bad ? EXP_NONFINITE : row_exponent_of(amax));
-    if (valid && lane == 0) exps[row] = e;
-    uint8_t *base = qa + (row / 16) * (size_t)kb * 2048 + (16 * ((lane >> 2) & 3) + row % 16) * 16 + 4 * (lane & 3);
-#pragma unroll
-    for (int i = 0; i < LNQ_MAX / 256; i++) {
-        const int t = 4 * i + (lane >> 4);
-        if (t < kb) {
-            uint32_t hi = 0, lo = 0;
-            if (valid) digits4(v[i].x, v[i].y, v[i].z, v[i].w, e, hi, lo);
-            *reinterpret_cast<uint32_t *>(base + (size_t)t * 2048) = hi;
-            *reinterpret_cast<uint32_t *>(base + (size_t)t * 2048 + 1024) = lo;
-        }
+    if (valid && tid == 0) exps[row] = e;
+    if (tid < kb * 16) {
+        uint32_t hi = 0, lo = 0;
+        if (valid) digits4(y.x, y.y, y.z, y.w, e, hi, lo);
+        const size_t at = qa_offset(row, tid >> 4, 0, kb) + ((tid & 15) >> 2) * 256 + (tid & 3) * 4;
+        *reinterpret_cast<uint32_t *>(qa + at) = hi;
+        *reinterpret_cast<uint32_t *>(qa + at + 1024) = lo;
     }
 }
 
-// Whether layer_norm_quad_kernel takes these rows: fewer than LNQ_ROWS_MAX of them (beyond, the
+// Whether layer_norm_row_kernel takes these rows: fewer than LNQ_ROWS_MAX of them (beyond, the
 // single-wavefront layer_norm4_kernel fills the chip and costs fewer instructions per row), n <= 1024
 // and a multiple of 4, x, gamma, beta (and out when given) 16-byte aligned with row strides of
 // whole 16-byte units.
 constexpr size_t LNQ_ROWS_MAX = 2048;
 
-bool layer_norm_quad_fits(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
+bool layer_norm_row_fits(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                           const float *out, size_t ldo) {
     uintptr_t al = reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
                    reinterpret_cast<uintptr_t>(beta);
@@ -1056,18 +1044,18 @@ bool layer_norm_quad_fits(const float *x, size_t ldx, size_t m, size_t n, const 
     return m < LNQ_ROWS_MAX && n > 0 && n <= (size_t)LNQ_MAX && n % 4 == 0 && al % 16 == 0;
 }
 
-hipError_t launch_layer_norm_quad(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+hipError_t launch_layer_norm_row(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                   const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
                                   hipStream_t s) {
     const size_t kb = div_ceil(n, KBLK);
-    // Four workgroups per 16-row block, bpx blocks per XCD.
+    // One workgroup per row of each 16-row block, bpx blocks per XCD.
     const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
-    const unsigned groups = (unsigned)(8 * bpx * 4);
+    const unsigned groups = (unsigned)(8 * bpx * 16);
     if (n == (size_t)LNQ_MAX)
-        hipLaunchKernelGGL(layer_norm_quad_kernel<true>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
+        hipLaunchKernelGGL(layer_norm_row_kernel<true>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
                            eps, out, ldo, qa, exps, (int)kb, bpx);
     else
-        hipLaunchKernelGGL(layer_norm_quad_kernel<false>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
+        hipLaunchKernelGGL(layer_norm_row_kernel<false>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
                            eps, out, ldo, qa, exps, (int)kb, bpx);
     return hipGetLastError();
 }
@@ -1076,8 +1064,8 @@ hipError_t launch_layer_norm_quant(const float *x, size_t ldx, size_t m, size_t 
                                    const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
                                    hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
-    if (layer_norm_quad_fits(x, ldx, m, n, gamma, beta, out, ldo))
-        return launch_layer_norm_quad(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
+    if (layer_norm_row_fits(x, ldx, m, n, gamma, beta, out, ldo))
+        return launch_layer_norm_row(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
     if (n <= (size_t)LN4_MAX) return launch_layer_norm4(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s);
     const size_t kb = div_ceil(n, KBLK);
     const int vec = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
