@@ -240,6 +240,23 @@ def timed_on(stream, fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def graph_timed(stream, fn, reps, replays=10):
+    """Mean ms per call of fn on the GPU: reps calls captured as one HIP graph, replayed `replays`
+    times between HIP events on `stream` (a small kernel's eager launch through Python costs more
+    host time than its GPU time, so eager back-to-back calls would time the host)."""
+    import torch
+
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(reps):
+            fn(i)
+    graph.replay()
+    ms = timed_on(stream, lambda i: graph.replay(), replays) / reps
+    del graph
+    return ms
+
+
 def step_times(stream, step, steps, warmup, check, reset):
     """(eager ms, graph ms) of `step`, the graph's output checked equal to an eager step's by check().
     A step works in place on its input rows, so each timed step takes the previous one's outputs as
@@ -324,7 +341,7 @@ def gpu_leg(args, params, x0_host):
     for name, k, n, *_ in PRODUCTS:
         for i in range(5):
             launches[name](i)
-        ms = timed_on(stream, launches[name], args.kernel_reps)
+        ms = graph_timed(stream, launches[name], args.kernel_reps)
         per_shape.append({"product": name, "m": T, "k": k, "n": n, "us": round(ms * 1e3, 3),
                           "tops": round(2 * T * k * n / (ms * 1e-3) / 1e12, 1)})
     dw_out = torch.empty((T, D), device="cuda")
@@ -346,7 +363,7 @@ def gpu_leg(args, params, x0_host):
     for name, fn in rows.items():
         for i in range(5):
             fn(i)
-        row_us[name] = round(timed_on(stream, fn, args.kernel_reps) * 1e3, 3)
+        row_us[name] = round(graph_timed(stream, fn, args.kernel_reps) * 1e3, 3)
     kern.synchronize()
     close_layer(w)
     kern.close()
@@ -1096,7 +1113,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--kernel-reps", type=int, default=500)
+    ap.add_argument("--kernel-reps", type=int, default=100,
+                    help="launches per captured graph in the per-kernel legs (the graph is replayed 10 times)")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
@@ -1136,7 +1154,8 @@ def main():
                 "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of these launches, committed in "
                                   "profiles/layer_T750_traffic.json (not measured in this run)" if traffic else None,
                 "kernel": "the eight products of the layer step as it runs them, each launched alone (FF in: the "
-                          "quantised-output product and its row quantiser)",
+                          "quantised-output product and its row quantiser), GPU time per launch from a replayed graph "
+                          "of back-to-back launches",
                 "dominant": dominant["product"],
                 "avg_launch_us": round(gemm_us / len(per_shape), 3), "ops_per_launch_avg": ops / len(per_shape),
                 "note": "two int8 digits per activation: the MFMAs execute 2x the algorithmic ops, so the "
