@@ -784,9 +784,24 @@ __device__ __forceinline__ float row_fold_q8(const uint8_t *pw, int KB, int NB, 
         if (((lane >> 4) & 1) == 0) tq[(2 * t + (lane >> 5)) * PANEL + (lane & 15)] = dh * 256 + dl;
     }
     __syncthreads();
+    // The fold in block order, its operands read from LDS eight blocks at a time so that the chain of
+    // fused multiply-adds does not wait on a read per block.
     float f = 0.0f;
-    if (wave == 0 && lane < PANEL)
-        for (int b = 0; b < NB; b++) f = __builtin_fmaf(ds[b * PANEL + lane], (float)tq[b * PANEL + lane], f);
+    if (wave == 0 && lane < PANEL) {
+        int b = 0;
+        for (; b + 8 <= NB; b += 8) {
+            float dv[8];
+            int32_t tv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                dv[u] = ds[(b + u) * PANEL + lane];
+                tv[u] = tq[(b + u) * PANEL + lane];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) f = __builtin_fmaf(dv[u], (float)tv[u], f);
+        }
+        for (; b < NB; b++) f = __builtin_fmaf(ds[b * PANEL + lane], (float)tq[b * PANEL + lane], f);
+    }
     return f;
 }
 
@@ -975,26 +990,29 @@ __global__ __launch_bounds__(RES_THREADS) void tdt_resident_kernel(ResArgs a) {
                 float fq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 if constexpr (Q8) {
                     // Half hh of k-block t is block 2 t + hh: lane 16 g + x reads 8 bytes of layout
-                    // lane 16 (2 hh + g / 2) + x, the same inputs for the digits and the weights.
+                    // lane 16 (2 hh + g / 2) + x, the same inputs for the digits and the weights. Both
+                    // halves' MFMAs are issued before their folds, which run in block order.
                     const uint8_t *wb = wj + (size_t)pi * KBJ * 1024;
                     const float *ds = qsj + (size_t)pi * NBJ * PANEL + j16;
                     const int g = lane >> 4, off0 = (16 * (g >> 1) + j16) * 16 + 8 * (g & 1);
                     for (int t = 0; t < KBJ; t++) {
+                        gemv::v4i H[2], L[2];
+#pragma unroll
+                        for (int hh = 0; hh < 2; hh++) {
+                            const int off = off0 + hh * 512;
+                            const long ah = *reinterpret_cast<const long *>(sq + t * 2048 + off);
+                            const long al = *reinterpret_cast<const long *>(sq + t * 2048 + 1024 + off);
+                            const long wv = *reinterpret_cast<const long *>(wb + (size_t)t * 1024 + off);
+                            H[hh] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, wv, gemv::v4i{0, 0, 0, 0}, 0, 0, 0);
+                            L[hh] = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, wv, gemv::v4i{0, 0, 0, 0}, 0, 0, 0);
+                        }
 #pragma unroll
                         for (int hh = 0; hh < 2; hh++) {
                             const int bk = 2 * t + hh;
                             if (bk < NBJ) {
-                                const int off = off0 + hh * 512;
-                                const long ah = *reinterpret_cast<const long *>(sq + t * 2048 + off);
-                                const long al = *reinterpret_cast<const long *>(sq + t * 2048 + 1024 + off);
-                                const long wv = *reinterpret_cast<const long *>(wb + (size_t)t * 1024 + off);
-                                const gemv::v4i H = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, wv, gemv::v4i{0, 0, 0, 0},
-                                                                                         0, 0, 0);
-                                const gemv::v4i L = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, wv, gemv::v4i{0, 0, 0, 0},
-                                                                                         0, 0, 0);
                                 const float d = ds[bk * PANEL];
 #pragma unroll
-                                for (int v = 0; v < 4; v++) fq[v] = __builtin_fmaf(d, (float)(H[v] * 256 + L[v]), fq[v]);
+                                for (int v = 0; v < 4; v++) fq[v] = __builtin_fmaf(d, (float)(H[hh][v] * 256 + L[hh][v]), fq[v]);
                             }
                         }
                     }
