@@ -397,8 +397,9 @@ typedef struct {
  * tg_tdt_decode_device gives for it. Up to 8 streams run resident in one launch (no counterpart in
  * the reference): the joint scores 16 / m frames of each stream's window per step, each stream's
  * window is walked on its own, and the streams that emitted a token run the prediction network
- * together as rows of one MFMA product with the matrices in LDS, so a step costs about what one
- * stream's step costs. More than 8 streams go in groups of 8. Without the resident multi-stream
+ * together as rows of one MFMA product with the matrices in LDS (on Parakeet's decoder a step of 8
+ * streams takes about three single-stream steps, so 8 streams decode 2.3 times one stream's tokens
+ * per second). More than 8 streams go in groups of 8. Without the resident multi-stream
  * decode (Q8_0 or mixed matrices, the device's resident lock held elsewhere, tg_tdt_set_resident(0),
  * one stream) the streams are decoded one after another. tg_tdt_last_resident then reports 2 for a
  * multi-stream launch. Streams must not share state or pred. Blocks until every stream ends; on an

@@ -1058,7 +1058,7 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     // per CU: 7500 x 4096 -> 1024 runs 81 us against 123 us on the direct kernel), else the
     // direct kernel, or the k-split kernel when the inputs are long (at least 32 k-blocks) and
     // the tiles too few to fill the CUs twice.
-    if (w.panels >= 128) return launch_lds<4, 4, 3, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    if (w.panels >= 128) return launch_lds<4, 4, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 256)
         return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512) {
@@ -1067,16 +1067,16 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         // 14.2 us); else 64-row tiles (at 1000 rows 336 workgroups would take two rounds: 25
         // against 16.4 us).
         if (div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
-            return launch_kq<3, 5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
-        return launch_kq<4, 5, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+            return launch_kq<3, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     }
     // The direct kernel: 64 x 64 tiles when they give about one workgroup per CU (161 to 256 of
     // them), else 32 x 64 tiles, four workgroups per CU: more of them on small grids, shorter
     // ones on large (750 x 1024 -> 640: 6.3 -> 4.9 us; 300 x 1024 -> 1000: 6.9 -> 5.4 us;
     // 1500 x 1024 -> 1024: 10.7 -> 9.7 us; 750 x 1024 -> 1024 keeps 64 x 64, 6.6 against 7.3 us).
     const size_t tiles64 = div_ceil(m, (size_t)64) * div_ceil(w.n, (size_t)64);
-    if (tiles64 > 160 && tiles64 <= GFX950_CUS) return launch_tile<2, 2, 6, 2, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
-    return launch_tile<1, 2, 6, 4, 0, 4>(qf, exps, m, w, c, ldc, epi, s);
+    if (tiles64 > 160 && tiles64 <= GFX950_CUS) return launch_tile<2, 2, 6, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+    return launch_tile<1, 2, 6, 4, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
 }
 
 // The product's f32 outputs and their row maxima per workgroup column (TileMax), on the tiles
@@ -1091,7 +1091,7 @@ hipError_t launch_gemm_i8_qout(const uint8_t *qf, const int32_t *exps, size_t m,
     if (w.precision != INT8 || epi.accumulate) return hipErrorInvalidValue;
     const TileMax q{tmax, gemm_qout_strips(m, w)};
     if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0, 0, 1>(qf, exps, m, w, h, ldh, epi, s, q);
-    return launch_lds<4, 4, 3, 0, 4, 0, 1>(qf, exps, m, w, h, ldh, epi, s, q);
+    return launch_lds<4, 4, 3, 1, 0, 0, 1>(qf, exps, m, w, h, ldh, epi, s, q);
 }
 
 // The GLU-fused product: 128 x 128 tiles (four panels of each half) when they fill the chip twice
@@ -1106,7 +1106,7 @@ hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, 
     const size_t half = w.n / 2;
     if (half % 64 == 0 && gemm_tile_choice(m, w.panels) == 0)
         return launch_lds<8, 8, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
-    return launch_lds<4, 4, 3, 0, 4, 1>(qf, exps, m, w, out, ldo, epi, s);
+    return launch_lds<4, 4, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
 }
 
 }  // namespace tg

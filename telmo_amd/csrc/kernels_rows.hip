@@ -259,7 +259,7 @@ hipError_t launch_quantize_rows(const float *a, size_t lda, size_t m, size_t k, 
 // values (row stride ldh, a multiple of 64, 16-byte aligned rows; values past n are ignored), and
 // tmax the largest |value| of each row over strips column ranges as unsigned bits, all ones for a
 // range holding a NaN or an infinity (tmax[row * strips + s], as gemm_lds_kernel<..., QOUT = 1>
-// leaves them). Workgroup (R, y) takes 16-row block R and k-blocks QK_CH y .. QK_CH y + QK_CH - 1.
+// leaves them). Each workgroup takes one 16-row block R and k-blocks QK_CH y .. QK_CH y + QK_CH - 1.
 // Thread (r = tid / 16, c = tid % 16) folds row r's maxima c, c + 16, ... over its 16 lanes into the
 // row exponent, the one quantize_rows_regs_kernel computes from the values, then writes the digits
 // of inputs 64 t + 4 c + [0, 4) as one hi and one lo dword at operand lane 16 (c / 4) + r, bytes
@@ -270,10 +270,15 @@ constexpr int QK_CH = 4;
 
 __global__ __launch_bounds__(256) void quantize_known_kernel(const float *__restrict__ h, size_t ldh, size_t m, int n,
                                                              int kb, const uint32_t *__restrict__ tmax, int strips,
-                                                             uint8_t *__restrict__ qa, int32_t *__restrict__ exps) {
+                                                             uint8_t *__restrict__ qa, int32_t *__restrict__ exps,
+                                                             size_t bpx, int ny) {
     const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
-    const size_t R = blockIdx.x, row = R * 16 + r;
-    const int t0 = blockIdx.y * QK_CH;
+    // Workgroup L runs on XCD L % 8; XCD x takes 16-row blocks x bpx .. x bpx + bpx - 1 (ny workgroups
+    // a block), the rows the product's tiles leave in that XCD's L2.
+    const size_t xg = blockIdx.x % 8, gi = blockIdx.x / 8;
+    const size_t R = xg * bpx + gi / ny, row = R * 16 + r;
+    if (R * 16 >= m) return;  // uniform
+    const int t0 = (int)(gi % ny) * QK_CH;
     const bool valid = row < m;
     const float *hr = h + (valid ? row : 0) * ldh;
     float4 v[QK_CH];
@@ -304,7 +309,7 @@ __global__ __launch_bounds__(256) void quantize_known_kernel(const float *__rest
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 16));
     const int32_t e = !valid ? 0 : (mx >= 0x7f800000u ? EXP_NONFINITE : row_exponent_of(__uint_as_float(mx)));
-    if (valid && blockIdx.y == 0 && c == 0) exps[row] = e;
+    if (valid && t0 == 0 && c == 0) exps[row] = e;
 #pragma unroll
     for (int j = 0; j < QK_CH; j++) {
         const int t = t0 + j;
@@ -322,8 +327,9 @@ hipError_t launch_quantize_known(const float *h, size_t ldh, size_t m, size_t n,
     if (m == 0 || n == 0) return hipSuccess;
     const size_t kb = div_ceil(n, KBLK);
     if (ldh % KBLK != 0 || ldh < kb * KBLK || reinterpret_cast<uintptr_t>(h) % 16 != 0) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)div_ceil(m, (size_t)16), (unsigned)div_ceil(kb, (size_t)QK_CH));
-    hipLaunchKernelGGL(quantize_known_kernel, grid, dim3(256), 0, s, h, ldh, m, (int)n, (int)kb, tmax, strips, qa, exps);
+    const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8), ny = div_ceil(kb, (size_t)QK_CH);
+    hipLaunchKernelGGL(quantize_known_kernel, dim3((unsigned)(8 * bpx * ny)), dim3(256), 0, s, h, ldh, m, (int)n,
+                       (int)kb, tmax, strips, qa, exps, bpx, (int)ny);
     return hipGetLastError();
 }
 
@@ -765,11 +771,15 @@ __global__ __launch_bounds__(64) void layer_norm4_kernel(const float *x, size_t 
                                                          const float *__restrict__ gamma,
                                                          const float *__restrict__ beta, float eps, float *out,
                                                          size_t ldo, uint8_t *__restrict__ qa,
-                                                         int32_t *__restrict__ exps, int kb, int vec) {
+                                                         int32_t *__restrict__ exps, int kb, int vec, size_t bpx) {
     __shared__ __attribute__((aligned(16))) float rows_s[4 * LN4_ROW];
     __shared__ float stat[4][2];
     const int lane = threadIdx.x;
-    const size_t row0 = (size_t)blockIdx.x * 4;
+    // Workgroup L runs on XCD L % 8; XCD x takes 16-row blocks x bpx .. x bpx + bpx - 1, four
+    // workgroups a block, the rows a product's tiles leave in that XCD's L2.
+    const size_t xg = blockIdx.x % 8, gi = blockIdx.x / 8;
+    const size_t row0 = (xg * bpx + gi / 4) * 16 + (gi % 4) * 4;
+    if (row0 >= (qa ? (m + 15) / 16 * 16 : m)) return;  // uniform
     {
         const int r = lane >> 4, j = lane & 15;
         const size_t row = row0 + r;
@@ -916,10 +926,11 @@ hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, co
     const size_t kb = div_ceil(n, KBLK);
     const int vec = ((reinterpret_cast<uintptr_t>(x) | ldx * sizeof(float) | reinterpret_cast<uintptr_t>(gamma) |
                       reinterpret_cast<uintptr_t>(beta)) % 16 == 0);
-    // Workgroups of four rows; a row block of 16 rows whose rows past m still get their zero digits.
-    const size_t groups = qa ? div_ceil(m, (size_t)16) * 4 : div_ceil(m, (size_t)4);
-    hipLaunchKernelGGL(layer_norm4_kernel, dim3((unsigned)groups), dim3(64), 0, s, x, ldx, m, (int)n, gamma, beta, eps,
-                       out, ldo, qa, exps, (int)kb, vec);
+    // Workgroups of four rows, four a 16-row block (whose rows past m still get their zero digits),
+    // bpx blocks per XCD.
+    const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
+    hipLaunchKernelGGL(layer_norm4_kernel, dim3((unsigned)(8 * bpx * 4)), dim3(64), 0, s, x, ldx, m, (int)n, gamma,
+                       beta, eps, out, ldo, qa, exps, (int)kb, vec, bpx);
     return hipGetLastError();
 }
 
