@@ -28,7 +28,8 @@ integer oracle composed in the same order reproduces it bit for bit. Q8_0 matric
 entry points; for them the quantised-output product and the quantised GLU run the product into a
 context buffer and then the quantiser or the GLU kernel (the same bits as the two calls).
 Batches of equal-length utterances are stacked along the rows; only the depthwise convolution sees
-the boundaries."""
+the boundaries. The matrices must be int8 or Q8_0, the staged entry points' precisions; a layer
+holding another precision raises ValueError before any launch."""
 from __future__ import annotations
 
 from dataclasses import dataclass
@@ -75,7 +76,7 @@ class ConformerLayer:
         self.qkv = f32(rows, 3 * d)
         self.glu = f32(rows, d)
         self.conv = f32(rows, d)
-        self._f32 = {}  # f32 rows of the unfused steps (weights other than int8), made on first use
+        self._f32 = {}  # f32 rows of the unfused feed-forward, made on first use
 
     def _rows(self, name: str, width: int):
         import torch
@@ -99,21 +100,20 @@ class ConformerLayer:
         half_acc = Epilogue(scale=0.5, accumulate=True)
         acc = Epilogue(accumulate=True)
 
+        for name, mat in m.items():
+            if mat.precision() not in (Precision.INT8, Precision.Q8_0):
+                raise ValueError(f"the device layer takes int8 or Q8_0 matrices ({name} is {mat.precision().name})")
+
         def feed_forward(norm, w_in, w_out):
             g, b = w.norms[norm]
             k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-            if m[w_in].precision() in (Precision.INT8, Precision.Q8_0) and self.quantised_hidden:
+            if self.quantised_hidden:
                 k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, m[w_in], self.qa_ff, self.ex_ff, silu)
-                k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
-            elif m[w_in].precision() == Precision.INT8:
+            else:  # the same bits through f32 rows and the row quantiser
                 hid = self._rows("hid", ff)[:t]
                 k.matmul_quantized_device(self.qa_d, self.ex_d, t, m[w_in], hid, ff, silu)
                 k.quantize_rows_device(hid, ff, t, ff, self.qa_ff, self.ex_ff)
-                k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
-            else:  # other precisions: the hidden rows go through f32 and tg_linear_device
-                hid = self._rows("hid", ff)[:t]
-                k.matmul_quantized_device(self.qa_d, self.ex_d, t, m[w_in], hid, ff, silu)
-                k.linear_device(hid, t, m[w_out], x, half_acc)
+            k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
 
         feed_forward("norm_ff1", "ff1_in", "ff1_out")
         # self-attention: q, k, v in f32 for the attention core
@@ -132,14 +132,9 @@ class ConformerLayer:
         # convolution module
         g, b = w.norms["norm_conv"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-        if m["pw1"].precision() in (Precision.INT8, Precision.Q8_0):
-            k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], d)
-        else:
-            g2 = self._rows("pw1", 2 * d)[:t]
-            k.matmul_quantized_device(self.qa_d, self.ex_d, t, m["pw1"], g2, 2 * d)
-            k.glu_device(g2, 2 * d, t, d, self.glu, d, out_len=t * d)
+        k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], d)
         # the convolution writes its rows quantised for pw2 when the fused kernel takes the shape
-        if m["pw2"].precision() in (Precision.INT8, Precision.Q8_0) and k.dwconv1d_quant_device(
+        if k.dwconv1d_quant_device(
                 self.glu, d, t // utterances, d, w.dw_w, self.conv_kernel, w.dw_b, self.qa_d, self.ex_d,
                 act=Act.SILU, batch=utterances, x_len=t * d):
             k.matmul_quantized_device(self.qa_d, self.ex_d, t, m["pw2"], x, d, acc)

@@ -32,7 +32,8 @@ accumulating epilogue adds the same value (scale 1 is exact), so the bits are th
 Each step writes what its unfused calls write (LayerNorm then quantise, product then quantise), so the
 block is the reference's sequence evaluated with the fast path's products: the integer oracle composed
 in the same order reproduces it bit for bit. Batches of equal-length utterances are stacked along the
-rows; only the depthwise convolution and the pooling see the boundaries."""
+rows; only the depthwise convolution and the pooling see the boundaries. The matrices must be int8
+or Q8_0; a block holding another precision raises ValueError before any launch."""
 from __future__ import annotations
 
 from dataclasses import dataclass
@@ -79,30 +80,17 @@ class GraniteBlock:
         self.qkv = f32(rows, 3 * d)
         self.glu = f32(rows, conv_channels)
         self.conv = f32(rows, conv_channels)
-        self._f32 = {}
-
-    def _rows(self, name: str, width: int):
-        import torch
-
-        if name not in self._f32:
-            self._f32[name] = torch.empty((self.rows, width), dtype=torch.float32, device="cuda")
-        return self._f32[name]
 
     def _feed_forward(self, x, t: int, w: BlockWeights, which: str) -> None:
         """x += 0.5 * (down(silu(up(norm(x)) + up.b)) + down.b) (src/granite.rs:752-793)."""
-        k, d, ff = self.kern, self.d, self.ff
+        k, d = self.kern, self.d
         g, b = w.norms[which + "_norm"]
         up, down = w.mats[which + "_up"], w.mats[which + "_down"]
         k.layer_norm_quant_device(x, d, t, d, g, b, self.eps, self.qa_d, self.ex_d)
         silu = Epilogue(bias=w.biases[which + "_up"], act=Act.SILU)
         half_acc = Epilogue(bias=w.biases[which + "_down"], scale=0.5, accumulate=True)
-        if up.precision() in (Precision.INT8, Precision.Q8_0):
-            k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, up, self.qa_ff, self.ex_ff, silu)
-            k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, down, x, d, half_acc)
-        else:  # other precisions: the hidden rows go through f32 and tg_linear_device
-            hid = self._rows("hid", ff)[:t]
-            k.matmul_quantized_device(self.qa_d, self.ex_d, t, up, hid, ff, silu)
-            k.linear_device(hid, t, down, x, half_acc)
+        k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, up, self.qa_ff, self.ex_ff, silu)
+        k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, down, x, d, half_acc)
 
     def forward(self, x, t: int, w: BlockWeights, utterances: int = 1, attention: Optional[Callable] = None,
                 out=None):
@@ -120,6 +108,9 @@ class GraniteBlock:
             raise ValueError("t must fit the block's rows and split into equal utterances")
         frames = t // utterances
         m = w.mats
+        for name, mat in m.items():
+            if mat.precision() not in (Precision.INT8, Precision.Q8_0):
+                raise ValueError(f"the device block takes int8 or Q8_0 matrices ({name} is {mat.precision().name})")
         self._feed_forward(x, t, w, "ff1")
         g, b = w.norms["norm_att"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
@@ -135,13 +126,8 @@ class GraniteBlock:
         # convolution module over the post-attention states of all t frames
         g, b = w.norms["norm_conv"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
-        pw1 = Epilogue(bias=w.biases["pw1"])
-        if m["pw1"].precision() in (Precision.INT8, Precision.Q8_0):
-            k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], cc, epi=pw1)
-        else:
-            g2 = self._rows("pw1", 2 * cc)[:t]
-            k.matmul_quantized_device(self.qa_d, self.ex_d, t, m["pw1"], g2, 2 * cc, pw1)
-            k.glu_device(g2, 2 * cc, t, cc, self.glu, cc, out_len=t * cc)
+        k.matmul_quantized_glu_device(self.qa_d, self.ex_d, t, m["pw1"], self.glu[:t], cc,
+                                      epi=Epilogue(bias=w.biases["pw1"]))
         if w.strided:
             rows = frames // 2
             n = rows * utterances

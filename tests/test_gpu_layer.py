@@ -128,15 +128,17 @@ def test_one_600_s_utterance(tk, orc):
         assert err <= 1e-3
 
 
-def test_q8_0_layer_at_750_frames(tk, orc):
-    """The layer with Q8_0 matrices (Parakeet's recommended precision), the Q8_0 GEMM everywhere, the
-    quantised-output feed-forward and the quantised GLU product included, against the oracle
-    composition with the Q8_0 integer oracle."""
+@pytest.mark.parametrize("quantised_hidden", [True, False])
+def test_q8_0_layer_at_750_frames(tk, orc, quantised_hidden):
+    """The layer with Q8_0 matrices (Parakeet's recommended precision), the Q8_0 GEMM everywhere and
+    the quantised GLU product, the feed-forward's hidden rows through the quantised-output product
+    or through f32 rows and the row quantiser, against the oracle composition with the Q8_0 integer
+    oracle."""
     mats, norms, dw_w, dw_b = bench.layer_params(1400, precision=4)
     x = bench.synth_normal((750, D), 15)
-    say("layer q8_0", 750)
+    say("layer q8_0", 750, "quantised hidden" if quantised_hidden else "f32 hidden")
     w = device_layer(tk, mats, norms, dw_w, dw_b, precision=4)
-    got = run_device(tk, [w], x, 1, quantised_hidden=True)
+    got = run_device(tk, [w], x, 1, quantised_hidden=quantised_hidden)
     close([w])
     want = layer_oracle.oracle_layer(orc, x, mats, norms, dw_w, dw_b, fast=True, precision=4)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -144,6 +146,28 @@ def test_q8_0_layer_at_750_frames(tk, orc):
     err = rel_norm_err(got, ref)
     print(f"[err] the Q8_0 layer at T=750 against the f32 reference: {err:.3e}", flush=True)
     assert err <= 1e-3
+
+
+def test_layer_refuses_other_precisions(tk):
+    """The device layer's products are the staged entry points, which take int8 and Q8_0 matrices:
+    a layer holding another precision is refused before any launch."""
+    import torch
+
+    import telmo_amd
+    from telmo_amd.conformer import ConformerLayer
+
+    mats, norms, dw_w, dw_b = bench.layer_params(1700)
+    w = device_layer(tk, mats, norms, dw_w, dw_b)
+    _, _, n, k = mats["ff1_in"]
+    f16 = telmo_amd.PackedWeights.from_parts(tk, n, k, telmo_amd.Precision.F16,
+                                             np.zeros(-(-n // 16) * 16 * k * 2, np.uint8))
+    w.mats["ff1_in"].close()
+    w.mats["ff1_in"] = f16
+    layer = ConformerLayer(tk, D, FF, K, 64)
+    x = torch.zeros((64, D), device="cuda")
+    with pytest.raises(ValueError, match="int8 or Q8_0"):
+        layer.forward(x, 64, w)
+    close([w])
 
 
 def test_position_projection(tk, orc):
