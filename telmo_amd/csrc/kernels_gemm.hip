@@ -1064,10 +1064,11 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512) {
         // 48-row tiles when their workgroups (one per CU) fit the chip in one round: every CU
         // busy and a quarter less work each (750 x 4096 -> 1024: 192 -> 256 workgroups, 15.7 ->
-        // 14.2 us); else 64-row tiles (at 1000 rows 336 workgroups would take two rounds: 25
-        // against 16.4 us).
+        // 14.2 us), with a six-stage register ring (four, five, seven, eight stages: 15.9, 15.1,
+        // 14.9, 15.5 against 14.1 us); else 64-row tiles (at 1000 rows 336 workgroups would take
+        // two rounds: 25 against 16.4 us).
         if (div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
-            return launch_kq<3, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+            return launch_kq<3, 6, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
         return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     }
     // The direct kernel: 64 x 64 tiles when they give about one workgroup per CU (161 to 256 of
