@@ -204,10 +204,11 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
  * to the two calls. For a feed-forward block's first product, whose only reader is the second
  * (src/parakeet.rs:1024-1060: ff_in with SiLU into s.big, then ff_out), which then takes qa_out
  * through tg_matmul_quantized_device. The f32 rows go through a context workspace of about 4 m n
- * bytes, grown on first use. Without activation or scale the product also leaves each row's largest
- * |y| per tile column, so the quantiser streams the rows once without a reduction; from 2048 rows an
- * activation and scale are applied by the quantiser as it loads the product's biased sums, off the
- * MFMA loop. Q8_0 weights run the product and then the row quantiser. int8 or Q8_0 weights, fast
+ * bytes, grown on first use. Without activation or scale an int8 product also leaves each row's
+ * largest |y| per tile column, so the quantiser streams the rows once without a reduction. With
+ * them, or with Q8_0 weights, the product's f32 rows go through the row quantiser, and from 2048 rows
+ * the activation and scale are applied by the quantiser as it loads the product's biased sums, off
+ * the MFMA loop (below that, in the product's epilogue). int8 or Q8_0 weights, fast
  * mode, no accumulation
  * (TG_ERR_ARG), n <= 65536. Calls on one context share the workspace; they run in order on its
  * stream. Device pointers, queued on the stream. No counterpart in the reference, whose sums are all

@@ -691,8 +691,10 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
     return TG_OK;
 }
 
-// Rows from which the quantised-output product leaves its activation to the quantiser (measured:
-// 212 against 228 us at 12000 x 1024 -> 4096 with SiLU, 25.4 against 23.9 us at 750 rows).
+// Rows from which the quantised-output product leaves an activation or a scale to the quantiser
+// rather than to its own epilogue (1024 -> 4096 with SiLU, measured: at 12000 rows 212 us against
+// 228 for the product that gathers row maxima; at 750 rows 20.6 us in the epilogue, 21.9 in the
+// quantiser, 22.2 with the row maxima).
 constexpr size_t QOUT_ACT_ROWS = 2048;
 
 int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
@@ -725,26 +727,23 @@ int tg_matmul_quantized_to_quant_device(tg_ctx *ctx, const void *qa, size_t qa_l
     const tg::EpiArgs ea = epi_args(epi, nullptr, false);
     int rc;
     if ((rc = grow(ctx, ctx->hid, ctx->hid_cap, m * ldh * sizeof(float)))) return rc;
-    if (q8) {
-        // Q8_0: the product's rows, then the row quantiser; the activation and scale go to the
-        // quantiser from QOUT_ACT_ROWS rows as for int8.
-        const bool later = (ea.act != tg::ACT_NONE || ea.scale != 1.0f) && m >= QOUT_ACT_ROWS;
+    const bool shaped = ea.act != tg::ACT_NONE || ea.scale != 1.0f;
+    if (q8 || shaped) {
+        // The product's f32 rows, then the row quantiser: for Q8_0 weights (the product that gathers
+        // row maxima is int8 only), and for an activation or a scale other than 1. From QOUT_ACT_ROWS
+        // rows those are VALU work that the product's epilogue adds to its MFMA loop, where it is not
+        // hidden; the quantiser then applies them to each input as it loads it (the same f32
+        // operations on the same values), under its memory time, and the product writes only the
+        // biased sums.
+        const bool later = shaped && m >= QOUT_ACT_ROWS;
         const tg::EpiArgs first = later ? tg::EpiArgs{ea.bias, tg::ACT_NONE, 1.0f, 0} : ea;
         TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, ctx->hid, ldh, first,
                                        ctx->stream));
         TG_HIP(ctx, tg::launch_quantize_rows(ctx->hid, ldh, m, n, static_cast<uint8_t *>(qa_out), exps_out,
                                              ctx->stream, later ? tg::RowAct{ea.act, ea.scale} : tg::RowAct{}));
-    } else if ((ea.act != tg::ACT_NONE || ea.scale != 1.0f) && m >= QOUT_ACT_ROWS) {
-        // The activation and the scale are VALU work that the product's epilogue adds to its MFMA
-        // loop, where it is not hidden at this many rows; the quantiser applies them to each input
-        // as it loads it (the same f32 operations on the same values), under its HBM time, and the
-        // product writes only the biased sums.
-        const tg::EpiArgs biased{ea.bias, tg::ACT_NONE, 1.0f, 0};
-        TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, ctx->hid, ldh, biased,
-                                       ctx->stream));
-        TG_HIP(ctx, tg::launch_quantize_rows(ctx->hid, ldh, m, n, static_cast<uint8_t *>(qa_out), exps_out,
-                                             ctx->stream, tg::RowAct{ea.act, ea.scale}));
     } else {
+        // The identity epilogue (a bias at most): the product keeps each row's largest magnitude per
+        // column strip, and the quantiser reads those instead of a pass over the row.
         if ((rc = grow(ctx, ctx->tmax, ctx->tmax_cap, m * (size_t)strips * sizeof(uint32_t)))) return rc;
         TG_HIP(ctx, tg::launch_gemm_i8_qout(static_cast<const uint8_t *>(qa), exps, m, w->d, ea, ctx->hid, ldh,
                                             ctx->tmax, ctx->stream));

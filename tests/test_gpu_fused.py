@@ -79,9 +79,10 @@ def test_layer_norm_quant_is_layer_norm_then_quantise(tk, m, n, ldx):
     assert torch.equal(qa2, want_qa)
 
 
-# m, k, n, act, with_bias, scale. From 2048 rows an activation or a scale other than 1 is applied by
-# the quantiser as it loads the product's biased sums (SiLU, ReLU with a scale, a negative scale
-# alone); otherwise the quantiser takes the row maxima from the product.
+# m, k, n, act, with_bias, scale. An activation or a scale other than 1 is applied by the product's
+# epilogue below 2048 rows and by the quantiser, as it loads the product's biased sums, from there
+# (SiLU, ReLU with a scale, a negative scale alone); with neither, the quantiser takes the row maxima
+# from the product.
 QOUT_CASES = [
     (750, 1024, 4096, 2, False, 1.0), (12000, 1024, 4096, 2, False, 1.0), (7500, 1024, 4096, 2, False, 0.75),
     (750, 1024, 4096, 0, True, 1.0), (12000, 1024, 4096, 0, False, 1.0),
