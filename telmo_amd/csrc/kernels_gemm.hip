@@ -1054,11 +1054,19 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     }
     if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     // Mid-size products: LDS staging pays from 2048 outputs (the direct kernel's duplicate operand
-    // loads dominate there). Narrower ones take 128 x 128 tiles once there are 256 of them (one
-    // per CU: 7500 x 4096 -> 1024 runs 81 us against 123 us on the direct kernel), else the
-    // direct kernel, or the k-split kernel when the inputs are long (at least 32 k-blocks) and
-    // the tiles too few to fill the CUs twice.
-    if (w.panels >= 128) return launch_lds<4, 4, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+    // loads dominate there), on 128 x 128 tiles from 384 of them (each tile's operands copied once
+    // for four times the 64 x 64 tile's work: 2000 x 1024 -> 4096 25.4 against 29.6 us, 3000 rows
+    // 39.8 against 44.0, 1500 rows 23.0 against 24.9; at 256-288 tiles, 1000 x 1024 -> 4096 and
+    // 1500 x 1024 -> 3072, the 64 x 64 tiles' fuller chip wins: 15.7 against 16.9, 20.6 against
+    // 21.4 us). Narrower ones take 128 x 128 tiles once there are 256 of them (one per CU: 7500 x
+    // 4096 -> 1024 runs 81 us against 123 us on the direct kernel), else the direct kernel, or the
+    // k-split kernel when the inputs are long (at least 32 k-blocks) and the tiles too few to fill
+    // the CUs twice.
+    if (w.panels >= 128) {
+        if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 384)
+            return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_lds<4, 4, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+    }
     if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 256)
         return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     if (w.kb >= 32 && div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 512) {
@@ -1095,9 +1103,10 @@ hipError_t launch_gemm_i8_qout(const uint8_t *qf, const int32_t *exps, size_t m,
     return launch_lds<4, 4, 3, 1, 0, 0, 1>(qf, exps, m, w, h, ldh, epi, s, q);
 }
 
-// The GLU-fused product: 128 x 128 tiles (four panels of each half) when they fill the chip twice
-// over and the half has a multiple of 64 outputs, else 64 x 64 tiles (two panels of each half),
-// which need a multiple of 32.
+// The GLU-fused product: 128 x 128 tiles (four panels of each half) from 512 of them when the half
+// has a multiple of 64 outputs, else 64 x 64 tiles (two panels of each half), which need a multiple
+// of 32 (x 1024 -> 2048: 7500 rows 43.0 against 49.2 us, 6000 rows 36.0 against 39.3; at 3000
+// rows, 384 tiles, 21.4 against 20.8).
 bool gemm_glu_fits(size_t n) { return n % 64 == 0; }
 
 hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *out,
@@ -1105,7 +1114,7 @@ hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, 
     if (m == 0 || w.n == 0) return hipSuccess;
     if (w.precision != INT8 || !gemm_glu_fits(w.n)) return hipErrorInvalidValue;
     const size_t half = w.n / 2;
-    if (half % 64 == 0 && gemm_tile_choice(m, w.panels) == 0)
+    if (half % 64 == 0 && div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 512)
         return launch_lds<8, 8, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
     return launch_lds<4, 4, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
 }

@@ -544,10 +544,11 @@ def test_pack_matrices_upload_like_their_parts(tk, tmp_path):
         pack.matrix(tk, "nope", 2, 3)
 
 
-@pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384), (4100, 200, 1000), (4100, 1000, 1000)])
+@pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384), (2000, 320, 4100), (4100, 200, 1000),
+                                   (4100, 1000, 1000)])
 def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
-    """Products that fill the chip with 128 x 128 tiles (>= 1024 of them), and narrow products
-    (< 2048 outputs) with >= 256 of them, run the 128 x 128 LDS-staged GEMM; partial edge tiles in
+    """Products of 2048 outputs or more with >= 384 128 x 128 tiles (2000 x 4100: 16 x 33), and
+    narrow products (< 2048 outputs) with >= 256 of them, run the 128 x 128 LDS-staged GEMM; partial edge tiles in
     both directions, every epilogue, bit-identical to the integer oracle. k = 1000 (16 k-blocks)
     goes round the three-stage ring five times and ends on a partial round."""
     rng = np.random.default_rng(m + k + n)
@@ -698,8 +699,8 @@ def test_row_fixtures(tk):
 # (m, k, n, ldo): the M=750 layer's pw1 (64 x 64 GLU tiles), 128 x 128 GLU tiles, ragged rows and
 # inputs, strided and unaligned outputs, and products the fused kernel does not take (n % 64 != 0,
 # GEMV rows), which go through the context's buffer.
-GLU_SHAPES = [(750, 1024, 2048, 1024), (1100, 200, 16384, 8192), (37, 200, 256, 130), (130, 64, 128, 64),
-              (300, 100, 96, 48), (5, 64, 128, 64)]
+GLU_SHAPES = [(750, 1024, 2048, 1024), (1100, 200, 16384, 8192), (4100, 64, 2048, 1030), (37, 200, 256, 130),
+              (130, 64, 128, 64), (300, 100, 96, 48), (5, 64, 128, 64)]
 
 
 @pytest.mark.parametrize("m,k,n,ldo", GLU_SHAPES)
