@@ -14,10 +14,12 @@ eight products int8 with per-output scales (the north star's layer projection se
 
 run as telmo_amd.conformer.ConformerLayer runs it: the five LayerNorms write quantised rows, FF in
 writes quantised hidden rows, pw1 carries the GLU in its epilogue. The LayerNorms, GLU and
-convolution are extra work beside the projection set, inside the timed step. Each step first
-restores the layer input (a 3 MB device copy). The step is timed launched eagerly on one stream
-and replayed as a captured HIP graph; the faster is the step time. value = 2 sum(M N K) over the
-eight products / step time, in TOPS. Inputs come from telmo's test generator (seeded xorshift,
+convolution are extra work beside the projection set, inside the timed step. Each step is one layer
+of a stack, applied in place to the previous step's outputs: it starts from the quantised rows of
+its first LayerNorm, which the previous step left, and ends with the layer boundary (its last
+LayerNorm and the next layer's first in one launch). The step is timed launched eagerly on one
+stream and replayed as a captured HIP graph; the faster is the step time. value = 2 sum(M N K) over
+the eight products / step time, in TOPS. Inputs come from telmo's test generator (seeded xorshift,
 src/kernels/mod.rs:795-805): synthetic data of the configs' distributions, random weights.
 
 The JSON line also carries:
@@ -304,10 +306,18 @@ def gpu_leg(args, params, x0_host):
     x0 = torch.from_numpy(x0_host).cuda()
     x = x0.clone()
 
+    # One layer of a stack: it starts from the quantised rows of its first LayerNorm (norm_ff1), which
+    # the previous layer's boundary left, and ends with the boundary (its norm_out in place and the
+    # next layer's norm_ff1 in one launch); the same layer stands for the next one.
     def step(_):
-        layer.forward(x, T, w)
+        layer.forward(x, T, w, prepared=True, next_norm=w.norms["norm_ff1"])
 
-    eager_ms, graph_ms = step_times(stream, step, args.steps, args.warmup, lambda: x.clone(), lambda: x.copy_(x0))
+    def reset():
+        x.copy_(x0)
+        layer.prepare(x, T, w)
+
+    reset()
+    eager_ms, graph_ms = step_times(stream, step, args.steps, args.warmup, lambda: x.clone(), reset)
     if not torch.isfinite(x).all():
         raise RuntimeError("the layer output is not finite")
 
@@ -399,8 +409,7 @@ def encoder_leg(args):
         x = x0.clone()
 
         def run(_):
-            for w in layers:
-                stack.forward(x, M, w, utterances=utt)
+            stack.run_stack(x, M, layers, utterances=utt)
 
         eager_ms, graph_ms = step_times(stream, run, 3, 1, lambda: x.clone(), lambda: x.copy_(x0))
         if not torch.isfinite(x).all():
@@ -514,9 +523,14 @@ def q8_leg(args):
     x = x0.clone()
 
     def step(_):  # in place on the previous step's outputs, as the int8 step is timed
-        layer.forward(x, T, w)
+        layer.forward(x, T, w, prepared=True, next_norm=w.norms["norm_ff1"])
 
-    eager_ms, graph_ms = step_times(stream, step, 200, 10, lambda: x.clone(), lambda: x.copy_(x0))
+    def reset():
+        x.copy_(x0)
+        layer.prepare(x, T, w)
+
+    reset()
+    eager_ms, graph_ms = step_times(stream, step, 200, 10, lambda: x.clone(), reset)
     t = min(eager_ms, graph_ms) * 1e-3
     out = {"layer_step": {"workload": "the device Conformer layer at T=750, Q8_0 weights",
                           "ms_per_step": round(t * 1e3, 4), "ms_per_step_eager": round(eager_ms, 4),

@@ -275,6 +275,20 @@ int tg_layer_norm_quant_device(tg_ctx *ctx, const float *x, size_t x_len, size_t
                                float *out, size_t out_len, size_t ldo, void *qa, size_t qa_len, int32_t *exps,
                                size_t exps_len);
 
+/* A stack's layer boundary in one call: x = LayerNorm(x; gamma, beta, eps) in place, as
+ * tg_layer_norm_device writes it (a layer's last LayerNorm, norm_out, src/parakeet.rs:1168-1170),
+ * then the quantised rows of LayerNorm(x; gamma2, beta2, eps2), as tg_layer_norm_quant_device
+ * writes them (the next layer's first, norm_ff1, src/parakeet.rs:1026; the layers run in turn at
+ * 893-894): bit-identical to those two calls.
+ * Rows of at most 1024 values (a multiple of 4, 16-byte aligned) below 2048 rows take one launch
+ * that reads each row once; other shapes run the two calls. n <= 65536. Device pointers, queued on
+ * the stream. No counterpart in the reference, which runs the two LayerNorms as two calls. */
+int tg_layer_norm_pair_quant_device(tg_ctx *ctx, float *x, size_t x_len, size_t ldx, size_t m, size_t n,
+                                    const float *gamma, size_t gamma_len, const float *beta, size_t beta_len,
+                                    float eps, const float *gamma2, size_t gamma2_len, const float *beta2,
+                                    size_t beta2_len, float eps2, void *qa, size_t qa_len, int32_t *exps,
+                                    size_t exps_len);
+
 /* Depthwise 1-D convolution of frames x channels rows, "same" zero padding: output row r is frame
  * t = t0 + r * stride, out[r, c] = bias[c] + sum over taps j in order of w[j * channels + c] *
  * x[t + j - kernel/2, c], each term a rounded product and a rounded sum, taps outside [0, frames)

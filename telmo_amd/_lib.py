@@ -69,6 +69,8 @@ SIGNATURES = {
                                              _sz]),
     "tg_layer_norm_quant_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, ctypes.c_float, _p,
                                                    _sz, _sz, _p, _sz, _p, _sz]),
+    "tg_layer_norm_pair_quant_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _p, _sz, _p, _sz, ctypes.c_float,
+                                                        _p, _sz, _p, _sz, ctypes.c_float, _p, _sz, _p, _sz]),
     "tg_dwconv1d_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p, _sz, _sz, _sz, _sz,
                                            _u32, _p, _sz, _sz]),
     "tg_dwconv1d_quant_device": (ctypes.c_int, [_p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _sz, _p, _sz, _u32, _p,

@@ -20,7 +20,11 @@ quantised wherever the product is their only reader:
                                        utterance on its own)
           pw2, x += .                                          tg_matmul_quantized_device
     FF2   as FF1 with norm_ff2, ff2_in, ff2_out
-    out   LayerNorm(norm_out), in place
+    out   LayerNorm(norm_out), in place                        tg_layer_norm_device
+
+In a stack (``run_stack``) a layer boundary is one call: the layer's norm_out in place and the next
+layer's norm_ff1 quantised, tg_layer_norm_pair_quant_device (one launch below 2048 rows of up to
+1024 values), and the next layer starts from those quantised rows (``prepared``).
 
 Each step writes exactly the bits the unfused calls write (LayerNorm then quantise, product then
 quantise), so the layer is the reference's sequence evaluated with the fast path's products: the
@@ -85,13 +89,31 @@ class ConformerLayer:
             self._f32[name] = torch.empty((self.rows, width), dtype=torch.float32, device="cuda")
         return self._f32[name]
 
+    def prepare(self, x, t: int, w: LayerWeights) -> None:
+        """The quantised rows of the layer's first LayerNorm (norm_ff1) of x, for forward(prepared=True)."""
+        g, b = w.norms["norm_ff1"]
+        self.kern.layer_norm_quant_device(x, self.d, t, self.d, g, b, self.eps, self.qa_d, self.ex_d)
+
+    def run_stack(self, x, t: int, layers, utterances: int = 1, attention: Optional[Callable] = None) -> None:
+        """The layers in turn on x (the reference's encode loop, src/parakeet.rs:893-894), each boundary
+        between two layers as one call: norm_out of one and norm_ff1 of the next."""
+        for i, w in enumerate(layers):
+            nxt = layers[i + 1].norms["norm_ff1"] if i + 1 < len(layers) else None
+            self.forward(x, t, w, utterances=utterances, attention=attention, prepared=i > 0, next_norm=nxt)
+
     def forward(self, x, t: int, w: LayerWeights, utterances: int = 1,
-                attention: Optional[Callable] = None, pos=None, p_out=None) -> None:
+                attention: Optional[Callable] = None, pos=None, p_out=None, prepared: bool = False,
+                next_norm: Optional[tuple] = None) -> None:
         """x: [t, d] float32 GPU tensor (the layer's input rows, updated in place); t frames in all,
         `utterances` equal-length utterances stacked along the rows. attention(qkv, p) -> att returns
         the heads' outputs [t, d] (rows at any stride, as a tensor view) from the f32 q, k, v rows and
         the projected positions; None uses the V third of qkv as the stand-in. pos ([2 t - 1, d] per
-        utterance) and p_out receive the position projection when both are given."""
+        utterance) and p_out receive the position projection when both are given.
+
+        prepared: the quantised rows of norm_ff1(x) are already in the layer's buffers (prepare(), or
+        the previous layer's boundary), so the first LayerNorm is not run again. next_norm: the next
+        layer's norm_ff1 (gamma, beta); the last LayerNorm then also leaves that LayerNorm's quantised
+        rows of the output for the next forward(prepared=True) on this object."""
         k, d, ff, eps = self.kern, self.d, self.ff, self.eps
         if t > self.rows or t % utterances:
             raise ValueError("t must fit the layer's rows and split into equal utterances")
@@ -104,9 +126,10 @@ class ConformerLayer:
             if mat.precision() not in (Precision.INT8, Precision.Q8_0):
                 raise ValueError(f"the device layer takes int8 or Q8_0 matrices ({name} is {mat.precision().name})")
 
-        def feed_forward(norm, w_in, w_out):
+        def feed_forward(norm, w_in, w_out, ready=False):
             g, b = w.norms[norm]
-            k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
+            if not ready:
+                k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
             if self.quantised_hidden:
                 k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, m[w_in], self.qa_ff, self.ex_ff, silu)
             else:  # the same bits through f32 rows and the row quantiser
@@ -115,7 +138,7 @@ class ConformerLayer:
                 k.quantize_rows_device(hid, ff, t, ff, self.qa_ff, self.ex_ff)
             k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, m[w_out], x, d, half_acc)
 
-        feed_forward("norm_ff1", "ff1_in", "ff1_out")
+        feed_forward("norm_ff1", "ff1_in", "ff1_out", ready=prepared)
         # self-attention: q, k, v in f32 for the attention core
         g, b = w.norms["norm_att"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
@@ -144,4 +167,8 @@ class ConformerLayer:
             k.linear_device(self.conv[:t], t, m["pw2"], x, acc)
         feed_forward("norm_ff2", "ff2_in", "ff2_out")
         g, b = w.norms["norm_out"]
-        k.layer_norm_device(x, d, t, d, g, b, eps, x, d)
+        if next_norm is None:
+            k.layer_norm_device(x, d, t, d, g, b, eps, x, d)
+        else:
+            g2, b2 = next_norm
+            k.layer_norm_pair_quant_device(x, d, t, d, g, b, eps, g2, b2, eps, self.qa_d, self.ex_d)

@@ -814,6 +814,31 @@ int tg_layer_norm_quant_device(tg_ctx *ctx, const float *x, size_t x_len, size_t
     return TG_OK;
 }
 
+int tg_layer_norm_pair_quant_device(tg_ctx *ctx, float *x, size_t x_len, size_t ldx, size_t m, size_t n,
+                                    const float *gamma, size_t gamma_len, const float *beta, size_t beta_len,
+                                    float eps, const float *gamma2, size_t gamma2_len, const float *beta2,
+                                    size_t beta2_len, float eps2, void *qa, size_t qa_len, int32_t *exps,
+                                    size_t exps_len) {
+    if (!ctx) return TG_ERR_NULL;
+    if (m == 0) return TG_OK;
+    if (!x || !gamma || !beta || !gamma2 || !beta2 || !qa || !exps) return fail(ctx, TG_ERR_NULL, "null buffer");
+    if (n == 0) return fail(ctx, TG_ERR_SHAPE, "rows of no values have no LayerNorm to quantise");
+    if (ldx < n) return fail(ctx, TG_ERR_SHAPE, "ldx must be >= n");
+    if (x_len < span(m, ldx, n)) return fail(ctx, TG_ERR_SHAPE, "x is too short");
+    if (gamma_len < n || beta_len < n || gamma2_len < n || beta2_len < n)
+        return fail(ctx, TG_ERR_SHAPE, "gamma, beta, gamma2 and beta2 must hold n values");
+    if (qa_len < tg_quant_bytes(m, n)) return fail(ctx, TG_ERR_SHAPE, "qa is too short");
+    if (exps_len < m) return fail(ctx, TG_ERR_SHAPE, "exps must hold m exponents");
+    if (n > tg::MAX_K_INT) return fail(ctx, TG_ERR_UNSUPPORTED, "rows beyond the integer path's limit (65536)");
+    if (m > (size_t)INT32_MAX) return fail(ctx, TG_ERR_UNSUPPORTED, "more than 2^31 - 1 rows");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    TG_HIP(ctx, hipSetDevice(ctx->device));
+    TG_HIP(ctx, tg::launch_layer_norm_pair(x, ldx, m, n, gamma, beta, eps, x, ldx, gamma2, beta2, eps2,
+                                           static_cast<uint8_t *>(qa), exps, ctx->stream));
+    clear_error(ctx);
+    return TG_OK;
+}
+
 int tg_glu_device(tg_ctx *ctx, const float *x, size_t x_len, size_t ldx, size_t m, size_t half, float *out,
                   size_t out_len, size_t ldo) {
     if (!ctx) return TG_ERR_NULL;

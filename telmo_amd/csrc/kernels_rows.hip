@@ -600,7 +600,8 @@ hipError_t launch_layer_norm4(const float *x, size_t ldx, size_t m, size_t n, co
                               float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps, hipStream_t s);
 hipError_t launch_layer_norm_row(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                   const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
-                                  hipStream_t s);
+                                  hipStream_t s, const float *gamma2 = nullptr, const float *beta2 = nullptr,
+                                  float eps2 = 0.0f);
 
 hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, const float *gamma, const float *beta,
                              float eps, float *out, size_t ldo, hipStream_t s) {
@@ -951,12 +952,60 @@ constexpr int LNQ_MAX = 1024;
 // Rows are spread over the XCDs in 16-row blocks as quantize_rows_regs_kernel spreads them; rows past
 // m up to the end of the last 16-row block get zero digits when qa is given. out may be x: a thread
 // reads its inputs before it writes their outputs, and no thread writes another's inputs.
-template <bool FULL>  // FULL: n == LNQ_MAX, no masking in the chains
+//
+// PAIR: two LayerNorms of the row in one launch, as a stack's layer boundary runs them (a layer's
+// last LayerNorm in place, then the next layer's first with its digits): the first (gamma, beta,
+// eps) goes to out as above; its outputs, exactly as stored, are then copied to LDS and run through
+// the same chains for the second (gamma2, beta2, eps2), whose outputs give the digits. The bits of
+// the two launches, with the row read from memory once.
+
+// Lanes p < 16 of wavefront 0: the row's mean and 1 / sqrt(var + eps) (step 2 above) into stat.
+template <bool FULL>
+__device__ __forceinline__ void row_stats(const float *row_s, int n, float eps, float *stat, int p) {
+    const float *xr = row_s + p;
+    float s = 0.0f;
+#pragma unroll
+    for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
+#pragma unroll
+        for (int q = q0; q < q0 + 16; q++) s = s + xr[16 * q];
+    }
+    s = s + __shfl_xor(s, 8, 16);
+    s = s + __shfl_xor(s, 4, 16);
+    s = s + __shfl_xor(s, 2, 16);
+    s = s + __shfl_xor(s, 1, 16);
+    const float mean = s / (float)n;
+    float sq = 0.0f;
+#pragma unroll
+    for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
+#pragma unroll
+        for (int q = q0; q < q0 + 16; q++) {
+            const float d = FULL || p + 16 * q < n ? xr[16 * q] - mean : 0.0f;
+            sq = __builtin_fmaf(d, d, sq);
+        }
+    }
+    sq = sq + __shfl_xor(sq, 8, 16);
+    sq = sq + __shfl_xor(sq, 4, 16);
+    sq = sq + __shfl_xor(sq, 2, 16);
+    sq = sq + __shfl_xor(sq, 1, 16);
+    if (p == 0) {
+        stat[0] = mean;
+        stat[1] = 1.0f / __builtin_sqrtf(sq / (float)n + eps);
+    }
+}
+
+__device__ __forceinline__ float4 ln_out(const float4 &v, float mean, float rstd, const float4 &g, const float4 &b) {
+    return float4{__builtin_fmaf((v.x - mean) * rstd, g.x, b.x), __builtin_fmaf((v.y - mean) * rstd, g.y, b.y),
+                  __builtin_fmaf((v.z - mean) * rstd, g.z, b.z), __builtin_fmaf((v.w - mean) * rstd, g.w, b.w)};
+}
+
+template <bool FULL, bool PAIR>  // FULL: n == LNQ_MAX, no masking in the chains
 __global__ __launch_bounds__(256) void layer_norm_row_kernel(const float *x, size_t ldx, size_t m, int n,
                                                              const float *__restrict__ gamma,
                                                              const float *__restrict__ beta, float eps, float *out,
                                                              size_t ldo, uint8_t *__restrict__ qa,
-                                                             int32_t *__restrict__ exps, int kb, size_t bpx) {
+                                                             int32_t *__restrict__ exps, int kb, size_t bpx,
+                                                             const float *__restrict__ gamma2,
+                                                             const float *__restrict__ beta2, float eps2) {
     __shared__ __attribute__((aligned(16))) float row_s[LNQ_MAX];
     __shared__ float stat[2];
     __shared__ float s_max[4];
@@ -968,55 +1017,33 @@ __global__ __launch_bounds__(256) void layer_norm_row_kernel(const float *x, siz
     if (!valid && (!qa || row >= (m + 15) / 16 * 16)) return;  // uniform over the workgroup
     const float4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool in = valid && (FULL || 4 * tid < n);
-    float4 v = zero, g = zero, b = zero;
+    float4 v = zero, g = zero, b = zero, g2 = zero, b2 = zero;
     if (in) {
         v = reinterpret_cast<const float4 *>(x + row * ldx)[tid];
         g = reinterpret_cast<const float4 *>(gamma)[tid];
         b = reinterpret_cast<const float4 *>(beta)[tid];
+        if constexpr (PAIR) {
+            g2 = reinterpret_cast<const float4 *>(gamma2)[tid];
+            b2 = reinterpret_cast<const float4 *>(beta2)[tid];
+        }
     }
     reinterpret_cast<float4 *>(row_s)[tid] = v;
     __syncthreads();
-    if (tid < 16) {
-        const int p = tid;
-        const float *xr = row_s + p;
-        float s = 0.0f;
-#pragma unroll
-        for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
-#pragma unroll
-            for (int q = q0; q < q0 + 16; q++) s = s + xr[16 * q];
-        }
-        s = s + __shfl_xor(s, 8, 16);
-        s = s + __shfl_xor(s, 4, 16);
-        s = s + __shfl_xor(s, 2, 16);
-        s = s + __shfl_xor(s, 1, 16);
-        const float mean = s / (float)n;
-        float sq = 0.0f;
-#pragma unroll
-        for (int q0 = 0; q0 < LNQ_MAX / 16; q0 += 16) {
-#pragma unroll
-            for (int q = q0; q < q0 + 16; q++) {
-                const float d = FULL || p + 16 * q < n ? xr[16 * q] - mean : 0.0f;
-                sq = __builtin_fmaf(d, d, sq);
-            }
-        }
-        sq = sq + __shfl_xor(sq, 8, 16);
-        sq = sq + __shfl_xor(sq, 4, 16);
-        sq = sq + __shfl_xor(sq, 2, 16);
-        sq = sq + __shfl_xor(sq, 1, 16);
-        if (p == 0) {
-            stat[0] = mean;
-            stat[1] = 1.0f / __builtin_sqrtf(sq / (float)n + eps);
-        }
-    }
+    if (tid < 16) row_stats<FULL>(row_s, n, eps, stat, tid);
     __syncthreads();
-    const float mean = stat[0], rstd = stat[1];
     float4 y = zero;
     if (in) {
-        y.x = __builtin_fmaf((v.x - mean) * rstd, g.x, b.x);
-        y.y = __builtin_fmaf((v.y - mean) * rstd, g.y, b.y);
-        y.z = __builtin_fmaf((v.z - mean) * rstd, g.z, b.z);
-        y.w = __builtin_fmaf((v.w - mean) * rstd, g.w, b.w);
+        y = ln_out(v, stat[0], stat[1], g, b);
         if (out) reinterpret_cast<float4 *>(out + row * ldo)[tid] = y;
+    }
+    if constexpr (PAIR) {
+        // Every thread has read stat and the chains have read row_s (the barrier above) before the
+        // second row and its statistics overwrite them.
+        reinterpret_cast<float4 *>(row_s)[tid] = y;
+        __syncthreads();
+        if (tid < 16) row_stats<FULL>(row_s, n, eps2, stat, tid);
+        __syncthreads();
+        if (in) y = ln_out(y, stat[0], stat[1], g2, b2);
     }
     if (!qa) return;  // uniform
     float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
@@ -1055,19 +1082,19 @@ bool layer_norm_row_fits(const float *x, size_t ldx, size_t m, size_t n, const f
     return m < LNQ_ROWS_MAX && n > 0 && n <= (size_t)LNQ_MAX && n % 4 == 0 && al % 16 == 0;
 }
 
+// gamma2 non-null: the PAIR instance (out must then be given).
 hipError_t launch_layer_norm_row(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                   const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
-                                  hipStream_t s) {
+                                  hipStream_t s, const float *gamma2, const float *beta2, float eps2) {
     const size_t kb = div_ceil(n, KBLK);
     // One workgroup per row of each 16-row block, bpx blocks per XCD.
     const size_t bpx = div_ceil(div_ceil(m, (size_t)16), (size_t)8);
     const unsigned groups = (unsigned)(8 * bpx * 16);
-    if (n == (size_t)LNQ_MAX)
-        hipLaunchKernelGGL(layer_norm_row_kernel<true>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
-                           eps, out, ldo, qa, exps, (int)kb, bpx);
-    else
-        hipLaunchKernelGGL(layer_norm_row_kernel<false>, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta,
-                           eps, out, ldo, qa, exps, (int)kb, bpx);
+    const bool full = n == (size_t)LNQ_MAX;
+    auto kernel = full ? &layer_norm_row_kernel<true, false> : &layer_norm_row_kernel<false, false>;
+    if (gamma2) kernel = full ? &layer_norm_row_kernel<true, true> : &layer_norm_row_kernel<false, true>;
+    hipLaunchKernelGGL(kernel, dim3(groups), dim3(256), 0, s, x, ldx, m, (int)n, gamma, beta, eps, out, ldo, qa, exps,
+                       (int)kb, bpx, gamma2, beta2, eps2);
     return hipGetLastError();
 }
 
@@ -1084,6 +1111,19 @@ hipError_t launch_layer_norm_quant(const float *x, size_t ldx, size_t m, size_t 
     hipLaunchKernelGGL(layer_norm_quant_kernel, dim3((unsigned)div_ceil(m, (size_t)16)), dim3(256), 0, s, x, ldx, m,
                        (int)n, gamma, beta, eps, out, ldo, qa, exps, (int)kb, vec);
     return hipGetLastError();
+}
+
+hipError_t launch_layer_norm_pair(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                                  const float *beta, float eps, float *out, size_t ldo, const float *gamma2,
+                                  const float *beta2, float eps2, uint8_t *qa, int32_t *exps, hipStream_t s) {
+    if (m == 0 || n == 0) return hipSuccess;
+    if (layer_norm_row_fits(x, ldx, m, n, gamma, beta, out, ldo) &&
+        (reinterpret_cast<uintptr_t>(gamma2) | reinterpret_cast<uintptr_t>(beta2)) % 16 == 0)
+        return launch_layer_norm_row(x, ldx, m, n, gamma, beta, eps, out, ldo, qa, exps, s, gamma2, beta2, eps2);
+    // Elsewhere the two launches, the second reading the first's outputs.
+    const hipError_t e = launch_layer_norm(x, ldx, m, n, gamma, beta, eps, out, ldo, s);
+    if (e != hipSuccess) return e;
+    return launch_layer_norm_quant(out, ldo, m, n, gamma2, beta2, eps2, nullptr, 0, qa, exps, s);
 }
 
 // Depthwise 1-D convolution with "same" zero padding, one output row per frame

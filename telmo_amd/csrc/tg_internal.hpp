@@ -268,6 +268,12 @@ hipError_t launch_layer_norm(const float *x, size_t ldx, size_t m, size_t n, con
 hipError_t launch_layer_norm_quant(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
                                    const float *beta, float eps, float *out, size_t ldo, uint8_t *qa, int32_t *exps,
                                    hipStream_t s);
+// A layer boundary's two LayerNorms: out = LayerNorm(x; gamma, beta, eps) (out may be x), then the
+// digits (qa, exps) of LayerNorm(out; gamma2, beta2, eps2), bit-identical to launch_layer_norm and
+// then launch_layer_norm_quant of its outputs; one launch where the row kernel takes the rows.
+hipError_t launch_layer_norm_pair(const float *x, size_t ldx, size_t m, size_t n, const float *gamma,
+                                  const float *beta, float eps, float *out, size_t ldo, const float *gamma2,
+                                  const float *beta2, float eps2, uint8_t *qa, int32_t *exps, hipStream_t s);
 
 // The two-digit int8 MFMA GEMM over quantised rows (int8 and Q8_0 weights).
 hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,

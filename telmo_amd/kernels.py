@@ -443,6 +443,18 @@ class Kernels:
             ldo, _dev(qa, "uint8", "qa"), _len(qa, None, "qa"), _dev(exps, "int32", "exps"), _len(exps, None, "exps"))
         _check(rc, self._ctx)
 
+    def layer_norm_pair_quant_device(self, x, ldx: int, m: int, n: int, gamma, beta, eps: float, gamma2, beta2,
+                                     eps2: float, qa, exps, x_len: Optional[int] = None):
+        """A layer boundary: x = LayerNorm(x; gamma, beta) in place, then LayerNorm(x; gamma2, beta2) of
+        the result quantised into qa and exps, the bits of layer_norm_device then layer_norm_quant_device."""
+        rc = _lib.lib().tg_layer_norm_pair_quant_device(
+            self._ctx, _dev(x, "float32", "x"), _len(x, x_len, "x"), ldx, m, n, _dev(gamma, "float32", "gamma"),
+            _len(gamma, None, "gamma"), _dev(beta, "float32", "beta"), _len(beta, None, "beta"), float(eps),
+            _dev(gamma2, "float32", "gamma2"), _len(gamma2, None, "gamma2"), _dev(beta2, "float32", "beta2"),
+            _len(beta2, None, "beta2"), float(eps2), _dev(qa, "uint8", "qa"), _len(qa, None, "qa"),
+            _dev(exps, "int32", "exps"), _len(exps, None, "exps"))
+        _check(rc, self._ctx)
+
     def dwconv1d_device(self, x, ldx: int, frames: int, channels: int, w, kernel: int, bias, out, ldo: int,
                         rows: int = None, t0: int = 0, stride: int = 1, act: "Act" = None, batch: int = 1,
                         x_len: Optional[int] = None, out_len: Optional[int] = None):

@@ -6,6 +6,8 @@ MI355X: each must write exactly the bytes of the calls it replaces.
 * tg_matmul_quantized_to_quant_device = tg_matmul_quantized_device into f32 rows then
   tg_quantize_rows_device, for every launch of a sequence and every replay of a captured graph (its
   workspace of f32 rows and row maxima is rewritten by every launch);
+* tg_layer_norm_pair_quant_device = tg_layer_norm_device in place then tg_layer_norm_quant_device of
+  its outputs (a stack's layer boundary);
 * tg_dwconv1d_quant_device = tg_dwconv1d_device then tg_quantize_rows_device, the f32 rows also
   bit-identical to the oracle's dwconv1d_frame loop.
 """
@@ -77,6 +79,40 @@ def test_layer_norm_quant_is_layer_norm_then_quantise(tk, m, n, ldx):
         assert same_floats(xd, ln)
     tk.synchronize()
     assert torch.equal(qa2, want_qa)
+
+
+# The one-launch kernel (< 2048 rows of <= 1024 values, a multiple of 4, aligned) with n = 1024 and
+# below, and the two launches elsewhere: 2048 rows and more, n = 4096, n not a multiple of 4, a row
+# stride that breaks the 16-byte alignment.
+PAIR_CASES = [(750, 1024, 1024), (40, 1020, 1020), (5, 64, 64), (1, 4, 4), (33, 2048, 2048), (2100, 1000, 1000),
+              (12000, 1024, 1024), (19, 100, 103), (16, 17, 17), (3, 4096, 4096), (37, 1000, 1024)]
+
+
+@pytest.mark.parametrize("m,n,ldx", PAIR_CASES)
+def test_layer_norm_pair_is_the_two_calls(tk, m, n, ldx):
+    import torch
+
+    rng = np.random.default_rng(m + 3 * n + ldx)
+    x = (0.5 + 2.0 * rng.standard_normal((m, ldx))).astype(np.float32)
+    if m > 3:
+        x[2, min(5, n - 1)] = np.inf  # a non-finite row
+    g1, g2 = ((1.0 + 0.2 * rng.standard_normal(n)).astype(np.float32) for _ in range(2))
+    b1, b2 = ((0.1 * rng.standard_normal(n)).astype(np.float32) for _ in range(2))
+    say("ln pair", m, n, ldx)
+    dev = lambda a: torch.from_numpy(a).cuda()  # noqa: E731
+    g1d, b1d, g2d, b2d = dev(g1), dev(b1), dev(g2), dev(b2)
+    want_x = dev(x.copy())
+    tk.layer_norm_device(want_x, ldx, m, n, g1d, b1d, 1e-5, want_x, ldx)
+    want_qa = torch.zeros(tk.quant_bytes(m, n), dtype=torch.uint8, device="cuda")
+    want_ex = torch.zeros(m, dtype=torch.int32, device="cuda")
+    tk.layer_norm_quant_device(want_x, ldx, m, n, g2d, b2d, 1e-5, want_qa, want_ex)
+    got_x = dev(x.copy())
+    got_qa, got_ex = torch.zeros_like(want_qa), torch.zeros_like(want_ex)
+    tk.layer_norm_pair_quant_device(got_x, ldx, m, n, g1d, b1d, 1e-5, g2d, b2d, 1e-5, got_qa, got_ex)
+    tk.synchronize()
+    assert same_floats(got_x, want_x)  # the columns past n left alone as well
+    assert torch.equal(got_ex, want_ex)
+    assert torch.equal(got_qa, want_qa)
 
 
 # m, k, n, act, with_bias, scale. An activation or a scale other than 1 is applied by the product's

@@ -4,8 +4,9 @@ the same sequence composed from the oracle's functions (tests/layer_oracle.py), 
 * Bit for bit against the composition with the integer oracle: every fused step writes what its
   unfused calls write, so the whole layer must give the integer oracle's bits.
 * Within 1e-3 row-normwise of the composition with the reference's fused f32 products.
-* At T = 750 (config 2's shapes), two layers stacked, and the batch of 32 utterances of 375 frames
-  (config 3's rows), whose utterances are independent: the first two and the last are checked.
+* At T = 750 (config 2's shapes), two layers stacked (also through run_stack), and the batch of 32
+  utterances of 375 frames (config 3's rows), whose utterances are independent: the first two and
+  the last are checked.
 """
 import numpy as np
 import pytest
@@ -35,7 +36,8 @@ def device_layer(tk, mats, norms, dw_w, dw_b, precision=3):
     return LayerWeights(W, {name: (dev(g), dev(b)) for name, (g, b) in norms.items()}, dev(dw_w), dev(dw_b))
 
 
-def run_device(tk, layers, x, utterances, quantised_hidden=False):
+def run_device(tk, layers, x, utterances, quantised_hidden=False, stack=False):
+    """The layers in turn; stack: through run_stack, each boundary one call."""
     import torch
 
     from telmo_amd.conformer import ConformerLayer
@@ -43,8 +45,11 @@ def run_device(tk, layers, x, utterances, quantised_hidden=False):
     t = x.shape[0]
     layer = ConformerLayer(tk, D, FF, K, t, quantised_hidden=quantised_hidden)
     xd = torch.from_numpy(x.copy()).cuda()
-    for w in layers:
-        layer.forward(xd, t, w, utterances=utterances)
+    if stack:
+        layer.run_stack(xd, t, layers, utterances=utterances)
+    else:
+        for w in layers:
+            layer.forward(xd, t, w, utterances=utterances)
     tk.synchronize()
     return xd.cpu().numpy()
 
@@ -71,13 +76,16 @@ def test_layer_at_750_frames(tk, orc, quantised_hidden):
     assert err <= 1e-3
 
 
-def test_two_stacked_layers(tk, orc):
+@pytest.mark.parametrize("stack", [False, True])
+def test_two_stacked_layers(tk, orc, stack):
+    """Two layers, as two calls of forward or through run_stack (the boundary's two LayerNorms in one
+    call, the second layer starting from the quantised rows it leaves)."""
     p1 = bench.layer_params(400)
     p2 = bench.layer_params(700)
     x = bench.synth_normal((750, D), 8)
-    say("two layers", 750)
+    say("two layers", 750, stack)
     ws = [device_layer(tk, *p1), device_layer(tk, *p2)]
-    got = run_device(tk, ws, x, 1)
+    got = run_device(tk, ws, x, 1, stack=stack)
     close(ws)
     want = layer_oracle.oracle_layer(orc, layer_oracle.oracle_layer(orc, x, *p1, fast=True), *p2, fast=True)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
