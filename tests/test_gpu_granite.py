@@ -139,7 +139,9 @@ def test_encoder_start_at_four_times_the_frames(tk, orc):
     print(f"[err] the chain end to end against the f32 reference chain: {end:.3e}", flush=True)
 
 
-@pytest.mark.parametrize("n", [1, 3, 16, 17, 1030, 4096, 4097, 16384, 20000])
+# Row lengths for each register-held instance (up to 1024, 4096, 8192, 16384 values, 16384 itself
+# without masks) and the chunked kernel beyond.
+@pytest.mark.parametrize("n", [1, 3, 16, 17, 1030, 4096, 4097, 6000, 12345, 16384, 20000])
 def test_softmax_matches_the_oracle(tk, orc, n):
     import torch
 
@@ -159,6 +161,18 @@ def test_softmax_matches_the_oracle(tk, orc, n):
     got = xd.cpu().numpy()
     want = orc.softmax(x)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
+
+
+def test_softmax_of_the_self_conditioning_shape(tk, orc):
+    """750 rows of 16384 (60 s of Granite's frames over the CTC vocabulary), more rows than CUs."""
+    import torch
+
+    x = (bench.synth_normal((750, 16384), 47) * np.float32(6.0)).astype(np.float32)
+    xd = torch.from_numpy(x.copy()).cuda()
+    say("softmax", 750, 16384)
+    tk.softmax_device(xd, 16384, 750, 16384)
+    tk.synchronize()
+    assert np.array_equal(xd.cpu().numpy().view(np.uint32), orc.softmax(x).view(np.uint32))
 
 
 def test_softmax_strided_rows_and_refusals(tk, orc):
