@@ -1062,10 +1062,14 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     // 4096 -> 1024 runs 81 us against 123 us on the direct kernel), else the direct kernel, or the
     // k-split kernel when the inputs are long (at least 32 k-blocks) and the tiles too few to fill
     // the CUs twice.
+    // The 64 x 64 tiles go to the XCDs in runs of four tile rows (tile_of<1, 4>: at 750 x 1024 ->
+    // 4096 four rows by 24 columns per XCD), so that each XCD reads 1.5 of the 4 MB of weights
+    // (12.1 against 13.5 us alone; with the k-split kernel's alike, the T = 750 layer step 0.1372 ->
+    // 0.1359 ms on one box).
     if (w.panels >= 128) {
         if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 384)
             return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
-        return launch_lds<4, 4, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_lds<4, 4, 3, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
     }
     if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 256)
         return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
@@ -1073,10 +1077,12 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         // 48-row tiles when their workgroups (one per CU) fit the chip in one round: every CU
         // busy and a quarter less work each (750 x 4096 -> 1024: 192 -> 256 workgroups, 15.7 ->
         // 14.2 us), with a six-stage register ring (four, five, seven, eight stages: 15.9, 15.1,
-        // 14.9, 15.5 against 14.1 us); else 64-row tiles (at 1000 rows 336 workgroups would take
-        // two rounds: 25 against 16.4 us).
+        // 14.9, 15.5 against 14.1 us), in runs of four tile rows by eight columns per XCD (each
+        // XCD reads half the weights: 13.1 -> 11.4 us alone, against 14.2 / 13.0 for runs of two
+        // or eight tile rows); else 64-row tiles (at 1000 rows 336 workgroups would take two
+        // rounds: 25 against 16.4 us).
         if (div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
-            return launch_kq<3, 6, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+            return launch_kq<3, 6, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
         return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     }
     // The direct kernel: 64 x 64 tiles when they give about one workgroup per CU (161 to 256 of
