@@ -1053,12 +1053,13 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         // layer step 0.2649 -> 0.2594 ms against the grouped order without XCD runs it took below
         // 1024 tiles of 128 x 128; runs of four tile rows 0.2632). Products with fewer 64 x 64 tiles
         // than CUs take 96 x 32 tiles when those fill the CUs at most once (750 x 4096 -> 1024: 256
-        // workgroups instead of 192, 42.2 -> 40.6 us; 750 x 1024 -> 1024 13.3 -> 12.9 us); 32 x 32,
-        // 32 x 64 and 64 x 32 tiles, and deeper operand rings, were slower. The fold over each
-        // output's blocks runs in block order, so k is never split.
+        // workgroups instead of 192, 42.2 -> 40.6 us; 750 x 1024 -> 1024 13.3 -> 12.9 us), with a
+        // three-stage operand ring (232 VGPRs, no spill: 40.6 -> 38.9 us; four stages spill into
+        // AGPRs, 43.6); 32 x 32, 32 x 64 and 64 x 32 tiles were slower. The fold over each output's
+        // blocks runs in block order, so k is never split.
         if (div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < GFX950_CUS &&
             div_ceil(m, (size_t)96) * div_ceil(w.panels, (size_t)2) <= GFX950_CUS)
-            return launch_q8<3, 1, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+            return launch_q8<3, 1, 3, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
         return launch_q8<2, 2, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     }
     if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
