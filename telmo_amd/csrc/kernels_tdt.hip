@@ -784,11 +784,23 @@ __device__ __forceinline__ float row_fold_q8(const uint8_t *pw, int KB, int NB, 
         if (((lane >> 4) & 1) == 0) tq[(2 * t + (lane >> 5)) * PANEL + (lane & 15)] = dh * 256 + dl;
     }
     __syncthreads();
-    // The fold in block order, its operands read from LDS eight blocks at a time so that the chain of
-    // fused multiply-adds does not wait on a read per block.
+    // The fold in block order, its operands read from LDS sixteen blocks at a time (then eight, then
+    // one) so that the chain of fused multiply-adds does not wait on a read per block (sixteen
+    // against eight: 20.10 -> 19.99 us per token of the Q8_0 decode; twenty, 20.02).
     float f = 0.0f;
     if (wave == 0 && lane < PANEL) {
         int b = 0;
+        for (; b + 16 <= NB; b += 16) {
+            float dv[16];
+            int32_t tv[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                dv[u] = ds[(b + u) * PANEL + lane];
+                tv[u] = tq[(b + u) * PANEL + lane];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) f = __builtin_fmaf(dv[u], (float)tv[u], f);
+        }
         for (; b + 8 <= NB; b += 8) {
             float dv[8];
             int32_t tv[8];
