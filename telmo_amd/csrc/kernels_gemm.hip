@@ -1096,11 +1096,14 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     }
     // The direct kernel: 64 x 64 tiles when they give about one workgroup per CU (161 to 256 of
-    // them), else 32 x 64 tiles, four workgroups per CU: more of them on small grids, shorter
-    // ones on large (750 x 1024 -> 640: 6.3 -> 4.9 us; 300 x 1024 -> 1000: 6.9 -> 5.4 us;
-    // 1500 x 1024 -> 1024: 10.7 -> 9.7 us; 750 x 1024 -> 1024 keeps 64 x 64, 6.6 against 7.3 us).
+    // them), else 32 x 64 tiles, four workgroups per CU, on small grids (750 x 1024 -> 640: 6.3 ->
+    // 4.9 us; 300 x 1024 -> 1000: 6.9 -> 5.4 us; 750 x 1024 -> 1024 keeps 64 x 64, 6.6 against
+    // 7.3 us). Beyond 256 tiles of 64 x 64 the LDS-staged kernel on them (in runs of four tile rows
+    // per XCD) copies each operand once per workgroup: 3000 x 1024 -> 1024 18.6 -> 13.4 us, 3000 x
+    // 4096 -> 1024 54.9 -> 35.1 us, 1500 x 1024 -> 1024 10.4 -> 9.2 us against the 32 x 64 tiles.
     const size_t tiles64 = div_ceil(m, (size_t)64) * div_ceil(w.n, (size_t)64);
     if (tiles64 > 160 && tiles64 <= GFX950_CUS) return launch_tile<2, 2, 6, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+    if (tiles64 > GFX950_CUS) return launch_lds<4, 4, 3, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
     return launch_tile<1, 2, 6, 4, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
 }
 
