@@ -1090,10 +1090,14 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         // 14.9, 15.5 against 14.1 us), in runs of four tile rows by eight columns per XCD (each
         // XCD reads half the weights: 13.1 -> 11.4 us alone, against 14.2 / 13.0 for runs of two
         // or eight tile rows); else 64-row tiles (at 1000 rows 336 workgroups would take two
-        // rounds: 25 against 16.4 us).
+        // rounds: 25 against 16.4 us), and the LDS-staged 64 x 64 kernel once there are more than
+        // 256 of those (1500 x 4096 -> 1024 32.0 -> 28.7 us, 1500 x 2048 -> 1024 20.5 -> 13.2 us;
+        // at 1000 x 4096 -> 1024, 256 tiles, the k-split kernel keeps 17.6 against 19.5 us).
         if (div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
             return launch_kq<3, 6, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
-        return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        if (div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
+            return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_lds<4, 4, 3, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
     }
     // The direct kernel: 64 x 64 tiles when they give about one workgroup per CU (161 to 256 of
     // them), else 32 x 64 tiles, four workgroups per CU, on small grids (750 x 1024 -> 640: 6.3 ->

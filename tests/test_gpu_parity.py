@@ -545,11 +545,12 @@ def test_pack_matrices_upload_like_their_parts(tk, tmp_path):
 
 
 @pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384), (2000, 320, 4100), (4100, 200, 1000),
-                                   (4100, 1000, 1000), (3000, 1024, 1000)])
+                                   (4100, 1000, 1000), (3000, 1024, 1000), (1500, 2048, 1000)])
 def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
     """Products of 2048 outputs or more with >= 384 128 x 128 tiles (2000 x 4100: 16 x 33), and
     narrow products (< 2048 outputs) with >= 256 of them, run the 128 x 128 LDS-staged GEMM; narrower
-    grids with more than 256 tiles of 64 x 64 the 64 x 64 one (3000 x 1000: 47 x 16); partial edge tiles in
+    grids with more than 256 tiles of 64 x 64 the 64 x 64 one (3000 x 1000: 47 x 16; 1500 x 1000 with
+    k = 2048, which the k-split kernel took before: 24 x 16); partial edge tiles in
     both directions, every epilogue, bit-identical to the integer oracle. k = 1000 (16 k-blocks)
     goes round the three-stage ring five times and ends on a partial round."""
     rng = np.random.default_rng(m + k + n)
