@@ -1076,9 +1076,14 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     // 4096 four rows by 24 columns per XCD), so that each XCD reads 1.5 of the 4 MB of weights
     // (12.1 against 13.5 us alone; with the k-split kernel's alike, the T = 750 layer step 0.1372 ->
     // 0.1359 ms on one box).
+    // Below one 64 x 64 tile per CU the direct kernel's 32 x 64 tiles fill more of the chip (100 x
+    // 1024 -> 4096 6.9 -> 5.1 us, 250 x 1024 -> 2048 7.1 -> 4.8 us; at 256 tiles and above the
+    // LDS-staged tiles tie or win: 200 x 1024 -> 4096 7.1 / 7.2, 300 rows 8.1 / 9.8).
+    const size_t tiles64 = div_ceil(m, (size_t)64) * div_ceil(w.n, (size_t)64);
     if (w.panels >= 128) {
         if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 384)
             return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        if (tiles64 < GFX950_CUS) return launch_tile<1, 2, 6, 4, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
         return launch_lds<4, 4, 3, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
     }
     if (div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 256)
@@ -1091,9 +1096,13 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
         // XCD reads half the weights: 13.1 -> 11.4 us alone, against 14.2 / 13.0 for runs of two
         // or eight tile rows); else 64-row tiles (at 1000 rows 336 workgroups would take two
         // rounds: 25 against 16.4 us), and the LDS-staged 64 x 64 kernel once there are more than
-        // 256 of those (1500 x 4096 -> 1024 32.0 -> 28.7 us, 1500 x 2048 -> 1024 20.5 -> 13.2 us;
-        // at 1000 x 4096 -> 1024, 256 tiles, the k-split kernel keeps 17.6 against 19.5 us).
-        if (div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
+        // 256 of those (1500 x 2048 -> 1024 20.5 -> 13.2 us; at 1000 x 4096 -> 1024, 256 tiles, the
+        // k-split kernel keeps 17.5 against 19.5 us). With 64 k-blocks or more the 48-row tiles
+        // also win when they fill two rounds at least seven eighths full (1500 x 4096 -> 1024: 512
+        // workgroups, 25.1 us against 28.6 on 64 x 64 tiles and 32.1 on 64-row ones; 1440 rows
+        // 25.4 against 30.1).
+        const size_t wg3 = div_ceil(div_ceil(m, (size_t)16), (size_t)3) * div_ceil(w.panels, (size_t)4);
+        if (wg3 <= GFX950_CUS || (w.kb >= 64 && wg3 <= 2 * GFX950_CUS && wg3 * 8 >= 2 * GFX950_CUS * 7))
             return launch_kq<3, 6, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
         if (div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) <= GFX950_CUS)
             return launch_kq<4, 5, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
@@ -1105,7 +1114,6 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     // 7.3 us). Beyond 256 tiles of 64 x 64 the LDS-staged kernel on them (in runs of four tile rows
     // per XCD) copies each operand once per workgroup: 3000 x 1024 -> 1024 18.6 -> 13.4 us, 3000 x
     // 4096 -> 1024 54.9 -> 35.1 us, 1500 x 1024 -> 1024 10.4 -> 9.2 us against the 32 x 64 tiles.
-    const size_t tiles64 = div_ceil(m, (size_t)64) * div_ceil(w.n, (size_t)64);
     if (tiles64 > 160 && tiles64 <= GFX950_CUS) return launch_tile<2, 2, 6, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     if (tiles64 > GFX950_CUS) return launch_lds<4, 4, 3, 1, 4>(qf, exps, m, w, c, ldc, epi, s);
     return launch_tile<1, 2, 6, 4, 1, 0>(qf, exps, m, w, c, ldc, epi, s);

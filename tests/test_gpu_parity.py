@@ -64,11 +64,12 @@ def test_exact_mode_is_bit_identical_to_the_fused_reference(tk, orc, p):
         tk.set_mode(tk.FAST)
 
 
-# (700, 2048, 1000) and (1300, 2048, 700) take the k-split kernel with 48- and 64-row tiles.
+# (700, 2048, 1000) and (1300, 2048, 700) take the k-split kernel with 48- and 64-row tiles;
+# (100, 1000, 4100) the direct kernel on a wide product with fewer 64 x 64 tiles than CUs.
 FAST_SHAPES = [(1, 1, 1), (3, 7, 5), (8, 64, 16), (9, 64, 16), (13, 100, 50), (64, 128, 96), (130, 1000, 255),
                (200, 640, 8198), (257, 2048, 130), (1, 4096, 1024), (8, 1280, 2560), (16, 2048, 100),
                (4, 2112, 300), (16, 2049, 77), (2, 64, 140000), (11, 700, 20000), (700, 2048, 1000),
-               (1300, 2048, 700)]
+               (1300, 2048, 700), (100, 1000, 4100)]
 
 
 @pytest.mark.parametrize("m,k,n", FAST_SHAPES)
@@ -545,12 +546,13 @@ def test_pack_matrices_upload_like_their_parts(tk, tmp_path):
 
 
 @pytest.mark.parametrize("m,k,n", [(1100, 200, 16380), (1030, 64, 16384), (2000, 320, 4100), (4100, 200, 1000),
-                                   (4100, 1000, 1000), (3000, 1024, 1000), (1500, 2048, 1000)])
+                                   (4100, 1000, 1000), (3000, 1024, 1000), (1500, 2048, 1000), (1440, 4096, 1000)])
 def test_large_products_take_the_lds_staged_gemm_bit_exactly(tk, orc, m, k, n):
     """Products of 2048 outputs or more with >= 384 128 x 128 tiles (2000 x 4100: 16 x 33), and
     narrow products (< 2048 outputs) with >= 256 of them, run the 128 x 128 LDS-staged GEMM; narrower
     grids with more than 256 tiles of 64 x 64 the 64 x 64 one (3000 x 1000: 47 x 16; 1500 x 1000 with
-    k = 2048, which the k-split kernel took before: 24 x 16); partial edge tiles in
+    k = 2048, which the k-split kernel took before: 24 x 16; with k = 4096 and 1440 rows the k-split
+    kernel's 48-row tiles instead, 480 workgroups in two rounds); partial edge tiles in
     both directions, every epilogue, bit-identical to the integer oracle. k = 1000 (16 k-blocks)
     goes round the three-stage ring five times and ends on a partial round."""
     rng = np.random.default_rng(m + k + n)
