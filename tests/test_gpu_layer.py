@@ -95,6 +95,23 @@ def test_two_stacked_layers(tk, orc, stack):
     assert err <= 1e-3
 
 
+def test_three_stacked_layers_on_ragged_rows(tk, orc):
+    """37 frames (a partial 16-row block) through three layers: run_stack, whose two boundaries are
+    one launch each, writes the bits of three plain calls of forward, and the integer oracle's."""
+    params = [bench.layer_params(1500 + 100 * i) for i in range(3)]
+    x = bench.synth_normal((37, D), 11)
+    say("three layers", 37)
+    ws = [device_layer(tk, *p) for p in params]
+    stacked = run_device(tk, ws, x, 1, stack=True)
+    plain = run_device(tk, ws, x, 1)
+    close(ws)
+    assert np.array_equal(stacked.view(np.uint32), plain.view(np.uint32))
+    want = x
+    for p in params:
+        want = layer_oracle.oracle_layer(orc, want, *p, fast=True)
+    assert np.array_equal(stacked.view(np.uint32), want.view(np.uint32))
+
+
 def test_batch_of_32_utterances(tk, orc):
     """M = 12000 rows: 32 utterances of 375 frames, each convolved on its own."""
     mats, norms, dw_w, dw_b = bench.layer_params(1000)
