@@ -5,7 +5,7 @@
 
 A step is one Conformer layer of Parakeet's encoder (src/parakeet.rs:1011-1172) on the device at
 T = 750 frames (60 s of audio at 80 ms per frame), d = 1024, ff = 4096, conv 2048 -> GLU -> 1024, all
-eight products int8 with per-output scales (the north star's layer projection set):
+eight products int8 with per-output scales (the layer's projection set):
 
     FF1 in 1024->4096 (SiLU), FF1 out 4096->1024 (x0.5, accumulate), QKV 1024->3072, attention
     out 1024->1024 (the V third of QKV standing in for the attention core, accumulate), pw1
@@ -20,7 +20,7 @@ its first LayerNorm, which the previous step left, and ends with the layer bound
 LayerNorm and the next layer's first in one launch). The step is timed launched eagerly on one
 stream and replayed as a captured HIP graph; the faster is the step time. value = 2 sum(M N K) over
 the eight products / step time, in TOPS. Inputs come from telmo's test generator (seeded xorshift,
-src/kernels/mod.rs:795-805): synthetic data of the configs' distributions, random weights.
+src/kernels/mod.rs:795-805): synthetic data of the workloads' distributions, random weights.
 
 The JSON line also carries:
   roofline      the eight products' GEMM kernels, each launched alone on the step's quantised rows
@@ -917,7 +917,7 @@ def tdt_leg(args, net, enc_host):
         dec.set_resident(True)
     frames = enc_host.shape[0]
     weight_bytes = joint.bytes() + sum(w.bytes() for w in lstm) + proj.bytes()
-    # Several streams of 60 s each in one resident launch (config 5's M concurrent streams), each
+    # Several streams of 60 s each in one resident launch (M concurrent decode streams), each
     # with encoder rows of its own; the first stream's are the single decode's.
     multi = []
     if resident and net["p"] == 3:

@@ -1,5 +1,5 @@
-"""Parakeet::layer (src/parakeet.rs:1011-1172) composed from the oracle's functions, the checker of the
-device layer (telmo_amd.conformer): LayerNorm rows (or_layer_norm), products (the integer oracle
+"""Parakeet::layer (src/parakeet.rs:1011-1172) composed from the oracle's functions, what the tests
+check the device layer (telmo_amd.conformer) against: LayerNorm rows (or_layer_norm), products (the integer oracle
 or_matmul_fast of the fast path, or the fused f32 reference or_matmul), the GLU, the depthwise
 convolution + SiLU per utterance, in the reference's order, with the V third of qkv standing in for
 the attention core as the device layer's default does. Products the device makes through

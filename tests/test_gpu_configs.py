@@ -1,11 +1,11 @@
 """Parity at the benchmark configurations' full sizes, through the entry points the benchmark and
 the device layer use, on an MI355X.
 
-* Config 2 (one Conformer layer's projection set at T = 750 frames, d = 1024, ff = 4096): each of
+* One Conformer layer's projection set at T = 750 frames (d = 1024, ff = 4096): each of
   the eight products with its epilogue: FF up (SiLU), FF down (x0.5, accumulate) on the k-split
   kernel, QKV, attention out on the strided V third of the QKV rows (lda = 3072, accumulate), pw1
   with its GLU fused, pw2 (accumulate), and the second FFN.
-* Configs 3 and 4 (the 24-layer stack at M = 12000 and 7500 rows): the same products at those
+* The 24-layer encoder stack at M = 12000 and 7500 rows: the same products at those
   rows, on the 128 x 128 LDS-staged kernel.
 
 Every output element is compared: bit for bit with the integer oracle (the fast path's two-digit
@@ -121,12 +121,12 @@ PRODUCTS = [
 
 
 @pytest.mark.parametrize("name,k,n,act,scale,acc,lda", PRODUCTS, ids=[p[0] for p in PRODUCTS])
-def test_config_2_products(tk, orc, name, k, n, act, scale, acc, lda):
+def test_layer_products_at_750_frames(tk, orc, name, k, n, act, scale, acc, lda):
     check_product(tk, orc, 750, k, n, act, scale, acc, seed=100 + PRODUCTS.index(
         (name, k, n, act, scale, acc, lda)) * 50, lda=lda)
 
 
-def test_config_2_pw1_glu(tk, orc):
+def test_layer_pw1_glu_at_750_frames(tk, orc):
     check_glu(tk, orc, 750, D, CONV, seed=900)
 
 
@@ -142,17 +142,17 @@ BIG = [
 
 
 @pytest.mark.parametrize("m,name,k,n,act,scale,acc,lda", BIG, ids=[f"{b[0]}-{b[1]}" for b in BIG])
-def test_configs_3_and_4_products(tk, orc, m, name, k, n, act, scale, acc, lda):
+def test_encoder_stack_products(tk, orc, m, name, k, n, act, scale, acc, lda):
     check_product(tk, orc, m, k, n, act, scale, acc, seed=2000 + BIG.index((m, name, k, n, act, scale, acc, lda)) * 50,
                   lda=lda)
 
 
 @pytest.mark.parametrize("m", [12000, 7500])
-def test_configs_3_and_4_pw1_glu(tk, orc, m):
+def test_encoder_stack_pw1_glu(tk, orc, m):
     check_glu(tk, orc, m, D, CONV, seed=3000 + m)
 
 
-# Call sites outside the configs whose shapes no other test reaches: Granite's out_mid (the CTC
+# Call sites outside the benchmark's workloads whose shapes no other test reaches: Granite's out_mid (the CTC
 # posteriors back to the hidden width, k = vocab = 16384, src/granite.rs:1060-1067) in chunks of 2,
 # 16 and 256 rows with its bias, and Parakeet's subsampling pw1 (k = 256 channels, m = 64 T rows for
 # T encoder frames, ReLU and bias, src/parakeet.rs:950-960).

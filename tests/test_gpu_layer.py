@@ -4,8 +4,8 @@ the same sequence composed from the oracle's functions (tests/layer_oracle.py), 
 * Bit for bit against the composition with the integer oracle: every fused step writes what its
   unfused calls write, so the whole layer must give the integer oracle's bits.
 * Within 1e-3 row-normwise of the composition with the reference's fused f32 products.
-* At T = 750 (config 2's shapes), two layers stacked (also through run_stack), and the batch of 32
-  utterances of 375 frames (config 3's rows), whose utterances are independent: the first two and
+* At T = 750 (d = 1024, ff = 4096), two layers stacked (also through run_stack), and the batch of 32
+  utterances of 375 frames (12000 rows), whose utterances are independent: the first two and
   the last are checked.
 """
 import numpy as np
@@ -132,7 +132,7 @@ def test_batch_of_32_utterances(tk, orc):
 
 
 def test_one_600_s_utterance(tk, orc):
-    """M = 7500 rows of one utterance (config 4's layer: the 16-row-block convolution with eight rows
+    """M = 7500 rows of one utterance (one 600 s utterance: the 16-row-block convolution with eight rows
     per thread, the four-row LayerNorm at 7500 rows). Only the depthwise convolution mixes rows (four
     on either side), so windows of the output are checked against the oracle run on the window's
     rows and four more on each side: the first, a middle and the last 256 rows."""
