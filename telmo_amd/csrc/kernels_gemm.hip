@@ -1075,7 +1075,7 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
     // The 64 x 64 tiles go to the XCDs in runs of four tile rows (tile_of<1, 4>: at 750 x 1024 ->
     // 4096 four rows by 24 columns per XCD), so that each XCD reads 1.5 of the 4 MB of weights
     // (12.1 against 13.5 us alone; with the k-split kernel's alike, the T = 750 layer step 0.1372 ->
-    // 0.1359 ms on one box).
+    // 0.1359 ms on one GPU, the two measured in turn).
     // Below one 64 x 64 tile per CU the direct kernel's 32 x 64 tiles fill more of the chip (100 x
     // 1024 -> 4096 6.9 -> 5.1 us, 250 x 1024 -> 2048 7.1 -> 4.8 us; at 256 tiles and above the
     // LDS-staged tiles tie or win: 200 x 1024 -> 4096 7.1 / 7.2, 300 rows 8.1 / 9.8).
