@@ -7,7 +7,7 @@
 //
 // Both the quantised rows (fragment-major QA) and the weights (MFMA layout) store each 16 x 64
 // MFMA operand as 1 KB in lane order, so one 16-byte load per lane is one operand, fully coalesced.
-// Three kernels share that layout:
+// Four kernels share that layout:
 //   gemm_lds_kernel    operands copied from global memory straight into an LDS ring
 //                      (global_load_lds_dwordx4), one copy per workgroup: 128 x 128 tiles when
 //                      they fill the chip twice over, 64 x 64 tiles for products of >= 2048 outputs;
@@ -18,10 +18,14 @@
 //                      7.5 -> 6.7 us);
 //   gemm_i8_kq_kernel  the narrower products with long inputs: each wavefront takes the whole
 //                      48 x 64 or 64 x 64 tile over a quarter of the k-blocks, and the integer
-//                      partial sums meet in LDS.
+//                      partial sums meet in LDS;
+//   gemm_q8_lds_kernel Q8_0 weights (a scale per 32 inputs): per-block sums on
+//                      v_mfma_i32_16x16x32_i8 folded in f32 in block order, on the LDS ring.
 // The k-split kernel, whose partial sums meet in LDS anyway, stages its sums there and stores them
 // through TileStore (the register-stored form was 0.5 us slower on it). launch_gemm_i8 at the end
 // picks one by shape.
+#include <type_traits>
+
 #include "tg_internal.hpp"
 
 namespace tg {
@@ -637,137 +641,6 @@ hipError_t launch_kq(const uint8_t *qf, const int32_t *exps, size_t m, const Dev
 }
 
 
-// Q8_0 weights: one scale per 32 inputs of each output. Each 32-input half of a k-block runs on
-// v_mfma_i32_16x16x32_i8 from zero, giving the block's exact sums H (hi digits) and L (lo digits);
-// T = 256 H + L (|T| < 2^31) is folded into an f32 accumulator as fmaf(d, (float)T, F), blocks in
-// order. The 8-byte operands come from the same 1 KB k-block layouts as the int8 path: for half h,
-// lane 16 g + x reads bytes 8 (g % 2) .. of layout lane 16 (2 h + g / 2) + x, i.e. inputs
-// 32 h + 8 g .. + 8 of its row (A) or output (B), the same k for both operands.
-template <int RB, int CB, int S, int OCC, int XCD, int G>
-__global__ __launch_bounds__(THREADS, OCC) void gemm_q8_kernel(const uint8_t *__restrict__ qf,
-                                                               const int32_t *__restrict__ exps, int M,
-                                                               const uint8_t *__restrict__ wv,
-                                                               const float *__restrict__ scales, int N, int P, int KB,
-                                                               int NB, float *__restrict__ c, size_t ldc,
-                                                               const float *__restrict__ bias, uint32_t act,
-                                                               float escale, int accumulate, size_t b_panel,
-                                                               size_t b_blk) {
-    constexpr int WM = RB * 16, WN = CB * 16;
-    constexpr int C_STRIDE = WN + 4;
-    __shared__ __attribute__((aligned(16))) float staged[4][WM * C_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-    int bx, by;
-    tile_of<XCD, G>(bx, by);
-    const int m0 = by * 2 * WM + wm * WM, n0 = bx * 2 * WN + wn * WN;
-    const int R0 = m0 / 16, P0 = n0 / 16, RLAST = (M + 15) / 16 - 1;
-    const int out_col = lane & 15, out_row = (lane >> 4) * 4;
-    const int g = lane >> 4;
-
-    int32_t e_row[RB][4];
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
-
-    // Byte offsets, within a 1 KB layout block, of this lane's 8 bytes for halves 0 and 1.
-    const int off0 = (16 * (g >> 1) + out_col) * 16 + 8 * (g & 1), off1 = off0 + 32 * 16;
-    const uint8_t *ap[RB];
-    const uint8_t *bp[CB];
-    const float *sp[CB];
-#pragma unroll
-    for (int r = 0; r < RB; r++) ap[r] = qf + (size_t)min(R0 + r, RLAST) * KB * 2048;
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++) {
-        const int p = min(P0 + cb, P - 1);
-        bp[cb] = wv + (size_t)p * b_panel;
-        sp[cb] = scales + (size_t)p * NB * PANEL + out_col;
-    }
-
-    typedef float v4f __attribute__((ext_vector_type(4)));
-    v4f acc[RB][CB];
-#pragma unroll
-    for (int i = 0; i < RB; i++)
-#pragma unroll
-        for (int j = 0; j < CB; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-    long fa[S][RB][2][2], fb[S][CB][2];
-    float fs[S][CB][2];
-#define TG_LOAD(st, tt)                                                                                 \
-    do {                                                                                                \
-        const size_t t_ = (size_t)(tt);                                                                 \
-        _Pragma("unroll") for (int r = 0; r < RB; r++) _Pragma("unroll") for (int d = 0; d < 2; d++) {  \
-            fa[st][r][d][0] = *reinterpret_cast<const long *>(ap[r] + t_ * 2048 + d * 1024 + off0);     \
-            fa[st][r][d][1] = *reinterpret_cast<const long *>(ap[r] + t_ * 2048 + d * 1024 + off1);     \
-        }                                                                                               \
-        _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                             \
-            fb[st][cb][0] = *reinterpret_cast<const long *>(bp[cb] + t_ * b_blk + off0);                \
-            fb[st][cb][1] = *reinterpret_cast<const long *>(bp[cb] + t_ * b_blk + off1);                \
-            const int b0_ = 2 * (int)t_, b1_ = b0_ + 1;                                                 \
-            fs[st][cb][0] = sp[cb][(size_t)b0_ * PANEL];                                                \
-            fs[st][cb][1] = b1_ < NB ? sp[cb][(size_t)b1_ * PANEL] : 0.0f;                              \
-        }                                                                                               \
-    } while (0)
-#define TG_MMA(st)                                                                                      \
-    do {                                                                                                \
-        _Pragma("unroll") for (int h = 0; h < 2; h++) _Pragma("unroll") for (int r = 0; r < RB; r++)    \
-            _Pragma("unroll") for (int cb = 0; cb < CB; cb++) {                                         \
-            const v4i hh = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[st][r][0][h], fb[st][cb][h],        \
-                                                                 v4i{0, 0, 0, 0}, 0, 0, 0);             \
-            const v4i ll = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[st][r][1][h], fb[st][cb][h],        \
-                                                                 v4i{0, 0, 0, 0}, 0, 0, 0);             \
-            _Pragma("unroll") for (int v = 0; v < 4; v++) acc[r][cb][v] =                               \
-                __builtin_fmaf(fs[st][cb][h], (float)(hh[v] * 256 + ll[v]), acc[r][cb][v]);             \
-        }                                                                                               \
-    } while (0)
-
-    if (KB > 0) {
-#pragma unroll
-        for (int s = 0; s < S - 1; s++) TG_LOAD(s, min(s, KB - 1));
-        int t = 0;
-        for (; t + S <= KB; t += S) {
-#pragma unroll
-            for (int s = 0; s < S; s++) {
-                TG_LOAD((s + S - 1) % S, min(t + s + S - 1, KB - 1));
-                TG_MMA(s);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < S - 1; j++)
-            if (t + j < KB) TG_MMA(j);
-    }
-#undef TG_LOAD
-#undef TG_MMA
-
-    TileStore<WM, WN, C_STRIDE> out;
-    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
-    float *tile = staged[wave];
-#pragma unroll
-    for (int r = 0; r < RB; r++)
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int32_t e = e_row[r][v];
-                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
-                    e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(acc[r][cb][v], -e);
-            }
-    __syncthreads();
-    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
-}
-
-template <int RB, int CB, int S, int OCC, int XCD, int G>
-hipError_t launch_q8(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c, size_t ldc,
-                     const EpiArgs &epi, hipStream_t s) {
-    const size_t bm = 2 * RB * 16, bn = 2 * CB * 16;
-    dim3 grid((unsigned)div_ceil(w.panels * PANEL, bn), (unsigned)div_ceil(m, bm));
-    hipLaunchKernelGGL((gemm_q8_kernel<RB, CB, S, OCC, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
-                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc, epi.bias,
-                       epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
-    return hipGetLastError();
-}
-
-
 // ---------------------------------------------------------------------------- LDS-staged GEMM
 //
 // The workgroup's operands go from global memory straight into LDS with global_load_lds_dwordx4
@@ -1034,6 +907,209 @@ hipError_t launch_lds(const uint8_t *qf, const int32_t *exps, size_t m, const De
     return hipGetLastError();
 }
 
+// 64 lanes x 4 bytes from base + voff to LDS at lds + 4 l (lane l), as copy_to_lds_s.
+__device__ __forceinline__ void copy_dword_to_lds_s(const uint8_t *base, uint32_t voff, uint32_t lds) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base) : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// Q8_0 weights: one scale per 32 inputs of each output. Each 32-input half of a k-block runs on
+// v_mfma_i32_16x16x32_i8 from zero, giving the block's exact sums H (hi digits) and L (lo digits);
+// T = 256 H + L (|T| < 2^31) is folded into an f32 accumulator as fmaf(d, (float)T, F), blocks in
+// order, so k is never split. The 8-byte operands come from the same 1 KB k-block layouts as the
+// int8 path: for half h, lane 16 g + x reads bytes 8 (g % 2) .. of layout lane 16 (2 h + g / 2) +
+// x, i.e. inputs 32 h + 8 g .. + 8 of its row (A) or output (B), the same k for both operands.
+//
+// The operands travel on gemm_lds_kernel's ring. A stage holds one k-block: 2 TM + TN chunks of
+// 1 KB (A: TM row blocks x hi, lo; B: TN panels) and the scales of the k-block's two 32-input
+// blocks for the TN panels (128 bytes a panel), copied once per workgroup: each wavefront moves
+// its share of the chunks and 256 bytes of scales (two panels: lanes 0-31 the first, lanes 32-63
+// the second; lanes 16-31 of each the second block). The four wavefronts (2 x 2, TM / 2 row blocks
+// by TN / 2 panels) read their operands and their columns' scales from LDS. When k is an odd
+// number of blocks the last k-block's second block does not exist: its lanes copy the first
+// block's scales, and its fold is skipped. Copying each operand once per workgroup, where
+// wavefronts loading their own operands into registers load each twice, took the T = 750 Q8_0
+// layer step from 0.250 to 0.224 ms on 64 x 64 tiles, and the smaller tiles the registers freed
+// (more workgroups per CU on the narrower products) to 0.204 ms.
+template <int TM, int TN, int NS, int XCD, int G>
+__global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *__restrict__ qf,
+                                                                 const int32_t *__restrict__ exps, int M,
+                                                                 const uint8_t *__restrict__ wv,
+                                                                 const float *__restrict__ scales, int N, int P,
+                                                                 int KB, int NB, float *__restrict__ c, size_t ldc,
+                                                                 const float *__restrict__ bias, uint32_t act,
+                                                                 float escale, int accumulate, size_t b_panel,
+                                                                 size_t b_blk) {
+    constexpr int RB = TM / 2, CB = TN / 2;  // 16 x 16 blocks per wavefront
+    constexpr int CH = 2 * TM + TN;          // 1 KB chunks per stage
+    static_assert(TN <= 8, "four 256-byte scale copies cover eight panels");
+    static_assert(NS >= 3, "block t + 1 lands while block t is multiplied, block t - 1's buffer refills");
+    // Chunk copies per wavefront: CPW for waves below FULL, CPW - 1 for the rest; each also copies
+    // its 256 bytes of scales.
+    constexpr int CPW = (CH + 3) / 4, FULL = CH - 4 * (CPW - 1), SC = CH * 1024, STAGE = SC + 1024;
+    constexpr int WM = RB * 16, WN = CB * 16, C_STRIDE = WN + 4;
+    static_assert(4 * WM * C_STRIDE * 4 <= NS * STAGE, "the epilogue reuses the ring");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    int bx, by;
+    tile_of<XCD, G>(bx, by);
+    const int R0 = by * TM, P0 = bx * TN, RLAST = (M + 15) / 16 - 1;
+    const int m0 = by * TM * 16 + wm * WM, n0 = bx * TN * 16 + wn * WN;
+    const int out_col = lane & 15, out_row = (lane >> 4) * 4, g = lane >> 4;
+
+    int32_t e_row[RB][4];
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) e_row[r][v] = exps[min(m0 + r * 16 + out_row + v, M - 1)];
+
+    // This wavefront's chunk copies (chunk ch = wave + 4 i: row block R0 + ch / 2, digit ch % 2 when
+    // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one) and
+    // its scale copy: lane l reads scales[((p NB + 2 t + b) 16 + j] for panel p = P0 + 2 wave +
+    // l / 32 (the last panel past the edge), block b = (l / 16) % 2 and column j = l % 16, as the
+    // wave-uniform base (panel P0 + 2 wave, block 2 t) plus a lane offset below NB * 64 + 128 bytes.
+    const uint8_t *gp[CPW];
+    size_t gs[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+        const int ch = min(wave + 4 * i, CH - 1);
+        if (ch < 2 * TM) {
+            gp[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024;
+            gs[i] = 2048;
+        } else {
+            gp[i] = wv + (size_t)min(P0 + ch - 2 * TM, P - 1) * b_panel;
+            gs[i] = b_blk;
+        }
+    }
+    const int s_first = min(P0 + 2 * wave, P - 1), s_blk = (lane >> 4) & 1;
+    const int s_panel = min(P0 + 2 * wave + (lane >> 5), P - 1) - s_first;
+    const uint32_t s_off = (uint32_t)(((s_panel * NB + s_blk) * PANEL + (lane & 15)) * sizeof(float));
+    const uint32_t s_off_one = s_off - (uint32_t)(s_blk * PANEL * sizeof(float));
+    const uint8_t *sbase = reinterpret_cast<const uint8_t *>(scales + (size_t)s_first * NB * PANEL);
+    const uint32_t voff = lane * 16, lds0 = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    const bool full = wave < FULL;
+    auto issue = [&](int buf, int tt) {
+#pragma unroll
+        for (int i = 0; i < CPW; i++)
+            if (i < CPW - 1 || full)
+                copy_to_lds_s(gp[i] + (size_t)tt * gs[i], voff, lds0 + buf * STAGE + (wave + 4 * i) * 1024);
+        copy_dword_to_lds_s(sbase + (size_t)tt * 2 * PANEL * sizeof(float), 2 * tt + 1 < NB ? s_off : s_off_one,
+                            lds0 + buf * STAGE + SC + wave * 256);
+    };
+
+    // Byte offsets, within a 1 KB chunk, of this lane's 8 bytes for halves 0 and 1.
+    const int off0 = (16 * (g >> 1) + out_col) * 16 + 8 * (g & 1), off1 = off0 + 32 * 16;
+    auto read_frags = [&](int buf, long (&fa)[RB][2][2], long (&fb)[CB][2], float (&fs)[CB][2]) {
+        const uint8_t *st = smem + buf * STAGE;
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {
+            const uint8_t *b = st + 2 * TM * 1024 + (wn * CB + cb) * 1024;
+            fb[cb][0] = *reinterpret_cast<const long *>(b + off0);
+            fb[cb][1] = *reinterpret_cast<const long *>(b + off1);
+            const float *sc = reinterpret_cast<const float *>(st + SC + (wn * CB + cb) * 128) + out_col;
+            fs[cb][0] = sc[0];
+            fs[cb][1] = sc[PANEL];
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+                const uint8_t *a = st + ((wm * RB + r) * 2 + d) * 1024;
+                fa[r][d][0] = *reinterpret_cast<const long *>(a + off0);
+                fa[r][d][1] = *reinterpret_cast<const long *>(a + off1);
+            }
+    };
+
+    v4f acc[RB][CB];
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+        for (int j = 0; j < CB; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // k-block t: the fold of its blocks 2 t and 2 t + 1 (the second only when it exists).
+    auto mma = [&](int t, const long (&fa)[RB][2][2], const long (&fb)[CB][2], const float (&fs)[CB][2]) {
+        const int halves = 2 * t + 1 < NB ? 2 : 1;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            if (h >= halves) break;
+#pragma unroll
+            for (int r = 0; r < RB; r++)
+#pragma unroll
+                for (int cb = 0; cb < CB; cb++) {
+                    const v4i hh = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[r][0][h], fb[cb][h], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const v4i ll = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[r][1][h], fb[cb][h], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[r][cb][v] = __builtin_fmaf(fs[cb][h], (float)(hh[v] * 256 + ll[v]), acc[r][cb][v]);
+                }
+        }
+    };
+
+    // The ring as gemm_lds_kernel's: k-block t in buffer t % NS, block t + 1's fragments read from
+    // LDS while block t's MFMAs run.
+    if (KB > 0) {
+        long fa0[RB][2][2], fb0[CB][2], fa1[RB][2][2], fb1[CB][2];
+        float fs0[CB][2], fs1[CB][2];
+#pragma unroll
+        for (int s = 0; s < NS - 1; s++)
+            if (s < KB) issue(s, s);
+        // Waits until at most `ahead` stages of this wavefront's copies are still on the way.
+        auto wait_ahead = [&](auto stages, int ahead) {
+            constexpr int A = decltype(stages)::value;
+            if (full) wait_stages<CPW + 1, A>(ahead);
+            else wait_stages<CPW, A>(ahead);
+        };
+        wait_ahead(std::integral_constant<int, NS - 2>{}, min(NS - 2, KB - 1));
+        __syncthreads();
+        read_frags(0, fa0, fb0, fs0);
+        auto step = [&](int t, const long (&ca)[RB][2][2], const long (&cb)[CB][2], const float (&cs)[CB][2],
+                        long (&na)[RB][2][2], long (&nb)[CB][2], float (&ns)[CB][2]) {
+            if (t + 1 < KB) {
+                wait_ahead(std::integral_constant<int, NS - 3>{}, min(NS - 3, KB - 2 - t));
+                __syncthreads();
+                if (t + NS - 1 < KB) issue((t + NS - 1) % NS, t + NS - 1);
+                read_frags((t + 1) % NS, na, nb, ns);
+            }
+            mma(t, ca, cb, cs);
+        };
+        int t = 0;
+        for (; t + 1 < KB; t += 2) {
+            step(t, fa0, fb0, fs0, fa1, fb1, fs1);
+            step(t + 1, fa1, fb1, fs1, fa0, fb0, fs0);
+        }
+        if (t < KB) step(t, fa0, fb0, fs0, fa1, fb1, fs1);
+    }
+
+    TileStore<WM, WN, C_STRIDE> out;
+    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
+    float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
+#pragma unroll
+    for (int r = 0; r < RB; r++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int32_t e = e_row[r][v];
+                tile[(r * 16 + out_row + v) * C_STRIDE + cb * 16 + out_col] =
+                    e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(acc[r][cb][v], -e);
+            }
+    __syncthreads();
+    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+}
+
+template <int TM, int TN, int NS, int XCD, int G>
+hipError_t launch_q8_lds(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
+                         size_t ldc, const EpiArgs &epi, hipStream_t s) {
+    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)TN), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
+    hipLaunchKernelGGL((gemm_q8_lds_kernel<TM, TN, NS, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
+                       w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc,
+                       epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 // 128 x 128 workgroup tiles when there are at least 1024 of them (two per CU, twice over), else
@@ -1047,20 +1123,16 @@ hipError_t launch_gemm_i8(const uint8_t *qf, const int32_t *exps, size_t m, cons
                           size_t ldc, const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
     if (w.precision == Q8_0) {
-        // 64 x 64 tiles: the 8-byte operands, block scales and per-block MFMA results do not leave
-        // room in registers for larger wavefront tiles. Tiles go to the XCDs in contiguous row-major
-        // runs at every size, the rows the row kernels leave in each XCD's L2 (the T = 750 Q8_0
-        // layer step 0.2649 -> 0.2594 ms against the grouped order without XCD runs it took below
-        // 1024 tiles of 128 x 128; runs of four tile rows 0.2632). Products with fewer 64 x 64 tiles
-        // than CUs take 96 x 32 tiles when those fill the CUs at most once (750 x 4096 -> 1024: 256
-        // workgroups instead of 192, 42.2 -> 40.6 us; 750 x 1024 -> 1024 13.3 -> 12.9 us), with a
-        // three-stage operand ring (232 VGPRs, no spill: 40.6 -> 38.9 us; four stages spill into
-        // AGPRs, 43.6); 32 x 32, 32 x 64 and 64 x 32 tiles were slower. The fold over each output's
-        // blocks runs in block order, so k is never split.
-        if (div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < GFX950_CUS &&
-            div_ceil(m, (size_t)96) * div_ceil(w.panels, (size_t)2) <= GFX950_CUS)
-            return launch_q8<3, 1, 3, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
-        return launch_q8<2, 2, 2, 2, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        // LDS-staged tiles, in contiguous row-major runs per XCD (the rows the row kernels leave in
+        // each XCD's L2): 64 x 64 from three per CU (750 x 1024 -> 4096, 768 tiles: 21.3 us against
+        // 24.0 on 32 x 64), 32 x 64 from one per CU (750 x 1024 -> 3072 18.8 against 20.1 us,
+        // x 1024 -> 2048 13.1 against 15.1), 32 x 32 below (750 x 4096 -> 1024, 768 workgroups:
+        // 31.4 against 32.4 on 32 x 64, 36.4 on 96 x 32; 38.9 before LDS staging). Four-stage
+        // rings were slower on both small tiles.
+        const size_t tiles64 = div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4);
+        if (tiles64 >= 3 * GFX950_CUS) return launch_q8_lds<4, 4, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        if (tiles64 >= GFX950_CUS) return launch_q8_lds<2, 4, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
+        return launch_q8_lds<2, 2, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     }
     if (gemm_tile_choice(m, w.panels) == 0) return launch_lds<8, 8, 3, 1, 0>(qf, exps, m, w, c, ldc, epi, s);
     // Mid-size products: LDS staging pays from 2048 outputs (the direct kernel's duplicate operand

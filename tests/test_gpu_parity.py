@@ -494,6 +494,29 @@ def test_random_q8_0_shapes_match_the_integer_oracle(tk, orc, m, k, n, e):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
 
 
+@pytest.mark.parametrize("m,k,n,e", [(200, 4096, 1000, 0), (300, 2080, 1500, 1), (700, 480, 1800, 2),
+                                     (1000, 224, 4000, 3)])
+def test_q8_0_products_on_each_tile_size(tk, orc, m, k, n, e):
+    """The Q8_0 product's three tile sizes (32 x 32 below one 64 x 64 tile per CU, 32 x 64 below
+    three, 64 x 64 from there): long and odd block counts (k = 4096, 2080, 480, 224: 128, 65, 15
+    and 7 blocks; an odd count's last k-block holds one), partial row blocks and panels;
+    bit-identical to the oracle."""
+    from helpers import pack_q8_0, q8_0_weights
+
+    rng = np.random.default_rng(m + k * 5 + n * 11)
+    a = normal(rng, m * k)
+    q, d = q8_0_weights(rng, n, k, full_range=True)
+    values, scales = pack_q8_0(q, d)
+    bias, c0 = normal(rng, n), normal(rng, m * n)
+    act, acc, with_bias = EPIS[e % len(EPIS)]
+    b = bias if with_bias else None
+    say("q8-tiles", m, k, n, act, acc, with_bias)
+    want = c0.copy()
+    assert orc.matmul_fast_q8(a, k, m, values, scales, n, k, want, n, b, act, 0.5, acc) == 0
+    got = run_gpu(tk, a, k, m, values, scales, Q8_0, n, k, c0, n, b, act, acc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (m, k, n, act)
+
+
 def test_fast_q8_0_unaligned_rows_take_the_gemm(tk, orc):
     from helpers import pack_q8_0, q8_0_weights
 
