@@ -1209,7 +1209,9 @@ hipError_t launch_gemm_i8_qout(const uint8_t *qf, const int32_t *exps, size_t m,
 // The GLU-fused product: 128 x 128 tiles (four panels of each half) from 512 of them when the half
 // has a multiple of 64 outputs, else 64 x 64 tiles (two panels of each half), which need a multiple
 // of 32 (x 1024 -> 2048: 7500 rows 43.0 against 49.2 us, 6000 rows 36.0 against 39.3; at 3000
-// rows, 384 tiles, 21.4 against 20.8).
+// rows, 384 tiles, 21.4 against 20.8), and 32 x 64 tiles below two 64 x 64 tiles per CU (750 x
+// 1024 -> 2048: 7.6 against 8.1 us, the T = 750 layer step 0.1383 -> 0.1367 ms; at 750 x 1024 ->
+// 4096 and 1500 rows the 64 x 64 tiles keep 11.8 against 12.2 and 11.4 against 12.6 us).
 bool gemm_glu_fits(size_t n) { return n % 64 == 0; }
 
 hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *out,
@@ -1219,6 +1221,8 @@ hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, 
     const size_t half = w.n / 2;
     if (half % 64 == 0 && div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 512)
         return launch_lds<8, 8, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
+    if (div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) < 2 * GFX950_CUS)
+        return launch_lds<2, 4, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
     return launch_lds<4, 4, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
 }
 

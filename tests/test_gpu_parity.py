@@ -723,11 +723,12 @@ def test_row_fixtures(tk):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), g["out"].view(np.uint32)), meta["name"]
 
 
-# (m, k, n, ldo): the M=750 layer's pw1 (64 x 64 GLU tiles), 128 x 128 GLU tiles, ragged rows and
-# inputs, strided and unaligned outputs, and products the fused kernel does not take (n % 64 != 0,
-# GEMV rows), which go through the context's buffer.
-GLU_SHAPES = [(750, 1024, 2048, 1024), (1100, 200, 16384, 8192), (4100, 64, 2048, 1030), (37, 200, 256, 130),
-              (130, 64, 128, 64), (300, 100, 96, 48), (5, 64, 128, 64)]
+# (m, k, n, ldo): the M=750 layer's pw1 (32 x 64 GLU tiles), 128 x 128 GLU tiles, 64 x 64 ones (a
+# half of 1056 outputs, which the 128 x 128 tiles do not take), ragged rows and inputs, strided and
+# unaligned outputs, and products the fused kernel does not take (n % 64 != 0, GEMV rows), which go
+# through the context's buffer.
+GLU_SHAPES = [(750, 1024, 2048, 1024), (1100, 200, 16384, 8192), (4100, 64, 2048, 1030), (1500, 96, 2112, 1060),
+              (37, 200, 256, 130), (130, 64, 128, 64), (300, 100, 96, 48), (5, 64, 128, 64)]
 
 
 @pytest.mark.parametrize("m,k,n,ldo", GLU_SHAPES)
