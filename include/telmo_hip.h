@@ -191,9 +191,9 @@ int tg_matmul_quantized_device(tg_ctx *ctx, const void *qa, size_t qa_len, const
 
 /* tg_linear_glu_device on quantised rows: out = glu(epi(qa . w)), the GLU in the GEMM's epilogue,
  * for a convolution module whose pointwise_conv1 input comes out of tg_layer_norm_quant_device.
- * int8 weights with n a multiple of 64; Q8_0 weights (any even n) run the product into a context
- * buffer and then the GLU kernel, the bits of the two calls. Fast mode (TG_ERR_UNSUPPORTED
- * otherwise); no accumulation. */
+ * int8 weights with n a multiple of 64, or Q8_0 weights with any even n (with n not a multiple of
+ * 64 the product goes into a context buffer and then the GLU kernel); either way the bits of the
+ * two calls. Fast mode (TG_ERR_UNSUPPORTED otherwise); no accumulation. */
 int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, const int32_t *exps, size_t m,
                                    const tg_weights *w, float *out, size_t out_len, size_t ldo,
                                    const tg_epilogue *epi);

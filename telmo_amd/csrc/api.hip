@@ -675,9 +675,10 @@ int tg_matmul_quantized_glu_device(tg_ctx *ctx, const void *qa, size_t qa_len, c
     if (w->device != ctx->device) return fail(ctx, TG_ERR_ARG, "weights live on another device");
     std::lock_guard<std::mutex> g(ctx->mu);
     TG_HIP(ctx, hipSetDevice(ctx->device));
-    if (q8) {
-        // Q8_0: the product's [m, n] rows through the context's buffer, then the GLU kernel (the
-        // bits of tg_matmul_quantized_device followed by tg_glu_device).
+    if (q8 && !tg::gemm_glu_fits(n)) {
+        // Q8_0 with n not a multiple of 64: the product's [m, n] rows through the context's buffer,
+        // then the GLU kernel (the bits of tg_matmul_quantized_device followed by tg_glu_device,
+        // which the fused product also gives).
         int rc = grow(ctx, ctx->dg, ctx->dg_cap, m * n * sizeof(float));
         if (rc) return rc;
         TG_HIP(ctx, tg::launch_gemm_i8(static_cast<const uint8_t *>(qa), exps, m, w->d, ctx->dg, n,

@@ -933,7 +933,7 @@ __device__ __forceinline__ void copy_dword_to_lds_s(const uint8_t *base, uint32_
 // wavefronts loading their own operands into registers load each twice, took the T = 750 Q8_0
 // layer step from 0.250 to 0.224 ms on 64 x 64 tiles, and the smaller tiles the registers freed
 // (more workgroups per CU on the narrower products) to 0.204 ms.
-template <int TM, int TN, int NS, int XCD, int G>
+template <int TM, int TN, int NS, int XCD, int G, int GLU>
 __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *__restrict__ qf,
                                                                  const int32_t *__restrict__ exps, int M,
                                                                  const uint8_t *__restrict__ wv,
@@ -941,10 +941,11 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *
                                                                  int KB, int NB, float *__restrict__ c, size_t ldc,
                                                                  const float *__restrict__ bias, uint32_t act,
                                                                  float escale, int accumulate, size_t b_panel,
-                                                                 size_t b_blk) {
+                                                                 size_t b_blk, int hp) {
     constexpr int RB = TM / 2, CB = TN / 2;  // 16 x 16 blocks per wavefront
     constexpr int CH = 2 * TM + TN;          // 1 KB chunks per stage
     static_assert(TN <= 8, "four 256-byte scale copies cover eight panels");
+    static_assert(!GLU || TN % 4 == 0, "a scale copy's two panels lie in one half of the GLU");
     static_assert(NS >= 3, "block t + 1 lands while block t is multiplied, block t - 1's buffer refills");
     // Chunk copies per wavefront: CPW for waves below FULL, CPW - 1 for the rest; each also copies
     // its 256 bytes of scales.
@@ -959,6 +960,14 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *
     const int R0 = by * TM, P0 = bx * TN, RLAST = (M + 15) / 16 - 1;
     const int m0 = by * TM * 16 + wm * WM, n0 = bx * TN * 16 + wn * WN;
     const int out_col = lane & 15, out_row = (lane >> 4) * 4, g = lane >> 4;
+    // Weight panel of B chunk cc (0 <= cc < TN; past the edge, the last panel). GLU: the first
+    // TN / 2 chunks are panels of the first half of the outputs and the rest their partners hp
+    // panels on, so the wavefronts with wn = 0 hold the a half of a GLU and those with wn = 1 the b
+    // half of the same columns (as gemm_lds_kernel's GLU).
+    auto panel_of = [&](int cc) {
+        if constexpr (GLU) return cc < TN / 2 ? bx * (TN / 2) + cc : hp + bx * (TN / 2) + cc - TN / 2;
+        return min(P0 + cc, P - 1);
+    };
 
     int32_t e_row[RB][4];
 #pragma unroll
@@ -968,9 +977,10 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *
 
     // This wavefront's chunk copies (chunk ch = wave + 4 i: row block R0 + ch / 2, digit ch % 2 when
     // ch < 2 TM, else panel P0 + ch - 2 TM; rows and panels past the edge repeat the last one) and
-    // its scale copy: lane l reads scales[((p NB + 2 t + b) 16 + j] for panel p = P0 + 2 wave +
-    // l / 32 (the last panel past the edge), block b = (l / 16) % 2 and column j = l % 16, as the
-    // wave-uniform base (panel P0 + 2 wave, block 2 t) plus a lane offset below NB * 64 + 128 bytes.
+    // its scale copy: lane l reads scales[((p NB + 2 t + b) 16 + j] for the panel p of chunk
+    // 2 wave + l / 32 (the last chunk's past TN), block b = (l / 16) % 2 and column j = l % 16, as
+    // the wave-uniform base (the panel of chunk 2 wave, block 2 t) plus a lane offset below
+    // NB * 64 + 128 bytes (the two panels are consecutive or the same).
     const uint8_t *gp[CPW];
     size_t gs[CPW];
 #pragma unroll
@@ -980,12 +990,12 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *
             gp[i] = qf + (size_t)min(R0 + (ch >> 1), RLAST) * KB * 2048 + (ch & 1) * 1024;
             gs[i] = 2048;
         } else {
-            gp[i] = wv + (size_t)min(P0 + ch - 2 * TM, P - 1) * b_panel;
+            gp[i] = wv + (size_t)panel_of(ch - 2 * TM) * b_panel;
             gs[i] = b_blk;
         }
     }
-    const int s_first = min(P0 + 2 * wave, P - 1), s_blk = (lane >> 4) & 1;
-    const int s_panel = min(P0 + 2 * wave + (lane >> 5), P - 1) - s_first;
+    const int s_first = panel_of(min(2 * wave, TN - 1)), s_blk = (lane >> 4) & 1;
+    const int s_panel = panel_of(min(2 * wave + (lane >> 5), TN - 1)) - s_first;
     const uint32_t s_off = (uint32_t)(((s_panel * NB + s_blk) * PANEL + (lane & 15)) * sizeof(float));
     const uint32_t s_off_one = s_off - (uint32_t)(s_blk * PANEL * sizeof(float));
     const uint8_t *sbase = reinterpret_cast<const uint8_t *>(scales + (size_t)s_first * NB * PANEL);
@@ -1083,7 +1093,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *
     }
 
     TileStore<WM, WN, C_STRIDE> out;
-    out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
+    if constexpr (!GLU) out.begin(lane, c, ldc, m0, n0, M, N, bias, accumulate);
     __syncthreads();  // every wavefront is done with the ring before it holds the staged outputs
     float *tile = reinterpret_cast<float *>(smem) + wave * WM * C_STRIDE;
 #pragma unroll
@@ -1097,16 +1107,27 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_q8_lds_kernel(const uint8_t *
                     e == EXP_NONFINITE ? __builtin_nanf("") : __builtin_ldexpf(acc[r][cb][v], -e);
             }
     __syncthreads();
-    out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+    if constexpr (GLU) {
+        // Wavefronts (wm, 0) and (wm, 1) hold the a and b halves of the same rows and columns; each
+        // stores the GLU of half of those rows. c is the GLU output, hp * 16 columns wide.
+        const float *ta = reinterpret_cast<const float *>(smem) + wm * WM * C_STRIDE + wn * (WM / 2) * C_STRIDE;
+        glu_store<WM / 2, WN, C_STRIDE>(ta, ta + 2 * WM * C_STRIDE, lane, c, ldc, m0 + wn * (WM / 2), bx * WN, M,
+                                        hp * 16, bias, act, escale);
+    } else {
+        out.finish(tile, c, ldc, m0, M, N, bias != nullptr, act, escale, accumulate);
+    }
 }
 
-template <int TM, int TN, int NS, int XCD, int G>
+// GLU: a workgroup column covers TN / 2 panels of each half (the caller checks that they divide the
+// half's panels).
+template <int TM, int TN, int NS, int XCD, int G, int GLU = 0>
 hipError_t launch_q8_lds(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                          size_t ldc, const EpiArgs &epi, hipStream_t s) {
-    const dim3 grid((unsigned)div_ceil(w.panels, (size_t)TN), (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
-    hipLaunchKernelGGL((gemm_q8_lds_kernel<TM, TN, NS, XCD, G>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
+    const size_t hp = w.panels / 2, cols = GLU ? hp / (TN / 2) : div_ceil(w.panels, (size_t)TN);
+    const dim3 grid((unsigned)cols, (unsigned)div_ceil(div_ceil(m, (size_t)16), (size_t)TM));
+    hipLaunchKernelGGL((gemm_q8_lds_kernel<TM, TN, NS, XCD, G, GLU>), grid, dim3(THREADS), 0, s, qf, exps, (int)m,
                        w.values, w.scales, (int)w.n, (int)w.panels, (int)w.kb, (int)(w.k / Q8_BLOCK), c, ldc,
-                       epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride);
+                       epi.bias, epi.act, epi.scale, epi.accumulate, w.panel_stride, w.blk_stride, (int)hp);
     return hipGetLastError();
 }
 
@@ -1217,7 +1238,14 @@ bool gemm_glu_fits(size_t n) { return n % 64 == 0; }
 hipError_t launch_gemm_i8_glu(const uint8_t *qf, const int32_t *exps, size_t m, const DeviceWeights &w, float *out,
                               size_t ldo, const EpiArgs &epi, hipStream_t s) {
     if (m == 0 || w.n == 0) return hipSuccess;
-    if (w.precision != INT8 || !gemm_glu_fits(w.n)) return hipErrorInvalidValue;
+    if ((w.precision != INT8 && w.precision != Q8_0) || !gemm_glu_fits(w.n)) return hipErrorInvalidValue;
+    if (w.precision == Q8_0) {
+        // The Q8_0 product's tiles (64 x 64 from three per CU, else 32 x 64: the 32 x 32 tiles' one
+        // panel per wavefront column cannot hold both halves).
+        if (div_ceil(m, (size_t)64) * div_ceil(w.panels, (size_t)4) >= 3 * GFX950_CUS)
+            return launch_q8_lds<4, 4, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
+        return launch_q8_lds<2, 4, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);
+    }
     const size_t half = w.n / 2;
     if (half % 64 == 0 && div_ceil(m, (size_t)128) * div_ceil(w.panels, (size_t)8) >= 512)
         return launch_lds<8, 8, 3, 1, 0, 1>(qf, exps, m, w, out, ldo, epi, s);

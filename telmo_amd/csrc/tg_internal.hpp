@@ -278,7 +278,7 @@ hipError_t launch_layer_norm_pair(const float *x, size_t ldx, size_t m, size_t n
 // The two-digit int8 MFMA GEMM over quantised rows (int8 and Q8_0 weights).
 hipError_t launch_gemm_i8(const uint8_t *qa, const int32_t *exps, size_t m, const DeviceWeights &w, float *c,
                           size_t ldc, const EpiArgs &epi, hipStream_t s);
-// The same GEMM (int8 weights) with the GLU of its two output halves in the epilogue:
+// The same GEMM (int8 or Q8_0 weights) with the GLU of its two output halves in the epilogue:
 // out[r, j] = g[r, j] / (1 + exp(0 - g[r, n / 2 + j])), g the product through epi (no
 // accumulation). n must be a multiple of 64 (gemm_glu_fits); out is m x n / 2, row stride ldo.
 bool gemm_glu_fits(size_t n);

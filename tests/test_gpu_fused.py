@@ -160,10 +160,13 @@ def test_quantised_output_product_is_product_then_quantise(tk, m, k, n, act, wit
 
 
 @pytest.mark.parametrize("m,k,n,act,with_bias,scale", [(750, 1024, 4096, 2, True, 1.0), (2500, 1024, 640, 2, True, 0.5),
-                                                      (37, 96, 130, 0, False, 1.0)])
+                                                      (37, 96, 130, 0, False, 1.0), (750, 1024, 2048, 0, False, 1.0),
+                                                      (37, 160, 192, 1, True, 0.5)])
 def test_q8_0_quantised_output_and_glu_are_the_two_calls(tk, m, k, n, act, with_bias, scale):
     """Q8_0 weights through the quantised-output product and the quantised GLU product: the product's
-    rows then the quantiser, and the product's rows then the GLU kernel, bit for bit."""
+    rows then the quantiser, and the product's rows then the GLU kernel, bit for bit (the GLU in the
+    product's epilogue on 64 x 64 and 32 x 64 tiles when n is a multiple of 64, else through a buffer;
+    k = 160 leaves the last k-block one block)."""
     import torch
 
     import telmo_amd
