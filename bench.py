@@ -475,8 +475,15 @@ def granite_leg(args):
     def run(_):
         x.copy_(x0)
         cur, t = x, G_ROWS
+        blk.prepare(cur, t, blocks[0])
+        ready = True
         for i, w in enumerate(blocks):
-            cur, t = blk.forward(cur, t, w, out=bufs[i] if i in G_STRIDED else None)
+            # each block boundary's two LayerNorms in one launch, except where the self-conditioning
+            # rewrites the rows between them
+            pair = i + 1 < len(blocks) and i != G_SELFCOND
+            cur, t = blk.forward(cur, t, w, out=bufs[i] if i in G_STRIDED else None, prepared=ready,
+                                 next_norm=blocks[i + 1].norms["ff1_norm"] if pair else None)
+            ready = pair
             if i == G_SELFCOND:
                 self_conditioning(kern, cur, t, H, hb, M, mb, logits)
         return cur

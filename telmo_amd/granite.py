@@ -81,26 +81,38 @@ class GraniteBlock:
         self.glu = f32(rows, conv_channels)
         self.conv = f32(rows, conv_channels)
 
-    def _feed_forward(self, x, t: int, w: BlockWeights, which: str) -> None:
-        """x += 0.5 * (down(silu(up(norm(x)) + up.b)) + down.b) (src/granite.rs:752-793)."""
+    def prepare(self, x, t: int, w: BlockWeights) -> None:
+        """The digits of ff1's LayerNorm of x's t rows in the block's buffers: what forward(...,
+        prepared=True) expects, as the previous block's forward(..., next_norm=...) leaves them."""
+        g, b = w.norms["ff1_norm"]
+        self.kern.layer_norm_quant_device(x, self.d, t, self.d, g, b, self.eps, self.qa_d, self.ex_d)
+
+    def _feed_forward(self, x, t: int, w: BlockWeights, which: str, ready: bool = False) -> None:
+        """x += 0.5 * (down(silu(up(norm(x)) + up.b)) + down.b) (src/granite.rs:752-793). ready: the
+        digits of norm(x) are already in the block's buffers."""
         k, d = self.kern, self.d
         g, b = w.norms[which + "_norm"]
         up, down = w.mats[which + "_up"], w.mats[which + "_down"]
-        k.layer_norm_quant_device(x, d, t, d, g, b, self.eps, self.qa_d, self.ex_d)
+        if not ready:
+            k.layer_norm_quant_device(x, d, t, d, g, b, self.eps, self.qa_d, self.ex_d)
         silu = Epilogue(bias=w.biases[which + "_up"], act=Act.SILU)
         half_acc = Epilogue(bias=w.biases[which + "_down"], scale=0.5, accumulate=True)
         k.matmul_quantized_to_quant_device(self.qa_d, self.ex_d, t, up, self.qa_ff, self.ex_ff, silu)
         k.matmul_quantized_device(self.qa_ff, self.ex_ff, t, down, x, d, half_acc)
 
     def forward(self, x, t: int, w: BlockWeights, utterances: int = 1, attention: Optional[Callable] = None,
-                out=None):
+                out=None, prepared: bool = False, next_norm=None):
         """x: [t, d] float32 GPU tensor, the block's input rows (rewritten: afterwards it holds the
         post-attention states, as the reference leaves it); t frames in all, `utterances` equal-length
         utterances stacked along the rows. attention(qkv) -> att returns the heads' outputs [t, d]
         (rows at any stride, as a tensor view) from the f32 q, k, v rows; None uses the V third of qkv.
         Returns (y, n): the block's output rows and their count, n = t (y is x) or, for a strided
         block, utterances * (t / utterances // 2) rows written to `out` ([n, d] float32 GPU tensor,
-        allocated when None)."""
+        allocated when None). prepared: the digits of ff1's LayerNorm of x are already in the block's
+        buffers (prepare, or the previous block's next_norm). next_norm = (gamma, beta): the next
+        block's ff1 LayerNorm, whose digits of the output rows are left in the buffers for it, the
+        block boundary in one launch (tg_layer_norm_pair_quant_device): the same bits as
+        prepare on the output."""
         import torch
 
         k, d, cc, eps = self.kern, self.d, self.cc, self.eps
@@ -111,7 +123,7 @@ class GraniteBlock:
         for name, mat in m.items():
             if mat.precision() not in (Precision.INT8, Precision.Q8_0):
                 raise ValueError(f"the device block takes int8 or Q8_0 matrices ({name} is {mat.precision().name})")
-        self._feed_forward(x, t, w, "ff1")
+        self._feed_forward(x, t, w, "ff1", ready=prepared)
         g, b = w.norms["norm_att"]
         k.layer_norm_quant_device(x, d, t, d, g, b, eps, self.qa_d, self.ex_d)
         qkv = self.qkv[:t]
@@ -153,7 +165,11 @@ class GraniteBlock:
                                   Epilogue(bias=w.biases["pw2"], accumulate=True))
         self._feed_forward(y, n, w, "ff2")
         g, b = w.norms["norm_out"]
-        k.layer_norm_device(y, d, n, d, g, b, eps, y, d)
+        if next_norm is None:
+            k.layer_norm_device(y, d, n, d, g, b, eps, y, d)
+        else:
+            k.layer_norm_pair_quant_device(y, d, n, d, g, b, eps, next_norm[0], next_norm[1], eps, self.qa_d,
+                                           self.ex_d, x_len=n * d)
         return y, n
 
 

@@ -27,9 +27,10 @@ def say(*args):
     print("[case]", *args, flush=True)
 
 
-def run_blocks(tk, blocks, x, utterances, selfcond=None):
+def run_blocks(tk, blocks, x, utterances, selfcond=None, paired=False):
     """The device blocks in order over x (numpy [t, d]); selfcond = (head, head_b, mid, mid_b) host
-    parameters applied after the last block. Returns the output rows."""
+    parameters applied after the last block. paired: each block boundary's two LayerNorms in one
+    launch (forward's prepared and next_norm). Returns the output rows."""
     import torch
 
     from telmo_amd.granite import GraniteBlock, self_conditioning
@@ -38,11 +39,12 @@ def run_blocks(tk, blocks, x, utterances, selfcond=None):
     blk = GraniteBlock(tk, D, bench.G_FF, bench.G_CC, bench.G_KERNEL, t)
     cur = torch.from_numpy(x.copy()).cuda()
     n = t
-    ws = []
-    for params in blocks:
-        w = bench.upload_granite_block(tk, params)
-        ws.append(w)
-        y, n = blk.forward(cur, n, w, utterances=utterances)
+    ws = [bench.upload_granite_block(tk, params) for params in blocks]
+    if paired and ws:
+        blk.prepare(cur, n, ws[0])
+    for i, w in enumerate(ws):
+        nxt = ws[i + 1].norms["ff1_norm"] if paired and i + 1 < len(ws) else None
+        y, n = blk.forward(cur, n, w, utterances=utterances, prepared=paired, next_norm=nxt)
         cur = y
     if selfcond is not None:
         import telmo_amd
@@ -97,6 +99,20 @@ def test_plain_block(tk, orc, frames, utterances):
     say("granite block", frames, utterances)
     got = run_blocks(tk, [p], x, utterances)
     check(orc, got, [p], x, utterances, f"block, {utterances} x {frames} frames")
+
+
+def test_block_boundaries_in_one_launch(tk):
+    """Two strided blocks and a plain one with each boundary's norm_out and the next block's ff1
+    LayerNorm in one launch, the first block's taken by prepare: the bits of the blocks run one
+    LayerNorm at a time (which the oracle tests pin), over 2 x 500 frames."""
+    blocks = [bench.granite_block_params(1700, True), bench.granite_block_params(1800, True),
+              bench.granite_block_params(1900, False)]
+    x = bench.synth_normal((1000, D), 15)
+    say("granite paired boundaries", 1000)
+    want = run_blocks(tk, blocks, x, 2)
+    got = run_blocks(tk, blocks, x, 2, paired=True)
+    assert got.shape == want.shape == (250, D)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_self_conditioning(tk, orc):
